@@ -1,0 +1,175 @@
+"""Benchmark of the MoE FFN block on one MI355X.
+
+Default workload: Qwen3.6-35B-A3B-shape MoE layer (hidden 2048, 256 experts
+top-8, shared expert, intermediate 512, 4-bit group-32 weights), batch-1
+decode: every step is one token's full MoE block (router, 8 routed experts,
+shared expert, combine) with a fresh activation, launched in sequence.
+Inputs are resident in HBM before the timed region.  Prints one JSON line.
+
+  python bench.py [--steps K] [--warmup W] [--workload decode|toy|stack]
+                  [--cpu-sample-s S] [--no-cpu]
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "disk-streaming-moe-engine_amd"))
+
+METRIC = "MoE-layer decode µs/token + achieved HBM GB/s (4-bit, batch 1, 1 GPU)"
+HBM_PEAK_GBPS = 8000.0
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=1000)
+    ap.add_argument("--warmup", type=int, default=50)
+    ap.add_argument("--workload", default="decode", choices=["decode", "toy", "stack"])
+    ap.add_argument("--layers", type=int, default=40, help="stack workload depth")
+    ap.add_argument("--cpu-sample-s", type=float, default=15.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--seed", type=int, default=1)
+    return ap.parse_args()
+
+
+def cpu_baseline(L, x_tokens, budget_s):
+    """The oracle (CPU restatement of the reference composition: per-use dequant
+    of the selected experts, fp32 SwiGLU, one thread) on a bounded token sample."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+    n, t0 = 0, time.perf_counter()
+    while n < len(x_tokens) and (time.perf_counter() - t0) < budget_s:
+        O.moe_layer_q4(L, x_tokens[n:n + 1], 1)
+        n += 1
+    dt = time.perf_counter() - t0
+    return {"value": round(dt / n * 1e6, 1), "unit": "us/token", "cores": 1, "kind": "port",
+            "sample": f"{n} decode tokens of the same layer, dequant-per-use, threads=1"}
+
+
+def main():
+    a = parse()
+    if a.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1"}))
+        sys.exit(2)
+    import numpy as np
+    import torch
+
+    from dismoen import MoEBlock, synth
+
+    dev = torch.device("cuda:0")
+    blk = MoEBlock(0)
+    stream = torch.cuda.current_stream(dev)
+    blk.set_stream(stream.cuda_stream)
+
+    if a.workload in ("decode", "toy"):
+        cfg = synth.CONFIG_QWEN36 if a.workload == "decode" else synth.CONFIG_TOY
+        L = synth.make_layer(**cfg, seed=a.seed)
+        blk.upload_layer(0, L)
+        H, K = L.hidden, L.top_k
+        ntok = a.warmup + a.steps
+        rng = np.random.default_rng(a.seed + 1000)
+        x_host = synth.make_activations(rng, (ntok, H))
+        x = torch.from_numpy(x_host).to(dev)
+        y = torch.empty((ntok, H), dtype=torch.float32, device=dev)
+        ids = torch.empty((ntok, K), dtype=torch.int32, device=dev)
+        probs = torch.empty((ntok, K), dtype=torch.float32, device=dev)
+        shg = torch.empty((ntok,), dtype=torch.float32, device=dev)
+        xp, yp, ip, pp, sp = (t.data_ptr() for t in (x, y, ids, probs, shg))
+
+        def step(t):
+            blk.forward_device(0, xp + t * H * 4, 1, yp + t * H * 4, ip + t * K * 4,
+                               pp + t * K * 4, sp + t * 4)
+
+        for t in range(a.warmup):
+            step(t)
+        torch.cuda.synchronize()
+        blk.sync()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        w0 = time.perf_counter()
+        e0.record(stream)
+        for t in range(a.warmup, ntok):
+            step(t)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - w0
+        blk.sync()
+        ms = e0.elapsed_time(e1) / a.steps
+        bytes_tok = synth.algorithmic_bytes_per_token(H, L.num_experts, K, L.inter, L.inter_sh)
+        us = ms * 1e3
+        gbps = bytes_tok / (us * 1e-6) / 1e9
+        # parity spot check of the last token against the oracle (outside timing)
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        import oracle as O
+        t_last = ntok - 1
+        yo, ido, po, _ = O.moe_layer_q4(L, x_host[t_last:t_last + 1], 1)
+        ids_ok = bool(np.array_equal(ids[t_last].cpu().numpy(), ido[0]))
+        yl = y[t_last].cpu().numpy().astype(np.float64)
+        rel = float(np.max(np.abs(yl - yo[0])) / np.sqrt(np.mean(yo[0].astype(np.float64) ** 2)))
+        out = {
+            "metric": METRIC, "value": round(us, 3), "unit": "us/token", "n_gpus": 1,
+            "steps": a.steps, "warmup": a.warmup, "ms_per_step": round(ms, 6),
+            "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+            "data": "synthetic",
+            "config": {"workload": ("qwen3.6-35b-a3b moe layer, batch-1 decode"
+                                    if a.workload == "decode" else "toy moe layer, batch-1 decode"),
+                       "hidden": H, "experts": L.num_experts, "top_k": K, "inter": L.inter,
+                       "inter_sh": L.inter_sh, "group": 32, "bits": 4, "tokens": a.steps},
+            "achieved_gbps": round(gbps, 1),
+            "roofline": {"bound": "hbm", "kernel": "moe block (all launches of one token)",
+                         "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                         "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None,
+                         "bytes_per_token": bytes_tok},
+            "parity_last_token": {"ids_bit_exact": ids_ok, "max_abs_over_rms": rel},
+            "wall_s": round(wall, 3),
+        }
+        if not a.no_cpu:
+            out["cpu_baseline"] = cpu_baseline(L, x_host, a.cpu_sample_s)
+        print(json.dumps(out))
+    else:  # stack
+        cfg = synth.CONFIG_QWEN36
+        nl = a.layers
+        for l in range(nl):
+            L = synth.make_layer(**cfg, seed=a.seed * 1000 + l)
+            blk.upload_layer(l, L)
+            del L
+        H, K = cfg["hidden"], cfg["top_k"]
+        ntok = a.warmup + a.steps
+        x_host = synth.make_activations(np.random.default_rng(a.seed + 7), (ntok, H))
+        x = torch.from_numpy(x_host).to(dev)
+        y = torch.empty((ntok, H), dtype=torch.float32, device=dev)
+        xp, yp = x.data_ptr(), y.data_ptr()
+        for t in range(a.warmup):
+            blk.forward_stack_device(xp + t * H * 4, 0, nl, 1, yp + t * H * 4)
+        torch.cuda.synchronize()
+        blk.sync()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for t in range(a.warmup, ntok):
+            blk.forward_stack_device(xp + t * H * 4, 0, nl, 1, yp + t * H * 4)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        blk.sync()
+        ms = e0.elapsed_time(e1) / a.steps
+        bytes_tok = nl * synth.algorithmic_bytes_per_token(H, cfg["num_experts"], K,
+                                                            cfg["inter"], cfg["inter_sh"])
+        gbps = bytes_tok / (ms * 1e-3) / 1e9
+        print(json.dumps({
+            "metric": METRIC, "value": round(ms * 1e3, 3), "unit": "us/token", "n_gpus": 1,
+            "steps": a.steps, "warmup": a.warmup, "ms_per_step": round(ms, 6),
+            "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+            "data": "synthetic",
+            "config": {"workload": f"{nl}-layer moe stack resident in HBM, batch-1 decode",
+                       "layers": nl, "hidden": H, "tokens": a.steps},
+            "roofline": {"bound": "hbm", "kernel": "moe stack", "achieved": round(gbps, 1),
+                         "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                         "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None,
+                         "bytes_per_token": bytes_tok}}))
+    blk.close()
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,685 @@
+// dm_api.cpp -- C ABI of libdismoen_hip.so (include/dismoen_hip.h): context,
+// one-time layer upload, and the MoE block entry points.
+#include <hip/hip_runtime.h>
+
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <string>
+#include <vector>
+
+#include "../../include/dismoen_hip.h"
+#include "dm_kernels.h"
+#include "dm_layout.h"
+
+using dm::LayerDev;
+
+namespace {
+
+constexpr int kMaxLayers = 4096;
+
+struct Layer {
+  dmh_moe_dims dims{};
+  void* buf = nullptr;
+  size_t bytes = 0;
+  LayerDev dev{};
+  bool router_w_bad = false;
+};
+
+template <typename T>
+struct DevBuf {
+  T* p = nullptr;
+  size_t cap = 0;  // elements
+  hipError_t ensure(size_t n) {
+    if (n <= cap) return hipSuccess;
+    if (p) (void)hipFree(p);
+    p = nullptr;
+    cap = 0;
+    hipError_t e = hipMalloc(&p, n * sizeof(T) + 256);
+    if (e == hipSuccess) cap = n;
+    return e;
+  }
+  void release() {
+    if (p) (void)hipFree(p);
+    p = nullptr;
+    cap = 0;
+  }
+};
+
+}  // namespace
+
+struct dmh_ctx {
+  int device = 0;
+  hipStream_t own = nullptr, cur = nullptr;
+  std::vector<Layer*> layers;
+  // scratch
+  DevBuf<float> x, res, y, z, probs, shg, h, xn, hstack;
+  DevBuf<int32_t> ids;
+  DevBuf<uint8_t> stage;
+  unsigned long long* status = nullptr;  // [kMaxLayers + 1] first-error keys (last = unit calls)
+  unsigned long long* vkey = nullptr;    // upload validation key
+  unsigned* flags = nullptr;             // upload flags
+  // where to find the routing of the last device-mode call per layer
+  std::vector<const int32_t*> last_ids;
+  std::vector<int> last_k;
+};
+
+namespace {
+
+int set_err(char* err, size_t errlen, int code, const char* fmt, ...) {
+  if (err && errlen) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(err, errlen, fmt, ap);
+    va_end(ap);
+  }
+  return code;
+}
+
+#define HIP_TRY(expr)                                                                      \
+  do {                                                                                     \
+    hipError_t _e = (expr);                                                                \
+    if (_e != hipSuccess)                                                                  \
+      return set_err(err, errlen, DMH_ERR_HIP, "{\"error_type\":\"HIP_ERROR\",\"detail\":" \
+                     "\"%s: %s\",\"stage\":\"hip\"}", #expr, hipGetErrorString(_e));       \
+  } while (0)
+
+size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+// Text of the first error recorded by the kernels (key layout in dm_layout.h).
+int decode_key(uint64_t key, int layer, int expert_id, int E, char* err, size_t errlen) {
+  using namespace dm;
+  const uint32_t ph = key_phase(key), pos = key_pos(key), kind = key_kind(key);
+#define RJ(code, type, detail, stage)                                                        \
+  return set_err(err, errlen, code,                                                          \
+                 "{\"error_type\":\"" type "\",\"detail\":\"" detail "\",\"stage\":\"" stage \
+                 "\",\"layer\":%d}", layer)
+#define EJ(code, type, detail)                                                              \
+  return set_err(err, errlen, code,                                                         \
+                 "{\"error_type\":\"" type "\",\"detail\":\"" detail                        \
+                 "\",\"stage\":\"swiglu\",\"layer\":%d,\"expert_id\":%d}", layer, expert_id)
+  switch (ph) {
+    case kPhX: RJ(DMH_ERR_ACT, "ACT_LOAD_FAILED", "non-finite value in activation", "router");
+    case kPhRouterW:
+      RJ(DMH_ERR_WEIGHT, "WEIGHT_LOAD_FAILED", "non-finite value in router weight", "router");
+    case kPhLogit: RJ(DMH_ERR_ROUTER, "ROUTER_ERROR", "non-finite router logit computed", "router");
+    case kPhSoftmax:
+      if (pos == 0) RJ(DMH_ERR_ROUTER, "ROUTER_ERROR", "non-finite max logit in router softmax", "router");
+      if ((int)pos <= E) RJ(DMH_ERR_ROUTER, "ROUTER_ERROR", "non-finite exp in router softmax", "router");
+      RJ(DMH_ERR_ROUTER, "ROUTER_ERROR", "invalid sum_exp in router softmax", "router");
+    case kPhTopk:
+      if (kind == kTkSum)
+        RJ(DMH_ERR_ROUTER, "ROUTER_ERROR", "sum of top-k probabilities exceeds 1.0", "router");
+      RJ(DMH_ERR_ROUTER, "ROUTER_ERROR",
+         "renormalization leak detected: sum of top-k probabilities is 1.0", "router");
+    case kPhExpert:
+    case kPhShared:
+      if (kind == kEkGate) EJ(DMH_ERR_EXPERT, "EXPERT_ERROR", "non-finite in gate projection");
+      if (kind == kEkUp) EJ(DMH_ERR_EXPERT, "EXPERT_ERROR", "non-finite in up projection");
+      if (kind == kEkH) EJ(DMH_ERR_SWIGLU, "SWIGLU_ERROR", "non-finite in element-wise product");
+      EJ(DMH_ERR_EXPERT, "EXPERT_ERROR", "non-finite in down projection");
+    case kPhGate:
+      if (kind == kGkLogit) RJ(DMH_ERR_GATE, "GATE_ERROR", "non-finite shared gate logit", "shared");
+      RJ(DMH_ERR_GATE, "GATE_ERROR", "shared gate score outside (0, 1)", "shared");
+    default:
+      RJ(DMH_ERR_EXPERT, "EXPERT_ERROR", "non-finite value in aggregation", "aggregation");
+  }
+#undef RJ
+#undef EJ
+}
+
+int router_config_check(int E, int K, int norm, char* err, size_t errlen) {
+  // RouterConfig.validate, src/layers/router_types.mojo:9-44
+  if (E <= 0)
+    return set_err(err, errlen, DMH_ERR_CONFIG,
+                   "{\"error_type\":\"CONFIG_ERROR\",\"detail\":\"num_experts must be"
+                   " positive\",\"stage\":\"router\"}");
+  if (K <= 0)
+    return set_err(err, errlen, DMH_ERR_CONFIG,
+                   "{\"error_type\":\"CONFIG_ERROR\",\"detail\":\"num_experts_per_tok"
+                   " must be positive\",\"stage\":\"router\"}");
+  if (K > E)
+    return set_err(err, errlen, DMH_ERR_CONFIG,
+                   "{\"error_type\":\"CONFIG_ERROR\",\"detail\":\"num_experts_per_tok"
+                   " cannot exceed num_experts\",\"stage\":\"router\"}");
+  if (norm)
+    return set_err(err, errlen, DMH_ERR_ROUTER,
+                   "{\"error_type\":\"ROUTER_ERROR\",\"detail\":\"norm_topk_prob=true"
+                   " forbidden; unrenormalized routing invariant violated\",\"stage\":\"router\"}");
+  return DMH_OK;
+}
+
+Layer* get_layer(dmh_ctx* ctx, int layer) {
+  if (!ctx || layer < 0 || layer >= (int)ctx->layers.size()) return nullptr;
+  return ctx->layers[layer];
+}
+
+hipError_t reset_status(dmh_ctx* ctx, int slot) {
+  return hipMemsetAsync(ctx->status + slot, 0xFF, sizeof(unsigned long long), ctx->cur);
+}
+
+// Runs the block for T tokens of a layer on device buffers.
+hipError_t run_block(dmh_ctx* ctx, Layer* Ly, int layer, const float* dx, const float* dres,
+                     int T, float* dy, int32_t* dids, float* dprobs, float* dshg) {
+  const LayerDev& L = Ly->dev;
+  hipStream_t st = ctx->cur;
+  unsigned long long* status = ctx->status + layer;
+  const int ldh = L.I > L.Ish ? L.I : L.Ish;
+  hipError_t e;
+  if ((e = ctx->z.ensure((size_t)T * (L.E + 1))) != hipSuccess) return e;
+  if ((e = ctx->h.ensure((size_t)(L.K + 1) * ldh)) != hipSuccess) return e;
+  if ((e = dm::launch_router_dec(L, dx, T, ctx->z.p, status, st)) != hipSuccess) return e;
+  if ((e = dm::launch_router_select(ctx->z.p, L.E + 1, T, L.E, L.K, 1, dids, dprobs, dshg, status,
+                                    st)) != hipSuccess)
+    return e;
+  for (int t = 0; t < T; ++t) {
+    const float* xt = dx + (size_t)t * L.H;
+    if ((e = dm::launch_gateup_dec(L, xt, dids + (size_t)t * L.K, ctx->h.p, ldh, t, status, st)) !=
+        hipSuccess)
+      return e;
+    if ((e = dm::launch_down_dec(L, ctx->h.p, ldh, dids + (size_t)t * L.K,
+                                 dprobs + (size_t)t * L.K, dshg + t,
+                                 dres ? dres + (size_t)t * L.H : nullptr, dy + (size_t)t * L.H, t,
+                                 status, st)) != hipSuccess)
+      return e;
+  }
+  return hipSuccess;
+}
+
+// Host-side decode of a layer's status word after a synchronous call.
+int finish_status(dmh_ctx* ctx, Layer* Ly, int layer, uint64_t key, const int32_t* host_ids,
+                  char* err, size_t errlen) {
+  if (Ly && Ly->router_w_bad) {
+    const uint64_t rk = dm::err_key(dm::kPhRouterW, 0, 0, 0, 0);
+    if (rk < key) key = rk;
+  }
+  if (key == dm::kNoError) return DMH_OK;
+  int expert_id = -1;
+  const int K = Ly ? Ly->dims.top_k : 0;
+  if (dm::key_phase(key) == dm::kPhExpert && host_ids)
+    expert_id = host_ids[(size_t)dm::key_token(key) * K + dm::key_slot(key)];
+  (void)ctx;
+  return decode_key(key, layer, expert_id, Ly ? Ly->dims.num_experts : 0, err, errlen);
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* dmh_version(void) { return "dismoen_hip 1 gfx950"; }
+
+int dmh_create(int device, dmh_ctx** out, char* err, size_t errlen) {
+  if (!out) return set_err(err, errlen, DMH_ERR_INVALID_ARG, "dmh_create: out is NULL");
+  *out = nullptr;
+  int n = 0;
+  HIP_TRY(hipGetDeviceCount(&n));
+  if (device < 0 || device >= n)
+    return set_err(err, errlen, DMH_ERR_INVALID_ARG, "dmh_create: no HIP device %d (%d present)",
+                   device, n);
+  HIP_TRY(hipSetDevice(device));
+  dmh_ctx* c = new dmh_ctx();
+  c->device = device;
+  hipError_t e = hipStreamCreateWithFlags(&c->own, hipStreamNonBlocking);
+  if (e == hipSuccess) e = hipMalloc(&c->status, sizeof(unsigned long long) * (kMaxLayers + 1));
+  if (e == hipSuccess) e = hipMalloc(&c->vkey, sizeof(unsigned long long));
+  if (e == hipSuccess) e = hipMalloc(&c->flags, sizeof(unsigned));
+  if (e == hipSuccess)
+    e = hipMemset(c->status, 0xFF, sizeof(unsigned long long) * (kMaxLayers + 1));
+  if (e != hipSuccess) {
+    dmh_destroy(c);
+    return set_err(err, errlen, DMH_ERR_HIP, "dmh_create: %s", hipGetErrorString(e));
+  }
+  c->cur = c->own;
+  c->last_ids.assign(kMaxLayers + 1, nullptr);
+  c->last_k.assign(kMaxLayers + 1, 0);
+  *out = c;
+  return DMH_OK;
+}
+
+int dmh_destroy(dmh_ctx* c) {
+  if (!c) return DMH_OK;
+  (void)hipSetDevice(c->device);
+  if (c->cur) (void)hipStreamSynchronize(c->cur);
+  for (Layer* L : c->layers)
+    if (L) {
+      if (L->buf) (void)hipFree(L->buf);
+      delete L;
+    }
+  DevBuf<float>* fb[] = {&c->x, &c->res, &c->y, &c->z, &c->probs, &c->shg, &c->h, &c->xn, &c->hstack};
+  for (auto* b : fb) b->release();
+  c->ids.release();
+  c->stage.release();
+  if (c->status) (void)hipFree(c->status);
+  if (c->vkey) (void)hipFree(c->vkey);
+  if (c->flags) (void)hipFree(c->flags);
+  if (c->own) (void)hipStreamDestroy(c->own);
+  delete c;
+  return DMH_OK;
+}
+
+int dmh_set_stream(dmh_ctx* c, void* s) {
+  if (!c) return DMH_ERR_INVALID_ARG;
+  c->cur = s ? (hipStream_t)s : c->own;
+  return DMH_OK;
+}
+
+void* dmh_get_stream(dmh_ctx* c) { return c ? (void*)c->cur : nullptr; }
+
+int dmh_sync(dmh_ctx* c, char* err, size_t errlen) {
+  if (!c) return set_err(err, errlen, DMH_ERR_INVALID_ARG, "dmh_sync: ctx is NULL");
+  HIP_TRY(hipSetDevice(c->device));
+  HIP_TRY(hipStreamSynchronize(c->cur));
+  std::vector<unsigned long long> keys(kMaxLayers + 1);
+  HIP_TRY(hipMemcpy(keys.data(), c->status, sizeof(unsigned long long) * keys.size(),
+                    hipMemcpyDeviceToHost));
+  int rc = DMH_OK;
+  for (int l = 0; l <= kMaxLayers && rc == DMH_OK; ++l) {
+    Layer* Ly = l < (int)c->layers.size() ? c->layers[l] : nullptr;
+    uint64_t key = keys[l];
+    if (key == dm::kNoError) continue;
+    std::vector<int32_t> ids;
+    if (dm::key_phase(key) == dm::kPhExpert && c->last_ids[l] && Ly) {
+      const size_t n = (size_t)(dm::key_token(key) + 1) * Ly->dims.top_k;
+      ids.resize(n);
+      if (hipMemcpy(ids.data(), c->last_ids[l], n * sizeof(int32_t), hipMemcpyDeviceToHost) !=
+          hipSuccess)
+        ids.clear();
+    }
+    rc = finish_status(c, Ly, l, key, ids.empty() ? nullptr : ids.data(), err, errlen);
+  }
+  HIP_TRY(hipMemset(c->status, 0xFF, sizeof(unsigned long long) * keys.size()));
+  return rc;
+}
+
+int dmh_upload_moe_layer(dmh_ctx* c, int layer, const dmh_moe_dims* d, const dmh_moe_weights* w,
+                         unsigned flags, char* err, size_t errlen) {
+  if (!c || !d || !w)
+    return set_err(err, errlen, DMH_ERR_INVALID_ARG, "dmh_upload_moe_layer: NULL argument");
+  if (layer < 0 || layer >= kMaxLayers)
+    return set_err(err, errlen, DMH_ERR_INVALID_ARG,
+                   "dmh_upload_moe_layer: layer %d outside [0, %d)", layer, kMaxLayers);
+  int rc = router_config_check(d->num_experts, d->top_k, d->norm_topk_prob, err, errlen);
+  if (rc) return rc;
+  const int H = d->hidden, E = d->num_experts, K = d->top_k, I = d->inter, Ish = d->inter_sh;
+  if (d->group_size != 32 || H <= 0 || I <= 0 || Ish <= 0 || H % 128 || I % 128 || Ish % 128 ||
+      E > 2048 || K + 1 > 33 || (size_t)(K + 1) * (I > Ish ? I : Ish) * 6 > 65536 || H > 8192)
+    return set_err(err, errlen, DMH_ERR_CONFIG,
+                   "{\"error_type\":\"CONFIG_ERROR\",\"detail\":\"unsupported MoE dims: G=%d H=%d"
+                   " E=%d K=%d I=%d Ish=%d (need G=32, H/I/Ish multiples of 128, E<=2048,"
+                   " K<=32, H<=8192)\",\"stage\":\"config\",\"layer\":%d}",
+                   d->group_size, H, E, K, I, Ish, layer);
+  if (!w->router_bf16 || !w->shgate_bf16 || !w->gu_scales || !w->gu_packed || !w->d_scales ||
+      !w->d_packed || !w->sh_gu_scales || !w->sh_gu_packed || !w->sh_d_scales || !w->sh_d_packed)
+    return set_err(err, errlen, DMH_ERR_INVALID_ARG, "dmh_upload_moe_layer: NULL weight pointer");
+  HIP_TRY(hipSetDevice(c->device));
+  hipStream_t st = c->cur;
+  const size_t G = 32;
+  const size_t n_gu = (size_t)E * 2 * I * H, n_d = (size_t)E * H * I;
+  const size_t n_sgu = (size_t)2 * Ish * H, n_sd = (size_t)H * Ish;
+  // device layout sizes
+  const size_t b_router = align256((size_t)(E + 1) * H * 2);
+  const size_t b_gun = align256(n_gu / 2), b_gus = align256(n_gu / G * 2);
+  const size_t b_dn = align256(n_d / 2), b_ds = align256(n_d / G * 2);
+  const size_t b_sgun = align256(n_sgu / 2), b_sgus = align256(n_sgu / G * 2);
+  const size_t b_sdn = align256(n_sd / 2), b_sds = align256(n_sd / G * 2);
+  const size_t total = b_router + b_gun + b_gus + b_dn + b_ds + b_sgun + b_sgus + b_sdn + b_sds;
+  Layer* Ly = new Layer();
+  Ly->dims = *d;
+  hipError_t e = hipMalloc(&Ly->buf, total);
+  if (e != hipSuccess) {
+    delete Ly;
+    return set_err(err, errlen, DMH_ERR_NO_MEMORY, "dmh_upload_moe_layer: hipMalloc(%zu): %s",
+                   total, hipGetErrorString(e));
+  }
+  Ly->bytes = total;
+  uint8_t* p = (uint8_t*)Ly->buf;
+  uint16_t* router = (uint16_t*)p; p += b_router;
+  uint8_t* gun = p; p += b_gun;
+  uint16_t* gus = (uint16_t*)p; p += b_gus;
+  uint8_t* dn = p; p += b_dn;
+  uint16_t* ds = (uint16_t*)p; p += b_ds;
+  uint8_t* sgun = p; p += b_sgun;
+  uint16_t* sgus = (uint16_t*)p; p += b_sgus;
+  uint8_t* sdn = p; p += b_sdn;
+  uint16_t* sds = (uint16_t*)p; p += b_sds;
+  Ly->dev = LayerDev{H, E, K, I, Ish, router, gun, gus, dn, ds, sgun, sgus, sdn, sds};
+
+  auto fail = [&](int code, const char* what, hipError_t he) {
+    (void)hipFree(Ly->buf);
+    delete Ly;
+    return set_err(err, errlen, code, "dmh_upload_moe_layer: %s: %s", what, hipGetErrorString(he));
+  };
+  e = hipMemsetAsync(c->vkey, 0xFF, sizeof(unsigned long long), st);
+  if (e == hipSuccess) e = hipMemsetAsync(c->flags, 0, sizeof(unsigned), st);
+  if (e != hipSuccess) return fail(DMH_ERR_HIP, "memset", e);
+
+  const bool dev = flags & DMH_F_DEVICE;
+  // staging: one tensor group (scales + codes) at a time
+  const size_t stage_bytes = align256(n_gu / 2) + align256(n_gu / G * 2) + 2 * b_router;
+  if (!dev && (e = c->stage.ensure(stage_bytes)) != hipSuccess)
+    return fail(DMH_ERR_NO_MEMORY, "staging", e);
+  auto src = [&](const void* hp, size_t bytes, size_t off, const void** dp) -> hipError_t {
+    if (dev) {
+      *dp = hp;
+      return hipSuccess;
+    }
+    *dp = c->stage.p + off;
+    return hipMemcpyAsync(c->stage.p + off, hp, bytes, hipMemcpyHostToDevice, st);
+  };
+  const void *s_nib, *s_sc, *s_r, *s_g;
+  // router + shared gate
+  if ((e = src(w->router_bf16, (size_t)E * H * 2, 0, &s_r)) != hipSuccess ||
+      (e = src(w->shgate_bf16, (size_t)H * 2, b_router, &s_g)) != hipSuccess ||
+      (e = dm::launch_repack_router((const uint16_t*)s_r, (const uint16_t*)s_g, router, E, H,
+                                    c->flags, st)) != hipSuccess)
+    return fail(DMH_ERR_HIP, "router upload", e);
+  if (!dev && (e = hipStreamSynchronize(st)) != hipSuccess) return fail(DMH_ERR_HIP, "sync", e);
+  struct Mat {
+    const uint8_t* nib;
+    const uint16_t* sc;
+    size_t n;
+    int R, C, nmat, tbase, per;
+    uint8_t* dn;
+    uint16_t* ds;
+  } mats[] = {
+      {w->gu_packed, w->gu_scales, n_gu, I, H, 2 * E, 0, 2, gun, gus},
+      {w->d_packed, w->d_scales, n_d, H, I, E, 2, 1, dn, ds},
+      {w->sh_gu_packed, w->sh_gu_scales, n_sgu, Ish, H, 2, 3 * E, 2, sgun, sgus},
+      {w->sh_d_packed, w->sh_d_scales, n_sd, H, Ish, 1, 3 * E + 2, 1, sdn, sds},
+  };
+  for (const Mat& m : mats) {
+    if ((e = src(m.nib, m.n / 2, 0, &s_nib)) != hipSuccess ||
+        (e = src(m.sc, m.n / G * 2, align256(m.n / 2), &s_sc)) != hipSuccess)
+      return fail(DMH_ERR_HIP, "weight copy", e);
+    // per-matrix launches keep the tensor index of the validation key in the
+    // reference's load order (gate, up, down of expert 0, then expert 1, ...)
+    const size_t mn = (size_t)m.R * m.C;
+    for (int i = 0; i < m.nmat; ++i) {
+      const int tens = m.tbase + (i / m.per) * 3 + (i % m.per);
+      e = dm::launch_repack_a16((const uint8_t*)s_nib + i * (mn / 2),
+                                (const uint16_t*)s_sc + i * (mn / G), m.dn + i * (mn / 2),
+                                m.ds + i * (mn / G), m.R, m.C, 1, tens, c->vkey, st);
+      if (e != hipSuccess) return fail(DMH_ERR_HIP, "repack", e);
+    }
+    if (!dev && (e = hipStreamSynchronize(st)) != hipSuccess) return fail(DMH_ERR_HIP, "sync", e);
+  }
+  unsigned long long vk = 0;
+  unsigned fl = 0;
+  if ((e = hipMemcpyAsync(&vk, c->vkey, sizeof(vk), hipMemcpyDeviceToHost, st)) != hipSuccess ||
+      (e = hipMemcpyAsync(&fl, c->flags, sizeof(fl), hipMemcpyDeviceToHost, st)) != hipSuccess ||
+      (e = hipStreamSynchronize(st)) != hipSuccess)
+    return fail(DMH_ERR_HIP, "validation readback", e);
+  if (vk != dm::kNoError) {
+    (void)hipFree(Ly->buf);
+    delete Ly;
+    const uint64_t sub = vk & ((1ull << 34) - 1);
+    if (sub & (1ull << 33))
+      return set_err(err, errlen, DMH_ERR_DEQUANT,
+                     "dequant_kernel: reserved nibble 0b1000 (-8) encountered");
+    if (sub & 1ull)
+      return set_err(err, errlen, DMH_ERR_DEQUANT,
+                     "dequant_kernel: scale is non-positive at group %llu",
+                     (unsigned long long)(sub >> 1));
+    return set_err(err, errlen, DMH_ERR_DEQUANT, "dequant_kernel: scale is NaN or Inf at group %llu",
+                   (unsigned long long)(sub >> 1));
+  }
+  Ly->router_w_bad = fl & 1u;
+  if (layer >= (int)c->layers.size()) c->layers.resize(layer + 1, nullptr);
+  if (c->layers[layer]) {
+    (void)hipFree(c->layers[layer]->buf);
+    delete c->layers[layer];
+  }
+  c->layers[layer] = Ly;
+  return DMH_OK;
+}
+
+int dmh_free_layer(dmh_ctx* c, int layer) {
+  Layer* Ly = get_layer(c, layer);
+  if (!Ly) return DMH_ERR_INVALID_ARG;
+  (void)hipSetDevice(c->device);
+  (void)hipStreamSynchronize(c->cur);
+  (void)hipFree(Ly->buf);
+  delete Ly;
+  c->layers[layer] = nullptr;
+  return DMH_OK;
+}
+
+int dmh_layer_bytes(dmh_ctx* c, int layer, int64_t* bytes) {
+  Layer* Ly = get_layer(c, layer);
+  if (!Ly || !bytes) return DMH_ERR_INVALID_ARG;
+  *bytes = (int64_t)Ly->bytes;
+  return DMH_OK;
+}
+
+int dmh_moe_forward(dmh_ctx* c, int layer, const float* x, const float* residual, int T,
+                    float* y, int32_t* ids, float* probs, float* shg, unsigned flags, char* err,
+                    size_t errlen) {
+  Layer* Ly = get_layer(c, layer);
+  if (!Ly)
+    return set_err(err, errlen, DMH_ERR_INVALID_ARG, "dmh_moe_forward: layer %d not uploaded",
+                   layer);
+  if (!x || !y)
+    return set_err(err, errlen, DMH_ERR_INVALID_ARG, "dmh_moe_forward: x and y are required");
+  if (T <= 0)
+    return set_err(err, errlen, DMH_ERR_ACT,
+                   "{\"error_type\":\"ACT_LOAD_FAILED\",\"detail\":\"dimensions must be"
+                   " positive\",\"stage\":\"router\",\"layer\":%d}", layer);
+  HIP_TRY(hipSetDevice(c->device));
+  const LayerDev& L = Ly->dev;
+  const size_t TH = (size_t)T * L.H, TK = (size_t)T * L.K;
+  const bool dev = flags & DMH_F_DEVICE;
+  hipStream_t st = c->cur;
+  int32_t* dids = dev ? ids : nullptr;
+  float* dprobs = dev ? probs : nullptr;
+  float* dshg = dev ? shg : nullptr;
+  if (!dids) { HIP_TRY(c->ids.ensure(TK)); dids = c->ids.p; }
+  if (!dprobs) { HIP_TRY(c->probs.ensure(TK)); dprobs = c->probs.p; }
+  if (!dshg) { HIP_TRY(c->shg.ensure(T)); dshg = c->shg.p; }
+  const float* dx = x;
+  const float* dres = residual;
+  float* dy = y;
+  if (!dev) {
+    HIP_TRY(c->x.ensure(TH));
+    HIP_TRY(c->y.ensure(TH));
+    HIP_TRY(hipMemcpyAsync(c->x.p, x, TH * 4, hipMemcpyHostToDevice, st));
+    dx = c->x.p;
+    dy = c->y.p;
+    if (residual) {
+      HIP_TRY(c->res.ensure(TH));
+      HIP_TRY(hipMemcpyAsync(c->res.p, residual, TH * 4, hipMemcpyHostToDevice, st));
+      dres = c->res.p;
+    }
+    HIP_TRY(reset_status(c, layer));
+  }
+  HIP_TRY(run_block(c, Ly, layer, dx, dres, T, dy, dids, dprobs, dshg));
+  c->last_ids[layer] = dids;
+  if (dev) return DMH_OK;
+  std::vector<int32_t> hids(TK);
+  unsigned long long key = 0;
+  HIP_TRY(hipMemcpyAsync(y, dy, TH * 4, hipMemcpyDeviceToHost, st));
+  HIP_TRY(hipMemcpyAsync(hids.data(), dids, TK * 4, hipMemcpyDeviceToHost, st));
+  if (probs) HIP_TRY(hipMemcpyAsync(probs, dprobs, TK * 4, hipMemcpyDeviceToHost, st));
+  if (shg) HIP_TRY(hipMemcpyAsync(shg, dshg, (size_t)T * 4, hipMemcpyDeviceToHost, st));
+  HIP_TRY(hipMemcpyAsync(&key, c->status + layer, sizeof(key), hipMemcpyDeviceToHost, st));
+  HIP_TRY(hipStreamSynchronize(st));
+  if (ids) memcpy(ids, hids.data(), TK * 4);
+  int rc = finish_status(c, Ly, layer, key, hids.data(), err, errlen);
+  if (rc) HIP_TRY(reset_status(c, layer));
+  return rc;
+}
+
+int dmh_moe_stack_forward(dmh_ctx* c, int first, int nl, float eps, const float* x, int T,
+                          float* out, int32_t* ids, float* probs, unsigned flags, char* err,
+                          size_t errlen) {
+  if (!c || !x || !out || nl <= 0 || T <= 0)
+    return set_err(err, errlen, DMH_ERR_INVALID_ARG, "dmh_moe_stack_forward: bad arguments");
+  if (eps != eps || eps <= 0.0f || eps > 3.0e38f)
+    return set_err(err, errlen, DMH_ERR_CONFIG,
+                   "{\"error_type\":\"CONFIG_ERROR\",\"detail\":\"rms_norm_eps must be finite"
+                   " and > 0\",\"stage\":\"config\"}");
+  Layer* L0 = get_layer(c, first);
+  if (!L0)
+    return set_err(err, errlen, DMH_ERR_INVALID_ARG, "dmh_moe_stack_forward: layer %d missing",
+                   first);
+  const int H = L0->dims.hidden, K = L0->dims.top_k;
+  for (int l = first; l < first + nl; ++l) {
+    Layer* Ly = get_layer(c, l);
+    if (!Ly || Ly->dims.hidden != H || Ly->dims.top_k != K)
+      return set_err(err, errlen, DMH_ERR_INVALID_ARG,
+                     "dmh_moe_stack_forward: layer %d missing or of another shape", l);
+  }
+  HIP_TRY(hipSetDevice(c->device));
+  const bool dev = flags & DMH_F_DEVICE;
+  hipStream_t st = c->cur;
+  const size_t TH = (size_t)T * H, TK = (size_t)T * K;
+  HIP_TRY(c->hstack.ensure(2 * TH));
+  HIP_TRY(c->xn.ensure(TH));
+  float* hA = c->hstack.p;
+  float* hB = c->hstack.p + TH;
+  HIP_TRY(hipMemcpyAsync(hA, x, TH * 4, dev ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice, st));
+  const bool own_ids = !(dev && ids), own_probs = !(dev && probs);
+  if (own_ids) HIP_TRY(c->ids.ensure(TK * nl));
+  if (own_probs) HIP_TRY(c->probs.ensure(TK * nl));
+  HIP_TRY(c->shg.ensure(T));
+  if (!dev)
+    for (int l = first; l < first + nl; ++l) HIP_TRY(reset_status(c, l));
+  for (int i = 0; i < nl; ++i) {
+    const int l = first + i;
+    int32_t* dids = (own_ids ? c->ids.p : ids) + (size_t)i * TK;
+    float* dprobs = (own_probs ? c->probs.p : probs) + (size_t)i * TK;
+    HIP_TRY(dm::launch_rmsnorm_rows(hA, T, H, eps, c->xn.p, nullptr, l, st));
+    HIP_TRY(run_block(c, c->layers[l], l, c->xn.p, hA, T, hB, dids, dprobs, c->shg.p));
+    c->last_ids[l] = dids;
+    float* tmp = hA; hA = hB; hB = tmp;
+  }
+  HIP_TRY(hipMemcpyAsync(out, hA, TH * 4, dev ? hipMemcpyDeviceToDevice : hipMemcpyDeviceToHost,
+                         st));
+  if (dev) return DMH_OK;
+  std::vector<int32_t> hids(TK * nl);
+  std::vector<unsigned long long> keys(nl);
+  HIP_TRY(hipMemcpyAsync(hids.data(), c->ids.p, TK * nl * 4, hipMemcpyDeviceToHost, st));
+  if (probs) HIP_TRY(hipMemcpyAsync(probs, c->probs.p, TK * nl * 4, hipMemcpyDeviceToHost, st));
+  HIP_TRY(hipMemcpyAsync(keys.data(), c->status + first, nl * 8, hipMemcpyDeviceToHost, st));
+  HIP_TRY(hipStreamSynchronize(st));
+  if (ids) memcpy(ids, hids.data(), TK * nl * 4);
+  for (int i = 0; i < nl; ++i) {
+    int rc = finish_status(c, c->layers[first + i], first + i, keys[i], hids.data() + i * TK, err,
+                           errlen);
+    if (rc) {
+      for (int l = first; l < first + nl; ++l) HIP_TRY(reset_status(c, l));
+      return rc;
+    }
+  }
+  return DMH_OK;
+}
+
+int dmh_router_forward(dmh_ctx* c, const float* x, const float* w, int T, int H, int E, int K,
+                       int norm, int layer, int32_t* ids, float* probs, unsigned flags, char* err,
+                       size_t errlen) {
+  if (!c || !x || !w || !ids || !probs)
+    return set_err(err, errlen, DMH_ERR_INVALID_ARG, "dmh_router_forward: NULL argument");
+  int rc = router_config_check(E, K, norm, err, errlen);
+  if (rc) return rc;
+  if (T <= 0 || H <= 0)
+    return set_err(err, errlen, DMH_ERR_ACT,
+                   "{\"error_type\":\"ACT_LOAD_FAILED\",\"detail\":\"dimensions must be"
+                   " positive\",\"stage\":\"router\",\"layer\":%d}", layer);
+  if (E > 2048)
+    return set_err(err, errlen, DMH_ERR_CONFIG,
+                   "{\"error_type\":\"CONFIG_ERROR\",\"detail\":\"num_experts > 2048 not"
+                   " supported\",\"stage\":\"router\",\"layer\":%d}", layer);
+  HIP_TRY(hipSetDevice(c->device));
+  hipStream_t st = c->cur;
+  const bool dev = flags & DMH_F_DEVICE;
+  const size_t TH = (size_t)T * H, EH = (size_t)E * H, TK = (size_t)T * K;
+  unsigned long long* status = c->status + kMaxLayers;
+  const float *dx = x, *dw = w;
+  int32_t* dids = ids;
+  float* dprobs = probs;
+  if (!dev) {
+    HIP_TRY(c->x.ensure(TH));
+    HIP_TRY(c->xn.ensure(EH));
+    HIP_TRY(c->ids.ensure(TK));
+    HIP_TRY(c->probs.ensure(TK));
+    HIP_TRY(hipMemcpyAsync(c->x.p, x, TH * 4, hipMemcpyHostToDevice, st));
+    HIP_TRY(hipMemcpyAsync(c->xn.p, w, EH * 4, hipMemcpyHostToDevice, st));
+    dx = c->x.p;
+    dw = c->xn.p;
+    dids = c->ids.p;
+    dprobs = c->probs.p;
+    HIP_TRY(reset_status(c, kMaxLayers));
+  }
+  HIP_TRY(c->z.ensure((size_t)T * E));
+  HIP_TRY(dm::launch_router_generic(dx, dw, T, H, E, c->z.p, status, st));
+  HIP_TRY(c->shg.ensure(T));
+  HIP_TRY(dm::launch_router_select(c->z.p, E, T, E, K, 0, dids, dprobs, c->shg.p, status, st));
+  if (dev) return DMH_OK;
+  unsigned long long key = 0;
+  HIP_TRY(hipMemcpyAsync(ids, dids, TK * 4, hipMemcpyDeviceToHost, st));
+  HIP_TRY(hipMemcpyAsync(probs, dprobs, TK * 4, hipMemcpyDeviceToHost, st));
+  HIP_TRY(hipMemcpyAsync(&key, status, 8, hipMemcpyDeviceToHost, st));
+  HIP_TRY(hipStreamSynchronize(st));
+  if (key == dm::kNoError) return DMH_OK;
+  HIP_TRY(reset_status(c, kMaxLayers));
+  return decode_key(key, layer, -1, E, err, errlen);
+}
+
+int dmh_dequant_q4_bf16(dmh_ctx* c, const uint16_t* scales, int64_t n_scales,
+                        const uint8_t* packed, int64_t n_packed, int64_t n, int G, uint16_t* out,
+                        unsigned flags, char* err, size_t errlen) {
+  // validation order and messages of src/quant/dequant_kernel.mojo:33-66
+  if (!(G == 32 || G == 64 || G == 128 || G == 256))
+    return set_err(err, errlen, DMH_ERR_DEQUANT,
+                   "dequant_kernel: group_size must be in {32, 64, 128, 256}, got %d", G);
+  if (n <= 0)
+    return set_err(err, errlen, DMH_ERR_DEQUANT, "dequant_kernel: num_elements must be positive");
+  if (n % G != 0)
+    return set_err(err, errlen, DMH_ERR_DEQUANT,
+                   "M6_ERR_INPUT: N %% G != 0 (tail group not supported): N=%lld, G=%d",
+                   (long long)n, G);
+  if (n_scales != n / G)
+    return set_err(err, errlen, DMH_ERR_DEQUANT,
+                   "dequant_kernel: scales length mismatch: expected %lld, got %lld",
+                   (long long)(n / G), (long long)n_scales);
+  if (n_packed != (n + 1) / 2)
+    return set_err(err, errlen, DMH_ERR_DEQUANT,
+                   "dequant_kernel: packed weights length mismatch: expected %lld, got %lld",
+                   (long long)((n + 1) / 2), (long long)n_packed);
+  if (!c || !scales || !packed || !out)
+    return set_err(err, errlen, DMH_ERR_INVALID_ARG, "dmh_dequant_q4_bf16: NULL argument");
+  HIP_TRY(hipSetDevice(c->device));
+  hipStream_t st = c->cur;
+  const bool dev = flags & DMH_F_DEVICE;
+  const uint16_t* ds = scales;
+  const uint8_t* dp = packed;
+  uint16_t* dout = out;
+  if (!dev) {
+    const size_t need = align256((size_t)n_scales * 2) + align256((size_t)n_packed) +
+                        align256((size_t)n * 2);
+    HIP_TRY(c->stage.ensure(need));
+    uint8_t* b = c->stage.p;
+    HIP_TRY(hipMemcpyAsync(b, scales, n_scales * 2, hipMemcpyHostToDevice, st));
+    HIP_TRY(hipMemcpyAsync(b + align256(n_scales * 2), packed, n_packed, hipMemcpyHostToDevice, st));
+    ds = (const uint16_t*)b;
+    dp = b + align256(n_scales * 2);
+    dout = (uint16_t*)(b + align256(n_scales * 2) + align256(n_packed));
+  }
+  HIP_TRY(hipMemsetAsync(c->vkey, 0xFF, 8, st));
+  HIP_TRY(dm::launch_dequant_ref(ds, dp, n, G, dout, c->vkey, st));
+  unsigned long long vk = 0;
+  HIP_TRY(hipMemcpyAsync(&vk, c->vkey, 8, hipMemcpyDeviceToHost, st));
+  if (!dev) HIP_TRY(hipMemcpyAsync(out, dout, (size_t)n * 2, hipMemcpyDeviceToHost, st));
+  HIP_TRY(hipStreamSynchronize(st));
+  if (vk == dm::kNoError) return DMH_OK;
+  if (vk == (1ull << 40))
+    return set_err(err, errlen, DMH_ERR_DEQUANT,
+                   "dequant_kernel: reserved nibble 0b1000 (-8) encountered");
+  if (vk & 1ull)
+    return set_err(err, errlen, DMH_ERR_DEQUANT, "dequant_kernel: scale is non-positive at group %llu",
+                   (unsigned long long)(vk >> 1));
+  return set_err(err, errlen, DMH_ERR_DEQUANT, "dequant_kernel: scale is NaN or Inf at group %llu",
+                 (unsigned long long)(vk >> 1));
+}
+
+}  // extern "C"

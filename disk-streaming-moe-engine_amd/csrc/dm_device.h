@@ -1,0 +1,130 @@
+// dm_device.h -- gfx950 device helpers shared by the MoE kernels.
+//
+// The library is compiled with -ffp-contract=off: every multiply and add in
+// this file rounds on its own unless written as an explicit fused
+// multiply-add, which keeps the router, softmax and gate arithmetic
+// bit-identical to the CPU restatement of the reference.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "dm_layout.h"
+
+namespace dm {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float u2f(uint32_t u) { return __builtin_bit_cast(float, u); }
+__device__ __forceinline__ uint32_t f2u(float f) { return __builtin_bit_cast(uint32_t, f); }
+__device__ __forceinline__ bool finite_f(float v) { return (f2u(v) & 0x7F800000u) != 0x7F800000u; }
+__device__ __forceinline__ float bf16lo(uint32_t w) { return u2f(w << 16); }
+__device__ __forceinline__ float bf16hi(uint32_t w) { return u2f(w & 0xFFFF0000u); }
+
+// exp(x): Cody & Waite reduction x = k*ln2 + r with a 15-bit ln2 head, the
+// degree-7 Taylor polynomial of exp(r) in Horner form with fused
+// multiply-adds, and scaling by 2^k through the exponent field.  The CPU
+// oracle evaluates the same operation sequence.
+__device__ __forceinline__ float dm_expf(float x) {
+  if (x != x) return x;
+  if (x > 0x1.62e43p+6f) return __builtin_inff();
+  if (x < -0x1.9fe36ap+6f) return 0.0f;
+  float kf = __builtin_rintf(x * 0x1.715476p+0f);
+  float r = __builtin_fmaf(kf, -0x1.62e4p-1f, x);
+  r = __builtin_fmaf(kf, -0x1.7f7d1cp-20f, r);
+  float p = 0x1.a01a02p-13f;
+  p = __builtin_fmaf(p, r, 0x1.6c16c2p-10f);
+  p = __builtin_fmaf(p, r, 0x1.111112p-7f);
+  p = __builtin_fmaf(p, r, 0x1.555556p-5f);
+  p = __builtin_fmaf(p, r, 0x1.555556p-3f);
+  p = __builtin_fmaf(p, r, 0x1p-1f);
+  p = __builtin_fmaf(p, r, 1.0f);
+  p = __builtin_fmaf(p, r, 1.0f);
+  int k = (int)kf;
+  if (k > 127) {
+    p = p * 0x1p127f;
+    k -= 127;
+  }
+  if (k < -126) {
+    p = p * u2f((uint32_t)(k + 227) << 23);
+    return p * 0x1p-100f;
+  }
+  return p * u2f((uint32_t)(k + 127) << 23);
+}
+
+// sigmoid_f32 / silu_f32 of src/layers/swiglu.mojo:11-38
+__device__ __forceinline__ float dm_sigmoid(float z) {
+  if (z != z) return z;
+  if (z < -88.0f) return 0.0f;
+  if (z > 88.0f) return 1.0f;
+  if (z < 0.0f) {
+    float ez = dm_expf(z);
+    return ez / (1.0f + ez);
+  }
+  return 1.0f / (1.0f + dm_expf(-z));
+}
+__device__ __forceinline__ float dm_silu(float z) {
+  if (z != z) return z;
+  if (!finite_f(z)) return z > 0.0f ? z : 0.0f;
+  return z * dm_sigmoid(z);
+}
+
+// Round-to-nearest-even fp32 -> bf16 pair packed as (lo, hi).
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  bf16x2 v = {(__bf16)lo, (__bf16)hi};
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+// Split eight fp32 activations into bf16 hi and lo parts (x ~= hi + lo with
+// a relative error below 2^-17), packed as MFMA B-operand lanes.
+__device__ __forceinline__ void split8(const float* v, uint4& hi, uint4& lo) {
+  float h[8], l[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    uint32_t hb = pack_bf16x2(v[i], 0.0f) & 0xFFFFu;
+    h[i] = u2f(hb << 16);
+    l[i] = v[i] - h[i];
+  }
+  hi = make_uint4(pack_bf16x2(h[0], h[1]), pack_bf16x2(h[2], h[3]), pack_bf16x2(h[4], h[5]),
+                  pack_bf16x2(h[6], h[7]));
+  lo = make_uint4(pack_bf16x2(l[0], l[1]), pack_bf16x2(l[2], l[3]), pack_bf16x2(l[4], l[5]),
+                  pack_bf16x2(l[6], l[7]));
+}
+
+// Dequantise one A16 word (8 codes of one group, one lane) to the bf16
+// A-operand: w = bf16_rne(fp32(s) * q), as src/quant/dequant_kernel.mojo:110-115.
+// The half 0x6400|u is 1024+u exactly, and fma(1024+u, s, -1032*s) equals
+// s*(u-8) = s*q exactly (both products fit the fp32 significand), so the
+// only rounding is the final bf16 RNE.
+__device__ __forceinline__ bf16x8 dequant8(uint32_t w, float s) {
+  const uint32_t M = 0x000F000Fu, O = 0x64006400u;
+  float c0 = -1032.0f * s;
+  uint32_t r[4] = {(w & M) | O, ((w >> 4) & M) | O, ((w >> 8) & M) | O, ((w >> 12) & M) | O};
+  uint32_t o[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    half2v h = __builtin_bit_cast(half2v, r[i]);
+    float a = __builtin_fmaf((float)h.x, s, c0);
+    float b = __builtin_fmaf((float)h.y, s, c0);
+    o[i] = pack_bf16x2(a, b);
+  }
+  uint4 v = make_uint4(o[0], o[1], o[2], o[3]);
+  return __builtin_bit_cast(bf16x8, v);
+}
+
+__device__ __forceinline__ float fp16_bits_to_f32(uint32_t h16) {
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)h16);
+}
+
+__device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+// Record a first-error key (integer atomic: order independent).
+__device__ __forceinline__ void record_err(unsigned long long* status, uint64_t key) {
+  atomicMin(status, (unsigned long long)key);
+}
+
+}  // namespace dm

@@ -1,0 +1,44 @@
+// dm_kernels.h -- host-side launchers for the kernels in dm_kernels.hip.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "dm_layout.h"
+
+namespace dm {
+
+// ---- upload-time re-tiling and validation ----
+// nmat matrices [R][C] in the reference 4-bit layout -> A16.  Invalid scales
+// or reserved codes record (tensor << 34 | sub) into *vkey (atomicMin).
+hipError_t launch_repack_a16(const uint8_t* src_nib, const uint16_t* src_sc, uint8_t* dst_nib,
+                             uint16_t* dst_sc, int R, int C, int nmat, int tensor_base,
+                             unsigned long long* vkey, hipStream_t st);
+// router [E][H] bf16 + shared gate [H] bf16 -> R16 (E+1 rows).  Non-finite
+// router weights set bit 0 of *flags.
+hipError_t launch_repack_router(const uint16_t* router, const uint16_t* shgate, uint16_t* dst,
+                                int E, int H, unsigned* flags, hipStream_t st);
+
+// ---- unit entry points ----
+hipError_t launch_dequant_ref(const uint16_t* scales, const uint8_t* packed, int64_t n,
+                              int group, uint16_t* out, unsigned long long* vkey,
+                              hipStream_t st);
+hipError_t launch_router_generic(const float* x, const float* w, int T, int H, int E, float* z,
+                                 unsigned long long* status, hipStream_t st);
+
+// ---- decode path (one token per launch set) ----
+hipError_t launch_router_dec(const LayerDev& L, const float* x, int T, float* z,
+                             unsigned long long* status, hipStream_t st);
+hipError_t launch_router_select(const float* z, int ldz, int T, int E, int K, int has_sh,
+                                int32_t* ids, float* probs, float* shg,
+                                unsigned long long* status, hipStream_t st);
+hipError_t launch_gateup_dec(const LayerDev& L, const float* x, const int32_t* ids, float* h,
+                             int ldh, int token, unsigned long long* status, hipStream_t st);
+hipError_t launch_down_dec(const LayerDev& L, const float* h, int ldh, const int32_t* ids,
+                           const float* probs, const float* shg, const float* residual,
+                           float* y, int token, unsigned long long* status, hipStream_t st);
+
+// ---- glue ----
+hipError_t launch_rmsnorm_rows(const float* x, int T, int H, float eps, float* out,
+                               unsigned long long* status, int layer_tag, hipStream_t st);
+
+}  // namespace dm

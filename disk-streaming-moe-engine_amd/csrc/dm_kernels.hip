@@ -1,0 +1,606 @@
+// dm_kernels.hip -- gfx950 kernels of the MoE FFN block (router, top-k,
+// 4-bit SwiGLU experts, shared expert, combine) and their upload helpers.
+//
+// Reference path (CPU, Mojo): src/layers/router.mojo:15-210,
+// src/layers/topk.mojo:11-133, src/layers/swiglu.mojo:11-230,
+// src/layers/moe.mojo:17-177, src/layers/forward_layer.mojo:181-247,
+// src/quant/dequant_kernel.mojo:22-155.
+#include <hip/hip_runtime.h>
+
+#include "dm_device.h"
+#include "dm_kernels.h"
+
+namespace dm {
+
+// ===========================================================================
+// Upload: reference 4-bit layout -> A16 tiles, with the validation of
+// src/quant/dequant_kernel.mojo:68-108 (scale NaN/Inf, scale <= 0, code -8).
+// One thread per (matrix, tile, lane): reads 4 aligned words of the source
+// row (32 codes per word group), writes 16 bytes; q == 0 lanes move scales.
+// Validation key: tensor << 34 | (2*group + kind) for scale errors
+// (kind 0 NaN/Inf, 1 non-positive), tensor << 34 | 1 << 33 for code -8.
+// ===========================================================================
+__global__ __launch_bounds__(256) void k_repack_a16(const uint8_t* __restrict__ src_nib,
+                                                     const uint16_t* __restrict__ src_sc,
+                                                     uint8_t* __restrict__ dst_nib,
+                                                     uint16_t* __restrict__ dst_sc, int R, int C,
+                                                     int nmat, int tensor_base,
+                                                     unsigned long long* vkey) {
+  const int nRB = R / kTileRows, nGQ = C / kQuadCols;
+  const int64_t per_mat = (int64_t)nRB * nGQ * 64;
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (gid >= per_mat * nmat) return;
+  const int m = (int)(gid / per_mat);
+  int64_t rem = gid - (int64_t)m * per_mat;
+  const int lane = (int)(rem & 63);
+  rem >>= 6;
+  const int gq = (int)(rem % nGQ);
+  const int rb = (int)(rem / nGQ);
+  const int r = lane & 15, q = lane >> 4;
+  const int row = rb * kTileRows + r;
+  const size_t mat_nib = (size_t)R * C / 2, mat_sc = (size_t)R * C / kGroup;
+  const uint8_t* sn = src_nib + (size_t)m * mat_nib;
+  const uint16_t* ss = src_sc + (size_t)m * mat_sc;
+  uint32_t out[4];
+  bool reserved = false;
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    const int g = gq * 4 + c;
+    const size_t e0 = (size_t)row * C + (size_t)g * kGroup + 8 * q;  // first element
+    const uint32_t win = *reinterpret_cast<const uint32_t*>(sn + e0 / 2);
+    uint32_t wo = 0;
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk) {
+      const uint32_t nib = (win >> (4 * kk)) & 0xFu;  // element e0+kk (low nibble = even)
+      reserved |= (nib == 8u);
+      wo |= (nib ^ 8u) << (4 * a16_slot_of_kk(kk));
+    }
+    out[c] = wo;
+  }
+  *reinterpret_cast<uint4*>(dst_nib + (size_t)m * mat_nib + a16_nib_offset(nGQ, rb, gq, lane)) =
+      make_uint4(out[0], out[1], out[2], out[3]);
+  uint64_t key = kNoError;
+  const uint64_t tens = (uint64_t)(tensor_base + m) << 34;
+  if (reserved) key = tens | (1ull << 33);
+  if (q == 0) {
+    uint16_t sv[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int g = gq * 4 + c;
+      const size_t gidx = (size_t)row * (C / kGroup) + g;  // group index inside the tensor
+      const uint16_t u = ss[gidx];
+      sv[c] = u;
+      uint64_t k2 = kNoError;
+      if (((u >> 10) & 0x1Fu) == 0x1Fu) k2 = tens | (2ull * gidx);
+      else if ((u & 0x8000u) || (u & 0x7FFFu) == 0) k2 = tens | (2ull * gidx + 1);
+      if (k2 < key) key = k2;
+    }
+    uint2 pk = make_uint2((uint32_t)sv[0] | ((uint32_t)sv[1] << 16),
+                          (uint32_t)sv[2] | ((uint32_t)sv[3] << 16));
+    *reinterpret_cast<uint2*>(dst_sc + (size_t)m * mat_sc + a16_sc_offset(nGQ, rb, gq, r)) = pk;
+  }
+  if (key != kNoError) atomicMin(vkey, (unsigned long long)key);
+}
+
+hipError_t launch_repack_a16(const uint8_t* src_nib, const uint16_t* src_sc, uint8_t* dst_nib,
+                             uint16_t* dst_sc, int R, int C, int nmat, int tensor_base,
+                             unsigned long long* vkey, hipStream_t st) {
+  const int64_t n = (int64_t)(R / kTileRows) * (C / kQuadCols) * 64 * nmat;
+  if (n <= 0) return hipSuccess;
+  const int64_t blocks = (n + 255) / 256;
+  hipLaunchKernelGGL(k_repack_a16, dim3((unsigned)blocks), dim3(256), 0, st, src_nib, src_sc,
+                     dst_nib, dst_sc, R, C, nmat, tensor_base, vkey);
+  return hipGetLastError();
+}
+
+__global__ __launch_bounds__(256) void k_repack_router(const uint16_t* __restrict__ router,
+                                                        const uint16_t* __restrict__ shgate,
+                                                        uint16_t* __restrict__ dst, int E, int H,
+                                                        unsigned* flags) {
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (gid >= (int64_t)(E + 1) * H) return;
+  const int e = (int)(gid / H), k = (int)(gid % H);
+  uint16_t v;
+  if (e < E) {
+    v = router[gid];
+    if ((v & 0x7F80u) == 0x7F80u) atomicOr(flags, 1u);  // bf16 NaN/Inf
+  } else {
+    v = shgate[k];
+  }
+  dst[r16_index(H, e, k)] = v;
+}
+
+hipError_t launch_repack_router(const uint16_t* router, const uint16_t* shgate, uint16_t* dst,
+                                int E, int H, unsigned* flags, hipStream_t st) {
+  const int64_t n = (int64_t)(E + 1) * H;
+  hipLaunchKernelGGL(k_repack_router, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
+                     router, shgate, dst, E, H, flags);
+  return hipGetLastError();
+}
+
+// ===========================================================================
+// Unit dequant (dequant_kernel_simd, src/quant/dequant_kernel.mojo:22-124):
+// reference layout in, bf16 out.  Each thread owns 8 codes (4 bytes).
+// vkey: scale errors 2*group+kind (kind 0 NaN/Inf, 1 <= 0); code -8 -> 1<<40.
+// ===========================================================================
+__global__ __launch_bounds__(256) void k_dequant_ref(const uint16_t* __restrict__ scales,
+                                                      const uint8_t* __restrict__ packed, int64_t n,
+                                                      int group, uint16_t* __restrict__ out,
+                                                      unsigned long long* vkey) {
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t e0 = gid * 8;
+  if (e0 >= n) return;
+  const int64_t g = e0 / group;
+  const uint16_t su = scales[g];
+  uint64_t key = kNoError;
+  if (e0 % group == 0) {  // one thread per group checks its scale
+    if (((su >> 10) & 0x1Fu) == 0x1Fu) key = 2ull * g;
+    else if ((su & 0x8000u) || (su & 0x7FFFu) == 0) key = 2ull * g + 1;
+  }
+  const float s = fp16_bits_to_f32(su);
+  const uint32_t w = *reinterpret_cast<const uint32_t*>(packed + e0 / 2);
+  uint32_t o[4];
+  bool bad = false;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t b = (w >> (8 * i)) & 0xFFu;
+    const int lo = (int)((b & 0xFu) ^ 8u) - 8;  // sign-extended low nibble
+    const int hi = (int)((b >> 4) ^ 8u) - 8;
+    bad |= (lo == -8) | (hi == -8);
+    o[i] = pack_bf16x2(s * (float)lo, s * (float)hi);
+  }
+  if (bad && (1ull << 40) < key) key = 1ull << 40;
+  *reinterpret_cast<uint4*>(out + e0) = make_uint4(o[0], o[1], o[2], o[3]);
+  if (key != kNoError) atomicMin(vkey, (unsigned long long)key);
+}
+
+hipError_t launch_dequant_ref(const uint16_t* scales, const uint8_t* packed, int64_t n,
+                              int group, uint16_t* out, unsigned long long* vkey,
+                              hipStream_t st) {
+  const int64_t threads = n / 8;
+  hipLaunchKernelGGL(k_dequant_ref, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st,
+                     scales, packed, n, group, out, vkey);
+  return hipGetLastError();
+}
+
+// ===========================================================================
+// Router logits with the association order of router_project
+// (src/layers/router.mojo:80-104): 16 strided lane partials accumulated
+// sequentially, halving tree, scalar tail.
+// ===========================================================================
+
+// Generic form for the unit entry point: fp32 weights [E][H], any H.  One
+// thread per (token, expert) replays the 16 lanes in registers.
+__global__ __launch_bounds__(128) void k_router_generic(const float* __restrict__ x,
+                                                         const float* __restrict__ w, int T,
+                                                         int H, int E, float* __restrict__ z,
+                                                         unsigned long long* status) {
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  // activation and weight scans (router.mojo:57-72)
+  for (int64_t i = gid; i < (int64_t)T * H; i += (int64_t)gridDim.x * blockDim.x)
+    if (!finite_f(x[i])) record_err(status, err_key(kPhX, 0, 0, 0, 0));
+  for (int64_t i = gid; i < (int64_t)E * H; i += (int64_t)gridDim.x * blockDim.x)
+    if (!finite_f(w[i])) record_err(status, err_key(kPhRouterW, 0, 0, 0, 0));
+  if (gid >= (int64_t)T * E) return;
+  const int t = (int)(gid / E), e = (int)(gid % E);
+  const float* xr = x + (int64_t)t * H;
+  const float* wr = w + (int64_t)e * H;
+  float acc[16];
+#pragma unroll
+  for (int l = 0; l < 16; ++l) acc[l] = 0.0f;
+  int k = 0;
+  for (; k + 16 <= H; k += 16)
+#pragma unroll
+    for (int l = 0; l < 16; ++l) acc[l] = acc[l] + xr[k + l] * wr[k + l];
+#pragma unroll
+  for (int wdt = 8; wdt >= 1; wdt >>= 1)
+#pragma unroll
+    for (int l = 0; l < wdt; ++l) acc[l] = acc[l] + acc[l + wdt];
+  float s = acc[0];
+  for (; k < H; ++k) s = s + xr[k] * wr[k];
+  if (!finite_f(s)) record_err(status, err_key(kPhLogit, t, 0, e, 0));
+  z[(int64_t)t * E + e] = s;
+}
+
+hipError_t launch_router_generic(const float* x, const float* w, int T, int H, int E, float* z,
+                                 unsigned long long* status, hipStream_t st) {
+  const int64_t n = (int64_t)T * E;
+  hipLaunchKernelGGL(k_router_generic, dim3((unsigned)((n + 127) / 128)), dim3(128), 0, st, x, w,
+                     T, H, E, z, status);
+  return hipGetLastError();
+}
+
+// Layer form: R16 bf16 weights with E+1 rows (row E = shared-expert gate,
+// which shared_gate_forward, src/layers/moe.mojo:70-100, reduces in the same
+// 16-lane order).  One lane per (row, chain l); 16 rows per 256-thread block;
+// blockIdx.y = token.  x is staged in LDS once per block.
+__global__ __launch_bounds__(256) void k_router_dec(LayerDev L, const float* __restrict__ x,
+                                                     float* __restrict__ z,
+                                                     unsigned long long* status) {
+  extern __shared__ float xs[];
+  const int H = L.H, t = blockIdx.y;
+  const float* xr = x + (size_t)t * H;
+  bool bad = false;
+  for (int i = threadIdx.x; i < H; i += 256) {
+    const float v = xr[i];
+    bad |= !finite_f(v);
+    xs[i] = v;
+  }
+  if (bad && blockIdx.x == 0) record_err(status, err_key(kPhX, 0, 0, 0, 0));
+  __syncthreads();
+  const int l = threadIdx.x & 15;
+  const int e = blockIdx.x * 16 + (threadIdx.x >> 4);
+  float acc = 0.0f;
+  if (e <= L.E) {
+    const uint4* wp = reinterpret_cast<const uint4*>(L.router + r16_index(H, e, l));
+    const int nj8 = H / 128;
+    for (int j8 = 0; j8 < nj8; ++j8) {
+      const uint4 w = wp[(size_t)j8 * 16];
+      const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+      const float* xc = xs + j8 * 128 + l;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        acc = acc + xc[(2 * i) * 16] * bf16lo(ww[i]);
+        acc = acc + xc[(2 * i + 1) * 16] * bf16hi(ww[i]);
+      }
+    }
+  }
+  // halving tree over the 16 chains of a row: lane l += lane l + w
+#pragma unroll
+  for (int wdt = 8; wdt >= 1; wdt >>= 1) acc = acc + __shfl_down(acc, wdt, 16);
+  if (l == 0 && e <= L.E) z[(size_t)t * (L.E + 1) + e] = acc;
+}
+
+hipError_t launch_router_dec(const LayerDev& L, const float* x, int T, float* z,
+                             unsigned long long* status, hipStream_t st) {
+  const int blocks = (L.E + 1 + 15) / 16;
+  hipLaunchKernelGGL(k_router_dec, dim3(blocks, T), dim3(256), (size_t)L.H * sizeof(float), st, L,
+                     x, z, status);
+  return hipGetLastError();
+}
+
+// ===========================================================================
+// Softmax + top-k + shared gate, one 64-lane wave per token:
+// router_softmax (src/layers/router.mojo:140-183: sequential max, exp, sum,
+// p = e * (1/sum)) and select_topk (src/layers/topk.mojo:79-128: largest p,
+// lowest expert id on ties, K rounds; sum and renormalisation-leak checks).
+// ===========================================================================
+__device__ __forceinline__ bool better(float va, int ia, float vb, int ib) {
+  return va > vb || (va == vb && ia < ib);
+}
+
+__global__ __launch_bounds__(64) void k_router_select(const float* __restrict__ z, int ldz, int E,
+                                                       int K, int has_sh,
+                                                       int32_t* __restrict__ ids,
+                                                       float* __restrict__ probs,
+                                                       float* __restrict__ shg,
+                                                       unsigned long long* status) {
+  extern __shared__ float sm[];  // p[E], then 2 scalars
+  float* pv = sm;
+  float* scal = sm + E;
+  const int t = blockIdx.x, lane = threadIdx.x;
+  const float* zr = z + (size_t)t * ldz;
+  float m = -__builtin_inff();
+  for (int e = lane; e < E; e += 64) {
+    const float v = zr[e];
+    if (!finite_f(v)) record_err(status, err_key(kPhLogit, t, 0, e, 0));
+    m = v > m ? v : m;
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    const float other = __shfl_xor(m, o);
+    m = other > m ? other : m;
+  }
+  if (lane == 0 && !finite_f(m)) record_err(status, err_key(kPhSoftmax, t, 0, 0, 0));
+  for (int e = lane; e < E; e += 64) {
+    const float ev = dm_expf(zr[e] - m);
+    if (!finite_f(ev)) record_err(status, err_key(kPhSoftmax, t, 0, 1 + e, 0));
+    pv[e] = ev;
+  }
+  __syncthreads();
+  if (lane == 0) {
+    float s = 0.0f;
+    for (int e = 0; e < E; ++e) s = s + pv[e];
+    if (!(s > 0.0f) || !finite_f(s)) record_err(status, err_key(kPhSoftmax, t, 0, 1 + E, 0));
+    scal[0] = 1.0f / s;
+  }
+  __syncthreads();
+  const float inv = scal[0];
+  for (int e = lane; e < E; e += 64) pv[e] = pv[e] * inv;
+  __syncthreads();
+  // K rounds of wave-wide (p desc, id asc) argmax over unselected experts.
+  uint32_t taken = 0;  // bit i: element lane + 64*i selected (E <= 2048)
+  float sum_topk = 0.0f;
+  for (int i = 0; i < K; ++i) {
+    float bv = -1.0f;
+    int bi = 0x7FFFFFFF;
+    for (int e = lane, s = 0; e < E; e += 64, ++s) {
+      if (taken >> s & 1u) continue;
+      const float v = pv[e];
+      if (better(v, e, bv, bi)) { bv = v; bi = e; }
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+      const float ov = __shfl_xor(bv, o);
+      const int oi = __shfl_xor(bi, o);
+      if (better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
+    }
+    if (bi < 0 || bi >= E) bi = 0;  // only reachable after a recorded error
+    if ((bi & 63) == lane) taken |= 1u << (bi >> 6);
+    sum_topk = sum_topk + bv;
+    if (lane == 0) {
+      ids[(size_t)t * K + i] = bi;
+      probs[(size_t)t * K + i] = bv;
+    }
+  }
+  if (lane == 0) {
+    if (sum_topk > 1.00001f) record_err(status, err_key(kPhTopk, t, 0, 0, kTkSum));
+    if (K < E && __builtin_fabsf(sum_topk - 1.0f) < 1e-6f) {
+      float sum_all = 0.0f;
+      for (int e = 0; e < E; ++e) sum_all = sum_all + pv[e];
+      if (sum_all - sum_topk > 1e-5f) record_err(status, err_key(kPhTopk, t, 0, 0, kTkLeak));
+    }
+    if (has_sh) {
+      const float lg = zr[E];
+      if (!finite_f(lg)) record_err(status, err_key(kPhGate, t, 0, 0, kGkLogit));
+      const float s = dm_sigmoid(lg);
+      if (!finite_f(s) || s < 0.0f || s > 1.0f)
+        record_err(status, err_key(kPhGate, t, 0, 0, kGkRange));
+      shg[t] = s;
+    }
+  }
+}
+
+hipError_t launch_router_select(const float* z, int ldz, int T, int E, int K, int has_sh,
+                                int32_t* ids, float* probs, float* shg,
+                                unsigned long long* status, hipStream_t st) {
+  hipLaunchKernelGGL(k_router_select, dim3(T), dim3(64), (size_t)(E + 2) * sizeof(float), st, z,
+                     ldz, E, K, has_sh, ids, probs, shg, status);
+  return hipGetLastError();
+}
+
+// ===========================================================================
+// Decode gate/up: h = SiLU(W_gate x) * (W_up x) for the K routed experts and
+// the shared expert (src/layers/swiglu.mojo:134-201, fp32 h).  Block =
+// (slot, 16-row tile); its 4 waves split the 128-column chunks of the
+// reduction and meet in LDS.  Each MFMA step dequantises one group of the
+// 16 rows into bf16 (bit-exact bf16_rne(s*q)) and multiplies it by the
+// activation split into bf16 hi/lo columns 0 and 1 of the B operand.
+// ===========================================================================
+struct ExpertView {
+  const uint8_t* nib;   // A16 matrix
+  const uint16_t* sc;
+  int rows, cols;
+};
+
+__device__ __forceinline__ void load_chunk(const ExpertView& v, int rb, int gq, int lane,
+                                           uint4& w, uint2& s) {
+  const int nGQ = v.cols / kQuadCols;
+  w = *reinterpret_cast<const uint4*>(v.nib + a16_nib_offset(nGQ, rb, gq, lane));
+  s = *reinterpret_cast<const uint2*>(v.sc + a16_sc_offset(nGQ, rb, gq, lane & 15));
+}
+
+__device__ __forceinline__ float scale_of(const uint2& s, int c) {
+  const uint32_t word = c < 2 ? s.x : s.y;
+  return fp16_bits_to_f32((c & 1) ? (word >> 16) : (word & 0xFFFFu));
+}
+
+__device__ __forceinline__ uint32_t word_of(const uint4& w, int c) {
+  return c == 0 ? w.x : c == 1 ? w.y : c == 2 ? w.z : w.w;
+}
+
+// Stage an fp32 vector v[n] (n % 32 == 0) as B-operand blocks in LDS:
+// blk[(g*4 + q)*3 + {0: hi, 1: lo, 2: zero}] holds columns 32g+8q..+7.
+__device__ __forceinline__ void stage_split(const float* __restrict__ v, int n, uint4* blk) {
+  for (int i = threadIdx.x; i < n / 8; i += blockDim.x) {
+    float f[8];
+    const float4 a = reinterpret_cast<const float4*>(v)[2 * i];
+    const float4 b = reinterpret_cast<const float4*>(v)[2 * i + 1];
+    f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w;
+    f[4] = b.x; f[5] = b.y; f[6] = b.z; f[7] = b.w;
+    uint4 hi, lo;
+    split8(f, hi, lo);
+    blk[3 * i + 0] = hi;
+    blk[3 * i + 1] = lo;
+    blk[3 * i + 2] = make_uint4(0, 0, 0, 0);
+  }
+}
+
+// Columns 0 (hi) + 1 (lo) of an MFMA accumulator: after the exchange, lanes
+// with (lane & 15) == 0 hold rows 4*(lane>>4) + i.
+__device__ __forceinline__ void fold_cols(f32x4& acc) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) acc[i] = acc[i] + __shfl_xor(acc[i], 1);
+}
+
+__global__ __launch_bounds__(256) void k_gateup_dec(LayerDev L, const float* __restrict__ x,
+                                                     const int32_t* __restrict__ ids,
+                                                     float* __restrict__ hout, int ldh, int token,
+                                                     unsigned long long* status) {
+  extern __shared__ uint4 xb[];  // (H/8)*3 blocks
+  __shared__ float red[4][2][16];
+  const int H = L.H;
+  const int nrb_r = L.I / kTileRows;
+  int slot, rb, I;
+  ExpertView gv, uv;
+  if ((int)blockIdx.x < L.K * nrb_r) {
+    slot = blockIdx.x / nrb_r;
+    rb = blockIdx.x % nrb_r;
+    I = L.I;
+    int e = ids[slot];
+    if (e < 0 || e >= L.E) e = 0;  // invalid ids come with a recorded router error
+    const size_t mat = (size_t)I * H;
+    gv = {L.gu_nib + (size_t)e * mat, L.gu_sc + (size_t)e * 2 * (mat / kGroup), I, H};
+    uv = {gv.nib + mat / 2, gv.sc + mat / kGroup, I, H};
+  } else {
+    slot = L.K;
+    rb = blockIdx.x - L.K * nrb_r;
+    I = L.Ish;
+    const size_t mat = (size_t)I * H;
+    gv = {L.sgu_nib, L.sgu_sc, I, H};
+    uv = {L.sgu_nib + mat / 2, L.sgu_sc + mat / kGroup, I, H};
+  }
+  stage_split(x, H, xb);
+  __syncthreads();
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int q = lane >> 4, j = lane & 15, jsel = j < 2 ? j : 2;
+  const int nGQ = H / kQuadCols;
+  f32x4 ag = {0, 0, 0, 0}, au = {0, 0, 0, 0};
+  for (int gq = w; gq < nGQ; gq += 4) {
+    uint4 wg, wu;
+    uint2 sg, su;
+    load_chunk(gv, rb, gq, lane, wg, sg);
+    load_chunk(uv, rb, gq, lane, wu, su);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int g = gq * 4 + c;
+      const bf16x8 b = __builtin_bit_cast(bf16x8, xb[(g * 4 + q) * 3 + jsel]);
+      ag = mfma16(dequant8(word_of(wg, c), scale_of(sg, c)), b, ag);
+      au = mfma16(dequant8(word_of(wu, c), scale_of(su, c)), b, au);
+    }
+  }
+  fold_cols(ag);
+  fold_cols(au);
+  if (j == 0) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      red[w][0][4 * q + i] = ag[i];
+      red[w][1][4 * q + i] = au[i];
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x < 16) {
+    const int r = threadIdx.x, row = rb * kTileRows + r;
+    const float g = ((red[0][0][r] + red[1][0][r]) + red[2][0][r]) + red[3][0][r];
+    const float u = ((red[0][1][r] + red[1][1][r]) + red[2][1][r]) + red[3][1][r];
+    const uint32_t ph = slot < L.K ? kPhExpert : kPhShared;
+    const uint32_t sl = slot < L.K ? slot : 0;
+    if (!finite_f(g)) record_err(status, err_key(ph, token, sl, row, kEkGate));
+    if (!finite_f(u)) record_err(status, err_key(ph, token, sl, row, kEkUp));
+    const float h = dm_silu(g) * u;
+    if (!finite_f(h)) record_err(status, err_key(ph, token, sl, row, kEkH));
+    hout[(size_t)slot * ldh + row] = h;
+  }
+}
+
+hipError_t launch_gateup_dec(const LayerDev& L, const float* x, const int32_t* ids, float* h,
+                             int ldh, int token, unsigned long long* status, hipStream_t st) {
+  const int blocks = L.K * (L.I / kTileRows) + L.Ish / kTileRows;
+  hipLaunchKernelGGL(k_gateup_dec, dim3(blocks), dim3(256), (size_t)(L.H / 8) * 3 * sizeof(uint4),
+                     st, L, x, ids, h, ldh, token, status);
+  return hipGetLastError();
+}
+
+// ===========================================================================
+// Decode down projection + combine: y_d = sum_k p_k (W_down_k h_k)_d
+// + g_sh (W_down_sh h_sh)_d (+ residual), k in routed order first, then the
+// shared expert, then the residual (src/layers/moe.mojo:157-166,
+// src/layers/forward_layer.mojo:226-238).  Block = 16 output rows; wave w
+// owns slots w, w+4, ...; the combine is one ordered pass, no atomics.
+// ===========================================================================
+__global__ __launch_bounds__(256) void k_down_dec(LayerDev L, const float* __restrict__ hin,
+                                                   int ldh, const int32_t* __restrict__ ids,
+                                                   const float* __restrict__ probs,
+                                                   const float* __restrict__ shg,
+                                                   const float* __restrict__ residual,
+                                                   float* __restrict__ y, int token,
+                                                   unsigned long long* status) {
+  extern __shared__ uint4 hb[];  // (K+1) * (ldh/8) * 3 blocks
+  __shared__ float red[33][16];
+  const int H = L.H, K = L.K;
+  const int rb = blockIdx.x;
+  const int nblk_slot = (ldh / 8) * 3;
+  for (int s = 0; s <= K; ++s) {
+    const int Is = s < K ? L.I : L.Ish;
+    stage_split(hin + (size_t)s * ldh, Is, hb + (size_t)s * nblk_slot);
+  }
+  __syncthreads();
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int q = lane >> 4, j = lane & 15, jsel = j < 2 ? j : 2;
+  for (int s = w; s <= K; s += 4) {
+    ExpertView dv;
+    if (s < K) {
+      int e = ids[s];
+      if (e < 0 || e >= L.E) e = 0;
+      const size_t mat = (size_t)H * L.I;
+      dv = {L.d_nib + (size_t)e * (mat / 2), L.d_sc + (size_t)e * (mat / kGroup), H, L.I};
+    } else {
+      dv = {L.sd_nib, L.sd_sc, H, L.Ish};
+    }
+    const int nGQ = dv.cols / kQuadCols;
+    const uint4* hbs = hb + (size_t)s * nblk_slot;
+    f32x4 acc = {0, 0, 0, 0};
+    for (int gq = 0; gq < nGQ; ++gq) {
+      uint4 wd;
+      uint2 sd;
+      load_chunk(dv, rb, gq, lane, wd, sd);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int g = gq * 4 + c;
+        const bf16x8 b = __builtin_bit_cast(bf16x8, hbs[(g * 4 + q) * 3 + jsel]);
+        acc = mfma16(dequant8(word_of(wd, c), scale_of(sd, c)), b, acc);
+      }
+    }
+    fold_cols(acc);
+    if (j == 0) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) red[s][4 * q + i] = acc[i];
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x < 16) {
+    const int r = threadIdx.x, d = rb * kTileRows + r;
+    float rs = 0.0f;
+    for (int s = 0; s < K; ++s) {
+      const float v = red[s][r];
+      if (!finite_f(v)) record_err(status, err_key(kPhExpert, token, s, ldh + d, kEkDown));
+      rs = rs + probs[s] * v;
+    }
+    const float vsh = red[K][r];
+    if (!finite_f(vsh)) record_err(status, err_key(kPhShared, token, 0, ldh + d, kEkDown));
+    float total = rs + shg[0] * vsh;
+    if (residual) total = total + residual[d];
+    if (!finite_f(total)) record_err(status, err_key(kPhAgg, token, 0, d, 0));
+    y[d] = total;
+  }
+}
+
+hipError_t launch_down_dec(const LayerDev& L, const float* h, int ldh, const int32_t* ids,
+                           const float* probs, const float* shg, const float* residual,
+                           float* y, int token, unsigned long long* status, hipStream_t st) {
+  if (L.K + 1 > 33) return hipErrorInvalidValue;
+  const size_t lds = (size_t)(L.K + 1) * (ldh / 8) * 3 * sizeof(uint4);
+  hipLaunchKernelGGL(k_down_dec, dim3(L.H / kTileRows), dim3(256), lds, st, L, h, ldh, ids, probs,
+                     shg, residual, y, token, status);
+  return hipGetLastError();
+}
+
+// ===========================================================================
+// RMSNorm per token with gamma = 1 (src/layers/rmsnorm.mojo:41-48), used by
+// the layer-stack entry point.  The sum of squares is reduced as 256 strided
+// partials then a halving tree (a fixed order shared with the oracle's stack).
+// ===========================================================================
+__global__ __launch_bounds__(256) void k_rmsnorm_rows(const float* __restrict__ x, int H,
+                                                       float eps, float* __restrict__ out) {
+  __shared__ float part[256];
+  const int t = blockIdx.x;
+  const float* xr = x + (size_t)t * H;
+  float acc = 0.0f;
+  for (int i = threadIdx.x; i < H; i += 256) acc = acc + xr[i] * xr[i];
+  part[threadIdx.x] = acc;
+  __syncthreads();
+  for (int wdt = 128; wdt >= 1; wdt >>= 1) {
+    if ((int)threadIdx.x < wdt) part[threadIdx.x] = part[threadIdx.x] + part[threadIdx.x + wdt];
+    __syncthreads();
+  }
+  const float denom = __builtin_sqrtf(part[0] / (float)H + eps);
+  for (int i = threadIdx.x; i < H; i += 256) out[(size_t)t * H + i] = xr[i] / denom;
+}
+
+hipError_t launch_rmsnorm_rows(const float* x, int T, int H, float eps, float* out,
+                               unsigned long long*, int, hipStream_t st) {
+  hipLaunchKernelGGL(k_rmsnorm_rows, dim3(T), dim3(256), 0, st, x, H, eps, out);
+  return hipGetLastError();
+}
+
+}  // namespace dm

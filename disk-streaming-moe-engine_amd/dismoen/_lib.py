@@ -1,0 +1,88 @@
+"""ctypes binding of libdismoen_hip.so (declarations in include/dismoen_hip.h).
+
+The library is the only compute path: when it is missing, importing this
+module's `lib()` raises instead of falling back to anything else.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+PKG_ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+LIB_PATH = os.path.join(PKG_ROOT, "libdismoen_hip.so")
+
+DMH_F_DEVICE = 0x1
+
+ERROR_NAMES = {
+    1: "INVALID_ARG", 2: "CONFIG", 3: "HIP", 4: "NO_MEMORY", 5: "DEQUANT", 6: "ACT",
+    7: "WEIGHT", 8: "ROUTER", 9: "EXPERT", 10: "SWIGLU", 11: "GATE", 12: "NORM",
+}
+
+# every symbol include/dismoen_hip.h declares
+EXPORTS = (
+    "dmh_version", "dmh_create", "dmh_destroy", "dmh_set_stream", "dmh_get_stream", "dmh_sync",
+    "dmh_upload_moe_layer", "dmh_free_layer", "dmh_layer_bytes", "dmh_moe_forward",
+    "dmh_moe_stack_forward", "dmh_router_forward", "dmh_dequant_q4_bf16",
+)
+
+
+class DmhDims(C.Structure):
+    _fields_ = [("hidden", C.c_int32), ("num_experts", C.c_int32), ("top_k", C.c_int32),
+                ("inter", C.c_int32), ("inter_sh", C.c_int32), ("group_size", C.c_int32),
+                ("norm_topk_prob", C.c_int32)]
+
+
+class DmhWeights(C.Structure):
+    _fields_ = [(n, C.c_void_p) for n in (
+        "router_bf16", "shgate_bf16", "gu_scales", "gu_packed", "d_scales", "d_packed",
+        "sh_gu_scales", "sh_gu_packed", "sh_d_scales", "sh_d_packed")]
+
+
+class DismoenError(RuntimeError):
+    """A nonzero status from the library; str() is the reference's error text."""
+
+    def __init__(self, code: int, message: str):
+        super().__init__(message)
+        self.code = code
+        self.kind = ERROR_NAMES.get(code, str(code))
+
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError(f"libdismoen_hip.so not built ({LIB_PATH}); run __graft_entry__.build()")
+    L = C.CDLL(LIB_PATH)
+    vp, sz, i32, i64, u32 = C.c_void_p, C.c_size_t, C.c_int, C.c_int64, C.c_uint
+    L.dmh_version.restype = C.c_char_p
+    L.dmh_create.argtypes = [i32, C.POINTER(vp), C.c_char_p, sz]
+    L.dmh_destroy.argtypes = [vp]
+    L.dmh_set_stream.argtypes = [vp, vp]
+    L.dmh_get_stream.argtypes = [vp]
+    L.dmh_get_stream.restype = vp
+    L.dmh_sync.argtypes = [vp, C.c_char_p, sz]
+    L.dmh_upload_moe_layer.argtypes = [vp, i32, C.POINTER(DmhDims), C.POINTER(DmhWeights), u32,
+                                       C.c_char_p, sz]
+    L.dmh_free_layer.argtypes = [vp, i32]
+    L.dmh_layer_bytes.argtypes = [vp, i32, C.POINTER(C.c_int64)]
+    L.dmh_moe_forward.argtypes = [vp, i32, vp, vp, i32, vp, vp, vp, vp, u32, C.c_char_p, sz]
+    L.dmh_moe_stack_forward.argtypes = [vp, i32, i32, C.c_float, vp, i32, vp, vp, vp, u32,
+                                        C.c_char_p, sz]
+    L.dmh_router_forward.argtypes = [vp, vp, vp, i32, i32, i32, i32, i32, i32, vp, vp, u32,
+                                     C.c_char_p, sz]
+    L.dmh_dequant_q4_bf16.argtypes = [vp, vp, i64, vp, i64, i64, i32, vp, u32, C.c_char_p, sz]
+    _lib = L
+    return L
+
+
+def check(rc: int, buf) -> None:
+    if rc:
+        raise DismoenError(rc, buf.value.decode(errors="replace"))
+
+
+def errbuf():
+    return C.create_string_buffer(2048)

@@ -1,0 +1,248 @@
+"""Host-side mirror of the reference's MoE layer interface over libdismoen_hip.so.
+
+Names, argument meaning and errors follow the Mojo sources:
+  RouterConfig / RoutingInfo      src/layers/router_types.mojo:9-81
+  router_forward                  src/layers/router.mojo:188-210
+  dequant_kernel_simd             src/quant/dequant_kernel.mojo:22-124
+  forward_moe_block               src/layers/moe_block.mojo:20-138
+  moe_combine_no_residual         src/layers/forward_layer.mojo:181-247
+  forward_port_block MoE section  src/layers/port_scheduler.mojo:381-482
+Errors surface as DismoenError whose text is the reference's JSON error.
+All compute runs in the HIP library; nothing here computes a result.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import json
+from dataclasses import dataclass, field
+
+import numpy as np
+
+from ._lib import (DMH_F_DEVICE, DismoenError, DmhDims, DmhWeights, check, errbuf, lib)
+
+
+@dataclass
+class RouterConfig:
+    """src/layers/router_types.mojo:9-44"""
+    num_experts: int
+    num_experts_per_tok: int
+    norm_topk_prob: bool = False
+
+    def validate(self) -> None:
+        def err(kind, detail):
+            return DismoenError(2 if kind == "CONFIG_ERROR" else 8, json.dumps(
+                {"error_type": kind, "detail": detail, "stage": "router"},
+                separators=(",", ":")))
+        if self.num_experts <= 0:
+            raise err("CONFIG_ERROR", "num_experts must be positive")
+        if self.num_experts_per_tok <= 0:
+            raise err("CONFIG_ERROR", "num_experts_per_tok must be positive")
+        if self.num_experts_per_tok > self.num_experts:
+            raise err("CONFIG_ERROR", "num_experts_per_tok cannot exceed num_experts")
+        if self.norm_topk_prob:
+            raise err("ROUTER_ERROR", "norm_topk_prob=true forbidden; unrenormalized routing"
+                      " invariant violated")
+
+
+@dataclass
+class RoutingInfo:
+    """src/layers/router_types.mojo:47-81"""
+    selected_experts: list = field(default_factory=list)
+    router_probs: list = field(default_factory=list)
+    num_tokens: int = 0
+    top_k: int = 0
+
+    @staticmethod
+    def from_arrays(ids: np.ndarray, probs: np.ndarray) -> "RoutingInfo":
+        return RoutingInfo([list(map(int, r)) for r in ids],
+                           [list(map(float, r)) for r in probs.astype(np.float32)],
+                           int(ids.shape[0]), int(ids.shape[1]))
+
+    def to_json(self) -> str:
+        sel = ",".join("[" + ",".join(str(e) for e in r) + "]" for r in self.selected_experts)
+        pr = ",".join("[" + ",".join(repr(float(np.float32(p))) for p in r) + "]"
+                      for r in self.router_probs)
+        return '{"selected_experts":[' + sel + '],"router_probs":[' + pr + "]}"
+
+
+def _ptr(a) -> int:
+    return a.ctypes.data if a is not None else None
+
+
+def _f32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+class MoEBlock:
+    """One device context: uploaded layers + the block entry points."""
+
+    def __init__(self, device: int = 0):
+        self._lib = lib()
+        h = C.c_void_p()
+        e = errbuf()
+        check(self._lib.dmh_create(device, C.byref(h), e, len(e)), e)
+        self._h = h
+        self.dims = {}
+
+    # -- lifetime --------------------------------------------------------
+    def close(self):
+        if getattr(self, "_h", None):
+            self._lib.dmh_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        self.close()
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()
+
+    @property
+    def handle(self):
+        return self._h
+
+    def set_stream(self, stream_ptr: int | None):
+        self._lib.dmh_set_stream(self._h, stream_ptr)
+
+    def stream(self) -> int:
+        return self._lib.dmh_get_stream(self._h) or 0
+
+    def sync(self):
+        e = errbuf()
+        check(self._lib.dmh_sync(self._h, e, len(e)), e)
+
+    # -- weights ---------------------------------------------------------
+    def upload_layer(self, layer_idx: int, L, norm_topk_prob: bool = False) -> None:
+        """Upload a layer given in the reference 4-bit layout (dismoen.synth.MoELayerQ4
+        or any object with the same fields)."""
+        d = DmhDims(L.hidden, L.num_experts, L.top_k, L.inter, L.inter_sh, L.group_size,
+                    int(norm_topk_prob))
+        arrs = {}
+        w = DmhWeights()
+        for name, dt in (("router_bf16", np.uint16), ("shgate_bf16", np.uint16),
+                         ("gu_scales", np.uint16), ("gu_packed", np.uint8),
+                         ("d_scales", np.uint16), ("d_packed", np.uint8),
+                         ("sh_gu_scales", np.uint16), ("sh_gu_packed", np.uint8),
+                         ("sh_d_scales", np.uint16), ("sh_d_packed", np.uint8)):
+            a = np.ascontiguousarray(getattr(L, name), dtype=dt)
+            arrs[name] = a
+            setattr(w, name, a.ctypes.data)
+        e = errbuf()
+        check(self._lib.dmh_upload_moe_layer(self._h, layer_idx, C.byref(d), C.byref(w), 0, e,
+                                             len(e)), e)
+        self.dims[layer_idx] = (L.hidden, L.num_experts, L.top_k, L.inter, L.inter_sh)
+
+    def upload_layer_device(self, layer_idx: int, dims: tuple, ptrs: dict) -> None:
+        """Upload from device buffers (ptrs: field name -> device address)."""
+        H, E, K, I, Ish = dims
+        d = DmhDims(H, E, K, I, Ish, 32, 0)
+        w = DmhWeights(**ptrs)
+        e = errbuf()
+        check(self._lib.dmh_upload_moe_layer(self._h, layer_idx, C.byref(d), C.byref(w),
+                                             DMH_F_DEVICE, e, len(e)), e)
+        self.dims[layer_idx] = dims
+
+    def free_layer(self, layer_idx: int) -> None:
+        self._lib.dmh_free_layer(self._h, layer_idx)
+        self.dims.pop(layer_idx, None)
+
+    def layer_bytes(self, layer_idx: int) -> int:
+        v = C.c_int64()
+        if self._lib.dmh_layer_bytes(self._h, layer_idx, C.byref(v)):
+            raise DismoenError(1, f"layer {layer_idx} not uploaded")
+        return v.value
+
+    # -- the block -------------------------------------------------------
+    def _forward(self, layer_idx, x, residual, seq_len):
+        H, E, K, I, Ish = self.dims[layer_idx]
+        x = _f32(x).reshape(-1)
+        res = None if residual is None else _f32(residual).reshape(-1)
+        y = np.empty(seq_len * H, np.float32)
+        ids = np.empty(seq_len * K, np.int32)
+        probs = np.empty(seq_len * K, np.float32)
+        shg = np.empty(seq_len, np.float32)
+        e = errbuf()
+        check(self._lib.dmh_moe_forward(self._h, layer_idx, x.ctypes.data, _ptr(res), seq_len,
+                                        y.ctypes.data, ids.ctypes.data, probs.ctypes.data,
+                                        shg.ctypes.data, 0, e, len(e)), e)
+        return (y.reshape(seq_len, H), ids.reshape(seq_len, K), probs.reshape(seq_len, K), shg)
+
+    def forward_moe_block(self, x, layer_idx: int, seq_len: int):
+        """forward_moe_block: y = sum_k p_k E_k(x) + sigmoid(g_sh) E_sh(x) + x.
+        Returns (y [seq_len*H] float32, RoutingInfo)."""
+        y, ids, probs, _ = self._forward(layer_idx, x, x, seq_len)
+        return y.reshape(-1), RoutingInfo.from_arrays(ids, probs)
+
+    def moe_combine_no_residual(self, x, layer_idx: int, seq_len: int):
+        """The same block without the residual (src/layers/forward_layer.mojo:181-247)."""
+        y, ids, probs, _ = self._forward(layer_idx, x, None, seq_len)
+        return y.reshape(-1), RoutingInfo.from_arrays(ids, probs)
+
+    def forward_port_moe(self, norm_x, x_mid, layer_idx: int, seq_len: int):
+        """MoE section of forward_port_block: router/experts on norm_x, residual x_mid."""
+        y, ids, probs, _ = self._forward(layer_idx, norm_x, x_mid, seq_len)
+        return y.reshape(-1), RoutingInfo.from_arrays(ids, probs)
+
+    def forward_arrays(self, layer_idx: int, x, seq_len: int, residual=None):
+        """(y, ids, probs, shared_gate) as numpy arrays."""
+        return self._forward(layer_idx, x, residual, seq_len)
+
+    def forward_device(self, layer_idx: int, x_ptr: int, seq_len: int, y_ptr: int,
+                       ids_ptr: int | None = None, probs_ptr: int | None = None,
+                       shg_ptr: int | None = None, residual_ptr: int | None = None) -> None:
+        """Stream-ordered call on device buffers; errors are reported by sync()."""
+        e = errbuf()
+        check(self._lib.dmh_moe_forward(self._h, layer_idx, x_ptr, residual_ptr, seq_len, y_ptr,
+                                        ids_ptr, probs_ptr, shg_ptr, DMH_F_DEVICE, e, len(e)), e)
+
+    def forward_stack(self, x, first_layer: int, num_layers: int, seq_len: int,
+                      eps: float = 1e-6):
+        H, E, K, I, Ish = self.dims[first_layer]
+        x = _f32(x).reshape(-1)
+        out = np.empty(seq_len * H, np.float32)
+        ids = np.empty(num_layers * seq_len * K, np.int32)
+        probs = np.empty(num_layers * seq_len * K, np.float32)
+        e = errbuf()
+        check(self._lib.dmh_moe_stack_forward(self._h, first_layer, num_layers, eps,
+                                              x.ctypes.data, seq_len, out.ctypes.data,
+                                              ids.ctypes.data, probs.ctypes.data, 0, e, len(e)),
+              e)
+        return (out.reshape(seq_len, H), ids.reshape(num_layers, seq_len, K),
+                probs.reshape(num_layers, seq_len, K))
+
+    def forward_stack_device(self, x_ptr: int, first_layer: int, num_layers: int, seq_len: int,
+                             out_ptr: int, eps: float = 1e-6, ids_ptr=None, probs_ptr=None):
+        e = errbuf()
+        check(self._lib.dmh_moe_stack_forward(self._h, first_layer, num_layers, eps, x_ptr,
+                                              seq_len, out_ptr, ids_ptr, probs_ptr, DMH_F_DEVICE,
+                                              e, len(e)), e)
+
+    # -- unit entry points ---------------------------------------------
+    def router_forward(self, x, w_router, seq_len: int, hidden_dim: int, cfg: RouterConfig,
+                       layer_idx: int = 0) -> RoutingInfo:
+        """router_forward with fp32 router weights [E][H]."""
+        x = _f32(x).reshape(-1)
+        w = _f32(w_router).reshape(-1)
+        K, E = cfg.num_experts_per_tok, cfg.num_experts
+        n = max(seq_len, 1) * max(K, 1)
+        ids = np.zeros(n, np.int32)
+        probs = np.zeros(n, np.float32)
+        e = errbuf()
+        check(self._lib.dmh_router_forward(self._h, x.ctypes.data, w.ctypes.data, seq_len,
+                                           hidden_dim, E, K, int(cfg.norm_topk_prob), layer_idx,
+                                           ids.ctypes.data, probs.ctypes.data, 0, e, len(e)), e)
+        return RoutingInfo.from_arrays(ids.reshape(seq_len, K), probs.reshape(seq_len, K))
+
+    def dequant_kernel_simd(self, scales, packed_weights, num_elements: int,
+                            group_size: int = 128) -> np.ndarray:
+        """Returns bf16 bit patterns (uint16) of bf16(fp32(s_g) * q)."""
+        s = np.ascontiguousarray(scales, dtype=np.uint16).reshape(-1)
+        p = np.ascontiguousarray(packed_weights, dtype=np.uint8).reshape(-1)
+        out = np.empty(max(int(num_elements), 1), np.uint16)
+        e = errbuf()
+        check(self._lib.dmh_dequant_q4_bf16(self._h, s.ctypes.data, s.size, p.ctypes.data,
+                                            p.size, num_elements, group_size, out.ctypes.data, 0,
+                                            e, len(e)), e)
+        return out[:num_elements]

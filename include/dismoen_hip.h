@@ -1,0 +1,165 @@
+/*
+ * dismoen_hip.h -- C ABI of libdismoen_hip.so, the gfx950 (MI355X) MoE FFN
+ * block of the disk-streaming MoE engine: router (logits, softmax, top-k),
+ * 4-bit group-quantised SwiGLU experts, the sigmoid-gated shared expert and
+ * the weighted combine.
+ *
+ * Plain C types only.  Every function returns DMH_OK (0) or a DMH_ERR_*
+ * code and, when err != NULL, writes the reference's error text into
+ * err[0..errlen): the JSON objects raised by the Mojo layers
+ * ({"error_type":...,"detail":...,"stage":...,"layer":...}) or the plain
+ * dequant strings, so a Mojo shim can `raise Error(String(err))` unchanged.
+ *
+ * Memory: by default every pointer is host memory and the call is
+ * synchronous.  With DMH_F_DEVICE every activation/output pointer is device
+ * memory, the call is ordered on the context's stream and returns at once;
+ * errors found on the device are then sticky and reported by dmh_sync().
+ *
+ * Threading: one context per host thread; a context is not re-entrant.
+ * Reference paths below are relative to the reference repository root.
+ */
+#ifndef DISMOEN_HIP_H
+#define DISMOEN_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define DMH_ABI_VERSION 1
+
+enum {
+  DMH_OK = 0,
+  DMH_ERR_INVALID_ARG = 1,  /* null pointer, bad length, unknown layer */
+  DMH_ERR_CONFIG = 2,       /* CONFIG_ERROR: dimensions the path does not support */
+  DMH_ERR_HIP = 3,          /* HIP runtime failure */
+  DMH_ERR_NO_MEMORY = 4,
+  DMH_ERR_DEQUANT = 5,      /* invalid 4-bit payload (reserved code, bad scale) */
+  DMH_ERR_ACT = 6,          /* ACT_LOAD_FAILED */
+  DMH_ERR_WEIGHT = 7,       /* WEIGHT_LOAD_FAILED */
+  DMH_ERR_ROUTER = 8,       /* ROUTER_ERROR */
+  DMH_ERR_EXPERT = 9,       /* EXPERT_ERROR */
+  DMH_ERR_SWIGLU = 10,      /* SWIGLU_ERROR */
+  DMH_ERR_GATE = 11,        /* GATE_ERROR */
+  DMH_ERR_NORM = 12,        /* NORM_ERROR */
+};
+
+#define DMH_F_DEVICE 0x1u   /* pointers are device memory; stream-ordered, no sync */
+
+typedef struct dmh_ctx dmh_ctx;
+
+/* Fields of ModelConfig that the block uses (src/core/config.mojo:11-174,
+ * src/layers/router_types.mojo:9-44).  group_size must be 32; hidden, inter
+ * and inter_sh must be multiples of 128; norm_topk_prob must be 0. */
+typedef struct {
+  int32_t hidden;          /* H */
+  int32_t num_experts;     /* E */
+  int32_t top_k;           /* K: num_experts_per_tok */
+  int32_t inter;           /* I: moe_intermediate_size */
+  int32_t inter_sh;        /* I_sh: shared_expert_intermediate_size */
+  int32_t group_size;      /* G */
+  int32_t norm_topk_prob;  /* forbidden (raises) when nonzero */
+} dmh_moe_dims;
+
+/* One layer's weights in the reference layouts.  4-bit tensors follow
+ * docs/format/quant_format.md:117-161: fp16 scales [N/G] then packed codes
+ * [N/2] (element i in byte i/2, low nibble = even i), groups along the input
+ * dimension.  gu_* is the fused experts.gate_up_proj [E][2I][H] (gate rows
+ * 0..I-1 then up rows I..2I-1 per expert, src/layers/moe_loader.mojo:47-72),
+ * which is the per-expert gate_proj [I][H] and up_proj [I][H] tensors of
+ * src/layers/quant_loader.mojo:89-111 laid end to end; d_* is
+ * experts.down_proj [E][H][I]; sh_* the shared expert
+ * (src/layers/quant_loader.mojo:114-136).  router_bf16 [E][H] is mlp.gate
+ * (src/layers/router.mojo:213-257) and shgate_bf16 [H] mlp.shared_expert_gate. */
+typedef struct {
+  const uint16_t* router_bf16;
+  const uint16_t* shgate_bf16;
+  const uint16_t* gu_scales;    /* [E*2I*H/G] fp16 bits */
+  const uint8_t* gu_packed;     /* [E*2I*H/2] */
+  const uint16_t* d_scales;     /* [E*H*I/G] */
+  const uint8_t* d_packed;      /* [E*H*I/2] */
+  const uint16_t* sh_gu_scales; /* [2*Ish*H/G] */
+  const uint8_t* sh_gu_packed;  /* [2*Ish*H/2] */
+  const uint16_t* sh_d_scales;  /* [H*Ish/G] */
+  const uint8_t* sh_d_packed;   /* [H*Ish/2] */
+} dmh_moe_weights;
+
+/* Library version string, e.g. "dismoen_hip 1 gfx950". */
+const char* dmh_version(void);
+
+/* Create a context on HIP device `device` with its own stream.  Replaces the
+ * engine's WorkerPool construction (src/core/worker_pool.mojo:228-294): the
+ * context owns all device memory of the block. */
+int dmh_create(int device, dmh_ctx** out, char* err, size_t errlen);
+int dmh_destroy(dmh_ctx* ctx);
+
+/* Use another HIP stream (a hipStream_t) for subsequent calls; NULL restores
+ * the context's own stream. */
+int dmh_set_stream(dmh_ctx* ctx, void* hip_stream);
+void* dmh_get_stream(dmh_ctx* ctx);
+
+/* Wait for the stream; return the first device-side error recorded since
+ * the last dmh_sync (DMH_F_DEVICE calls), then clear it. */
+int dmh_sync(dmh_ctx* ctx, char* err, size_t errlen);
+
+/* Upload one layer once into HBM, re-tiled for the gfx950 kernels and
+ * validated (reserved code 0x8, fp16 scale NaN/Inf or <= 0: the checks of
+ * src/quant/dequant_kernel.mojo:68-108; non-finite router weights: the scan
+ * of src/layers/router.mojo:65-72, reported when the layer is used).
+ * Replaces the per-use pread + dequant of load_quant_routed_expert_weights /
+ * load_quant_shared_expert_weights (src/layers/quant_loader.mojo:89-136) and
+ * load_layer_router_weights (src/layers/router.mojo:213-257).
+ * flags & DMH_F_DEVICE: the weight pointers are device memory. */
+int dmh_upload_moe_layer(dmh_ctx* ctx, int layer, const dmh_moe_dims* dims,
+                         const dmh_moe_weights* w, unsigned flags, char* err,
+                         size_t errlen);
+int dmh_free_layer(dmh_ctx* ctx, int layer);
+/* Device bytes held by an uploaded layer. */
+int dmh_layer_bytes(dmh_ctx* ctx, int layer, int64_t* bytes);
+
+/* The MoE block for seq_len tokens of one uploaded layer: router_forward ->
+ * routed SwiGLU experts -> shared expert + sigmoid gate -> combine.
+ * Replaces forward_moe_block (src/layers/moe_block.mojo:20-138) and the MoE
+ * section of forward_port_block (src/layers/port_scheduler.mojo:381-482).
+ *   x        [seq_len][H] fp32 input of the router and experts
+ *   residual [seq_len][H] fp32 or NULL.  Non-NULL: moe_aggregate_forward
+ *            (src/layers/moe.mojo:105-177), y = routed + shared + residual;
+ *            NULL: moe_combine_no_residual (src/layers/forward_layer.mojo:181-247).
+ *   y        [seq_len][H] fp32 output
+ *   ids      [seq_len][K] int32 selected experts (RoutingInfo.selected_experts,
+ *            src/layers/router_types.mojo:47-81), p descending, lowest id on ties;
+ *            may be NULL
+ *   probs    [seq_len][K] fp32 raw softmax probabilities (no renormalisation); may be NULL
+ *   shared_gate [seq_len] fp32 sigmoid(w_sh . x); may be NULL */
+int dmh_moe_forward(dmh_ctx* ctx, int layer, const float* x, const float* residual,
+                    int seq_len, float* y, int32_t* ids, float* probs,
+                    float* shared_gate, unsigned flags, char* err, size_t errlen);
+
+/* num_layers consecutive uploaded layers, token mixer replaced by identity:
+ * per layer h <- moe_aggregate_forward(h, MoE(RMSNorm_{gamma=1,eps}(h))), the
+ * composition of src/layers/port_scheduler.mojo:381-482.  ids/probs
+ * [num_layers][seq_len][K] may be NULL. */
+int dmh_moe_stack_forward(dmh_ctx* ctx, int first_layer, int num_layers, float eps,
+                          const float* x, int seq_len, float* out, int32_t* ids,
+                          float* probs, unsigned flags, char* err, size_t errlen);
+
+/* router_forward (src/layers/router.mojo:188-210) with fp32 weights
+ * w_router [E][H]: router_project + router_softmax + select_topk. */
+int dmh_router_forward(dmh_ctx* ctx, const float* x, const float* w_router, int seq_len,
+                       int hidden, int num_experts, int top_k, int norm_topk_prob,
+                       int layer, int32_t* ids, float* probs, unsigned flags, char* err,
+                       size_t errlen);
+
+/* dequant_kernel_simd (src/quant/dequant_kernel.mojo:22-124): 4-bit codes +
+ * fp16 scales -> bf16 bits, out[i] = bf16_rne(fp32(s_g) * q_i). */
+int dmh_dequant_q4_bf16(dmh_ctx* ctx, const uint16_t* scales, int64_t n_scales,
+                        const uint8_t* packed, int64_t n_packed, int64_t num_elements,
+                        int group_size, uint16_t* out, unsigned flags, char* err,
+                        size_t errlen);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* DISMOEN_HIP_H */

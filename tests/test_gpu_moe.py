@@ -1,0 +1,115 @@
+"""GPU parity of the MoE block (dmh_moe_forward / dmh_moe_stack_forward)
+against the CPU oracle's restatement of the reference composition.
+
+Bar: selected expert ids and their probabilities bit-exact; the no-residual
+output within max-abs-err <= 1e-3 x RMS(oracle output)."""
+import numpy as np
+import pytest
+
+from conftest import tol_check
+from dismoen import DismoenError, synth
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def toy(block):
+    L = synth.make_layer(**synth.CONFIG_TOY, seed=0)
+    block.upload_layer(0, L)
+    return L
+
+
+@pytest.fixture(scope="module")
+def qwen(block):
+    L = synth.make_layer(**synth.CONFIG_QWEN36, seed=1)
+    block.upload_layer(1, L)
+    return L
+
+
+def check_layer(block, oracle, L, layer, x, residual=None):
+    T = x.shape[0]
+    y, ids, probs, shg = block.forward_arrays(layer, x, T, residual=residual)
+    yo, ido, po, so = oracle.moe_layer_q4(L, x, T, residual=residual)
+    assert np.array_equal(ids, ido)
+    assert np.array_equal(probs.view(np.uint32), po.view(np.uint32))
+    assert np.array_equal(shg.view(np.uint32), so.view(np.uint32))
+    if residual is None:
+        err, rms, ok = tol_check(y, yo)
+        assert ok, (err, rms)
+    else:
+        yn, _, _, _ = block.forward_arrays(layer, x, T)
+        err, rms, ok = tol_check(y - residual, yo - residual)
+        assert ok, (err, rms)
+    return y, yo
+
+
+def test_toy_layer_single_token(block, oracle, toy):
+    x = synth.make_activations(np.random.default_rng(100), (1, 256))
+    check_layer(block, oracle, toy, 0, x)
+
+
+def test_toy_layer_tokens_and_residual(block, oracle, toy):
+    x = synth.make_activations(np.random.default_rng(101), (7, 256))
+    check_layer(block, oracle, toy, 0, x)
+    check_layer(block, oracle, toy, 0, x, residual=x)
+
+
+def test_toy_reference_api_mirror(block, oracle, toy):
+    x = synth.make_activations(np.random.default_rng(102), (3, 256))
+    y, info = block.forward_moe_block(x, 0, 3)
+    yo, ido, po, _ = oracle.moe_layer_q4(toy, x, 3, residual=x)
+    assert info.selected_experts == ido.tolist() and info.num_tokens == 3 and info.top_k == 4
+    err, rms, ok = tol_check(y.reshape(3, -1) - x, yo - x)
+    assert ok
+
+
+def test_qwen_layer_decode_tokens(block, oracle, qwen):
+    x = synth.make_activations(np.random.default_rng(103), (6, 2048))
+    for t in range(6):
+        check_layer(block, oracle, qwen, 1, x[t:t + 1])
+
+
+def test_deterministic_run_to_run(block, qwen):
+    x = synth.make_activations(np.random.default_rng(104), (2, 2048))
+    a = block.forward_arrays(1, x, 2)
+    b = block.forward_arrays(1, x, 2)
+    for u, v in zip(a, b):
+        assert np.array_equal(np.asarray(u).view(np.uint8), np.asarray(v).view(np.uint8))
+
+
+def test_nonfinite_activation_error_matches_oracle(block, oracle, toy):
+    x = synth.make_activations(np.random.default_rng(105), (2, 256))
+    x[1, 17] = np.nan
+    with pytest.raises(oracle.OracleError) as eo:
+        oracle.moe_layer_q4(toy, x, 2)
+    with pytest.raises(DismoenError) as eg:
+        block.forward_arrays(0, x, 2)
+    assert str(eg.value) == str(eo.value)
+    # the context stays usable after an error
+    x[1, 17] = 0.0
+    check_layer(block, oracle, toy, 0, x)
+
+
+def test_upload_rejects_reserved_code_and_bad_scale(block):
+    L = synth.make_layer(**synth.CONFIG_TOY, seed=7)
+    L.d_packed = L.d_packed.copy()
+    L.d_packed[1000] = 0x80
+    with pytest.raises(DismoenError, match="reserved nibble"):
+        block.upload_layer(5, L)
+    L = synth.make_layer(**synth.CONFIG_TOY, seed=7)
+    L.gu_scales = L.gu_scales.copy()
+    L.gu_scales[3] = 0x7E00
+    with pytest.raises(DismoenError, match="scale is NaN or Inf at group 3"):
+        block.upload_layer(5, L)
+
+
+def test_stack_of_layers(block, oracle):
+    layers = [synth.make_layer(**synth.CONFIG_TOY, seed=20 + l) for l in range(4)]
+    for l, L in enumerate(layers):
+        block.upload_layer(10 + l, L)
+    x = synth.make_activations(np.random.default_rng(106), (3, 256))
+    out, ids, probs = block.forward_stack(x, 10, 4, 3, eps=1e-6)
+    oo, ido, po = oracle.moe_stack_q4(layers, x, 3, 1e-6)
+    assert np.array_equal(ids, ido)
+    err, rms, ok = tol_check(out - x, oo - x)
+    assert ok, (err, rms)
