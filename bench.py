@@ -119,7 +119,7 @@ def main():
                        "hidden": H, "experts": L.num_experts, "top_k": K, "inter": L.inter,
                        "inter_sh": L.inter_sh, "group": 32, "bits": 4, "tokens": a.steps},
             "achieved_gbps": round(gbps, 1),
-            "roofline": {"bound": "hbm", "kernel": "moe block (all launches of one token)",
+            "roofline": {"bound": "hbm", "kernel": "k_moe_decode (one fused launch per token)",
                          "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                          "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None,
                          "bytes_per_token": bytes_tok},

@@ -10,6 +10,7 @@
 #include <vector>
 
 #include "../../include/dismoen_hip.h"
+#include "dm_decode.h"
 #include "dm_kernels.h"
 #include "dm_layout.h"
 
@@ -25,6 +26,13 @@ struct Layer {
   size_t bytes = 0;
   LayerDev dev{};
   bool router_w_bad = false;
+  dm::DecodePlan plan{};
+  bool fused = false;  // the fused decode kernel fits this layer on this device
+  // The fused kernel's counters only grow; launch n of this layer waits for
+  // n times the arrivals one launch of this layer makes, so each layer keeps
+  // its own counters and launch count.
+  unsigned* cnt = nullptr;  // [1 + 64 + 1024]
+  unsigned launches = 0;
 };
 
 template <typename T>
@@ -63,6 +71,9 @@ struct dmh_ctx {
   // where to find the routing of the last device-mode call per layer
   std::vector<const int32_t*> last_ids;
   std::vector<int> last_k;
+  // fused decode kernel scratch (launches on one stream never overlap)
+  int num_cus = 0;
+  DevBuf<float> dz, dh, dyp; // logits, h, half partials
 };
 
 namespace {
@@ -122,6 +133,8 @@ int decode_key(uint64_t key, int layer, int expert_id, int E, char* err, size_t 
     case kPhGate:
       if (kind == kGkLogit) RJ(DMH_ERR_GATE, "GATE_ERROR", "non-finite shared gate logit", "shared");
       RJ(DMH_ERR_GATE, "GATE_ERROR", "shared gate score outside (0, 1)", "shared");
+    case kPhSync:
+      RJ(DMH_ERR_HIP, "HIP_ERROR", "cross-workgroup handoff timed out in the decode kernel", "hip");
     default:
       RJ(DMH_ERR_EXPERT, "EXPERT_ERROR", "non-finite value in aggregation", "aggregation");
   }
@@ -160,6 +173,21 @@ hipError_t reset_status(dmh_ctx* ctx, int slot) {
 }
 
 // Runs the block for T tokens of a layer on device buffers.
+constexpr int kCntH = 1, kCntY = 65, kCntTotal = 1 + 64 + 1024;
+
+hipError_t reset_counters(dmh_ctx* ctx, Layer* Ly) {
+  Ly->launches = 0;
+  if (!Ly->cnt) return hipSuccess;
+  return hipMemsetAsync(Ly->cnt, 0, sizeof(unsigned) * kCntTotal, ctx->cur);
+}
+
+void free_layer(Layer* Ly) {
+  if (!Ly) return;
+  if (Ly->buf) (void)hipFree(Ly->buf);
+  if (Ly->cnt) (void)hipFree(Ly->cnt);
+  delete Ly;
+}
+
 hipError_t run_block(dmh_ctx* ctx, Layer* Ly, int layer, const float* dx, const float* dres,
                      int T, float* dy, int32_t* dids, float* dprobs, float* dshg) {
   const LayerDev& L = Ly->dev;
@@ -167,6 +195,19 @@ hipError_t run_block(dmh_ctx* ctx, Layer* Ly, int layer, const float* dx, const 
   unsigned long long* status = ctx->status + layer;
   const int ldh = L.I > L.Ish ? L.I : L.Ish;
   hipError_t e;
+  if (Ly->fused) {
+    for (int t = 0; t < T; ++t) {
+      if (Ly->launches >= (1u << 24) && (e = reset_counters(ctx, Ly)) != hipSuccess) return e;
+      dm::DecodeSync S{Ly->cnt, Ly->cnt + kCntH, Ly->cnt + kCntY, ctx->dz.p, ctx->dh.p,
+                       ctx->dyp.p, ++Ly->launches};
+      e = dm::launch_moe_decode(L, Ly->plan, dx + (size_t)t * L.H,
+                                dres ? dres + (size_t)t * L.H : nullptr, dy + (size_t)t * L.H,
+                                dids + (size_t)t * L.K, dprobs + (size_t)t * L.K, dshg + t, S,
+                                status, t, st);
+      if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+  }
   if ((e = ctx->z.ensure((size_t)T * (L.E + 1))) != hipSuccess) return e;
   if ((e = ctx->h.ensure((size_t)(L.K + 1) * ldh)) != hipSuccess) return e;
   if ((e = dm::launch_router_dec(L, dx, T, ctx->z.p, status, st)) != hipSuccess) return e;
@@ -195,11 +236,14 @@ int finish_status(dmh_ctx* ctx, Layer* Ly, int layer, uint64_t key, const int32_
     if (rk < key) key = rk;
   }
   if (key == dm::kNoError) return DMH_OK;
+  if (dm::key_phase(key) == dm::kPhSync && Ly) {
+    (void)hipStreamSynchronize(ctx->cur);
+    (void)reset_counters(ctx, Ly);
+  }
   int expert_id = -1;
   const int K = Ly ? Ly->dims.top_k : 0;
   if (dm::key_phase(key) == dm::kPhExpert && host_ids)
     expert_id = host_ids[(size_t)dm::key_token(key) * K + dm::key_slot(key)];
-  (void)ctx;
   return decode_key(key, layer, expert_id, Ly ? Ly->dims.num_experts : 0, err, errlen);
 }
 
@@ -231,6 +275,8 @@ int dmh_create(int device, dmh_ctx** out, char* err, size_t errlen) {
     return set_err(err, errlen, DMH_ERR_HIP, "dmh_create: %s", hipGetErrorString(e));
   }
   c->cur = c->own;
+  hipDeviceProp_t prop;
+  if (hipGetDeviceProperties(&prop, device) == hipSuccess) c->num_cus = prop.multiProcessorCount;
   c->last_ids.assign(kMaxLayers + 1, nullptr);
   c->last_k.assign(kMaxLayers + 1, 0);
   *out = c;
@@ -241,12 +287,9 @@ int dmh_destroy(dmh_ctx* c) {
   if (!c) return DMH_OK;
   (void)hipSetDevice(c->device);
   if (c->cur) (void)hipStreamSynchronize(c->cur);
-  for (Layer* L : c->layers)
-    if (L) {
-      if (L->buf) (void)hipFree(L->buf);
-      delete L;
-    }
-  DevBuf<float>* fb[] = {&c->x, &c->res, &c->y, &c->z, &c->probs, &c->shg, &c->h, &c->xn, &c->hstack};
+  for (Layer* L : c->layers) free_layer(L);
+  DevBuf<float>* fb[] = {&c->x,  &c->res, &c->y,  &c->z,  &c->probs, &c->shg,
+                         &c->h,  &c->xn,  &c->hstack, &c->dz, &c->dh, &c->dyp};
   for (auto* b : fb) b->release();
   c->ids.release();
   c->stage.release();
@@ -425,10 +468,24 @@ int dmh_upload_moe_layer(dmh_ctx* c, int layer, const dmh_moe_dims* d, const dmh
                    (unsigned long long)(sub >> 1));
   }
   Ly->router_w_bad = fl & 1u;
+  // fused decode kernel: all workgroups must be co-resident
+  Ly->plan = dm::make_decode_plan(Ly->dev, c->num_cus);
+  {
+    int per_cu = 0;
+    const int ldh = I > Ish ? I : Ish;
+    if (dm::decode_occupancy(Ly->dev, Ly->plan, &per_cu) == hipSuccess && c->num_cus > 0 &&
+        per_cu * c->num_cus >= Ly->plan.grid && Ly->plan.lds_bytes <= 65536 && H / 16 <= 1024 &&
+        K + 1 <= 64 && c->dz.ensure(E + 1) == hipSuccess &&
+        c->dh.ensure((size_t)(K + 1) * ldh) == hipSuccess &&
+        c->dyp.ensure(2 * (size_t)H) == hipSuccess &&
+        hipMalloc(&Ly->cnt, sizeof(unsigned) * kCntTotal) == hipSuccess &&
+        hipMemsetAsync(Ly->cnt, 0, sizeof(unsigned) * kCntTotal, st) == hipSuccess)
+      Ly->fused = true;
+  }
   if (layer >= (int)c->layers.size()) c->layers.resize(layer + 1, nullptr);
   if (c->layers[layer]) {
-    (void)hipFree(c->layers[layer]->buf);
-    delete c->layers[layer];
+    (void)hipStreamSynchronize(st);
+    free_layer(c->layers[layer]);
   }
   c->layers[layer] = Ly;
   return DMH_OK;
@@ -439,8 +496,7 @@ int dmh_free_layer(dmh_ctx* c, int layer) {
   if (!Ly) return DMH_ERR_INVALID_ARG;
   (void)hipSetDevice(c->device);
   (void)hipStreamSynchronize(c->cur);
-  (void)hipFree(Ly->buf);
-  delete Ly;
+  free_layer(Ly);
   c->layers[layer] = nullptr;
   return DMH_OK;
 }

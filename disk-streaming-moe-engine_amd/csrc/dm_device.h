@@ -127,4 +127,82 @@ __device__ __forceinline__ void record_err(unsigned long long* status, uint64_t 
   atomicMin(status, (unsigned long long)key);
 }
 
+// ---- cross-workgroup handoff inside one launch -----------------------------
+// Data handed between workgroups is written and read with agent-scope relaxed
+// atomics: they go to the device-coherent level and bypass the per-XCD L2,
+// so no cache write-back / invalidate fences are needed.  A producer writes
+// its data, waits for the stores to complete, then bumps a counter; a
+// consumer polls the counter, then reads the data.
+__device__ __forceinline__ void st_coh(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_coh(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ unsigned ld_coh_u32(const unsigned* p) {
+  return __hip_atomic_load(const_cast<unsigned*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void wait_stores() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// Bounded poll until *c reaches target (wrap-safe).  About one second at the
+// limit; on timeout records a sync error and returns false so that the
+// caller skips later waits and the grid always drains.
+constexpr long kSpinLimit = 1l << 20;
+__device__ __forceinline__ bool wait_count(const unsigned* c, unsigned target,
+                                           unsigned long long* status) {
+  for (long i = 0; i < kSpinLimit; ++i) {
+    if ((int)(ld_coh_u32(c) - target) >= 0) return true;
+    __builtin_amdgcn_s_sleep(1);
+  }
+  record_err(status, err_key(kPhSync, 0, 0, 0, 0));
+  return false;
+}
+
+// ---- A16 tile access ------------------------------------------------------
+struct ExpertView {
+  const uint8_t* nib;   // A16 matrix
+  const uint16_t* sc;
+  int rows, cols;
+};
+
+__device__ __forceinline__ void load_chunk(const ExpertView& v, int rb, int gq, int lane,
+                                           uint4& w, uint2& s) {
+  const int nGQ = v.cols / kQuadCols;
+  w = *reinterpret_cast<const uint4*>(v.nib + a16_nib_offset(nGQ, rb, gq, lane));
+  s = *reinterpret_cast<const uint2*>(v.sc + a16_sc_offset(nGQ, rb, gq, lane & 15));
+}
+
+__device__ __forceinline__ float scale_of(const uint2& s, int c) {
+  const uint32_t word = c < 2 ? s.x : s.y;
+  return fp16_bits_to_f32((c & 1) ? (word >> 16) : (word & 0xFFFFu));
+}
+
+__device__ __forceinline__ uint32_t word_of(const uint4& w, int c) {
+  return c == 0 ? w.x : c == 1 ? w.y : c == 2 ? w.z : w.w;
+}
+
+// Stage an fp32 vector v[n] (n % 32 == 0) as B-operand blocks in LDS:
+// blk[(g*4 + q)*3 + {0: hi, 1: lo, 2: zero}] holds columns 32g+8q..+7.
+__device__ __forceinline__ void stage_split(const float* __restrict__ v, int n, uint4* blk) {
+  for (int i = threadIdx.x; i < n / 8; i += blockDim.x) {
+    float f[8];
+    const float4 a = reinterpret_cast<const float4*>(v)[2 * i];
+    const float4 b = reinterpret_cast<const float4*>(v)[2 * i + 1];
+    f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w;
+    f[4] = b.x; f[5] = b.y; f[6] = b.z; f[7] = b.w;
+    uint4 hi, lo;
+    split8(f, hi, lo);
+    blk[3 * i + 0] = hi;
+    blk[3 * i + 1] = lo;
+    blk[3 * i + 2] = make_uint4(0, 0, 0, 0);
+  }
+}
+
+// Columns 0 (hi) + 1 (lo) of an MFMA accumulator: after the exchange, lanes
+// with (lane & 15) == 0 hold rows 4*(lane>>4) + i.
+__device__ __forceinline__ void fold_cols(f32x4& acc) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) acc[i] = acc[i] + __shfl_xor(acc[i], 1);
+}
+
 }  // namespace dm

@@ -367,52 +367,6 @@ hipError_t launch_router_select(const float* z, int ldz, int T, int E, int K, in
 // 16 rows into bf16 (bit-exact bf16_rne(s*q)) and multiplies it by the
 // activation split into bf16 hi/lo columns 0 and 1 of the B operand.
 // ===========================================================================
-struct ExpertView {
-  const uint8_t* nib;   // A16 matrix
-  const uint16_t* sc;
-  int rows, cols;
-};
-
-__device__ __forceinline__ void load_chunk(const ExpertView& v, int rb, int gq, int lane,
-                                           uint4& w, uint2& s) {
-  const int nGQ = v.cols / kQuadCols;
-  w = *reinterpret_cast<const uint4*>(v.nib + a16_nib_offset(nGQ, rb, gq, lane));
-  s = *reinterpret_cast<const uint2*>(v.sc + a16_sc_offset(nGQ, rb, gq, lane & 15));
-}
-
-__device__ __forceinline__ float scale_of(const uint2& s, int c) {
-  const uint32_t word = c < 2 ? s.x : s.y;
-  return fp16_bits_to_f32((c & 1) ? (word >> 16) : (word & 0xFFFFu));
-}
-
-__device__ __forceinline__ uint32_t word_of(const uint4& w, int c) {
-  return c == 0 ? w.x : c == 1 ? w.y : c == 2 ? w.z : w.w;
-}
-
-// Stage an fp32 vector v[n] (n % 32 == 0) as B-operand blocks in LDS:
-// blk[(g*4 + q)*3 + {0: hi, 1: lo, 2: zero}] holds columns 32g+8q..+7.
-__device__ __forceinline__ void stage_split(const float* __restrict__ v, int n, uint4* blk) {
-  for (int i = threadIdx.x; i < n / 8; i += blockDim.x) {
-    float f[8];
-    const float4 a = reinterpret_cast<const float4*>(v)[2 * i];
-    const float4 b = reinterpret_cast<const float4*>(v)[2 * i + 1];
-    f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w;
-    f[4] = b.x; f[5] = b.y; f[6] = b.z; f[7] = b.w;
-    uint4 hi, lo;
-    split8(f, hi, lo);
-    blk[3 * i + 0] = hi;
-    blk[3 * i + 1] = lo;
-    blk[3 * i + 2] = make_uint4(0, 0, 0, 0);
-  }
-}
-
-// Columns 0 (hi) + 1 (lo) of an MFMA accumulator: after the exchange, lanes
-// with (lane & 15) == 0 hold rows 4*(lane>>4) + i.
-__device__ __forceinline__ void fold_cols(f32x4& acc) {
-#pragma unroll
-  for (int i = 0; i < 4; ++i) acc[i] = acc[i] + __shfl_xor(acc[i], 1);
-}
-
 __global__ __launch_bounds__(256) void k_gateup_dec(LayerDev L, const float* __restrict__ x,
                                                      const int32_t* __restrict__ ids,
                                                      float* __restrict__ hout, int ldh, int token,

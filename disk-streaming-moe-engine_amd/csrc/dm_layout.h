@@ -79,7 +79,7 @@ struct LayerDev {
 //   [63:60] phase  [59:40] token  [39:32] slot  [31:4] pos  [3:0] kind
 enum : uint32_t {
   kPhX = 0, kPhRouterW = 1, kPhLogit = 2, kPhSoftmax = 3, kPhTopk = 4,
-  kPhExpert = 5, kPhShared = 6, kPhGate = 7, kPhAgg = 8,
+  kPhExpert = 5, kPhShared = 6, kPhGate = 7, kPhAgg = 8, kPhSync = 15,
 };
 enum : uint32_t {  // kinds
   kTkSum = 0, kTkLeak = 1,                          // top-k

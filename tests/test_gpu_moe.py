@@ -113,3 +113,14 @@ def test_stack_of_layers(block, oracle):
     assert np.array_equal(ids, ido)
     err, rms, ok = tol_check(out - x, oo - x)
     assert ok, (err, rms)
+
+
+def test_interleaved_layers_of_different_shapes(block, oracle, toy, qwen):
+    """Launches of layers with different workgroup counts alternate on one
+    context (each layer keeps its own handoff counters)."""
+    rng = np.random.default_rng(107)
+    for rep in range(3):
+        xt = synth.make_activations(rng, (1, 256))
+        xq = synth.make_activations(rng, (1, 2048))
+        check_layer(block, oracle, toy, 0, xt)
+        check_layer(block, oracle, qwen, 1, xq)
