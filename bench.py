@@ -61,8 +61,8 @@ def main():
 
     dev = torch.device("cuda:0")
     blk = MoEBlock(0)
-    stream = torch.cuda.current_stream(dev)
-    blk.set_stream(stream.cuda_stream)
+    # time on the library's own stream (the stream every launch goes to)
+    stream = torch.cuda.ExternalStream(blk.stream(), device=dev)
 
     if a.workload in ("decode", "toy"):
         cfg = synth.CONFIG_QWEN36 if a.workload == "decode" else synth.CONFIG_TOY

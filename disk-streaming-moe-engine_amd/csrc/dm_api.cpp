@@ -28,10 +28,11 @@ struct Layer {
   bool router_w_bad = false;
   dm::DecodePlan plan{};
   bool fused = false;  // the fused decode kernel fits this layer on this device
-  // The fused kernel's counters only grow; launch n of this layer waits for
-  // n times the arrivals one launch of this layer makes, so each layer keeps
-  // its own counters and launch count.
-  unsigned* cnt = nullptr;  // [1 + 64 + 1024]
+  // The fused kernel's counters and tags only grow; launch n of this layer
+  // waits for n times the arrivals of one launch (or tag n), so each layer
+  // keeps its own hand-off buffers and launch count.
+  void* sync = nullptr;
+  size_t sync_bytes = 0;
   unsigned launches = 0;
 };
 
@@ -71,9 +72,7 @@ struct dmh_ctx {
   // where to find the routing of the last device-mode call per layer
   std::vector<const int32_t*> last_ids;
   std::vector<int> last_k;
-  // fused decode kernel scratch (launches on one stream never overlap)
   int num_cus = 0;
-  DevBuf<float> dz, dh, dyp; // logits, h, half partials
 };
 
 namespace {
@@ -173,18 +172,16 @@ hipError_t reset_status(dmh_ctx* ctx, int slot) {
 }
 
 // Runs the block for T tokens of a layer on device buffers.
-constexpr int kCntH = 1, kCntY = 65, kCntTotal = 1 + 64 + 1024;
-
 hipError_t reset_counters(dmh_ctx* ctx, Layer* Ly) {
   Ly->launches = 0;
-  if (!Ly->cnt) return hipSuccess;
-  return hipMemsetAsync(Ly->cnt, 0, sizeof(unsigned) * kCntTotal, ctx->cur);
+  if (!Ly->sync) return hipSuccess;
+  return hipMemsetAsync(Ly->sync, 0, Ly->sync_bytes, ctx->cur);
 }
 
 void free_layer(Layer* Ly) {
   if (!Ly) return;
   if (Ly->buf) (void)hipFree(Ly->buf);
-  if (Ly->cnt) (void)hipFree(Ly->cnt);
+  if (Ly->sync) (void)hipFree(Ly->sync);
   delete Ly;
 }
 
@@ -198,8 +195,8 @@ hipError_t run_block(dmh_ctx* ctx, Layer* Ly, int layer, const float* dx, const 
   if (Ly->fused) {
     for (int t = 0; t < T; ++t) {
       if (Ly->launches >= (1u << 24) && (e = reset_counters(ctx, Ly)) != hipSuccess) return e;
-      dm::DecodeSync S{Ly->cnt, Ly->cnt + kCntH, Ly->cnt + kCntY, ctx->dz.p, ctx->dh.p,
-                       ctx->dyp.p, ++Ly->launches};
+      dm::DecodeSync S = dm::decode_sync_carve(L, Ly->sync);
+      S.n = ++Ly->launches;
       e = dm::launch_moe_decode(L, Ly->plan, dx + (size_t)t * L.H,
                                 dres ? dres + (size_t)t * L.H : nullptr, dy + (size_t)t * L.H,
                                 dids + (size_t)t * L.K, dprobs + (size_t)t * L.K, dshg + t, S,
@@ -288,8 +285,7 @@ int dmh_destroy(dmh_ctx* c) {
   (void)hipSetDevice(c->device);
   if (c->cur) (void)hipStreamSynchronize(c->cur);
   for (Layer* L : c->layers) free_layer(L);
-  DevBuf<float>* fb[] = {&c->x,  &c->res, &c->y,  &c->z,  &c->probs, &c->shg,
-                         &c->h,  &c->xn,  &c->hstack, &c->dz, &c->dh, &c->dyp};
+  DevBuf<float>* fb[] = {&c->x, &c->res, &c->y, &c->z, &c->probs, &c->shg, &c->h, &c->xn, &c->hstack};
   for (auto* b : fb) b->release();
   c->ids.release();
   c->stage.release();
@@ -472,14 +468,11 @@ int dmh_upload_moe_layer(dmh_ctx* c, int layer, const dmh_moe_dims* d, const dmh
   Ly->plan = dm::make_decode_plan(Ly->dev, c->num_cus);
   {
     int per_cu = 0;
-    const int ldh = I > Ish ? I : Ish;
+    Ly->sync_bytes = dm::decode_sync_bytes(Ly->dev);
     if (dm::decode_occupancy(Ly->dev, Ly->plan, &per_cu) == hipSuccess && c->num_cus > 0 &&
-        per_cu * c->num_cus >= Ly->plan.grid && Ly->plan.lds_bytes <= 65536 && H / 16 <= 1024 &&
-        K + 1 <= 64 && c->dz.ensure(E + 1) == hipSuccess &&
-        c->dh.ensure((size_t)(K + 1) * ldh) == hipSuccess &&
-        c->dyp.ensure(2 * (size_t)H) == hipSuccess &&
-        hipMalloc(&Ly->cnt, sizeof(unsigned) * kCntTotal) == hipSuccess &&
-        hipMemsetAsync(Ly->cnt, 0, sizeof(unsigned) * kCntTotal, st) == hipSuccess)
+        per_cu * c->num_cus >= Ly->plan.grid && Ly->plan.lds_bytes <= 65536 && K + 1 <= 64 &&
+        hipMalloc(&Ly->sync, Ly->sync_bytes) == hipSuccess &&
+        hipMemsetAsync(Ly->sync, 0, Ly->sync_bytes, st) == hipSuccess)
       Ly->fused = true;
   }
   if (layer >= (int)c->layers.size()) c->layers.resize(layer + 1, nullptr);

@@ -9,25 +9,23 @@ namespace dm {
 
 // Launch geometry and LDS carve-up, computed once per layer on the host.
 struct DecodePlan {
-  int grid;         // persistent workgroups (one per CU, at least 2*H/16)
+  int grid;         // persistent workgroups (one per CU, at least H/16)
   int lds_bytes;
   int off_xs, off_xb, off_pv, off_sel, off_red, off_hb, off_redd;
   int n_router_wg;  // ceil((E+1)/16) router workgroups
-  int s0;           // down halves: slots [0, s0) and [s0, K+1)
+  int s0;           // unused
   int ldh;          // row stride of h (max(I, Ish))
 };
 
-// Cross-workgroup state of one context; counters only grow (launch n waits
-// for n times the arrivals of one launch).
+// Cross-workgroup state of one layer: tagged words carry the launch index in
+// their high half, so a consumer polls the data itself.
 struct DecodeSync {
-  unsigned* cnt_router;  // [1]
-  unsigned* cnt_h;       // [K+1]
-  unsigned* cnt_y;       // [H/16]
-  float* z;              // [E+1] logits
-  float* h;              // [K+1][ldh]
-  float* ypart;          // [2][H]
-  unsigned n;            // launch index, >= 1
+  uint64_t* zt;  // [256*ceil(E/256) + 64] (tag, logit); entry E = shared-expert gate
+  uint64_t* ht;  // [K+1][ldh] (tag, h)
+  unsigned n;    // launch index, >= 1 (the tag of this launch)
 };
+size_t decode_sync_bytes(const LayerDev& L);
+DecodeSync decode_sync_carve(const LayerDev& L, void* base);
 
 DecodePlan make_decode_plan(const LayerDev& L, int num_cus);
 hipError_t decode_occupancy(const LayerDev& L, const DecodePlan& P, int* blocks_per_cu);

@@ -124,3 +124,30 @@ def test_interleaved_layers_of_different_shapes(block, oracle, toy, qwen):
         xq = synth.make_activations(rng, (1, 2048))
         check_layer(block, oracle, toy, 0, xt)
         check_layer(block, oracle, qwen, 1, xq)
+
+
+@pytest.mark.parametrize("gap_ulp", [0, 1, 2, 3, 4, 8, 64])
+def test_routing_near_ties_at_topk_boundary(block, oracle, gap_ulp):
+    """Experts 3 and 4 get logits gap_ulp fp32 ulp apart around the 4th place
+    (0 = exact tie, lowest id must win); ids and probabilities must equal the
+    oracle's bit for bit, including the path that forms the softmax
+    normaliser before selecting."""
+    L = synth.make_layer(**synth.CONFIG_TOY, seed=30)
+    H, E = L.hidden, L.num_experts
+    w = np.zeros((E, H), np.float32)
+    w[:, 0] = 0.5
+    w[0, 0], w[1, 0], w[2, 0] = 1.5, 1.25, 1.125
+    w[3, 0], w[4, 0] = 1.0, 1.0
+    w[3, 1] = 1.0
+    w[4, 1] = 1.0 + gap_ulp * 2.0 ** -7  # z4 - z3 = gap_ulp * 2^-23
+    L.router_bf16 = synth.f32_to_bf16_bits(w).reshape(-1)
+    assert np.array_equal(synth.bf16_bits_to_f32(L.router_bf16).reshape(E, H)[:, :2], w[:, :2])
+    block.upload_layer(40 + gap_ulp % 50, L)
+    x = np.zeros((1, H), np.float32)
+    x[0, 0], x[0, 1] = 1.0, 2.0 ** -16
+    y, ids, probs, shg = block.forward_arrays(40 + gap_ulp % 50, x, 1)
+    yo, ido, po, so = oracle.moe_layer_q4(L, x, 1)
+    assert np.array_equal(ids, ido), (ids, ido)
+    assert np.array_equal(probs.view(np.uint32), po.view(np.uint32))
+    err, rms, ok = tol_check(y, yo)
+    assert ok, (err, rms)
