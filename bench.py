@@ -20,6 +20,20 @@ sys.path.insert(0, os.path.join(ROOT, "disk-streaming-moe-engine_amd"))
 
 METRIC = "MoE-layer decode µs/token + achieved HBM GB/s (4-bit, batch 1, 1 GPU)"
 HBM_PEAK_GBPS = 8000.0
+# HBM bytes per launch of the decode kernel from the rocprofv3 FETCH_SIZE and
+# WRITE_SIZE runs (scaled by a copy-kernel calibration) recorded in this file
+TRAFFIC_PROFILE = os.path.join("profiles", "k_moe_decode_qwen36_layer_decode.md")
+
+
+def profiled_traffic():
+    try:
+        with open(os.path.join(ROOT, TRAFFIC_PROFILE)) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":")[1])
+    except OSError:
+        pass
+    return None
 
 
 def parse():
@@ -27,7 +41,10 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=1000)
     ap.add_argument("--warmup", type=int, default=50)
-    ap.add_argument("--workload", default="decode", choices=["decode", "toy", "stack"])
+    ap.add_argument("--workload", default="decode", choices=["decode", "toy", "stack", "copy"],
+                    help="copy: a plain device copy of --copy-mib MiB, the calibration "
+                         "kernel for HBM byte counters")
+    ap.add_argument("--copy-mib", type=int, default=256)
     ap.add_argument("--layers", type=int, default=40, help="stack workload depth")
     ap.add_argument("--cpu-sample-s", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true")
@@ -60,6 +77,27 @@ def main():
     from dismoen import MoEBlock, synth
 
     dev = torch.device("cuda:0")
+    if a.workload == "copy":
+        n = a.copy_mib * (1 << 20) // 4
+        src = torch.randn(n, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(a.warmup):
+            torch.neg(src, out=dst)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(a.steps):
+            torch.neg(src, out=dst)
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / a.steps
+        nbytes = 2 * n * 4
+        print(json.dumps({"metric": "device copy GB/s (read+write)", "value": round(nbytes / ms / 1e6, 1),
+                          "unit": "GB/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
+                          "ms_per_step": round(ms, 6), "higher_is_better": True,
+                          "read_bytes": n * 4, "write_bytes": n * 4, "dtype": "f32",
+                          "data": "synthetic", "config": {"workload": f"copy {a.copy_mib} MiB"}}))
+        return
     blk = MoEBlock(0)
     # time on the library's own stream (the stream every launch goes to)
     stream = torch.cuda.ExternalStream(blk.stream(), device=dev)
@@ -109,6 +147,7 @@ def main():
         ids_ok = bool(np.array_equal(ids[t_last].cpu().numpy(), ido[0]))
         yl = y[t_last].cpu().numpy().astype(np.float64)
         rel = float(np.max(np.abs(yl - yo[0])) / np.sqrt(np.mean(yo[0].astype(np.float64) ** 2)))
+        traffic = profiled_traffic() if a.workload == "decode" else None
         out = {
             "metric": METRIC, "value": round(us, 3), "unit": "us/token", "n_gpus": 1,
             "steps": a.steps, "warmup": a.warmup, "ms_per_step": round(ms, 6),
@@ -121,7 +160,8 @@ def main():
             "achieved_gbps": round(gbps, 1),
             "roofline": {"bound": "hbm", "kernel": "k_moe_decode (one fused launch per token)",
                          "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                         "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None,
+                         "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": traffic,
+                         "traffic_source": TRAFFIC_PROFILE if traffic else None,
                          "bytes_per_token": bytes_tok},
             "parity_last_token": {"ids_bit_exact": ids_ok, "max_abs_over_rms": rel},
             "wall_s": round(wall, 3),

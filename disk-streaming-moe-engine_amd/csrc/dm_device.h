@@ -27,11 +27,12 @@ __device__ __forceinline__ float bf16hi(uint32_t w) { return u2f(w & 0xFFFF0000u
 // multiply-adds, and scaling by 2^k through the exponent field.  The CPU
 // oracle evaluates the same operation sequence.
 __device__ __forceinline__ float dm_expf(float x) {
-  if (x != x) return x;
-  if (x > 0x1.62e43p+6f) return __builtin_inff();
-  if (x < -0x1.9fe36ap+6f) return 0.0f;
-  float kf = __builtin_rintf(x * 0x1.715476p+0f);
-  float r = __builtin_fmaf(kf, -0x1.62e4p-1f, x);
+  // branch-free form of the same operation sequence: the polynomial path is
+  // evaluated on a clamped argument and the out-of-range cases are selected
+  const bool nan = x != x, over = x > 0x1.62e43p+6f, under = x < -0x1.9fe36ap+6f;
+  const float xc = (nan || over || under) ? 0.0f : x;
+  const float kf = __builtin_rintf(xc * 0x1.715476p+0f);
+  float r = __builtin_fmaf(kf, -0x1.62e4p-1f, xc);
   r = __builtin_fmaf(kf, -0x1.7f7d1cp-20f, r);
   float p = 0x1.a01a02p-13f;
   p = __builtin_fmaf(p, r, 0x1.6c16c2p-10f);
@@ -42,15 +43,16 @@ __device__ __forceinline__ float dm_expf(float x) {
   p = __builtin_fmaf(p, r, 1.0f);
   p = __builtin_fmaf(p, r, 1.0f);
   int k = (int)kf;
-  if (k > 127) {
-    p = p * 0x1p127f;
-    k -= 127;
-  }
-  if (k < -126) {
-    p = p * u2f((uint32_t)(k + 227) << 23);
-    return p * 0x1p-100f;
-  }
-  return p * u2f((uint32_t)(k + 127) << 23);
+  const bool hi = k > 127;
+  p = hi ? p * 0x1p127f : p;
+  k = hi ? k - 127 : k;
+  const bool sub = k < -126;
+  const float s1 = u2f((uint32_t)((sub ? k + 227 : k + 127) & 0xFF) << 23);
+  float res = p * s1;
+  res = sub ? res * 0x1p-100f : res;
+  res = over ? __builtin_inff() : res;
+  res = under ? 0.0f : res;
+  return nan ? x : res;
 }
 
 // sigmoid_f32 / silu_f32 of src/layers/swiglu.mojo:11-38
@@ -238,8 +240,14 @@ __device__ __forceinline__ void stage_split(const float* __restrict__ v, int n, 
 // Columns 0 (hi) + 1 (lo) of an MFMA accumulator: after the exchange, lanes
 // with (lane & 15) == 0 hold rows 4*(lane>>4) + i.
 __device__ __forceinline__ void fold_cols(f32x4& acc) {
+  // quad_perm [1,0,3,2]: lane l reads lane l^1
 #pragma unroll
-  for (int i = 0; i < 4; ++i) acc[i] = acc[i] + __shfl_xor(acc[i], 1);
+  for (int i = 0; i < 4; ++i) {
+    const float v = acc[i];
+    const float o = __builtin_bit_cast(
+        float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, true));
+    acc[i] = v + o;
+  }
 }
 
 }  // namespace dm
