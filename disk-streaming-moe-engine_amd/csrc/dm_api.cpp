@@ -128,6 +128,8 @@ int decode_key(uint64_t key, int layer, int expert_id, int E, char* err, size_t 
       if (kind == kEkGate) EJ(DMH_ERR_EXPERT, "EXPERT_ERROR", "non-finite in gate projection");
       if (kind == kEkUp) EJ(DMH_ERR_EXPERT, "EXPERT_ERROR", "non-finite in up projection");
       if (kind == kEkH) EJ(DMH_ERR_SWIGLU, "SWIGLU_ERROR", "non-finite in element-wise product");
+      if (kind == kEkRecheck)
+        RJ(DMH_ERR_EXPERT, "EXPERT_ERROR", "non-finite value in aggregation", "aggregation");
       EJ(DMH_ERR_EXPERT, "EXPERT_ERROR", "non-finite in down projection");
     case kPhGate:
       if (kind == kGkLogit) RJ(DMH_ERR_GATE, "GATE_ERROR", "non-finite shared gate logit", "shared");
@@ -186,13 +188,14 @@ void free_layer(Layer* Ly) {
 }
 
 hipError_t run_block(dmh_ctx* ctx, Layer* Ly, int layer, const float* dx, const float* dres,
-                     int T, float* dy, int32_t* dids, float* dprobs, float* dshg) {
+                     int T, float* dy, int32_t* dids, float* dprobs, float* dshg,
+                     bool allow_fused = true) {
   const LayerDev& L = Ly->dev;
   hipStream_t st = ctx->cur;
   unsigned long long* status = ctx->status + layer;
   const int ldh = L.I > L.Ish ? L.I : L.Ish;
   hipError_t e;
-  if (Ly->fused) {
+  if (Ly->fused && allow_fused) {
     for (int t = 0; t < T; ++t) {
       if (Ly->launches >= (1u << 24) && (e = reset_counters(ctx, Ly)) != hipSuccess) return e;
       dm::DecodeSync S = dm::decode_sync_carve(L, Ly->sync);
@@ -552,6 +555,19 @@ int dmh_moe_forward(dmh_ctx* c, int layer, const float* x, const float* residual
   if (shg) HIP_TRY(hipMemcpyAsync(shg, dshg, (size_t)T * 4, hipMemcpyDeviceToHost, st));
   HIP_TRY(hipMemcpyAsync(&key, c->status + layer, sizeof(key), hipMemcpyDeviceToHost, st));
   HIP_TRY(hipStreamSynchronize(st));
+  if (dm::key_phase(key) == dm::kPhExpert && dm::key_kind(key) == dm::kEkRecheck) {
+    // The fused kernel folds the routed and shared down projections into one
+    // sum, so a non-finite output does not say which check of the reference
+    // fires first; the multi-kernel path keeps them apart and re-derives it.
+    HIP_TRY(reset_status(c, layer));
+    HIP_TRY(run_block(c, Ly, layer, dx, dres, T, dy, dids, dprobs, dshg, false));
+    HIP_TRY(hipMemcpyAsync(y, dy, TH * 4, hipMemcpyDeviceToHost, st));
+    HIP_TRY(hipMemcpyAsync(hids.data(), dids, TK * 4, hipMemcpyDeviceToHost, st));
+    if (probs) HIP_TRY(hipMemcpyAsync(probs, dprobs, TK * 4, hipMemcpyDeviceToHost, st));
+    if (shg) HIP_TRY(hipMemcpyAsync(shg, dshg, (size_t)T * 4, hipMemcpyDeviceToHost, st));
+    HIP_TRY(hipMemcpyAsync(&key, c->status + layer, sizeof(key), hipMemcpyDeviceToHost, st));
+    HIP_TRY(hipStreamSynchronize(st));
+  }
   if (ids) memcpy(ids, hids.data(), TK * 4);
   int rc = finish_status(c, Ly, layer, key, hids.data(), err, errlen);
   if (rc) HIP_TRY(reset_status(c, layer));

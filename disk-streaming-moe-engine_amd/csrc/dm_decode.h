@@ -10,10 +10,10 @@ namespace dm {
 // Launch geometry and LDS carve-up, computed once per layer on the host.
 struct DecodePlan {
   int grid;         // persistent workgroups (one per CU, at least H/16)
+  int threads;      // workgroup size
   int lds_bytes;
-  int off_xs, off_xb, off_pv, off_sel, off_red, off_hb, off_redd;
+  int off_xt, off_xb, off_zv, off_ev, off_sel, off_red, off_hb, off_yred;
   int n_router_wg;  // ceil((E+1)/16) router workgroups
-  int s0;           // unused
   int ldh;          // row stride of h (max(I, Ish))
 };
 
