@@ -13,15 +13,15 @@ struct DecodePlan {
   int threads;      // workgroup size
   int lds_bytes;
   int off_xt, off_xb, off_zv, off_ev, off_sel, off_red, off_hb, off_yred;
-  int n_router_wg;  // ceil((E+1)/16) router workgroups
-  int ldh;          // row stride of h (max(I, Ish))
+  int n_router_wg;  // router workgroups (4 rows each)
+  int ldh_log2;     // row stride of h: the power of two >= max(I, Ish)
 };
 
 // Cross-workgroup state of one layer: tagged words carry the launch index in
 // their high half, so a consumer polls the data itself.
 struct DecodeSync {
   uint64_t* zt;  // [256*ceil(E/256) + 64] (tag, logit); entry E = shared-expert gate
-  uint64_t* ht;  // [K+1][ldh] (tag, h)
+  uint64_t* ht;  // [K+1][ldh] (tag, h), ldh = 2^ldh_log2 >= max(I, Ish)
   unsigned n;    // launch index, >= 1 (the tag of this launch)
 };
 size_t decode_sync_bytes(const LayerDev& L);

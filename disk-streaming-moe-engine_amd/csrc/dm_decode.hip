@@ -43,11 +43,12 @@ namespace dm {
 
 constexpr int kThreads = 512;
 constexpr int kWaves = kThreads / 64;
-constexpr int kRouterRows = 16;      // router rows per router workgroup (waves 0..3)
+constexpr int kRouterRows = 4;       // router rows per router workgroup (wave 0)
 constexpr int kRwMax = 16;           // router chain chunks (8 bf16 each) held per lane
 constexpr int kDownBatch = 5;        // down chunks per wave held in registers
-constexpr int kPollItems = 2;        // h items (8 values) per thread per poll pass
-constexpr int kProbWave = kWaves - 1;
+constexpr int kHw = 10;              // h words per thread (all polled at once)
+constexpr int kNormWave = 1;          // forms the softmax normaliser during routing
+constexpr int kProbWave = kWaves - 1;  // probabilities, ranks and outputs after routing
 
 // LDS state of the routing decision.
 struct SelState {
@@ -56,10 +57,14 @@ struct SelState {
   int* ids;     // [32] selected experts, slot order
   int* rank;    // [32] position of each slot in the (p desc, id asc) order
   float* pw;    // [33] B-operand weight of slot s: p_s; slot K: the shared gate
-  float* misc;  // [0] shared gate, [1] max logit, [2] ok flag
-  float* p;     // [32] probabilities by slot
-  int* order;   // [32] slots in (p desc, id asc) order
+  float* misc;  // [0] shared gate, [2] ok flag, [3] 1/S
 };
+
+// The wave index as a uniform (scalar) value: derived from threadIdx the
+// compiler treats it as divergent and masks every per-wave branch.
+__device__ __forceinline__ int wave_id() {
+  return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+}
 
 // B operand of a 16x16x32 MFMA from split blocks blk2[2*b + {hi, lo}]:
 // lane (q, j) holds rows 8q..8q+7 of column j; columns 0/1 carry hi/lo, the
@@ -70,21 +75,40 @@ __device__ __forceinline__ bf16x8 ld_b(const uint4* blk2, int blk, int j) {
   return __builtin_bit_cast(bf16x8, v);
 }
 
+// The same operand from separate bf16 arrays hi[] / lo[] (8 values per block).
+__device__ __forceinline__ bf16x8 ld_b2(const uint16_t* hi, const uint16_t* lo, int blk, int j) {
+  uint4 v = *reinterpret_cast<const uint4*>((j & 1 ? lo : hi) + 8 * blk);
+  if (j >= 2) v = make_uint4(0, 0, 0, 0);
+  return __builtin_bit_cast(bf16x8, v);
+}
+
+// fp32 -> bf16 hi + bf16 lo (v ~= hi + lo within 2^-17 relative).
+__device__ __forceinline__ void split1(float v, uint16_t& hi, uint16_t& lo) {
+  const uint32_t h = pack_bf16x2(v, 0.0f) & 0xFFFFu;
+  hi = (uint16_t)h;
+  lo = (uint16_t)(pack_bf16x2(v - u2f(h << 16), 0.0f) & 0xFFFFu);
+}
+
 // ---------------------------------------------------------------------------
 // Gate/up of one 16-row tile: h = SiLU(W_g x) * (W_u x) for rows 16rb..+15,
 // reduced over all H columns inside the workgroup (wave w owns the 128-column
 // chunks w, w+8, ...).  gu_load issues the loads; gu_compute consumes them and
 // stores the 16 h values as (tag, value) words to hdst[row].
-template <int GQW>
+template <int GQW, bool NT>
 __device__ __forceinline__ void gu_load(const ExpertView& gv, const ExpertView& uv, int rb,
                                         uint4 (&wg)[GQW], uint4 (&wu)[GQW], uint2 (&sg)[GQW],
                                         uint2 (&su)[GQW]) {
-  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int w = wave_id(), lane = threadIdx.x & 63;
   const int nGQ = gv.cols / kQuadCols;
+  // unconditional loads (a chunk past the end re-reads the last one and is
+  // not used): conditional loads in unrolled code get serialized
 #pragma unroll
   for (int i = 0; i < GQW; ++i) {
-    const int gq = w + kWaves * i;
-    if (gq < nGQ) {
+    const int gq = min(w + kWaves * i, nGQ - 1);
+    if (NT) {
+      load_chunk_nt(gv, rb, gq, lane, wg[i], sg[i]);
+      load_chunk_nt(uv, rb, gq, lane, wu[i], su[i]);
+    } else {
       load_chunk(gv, rb, gq, lane, wg[i], sg[i]);
       load_chunk(uv, rb, gq, lane, wu[i], su[i]);
     }
@@ -96,9 +120,8 @@ __device__ __forceinline__ void gu_compute(const ExpertView& gv, int rb, const u
                                            const uint4 (&wu)[GQW], const uint2 (&sg)[GQW],
                                            const uint2 (&su)[GQW], const uint4* xb2, float* red,
                                            uint64_t* hdst, unsigned tag, uint32_t phase,
-                                           uint32_t token, int slot, const int* rank,
-                                           unsigned long long* status) {
-  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+                                           uint32_t token, unsigned long long* status) {
+  const int w = wave_id(), lane = threadIdx.x & 63;
   const int q = lane >> 4, j = lane & 15;
   const int nGQ = gv.cols / kQuadCols;
   f32x4 ag = {0, 0, 0, 0}, au = {0, 0, 0, 0};
@@ -126,18 +149,23 @@ __device__ __forceinline__ void gu_compute(const ExpertView& gv, int rb, const u
   __syncthreads();
   if (threadIdx.x < 16) {
     const int r = threadIdx.x, row = rb * kTileRows + r;
-    // error keys name the slot by its position in the reference's order
-    const uint32_t sl = rank ? (uint32_t)rank[slot] : (uint32_t)slot;
     float g = 0.0f, u = 0.0f;
 #pragma unroll
     for (int v = 0; v < kWaves; ++v) {
       g = g + red[v * 32 + r];
       u = u + red[v * 32 + 16 + r];
     }
-    if (!finite_f(g)) record_err(status, err_key(phase, token, sl, row, kEkGate));
-    if (!finite_f(u)) record_err(status, err_key(phase, token, sl, row, kEkUp));
     const float h = dm_silu(g) * u;
-    if (!finite_f(h)) record_err(status, err_key(phase, token, sl, row, kEkH));
+    if (!finite_f(g) || !finite_f(u) || !finite_f(h)) {
+      // shared expert: the exact key (slot 0); routed expert: the slot's
+      // position in the reference's order is formed later, so the host
+      // re-derives the first failing check
+      if (phase == kPhShared)
+        record_err(status, err_key(phase, token, 0, row,
+                                   !finite_f(g) ? kEkGate : !finite_f(u) ? kEkUp : kEkH));
+      else
+        record_err(status, err_key(kPhExpert, token, 0, 0, kEkRecheck));
+    }
     st_coh_u64(hdst + row, ((uint64_t)tag << 32) | f2u(h));
   }
   __syncthreads();
@@ -191,8 +219,8 @@ __device__ __forceinline__ void router_compute(const LayerDev& L, uint4 (&rw)[kR
 
 // ---------------------------------------------------------------------------
 // One selection round set over NK keys per lane (lane l owns experts
-// NK*l .. NK*l+NK-1, so lane order is id order): `rounds` times take the
-// largest remaining key, the lowest id on equal keys.  Winners go to ids[].
+// l + 64 i, i < NK): `rounds` times take the largest remaining key, the
+// lowest id on equal keys (lowest i first, then lowest lane).  Winners go to ids[].
 // Returns the key of each round through kr (kr[0] = first, kr[1] = last,
 // kr[2] = the best key left after `rounds` rounds when want_next).
 template <int NK>
@@ -215,95 +243,182 @@ __device__ __forceinline__ void select_keys(const uint32_t (&key)[NK], int round
     }
     if (it == 0) kr[0] = gm;
     kr[1] = gm;
-    const uint64_t bal = __builtin_amdgcn_ballot_w64(lm == gm);
-    const int fl = bal ? (int)__builtin_ctzll(bal) : 0;
-    if (lane == fl) {
-      int si = 0;
+    int wi = -1, wl = 0;
 #pragma unroll
-      for (int i = NK - 1; i >= 0; --i)
-        if (!(taken >> i & 1u) && key[i] == gm) si = i;
-      taken |= 1u << si;
-      const int e = NK * lane + si;
+    for (int i = 0; i < NK; ++i) {
+      const uint64_t mk = __builtin_amdgcn_ballot_w64(!(taken >> i & 1u) && key[i] == gm);
+      if (wi < 0 && mk) {
+        wi = i;
+        wl = (int)__builtin_ctzll(mk);
+      }
+    }
+    if (wi < 0) wi = 0;
+    if (lane == wl) taken |= 1u << wi;
+    if (lane == 0) {
+      const int e = 64 * wi + wl;
       ids[it] = e < E ? e : E - 1;
     }
     if (!want_next && it == rounds - 1) break;
   }
 }
 
-// Routing on wave 0: poll the tagged logits until every entry carries this
-// launch's tag, select the top-k (fast path on z, exact path on p), the
-// shared gate sigmoid(z_E) (src/layers/moe.mojo:70-100).  Identical in every
-// workgroup; only `record` workgroups write error keys.  Returns false on a
-// poll timeout.
+// The softmax normaliser, summed sequentially in expert order
+// (src/layers/router.mojo:160-170), read from LDS in batches of 64 values.
+__device__ __forceinline__ float seq_sum(const float* v, int n) {
+  float s = 0.0f;
+  const float4* v4 = reinterpret_cast<const float4*>(v);
+  const int n4 = n >> 2;
+  for (int b0 = 0; b0 < n4; b0 += 16) {
+    float4 t[16];
+#pragma unroll
+    for (int u = 0; u < 16; ++u) t[u] = b0 + u < n4 ? v4[b0 + u] : make_float4(0, 0, 0, 0);
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      if (b0 + u < n4) {
+        s = s + t[u].x;
+        s = s + t[u].y;
+        s = s + t[u].z;
+        s = s + t[u].w;
+      }
+    }
+  }
+  for (int e = n4 * 4; e < n; ++e) s = s + v[e];
+  return s;
+}
+
+// Poll the tagged logits until every entry carries this launch's tag.  Lane
+// l holds experts l + 64 i (coalesced loads); lane 0 also the shared-gate
+// logit (entry E) when gl is given.  Returns false on a timeout.
+template <int R>
+__device__ __forceinline__ void issue_logits(const uint64_t* zt, int E, bool gate,
+                                             uint64_t (&v)[4 * R + 1]) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int i = 0; i < 4 * R; ++i) v[i] = ld_coh_u64(zt + min(lane + 64 * i, E - 1));
+  v[4 * R] = gate ? ld_coh_u64(zt + E) : 0;
+}
+template <int R>
+__device__ __forceinline__ bool logits_ready(const uint64_t (&v)[4 * R + 1], unsigned tag, int E,
+                                             bool gate, float (&z)[4 * R], float* gl) {
+  const int lane = threadIdx.x & 63;
+  bool ready = true;
+#pragma unroll
+  for (int i = 0; i < 4 * R; ++i) {
+    z[i] = 0.0f;
+    if (lane + 64 * i < E) {
+      z[i] = u2f((uint32_t)v[i]);
+      ready &= (uint32_t)(v[i] >> 32) == tag;
+    }
+  }
+  if (gate && lane == 0) {
+    *gl = u2f((uint32_t)v[4 * R]);
+    ready &= (uint32_t)(v[4 * R] >> 32) == tag;
+  }
+  return __builtin_amdgcn_ballot_w64(!ready) == 0;
+}
+
+// Poll the tagged logits until every entry carries this launch's tag.  Lane
+// l holds experts l + 64 i (coalesced loads); lane 0 also the shared-gate
+// logit (entry E) when gl is given.  Two polls are kept in flight, so a
+// result lands within about half a round trip.  Returns false on a timeout.
+template <int R>
+__device__ __forceinline__ bool poll_logits(const uint64_t* zt, unsigned tag, int E, float (&z)[4 * R],
+                                            float* gl) {
+  const bool gate = gl != nullptr;
+  uint64_t va[4 * R + 1], vb[4 * R + 1];
+  issue_logits<R>(zt, E, gate, va);
+  for (long spin = 0; spin < kSpinLimit; spin += 2) {
+    issue_logits<R>(zt, E, gate, vb);
+    if (logits_ready<R>(va, tag, E, gate, z, gl)) return true;
+    issue_logits<R>(zt, E, gate, va);
+    if (logits_ready<R>(vb, tag, E, gate, z, gl)) return true;
+  }
+  return false;
+}
+
+__device__ __forceinline__ void wait_lds() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+
+// Routing on wave 0.  Selects the K largest logits with unique 32-bit keys
+// (the high bits of the logit's order key, then the inverted expert id, so
+// one DPP max per round names the winner), then checks that the smallest
+// selected logit and the largest unselected one are far enough apart that
+// p = exp(z - max) * (1/S) keeps them strictly ordered; otherwise it forms S
+// and selects on the exact probabilities with the lowest-id tie-break.  Also
+// the shared gate sigmoid(z_E) (src/layers/moe.mojo:70-100).  Identical in
+// every workgroup; only `record` workgroups write error keys.
 template <int R>
 __device__ __forceinline__ bool route(const uint64_t* zt, unsigned tag, int E, int K, SelState& st,
                                       bool record, int token, unsigned long long* status) {
   constexpr int NK = 4 * R;
+  constexpr int IDB = R == 1 ? 8 : 11;  // id bits of a selection key
+  constexpr uint32_t IDM = (1u << IDB) - 1;
   const int lane = threadIdx.x & 63;
-  const int e0 = NK * lane;
   float z[NK];
   float gl = 0.0f;
-  bool ok = false;
-  for (long spin = 0; spin < kSpinLimit; ++spin) {
-    bool ready = true;
-#pragma unroll
-    for (int i = 0; i < NK; ++i) {
-      z[i] = 0.0f;
-      if (e0 + i < E) {
-        const uint64_t v = ld_coh_u64(zt + e0 + i);
-        z[i] = u2f((uint32_t)v);
-        ready &= (uint32_t)(v >> 32) == tag;
-      }
-    }
-    if (lane == 0) {
-      const uint64_t v = ld_coh_u64(zt + E);
-      gl = u2f((uint32_t)v);
-      ready &= (uint32_t)(v >> 32) == tag;
-    }
-    if (__builtin_amdgcn_ballot_w64(!ready) == 0) {
-      ok = true;
-      break;
-    }
-    __builtin_amdgcn_s_sleep(1);
-  }
+  const bool ok = poll_logits<R>(zt, tag, E, z, &gl);
   if (!ok && lane == 0) record_err(status, err_key(kPhSync, 0, 0, 0, 0));
-  uint32_t key[NK];
+  uint32_t fk[NK], key[NK];
+  uint32_t lm = 0;
 #pragma unroll
   for (int i = 0; i < NK; ++i) {
+    const int e = lane + 64 * i;
+    fk[i] = 0;
     key[i] = 0;
-    const int e = e0 + i;
     if (e < E) {
       st.zv[e] = z[i];
       if (record && !finite_f(z[i])) record_err(status, err_key(kPhLogit, token, 0, e, 0));
-      key[i] = f2key(z[i]);
+      fk[i] = f2key(z[i]);
+      key[i] = ((fk[i] >> IDB) << IDB) | (IDM - (uint32_t)e);
+      lm = fk[i] > lm ? fk[i] : lm;
     }
   }
-  uint32_t kr[3];
-  select_keys<NK>(key, K, E, st.ids, K < E, kr);
-  const float m = key2f(kr[0]);
+  const float m = key2f(wave_max_u32(lm));
   if (record && lane == 0 && !finite_f(m)) record_err(status, err_key(kPhSoftmax, token, 0, 0, 0));
+  uint32_t taken = 0;
+  for (int it = 0; it < K; ++it) {
+    uint32_t km = 0;
+#pragma unroll
+    for (int i = 0; i < NK; ++i) km = key[i] > km ? key[i] : km;
+    const uint32_t gm = wave_max_u32(km);
+#pragma unroll
+    for (int i = 0; i < NK; ++i) {
+      if (key[i] == gm) {
+        key[i] = 0;
+        taken |= 1u << i;
+      }
+    }
+    if (lane == 0) {
+      const uint32_t e = IDM - (gm & IDM);
+      st.ids[it] = e < (uint32_t)E ? (int)e : E - 1;
+    }
+  }
   bool unsafe = false;
   if (K < E) {
-    const float ek = dm_expf(key2f(kr[1]) - m), en = dm_expf(key2f(kr[2]) - m);
+    uint32_t mins = 0xFFFFFFFFu, maxu = 0;
+#pragma unroll
+    for (int i = 0; i < NK; ++i) {
+      if (lane + 64 * i < E) {
+        if (taken >> i & 1u) mins = fk[i] < mins ? fk[i] : mins;
+        else maxu = fk[i] > maxu ? fk[i] : maxu;
+      }
+    }
+    const float zs = key2f(wave_min_u32(mins)), zu = key2f(wave_max_u32(maxu));
+    const float ek = dm_expf(zs - m), en = dm_expf(zu - m);
     unsafe = !(ek > en + en * 0x1p-20f);
   }
   if (unsafe) {  // select on the exact probabilities
     float ev[NK];
 #pragma unroll
     for (int i = 0; i < NK; ++i) {
-      ev[i] = 0.0f;
-      if (e0 + i < E) {
-        ev[i] = dm_expf(z[i] - m);
-        st.ev[e0 + i] = ev[i];
-      }
+      ev[i] = lane + 64 * i < E ? dm_expf(z[i] - m) : 0.0f;
+      st.ev[lane + 64 * i] = ev[i];
     }
-    __builtin_amdgcn_s_waitcnt(0);
+    wait_lds();
     __builtin_amdgcn_wave_barrier();
-    float s = 0.0f;
-    for (int e = 0; e < E; ++e) s = s + st.ev[e];
-    const float inv = 1.0f / s;
+    const float inv = 1.0f / seq_sum(st.ev, 256 * R);
 #pragma unroll
-    for (int i = 0; i < NK; ++i) key[i] = e0 + i < E ? f2u(ev[i] * inv) + 1u : 0u;
+    for (int i = 0; i < NK; ++i) key[i] = lane + 64 * i < E ? f2u(ev[i] * inv) + 1u : 0u;
+    uint32_t kr[3];
     select_keys<NK>(key, K, E, st.ids, false, kr);
   }
   if (lane == 0) {
@@ -312,86 +427,93 @@ __device__ __forceinline__ bool route(const uint64_t* zt, unsigned tag, int E, i
     if (record && (!finite_f(sg) || sg < 0.0f || sg > 1.0f))
       record_err(status, err_key(kPhGate, token, 0, 0, kGkRange));
     st.misc[0] = sg;
-    st.misc[1] = m;
   }
   return ok;
 }
 
-// The softmax normaliser (sequential over e, src/layers/router.mojo:150-183),
-// the K probabilities, their (p desc, id asc) order and the checks of
-// src/layers/topk.mojo:109-128, on one wave.  Writes the slot weights pw[]
-// (p_k; the shared gate for slot K) and ranks; `outputs` also writes ids /
-// probs / shared gate in the reference's order.
+// The softmax normaliser on another wave while wave 0 selects: max, e =
+// exp(z - max) (zero-padded to 256R entries) and S summed sequentially in
+// expert order (src/layers/router.mojo:140-183); 1/S to misc[3].
 template <int R>
+__device__ __forceinline__ void softmax_norm(const uint64_t* zt, unsigned tag, int E, SelState& st,
+                                             bool record, int token, unsigned long long* status) {
+  constexpr int NK = 4 * R;
+  const int lane = threadIdx.x & 63;
+  float z[NK];
+  (void)poll_logits<R>(zt, tag, E, z, nullptr);  // wave 0 reports a timeout
+  uint32_t lm = 0;
+#pragma unroll
+  for (int i = 0; i < NK; ++i)
+    if (lane + 64 * i < E) {
+      const uint32_t k = f2key(z[i]);
+      lm = k > lm ? k : lm;
+    }
+  const float m = key2f(wave_max_u32(lm));
+#pragma unroll
+  for (int i = 0; i < NK; ++i) {
+    const int e = lane + 64 * i;
+    float ev = 0.0f;
+    if (e < E) {
+      ev = dm_expf(z[i] - m);
+      if (record && !finite_f(ev)) record_err(status, err_key(kPhSoftmax, token, 0, 1 + e, 0));
+    }
+    st.ev[e] = ev;
+  }
+  wait_lds();
+  __builtin_amdgcn_wave_barrier();
+  if (lane == 0) {
+    const float s = seq_sum(st.ev, 256 * R);
+    if (record && (!(s > 0.0f) || !finite_f(s)))
+      record_err(status, err_key(kPhSoftmax, token, 0, 1 + E, 0));
+    st.misc[3] = 1.0f / s;
+  }
+}
+
+// After routing, on one wave: the K probabilities p_k = e_k * (1/S), their
+// (p desc, id asc) order (lane k < K finds the rank of slot k by comparing
+// with every other slot) and the checks of src/layers/topk.mojo:109-128.
+// Writes the slot weights pw[] (p_k; the shared gate for slot K) and ranks;
+// `outputs` also writes ids / probs / shared gate in the reference's order.
 __device__ __forceinline__ void finish_probs(int E, int K, SelState& st, bool record, int token,
                                              unsigned long long* status, int32_t* ids_out,
                                              float* probs_out, float* shg_out) {
-  constexpr int NK = 4 * R;
-  const int lane = threadIdx.x & 63, e0 = NK * lane;
-  const float m = st.misc[1];
-#pragma unroll
-  for (int i = 0; i < NK; ++i) {
-    const int e = e0 + i;
-    if (e < E) {
-      const float ev = dm_expf(st.zv[e] - m);
-      if (record && !finite_f(ev)) record_err(status, err_key(kPhSoftmax, token, 0, 1 + e, 0));
-      st.ev[e] = ev;
-    }
+  const int lane = threadIdx.x & 63;
+  const float inv = st.misc[3];
+  const int idk = lane < K ? st.ids[lane] : 0;
+  const float pk = lane < K ? st.ev[idk] * inv : 0.0f;
+  int rank = 0;
+  for (int j2 = 0; j2 < K; ++j2) {
+    const float pj = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, pk), j2));
+    const int idj = __builtin_amdgcn_readlane(idk, j2);
+    rank += (pj > pk || (pj == pk && idj < idk)) ? 1 : 0;
   }
-  __builtin_amdgcn_s_waitcnt(0);
-  __builtin_amdgcn_wave_barrier();
-  if (lane != 0) return;
-  float s = 0.0f;
-  const float4* ev4 = reinterpret_cast<const float4*>(st.ev);
-  int e = 0;
-#pragma unroll 8
-  for (; e + 4 <= E; e += 4) {
-    const float4 v = ev4[e >> 2];
-    s = s + v.x;
-    s = s + v.y;
-    s = s + v.z;
-    s = s + v.w;
-  }
-  for (; e < E; ++e) s = s + st.ev[e];
-  if (record && (!(s > 0.0f) || !finite_f(s)))
-    record_err(status, err_key(kPhSoftmax, token, 0, 1 + E, 0));
-  const float inv = 1.0f / s;
-  float* p = st.p;
-  int* order = st.order;
-  for (int k = 0; k < K; ++k) {
-    p[k] = st.ev[st.ids[k]] * inv;
-    order[k] = k;
-  }
-  for (int a = 1; a < K; ++a) {  // (p desc, id asc)
-    const int v = order[a];
-    int b = a - 1;
-    while (b >= 0 && (p[order[b]] < p[v] || (p[order[b]] == p[v] && st.ids[order[b]] > st.ids[v]))) {
-      order[b + 1] = order[b];
-      --b;
-    }
-    order[b + 1] = v;
-  }
+  // sum of the top-k probabilities in the reference's order
   float sum_topk = 0.0f;
-  for (int k = 0; k < K; ++k) {
-    sum_topk = sum_topk + p[order[k]];
-    st.rank[order[k]] = k;
-    st.pw[k] = p[k];
+  for (int r = 0; r < K; ++r) {
+    const uint64_t mk = __builtin_amdgcn_ballot_w64(lane < K && rank == r);
+    const int src = mk ? (int)__builtin_ctzll(mk) : 0;
+    sum_topk = sum_topk +
+               __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, pk), src));
   }
-  st.pw[K] = st.misc[0];
-  if (record) {
-    if (sum_topk > 1.00001f) record_err(status, err_key(kPhTopk, token, 0, 0, kTkSum));
-    if (K < E && __builtin_fabsf(sum_topk - 1.0f) < 1e-6f) {
-      float sum_all = 0.0f;
-      for (int e2 = 0; e2 < E; ++e2) sum_all = sum_all + st.ev[e2] * inv;
-      if (sum_all - sum_topk > 1e-5f) record_err(status, err_key(kPhTopk, token, 0, 0, kTkLeak));
+  if (lane < K) {
+    st.rank[lane] = rank;
+    st.pw[lane] = pk;
+    if (ids_out) {
+      ids_out[rank] = idk;
+      probs_out[rank] = pk;
     }
   }
-  if (ids_out) {
-    for (int k = 0; k < K; ++k) {
-      ids_out[k] = st.ids[order[k]];
-      probs_out[k] = p[order[k]];
+  if (lane == 0) {
+    st.pw[K] = st.misc[0];
+    if (ids_out) shg_out[0] = st.misc[0];
+    if (record) {
+      if (sum_topk > 1.00001f) record_err(status, err_key(kPhTopk, token, 0, 0, kTkSum));
+      if (K < E && __builtin_fabsf(sum_topk - 1.0f) < 1e-6f) {
+        float sum_all = 0.0f;
+        for (int e2 = 0; e2 < E; ++e2) sum_all = sum_all + st.ev[e2] * inv;
+        if (sum_all - sum_topk > 1e-5f) record_err(status, err_key(kPhTopk, token, 0, 0, kTkLeak));
+      }
     }
-    shg_out[0] = st.misc[0];
   }
 }
 
@@ -405,17 +527,15 @@ __global__ __launch_bounds__(kThreads) void k_moe_decode(
   float* xt = reinterpret_cast<float*>(smem + P.off_xt);
   uint4* xb2 = reinterpret_cast<uint4*>(smem + P.off_xb);
   float* red = reinterpret_cast<float*>(smem + P.off_red);
-  uint4* hb2 = reinterpret_cast<uint4*>(smem + P.off_hb);
   float* yred = reinterpret_cast<float*>(smem + P.off_yred);
   unsigned char* sel = smem + P.off_sel;
   SelState st{reinterpret_cast<float*>(smem + P.off_zv), reinterpret_cast<float*>(smem + P.off_ev),
-              reinterpret_cast<int*>(sel),         reinterpret_cast<int*>(sel + 128),
-              reinterpret_cast<float*>(sel + 256), reinterpret_cast<float*>(sel + 400),
-              reinterpret_cast<float*>(sel + 416), reinterpret_cast<int*>(sel + 544)};
+              reinterpret_cast<int*>(sel), reinterpret_cast<int*>(sel + 128),
+              reinterpret_cast<float*>(sel + 256), reinterpret_cast<float*>(sel + 400)};
 
   const int H = L.H, K = L.K, E = L.E;
   const int b = blockIdx.x, nb = gridDim.x;
-  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+  const int tid = threadIdx.x, w = wave_id(), lane = tid & 63;
   const int q = lane >> 4, j = lane & 15;
   const unsigned n = S.n;
   const int nGQI = L.I / kQuadCols, nGQS = L.Ish / kQuadCols;
@@ -427,94 +547,103 @@ __global__ __launch_bounds__(kThreads) void k_moe_decode(
   const bool router_wg = b < P.n_router_wg;
   const int sh_tile = (b + nb - P.n_router_wg % nb) % nb;
 
-  // ---- entry: every load that depends on neither x nor routing --------------
+  // ---- entry: x first (a wave's loads complete in order), then every load
+  // that depends on neither x nor routing
+  float4 xr[2][2];
+#pragma unroll
+  for (int ii = 0; ii < 2; ++ii) {
+    const int i = min(tid + kThreads * ii, H / 8 - 1);
+    xr[ii][0] = reinterpret_cast<const float4*>(x)[2 * i];
+    xr[ii][1] = reinterpret_cast<const float4*>(x)[2 * i + 1];
+  }
   uint4 rw[kRwMax];
   const int re = b * kRouterRows + (tid >> 4);
-  if (router_wg && tid < kRouterRows * 16 && re <= E) {
-    const uint4* wp = reinterpret_cast<const uint4*>(L.router + r16_index(H, re, tid & 15));
+  if (router_wg && tid < kRouterRows * 16) {
+    const uint4* wp =
+        reinterpret_cast<const uint4*>(L.router + r16_index(H, min(re, E), tid & 15));
 #pragma unroll
-    for (int j8 = 0; j8 < kRwMax; ++j8)
-      if (j8 < H / 128) rw[j8] = wp[(size_t)j8 * 16];
+    for (int j8 = 0; j8 < kRwMax; ++j8) rw[j8] = wp[(size_t)min(j8, H / 128 - 1) * 16];
   }
   const size_t matS = (size_t)L.Ish * H;
   const ExpertView sgv = {L.sgu_nib, L.sgu_sc, L.Ish, H};
   const ExpertView suv = {L.sgu_nib + matS / 2, L.sgu_sc + matS / kGroup, L.Ish, H};
   uint4 swg[GQW], swu[GQW];
   uint2 ssg[GQW], ssu[GQW];
-  if (sh_tile < nsh) gu_load<GQW>(sgv, suv, sh_tile, swg, swu, ssg, ssu);
+  if (sh_tile < nsh) gu_load<GQW, false>(sgv, suv, sh_tile, swg, swu, ssg, ssu);
   const ExpertView sdv = {L.sd_nib, L.sd_sc, H, L.Ish};
   uint4 dw[kDownBatch];
   uint2 ds[kDownBatch];
-#pragma unroll
-  for (int i = 0; i < kDownBatch; ++i) {
-    const int c = w + kWaves * i;
-    if (i < my_chunks && c >= nch_r) load_chunk(sdv, b, c - nch_r, lane, dw[i], ds[i]);
-  }
 
   // ---- stage x: transposed fp32 (router chains) and bf16 hi/lo B blocks -----
   {
     bool bad = false;
-    for (int i = tid; i < H / 8; i += kThreads) {
-      const float4 a = reinterpret_cast<const float4*>(x)[2 * i];
-      const float4 c = reinterpret_cast<const float4*>(x)[2 * i + 1];
-      const float f[8] = {a.x, a.y, a.z, a.w, c.x, c.y, c.z, c.w};
 #pragma unroll
-      for (int k2 = 0; k2 < 8; ++k2) bad |= !finite_f(f[k2]);
-      if (router_wg) {
-        // columns 8i..8i+7 are chains l = 8(i&1)+k2 at step j = i/2
-        const int xts = H / 16 + 4;
-        float* dst = xt + (8 * (i & 1)) * xts + (i >> 1);
+    for (int ii = 0; ii < 2; ++ii) {
+      const int i = tid + kThreads * ii;
+      if (i < H / 8) {  // (loaded unconditionally above, used only when valid)
+        const float f[8] = {xr[ii][0].x, xr[ii][0].y, xr[ii][0].z, xr[ii][0].w,
+                            xr[ii][1].x, xr[ii][1].y, xr[ii][1].z, xr[ii][1].w};
 #pragma unroll
-        for (int k2 = 0; k2 < 8; ++k2) dst[k2 * xts] = f[k2];
+        for (int k2 = 0; k2 < 8; ++k2) bad |= !finite_f(f[k2]);
+        if (router_wg) {
+          // columns 8i..8i+7 are chains l = 8(i&1)+k2 at step j = i/2
+          const int xts = H / 16 + 4;
+          float* dst = xt + (8 * (i & 1)) * xts + (i >> 1);
+#pragma unroll
+          for (int k2 = 0; k2 < 8; ++k2) dst[k2 * xts] = f[k2];
+        }
+        uint4 hi, lo;
+        split8(f, hi, lo);
+        xb2[2 * i + 0] = hi;
+        xb2[2 * i + 1] = lo;
       }
-      uint4 hi, lo;
-      split8(f, hi, lo);
-      xb2[2 * i + 0] = hi;
-      xb2[2 * i + 1] = lo;
     }
     if (bad && b == 0) record_err(status, err_key(kPhX, 0, 0, 0, 0));
   }
   __syncthreads();
 
-  // ---- P1: router rows; shared-expert gate/up tile --------------------------
+  // ---- P1: router rows (wave 0); shared-expert gate/up tile ------------------
   if (router_wg && tid < kRouterRows * 16) router_compute(L, rw, re, xt, S.zt, n);
   for (int rr = b + nb; rr < P.n_router_wg; rr += nb) {  // only when the grid is small
+    // (every workgroup is then a router workgroup and has staged xt)
     if (tid < kRouterRows * 16) {
-      // the transposed x is staged only by router workgroups, which this one is
       const int e2 = rr * kRouterRows + (tid >> 4);
-      if (e2 <= E) {
-        const uint4* wp = reinterpret_cast<const uint4*>(L.router + r16_index(H, e2, tid & 15));
+      {
+        const uint4* wp =
+            reinterpret_cast<const uint4*>(L.router + r16_index(H, min(e2, E), tid & 15));
 #pragma unroll
-        for (int j8 = 0; j8 < kRwMax; ++j8)
-          if (j8 < H / 128) rw[j8] = wp[(size_t)j8 * 16];
+        for (int j8 = 0; j8 < kRwMax; ++j8) rw[j8] = wp[(size_t)min(j8, H / 128 - 1) * 16];
       }
       router_compute(L, rw, e2, xt, S.zt, n);
     }
   }
   for (int t = sh_tile; t < nsh; t += nb) {
-    if (t != sh_tile) gu_load<GQW>(sgv, suv, t, swg, swu, ssg, ssu);
-    gu_compute<GQW>(sgv, t, swg, swu, ssg, ssu, xb2, red, S.ht + (size_t)K * P.ldh, n, kPhShared,
-                    token, 0, nullptr, status);
+    if (t != sh_tile) gu_load<GQW, false>(sgv, suv, t, swg, swu, ssg, ssu);
+    gu_compute<GQW>(sgv, t, swg, swu, ssg, ssu, xb2, red, S.ht + ((size_t)K << P.ldh_log2), n,
+                    kPhShared, token, status);
   }
 
-  // ---- P2: routing (every workgroup computes the same top-k) ----------------
+  // ---- P2: routing on wave 0, softmax normaliser on wave 1 (every workgroup
+  // computes the same result, so there is no broadcast hand-off) -------------
   if (w == 0) {
     const bool rok = route<R>(S.zt, n, E, K, st, b == 0, token, status);
     if (lane == 0) st.misc[2] = rok ? 1.0f : 0.0f;
+  } else if (w == kNormWave) {
+    softmax_norm<R>(S.zt, n, E, st, b == 0, token, status);
   }
   __syncthreads();
   const bool ok = st.misc[2] != 0.0f;
 
-  // ---- P3: routed loads; normaliser; routed gate/up tile --------------------
+  // ---- P3: routed loads; probabilities; routed gate/up tile -----------------
   const size_t matI = (size_t)L.I * H;
   auto gu_views = [&](int t, ExpertView& gv, ExpertView& uv) {
-    const int e = st.ids[t / nrb];
+    const int e = __builtin_amdgcn_readfirstlane(st.ids[t / nrb]);
     gv = {L.gu_nib + (size_t)e * matI, L.gu_sc + (size_t)e * 2 * (matI / kGroup), L.I, H};
     uv = {gv.nib + matI / 2, gv.sc + matI / kGroup, L.I, H};
   };
   const size_t matD = (size_t)H * L.I;
   auto down_view = [&](int s) -> ExpertView {
-    const int e = st.ids[s];
+    const int e = __builtin_amdgcn_readfirstlane(st.ids[s]);
     return {L.d_nib + (size_t)e * (matD / 2), L.d_sc + (size_t)e * (matD / kGroup), H, L.I};
   };
   uint4 gwg[GQW], gwu[GQW];
@@ -522,77 +651,75 @@ __global__ __launch_bounds__(kThreads) void k_moe_decode(
   ExpertView gv, uv;
   if (b < K * nrb) {
     gu_views(b, gv, uv);
-    gu_load<GQW>(gv, uv, b % nrb, gwg, gwu, gsg, gsu);
+    gu_load<GQW, true>(gv, uv, b % nrb, gwg, gwu, gsg, gsu);
   }
+  // down chunks of this workgroup's output tile (routed: non-temporal;
+  // shared: cached), unconditional with clamped indices
+  if (down_wg) {
 #pragma unroll
-  for (int i = 0; i < kDownBatch; ++i) {
-    const int c = w + kWaves * i;
-    if (i < my_chunks && c < nch_r) load_chunk(down_view(c / nGQI), b, c % nGQI, lane, dw[i], ds[i]);
+    for (int i = 0; i < kDownBatch; ++i) {
+      const int c = min(w + kWaves * i, nch - 1);
+      const bool routed = c < nch_r;
+      const ExpertView v = routed ? down_view(c / nGQI) : sdv;
+      load_chunk_nt(v, b, routed ? c % nGQI : c - nch_r, lane, dw[i], ds[i]);
+    }
   }
-  if (w == kProbWave)
-    finish_probs<R>(E, K, st, b == 0, token, status, b == 0 ? ids_out : nullptr, probs_out,
-                    shg_out);
   for (int t = b; t < K * nrb; t += nb) {
     if (t != b) {
       gu_views(t, gv, uv);
-      gu_load<GQW>(gv, uv, t % nrb, gwg, gwu, gsg, gsu);
+      gu_load<GQW, true>(gv, uv, t % nrb, gwg, gwu, gsg, gsu);
     }
     const int k = t / nrb;
-    // (the first barrier inside also publishes the normaliser wave's results)
-    gu_compute<GQW>(gv, t % nrb, gwg, gwu, gsg, gsu, xb2, red, S.ht + (size_t)k * P.ldh, n,
-                    kPhExpert, token, k, st.rank, status);
+    gu_compute<GQW>(gv, t % nrb, gwg, gwu, gsg, gsu, xb2, red, S.ht + ((size_t)k << P.ldh_log2), n,
+                    kPhExpert, token, status);
   }
-  if (K * nrb <= b) __syncthreads();  // publish the normaliser results here instead
   if (!down_wg) return;
 
   // ---- P4: down projection of this workgroup's 16 output rows ---------------
+  // Issue the first poll of h (thread t reads words t, t + 512, ...), then
+  // dequantize the down chunks while it is in flight.
+  const int lg = P.ldh_log2, ldh = 1 << lg;
+  uint16_t* hbh = reinterpret_cast<uint16_t*>(smem + P.off_hb);
+  uint16_t* hbl = hbh + ((size_t)(K + 1) << lg);
+  const int nwords = (K + 1) << lg;
+  uint64_t hv[kHw];
+#pragma unroll
+  for (int u = 0; u < kHw; ++u) {
+    hv[u] = ld_coh_u64(S.ht + min(tid + kThreads * u, nwords - 1));
+  }
+  // the probabilities (slot weights) while the poll is in flight
+  if (w == kProbWave)
+    finish_probs(E, K, st, b == 0, token, status, b == 0 ? ids_out : nullptr, probs_out, shg_out);
+  // keep the dequantization after the poll loads are issued
+#pragma unroll
+  for (int i = 0; i < kDownBatch; ++i)
+    asm volatile("" : "+v"(dw[i].x), "+v"(dw[i].y), "+v"(dw[i].z), "+v"(dw[i].w), "+v"(ds[i].x),
+                 "+v"(ds[i].y)::"memory");
   bf16x8 A[kDownBatch][4];
 #pragma unroll
   for (int i = 0; i < kDownBatch; ++i)
     if (i < my_chunks)
 #pragma unroll
       for (int c = 0; c < 4; ++c) A[i][c] = dequant8(word_of(dw[i], c), scale_of(ds[i], c));
-  // poll the tagged h of all slots; stage h * weight(slot) as split B blocks
-  const int nblk_slot = P.ldh / 8;
-  const int items_r = K * (L.I / 8), items = items_r + L.Ish / 8;
+  __syncthreads();  // publishes finish_probs' slot weights
   {
     bool done = false;
     uint32_t have = 0;
     for (long spin = 0; spin < kSpinLimit; ++spin) {
       bool mine = true;
-      uint64_t v[kPollItems][8];
 #pragma unroll
-      for (int bi = 0; bi < kPollItems; ++bi) {  // all loads of the pass first
-        const int it = tid + kThreads * bi;
-        if (it < items && !(have >> bi & 1u)) {
-          const int s = it < items_r ? it / (L.I / 8) : K;
-          const int ii = it < items_r ? it % (L.I / 8) : it - items_r;
-          const uint64_t* src = S.ht + (size_t)s * P.ldh + 8 * ii;
-#pragma unroll
-          for (int k2 = 0; k2 < 8; ++k2) v[bi][k2] = ld_coh_u64(src + k2);
-        }
-      }
-#pragma unroll
-      for (int bi = 0; bi < kPollItems; ++bi) {
-        const int it = tid + kThreads * bi;
-        if (it < items && !(have >> bi & 1u)) {
-          const int s = it < items_r ? it / (L.I / 8) : K;
-          const int ii = it < items_r ? it % (L.I / 8) : it - items_r;
-          bool tags = true;
-          float f[8];
-          const float wgt = st.pw[s];
-#pragma unroll
-          for (int k2 = 0; k2 < 8; ++k2) {
-            tags &= (uint32_t)(v[bi][k2] >> 32) == n;
-            f[k2] = u2f((uint32_t)v[bi][k2]) * wgt;
-          }
-          if (tags) {
-            uint4 hi, lo;
-            split8(f, hi, lo);
-            uint4* dst = hb2 + 2 * ((size_t)s * nblk_slot + ii);
-            dst[0] = hi;
-            dst[1] = lo;
-            have |= 1u << bi;
+      for (int u = 0; u < kHw; ++u) {
+        const int wd = tid + kThreads * u;
+        if (wd < nwords && !(have >> u & 1u)) {
+          const int s2 = wd >> lg, idx = wd & (ldh - 1);
+          if (idx >= (s2 < K ? L.I : L.Ish)) {  // padding entries: never written
+            have |= 1u << u;
+          } else if ((uint32_t)(hv[u] >> 32) == n) {
+            uint16_t hi, lo;
+            split1(u2f((uint32_t)hv[u]) * st.pw[s2], hi, lo);
+            hbh[wd] = hi;
+            hbl[wd] = lo;
+            have |= 1u << u;
           } else {
             mine = false;
           }
@@ -603,6 +730,9 @@ __global__ __launch_bounds__(kThreads) void k_moe_decode(
         break;
       }
       __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+      for (int u = 0; u < kHw; ++u)  // poll again (unconditional loads stay in flight together)
+        hv[u] = ld_coh_u64(S.ht + min(tid + kThreads * u, nwords - 1));
     }
     if (!done && tid == 0) record_err(status, err_key(kPhSync, 0, 0, 0, 0));
   }
@@ -614,8 +744,9 @@ __global__ __launch_bounds__(kThreads) void k_moe_decode(
       for (int i = 0; i < kDownBatch; ++i) {
         const int c = w + kWaves * (base + i);
         if (base + i < my_chunks) {
-          if (c < nch_r) load_chunk(down_view(c / nGQI), b, c % nGQI, lane, dw[i], ds[i]);
-          else load_chunk(sdv, b, c - nch_r, lane, dw[i], ds[i]);
+          const bool routed = c < nch_r;
+          const ExpertView v = routed ? down_view(c / nGQI) : sdv;
+          load_chunk_nt(v, b, routed ? c % nGQI : c - nch_r, lane, dw[i], ds[i]);
         }
       }
 #pragma unroll
@@ -629,9 +760,11 @@ __global__ __launch_bounds__(kThreads) void k_moe_decode(
       if (base + i < my_chunks) {
         const int c = w + kWaves * (base + i);
         const int s = c < nch_r ? c / nGQI : K, gq = c < nch_r ? c % nGQI : c - nch_r;
-        const uint4* hbs = hb2 + 2 * (size_t)s * nblk_slot;
+        const uint16_t* hs = hbh + ((size_t)s << lg);
+        const uint16_t* ls = hbl + ((size_t)s << lg);
 #pragma unroll
-        for (int cc = 0; cc < 4; ++cc) acc = mfma16(A[i][cc], ld_b(hbs, (gq * 4 + cc) * 4 + q, j), acc);
+        for (int cc = 0; cc < 4; ++cc)
+          acc = mfma16(A[i][cc], ld_b2(hs, ls, (gq * 4 + cc) * 4 + q, j), acc);
       }
     }
   }
@@ -653,11 +786,18 @@ __global__ __launch_bounds__(kThreads) void k_moe_decode(
   }
 }
 
+static int ldh_log2_of(const LayerDev& L) {
+  const int m = L.I > L.Ish ? L.I : L.Ish;
+  int lg = 0;
+  while ((1 << lg) < m) ++lg;
+  return lg;
+}
+
 static int align16(int v) { return (v + 15) & ~15; }
 static size_t align256z(size_t v) { return (v + 255) & ~(size_t)255; }
 
 size_t decode_sync_bytes(const LayerDev& L) {
-  const int ldh = L.I > L.Ish ? L.I : L.Ish;
+  const size_t ldh = (size_t)1 << ldh_log2_of(L);
   const size_t R = (size_t)(L.E + 255) / 256;
   return align256z((256 * R + 64) * 8) + align256z((size_t)(L.K + 1) * ldh * 8);
 }
@@ -674,18 +814,19 @@ DecodeSync decode_sync_carve(const LayerDev& L, void* base) {
 
 DecodePlan make_decode_plan(const LayerDev& L, int num_cus) {
   DecodePlan P{};
-  P.ldh = L.I > L.Ish ? L.I : L.Ish;
+  P.ldh_log2 = ldh_log2_of(L);
+  const int ldh = 1 << P.ldh_log2;
   P.n_router_wg = (L.E + 1 + kRouterRows - 1) / kRouterRows;
   const int R = (L.E + 255) / 256;
   const int slots = L.K + 1;
   int off = 0;
-  P.off_xt = off; off += align16(4 * kRouterRows * (L.H / 16 + 4));
+  P.off_xt = off; off += align16(4 * 16 * (L.H / 16 + 4));  // 16 chains
   P.off_xb = off; off += align16(4 * L.H);
   P.off_zv = off; off += align16(4 * 256 * R);
   P.off_ev = off; off += align16(4 * 256 * R);
   P.off_sel = off; off += 768;
   P.off_red = off; off += align16(kWaves * 2 * 16 * 4);
-  P.off_hb = off; off += align16(slots * (P.ldh / 8) * 32);
+  P.off_hb = off; off += align16(slots * ldh * 4);
   P.off_yred = off; off += align16(kWaves * 16 * 4);
   P.lds_bytes = off;
   P.threads = kThreads;
@@ -701,7 +842,8 @@ static const void* pick_r(int R) {
 static const void* pick_kernel(const LayerDev& L) {
   const int gqw = (L.H / kQuadCols + kWaves - 1) / kWaves;
   const int R = (L.E + 255) / 256;
-  if (R > 8 || L.K > 32) return nullptr;
+  const int ldh = 1 << ldh_log2_of(L);
+  if (R > 8 || L.K > 32 || (L.K + 1) * ldh > kHw * kThreads) return nullptr;
   return gqw <= 2 ? pick_r<2>(R) : gqw <= 8 ? pick_r<8>(R) : nullptr;
 }
 

@@ -211,6 +211,21 @@ __device__ __forceinline__ void load_chunk(const ExpertView& v, int rb, int gq, 
   s = *reinterpret_cast<const uint2*>(v.sc + a16_sc_offset(nGQ, rb, gq, lane & 15));
 }
 
+// The same with non-temporal loads: for weights read once per use (routed
+// experts), so that they do not evict data reused across launches from L2.
+__device__ __forceinline__ void load_chunk_nt(const ExpertView& v, int rb, int gq, int lane,
+                                              uint4& w, uint2& s) {
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+  const int nGQ = v.cols / kQuadCols;
+  const u32x4 a = __builtin_nontemporal_load(
+      reinterpret_cast<const u32x4*>(v.nib + a16_nib_offset(nGQ, rb, gq, lane)));
+  const u32x2 c = __builtin_nontemporal_load(
+      reinterpret_cast<const u32x2*>(v.sc + a16_sc_offset(nGQ, rb, gq, lane & 15)));
+  w = make_uint4(a.x, a.y, a.z, a.w);
+  s = make_uint2(c.x, c.y);
+}
+
 __device__ __forceinline__ float scale_of(const uint2& s, int c) {
   const uint32_t word = c < 2 ? s.x : s.y;
   return fp16_bits_to_f32((c & 1) ? (word >> 16) : (word & 0xFFFFu));
