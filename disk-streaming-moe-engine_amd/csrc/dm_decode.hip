@@ -48,7 +48,6 @@ constexpr int kRwMax = 16;           // router chain chunks (8 bf16 each) held p
 constexpr int kDownBatch = 5;        // down chunks per wave held in registers
 constexpr int kHw = 10;              // h words per thread (all polled at once)
 constexpr int kNormWave = 1;          // forms the softmax normaliser during routing
-constexpr int kProbWave = kWaves - 1;  // probabilities, ranks and outputs after routing
 
 // LDS state of the routing decision.
 struct SelState {
@@ -470,32 +469,36 @@ __device__ __forceinline__ void softmax_norm(const uint64_t* zt, unsigned tag, i
 }
 
 // After routing, on one wave: the K probabilities p_k = e_k * (1/S), their
-// (p desc, id asc) order (lane k < K finds the rank of slot k by comparing
-// with every other slot) and the checks of src/layers/topk.mojo:109-128.
-// Writes the slot weights pw[] (p_k; the shared gate for slot K) and ranks;
-// `outputs` also writes ids / probs / shared gate in the reference's order.
-__device__ __forceinline__ void finish_probs(int E, int K, SelState& st, bool record, int token,
-                                             unsigned long long* status, int32_t* ids_out,
-                                             float* probs_out, float* shg_out) {
+// (p desc, id asc) order and the checks of src/layers/topk.mojo:109-128.
+// Lane k < K owns slot k; it reads every slot's (p, id) from LDS and counts
+// the slots ahead of it, which is its rank.  Writes the slot weights pw[]
+// (p_k; the shared gate for slot K) and ranks; `outputs` also writes ids /
+// probs / shared gate in the reference's order.
+__device__ __forceinline__ void finish_probs(int E, int K, SelState& st, float* scr, bool record,
+                                             int token, unsigned long long* status,
+                                             int32_t* ids_out, float* probs_out,
+                                             float* shg_out) {
   const int lane = threadIdx.x & 63;
   const float inv = st.misc[3];
   const int idk = lane < K ? st.ids[lane] : 0;
   const float pk = lane < K ? st.ev[idk] * inv : 0.0f;
+  float* ps = scr;       // [32] p by slot
+  int* is = reinterpret_cast<int*>(scr + 32);  // [32] id by slot
+  float* sorted = scr + 64;                    // [32] p by rank
+  if (lane < K) {
+    ps[lane] = pk;
+    is[lane] = idk;
+  }
+  wait_lds();
+  __builtin_amdgcn_wave_barrier();
   int rank = 0;
-  for (int j2 = 0; j2 < K; ++j2) {
-    const float pj = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, pk), j2));
-    const int idj = __builtin_amdgcn_readlane(idk, j2);
+  for (int j2 = 0; j2 < K; ++j2) {  // broadcast reads, independent compares
+    const float pj = ps[j2];
+    const int idj = is[j2];
     rank += (pj > pk || (pj == pk && idj < idk)) ? 1 : 0;
   }
-  // sum of the top-k probabilities in the reference's order
-  float sum_topk = 0.0f;
-  for (int r = 0; r < K; ++r) {
-    const uint64_t mk = __builtin_amdgcn_ballot_w64(lane < K && rank == r);
-    const int src = mk ? (int)__builtin_ctzll(mk) : 0;
-    sum_topk = sum_topk +
-               __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, pk), src));
-  }
   if (lane < K) {
+    sorted[rank] = pk;
     st.rank[lane] = rank;
     st.pw[lane] = pk;
     if (ids_out) {
@@ -503,7 +506,11 @@ __device__ __forceinline__ void finish_probs(int E, int K, SelState& st, bool re
       probs_out[rank] = pk;
     }
   }
+  wait_lds();
+  __builtin_amdgcn_wave_barrier();
   if (lane == 0) {
+    float sum_topk = 0.0f;  // in the reference's order
+    for (int r = 0; r < K; ++r) sum_topk = sum_topk + sorted[r];
     st.pw[K] = st.misc[0];
     if (ids_out) shg_out[0] = st.misc[0];
     if (record) {
@@ -664,6 +671,11 @@ __global__ __launch_bounds__(kThreads) void k_moe_decode(
       load_chunk_nt(v, b, routed ? c % nGQI : c - nch_r, lane, dw[i], ds[i]);
     }
   }
+  // the probabilities while this wave's loads are in flight (published by
+  // the first barrier of the gate/up tile, or by the barrier below)
+  if (w == kNormWave)
+    finish_probs(E, K, st, red + kWaves * 32, b == 0, token, status, b == 0 ? ids_out : nullptr,
+                 probs_out, shg_out);
   for (int t = b; t < K * nrb; t += nb) {
     if (t != b) {
       gu_views(t, gv, uv);
@@ -673,6 +685,7 @@ __global__ __launch_bounds__(kThreads) void k_moe_decode(
     gu_compute<GQW>(gv, t % nrb, gwg, gwu, gsg, gsu, xb2, red, S.ht + ((size_t)k << P.ldh_log2), n,
                     kPhExpert, token, status);
   }
+  if (K * nrb <= b) __syncthreads();
   if (!down_wg) return;
 
   // ---- P4: down projection of this workgroup's 16 output rows ---------------
@@ -687,9 +700,6 @@ __global__ __launch_bounds__(kThreads) void k_moe_decode(
   for (int u = 0; u < kHw; ++u) {
     hv[u] = ld_coh_u64(S.ht + min(tid + kThreads * u, nwords - 1));
   }
-  // the probabilities (slot weights) while the poll is in flight
-  if (w == kProbWave)
-    finish_probs(E, K, st, b == 0, token, status, b == 0 ? ids_out : nullptr, probs_out, shg_out);
   // keep the dequantization after the poll loads are issued
 #pragma unroll
   for (int i = 0; i < kDownBatch; ++i)
@@ -701,43 +711,45 @@ __global__ __launch_bounds__(kThreads) void k_moe_decode(
     if (i < my_chunks)
 #pragma unroll
       for (int c = 0; c < 4; ++c) A[i][c] = dequant8(word_of(dw[i], c), scale_of(ds[i], c));
-  __syncthreads();  // publishes finish_probs' slot weights
   {
-    bool done = false;
+    // per word: its slot weight, or a negative mark for padding entries
+    // (never written); each thread re-polls only its own stale words and the
+    // workgroup meets once at the end
+    float wgt[kHw];
+#pragma unroll
+    for (int u = 0; u < kHw; ++u) {
+      const int wd = min(tid + kThreads * u, nwords - 1), s2 = wd >> lg, idx = wd & (ldh - 1);
+      wgt[u] = idx < (s2 < K ? L.I : L.Ish) ? st.pw[s2] : -1.0f;
+    }
     uint32_t have = 0;
-    for (long spin = 0; spin < kSpinLimit; ++spin) {
-      bool mine = true;
+    const uint32_t all = (1u << min(kHw, (nwords - tid + kThreads - 1) / kThreads)) - 1u;
+    for (long spin = 0; spin < kSpinLimit && ok; ++spin) {
 #pragma unroll
       for (int u = 0; u < kHw; ++u) {
-        const int wd = tid + kThreads * u;
-        if (wd < nwords && !(have >> u & 1u)) {
-          const int s2 = wd >> lg, idx = wd & (ldh - 1);
-          if (idx >= (s2 < K ? L.I : L.Ish)) {  // padding entries: never written
+        if (!(have >> u & 1u) && (all >> u & 1u)) {
+          const int wd = tid + kThreads * u;
+          if (wgt[u] < 0.0f) {
             have |= 1u << u;
           } else if ((uint32_t)(hv[u] >> 32) == n) {
             uint16_t hi, lo;
-            split1(u2f((uint32_t)hv[u]) * st.pw[s2], hi, lo);
+            split1(u2f((uint32_t)hv[u]) * wgt[u], hi, lo);
             hbh[wd] = hi;
             hbl[wd] = lo;
             have |= 1u << u;
-          } else {
-            mine = false;
           }
         }
       }
-      if (__syncthreads_and(mine || !ok)) {
-        done = true;
-        break;
-      }
+      if (have == all) break;
       __builtin_amdgcn_s_sleep(1);
 #pragma unroll
-      for (int u = 0; u < kHw; ++u)  // poll again (unconditional loads stay in flight together)
+      for (int u = 0; u < kHw; ++u)  // unconditional loads stay in flight together
         hv[u] = ld_coh_u64(S.ht + min(tid + kThreads * u, nwords - 1));
     }
-    if (!done && tid == 0) record_err(status, err_key(kPhSync, 0, 0, 0, 0));
+    if (!__syncthreads_and(have == all || !ok) && tid == 0)
+      record_err(status, err_key(kPhSync, 0, 0, 0, 0));
   }
-  // one MFMA chain per wave over its chunks: sum_k W_k (p_k h_k) + W_sh (g h_sh)
-  f32x4 acc = {0, 0, 0, 0};
+  // two MFMA chains per wave over its chunks: sum_k W_k (p_k h_k) + W_sh (g h_sh)
+  f32x4 acc = {0, 0, 0, 0}, acc2 = {0, 0, 0, 0};
   for (int base = 0; base < my_chunks; base += kDownBatch) {
     if (base > 0) {  // chunks beyond the register batch
 #pragma unroll
@@ -763,11 +775,15 @@ __global__ __launch_bounds__(kThreads) void k_moe_decode(
         const uint16_t* hs = hbh + ((size_t)s << lg);
         const uint16_t* ls = hbl + ((size_t)s << lg);
 #pragma unroll
-        for (int cc = 0; cc < 4; ++cc)
+        for (int cc = 0; cc < 4; cc += 2) {
           acc = mfma16(A[i][cc], ld_b2(hs, ls, (gq * 4 + cc) * 4 + q, j), acc);
+          acc2 = mfma16(A[i][cc + 1], ld_b2(hs, ls, (gq * 4 + cc + 1) * 4 + q, j), acc2);
+        }
       }
     }
   }
+#pragma unroll
+  for (int r = 0; r < 4; ++r) acc[r] = acc[r] + acc2[r];
   fold_cols(acc);
   if (j == 0) {
 #pragma unroll
@@ -825,7 +841,7 @@ DecodePlan make_decode_plan(const LayerDev& L, int num_cus) {
   P.off_zv = off; off += align16(4 * 256 * R);
   P.off_ev = off; off += align16(4 * 256 * R);
   P.off_sel = off; off += 768;
-  P.off_red = off; off += align16(kWaves * 2 * 16 * 4);
+  P.off_red = off; off += align16(kWaves * 2 * 16 * 4 + 96 * 4);  // + finish_probs scratch
   P.off_hb = off; off += align16(slots * ldh * 4);
   P.off_yred = off; off += align16(kWaves * 16 * 4);
   P.lds_bytes = off;

@@ -100,10 +100,19 @@ __device__ __forceinline__ void split8(const float* v, uint4& hi, uint4& lo) {
 // The half 0x6400|u is 1024+u exactly, and fma(1024+u, s, -1032*s) equals
 // s*(u-8) = s*q exactly (both products fit the fp32 significand), so the
 // only rounding is the final bf16 RNE.
+// (a & m) | o in one instruction: the compiler otherwise emits two, since a
+// VOP3 operand cannot be a 32-bit literal on this target.
+__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t m, uint32_t o) {
+  uint32_t d;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(d) : "v"(a), "s"(m), "v"(o));
+  return d;
+}
+
 __device__ __forceinline__ bf16x8 dequant8(uint32_t w, float s) {
   const uint32_t M = 0x000F000Fu, O = 0x64006400u;
   float c0 = -1032.0f * s;
-  uint32_t r[4] = {(w & M) | O, ((w >> 4) & M) | O, ((w >> 8) & M) | O, ((w >> 12) & M) | O};
+  uint32_t r[4] = {and_or(w, M, O), and_or(w >> 4, M, O), and_or(w >> 8, M, O),
+                   and_or(w >> 12, M, O)};
   uint32_t o[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
