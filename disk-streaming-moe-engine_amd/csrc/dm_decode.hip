@@ -8,19 +8,19 @@
 // each other through tagged words in global memory instead of kernel
 // boundaries:
 //
-//   entry  every workgroup issues the loads that do not depend on x or on
-//          routing: router rows, a shared-expert gate/up tile, shared-expert
-//          down chunks.
-//   P1     router rows (16 per router workgroup, the exact 16-lane order of
+//   entry  x first, then the loads that depend on neither x nor routing:
+//          router rows, a shared-expert gate/up tile.
+//   P1     router rows (4 per router workgroup, the exact 16-lane order of
 //          router_project) -> z;  shared-expert gate/up tile -> h[K].
-//   P2     every workgroup polls z and selects the top-k itself (identical
-//          everywhere, so no broadcast hand-off), then issues its routed
-//          gate/up and down loads.  One wave forms the softmax normaliser and
-//          the probabilities while the loads are in flight.
-//   P3     routed gate/up tile (slot, 16 rows) -> h[k].
-//   P4     down tile (16 output rows, all K+1 slots): poll h, scale each slot
-//          by its weight (p_k, or the shared gate), one MFMA chain per wave,
-//          residual, y.
+//   P2     every workgroup polls z and selects the top-k itself on wave 0
+//          (identical everywhere, so no broadcast hand-off) while wave 1
+//          forms the softmax normaliser and the shared gate.
+//   P3     routed gate/up and down loads; wave 1 forms the probabilities
+//          while they are in flight; routed gate/up tile (slot, 16 rows) ->
+//          h[k], published with its bf16 hi/lo split.
+//   P4     down tile (16 output rows, all K+1 slots): poll h, dequantize the
+//          down chunks meanwhile, MFMA per chunk scaled by its slot's weight
+//          (p_k, or the shared gate), residual, y.
 //
 // Hand-offs are 64-bit (launch tag, value) words: the consumer polls the data
 // itself (one round trip, no counters, nothing reset between launches).
@@ -92,7 +92,7 @@ __device__ __forceinline__ void split1(float v, uint16_t& hi, uint16_t& lo) {
 // Gate/up of one 16-row tile: h = SiLU(W_g x) * (W_u x) for rows 16rb..+15,
 // reduced over all H columns inside the workgroup (wave w owns the 128-column
 // chunks w, w+8, ...).  gu_load issues the loads; gu_compute consumes them and
-// stores the 16 h values as (tag, value) words to hdst[row].
+// stores the 16 h values as (tag, bf16 hi | bf16 lo << 16) words to hdst[row].
 template <int GQW, bool NT>
 __device__ __forceinline__ void gu_load(const ExpertView& gv, const ExpertView& uv, int rb,
                                         uint4 (&wg)[GQW], uint4 (&wu)[GQW], uint2 (&sg)[GQW],
@@ -165,7 +165,10 @@ __device__ __forceinline__ void gu_compute(const ExpertView& gv, int rb, const u
       else
         record_err(status, err_key(kPhExpert, token, 0, 0, kEkRecheck));
     }
-    st_coh_u64(hdst + row, ((uint64_t)tag << 32) | f2u(h));
+    // published as (tag, bf16 hi | bf16 lo << 16): the consumer's MFMA operand
+    uint16_t hh, hl;
+    split1(h, hh, hl);
+    st_coh_u64(hdst + row, ((uint64_t)tag << 32) | ((uint32_t)hl << 16) | hh);
   }
   __syncthreads();
 }
@@ -285,9 +288,6 @@ __device__ __forceinline__ float seq_sum(const float* v, int n) {
   return s;
 }
 
-// Poll the tagged logits until every entry carries this launch's tag.  Lane
-// l holds experts l + 64 i (coalesced loads); lane 0 also the shared-gate
-// logit (entry E) when gl is given.  Returns false on a timeout.
 template <int R>
 __device__ __forceinline__ void issue_logits(const uint64_t* zt, int E, bool gate,
                                              uint64_t (&v)[4 * R + 1]) {
@@ -318,19 +318,18 @@ __device__ __forceinline__ bool logits_ready(const uint64_t (&v)[4 * R + 1], uns
 
 // Poll the tagged logits until every entry carries this launch's tag.  Lane
 // l holds experts l + 64 i (coalesced loads); lane 0 also the shared-gate
-// logit (entry E) when gl is given.  Two polls are kept in flight, so a
-// result lands within about half a round trip.  Returns false on a timeout.
+// logit (entry E) when gl is given.  One poll in flight at a time: loads
+// left in flight would stall the first later reuse of their registers.
+// Returns false on a timeout.
 template <int R>
 __device__ __forceinline__ bool poll_logits(const uint64_t* zt, unsigned tag, int E, float (&z)[4 * R],
                                             float* gl) {
   const bool gate = gl != nullptr;
-  uint64_t va[4 * R + 1], vb[4 * R + 1];
-  issue_logits<R>(zt, E, gate, va);
-  for (long spin = 0; spin < kSpinLimit; spin += 2) {
-    issue_logits<R>(zt, E, gate, vb);
-    if (logits_ready<R>(va, tag, E, gate, z, gl)) return true;
-    issue_logits<R>(zt, E, gate, va);
-    if (logits_ready<R>(vb, tag, E, gate, z, gl)) return true;
+  uint64_t v[4 * R + 1];
+  for (long spin = 0; spin < kSpinLimit; ++spin) {
+    issue_logits<R>(zt, E, gate, v);
+    if (logits_ready<R>(v, tag, E, gate, z, gl)) return true;
+    __builtin_amdgcn_s_sleep(1);
   }
   return false;
 }
@@ -342,9 +341,8 @@ __device__ __forceinline__ void wait_lds() { asm volatile("s_waitcnt lgkmcnt(0)"
 // one DPP max per round names the winner), then checks that the smallest
 // selected logit and the largest unselected one are far enough apart that
 // p = exp(z - max) * (1/S) keeps them strictly ordered; otherwise it forms S
-// and selects on the exact probabilities with the lowest-id tie-break.  Also
-// the shared gate sigmoid(z_E) (src/layers/moe.mojo:70-100).  Identical in
-// every workgroup; only `record` workgroups write error keys.
+// and selects on the exact probabilities with the lowest-id tie-break.
+// Identical in every workgroup; only `record` workgroups write error keys.
 template <int R>
 __device__ __forceinline__ bool route(const uint64_t* zt, unsigned tag, int E, int K, SelState& st,
                                       bool record, int token, unsigned long long* status) {
@@ -353,11 +351,9 @@ __device__ __forceinline__ bool route(const uint64_t* zt, unsigned tag, int E, i
   constexpr uint32_t IDM = (1u << IDB) - 1;
   const int lane = threadIdx.x & 63;
   float z[NK];
-  float gl = 0.0f;
-  const bool ok = poll_logits<R>(zt, tag, E, z, &gl);
+  const bool ok = poll_logits<R>(zt, tag, E, z, nullptr);
   if (!ok && lane == 0) record_err(status, err_key(kPhSync, 0, 0, 0, 0));
-  uint32_t fk[NK], key[NK];
-  uint32_t lm = 0;
+  uint32_t fk[NK], key[NK], key0[NK];
 #pragma unroll
   for (int i = 0; i < NK; ++i) {
     const int e = lane + 64 * i;
@@ -368,43 +364,43 @@ __device__ __forceinline__ bool route(const uint64_t* zt, unsigned tag, int E, i
       if (record && !finite_f(z[i])) record_err(status, err_key(kPhLogit, token, 0, e, 0));
       fk[i] = f2key(z[i]);
       key[i] = ((fk[i] >> IDB) << IDB) | (IDM - (uint32_t)e);
-      lm = fk[i] > lm ? fk[i] : lm;
     }
+    key0[i] = key[i];
   }
-  const float m = key2f(wave_max_u32(lm));
-  if (record && lane == 0 && !finite_f(m)) record_err(status, err_key(kPhSoftmax, token, 0, 0, 0));
-  uint32_t taken = 0;
+  // K rounds: the largest remaining key; its low bits name the expert.  Lane
+  // `it` keeps the id of round it (no branches inside the loop).
+  int myid = 0;
+  uint32_t gm = 0;
+#pragma unroll 8
   for (int it = 0; it < K; ++it) {
     uint32_t km = 0;
 #pragma unroll
     for (int i = 0; i < NK; ++i) km = key[i] > km ? key[i] : km;
-    const uint32_t gm = wave_max_u32(km);
+    gm = wave_max_u32(km);
 #pragma unroll
-    for (int i = 0; i < NK; ++i) {
-      if (key[i] == gm) {
-        key[i] = 0;
-        taken |= 1u << i;
-      }
-    }
-    if (lane == 0) {
-      const uint32_t e = IDM - (gm & IDM);
-      st.ids[it] = e < (uint32_t)E ? (int)e : E - 1;
+    for (int i = 0; i < NK; ++i) key[i] = key[i] == gm ? 0u : key[i];
+    myid = lane == it ? (int)(IDM - (gm & IDM)) : myid;
+  }
+  // selected = key at or above the last winner; exact max, smallest selected
+  // and largest unselected logit in three independent reductions
+  uint32_t lmax = 0, mins = 0xFFFFFFFFu, maxu = 0;
+#pragma unroll
+  for (int i = 0; i < NK; ++i) {
+    if (lane + 64 * i < E) {
+      lmax = fk[i] > lmax ? fk[i] : lmax;
+      if (key0[i] >= gm) mins = fk[i] < mins ? fk[i] : mins;
+      else maxu = fk[i] > maxu ? fk[i] : maxu;
     }
   }
+  const float m = key2f(wave_max_u32(lmax));
+  const float zs = key2f(wave_min_u32(mins)), zu = key2f(wave_max_u32(maxu));
+  if (record && lane == 0 && !finite_f(m)) record_err(status, err_key(kPhSoftmax, token, 0, 0, 0));
   bool unsafe = false;
   if (K < E) {
-    uint32_t mins = 0xFFFFFFFFu, maxu = 0;
-#pragma unroll
-    for (int i = 0; i < NK; ++i) {
-      if (lane + 64 * i < E) {
-        if (taken >> i & 1u) mins = fk[i] < mins ? fk[i] : mins;
-        else maxu = fk[i] > maxu ? fk[i] : maxu;
-      }
-    }
-    const float zs = key2f(wave_min_u32(mins)), zu = key2f(wave_max_u32(maxu));
     const float ek = dm_expf(zs - m), en = dm_expf(zu - m);
     unsafe = !(ek > en + en * 0x1p-20f);
   }
+  if (lane < K) st.ids[lane] = myid < E ? myid : E - 1;
   if (unsafe) {  // select on the exact probabilities
     float ev[NK];
 #pragma unroll
@@ -420,26 +416,21 @@ __device__ __forceinline__ bool route(const uint64_t* zt, unsigned tag, int E, i
     uint32_t kr[3];
     select_keys<NK>(key, K, E, st.ids, false, kr);
   }
-  if (lane == 0) {
-    if (record && !finite_f(gl)) record_err(status, err_key(kPhGate, token, 0, 0, kGkLogit));
-    const float sg = dm_sigmoid(gl);
-    if (record && (!finite_f(sg) || sg < 0.0f || sg > 1.0f))
-      record_err(status, err_key(kPhGate, token, 0, 0, kGkRange));
-    st.misc[0] = sg;
-  }
   return ok;
 }
 
 // The softmax normaliser on another wave while wave 0 selects: max, e =
 // exp(z - max) (zero-padded to 256R entries) and S summed sequentially in
-// expert order (src/layers/router.mojo:140-183); 1/S to misc[3].
+// expert order (src/layers/router.mojo:140-183), 1/S to misc[3]; and the
+// shared-expert gate to misc[0].
 template <int R>
 __device__ __forceinline__ void softmax_norm(const uint64_t* zt, unsigned tag, int E, SelState& st,
                                              bool record, int token, unsigned long long* status) {
   constexpr int NK = 4 * R;
   const int lane = threadIdx.x & 63;
   float z[NK];
-  (void)poll_logits<R>(zt, tag, E, z, nullptr);  // wave 0 reports a timeout
+  float gl = 0.0f;
+  (void)poll_logits<R>(zt, tag, E, z, &gl);  // wave 0 reports a timeout
   uint32_t lm = 0;
 #pragma unroll
   for (int i = 0; i < NK; ++i)
@@ -465,6 +456,12 @@ __device__ __forceinline__ void softmax_norm(const uint64_t* zt, unsigned tag, i
     if (record && (!(s > 0.0f) || !finite_f(s)))
       record_err(status, err_key(kPhSoftmax, token, 0, 1 + E, 0));
     st.misc[3] = 1.0f / s;
+    // the shared-expert gate sigmoid(z_E) (src/layers/moe.mojo:70-100)
+    if (record && !finite_f(gl)) record_err(status, err_key(kPhGate, token, 0, 0, kGkLogit));
+    const float sg = dm_sigmoid(gl);
+    if (record && (!finite_f(sg) || sg < 0.0f || sg > 1.0f))
+      record_err(status, err_key(kPhGate, token, 0, 0, kGkRange));
+    st.misc[0] = sg;
   }
 }
 
@@ -692,54 +689,70 @@ __global__ __launch_bounds__(kThreads) void k_moe_decode(
   // Issue the first poll of h (thread t reads words t, t + 512, ...), then
   // dequantize the down chunks while it is in flight.
   const int lg = P.ldh_log2, ldh = 1 << lg;
-  uint16_t* hbh = reinterpret_cast<uint16_t*>(smem + P.off_hb);
-  uint16_t* hbl = hbh + ((size_t)(K + 1) << lg);
+  uint16_t* hbh = reinterpret_cast<uint16_t*>(smem + P.off_hb);  // [K+1][ldh] bf16 hi
+  uint16_t* hbl = hbh + ((size_t)(K + 1) << lg);                  // [K+1][ldh] bf16 lo
   const int nwords = (K + 1) << lg;
   uint64_t hv[kHw];
 #pragma unroll
   for (int u = 0; u < kHw; ++u) {
     hv[u] = ld_coh_u64(S.ht + min(tid + kThreads * u, nwords - 1));
   }
-  // keep the dequantization after the poll loads are issued
-#pragma unroll
-  for (int i = 0; i < kDownBatch; ++i)
+  // Dequantize the down chunks while the poll is in flight; a second poll
+  // is issued halfway, so that words still stale in the first one are
+  // usually current in the second.  (The empty asm statements pin the
+  // order: the compiler would otherwise hoist the dequantization.)
+  auto pin = [&](int i) {
     asm volatile("" : "+v"(dw[i].x), "+v"(dw[i].y), "+v"(dw[i].z), "+v"(dw[i].w), "+v"(ds[i].x),
                  "+v"(ds[i].y)::"memory");
+  };
   bf16x8 A[kDownBatch][4];
-#pragma unroll
-  for (int i = 0; i < kDownBatch; ++i)
+  auto deq = [&](int i) {
     if (i < my_chunks)
 #pragma unroll
       for (int c = 0; c < 4; ++c) A[i][c] = dequant8(word_of(dw[i], c), scale_of(ds[i], c));
+  };
+  constexpr int kHalf = (kDownBatch + 1) / 2;
+#pragma unroll
+  for (int i = 0; i < kHalf; ++i) pin(i);
+#pragma unroll
+  for (int i = 0; i < kHalf; ++i) deq(i);
+  uint64_t hv2[kHw];
+#pragma unroll
+  for (int u = 0; u < kHw; ++u) hv2[u] = ld_coh_u64(S.ht + min(tid + kThreads * u, nwords - 1));
+#pragma unroll
+  for (int i = kHalf; i < kDownBatch; ++i) pin(i);
+#pragma unroll
+  for (int i = kHalf; i < kDownBatch; ++i) deq(i);
   {
-    // per word: its slot weight, or a negative mark for padding entries
-    // (never written); each thread re-polls only its own stale words and the
-    // workgroup meets once at the end
-    float wgt[kHw];
+    // padding entries of a slot row are never written: they count as staged;
+    // each thread re-polls only its own stale words and the workgroup meets
+    // once at the end
+    uint32_t have = 0;
 #pragma unroll
     for (int u = 0; u < kHw; ++u) {
       const int wd = min(tid + kThreads * u, nwords - 1), s2 = wd >> lg, idx = wd & (ldh - 1);
-      wgt[u] = idx < (s2 < K ? L.I : L.Ish) ? st.pw[s2] : -1.0f;
+      if (idx >= (s2 < K ? L.I : L.Ish)) have |= 1u << u;
     }
-    uint32_t have = 0;
     const uint32_t all = (1u << min(kHw, (nwords - tid + kThreads - 1) / kThreads)) - 1u;
+    have &= all;
     for (long spin = 0; spin < kSpinLimit && ok; ++spin) {
 #pragma unroll
       for (int u = 0; u < kHw; ++u) {
         if (!(have >> u & 1u) && (all >> u & 1u)) {
           const int wd = tid + kThreads * u;
-          if (wgt[u] < 0.0f) {
-            have |= 1u << u;
-          } else if ((uint32_t)(hv[u] >> 32) == n) {
-            uint16_t hi, lo;
-            split1(u2f((uint32_t)hv[u]) * wgt[u], hi, lo);
-            hbh[wd] = hi;
-            hbl[wd] = lo;
+          if ((uint32_t)(hv[u] >> 32) == n) {
+            hbh[wd] = (uint16_t)hv[u];
+            hbl[wd] = (uint16_t)(hv[u] >> 16);
             have |= 1u << u;
           }
         }
       }
       if (have == all) break;
+      if (spin == 0) {  // stale in the first poll: the later one (waited for only here)
+#pragma unroll
+        for (int u = 0; u < kHw; ++u) hv[u] = hv2[u];
+        continue;
+      }
       __builtin_amdgcn_s_sleep(1);
 #pragma unroll
       for (int u = 0; u < kHw; ++u)  // unconditional loads stay in flight together
@@ -748,8 +761,9 @@ __global__ __launch_bounds__(kThreads) void k_moe_decode(
     if (!__syncthreads_and(have == all || !ok) && tid == 0)
       record_err(status, err_key(kPhSync, 0, 0, 0, 0));
   }
-  // two MFMA chains per wave over its chunks: sum_k W_k (p_k h_k) + W_sh (g h_sh)
-  f32x4 acc = {0, 0, 0, 0}, acc2 = {0, 0, 0, 0};
+  // per chunk two MFMA chains over its four k-steps, then the slot weight:
+  // y = sum_k p_k (W_k h_k) + g (W_sh h_sh)
+  f32x4 acc = {0, 0, 0, 0};
   for (int base = 0; base < my_chunks; base += kDownBatch) {
     if (base > 0) {  // chunks beyond the register batch
 #pragma unroll
@@ -774,16 +788,20 @@ __global__ __launch_bounds__(kThreads) void k_moe_decode(
         const int s = c < nch_r ? c / nGQI : K, gq = c < nch_r ? c % nGQI : c - nch_r;
         const uint16_t* hs = hbh + ((size_t)s << lg);
         const uint16_t* ls = hbl + ((size_t)s << lg);
+        const float wgt = st.pw[s];
+        bf16x8 B[4];
 #pragma unroll
-        for (int cc = 0; cc < 4; cc += 2) {
-          acc = mfma16(A[i][cc], ld_b2(hs, ls, (gq * 4 + cc) * 4 + q, j), acc);
-          acc2 = mfma16(A[i][cc + 1], ld_b2(hs, ls, (gq * 4 + cc + 1) * 4 + q, j), acc2);
-        }
+        for (int cc = 0; cc < 4; ++cc) B[cc] = ld_b2(hs, ls, (gq * 4 + cc) * 4 + q, j);
+        f32x4 a0 = {0, 0, 0, 0}, a1 = {0, 0, 0, 0};
+        a0 = mfma16(A[i][0], B[0], a0);
+        a1 = mfma16(A[i][1], B[1], a1);
+        a0 = mfma16(A[i][2], B[2], a0);
+        a1 = mfma16(A[i][3], B[3], a1);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[r] = acc[r] + wgt * (a0[r] + a1[r]);
       }
     }
   }
-#pragma unroll
-  for (int r = 0; r < 4; ++r) acc[r] = acc[r] + acc2[r];
   fold_cols(acc);
   if (j == 0) {
 #pragma unroll
