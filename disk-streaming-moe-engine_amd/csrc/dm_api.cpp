@@ -11,6 +11,7 @@
 
 #include "../../include/dismoen_hip.h"
 #include "dm_decode.h"
+#include "dm_grouped.h"
 #include "dm_kernels.h"
 #include "dm_layout.h"
 
@@ -66,6 +67,11 @@ struct dmh_ctx {
   DevBuf<float> x, res, y, z, probs, shg, h, xn, hstack;
   DevBuf<int32_t> ids;
   DevBuf<uint8_t> stage;
+  // several tokens per call (grouped experts)
+  DevBuf<int32_t> g_off, g_perm, g_meta, g_needlo;
+  DevBuf<int2> g_units;
+  DevBuf<uint16_t> g_xhi, g_xlo;
+  DevBuf<float> g_hr, g_hs, g_r, g_rs;
   unsigned long long* status = nullptr;  // [kMaxLayers + 1] first-error keys (last = unit calls)
   unsigned long long* vkey = nullptr;    // upload validation key
   unsigned* flags = nullptr;             // upload flags
@@ -195,7 +201,7 @@ hipError_t run_block(dmh_ctx* ctx, Layer* Ly, int layer, const float* dx, const 
   unsigned long long* status = ctx->status + layer;
   const int ldh = L.I > L.Ish ? L.I : L.Ish;
   hipError_t e;
-  if (Ly->fused && allow_fused) {
+  if (Ly->fused && allow_fused && T == 1) {
     for (int t = 0; t < T; ++t) {
       if (Ly->launches >= (1u << 24) && (e = reset_counters(ctx, Ly)) != hipSuccess) return e;
       dm::DecodeSync S = dm::decode_sync_carve(L, Ly->sync);
@@ -214,6 +220,36 @@ hipError_t run_block(dmh_ctx* ctx, Layer* Ly, int layer, const float* dx, const 
   if ((e = dm::launch_router_select(ctx->z.p, L.E + 1, T, L.E, L.K, 1, dids, dprobs, dshg, status,
                                     st)) != hipSuccess)
     return e;
+  if (T > 1) {
+    // several tokens: group the assignments by expert and run each expert's
+    // tokens together as a grouped GEMM
+    const size_t TK = (size_t)T * L.K, TH = (size_t)T * L.H;
+    if ((e = ctx->g_off.ensure(L.E + 1)) != hipSuccess) return e;
+    if ((e = ctx->g_perm.ensure(TK)) != hipSuccess) return e;
+    if ((e = ctx->g_meta.ensure(1)) != hipSuccess) return e;
+    if ((e = ctx->g_needlo.ensure(1)) != hipSuccess) return e;
+    if ((e = ctx->g_units.ensure(dm::group_units_max(T, L.K, L.E))) != hipSuccess) return e;
+    if ((e = ctx->g_xhi.ensure(TH)) != hipSuccess) return e;
+    if ((e = ctx->g_xlo.ensure(TH)) != hipSuccess) return e;
+    if ((e = ctx->g_hr.ensure(TK * L.I)) != hipSuccess) return e;
+    if ((e = ctx->g_hs.ensure((size_t)T * L.Ish)) != hipSuccess) return e;
+    if ((e = ctx->g_r.ensure(TK * L.H)) != hipSuccess) return e;
+    if ((e = ctx->g_rs.ensure(TH)) != hipSuccess) return e;
+    if ((e = dm::launch_group_build(dids, T, L.K, L.E, ctx->g_off.p, ctx->g_perm.p,
+                                    ctx->g_units.p, ctx->g_meta.p, st)) != hipSuccess)
+      return e;
+    if ((e = hipMemsetAsync(ctx->g_needlo.p, 0, sizeof(int), st)) != hipSuccess) return e;
+    if ((e = dm::launch_split_rows(dx, (int64_t)TH, ctx->g_xhi.p, ctx->g_xlo.p, ctx->g_needlo.p,
+                                   st)) != hipSuccess)
+      return e;
+    if ((e = dm::launch_experts_grouped(L, ctx->g_xhi.p, ctx->g_xlo.p, ctx->g_needlo.p,
+                                        ctx->g_off.p, ctx->g_perm.p, ctx->g_units.p,
+                                        ctx->g_meta.p, T, ctx->g_hr.p, ctx->g_hs.p, ctx->g_r.p,
+                                        ctx->g_rs.p, status, st)) != hipSuccess)
+      return e;
+    return dm::launch_combine(ctx->g_r.p, ctx->g_rs.p, dprobs, dshg, dres, T, L.H, L.K, dy, status,
+                              st);
+  }
   for (int t = 0; t < T; ++t) {
     const float* xt = dx + (size_t)t * L.H;
     if ((e = dm::launch_gateup_dec(L, xt, dids + (size_t)t * L.K, ctx->h.p, ldh, t, status, st)) !=
@@ -292,6 +328,15 @@ int dmh_destroy(dmh_ctx* c) {
   for (auto* b : fb) b->release();
   c->ids.release();
   c->stage.release();
+  c->g_off.release();
+  c->g_perm.release();
+  c->g_meta.release();
+  c->g_needlo.release();
+  c->g_units.release();
+  c->g_xhi.release();
+  c->g_xlo.release();
+  DevBuf<float>* gb[] = {&c->g_hr, &c->g_hs, &c->g_r, &c->g_rs};
+  for (auto* b : gb) b->release();
   if (c->status) (void)hipFree(c->status);
   if (c->vkey) (void)hipFree(c->vkey);
   if (c->flags) (void)hipFree(c->flags);

@@ -1,0 +1,35 @@
+// dm_grouped.h -- the MoE block for several tokens at once (dm_grouped.hip).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "dm_layout.h"
+
+namespace dm {
+
+// Upper bound of the work units for T tokens (size of the units buffer).
+int group_units_max(int T, int K, int E);
+
+// Group the T*K assignments by expert: off [E+1], perm [T*K], units, meta[0].
+hipError_t launch_group_build(const int32_t* ids, int T, int K, int E, int32_t* off,
+                              int32_t* perm, int2* units, int32_t* meta, hipStream_t st);
+
+// n fp32 values (n % 8 == 0) -> bf16 hi / lo; *need_lo |= 1 if a lo part is nonzero
+// (the caller zeroes *need_lo first).
+hipError_t launch_split_rows(const float* x, int64_t n, uint16_t* hi, uint16_t* lo, int* need_lo,
+                             hipStream_t st);
+
+// Routed and shared experts of all units: h (hr [T*K][I], hs [T][Ish]) then the
+// down projections r [T*K][H] (by assignment t*K + k) and rs [T][H].
+hipError_t launch_experts_grouped(const LayerDev& L, const uint16_t* xhi, const uint16_t* xlo,
+                                  const int* need_lo, const int32_t* off, const int32_t* perm,
+                                  const int2* units, const int32_t* meta, int T, float* hr,
+                                  float* hs, float* r, float* rs, unsigned long long* status,
+                                  hipStream_t st);
+
+// y = sum_k p_k r_k + g rs (+ residual), per token in the reference order.
+hipError_t launch_combine(const float* r, const float* rs, const float* probs, const float* shg,
+                          const float* residual, int T, int H, int K, float* y,
+                          unsigned long long* status, hipStream_t st);
+
+}  // namespace dm

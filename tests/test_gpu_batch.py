@@ -1,0 +1,124 @@
+"""GPU parity of the MoE block for several tokens per call (small batches and
+prefill: routing, grouping of the tokens by expert, grouped expert GEMMs,
+combine) against the CPU oracle.
+
+Bar as for decode: ids and probabilities bit-exact, the no-residual output
+within max-abs-err <= 1e-3 x RMS(oracle output).  Every token's output depends
+only on its own activation, so at prefill size the oracle is run on a sample
+of the batch's tokens and compared with those rows."""
+import numpy as np
+import pytest
+
+from conftest import tol_check
+from dismoen import synth
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def qwen(block):
+    L = synth.make_layer(**synth.CONFIG_QWEN36, seed=11)
+    block.upload_layer(5, L)
+    return L
+
+
+def _check(block, oracle, L, layer, x, residual=None, pool=None):
+    T = x.shape[0]
+    y, ids, probs, shg = block.forward_arrays(layer, x, T, residual=residual)
+    yo, ido, po, so = oracle.moe_layer_q4(L, x, T, residual=residual, pool=pool)
+    assert np.array_equal(ids, ido)
+    assert np.array_equal(probs.view(np.uint32), po.view(np.uint32))
+    assert np.array_equal(shg.view(np.uint32), so.view(np.uint32))
+    if residual is None:
+        err, rms, ok = tol_check(y, yo)
+    else:
+        err, rms, ok = tol_check(y - residual, yo - residual)
+    assert ok, (err, rms)
+
+
+@pytest.mark.parametrize("T", [2, 8, 32])
+def test_small_batch_vs_oracle(block, oracle, qwen, T):
+    x = synth.make_activations(np.random.default_rng(200 + T), (T, 2048))
+    pool = oracle.Pool(8)
+    try:
+        _check(block, oracle, qwen, 5, x, pool=pool)
+        if T == 8:
+            _check(block, oracle, qwen, 5, x, residual=x, pool=pool)
+    finally:
+        pool.close()
+
+
+def test_batch_matches_single_token_calls(block, qwen):
+    """The grouped path and the single-token decode kernel agree token by token."""
+    T = 48
+    x = synth.make_activations(np.random.default_rng(300), (T, 2048))
+    y, ids, probs, shg = block.forward_arrays(5, x, T)
+    for t in range(0, T, 5):
+        y1, ids1, p1, s1 = block.forward_arrays(5, x[t:t + 1], 1)
+        assert np.array_equal(ids[t], ids1[0])
+        assert np.array_equal(probs[t].view(np.uint32), p1[0].view(np.uint32))
+        err, rms, ok = tol_check(y1[0], y[t])
+        assert ok, (t, err, rms)
+
+
+def test_fp32_activations_need_lo_parts(block, oracle, qwen):
+    """Activations that are not bf16 values exercise the bf16 lo pass."""
+    rng = np.random.default_rng(301)
+    x = rng.standard_normal((12, 2048)).astype(np.float32)
+    _check(block, oracle, qwen, 5, x)
+
+
+def test_prefill_2048_tokens_sampled_vs_oracle(block, oracle, qwen):
+    T = 2048
+    x = synth.make_activations(np.random.default_rng(302), (T, 2048))
+    y, ids, probs, shg = block.forward_arrays(5, x, T)
+    sample = np.random.default_rng(303).choice(T, 24, replace=False)
+    pool = oracle.Pool(8)
+    try:
+        yo, ido, po, so = oracle.moe_layer_q4(qwen, x[sample], len(sample), pool=pool)
+    finally:
+        pool.close()
+    assert np.array_equal(ids[sample], ido)
+    assert np.array_equal(probs[sample].view(np.uint32), po.view(np.uint32))
+    for i, t in enumerate(sample):
+        err, rms, ok = tol_check(y[t], yo[i])
+        assert ok, (t, err, rms)
+    # every token used exactly K distinct experts
+    assert all(len(set(r)) == 8 for r in ids.tolist())
+
+
+def test_batch_deterministic(block, qwen):
+    x = synth.make_activations(np.random.default_rng(304), (200, 2048))
+    a = block.forward_arrays(5, x, 200)
+    b = block.forward_arrays(5, x, 200)
+    for u, v in zip(a, b):
+        assert np.array_equal(np.asarray(u).view(np.uint8), np.asarray(v).view(np.uint8))
+
+
+def test_batch_nonfinite_activation_error_matches_oracle(block, oracle, qwen):
+    from dismoen import DismoenError
+    x = synth.make_activations(np.random.default_rng(305), (5, 2048))
+    x[3, 17] = np.nan
+    with pytest.raises(DismoenError) as e_gpu:
+        block.forward_arrays(5, x, 5)
+    with pytest.raises(oracle.OracleError) as e_cpu:
+        oracle.moe_layer_q4(qwen, x, 5, layer=5)
+    assert str(e_gpu.value) == str(e_cpu.value)
+
+
+def test_batch_overflow_error_matches_oracle(block, oracle):
+    """An overflowing activation in one token of a batch: the first failing
+    check (in the reference's order of tokens, phases and rows) gives the same
+    error text as the oracle."""
+    from dismoen import DismoenError
+    L = synth.make_layer(**synth.CONFIG_TOY, seed=7)
+    block.upload_layer(6, L)
+    x = synth.make_activations(np.random.default_rng(306), (4, 256))
+    x[2] *= np.float32(3e37)
+    msgs = []
+    for call in (lambda: block.forward_arrays(6, x, 4),
+                 lambda: oracle.moe_layer_q4(L, x, 4, layer=6)):
+        with pytest.raises((DismoenError, oracle.OracleError)) as e:
+            call()
+        msgs.append(str(e.value))
+    assert msgs[0] == msgs[1], msgs
