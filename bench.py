@@ -41,9 +41,15 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=1000)
     ap.add_argument("--warmup", type=int, default=50)
-    ap.add_argument("--workload", default="decode", choices=["decode", "toy", "stack", "copy"],
-                    help="copy: a plain device copy of --copy-mib MiB, the calibration "
+    ap.add_argument("--workload", default="decode",
+                    choices=["decode", "toy", "stack", "batch", "prefill", "copy"],
+                    help="batch: --batch tokens per call (ragged small-batch decode); "
+                         "prefill: --tokens per call with Zipf-skewed routing; "
+                         "copy: a plain device copy of --copy-mib MiB, the calibration "
                          "kernel for HBM byte counters")
+    ap.add_argument("--batch", type=int, default=32, help="tokens per call, batch workload")
+    ap.add_argument("--tokens", type=int, default=2048, help="tokens per call, prefill workload")
+    ap.add_argument("--zipf-s", type=float, default=1.1, help="prefill router skew exponent")
     ap.add_argument("--copy-mib", type=int, default=256)
     ap.add_argument("--layers", type=int, default=40, help="stack workload depth")
     ap.add_argument("--cpu-sample-s", type=float, default=15.0)
@@ -64,6 +70,115 @@ def cpu_baseline(L, x_tokens, budget_s):
     dt = time.perf_counter() - t0
     return {"value": round(dt / n * 1e6, 1), "unit": "us/token", "cores": 1, "kind": "port",
             "sample": f"{n} decode tokens of the same layer, dequant-per-use, threads=1"}
+
+
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+
+
+def grouped(a, blk, stream, dev):
+    """Several tokens per call: routing, count/scan/scatter by expert, grouped
+    expert GEMMs and the ordered combine.  batch: fresh tokens every step,
+    HBM-bound, bytes = union of the step's experts + shared + router + x/y.
+    prefill: a chunk of tokens per step with a Zipf(s) log-popularity router
+    bias (folded into router column 0, activations' feature 0 = 1), reported
+    as tokens/s and MFMA utilisation of the algorithmic FLOPs."""
+    import numpy as np
+    import torch
+
+    from dismoen import synth
+    cfg = synth.CONFIG_QWEN36
+    L = synth.make_layer(**cfg, seed=a.seed)
+    prefill = a.workload == "prefill"
+    if prefill:
+        L = synth.with_router_bias(L, synth.zipf_router_bias(L.num_experts, a.zipf_s, a.seed + 5))
+    blk.upload_layer(0, L)
+    H, E, K, I, Ish = L.hidden, L.num_experts, L.top_k, L.inter, L.inter_sh
+    T = a.tokens if prefill else a.batch
+    nbuf = (a.warmup + a.steps) if not prefill else min(a.warmup + a.steps, 8)
+    rng = np.random.default_rng(a.seed + 2000)
+    x_host = synth.make_activations(rng, (nbuf, T, H))
+    if prefill:
+        x_host = synth.bias_feature(x_host)
+    x = torch.from_numpy(x_host).to(dev)
+    y = torch.empty((nbuf, T, H), dtype=torch.float32, device=dev)
+    ids = torch.empty((nbuf, T, K), dtype=torch.int32, device=dev)
+    probs = torch.empty((nbuf, T, K), dtype=torch.float32, device=dev)
+    shg = torch.empty((nbuf, T), dtype=torch.float32, device=dev)
+    xp, yp, ip, pp, sp = (t.data_ptr() for t in (x, y, ids, probs, shg))
+
+    def step(i):
+        b = i % nbuf
+        blk.forward_device(0, xp + b * T * H * 4, T, yp + b * T * H * 4, ip + b * T * K * 4,
+                           pp + b * T * K * 4, sp + b * T * 4)
+
+    for i in range(a.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    blk.sync()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for i in range(a.warmup, a.warmup + a.steps):
+        step(i)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    blk.sync()
+    ms = e0.elapsed_time(e1) / a.steps
+    ids_h = ids.cpu().numpy()
+    used = [i % nbuf for i in range(a.warmup, a.warmup + a.steps)]
+    unions = [len(np.unique(ids_h[b])) for b in used]
+    u_mean = float(np.mean(unions))
+    eb = synth.expert_bytes(H, I)
+    counts = np.bincount(ids_h[used[-1]].reshape(-1), minlength=E)
+    # parity spot check of a few tokens of the last step against the oracle
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+    b = used[-1]
+    smp = np.random.default_rng(7).choice(T, min(T, 4), replace=False)
+    yo, ido, _, _ = O.moe_layer_q4(L, x_host[b][smp], len(smp))
+    yg = y[b].cpu().numpy()[smp].astype(np.float64)
+    rel = max(float(np.max(np.abs(yg[j] - yo[j])) / np.sqrt(np.mean(yo[j].astype(np.float64) ** 2)))
+              for j in range(len(smp)))
+    ids_ok = bool(np.array_equal(ids_h[b][smp], ido))
+    us = ms * 1e3
+    common = {"n_gpus": 1, "steps": a.steps, "warmup": a.warmup, "ms_per_step": round(ms, 6),
+              "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+              "parity_sample": {"tokens": len(smp), "ids_bit_exact": ids_ok,
+                                "max_abs_over_rms": rel}}
+    if not prefill:
+        nbytes = u_mean * eb + synth.expert_bytes(H, Ish) + 2 * E * H + 2 * H + T * H * 8
+        gbps = nbytes / (ms * 1e-3) / 1e9
+        out = {"metric": f"MoE-layer small-batch decode µs/token + achieved HBM GB/s "
+                         f"(4-bit, batch {T}, 1 GPU)",
+               "value": round(us / T, 3), "unit": "us/token", "higher_is_better": False,
+               "us_per_step": round(us, 3), **common,
+               "config": {"workload": f"qwen3.6-35b-a3b moe layer, batch-{T} decode",
+                          "batch": T, "hidden": H, "experts": E, "top_k": K, "inter": I,
+                          "group": 32, "bits": 4},
+               "expert_union_mean": round(u_mean, 2),
+               "roofline": {"bound": "hbm", "kernel": "grouped path (router, build, gate/up, "
+                            "down, combine)", "achieved": round(gbps, 1),
+                            "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                            "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None,
+                            "bytes_per_step": int(nbytes)}}
+    else:
+        flops = T * (K + 1) * 2 * 3 * H * I + 2 * T * E * H
+        tflops = flops / (ms * 1e-3) / 1e12
+        out = {"metric": "MoE-layer prefill tokens/s + MFMA utilisation (4-bit weights, bf16 "
+                         "MFMA, 1 GPU)",
+               "value": round(T / (ms * 1e-3), 1), "unit": "tokens/s", "higher_is_better": True,
+               "us_per_step": round(us, 3), **common,
+               "config": {"workload": f"qwen3.6-35b-a3b moe layer, {T}-token prefill chunk, "
+                                      f"zipf(s={a.zipf_s}) router bias",
+                          "tokens": T, "hidden": H, "experts": E, "top_k": K, "inter": I,
+                          "group": 32, "bits": 4},
+               "experts_touched": int((counts > 0).sum()),
+               "hottest_expert_tokens": int(counts.max()),
+               "roofline": {"bound": "mfma", "kernel": "grouped path (router, build, gate/up, "
+                            "down, combine)", "achieved": round(tflops, 2),
+                            "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                            "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": None,
+                            "flops_per_step": flops}}
+    print(json.dumps(out))
 
 
 def main():
@@ -169,6 +284,8 @@ def main():
         if not a.no_cpu:
             out["cpu_baseline"] = cpu_baseline(L, x_host, a.cpu_sample_s)
         print(json.dumps(out))
+    elif a.workload in ("batch", "prefill"):
+        grouped(a, blk, stream, dev)
     else:  # stack
         cfg = synth.CONFIG_QWEN36
         nl = a.layers

@@ -71,7 +71,8 @@ struct dmh_ctx {
   DevBuf<int32_t> g_off, g_perm, g_meta, g_needlo;
   DevBuf<int2> g_units;
   DevBuf<uint16_t> g_xhi, g_xlo;
-  DevBuf<float> g_hr, g_hs, g_r, g_rs;
+  DevBuf<uint16_t> g_hr, g_hs;  // bf16 hi parts, then lo parts
+  DevBuf<float> g_r, g_rs;
   unsigned long long* status = nullptr;  // [kMaxLayers + 1] first-error keys (last = unit calls)
   unsigned long long* vkey = nullptr;    // upload validation key
   unsigned* flags = nullptr;             // upload flags
@@ -231,8 +232,8 @@ hipError_t run_block(dmh_ctx* ctx, Layer* Ly, int layer, const float* dx, const 
     if ((e = ctx->g_units.ensure(dm::group_units_max(T, L.K, L.E))) != hipSuccess) return e;
     if ((e = ctx->g_xhi.ensure(TH)) != hipSuccess) return e;
     if ((e = ctx->g_xlo.ensure(TH)) != hipSuccess) return e;
-    if ((e = ctx->g_hr.ensure(TK * L.I)) != hipSuccess) return e;
-    if ((e = ctx->g_hs.ensure((size_t)T * L.Ish)) != hipSuccess) return e;
+    if ((e = ctx->g_hr.ensure(2 * TK * L.I)) != hipSuccess) return e;
+    if ((e = ctx->g_hs.ensure(2 * (size_t)T * L.Ish)) != hipSuccess) return e;
     if ((e = ctx->g_r.ensure(TK * L.H)) != hipSuccess) return e;
     if ((e = ctx->g_rs.ensure(TH)) != hipSuccess) return e;
     if ((e = dm::launch_group_build(dids, T, L.K, L.E, ctx->g_off.p, ctx->g_perm.p,
@@ -244,7 +245,8 @@ hipError_t run_block(dmh_ctx* ctx, Layer* Ly, int layer, const float* dx, const 
       return e;
     if ((e = dm::launch_experts_grouped(L, ctx->g_xhi.p, ctx->g_xlo.p, ctx->g_needlo.p,
                                         ctx->g_off.p, ctx->g_perm.p, ctx->g_units.p,
-                                        ctx->g_meta.p, T, ctx->g_hr.p, ctx->g_hs.p, ctx->g_r.p,
+                                        ctx->g_meta.p, T, ctx->g_hr.p, ctx->g_hr.p + TK * L.I,
+                                        ctx->g_hs.p, ctx->g_hs.p + (size_t)T * L.Ish, ctx->g_r.p,
                                         ctx->g_rs.p, status, st)) != hipSuccess)
       return e;
     return dm::launch_combine(ctx->g_r.p, ctx->g_rs.p, dprobs, dshg, dres, T, L.H, L.K, dy, status,
@@ -335,8 +337,10 @@ int dmh_destroy(dmh_ctx* c) {
   c->g_units.release();
   c->g_xhi.release();
   c->g_xlo.release();
-  DevBuf<float>* gb[] = {&c->g_hr, &c->g_hs, &c->g_r, &c->g_rs};
-  for (auto* b : gb) b->release();
+  c->g_hr.release();
+  c->g_hs.release();
+  c->g_r.release();
+  c->g_rs.release();
   if (c->status) (void)hipFree(c->status);
   if (c->vkey) (void)hipFree(c->vkey);
   if (c->flags) (void)hipFree(c->flags);

@@ -19,13 +19,14 @@ hipError_t launch_group_build(const int32_t* ids, int T, int K, int E, int32_t* 
 hipError_t launch_split_rows(const float* x, int64_t n, uint16_t* hi, uint16_t* lo, int* need_lo,
                              hipStream_t st);
 
-// Routed and shared experts of all units: h (hr [T*K][I], hs [T][Ish]) then the
-// down projections r [T*K][H] (by assignment t*K + k) and rs [T][H].
+// Routed and shared experts of all units: h as bf16 hi / lo parts (hrh, hrl
+// [T*K][I] by position in expert order; hsh, hsl [T][Ish]), then the down
+// projections r [T*K][H] (by assignment t*K + k) and rs [T][H].
 hipError_t launch_experts_grouped(const LayerDev& L, const uint16_t* xhi, const uint16_t* xlo,
                                   const int* need_lo, const int32_t* off, const int32_t* perm,
-                                  const int2* units, const int32_t* meta, int T, float* hr,
-                                  float* hs, float* r, float* rs, unsigned long long* status,
-                                  hipStream_t st);
+                                  const int2* units, const int32_t* meta, int T, uint16_t* hrh,
+                                  uint16_t* hrl, uint16_t* hsh, uint16_t* hsl, float* r,
+                                  float* rs, unsigned long long* status, hipStream_t st);
 
 // y = sum_k p_k r_k + g rs (+ residual), per token in the reference order.
 hipError_t launch_combine(const float* r, const float* rs, const float* probs, const float* shg,

@@ -10,14 +10,17 @@
 //   k_router_dec / k_router_select (dm_kernels.hip)  logits, softmax, top-k
 //   k_group_build   one workgroup: count assignments per expert, scan,
 //                   scatter them into expert order, emit the work units
-//                   (expert, 64-token tile); the shared expert follows as
-//                   expert E over all tokens
-//   k_split_rows    activations -> bf16 hi / lo rows (lo only when needed)
-//   k_gu_grouped    h = SiLU(W_g x) * (W_u x): per unit and 64-feature block,
-//                   A = dequantized 4-bit weights (16 features x 32 k per
-//                   MFMA), B = 16 gathered tokens; one dequantized tile feeds
-//                   every token sub-tile of the unit
-//   k_down_grouped  r = W_d h, B = h split into bf16 hi / lo on the fly
+//                   (expert, tile of up to 128 tokens); the shared expert is
+//                   expert E over all tokens.  Units of more than 16 tokens
+//                   ("big") come first, then the small ones.
+//   k_split_rows    activations -> bf16 hi / lo rows
+//   k_gu_big        h = SiLU(W_g x) * (W_u x) for big units: A = 4-bit weights
+//                   dequantised in registers (16 features x 32 k per MFMA),
+//                   B = the unit's token rows staged in LDS per 128-column
+//                   step (double-buffered, one barrier per step)
+//   k_gu_small      the same for units of <= 16 tokens: B fragments straight
+//                   from memory, no LDS and no barriers, deeper prefetch
+//   k_down_big / k_down_small   r = W_d h, B = h as bf16 hi + lo parts
 //   k_combine       y = sum_k p_k r_k + g r_sh (+ residual), reference order
 //
 // Each token's outputs depend only on its own column of the MFMA tiles, so
@@ -30,24 +33,29 @@
 
 namespace dm {
 
-constexpr int kMT = 64;       // tokens per work unit (4 MFMA column tiles of 16)
+constexpr int kMT = 128;       // tokens per big work unit (8 MFMA column tiles of 16)
+constexpr int kNCT = kMT / 16;
+constexpr int kSmallMax = 16;  // units of at most this many tokens are small
 constexpr int kGThreads = 256;
 
 // ---------------------------------------------------------------------------
 // One workgroup of 1024 threads.  ids [T*K] in the reference order (slot k of
 // token t at t*K + k).  Outputs: off [E+1] expert offsets into perm, perm
 // [T*K] assignment indices grouped by expert, units [nmax] (expert, tile),
-// meta[0] = number of units.
+// meta[0] = number of units, meta[1] = number of big units.  Order: full
+// routed tiles, full shared tiles, partial big routed tiles, a partial big
+// shared tile, then the small routed tiles and a small shared tile, so that
+// the costly workgroups start first.
 __global__ __launch_bounds__(1024) void k_group_build(const int32_t* __restrict__ ids, int T, int K,
                                                       int E, int32_t* __restrict__ off,
                                                       int32_t* __restrict__ perm,
                                                       int2* __restrict__ units,
                                                       int32_t* __restrict__ meta) {
-  extern __shared__ int lds[];  // cnt[E] | cur[E] | part[1024] | upart[1024]
+  // cnt[E] | cur[E] | 4 scans of 1024: counts, full tiles, partial big, small
+  extern __shared__ int lds[];
   int* cnt = lds;
   int* cur = lds + E;
-  int* part = lds + 2 * E;
-  int* upart = part + 1024;
+  int* sc = lds + 2 * E;
   const int tid = threadIdx.x, TK = T * K;
   for (int e = tid; e < E; e += 1024) cnt[e] = 0;
   __syncthreads();
@@ -56,47 +64,62 @@ __global__ __launch_bounds__(1024) void k_group_build(const int32_t* __restrict_
     atomicAdd(&cnt[e], 1);
   }
   __syncthreads();
-  // scan of counts and of unit counts: thread tid owns experts [e0, e1)
+  // thread tid owns experts [e0, e1)
   const int per = (E + 1023) / 1024, e0 = min(tid * per, E), e1 = min(e0 + per, E);
-  int s = 0, us = 0;
+  int v[4] = {0, 0, 0, 0};
   for (int e = e0; e < e1; ++e) {
-    s += cnt[e];
-    us += (cnt[e] + kMT - 1) / kMT;
+    const int c = cnt[e], r = c % kMT;
+    v[0] += c;
+    v[1] += c / kMT;
+    v[2] += r > kSmallMax;
+    v[3] += r > 0 && r <= kSmallMax;
   }
-  part[tid] = s;
-  upart[tid] = us;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) sc[i * 1024 + tid] = v[i];
   __syncthreads();
-  for (int d = 1; d < 1024; d <<= 1) {  // inclusive Hillis-Steele scan
-    const int a = tid >= d ? part[tid - d] : 0, b = tid >= d ? upart[tid - d] : 0;
+  for (int d = 1; d < 1024; d <<= 1) {  // inclusive Hillis-Steele scans
+    int a[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) a[i] = tid >= d ? sc[i * 1024 + tid - d] : 0;
     __syncthreads();
-    part[tid] += a;
-    upart[tid] += b;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) sc[i * 1024 + tid] += a[i];
     __syncthreads();
   }
-  int base = part[tid] - s, ubase = upart[tid] - us;
+  const int nf = sc[1024 + 1023], npb = sc[2048 + 1023], nps = sc[3072 + 1023];
+  const int sf = T / kMT, sr = T % kMT;
+  const int spb = sr > kSmallMax, sps = sr > 0 && sr <= kSmallMax;
+  const int pb0 = nf + sf, s0 = pb0 + npb + spb;
+  int base = sc[tid] - v[0], fb = sc[1024 + tid] - v[1], pb = pb0 + sc[2048 + tid] - v[2],
+      ps = s0 + sc[3072 + tid] - v[3];
   for (int e = e0; e < e1; ++e) {
+    const int c = cnt[e], nfe = c / kMT, r = c % kMT;
     off[e] = base;
     cur[e] = base;
-    const int nt = (cnt[e] + kMT - 1) / kMT;
-    for (int tc = 0; tc < nt; ++tc) units[ubase + tc] = make_int2(e, tc);
-    base += cnt[e];
-    ubase += nt;
+    for (int tc = 0; tc < nfe; ++tc) units[fb + tc] = make_int2(e, tc);
+    if (r > kSmallMax) units[pb++] = make_int2(e, nfe);
+    else if (r > 0) units[ps++] = make_int2(e, nfe);
+    base += c;
+    fb += nfe;
   }
-  const int nrouted = upart[1023];
   if (tid == 0) off[E] = TK;
   __syncthreads();
   for (int a = tid; a < TK; a += 1024) {
     const int e = min(max((int)ids[a], 0), E - 1);
     perm[atomicAdd(&cur[e], 1)] = a;
   }
-  const int nsh = (T + kMT - 1) / kMT;
-  for (int tc = tid; tc < nsh; tc += 1024) units[nrouted + tc] = make_int2(E, tc);
-  if (tid == 0) meta[0] = nrouted + nsh;
+  for (int tc = tid; tc < sf; tc += 1024) units[nf + tc] = make_int2(E, tc);
+  if (tid == 0) {
+    if (spb) units[pb0 + npb] = make_int2(E, sf);
+    if (sps) units[s0 + nps] = make_int2(E, sf);
+    meta[0] = s0 + nps + sps;
+    meta[1] = s0;
+  }
 }
 
 hipError_t launch_group_build(const int32_t* ids, int T, int K, int E, int32_t* off,
                               int32_t* perm, int2* units, int32_t* meta, hipStream_t st) {
-  const size_t lds = (size_t)(2 * E + 2048) * sizeof(int);
+  const size_t lds = (size_t)(2 * E + 4096) * sizeof(int);
   hipLaunchKernelGGL(k_group_build, dim3(1), dim3(1024), lds, st, ids, T, K, E, off, perm, units,
                      meta);
   return hipGetLastError();
@@ -135,9 +158,9 @@ hipError_t launch_split_rows(const float* x, int64_t n, uint16_t* hi, uint16_t* 
 }
 
 // ---------------------------------------------------------------------------
-// Token rows of a unit: column c of tile (e, tc) is position p = off[e] +
-// 64 tc + c of the expert order, i.e. assignment a = perm[p] of token a / K;
-// for the shared expert (e == E) column c is token 64 tc + c itself.
+// Token rows of a unit: row r of tile (e, tc) is position p = off[e] + kMT tc
+// + r of the expert order, i.e. assignment a = perm[p] of token a / K; for the
+// shared expert (e == E) row r is token kMT tc + r itself.
 struct UnitTokens {
   int e, p0, n;   // expert, first position, tokens in this unit
   bool shared;
@@ -156,198 +179,438 @@ __device__ __forceinline__ UnitTokens unit_tokens(int2 u, const int32_t* off, in
   return r;
 }
 
-// ---------------------------------------------------------------------------
-// Gate/up: blockIdx.x = unit, blockIdx.y = block of 64 features (4 row tiles,
-// wave w owns tile 4*blockIdx.y + w) of the gate and the up matrix.  Output
-// h [p][I] fp32 at the unit's positions (routed) or hs [t][Ish] (shared).
-__global__ __launch_bounds__(kGThreads) void k_gu_grouped(
-    LayerDev L, const uint16_t* __restrict__ xhi, const uint16_t* __restrict__ xlo,
-    const int* __restrict__ need_lo, const int32_t* __restrict__ off,
-    const int32_t* __restrict__ perm, const int2* __restrict__ units,
-    const int32_t* __restrict__ meta, int T, float* __restrict__ hr, float* __restrict__ hs,
-    unsigned long long* status) {
-  if ((int)blockIdx.x >= meta[0]) return;
-  const UnitTokens ut = unit_tokens(units[blockIdx.x], off, L.E, T);
-  const int H = L.H, K = L.K;
-  const int I = ut.shared ? L.Ish : L.I;
-  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
-  const int q = lane >> 4, j = lane & 15;
-  const int rb = blockIdx.y * 4 + w;
-  if (rb * kTileRows >= I) return;  // (uniform per wave; no barriers below)
-  const size_t mat = (size_t)I * H;
-  ExpertView gv, uv;
-  if (ut.shared) {
-    gv = {L.sgu_nib, L.sgu_sc, I, H};
-  } else {
-    gv = {L.gu_nib + (size_t)ut.e * mat, L.gu_sc + (size_t)ut.e * 2 * (mat / kGroup), I, H};
+struct GroupArgs {
+  LayerDev L;
+  const uint16_t* xhi;   // [T][H] bf16 parts of the activations
+  const uint16_t* xlo;
+  const int* need_lo;    // nonzero: some activation is not a bf16 value
+  const int32_t* off;
+  const int32_t* perm;
+  const int2* units;
+  const int32_t* meta;
+  int T;
+  uint16_t* hrh;         // h of routed positions [T*K][I], bf16 hi / lo
+  uint16_t* hrl;
+  uint16_t* hsh;         // h of the shared expert [T][Ish]
+  uint16_t* hsl;
+  float* r;              // routed down outputs [T*K][H] by assignment
+  float* rs;             // shared down outputs [T][H]
+  unsigned long long* status;
+};
+
+__device__ __forceinline__ int gwave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
+
+typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+
+// The four A chunks (16 rows x 128 columns, 4-bit + scales) of one k-step.
+struct AChunks {
+  uint4 w[4];
+  uint2 s[4];
+};
+
+__device__ __forceinline__ void load_a4(const ExpertView& v01, const ExpertView& v23, int rb0,
+                                        int rstep, int s, int lane, AChunks& a) {
+  // tiles 0, 1 of view v01 at rb0, rb0 + rstep; tiles 2, 3 of v23 likewise
+  // (gate/up: rstep 1 within each matrix; down: one view, rows rb0 + tl)
+  load_chunk_nt(v01, rb0, s, lane, a.w[0], a.s[0]);
+  load_chunk_nt(v01, rb0 + rstep, s, lane, a.w[1], a.s[1]);
+  load_chunk_nt(v23, rb0 + (v01.nib == v23.nib ? 2 * rstep : 0), s, lane, a.w[2], a.s[2]);
+  load_chunk_nt(v23, rb0 + (v01.nib == v23.nib ? 3 * rstep : rstep), s, lane, a.w[3], a.s[3]);
+}
+
+__device__ __forceinline__ void dequant_a4(const AChunks& a, int kk, bf16x8 (&av)[4]) {
+#pragma unroll
+  for (int tl = 0; tl < 4; ++tl) av[tl] = dequant8(word_of(a.w[tl], kk), scale_of(a.s[tl], kk));
+}
+
+__device__ __forceinline__ void split4(const float* v, uint2& hi, uint2& lo) {
+  float h[4], l[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t hb = pack_bf16x2(v[i], 0.0f) & 0xFFFFu;
+    h[i] = u2f(hb << 16);
+    l[i] = v[i] - h[i];
   }
-  uv = {gv.nib + mat / 2, gv.sc + mat / kGroup, I, H};
-  const bool lo = need_lo[0] != 0;
-  // token row of each column tile for this lane (column j)
-  int tok[4];
-  bool valid[4];
+  hi = make_uint2(pack_bf16x2(h[0], h[1]), pack_bf16x2(h[2], h[3]));
+  lo = make_uint2(pack_bf16x2(l[0], l[1]), pack_bf16x2(l[2], l[3]));
+}
+
+// ---- epilogues -------------------------------------------------------------
+// Gate/up: tiles 0/1 are gate features f0 + 16 half + 4q + i, tiles 2/3 the
+// up features; h = SiLU(g) * u with the reference's checks
+// (src/layers/swiglu.mojo:191-201), stored as bf16 hi / lo.
+template <int NC>
+__device__ __forceinline__ void gu_epilogue(const GroupArgs& g, const UnitTokens& ut, int I,
+                                            int f0, int q, int j, const f32x4 (&acc)[4][NC]) {
+  const int K = g.L.K;
 #pragma unroll
-  for (int ts = 0; ts < 4; ++ts) {
-    const int c = 16 * ts + j;
-    valid[ts] = c < ut.n;
-    const int cc = valid[ts] ? c : 0;
-    tok[ts] = ut.shared ? ut.p0 + cc : perm[ut.p0 + cc] / K;
-  }
-  f32x4 ag[4], au[4];
+  for (int ct = 0; ct < NC; ++ct) {
+    const int c = 16 * ct + j;
+    if (c < ut.n) {
+      const int p = ut.p0 + c;
+      const int a = ut.shared ? p : g.perm[p];
+      const int t = ut.shared ? p : a / K, k = ut.shared ? 0 : a % K;
 #pragma unroll
-  for (int ts = 0; ts < 4; ++ts) ag[ts] = au[ts] = f32x4{0, 0, 0, 0};
-  const int nGQ = H / kQuadCols;
-  const int nts = (ut.n + 15) / 16;
-  for (int gq = 0; gq < nGQ; ++gq) {
-    uint4 wg, wu;
-    uint2 sg, su;
-    load_chunk_nt(gv, rb, gq, lane, wg, sg);
-    load_chunk_nt(uv, rb, gq, lane, wu, su);
+      for (int half = 0; half < 2; ++half) {
+        const int fr = f0 + 16 * half + 4 * q;
+        float hv[4];
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const bf16x8 a_g = dequant8(word_of(wg, c), scale_of(sg, c));
-      const bf16x8 a_u = dequant8(word_of(wu, c), scale_of(su, c));
-      const int k0 = gq * kQuadCols + c * kGroup + 8 * q;
-#pragma unroll
-      for (int ts = 0; ts < 4; ++ts) {
-        if (ts < nts) {
-          uint4 bv = *reinterpret_cast<const uint4*>(xhi + (size_t)tok[ts] * H + k0);
-          if (!valid[ts]) bv = make_uint4(0, 0, 0, 0);
-          const bf16x8 b = __builtin_bit_cast(bf16x8, bv);
-          ag[ts] = mfma16(a_g, b, ag[ts]);
-          au[ts] = mfma16(a_u, b, au[ts]);
-          if (lo) {
-            uint4 lv = *reinterpret_cast<const uint4*>(xlo + (size_t)tok[ts] * H + k0);
-            if (!valid[ts]) lv = make_uint4(0, 0, 0, 0);
-            const bf16x8 bl = __builtin_bit_cast(bf16x8, lv);
-            ag[ts] = mfma16(a_g, bl, ag[ts]);
-            au[ts] = mfma16(a_u, bl, au[ts]);
+        for (int i = 0; i < 4; ++i) {
+          const float gg = acc[half][ct][i], u = acc[2 + half][ct][i];
+          hv[i] = dm_silu(gg) * u;
+          if (!finite_f(gg) || !finite_f(u) || !finite_f(hv[i])) {
+            const uint32_t ph = ut.shared ? kPhShared : kPhExpert;
+            const uint32_t kind = !finite_f(gg) ? kEkGate : !finite_f(u) ? kEkUp : kEkH;
+            record_err(g.status, err_key(ph, t, k, fr + i, kind));
           }
         }
+        uint2 h2, l2;
+        split4(hv, h2, l2);
+        const size_t o = (size_t)p * I + fr;
+        *reinterpret_cast<uint2*>((ut.shared ? g.hsh : g.hrh) + o) = h2;
+        *reinterpret_cast<uint2*>((ut.shared ? g.hsl : g.hrl) + o) = l2;
       }
     }
   }
-  // D: lane (q, j) holds features 16 rb + 4q + i of column j
+}
+
+// Down: tile tl holds output rows row0 + 16 tl + 4q + i of column j.
+template <int NC>
+__device__ __forceinline__ void down_epilogue(const GroupArgs& g, const UnitTokens& ut, int I,
+                                              int row0, int q, int j,
+                                              const f32x4 (&acc)[4][NC]) {
+  const int H = g.L.H, K = g.L.K;
 #pragma unroll
-  for (int ts = 0; ts < 4; ++ts) {
-    if (ts < nts && valid[ts]) {
-      const int c = 16 * ts + j;
+  for (int ct = 0; ct < NC; ++ct) {
+    const int c = 16 * ct + j;
+    if (c < ut.n) {
       const int p = ut.p0 + c;
-      const int a = ut.shared ? p : perm[p];
+      const int a = ut.shared ? p : g.perm[p];
       const int t = ut.shared ? p : a / K, k = ut.shared ? 0 : a % K;
-      float hv[4];
+      float* dst = ut.shared ? g.rs + (size_t)t * H : g.r + (size_t)a * H;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int row = rb * kTileRows + 4 * q + i;
-        const float g = ag[ts][i], u = au[ts][i];
-        hv[i] = dm_silu(g) * u;
-        if (!finite_f(g) || !finite_f(u) || !finite_f(hv[i])) {
-          const uint32_t ph = ut.shared ? kPhShared : kPhExpert;
-          const uint32_t kind = !finite_f(g) ? kEkGate : !finite_f(u) ? kEkUp : kEkH;
-          record_err(status, err_key(ph, t, k, row, kind));
+      for (int tl = 0; tl < 4; ++tl) {
+        const int d0 = row0 + 16 * tl + 4 * q;
+        float v[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          v[i] = acc[tl][ct][i];
+          if (!finite_f(v[i])) {
+            const uint32_t ph = ut.shared ? kPhShared : kPhExpert;
+            record_err(g.status, err_key(ph, t, k, I + d0 + i, kEkDown));
+          }
         }
+        *reinterpret_cast<float4*>(dst + d0) = make_float4(v[0], v[1], v[2], v[3]);
       }
-      float* dst = ut.shared ? hs + (size_t)t * I : hr + (size_t)p * I;
-      *reinterpret_cast<float4*>(dst + rb * kTileRows + 4 * q) = make_float4(hv[0], hv[1], hv[2], hv[3]);
     }
   }
 }
 
 // ---------------------------------------------------------------------------
-// Down: blockIdx.x = unit, blockIdx.y = block of 64 output rows.  B = h of the
-// unit's tokens split into bf16 hi / lo on the fly.  Output r [a][H]
-// (routed, a = assignment) or rs [t][H] (shared).
-__global__ __launch_bounds__(kGThreads) void k_down_grouped(
-    LayerDev L, const int32_t* __restrict__ off, const int32_t* __restrict__ perm,
-    const int2* __restrict__ units, const int32_t* __restrict__ meta, int T,
-    const float* __restrict__ hr, const float* __restrict__ hs, float* __restrict__ r,
-    float* __restrict__ rs, unsigned long long* status) {
-  if ((int)blockIdx.x >= meta[0]) return;
-  const UnitTokens ut = unit_tokens(units[blockIdx.x], off, L.E, T);
-  const int H = L.H, K = L.K;
-  const int I = ut.shared ? L.Ish : L.I;
-  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
-  const int q = lane >> 4, j = lane & 15;
-  const int rb = blockIdx.y * 4 + w;
-  if (rb * kTileRows >= H) return;
+// Big units.  A workgroup of 4 waves takes one unit (17..128 tokens) and
+// 128 features (gate/up: wave w owns features f0 = 128 blockIdx.y + 32 w ..
+// f0 + 31, i.e. gate tiles f0, f0 + 16 and the same up tiles) or 256 output
+// rows (down: wave w owns rows 256 blockIdx.y + 64 w .. + 63).  All 8 column
+// tiles are computed (columns past the unit's tokens are never stored).
+//
+// B staging: per k-step of 128 columns, the unit's 128 rows (row r clamped
+// to the last token) move global -> registers -> LDS: thread tid carries the
+// 16-byte segment tid & 15 of rows (tid >> 4) + 16 i.  Two LDS buffers: step
+// s computes from buffer s & 1 while the rows of step s + 1 are written to
+// the other and those of step s + 2 are in flight; one barrier per step.
+// Rows are padded to kBPitch elements so that the 16 rows of one MFMA operand
+// fetch (ds_read_b128 by lanes j = 0..15 at one q) fall on 16 distinct
+// 4-bank groups.  A: the chunks of step s + 2 are requested while step s
+// computes (kBigPre = 2, which also keeps the buffer index of each unrolled
+// step a constant).
+constexpr int kBPitch = kQuadCols + 8;
+constexpr int kBTile = kMT * kBPitch;  // elements per staged plane
+constexpr int kBigPre = 2;
+constexpr size_t kBigLds = 2 * 2 * kBTile * sizeof(uint16_t);  // 2 buffers x (hi, lo)
+
+__device__ __forceinline__ bf16x8 lds_b(const uint16_t* bs, int ct, int kk, int q, int j) {
+  return *reinterpret_cast<const bf16x8*>(bs + (ct * 16 + j) * kBPitch + kk * kGroup + 8 * q);
+}
+
+template <bool LO>
+__device__ __forceinline__ void rows_load(const uint16_t* __restrict__ sh,
+                                          const uint16_t* __restrict__ sl,
+                                          const int (&roff)[kNCT], int s, v4u (&bh)[kNCT],
+                                          v4u (&bl)[kNCT]) {
+#pragma unroll
+  for (int i = 0; i < kNCT; ++i) {
+    const uint32_t o = (uint32_t)roff[i] + (uint32_t)(s * kQuadCols);
+    bh[i] = *reinterpret_cast<const v4u*>(sh + o);
+    if (LO) bl[i] = *reinterpret_cast<const v4u*>(sl + o);
+  }
+}
+
+template <bool LO>
+__device__ __forceinline__ void rows_store(uint16_t* bs, int srow, int seg, const v4u (&bh)[kNCT],
+                                           const v4u (&bl)[kNCT]) {
+#pragma unroll
+  for (int i = 0; i < kNCT; ++i) {
+    const int o = (srow + 16 * i) * kBPitch + seg * 8;
+    *reinterpret_cast<v4u*>(bs + o) = bh[i];
+    if (LO) *reinterpret_cast<v4u*>(bs + kBTile + o) = bl[i];
+  }
+}
+
+// One k-step of a big unit: 4 k-groups x (4 A tiles x 8 column tiles).
+template <bool LO>
+__device__ __forceinline__ void big_step(const uint16_t* bs, const AChunks& a, int q, int j,
+                                         f32x4 (&acc)[4][kNCT]) {
+#pragma unroll
+  for (int kk = 0; kk < kGroupsPerQuad; ++kk) {
+    bf16x8 av[4];
+    dequant_a4(a, kk, av);
+#pragma unroll
+    for (int ct = 0; ct < kNCT; ++ct) {
+      const bf16x8 b = lds_b(bs, ct, kk, q, j);
+#pragma unroll
+      for (int tl = 0; tl < 4; ++tl) acc[tl][ct] = mfma16(av[tl], b, acc[tl][ct]);
+      if (LO) {
+        const bf16x8 b2 = lds_b(bs + kBTile, ct, kk, q, j);
+#pragma unroll
+        for (int tl = 0; tl < 4; ++tl) acc[tl][ct] = mfma16(av[tl], b2, acc[tl][ct]);
+      }
+    }
+  }
+}
+
+// The k-loop of a big unit over ns steps (A views, staged rows from sh/sl).
+template <bool LO>
+__device__ __forceinline__ void big_loop(uint16_t* lds, const ExpertView& v01,
+                                         const ExpertView& v23, int rb0, int rstep, bool active,
+                                         const uint16_t* sh, const uint16_t* sl,
+                                         const int (&roff)[kNCT], int ns, f32x4 (&acc)[4][kNCT]) {
+  const int tid = threadIdx.x, lane = tid & 63, q = lane >> 4, j = lane & 15;
+  const int seg = tid & 15, srow = tid >> 4;
+  constexpr int kBuf = 2 * kBTile;  // elements per buffer (hi, lo planes)
+  v4u bh[kNCT], bl[kNCT];
+  rows_load<LO>(sh, sl, roff, 0, bh, bl);
+  rows_store<LO>(lds, srow, seg, bh, bl);
+  rows_load<LO>(sh, sl, roff, min(1, ns - 1), bh, bl);
+  AChunks ring[kBigPre];
+  if (active) {
+#pragma unroll
+    for (int u = 0; u < kBigPre; ++u) load_a4(v01, v23, rb0, rstep, min(u, ns - 1), lane, ring[u]);
+  }
+#pragma unroll
+  for (int tl = 0; tl < 4; ++tl)
+#pragma unroll
+    for (int ct = 0; ct < kNCT; ++ct) acc[tl][ct] = f32x4{0, 0, 0, 0};
+  __syncthreads();
+  int s0 = 0;
+  for (; s0 + kBigPre < ns; s0 += kBigPre) {
+#pragma unroll
+    for (int u = 0; u < kBigPre; ++u) {
+      const int s = s0 + u;
+      rows_store<LO>(lds + ((u + 1) & 1) * kBuf, srow, seg, bh, bl);
+      rows_load<LO>(sh, sl, roff, min(s + 2, ns - 1), bh, bl);
+      if (active) {
+        big_step<LO>(lds + (u & 1) * kBuf, ring[u], q, j, acc);
+        load_a4(v01, v23, rb0, rstep, s + kBigPre, lane, ring[u]);
+      }
+      __syncthreads();
+    }
+  }
+  // the last 1..kBigPre steps: nothing left to request
+#pragma unroll
+  for (int u = 0; u < kBigPre; ++u) {
+    const int s = s0 + u;
+    if (s < ns) {
+      if (s + 1 < ns) rows_store<LO>(lds + ((u + 1) & 1) * kBuf, srow, seg, bh, bl);
+      if (active) big_step<LO>(lds + (u & 1) * kBuf, ring[u], q, j, acc);
+      __syncthreads();
+    }
+  }
+}
+
+__global__ __launch_bounds__(kGThreads) void k_gu_big(GroupArgs g) {
+  extern __shared__ __attribute__((aligned(16))) uint16_t glds[];
+  if ((int)blockIdx.x >= g.meta[1]) return;
+  const UnitTokens ut = unit_tokens(g.units[blockIdx.x], g.off, g.L.E, g.T);
+  const LayerDev& L = g.L;
+  const int H = L.H, K = L.K, I = ut.shared ? L.Ish : L.I;
+  if ((int)blockIdx.y * 128 >= I) return;  // uniform per workgroup
+  const int tid = threadIdx.x, w = gwave_id(), lane = tid & 63, q = lane >> 4, j = lane & 15;
+  const int f0 = blockIdx.y * 128 + 32 * w;
+  const bool active = f0 < I;  // uniform per wave
+  const int rb0 = active ? f0 / kTileRows : 0;
+  const size_t mat = (size_t)I * H;
+  const ExpertView gv = ut.shared ? ExpertView{L.sgu_nib, L.sgu_sc, I, H}
+                                  : ExpertView{L.gu_nib + (size_t)ut.e * mat,
+                                               L.gu_sc + (size_t)ut.e * 2 * (mat / kGroup), I, H};
+  const ExpertView uv = {gv.nib + mat / 2, gv.sc + mat / kGroup, I, H};
+  int roff[kNCT];
+  const int seg = tid & 15, srow = tid >> 4;
+#pragma unroll
+  for (int i = 0; i < kNCT; ++i) {
+    const int r = min(srow + 16 * i, ut.n - 1);
+    const int t = ut.shared ? ut.p0 + r : g.perm[ut.p0 + r] / K;
+    roff[i] = t * H + seg * 8;
+  }
+  f32x4 acc[4][kNCT];
+  const int ns = H / kQuadCols;
+  if (g.need_lo[0] != 0)
+    big_loop<true>(glds, gv, uv, rb0, 1, active, g.xhi, g.xlo, roff, ns, acc);
+  else
+    big_loop<false>(glds, gv, uv, rb0, 1, active, g.xhi, g.xlo, roff, ns, acc);
+  if (active) gu_epilogue<kNCT>(g, ut, I, f0, q, j, acc);
+}
+
+__global__ __launch_bounds__(kGThreads) void k_down_big(GroupArgs g) {
+  extern __shared__ __attribute__((aligned(16))) uint16_t glds[];
+  if ((int)blockIdx.x >= g.meta[1]) return;
+  const UnitTokens ut = unit_tokens(g.units[blockIdx.x], g.off, g.L.E, g.T);
+  const LayerDev& L = g.L;
+  const int H = L.H, I = ut.shared ? L.Ish : L.I;
+  const int tid = threadIdx.x, w = gwave_id(), lane = tid & 63, q = lane >> 4, j = lane & 15;
+  const int row0 = blockIdx.y * 256 + 64 * w;
+  const bool active = row0 < H;
+  const int rb0 = active ? row0 / kTileRows : 0;
   const size_t mat = (size_t)H * I;
   const ExpertView dv = ut.shared ? ExpertView{L.sd_nib, L.sd_sc, H, I}
                                   : ExpertView{L.d_nib + (size_t)ut.e * (mat / 2),
                                                L.d_sc + (size_t)ut.e * (mat / kGroup), H, I};
-  const float* hrow[4];
-  bool valid[4];
+  int roff[kNCT];
+  const int seg = tid & 15, srow = tid >> 4;
 #pragma unroll
-  for (int ts = 0; ts < 4; ++ts) {
-    const int c = 16 * ts + j;
-    valid[ts] = c < ut.n;
-    const int p = ut.p0 + (valid[ts] ? c : 0);
-    hrow[ts] = ut.shared ? hs + (size_t)p * I : hr + (size_t)p * I;
+  for (int i = 0; i < kNCT; ++i) roff[i] = (ut.p0 + min(srow + 16 * i, ut.n - 1)) * I + seg * 8;
+  f32x4 acc[4][kNCT];
+  big_loop<true>(glds, dv, dv, rb0, 1, active, ut.shared ? g.hsh : g.hrh,
+                 ut.shared ? g.hsl : g.hrl, roff, I / kQuadCols, acc);
+  if (active) down_epilogue<kNCT>(g, ut, I, row0, q, j, acc);
+}
+
+// ---------------------------------------------------------------------------
+// Small units (<= 16 tokens): one column tile.  Waves are independent (no
+// LDS, no barrier): each wave owns 4 A tiles as in the big kernels and reads
+// its B fragments (lane (q, j): token j, columns 8q..8q+7 of each group)
+// straight from memory into the same prefetch ring as the A chunks, P
+// k-steps ahead.
+template <bool LO>
+struct SmallStep {
+  AChunks a;
+  v4u b[kGroupsPerQuad];
+  v4u bl[LO ? kGroupsPerQuad : 1];
+};
+
+template <bool LO>
+__device__ __forceinline__ void small_load(const ExpertView& v01, const ExpertView& v23, int rb0,
+                                           int rstep, int s, int lane, const uint16_t* bh,
+                                           const uint16_t* bl, SmallStep<LO>& st) {
+  load_a4(v01, v23, rb0, rstep, s, lane, st.a);
+#pragma unroll
+  for (int kk = 0; kk < kGroupsPerQuad; ++kk) {
+    const int o = s * kQuadCols + kk * kGroup;
+    st.b[kk] = *reinterpret_cast<const v4u*>(bh + o);
+    if (LO) st.bl[kk] = *reinterpret_cast<const v4u*>(bl + o);
   }
-  f32x4 acc[4];
+}
+
+template <bool LO>
+__device__ __forceinline__ void small_step(const SmallStep<LO>& st, f32x4 (&acc)[4][1]) {
 #pragma unroll
-  for (int ts = 0; ts < 4; ++ts) acc[ts] = f32x4{0, 0, 0, 0};
-  const int nGQ = I / kQuadCols;
-  const int nts = (ut.n + 15) / 16;
-  for (int gq = 0; gq < nGQ; ++gq) {
-    uint4 wd;
-    uint2 sd;
-    load_chunk_nt(dv, rb, gq, lane, wd, sd);
+  for (int kk = 0; kk < kGroupsPerQuad; ++kk) {
+    bf16x8 av[4];
+    dequant_a4(st.a, kk, av);
+    const bf16x8 b = __builtin_bit_cast(bf16x8, st.b[kk]);
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const bf16x8 a = dequant8(word_of(wd, c), scale_of(sd, c));
-      const int k0 = gq * kQuadCols + c * kGroup + 8 * q;
+    for (int tl = 0; tl < 4; ++tl) acc[tl][0] = mfma16(av[tl], b, acc[tl][0]);
+    if (LO) {
+      const bf16x8 b2 = __builtin_bit_cast(bf16x8, st.bl[kk]);
 #pragma unroll
-      for (int ts = 0; ts < 4; ++ts) {
-        if (ts < nts) {
-          const float4 u0 = *reinterpret_cast<const float4*>(hrow[ts] + k0);
-          const float4 u1 = *reinterpret_cast<const float4*>(hrow[ts] + k0 + 4);
-          float f[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
-          if (!valid[ts])
-#pragma unroll
-            for (int z = 0; z < 8; ++z) f[z] = 0.0f;
-          uint4 bh, bl;
-          split8(f, bh, bl);
-          acc[ts] = mfma16(a, __builtin_bit_cast(bf16x8, bh), acc[ts]);
-          acc[ts] = mfma16(a, __builtin_bit_cast(bf16x8, bl), acc[ts]);
-        }
-      }
-    }
-  }
-#pragma unroll
-  for (int ts = 0; ts < 4; ++ts) {
-    if (ts < nts && valid[ts]) {
-      const int c = 16 * ts + j;
-      const int p = ut.p0 + c;
-      const int a = ut.shared ? p : perm[p];
-      const int t = ut.shared ? p : a / K, k = ut.shared ? 0 : a % K;
-      float v[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        v[i] = acc[ts][i];
-        if (!finite_f(v[i])) {
-          const uint32_t ph = ut.shared ? kPhShared : kPhExpert;
-          record_err(status, err_key(ph, t, k, I + rb * kTileRows + 4 * q + i, kEkDown));
-        }
-      }
-      float* dst = ut.shared ? rs + (size_t)t * H : r + (size_t)a * H;
-      *reinterpret_cast<float4*>(dst + rb * kTileRows + 4 * q) = make_float4(v[0], v[1], v[2], v[3]);
+      for (int tl = 0; tl < 4; ++tl) acc[tl][0] = mfma16(av[tl], b2, acc[tl][0]);
     }
   }
 }
 
+// bh / bl point at this lane's B row (+ 8q) at column 0.
+template <bool LO, int P>
+__device__ __forceinline__ void small_loop(const ExpertView& v01, const ExpertView& v23, int rb0,
+                                           int rstep, const uint16_t* bh, const uint16_t* bl,
+                                           int ns, f32x4 (&acc)[4][1]) {
+  const int lane = threadIdx.x & 63;
+  SmallStep<LO> ring[P];
+#pragma unroll
+  for (int u = 0; u < P; ++u) small_load<LO>(v01, v23, rb0, rstep, min(u, ns - 1), lane, bh, bl, ring[u]);
+#pragma unroll
+  for (int tl = 0; tl < 4; ++tl) acc[tl][0] = f32x4{0, 0, 0, 0};
+  int s0 = 0;
+  for (; s0 + P < ns; s0 += P) {
+#pragma unroll
+    for (int u = 0; u < P; ++u) {
+      small_step<LO>(ring[u], acc);
+      small_load<LO>(v01, v23, rb0, rstep, min(s0 + u + P, ns - 1), lane, bh, bl, ring[u]);
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < P; ++u)
+    if (s0 + u < ns) small_step<LO>(ring[u], acc);
+}
+
+__global__ __launch_bounds__(kGThreads) void k_gu_small(GroupArgs g) {
+  const int ui = g.meta[1] + blockIdx.x;
+  if (ui >= g.meta[0]) return;
+  const UnitTokens ut = unit_tokens(g.units[ui], g.off, g.L.E, g.T);
+  const LayerDev& L = g.L;
+  const int H = L.H, K = L.K, I = ut.shared ? L.Ish : L.I;
+  const int w = gwave_id(), lane = threadIdx.x & 63, q = lane >> 4, j = lane & 15;
+  const int f0 = blockIdx.y * 128 + 32 * w;
+  if (f0 >= I) return;  // uniform per wave; no barriers in this kernel
+  const size_t mat = (size_t)I * H;
+  const ExpertView gv = ut.shared ? ExpertView{L.sgu_nib, L.sgu_sc, I, H}
+                                  : ExpertView{L.gu_nib + (size_t)ut.e * mat,
+                                               L.gu_sc + (size_t)ut.e * 2 * (mat / kGroup), I, H};
+  const ExpertView uv = {gv.nib + mat / 2, gv.sc + mat / kGroup, I, H};
+  const int r = min(j, ut.n - 1);
+  const int t = ut.shared ? ut.p0 + r : g.perm[ut.p0 + r] / K;
+  const size_t o = (size_t)t * H + 8 * q;
+  f32x4 acc[4][1];
+  const int ns = H / kQuadCols;
+  if (g.need_lo[0] != 0)
+    small_loop<true, 2>(gv, uv, f0 / kTileRows, 1, g.xhi + o, g.xlo + o, ns, acc);
+  else
+    small_loop<false, 4>(gv, uv, f0 / kTileRows, 1, g.xhi + o, g.xlo + o, ns, acc);
+  gu_epilogue<1>(g, ut, I, f0, q, j, acc);
+}
+
+__global__ __launch_bounds__(kGThreads) void k_down_small(GroupArgs g) {
+  const int ui = g.meta[1] + blockIdx.x;
+  if (ui >= g.meta[0]) return;
+  const UnitTokens ut = unit_tokens(g.units[ui], g.off, g.L.E, g.T);
+  const LayerDev& L = g.L;
+  const int H = L.H, I = ut.shared ? L.Ish : L.I;
+  const int w = gwave_id(), lane = threadIdx.x & 63, q = lane >> 4, j = lane & 15;
+  const int row0 = blockIdx.y * 256 + 64 * w;
+  if (row0 >= H) return;
+  const size_t mat = (size_t)H * I;
+  const ExpertView dv = ut.shared ? ExpertView{L.sd_nib, L.sd_sc, H, I}
+                                  : ExpertView{L.d_nib + (size_t)ut.e * (mat / 2),
+                                               L.d_sc + (size_t)ut.e * (mat / kGroup), H, I};
+  const size_t o = (size_t)(ut.p0 + min(j, ut.n - 1)) * I + 8 * q;
+  f32x4 acc[4][1];
+  small_loop<true, 2>(dv, dv, row0 / kTileRows, 1, (ut.shared ? g.hsh : g.hrh) + o,
+                      (ut.shared ? g.hsl : g.hrl) + o, I / kQuadCols, acc);
+  down_epilogue<1>(g, ut, I, row0, q, j, acc);
+}
+
 hipError_t launch_experts_grouped(const LayerDev& L, const uint16_t* xhi, const uint16_t* xlo,
                                   const int* need_lo, const int32_t* off, const int32_t* perm,
-                                  const int2* units, const int32_t* meta, int T, float* hr,
-                                  float* hs, float* r, float* rs, unsigned long long* status,
-                                  hipStream_t st) {
+                                  const int2* units, const int32_t* meta, int T, uint16_t* hrh,
+                                  uint16_t* hrl, uint16_t* hsh, uint16_t* hsl, float* r,
+                                  float* rs, unsigned long long* status, hipStream_t st) {
+  const GroupArgs g = {L, xhi, xlo, need_lo, off, perm, units, meta, T,
+                       hrh, hrl, hsh, hsl, r, rs, status};
   const int nu = group_units_max(T, L.K, L.E);
   const int imax = L.I > L.Ish ? L.I : L.Ish;
-  hipLaunchKernelGGL(k_gu_grouped, dim3(nu, (imax + 63) / 64), dim3(kGThreads), 0, st, L, xhi,
-                     xlo, need_lo, off, perm, units, meta, T, hr, hs, status);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(k_down_grouped, dim3(nu, (L.H + 63) / 64), dim3(kGThreads), 0, st, L, off,
-                     perm, units, meta, T, hr, hs, r, rs, status);
+  const dim3 gu_grid(nu, (imax + 127) / 128), dn_grid(nu, (L.H + 255) / 256);
+  hipLaunchKernelGGL(k_gu_big, gu_grid, dim3(kGThreads), kBigLds, st, g);
+  hipLaunchKernelGGL(k_gu_small, gu_grid, dim3(kGThreads), 0, st, g);
+  hipLaunchKernelGGL(k_down_big, dn_grid, dim3(kGThreads), kBigLds, st, g);
+  hipLaunchKernelGGL(k_down_small, dn_grid, dim3(kGThreads), 0, st, g);
   return hipGetLastError();
 }
 

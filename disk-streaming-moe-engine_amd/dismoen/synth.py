@@ -107,10 +107,35 @@ def zipf_router_bias(num_experts: int, s: float = 1.1, seed: int = 0) -> np.ndar
     return (-s * np.log(ranks)).astype(np.float32)
 
 
+def with_router_bias(L: MoELayerQ4, bias: np.ndarray) -> MoELayerQ4:
+    """A copy of L whose router carries a per-expert logit bias in input
+    column 0: W_r[e, 0] = bf16(bias[e]).  With activations whose feature 0 is
+    1.0 (bias_feature) the router logit is z_e = bias_e + sum_{h>0} x_h W_r[e, h],
+    i.e. a biased router expressed in the reference's unbiased router
+    (src/layers/router.mojo:15-106 has no bias term)."""
+    import dataclasses
+    H, E = L.hidden, L.num_experts
+    r = L.router_bf16.reshape(E, H).copy()
+    r[:, 0] = f32_to_bf16_bits(np.asarray(bias, np.float32))
+    return dataclasses.replace(L, router_bf16=r.reshape(-1))
+
+
+def bias_feature(x: np.ndarray) -> np.ndarray:
+    """Activations with feature 0 set to 1.0, the input of a router bias
+    folded in by with_router_bias."""
+    x = np.array(x, dtype=np.float32, copy=True)
+    x[..., 0] = 1.0
+    return x
+
+
+def expert_bytes(H, I, G=32) -> int:
+    """4-bit codes plus fp16 group scales of one expert's gate, up and down."""
+    n = 3 * I * H
+    return n // 2 + 2 * n // G
+
+
 def algorithmic_bytes_per_token(H, E, K, I, Ish, G=32, x_bytes=4, y_bytes=4) -> int:
     """Bytes one decode token must move: K routed + 1 shared expert in 4 bits
     with fp16 group scales, the bf16 router and shared gate, x in, y out."""
-    def expert(i):
-        n = 3 * i * H
-        return n // 2 + 2 * n // G
-    return K * expert(I) + expert(Ish) + 2 * E * H + 2 * H + x_bytes * H + y_bytes * H
+    return (K * expert_bytes(H, I, G) + expert_bytes(H, Ish, G) + 2 * E * H + 2 * H
+            + x_bytes * H + y_bytes * H)
