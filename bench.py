@@ -289,10 +289,13 @@ def main():
     else:  # stack
         cfg = synth.CONFIG_QWEN36
         nl = a.layers
+        dims = (cfg["hidden"], cfg["num_experts"], cfg["top_k"], cfg["inter"], cfg["inter_sh"])
         for l in range(nl):
-            L = synth.make_layer(**cfg, seed=a.seed * 1000 + l)
-            blk.upload_layer(l, L)
-            del L
+            W = synth.make_layer_device(**cfg, seed=a.seed * 1000 + l, device=dev)
+            torch.cuda.synchronize()  # drawn on torch's stream, read on the library's
+            blk.upload_layer_device(l, dims, {k: v.data_ptr() for k, v in W.items()})
+            blk.sync()
+            del W
         H, K = cfg["hidden"], cfg["top_k"]
         ntok = a.warmup + a.steps
         x_host = synth.make_activations(np.random.default_rng(a.seed + 7), (ntok, H))

@@ -194,6 +194,10 @@ void free_layer(Layer* Ly) {
   delete Ly;
 }
 
+// Token counts from which the router runs on the matrix cores (bf16
+// activations); below it the lane-chain router is as fast.
+constexpr int kMfmaRouterMinTokens = 64;
+
 hipError_t run_block(dmh_ctx* ctx, Layer* Ly, int layer, const float* dx, const float* dres,
                      int T, float* dy, int32_t* dids, float* dprobs, float* dshg,
                      bool allow_fused = true) {
@@ -217,17 +221,13 @@ hipError_t run_block(dmh_ctx* ctx, Layer* Ly, int layer, const float* dx, const 
   }
   if ((e = ctx->z.ensure((size_t)T * (L.E + 1))) != hipSuccess) return e;
   if ((e = ctx->h.ensure((size_t)(L.K + 1) * ldh)) != hipSuccess) return e;
-  if ((e = dm::launch_router_dec(L, dx, T, ctx->z.p, status, st)) != hipSuccess) return e;
-  if ((e = dm::launch_router_select(ctx->z.p, L.E + 1, T, L.E, L.K, 1, dids, dprobs, dshg, status,
-                                    st)) != hipSuccess)
-    return e;
   if (T > 1) {
-    // several tokens: group the assignments by expert and run each expert's
-    // tokens together as a grouped GEMM
+    // several tokens: route, group the assignments by expert and run each
+    // expert's tokens together as a grouped GEMM
     const size_t TK = (size_t)T * L.K, TH = (size_t)T * L.H;
     if ((e = ctx->g_off.ensure(L.E + 1)) != hipSuccess) return e;
     if ((e = ctx->g_perm.ensure(TK)) != hipSuccess) return e;
-    if ((e = ctx->g_meta.ensure(1)) != hipSuccess) return e;
+    if ((e = ctx->g_meta.ensure(2)) != hipSuccess) return e;
     if ((e = ctx->g_needlo.ensure(1)) != hipSuccess) return e;
     if ((e = ctx->g_units.ensure(dm::group_units_max(T, L.K, L.E))) != hipSuccess) return e;
     if ((e = ctx->g_xhi.ensure(TH)) != hipSuccess) return e;
@@ -236,12 +236,26 @@ hipError_t run_block(dmh_ctx* ctx, Layer* Ly, int layer, const float* dx, const 
     if ((e = ctx->g_hs.ensure(2 * (size_t)T * L.Ish)) != hipSuccess) return e;
     if ((e = ctx->g_r.ensure(TK * L.H)) != hipSuccess) return e;
     if ((e = ctx->g_rs.ensure(TH)) != hipSuccess) return e;
-    if ((e = dm::launch_group_build(dids, T, L.K, L.E, ctx->g_off.p, ctx->g_perm.p,
-                                    ctx->g_units.p, ctx->g_meta.p, st)) != hipSuccess)
-      return e;
     if ((e = hipMemsetAsync(ctx->g_needlo.p, 0, sizeof(int), st)) != hipSuccess) return e;
     if ((e = dm::launch_split_rows(dx, (int64_t)TH, ctx->g_xhi.p, ctx->g_xlo.p, ctx->g_needlo.p,
                                    st)) != hipSuccess)
+      return e;
+    if (T >= kMfmaRouterMinTokens) {
+      // bf16 activations: matrix-core router; otherwise the lane-chain router
+      if ((e = dm::launch_router_mfma(L, ctx->g_xhi.p, ctx->g_needlo.p, T, ctx->z.p, st)) !=
+          hipSuccess)
+        return e;
+      if ((e = dm::launch_router_dec(L, dx, T, ctx->z.p, status, st, ctx->g_needlo.p)) !=
+          hipSuccess)
+        return e;
+    } else if ((e = dm::launch_router_dec(L, dx, T, ctx->z.p, status, st)) != hipSuccess) {
+      return e;
+    }
+    if ((e = dm::launch_router_select(ctx->z.p, L.E + 1, T, L.E, L.K, 1, dids, dprobs, dshg,
+                                      status, st)) != hipSuccess)
+      return e;
+    if ((e = dm::launch_group_build(dids, T, L.K, L.E, ctx->g_off.p, ctx->g_perm.p,
+                                    ctx->g_units.p, ctx->g_meta.p, st)) != hipSuccess)
       return e;
     if ((e = dm::launch_experts_grouped(L, ctx->g_xhi.p, ctx->g_xlo.p, ctx->g_needlo.p,
                                         ctx->g_off.p, ctx->g_perm.p, ctx->g_units.p,
@@ -252,6 +266,10 @@ hipError_t run_block(dmh_ctx* ctx, Layer* Ly, int layer, const float* dx, const 
     return dm::launch_combine(ctx->g_r.p, ctx->g_rs.p, dprobs, dshg, dres, T, L.H, L.K, dy, status,
                               st);
   }
+  if ((e = dm::launch_router_dec(L, dx, T, ctx->z.p, status, st)) != hipSuccess) return e;
+  if ((e = dm::launch_router_select(ctx->z.p, L.E + 1, T, L.E, L.K, 1, dids, dprobs, dshg, status,
+                                    st)) != hipSuccess)
+    return e;
   for (int t = 0; t < T; ++t) {
     const float* xt = dx + (size_t)t * L.H;
     if ((e = dm::launch_gateup_dec(L, xt, dids + (size_t)t * L.K, ctx->h.p, ldh, t, status, st)) !=

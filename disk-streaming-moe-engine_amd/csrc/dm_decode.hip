@@ -264,30 +264,6 @@ __device__ __forceinline__ void select_keys(const uint32_t (&key)[NK], int round
   }
 }
 
-// The softmax normaliser, summed sequentially in expert order
-// (src/layers/router.mojo:160-170), read from LDS in batches of 64 values.
-__device__ __forceinline__ float seq_sum(const float* v, int n) {
-  float s = 0.0f;
-  const float4* v4 = reinterpret_cast<const float4*>(v);
-  const int n4 = n >> 2;
-  for (int b0 = 0; b0 < n4; b0 += 16) {
-    float4 t[16];
-#pragma unroll
-    for (int u = 0; u < 16; ++u) t[u] = b0 + u < n4 ? v4[b0 + u] : make_float4(0, 0, 0, 0);
-#pragma unroll
-    for (int u = 0; u < 16; ++u) {
-      if (b0 + u < n4) {
-        s = s + t[u].x;
-        s = s + t[u].y;
-        s = s + t[u].z;
-        s = s + t[u].w;
-      }
-    }
-  }
-  for (int e = n4 * 4; e < n; ++e) s = s + v[e];
-  return s;
-}
-
 template <int R>
 __device__ __forceinline__ void issue_logits(const uint64_t* zt, int E, bool gate,
                                              uint64_t (&v)[4 * R + 1]) {

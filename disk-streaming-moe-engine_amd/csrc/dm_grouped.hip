@@ -7,7 +7,8 @@
 // src/layers/swiglu.mojo:52-230, then the shared expert for all tokens, then
 // the combine of src/layers/moe.mojo:105-177.  Here:
 //
-//   k_router_dec / k_router_select (dm_kernels.hip)  logits, softmax, top-k
+//   k_router_mfma / k_router_dec, k_router_select (dm_kernels.hip)  logits
+//                   (matrix cores for bf16 activations), softmax, top-k
 //   k_group_build   one workgroup: count assignments per expert, scan,
 //                   scatter them into expert order, emit the work units
 //                   (expert, tile of up to 128 tokens); the shared expert is
@@ -41,17 +42,26 @@ constexpr int kGThreads = 256;
 // ---------------------------------------------------------------------------
 // One workgroup of 1024 threads.  ids [T*K] in the reference order (slot k of
 // token t at t*K + k).  Outputs: off [E+1] expert offsets into perm, perm
-// [T*K] assignment indices grouped by expert, units [nmax] (expert, tile),
-// meta[0] = number of units, meta[1] = number of big units.  Order: full
-// routed tiles, full shared tiles, partial big routed tiles, a partial big
-// shared tile, then the small routed tiles and a small shared tile, so that
-// the costly workgroups start first.
+// [T*K] assignment indices grouped by expert, units [nmax] = (expert, first
+// position within the expert), meta[0] = number of units, meta[1] = number of
+// big units.  An expert's c tokens form c / 128 full big units; a remainder
+// r > 32 is one more big unit, a remainder r <= 32 becomes ceil(r / 16) small
+// units.  Order: full routed units, full shared units, partial big routed
+// units, a partial big shared unit, then the small routed and shared units,
+// so that the costly workgroups start first.
+__device__ __forceinline__ void unit_split(int c, int& nf, int& pb, int& ps) {
+  const int r = c % kMT;
+  nf = c / kMT;
+  pb = r > 2 * kSmallMax;
+  ps = (r > 0 && r <= 2 * kSmallMax) ? (r + kSmallMax - 1) / kSmallMax : 0;
+}
+
 __global__ __launch_bounds__(1024) void k_group_build(const int32_t* __restrict__ ids, int T, int K,
                                                       int E, int32_t* __restrict__ off,
                                                       int32_t* __restrict__ perm,
                                                       int2* __restrict__ units,
                                                       int32_t* __restrict__ meta) {
-  // cnt[E] | cur[E] | 4 scans of 1024: counts, full tiles, partial big, small
+  // cnt[E] | cur[E] | 4 scans of 1024: counts, full units, partial big, small
   extern __shared__ int lds[];
   int* cnt = lds;
   int* cur = lds + E;
@@ -68,11 +78,12 @@ __global__ __launch_bounds__(1024) void k_group_build(const int32_t* __restrict_
   const int per = (E + 1023) / 1024, e0 = min(tid * per, E), e1 = min(e0 + per, E);
   int v[4] = {0, 0, 0, 0};
   for (int e = e0; e < e1; ++e) {
-    const int c = cnt[e], r = c % kMT;
-    v[0] += c;
-    v[1] += c / kMT;
-    v[2] += r > kSmallMax;
-    v[3] += r > 0 && r <= kSmallMax;
+    int nf, pb, ps;
+    unit_split(cnt[e], nf, pb, ps);
+    v[0] += cnt[e];
+    v[1] += nf;
+    v[2] += pb;
+    v[3] += ps;
   }
 #pragma unroll
   for (int i = 0; i < 4; ++i) sc[i * 1024 + tid] = v[i];
@@ -87,19 +98,20 @@ __global__ __launch_bounds__(1024) void k_group_build(const int32_t* __restrict_
     __syncthreads();
   }
   const int nf = sc[1024 + 1023], npb = sc[2048 + 1023], nps = sc[3072 + 1023];
-  const int sf = T / kMT, sr = T % kMT;
-  const int spb = sr > kSmallMax, sps = sr > 0 && sr <= kSmallMax;
-  const int pb0 = nf + sf, s0 = pb0 + npb + spb;
+  int snf, spb, sps;
+  unit_split(T, snf, spb, sps);
+  const int pb0 = nf + snf, s0 = pb0 + npb + spb;
   int base = sc[tid] - v[0], fb = sc[1024 + tid] - v[1], pb = pb0 + sc[2048 + tid] - v[2],
       ps = s0 + sc[3072 + tid] - v[3];
   for (int e = e0; e < e1; ++e) {
-    const int c = cnt[e], nfe = c / kMT, r = c % kMT;
+    int nfe, pbe, pse;
+    unit_split(cnt[e], nfe, pbe, pse);
     off[e] = base;
     cur[e] = base;
-    for (int tc = 0; tc < nfe; ++tc) units[fb + tc] = make_int2(e, tc);
-    if (r > kSmallMax) units[pb++] = make_int2(e, nfe);
-    else if (r > 0) units[ps++] = make_int2(e, nfe);
-    base += c;
+    for (int i = 0; i < nfe; ++i) units[fb + i] = make_int2(e, kMT * i);
+    if (pbe) units[pb++] = make_int2(e, kMT * nfe);
+    for (int i = 0; i < pse; ++i) units[ps++] = make_int2(e, kMT * nfe + kSmallMax * i);
+    base += cnt[e];
     fb += nfe;
   }
   if (tid == 0) off[E] = TK;
@@ -108,10 +120,10 @@ __global__ __launch_bounds__(1024) void k_group_build(const int32_t* __restrict_
     const int e = min(max((int)ids[a], 0), E - 1);
     perm[atomicAdd(&cur[e], 1)] = a;
   }
-  for (int tc = tid; tc < sf; tc += 1024) units[nf + tc] = make_int2(E, tc);
+  for (int i = tid; i < snf; i += 1024) units[nf + i] = make_int2(E, kMT * i);
   if (tid == 0) {
-    if (spb) units[pb0 + npb] = make_int2(E, sf);
-    if (sps) units[s0 + nps] = make_int2(E, sf);
+    if (spb) units[pb0 + npb] = make_int2(E, kMT * snf);
+    for (int i = 0; i < sps; ++i) units[s0 + nps + i] = make_int2(E, kMT * snf + kSmallMax * i);
     meta[0] = s0 + nps + sps;
     meta[1] = s0;
   }
@@ -126,7 +138,8 @@ hipError_t launch_group_build(const int32_t* ids, int T, int K, int E, int32_t* 
 }
 
 int group_units_max(int T, int K, int E) {
-  return E + (T * K + kMT - 1) / kMT + (T + kMT - 1) / kMT;
+  // per expert at most c / 128 + 2 units (two small units of a remainder <= 32)
+  return 2 * E + (T * K + kMT - 1) / kMT + (T + kMT - 1) / kMT + 2;
 }
 
 // ---------------------------------------------------------------------------
@@ -158,23 +171,25 @@ hipError_t launch_split_rows(const float* x, int64_t n, uint16_t* hi, uint16_t* 
 }
 
 // ---------------------------------------------------------------------------
-// Token rows of a unit: row r of tile (e, tc) is position p = off[e] + kMT tc
-// + r of the expert order, i.e. assignment a = perm[p] of token a / K; for the
-// shared expert (e == E) row r is token kMT tc + r itself.
+// Token rows of a unit (e, start): row r is position p = off[e] + start + r
+// of the expert order, i.e. assignment a = perm[p] of token a / K; for the
+// shared expert (e == E) row r is token start + r itself.  Big units hold up
+// to kMT rows, small units up to kSmallMax.
 struct UnitTokens {
   int e, p0, n;   // expert, first position, tokens in this unit
   bool shared;
 };
-__device__ __forceinline__ UnitTokens unit_tokens(int2 u, const int32_t* off, int E, int T) {
+__device__ __forceinline__ UnitTokens unit_tokens(int2 u, const int32_t* off, int E, int T,
+                                                  int size) {
   UnitTokens r;
   r.e = u.x;
   r.shared = u.x >= E;
   if (r.shared) {
-    r.p0 = kMT * u.y;
-    r.n = min(kMT, T - r.p0);
+    r.p0 = u.y;
+    r.n = min(size, T - r.p0);
   } else {
-    r.p0 = off[u.x] + kMT * u.y;
-    r.n = min(kMT, off[u.x + 1] - r.p0);
+    r.p0 = off[u.x] + u.y;
+    r.n = min(size, off[u.x + 1] - r.p0);
   }
   return r;
 }
@@ -202,25 +217,31 @@ __device__ __forceinline__ int gwave_id() { return __builtin_amdgcn_readfirstlan
 
 typedef uint32_t v4u __attribute__((ext_vector_type(4)));
 
-// The four A chunks (16 rows x 128 columns, 4-bit + scales) of one k-step.
+// The A chunks (16 rows x 128 columns, 4-bit + scales) of NT tiles for one
+// k-step.  Gate/up (GU): tiles 0..NT/2-1 are gate tiles rb0 + t, tiles
+// NT/2.. the up tiles at the same rows; down: tiles rb0 + t of one matrix.
+template <int NT>
 struct AChunks {
-  uint4 w[4];
-  uint2 s[4];
+  uint4 w[NT];
+  uint2 s[NT];
 };
 
-__device__ __forceinline__ void load_a4(const ExpertView& v01, const ExpertView& v23, int rb0,
-                                        int rstep, int s, int lane, AChunks& a) {
-  // tiles 0, 1 of view v01 at rb0, rb0 + rstep; tiles 2, 3 of v23 likewise
-  // (gate/up: rstep 1 within each matrix; down: one view, rows rb0 + tl)
-  load_chunk_nt(v01, rb0, s, lane, a.w[0], a.s[0]);
-  load_chunk_nt(v01, rb0 + rstep, s, lane, a.w[1], a.s[1]);
-  load_chunk_nt(v23, rb0 + (v01.nib == v23.nib ? 2 * rstep : 0), s, lane, a.w[2], a.s[2]);
-  load_chunk_nt(v23, rb0 + (v01.nib == v23.nib ? 3 * rstep : rstep), s, lane, a.w[3], a.s[3]);
+template <int NT, bool GU>
+__device__ __forceinline__ void load_a(const ExpertView& v0, const ExpertView& v1, int rb0, int s,
+                                       int lane, AChunks<NT>& a) {
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    if (GU)
+      load_chunk_nt(t < NT / 2 ? v0 : v1, rb0 + (t % (NT / 2)), s, lane, a.w[t], a.s[t]);
+    else
+      load_chunk_nt(v0, rb0 + t, s, lane, a.w[t], a.s[t]);
+  }
 }
 
-__device__ __forceinline__ void dequant_a4(const AChunks& a, int kk, bf16x8 (&av)[4]) {
+template <int NT>
+__device__ __forceinline__ void dequant_a(const AChunks<NT>& a, int kk, bf16x8 (&av)[NT]) {
 #pragma unroll
-  for (int tl = 0; tl < 4; ++tl) av[tl] = dequant8(word_of(a.w[tl], kk), scale_of(a.s[tl], kk));
+  for (int tl = 0; tl < NT; ++tl) av[tl] = dequant8(word_of(a.w[tl], kk), scale_of(a.s[tl], kk));
 }
 
 __device__ __forceinline__ void split4(const float* v, uint2& hi, uint2& lo) {
@@ -236,12 +257,12 @@ __device__ __forceinline__ void split4(const float* v, uint2& hi, uint2& lo) {
 }
 
 // ---- epilogues -------------------------------------------------------------
-// Gate/up: tiles 0/1 are gate features f0 + 16 half + 4q + i, tiles 2/3 the
-// up features; h = SiLU(g) * u with the reference's checks
+// Gate/up: tile t < NT/2 holds gate features f0 + 16 t + 4q + i, tile
+// NT/2 + t the same up features; h = SiLU(g) * u with the reference's checks
 // (src/layers/swiglu.mojo:191-201), stored as bf16 hi / lo.
-template <int NC>
+template <int NT, int NC>
 __device__ __forceinline__ void gu_epilogue(const GroupArgs& g, const UnitTokens& ut, int I,
-                                            int f0, int q, int j, const f32x4 (&acc)[4][NC]) {
+                                            int f0, int q, int j, const f32x4 (&acc)[NT][NC]) {
   const int K = g.L.K;
 #pragma unroll
   for (int ct = 0; ct < NC; ++ct) {
@@ -251,12 +272,12 @@ __device__ __forceinline__ void gu_epilogue(const GroupArgs& g, const UnitTokens
       const int a = ut.shared ? p : g.perm[p];
       const int t = ut.shared ? p : a / K, k = ut.shared ? 0 : a % K;
 #pragma unroll
-      for (int half = 0; half < 2; ++half) {
+      for (int half = 0; half < NT / 2; ++half) {
         const int fr = f0 + 16 * half + 4 * q;
         float hv[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const float gg = acc[half][ct][i], u = acc[2 + half][ct][i];
+          const float gg = acc[half][ct][i], u = acc[NT / 2 + half][ct][i];
           hv[i] = dm_silu(gg) * u;
           if (!finite_f(gg) || !finite_f(u) || !finite_f(hv[i])) {
             const uint32_t ph = ut.shared ? kPhShared : kPhExpert;
@@ -275,10 +296,10 @@ __device__ __forceinline__ void gu_epilogue(const GroupArgs& g, const UnitTokens
 }
 
 // Down: tile tl holds output rows row0 + 16 tl + 4q + i of column j.
-template <int NC>
+template <int NT, int NC>
 __device__ __forceinline__ void down_epilogue(const GroupArgs& g, const UnitTokens& ut, int I,
                                               int row0, int q, int j,
-                                              const f32x4 (&acc)[4][NC]) {
+                                              const f32x4 (&acc)[NT][NC]) {
   const int H = g.L.H, K = g.L.K;
 #pragma unroll
   for (int ct = 0; ct < NC; ++ct) {
@@ -289,7 +310,7 @@ __device__ __forceinline__ void down_epilogue(const GroupArgs& g, const UnitToke
       const int t = ut.shared ? p : a / K, k = ut.shared ? 0 : a % K;
       float* dst = ut.shared ? g.rs + (size_t)t * H : g.r + (size_t)a * H;
 #pragma unroll
-      for (int tl = 0; tl < 4; ++tl) {
+      for (int tl = 0; tl < NT; ++tl) {
         const int d0 = row0 + 16 * tl + 4 * q;
         float v[4];
 #pragma unroll
@@ -358,12 +379,12 @@ __device__ __forceinline__ void rows_store(uint16_t* bs, int srow, int seg, cons
 
 // One k-step of a big unit: 4 k-groups x (4 A tiles x 8 column tiles).
 template <bool LO>
-__device__ __forceinline__ void big_step(const uint16_t* bs, const AChunks& a, int q, int j,
+__device__ __forceinline__ void big_step(const uint16_t* bs, const AChunks<4>& a, int q, int j,
                                          f32x4 (&acc)[4][kNCT]) {
 #pragma unroll
   for (int kk = 0; kk < kGroupsPerQuad; ++kk) {
     bf16x8 av[4];
-    dequant_a4(a, kk, av);
+    dequant_a<4>(a, kk, av);
 #pragma unroll
     for (int ct = 0; ct < kNCT; ++ct) {
       const bf16x8 b = lds_b(bs, ct, kk, q, j);
@@ -379,9 +400,9 @@ __device__ __forceinline__ void big_step(const uint16_t* bs, const AChunks& a, i
 }
 
 // The k-loop of a big unit over ns steps (A views, staged rows from sh/sl).
-template <bool LO>
-__device__ __forceinline__ void big_loop(uint16_t* lds, const ExpertView& v01,
-                                         const ExpertView& v23, int rb0, int rstep, bool active,
+template <bool LO, bool GU>
+__device__ __forceinline__ void big_loop(uint16_t* lds, const ExpertView& v0,
+                                         const ExpertView& v1, int rb0, bool active,
                                          const uint16_t* sh, const uint16_t* sl,
                                          const int (&roff)[kNCT], int ns, f32x4 (&acc)[4][kNCT]) {
   const int tid = threadIdx.x, lane = tid & 63, q = lane >> 4, j = lane & 15;
@@ -391,10 +412,10 @@ __device__ __forceinline__ void big_loop(uint16_t* lds, const ExpertView& v01,
   rows_load<LO>(sh, sl, roff, 0, bh, bl);
   rows_store<LO>(lds, srow, seg, bh, bl);
   rows_load<LO>(sh, sl, roff, min(1, ns - 1), bh, bl);
-  AChunks ring[kBigPre];
+  AChunks<4> ring[kBigPre];
   if (active) {
 #pragma unroll
-    for (int u = 0; u < kBigPre; ++u) load_a4(v01, v23, rb0, rstep, min(u, ns - 1), lane, ring[u]);
+    for (int u = 0; u < kBigPre; ++u) load_a<4, GU>(v0, v1, rb0, min(u, ns - 1), lane, ring[u]);
   }
 #pragma unroll
   for (int tl = 0; tl < 4; ++tl)
@@ -410,7 +431,7 @@ __device__ __forceinline__ void big_loop(uint16_t* lds, const ExpertView& v01,
       rows_load<LO>(sh, sl, roff, min(s + 2, ns - 1), bh, bl);
       if (active) {
         big_step<LO>(lds + (u & 1) * kBuf, ring[u], q, j, acc);
-        load_a4(v01, v23, rb0, rstep, s + kBigPre, lane, ring[u]);
+        load_a<4, GU>(v0, v1, rb0, s + kBigPre, lane, ring[u]);
       }
       __syncthreads();
     }
@@ -430,7 +451,7 @@ __device__ __forceinline__ void big_loop(uint16_t* lds, const ExpertView& v01,
 __global__ __launch_bounds__(kGThreads) void k_gu_big(GroupArgs g) {
   extern __shared__ __attribute__((aligned(16))) uint16_t glds[];
   if ((int)blockIdx.x >= g.meta[1]) return;
-  const UnitTokens ut = unit_tokens(g.units[blockIdx.x], g.off, g.L.E, g.T);
+  const UnitTokens ut = unit_tokens(g.units[blockIdx.x], g.off, g.L.E, g.T, kMT);
   const LayerDev& L = g.L;
   const int H = L.H, K = L.K, I = ut.shared ? L.Ish : L.I;
   if ((int)blockIdx.y * 128 >= I) return;  // uniform per workgroup
@@ -454,16 +475,16 @@ __global__ __launch_bounds__(kGThreads) void k_gu_big(GroupArgs g) {
   f32x4 acc[4][kNCT];
   const int ns = H / kQuadCols;
   if (g.need_lo[0] != 0)
-    big_loop<true>(glds, gv, uv, rb0, 1, active, g.xhi, g.xlo, roff, ns, acc);
+    big_loop<true, true>(glds, gv, uv, rb0, active, g.xhi, g.xlo, roff, ns, acc);
   else
-    big_loop<false>(glds, gv, uv, rb0, 1, active, g.xhi, g.xlo, roff, ns, acc);
-  if (active) gu_epilogue<kNCT>(g, ut, I, f0, q, j, acc);
+    big_loop<false, true>(glds, gv, uv, rb0, active, g.xhi, g.xlo, roff, ns, acc);
+  if (active) gu_epilogue<4, kNCT>(g, ut, I, f0, q, j, acc);
 }
 
 __global__ __launch_bounds__(kGThreads) void k_down_big(GroupArgs g) {
   extern __shared__ __attribute__((aligned(16))) uint16_t glds[];
   if ((int)blockIdx.x >= g.meta[1]) return;
-  const UnitTokens ut = unit_tokens(g.units[blockIdx.x], g.off, g.L.E, g.T);
+  const UnitTokens ut = unit_tokens(g.units[blockIdx.x], g.off, g.L.E, g.T, kMT);
   const LayerDev& L = g.L;
   const int H = L.H, I = ut.shared ? L.Ish : L.I;
   const int tid = threadIdx.x, w = gwave_id(), lane = tid & 63, q = lane >> 4, j = lane & 15;
@@ -479,29 +500,32 @@ __global__ __launch_bounds__(kGThreads) void k_down_big(GroupArgs g) {
 #pragma unroll
   for (int i = 0; i < kNCT; ++i) roff[i] = (ut.p0 + min(srow + 16 * i, ut.n - 1)) * I + seg * 8;
   f32x4 acc[4][kNCT];
-  big_loop<true>(glds, dv, dv, rb0, 1, active, ut.shared ? g.hsh : g.hrh,
-                 ut.shared ? g.hsl : g.hrl, roff, I / kQuadCols, acc);
-  if (active) down_epilogue<kNCT>(g, ut, I, row0, q, j, acc);
+  big_loop<true, false>(glds, dv, dv, rb0, active, ut.shared ? g.hsh : g.hrh,
+                        ut.shared ? g.hsl : g.hrl, roff, I / kQuadCols, acc);
+  if (active) down_epilogue<4, kNCT>(g, ut, I, row0, q, j, acc);
 }
 
 // ---------------------------------------------------------------------------
 // Small units (<= 16 tokens): one column tile.  Waves are independent (no
-// LDS, no barrier): each wave owns 4 A tiles as in the big kernels and reads
-// its B fragments (lane (q, j): token j, columns 8q..8q+7 of each group)
-// straight from memory into the same prefetch ring as the A chunks, P
-// k-steps ahead.
+// LDS, no barrier): each wave owns 2 A tiles (gate/up: 16 features, gate and
+// up tile; down: 32 output rows) and reads its B fragments (lane (q, j):
+// token j, columns 8q..8q+7 of each group) straight from memory into the
+// same prefetch ring as the A chunks, P k-steps ahead.  At most 168 registers
+// per lane, so that three waves share a SIMD and their loads overlap.
+constexpr int kSmallTiles = 2;
+
 template <bool LO>
 struct SmallStep {
-  AChunks a;
+  AChunks<kSmallTiles> a;
   v4u b[kGroupsPerQuad];
   v4u bl[LO ? kGroupsPerQuad : 1];
 };
 
-template <bool LO>
-__device__ __forceinline__ void small_load(const ExpertView& v01, const ExpertView& v23, int rb0,
-                                           int rstep, int s, int lane, const uint16_t* bh,
+template <bool LO, bool GU>
+__device__ __forceinline__ void small_load(const ExpertView& v0, const ExpertView& v1, int rb0,
+                                           int s, int lane, const uint16_t* bh,
                                            const uint16_t* bl, SmallStep<LO>& st) {
-  load_a4(v01, v23, rb0, rstep, s, lane, st.a);
+  load_a<kSmallTiles, GU>(v0, v1, rb0, s, lane, st.a);
 #pragma unroll
   for (int kk = 0; kk < kGroupsPerQuad; ++kk) {
     const int o = s * kQuadCols + kk * kGroup;
@@ -511,39 +535,42 @@ __device__ __forceinline__ void small_load(const ExpertView& v01, const ExpertVi
 }
 
 template <bool LO>
-__device__ __forceinline__ void small_step(const SmallStep<LO>& st, f32x4 (&acc)[4][1]) {
+__device__ __forceinline__ void small_step(const SmallStep<LO>& st,
+                                           f32x4 (&acc)[kSmallTiles][1]) {
 #pragma unroll
   for (int kk = 0; kk < kGroupsPerQuad; ++kk) {
-    bf16x8 av[4];
-    dequant_a4(st.a, kk, av);
+    bf16x8 av[kSmallTiles];
+    dequant_a<kSmallTiles>(st.a, kk, av);
     const bf16x8 b = __builtin_bit_cast(bf16x8, st.b[kk]);
 #pragma unroll
-    for (int tl = 0; tl < 4; ++tl) acc[tl][0] = mfma16(av[tl], b, acc[tl][0]);
+    for (int tl = 0; tl < kSmallTiles; ++tl) acc[tl][0] = mfma16(av[tl], b, acc[tl][0]);
     if (LO) {
       const bf16x8 b2 = __builtin_bit_cast(bf16x8, st.bl[kk]);
 #pragma unroll
-      for (int tl = 0; tl < 4; ++tl) acc[tl][0] = mfma16(av[tl], b2, acc[tl][0]);
+      for (int tl = 0; tl < kSmallTiles; ++tl) acc[tl][0] = mfma16(av[tl], b2, acc[tl][0]);
     }
   }
 }
 
-// bh / bl point at this lane's B row (+ 8q) at column 0.
-template <bool LO, int P>
-__device__ __forceinline__ void small_loop(const ExpertView& v01, const ExpertView& v23, int rb0,
-                                           int rstep, const uint16_t* bh, const uint16_t* bl,
-                                           int ns, f32x4 (&acc)[4][1]) {
+// bh / bl point at this lane's B row (+ 8q) at column 0.  The ring slot of a
+// step is a constant of the unrolled body; steps past the last are clamped
+// to it (redundant loads only when ns % P != 0).
+template <bool LO, bool GU, int P>
+__device__ __forceinline__ void small_loop(const ExpertView& v0, const ExpertView& v1, int rb0,
+                                           const uint16_t* bh, const uint16_t* bl, int ns,
+                                           f32x4 (&acc)[kSmallTiles][1]) {
   const int lane = threadIdx.x & 63;
   SmallStep<LO> ring[P];
 #pragma unroll
-  for (int u = 0; u < P; ++u) small_load<LO>(v01, v23, rb0, rstep, min(u, ns - 1), lane, bh, bl, ring[u]);
+  for (int u = 0; u < P; ++u) small_load<LO, GU>(v0, v1, rb0, min(u, ns - 1), lane, bh, bl, ring[u]);
 #pragma unroll
-  for (int tl = 0; tl < 4; ++tl) acc[tl][0] = f32x4{0, 0, 0, 0};
+  for (int tl = 0; tl < kSmallTiles; ++tl) acc[tl][0] = f32x4{0, 0, 0, 0};
   int s0 = 0;
   for (; s0 + P < ns; s0 += P) {
 #pragma unroll
     for (int u = 0; u < P; ++u) {
       small_step<LO>(ring[u], acc);
-      small_load<LO>(v01, v23, rb0, rstep, min(s0 + u + P, ns - 1), lane, bh, bl, ring[u]);
+      small_load<LO, GU>(v0, v1, rb0, min(s0 + u + P, ns - 1), lane, bh, bl, ring[u]);
     }
   }
 #pragma unroll
@@ -551,14 +578,18 @@ __device__ __forceinline__ void small_loop(const ExpertView& v01, const ExpertVi
     if (s0 + u < ns) small_step<LO>(ring[u], acc);
 }
 
-__global__ __launch_bounds__(kGThreads) void k_gu_small(GroupArgs g) {
+constexpr int kSmallGuCols = 4 * 16;   // features per small gate/up workgroup
+constexpr int kSmallDnRows = 4 * 32;   // output rows per small down workgroup
+
+__global__ __launch_bounds__(kGThreads) __attribute__((amdgpu_waves_per_eu(3))) void k_gu_small(
+    GroupArgs g) {
   const int ui = g.meta[1] + blockIdx.x;
   if (ui >= g.meta[0]) return;
-  const UnitTokens ut = unit_tokens(g.units[ui], g.off, g.L.E, g.T);
+  const UnitTokens ut = unit_tokens(g.units[ui], g.off, g.L.E, g.T, kSmallMax);
   const LayerDev& L = g.L;
   const int H = L.H, K = L.K, I = ut.shared ? L.Ish : L.I;
   const int w = gwave_id(), lane = threadIdx.x & 63, q = lane >> 4, j = lane & 15;
-  const int f0 = blockIdx.y * 128 + 32 * w;
+  const int f0 = blockIdx.y * kSmallGuCols + 16 * w;
   if (f0 >= I) return;  // uniform per wave; no barriers in this kernel
   const size_t mat = (size_t)I * H;
   const ExpertView gv = ut.shared ? ExpertView{L.sgu_nib, L.sgu_sc, I, H}
@@ -568,33 +599,34 @@ __global__ __launch_bounds__(kGThreads) void k_gu_small(GroupArgs g) {
   const int r = min(j, ut.n - 1);
   const int t = ut.shared ? ut.p0 + r : g.perm[ut.p0 + r] / K;
   const size_t o = (size_t)t * H + 8 * q;
-  f32x4 acc[4][1];
+  f32x4 acc[kSmallTiles][1];
   const int ns = H / kQuadCols;
   if (g.need_lo[0] != 0)
-    small_loop<true, 2>(gv, uv, f0 / kTileRows, 1, g.xhi + o, g.xlo + o, ns, acc);
+    small_loop<true, true, 2>(gv, uv, f0 / kTileRows, g.xhi + o, g.xlo + o, ns, acc);
   else
-    small_loop<false, 4>(gv, uv, f0 / kTileRows, 1, g.xhi + o, g.xlo + o, ns, acc);
-  gu_epilogue<1>(g, ut, I, f0, q, j, acc);
+    small_loop<false, true, 4>(gv, uv, f0 / kTileRows, g.xhi + o, g.xlo + o, ns, acc);
+  gu_epilogue<kSmallTiles, 1>(g, ut, I, f0, q, j, acc);
 }
 
-__global__ __launch_bounds__(kGThreads) void k_down_small(GroupArgs g) {
+__global__ __launch_bounds__(kGThreads) __attribute__((amdgpu_waves_per_eu(3))) void k_down_small(
+    GroupArgs g) {
   const int ui = g.meta[1] + blockIdx.x;
   if (ui >= g.meta[0]) return;
-  const UnitTokens ut = unit_tokens(g.units[ui], g.off, g.L.E, g.T);
+  const UnitTokens ut = unit_tokens(g.units[ui], g.off, g.L.E, g.T, kSmallMax);
   const LayerDev& L = g.L;
   const int H = L.H, I = ut.shared ? L.Ish : L.I;
   const int w = gwave_id(), lane = threadIdx.x & 63, q = lane >> 4, j = lane & 15;
-  const int row0 = blockIdx.y * 256 + 64 * w;
+  const int row0 = blockIdx.y * kSmallDnRows + 32 * w;
   if (row0 >= H) return;
   const size_t mat = (size_t)H * I;
   const ExpertView dv = ut.shared ? ExpertView{L.sd_nib, L.sd_sc, H, I}
                                   : ExpertView{L.d_nib + (size_t)ut.e * (mat / 2),
                                                L.d_sc + (size_t)ut.e * (mat / kGroup), H, I};
   const size_t o = (size_t)(ut.p0 + min(j, ut.n - 1)) * I + 8 * q;
-  f32x4 acc[4][1];
-  small_loop<true, 2>(dv, dv, row0 / kTileRows, 1, (ut.shared ? g.hsh : g.hrh) + o,
-                      (ut.shared ? g.hsl : g.hrl) + o, I / kQuadCols, acc);
-  down_epilogue<1>(g, ut, I, row0, q, j, acc);
+  f32x4 acc[kSmallTiles][1];
+  small_loop<true, false, 2>(dv, dv, row0 / kTileRows, (ut.shared ? g.hsh : g.hrh) + o,
+                             (ut.shared ? g.hsl : g.hrl) + o, I / kQuadCols, acc);
+  down_epilogue<kSmallTiles, 1>(g, ut, I, row0, q, j, acc);
 }
 
 hipError_t launch_experts_grouped(const LayerDev& L, const uint16_t* xhi, const uint16_t* xlo,
@@ -606,11 +638,12 @@ hipError_t launch_experts_grouped(const LayerDev& L, const uint16_t* xhi, const 
                        hrh, hrl, hsh, hsl, r, rs, status};
   const int nu = group_units_max(T, L.K, L.E);
   const int imax = L.I > L.Ish ? L.I : L.Ish;
-  const dim3 gu_grid(nu, (imax + 127) / 128), dn_grid(nu, (L.H + 255) / 256);
-  hipLaunchKernelGGL(k_gu_big, gu_grid, dim3(kGThreads), kBigLds, st, g);
-  hipLaunchKernelGGL(k_gu_small, gu_grid, dim3(kGThreads), 0, st, g);
-  hipLaunchKernelGGL(k_down_big, dn_grid, dim3(kGThreads), kBigLds, st, g);
-  hipLaunchKernelGGL(k_down_small, dn_grid, dim3(kGThreads), 0, st, g);
+  hipLaunchKernelGGL(k_gu_big, dim3(nu, (imax + 127) / 128), dim3(kGThreads), kBigLds, st, g);
+  hipLaunchKernelGGL(k_gu_small, dim3(nu, (imax + kSmallGuCols - 1) / kSmallGuCols),
+                     dim3(kGThreads), 0, st, g);
+  hipLaunchKernelGGL(k_down_big, dim3(nu, (L.H + 255) / 256), dim3(kGThreads), kBigLds, st, g);
+  hipLaunchKernelGGL(k_down_small, dim3(nu, (L.H + kSmallDnRows - 1) / kSmallDnRows),
+                     dim3(kGThreads), 0, st, g);
   return hipGetLastError();
 }
 

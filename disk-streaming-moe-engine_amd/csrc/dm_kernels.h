@@ -27,7 +27,12 @@ hipError_t launch_router_generic(const float* x, const float* w, int T, int H, i
 
 // ---- decode path (one token per launch set) ----
 hipError_t launch_router_dec(const LayerDev& L, const float* x, int T, float* z,
-                             unsigned long long* status, hipStream_t st);
+                             unsigned long long* status, hipStream_t st,
+                             const int* gate = nullptr);
+// Many tokens whose activations are bf16 values (*need_lo == 0): logits of
+// all E experts and the shared gate, z [T][E+1], on the matrix cores.
+hipError_t launch_router_mfma(const LayerDev& L, const uint16_t* xhi, const int* need_lo, int T,
+                              float* z, hipStream_t st);
 hipError_t launch_router_select(const float* z, int ldz, int T, int E, int K, int has_sh,
                                 int32_t* ids, float* probs, float* shg,
                                 unsigned long long* status, hipStream_t st);

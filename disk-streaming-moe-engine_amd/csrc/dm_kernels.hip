@@ -213,49 +213,191 @@ hipError_t launch_router_generic(const float* x, const float* w, int T, int H, i
 // Layer form: R16 bf16 weights with E+1 rows (row E = shared-expert gate,
 // which shared_gate_forward, src/layers/moe.mojo:70-100, reduces in the same
 // 16-lane order).  One lane per (row, chain l); 16 rows per 256-thread block;
-// blockIdx.y = token.  x is staged in LDS once per block.
-__global__ __launch_bounds__(256) void k_router_dec(LayerDev L, const float* __restrict__ x,
+// blockIdx.y = token.  x is staged in LDS once per block.  With gate set, the
+// kernel runs only when *gate is nonzero (activations that are not all bf16
+// values, which k_router_mfma leaves to it).
+__global__ __launch_bounds__(256) void k_router_dec(LayerDev L, const float* __restrict__ x, int T,
                                                      float* __restrict__ z,
-                                                     unsigned long long* status) {
+                                                     unsigned long long* status,
+                                                     const int* __restrict__ gate) {
   extern __shared__ float xs[];
-  const int H = L.H, t = blockIdx.y;
-  const float* xr = x + (size_t)t * H;
-  bool bad = false;
-  for (int i = threadIdx.x; i < H; i += 256) {
-    const float v = xr[i];
-    bad |= !finite_f(v);
-    xs[i] = v;
-  }
-  if (bad && blockIdx.x == 0) record_err(status, err_key(kPhX, 0, 0, 0, 0));
-  __syncthreads();
+  if (gate && gate[0] == 0) return;  // uniform: k_router_mfma computed these logits
+  const int H = L.H;
   const int l = threadIdx.x & 15;
   const int e = blockIdx.x * 16 + (threadIdx.x >> 4);
-  float acc = 0.0f;
-  if (e <= L.E) {
-    const uint4* wp = reinterpret_cast<const uint4*>(L.router + r16_index(H, e, l));
-    const int nj8 = H / 128;
-    for (int j8 = 0; j8 < nj8; ++j8) {
-      const uint4 w = wp[(size_t)j8 * 16];
-      const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
-      const float* xc = xs + j8 * 128 + l;
+  for (int t = blockIdx.y; t < T; t += gridDim.y) {
+    const float* xr = x + (size_t)t * H;
+    bool bad = false;
+    for (int i = threadIdx.x; i < H; i += 256) {
+      const float v = xr[i];
+      bad |= !finite_f(v);
+      xs[i] = v;
+    }
+    if (bad && blockIdx.x == 0) record_err(status, err_key(kPhX, 0, 0, 0, 0));
+    __syncthreads();
+    float acc = 0.0f;
+    if (e <= L.E) {
+      const uint4* wp = reinterpret_cast<const uint4*>(L.router + r16_index(H, e, l));
+      const int nj8 = H / 128;
+      for (int j8 = 0; j8 < nj8; ++j8) {
+        const uint4 w = wp[(size_t)j8 * 16];
+        const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+        const float* xc = xs + j8 * 128 + l;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        acc = acc + xc[(2 * i) * 16] * bf16lo(ww[i]);
-        acc = acc + xc[(2 * i + 1) * 16] * bf16hi(ww[i]);
+        for (int i = 0; i < 4; ++i) {
+          acc = acc + xc[(2 * i) * 16] * bf16lo(ww[i]);
+          acc = acc + xc[(2 * i + 1) * 16] * bf16hi(ww[i]);
+        }
       }
     }
-  }
-  // halving tree over the 16 chains of a row: lane l += lane l + w
+    // halving tree over the 16 chains of a row: lane l += lane l + w
 #pragma unroll
-  for (int wdt = 8; wdt >= 1; wdt >>= 1) acc = acc + __shfl_down(acc, wdt, 16);
-  if (l == 0 && e <= L.E) z[(size_t)t * (L.E + 1) + e] = acc;
+    for (int wdt = 8; wdt >= 1; wdt >>= 1) acc = acc + __shfl_down(acc, wdt, 16);
+    if (l == 0 && e <= L.E) z[(size_t)t * (L.E + 1) + e] = acc;
+    __syncthreads();  // xs is restaged for the next token
+  }
 }
 
 hipError_t launch_router_dec(const LayerDev& L, const float* x, int T, float* z,
-                             unsigned long long* status, hipStream_t st) {
+                             unsigned long long* status, hipStream_t st, const int* gate) {
   const int blocks = (L.E + 1 + 15) / 16;
-  hipLaunchKernelGGL(k_router_dec, dim3(blocks, T), dim3(256), (size_t)L.H * sizeof(float), st, L,
-                     x, z, status);
+  const int ty = T < 256 ? T : 256;  // workgroups loop over the tokens beyond
+  hipLaunchKernelGGL(k_router_dec, dim3(blocks, ty), dim3(256), (size_t)L.H * sizeof(float), st, L,
+                     x, T, z, status, gate);
+  return hipGetLastError();
+}
+
+// ===========================================================================
+// Router logits for many tokens on the matrix cores, for activations that
+// are bf16 values (need_lo == 0; otherwise the workgroups return and
+// k_router_dec computes the logits).  Every chain of router_project
+// (src/layers/router.mojo:15-106) is acc_l = acc_l + x[16s+l] * w[16s+l] in s
+// order; with x and w bf16 the product is exact in fp32, so an fp32 MFMA with
+// a reduction depth of 1 (v_mfma_f32_16x16x1f32: four blocks of 16x16 outer
+// products, one rounding per accumulation) computes exactly that step for 16
+// tokens x 16 experts at once.  Block b of instruction g carries chain
+// l = 4g + b; the output of block b for (token i, expert j) sits in lane
+// j + 16 (i / 4), register 4b + i % 4, so the 16 chains of one logit share a
+// lane and the halving tree (l += l + w, w = 8, 4, 2, 1) is plain adds.
+//
+// Workgroup: 16 tokens x 64 experts (wave w: experts 64 blockIdx.x + 16 w);
+// the last column of workgroups computes the shared-expert gate logit (row E)
+// with one lane per (token, chain) instead.  The tokens' activations are
+// staged once in LDS in chain-major order: xs[i][l][s] = x[t0 + i][16 s + l]
+// (bf16), rows padded by 16 bytes so that the 16 lanes of one operand fetch
+// hit distinct banks.
+// ===========================================================================
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+__global__ __launch_bounds__(256) void k_router_mfma(LayerDev L, const uint16_t* __restrict__ xhi,
+                                                      const int* __restrict__ need_lo, int T,
+                                                      float* __restrict__ z) {
+  extern __shared__ __attribute__((aligned(16))) uint16_t xs_chain[];
+  uint16_t* xs = xs_chain;
+  if (need_lo[0] != 0) return;  // uniform: k_router_dec takes these tokens
+  const int H = L.H, E = L.E, ns = H / 16;
+  const int pitch = 16 * ns + 8;  // elements per staged token (16 B of padding)
+  const int t0 = blockIdx.y * 16, tid = threadIdx.x;
+  // stage: thread item (token i, step pair sp) reads x[32 sp .. 32 sp + 31]
+  // and writes, for each chain l, steps 2 sp and 2 sp + 1 as one word
+  const int npair = ns / 2;
+  for (int idx = tid; idx < 16 * npair; idx += 256) {
+    const int i = idx / npair, sp = idx % npair;
+    uint32_t v[16];
+    if (t0 + i < T) {
+      const uint4* src = reinterpret_cast<const uint4*>(xhi + (size_t)(t0 + i) * H + 32 * sp);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const uint4 u = src[c];
+        v[4 * c] = u.x; v[4 * c + 1] = u.y; v[4 * c + 2] = u.z; v[4 * c + 3] = u.w;
+      }
+    } else {
+#pragma unroll
+      for (int c = 0; c < 16; ++c) v[c] = 0;
+    }
+#pragma unroll
+    for (int l = 0; l < 16; ++l) {
+      const uint32_t a = (v[l >> 1] >> (16 * (l & 1))) & 0xFFFFu;          // step 2 sp
+      const uint32_t bq = (v[8 + (l >> 1)] >> (16 * (l & 1))) & 0xFFFFu;   // step 2 sp + 1
+      *reinterpret_cast<uint32_t*>(xs + i * pitch + l * ns + 2 * sp) = a | (bq << 16);
+    }
+  }
+  __syncthreads();
+  const int lane = tid & 63, w = tid >> 6;
+  if ((int)blockIdx.x == (E + 63) / 64) {
+    // shared-expert gate: lane (token i, chain l), 8 steps per 16-byte read
+    const int i = tid >> 4, l = tid & 15;
+    const uint16_t* xr = xs + i * pitch + l * ns;
+    const uint16_t* wr = L.router + r16_index(H, E, l);
+    float acc = 0.0f;
+    for (int c = 0; c < ns / 8; ++c) {
+      const uint4 xv = *reinterpret_cast<const uint4*>(xr + 8 * c);
+      const uint4 wv = *reinterpret_cast<const uint4*>(wr + (size_t)c * 128);
+      const uint32_t xa[4] = {xv.x, xv.y, xv.z, xv.w}, wa[4] = {wv.x, wv.y, wv.z, wv.w};
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        acc = acc + bf16lo(xa[u]) * bf16lo(wa[u]);
+        acc = acc + bf16hi(xa[u]) * bf16hi(wa[u]);
+      }
+    }
+#pragma unroll
+    for (int wdt = 8; wdt >= 1; wdt >>= 1) acc = acc + __shfl_down(acc, wdt, 16);
+    if (l == 0 && t0 + i < T) z[(size_t)(t0 + i) * (E + 1) + E] = acc;
+    return;
+  }
+  const int e0 = blockIdx.x * 64 + 16 * w;
+  if (e0 >= E) return;  // uniform per wave (no barrier below)
+  const int b = lane >> 4, jj = lane & 15;
+  const int er = min(e0 + jj, E - 1);
+  // A: token jj (as row i = lane & 15 of block b), chain 4g + b
+  const uint16_t* xa = xs + jj * pitch + b * ns;
+  const uint16_t* wb = L.router + r16_index(H, er, b);
+  f32x16 acc[4];
+#pragma unroll
+  for (int g = 0; g < 4; ++g) acc[g] = f32x16{};
+  for (int c = 0; c < ns / 8; ++c) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      // chain 4g + b: steps 8c .. 8c + 7
+      const uint4 xv = *reinterpret_cast<const uint4*>(xa + 4 * g * ns + 8 * c);
+      const uint4 wv = *reinterpret_cast<const uint4*>(wb + (size_t)c * 128 + 4 * g * 8);
+      const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w}, ww[4] = {wv.x, wv.y, wv.z, wv.w};
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        acc[g] = __builtin_amdgcn_mfma_f32_16x16x1f32(bf16lo(xw[u]), bf16lo(ww[u]), acc[g], 0, 0, 0);
+        acc[g] = __builtin_amdgcn_mfma_f32_16x16x1f32(bf16hi(xw[u]), bf16hi(ww[u]), acc[g], 0, 0, 0);
+      }
+    }
+  }
+  // lane holds tokens t0 + 4 b + r, expert e0 + jj; chain 4g + bb at acc[g][4 bb + r]
+  const int e = e0 + jj;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    float v[4][4];
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+#pragma unroll
+      for (int bb = 0; bb < 4; ++bb) v[g][bb] = acc[g][4 * bb + r];
+#pragma unroll
+    for (int bb = 0; bb < 4; ++bb) {  // w = 8: chain l += chain l + 8
+      v[0][bb] = v[0][bb] + v[2][bb];
+      v[1][bb] = v[1][bb] + v[3][bb];
+    }
+#pragma unroll
+    for (int bb = 0; bb < 4; ++bb) v[0][bb] = v[0][bb] + v[1][bb];  // w = 4
+    v[0][0] = v[0][0] + v[0][2];  // w = 2
+    v[0][1] = v[0][1] + v[0][3];
+    const float s = v[0][0] + v[0][1];  // w = 1
+    const int t = t0 + 4 * b + r;
+    if (t < T && e < E) z[(size_t)t * (E + 1) + e] = s;
+  }
+}
+
+hipError_t launch_router_mfma(const LayerDev& L, const uint16_t* xhi, const int* need_lo, int T,
+                              float* z, hipStream_t st) {
+  const size_t lds = (size_t)16 * (16 * (L.H / 16) + 8) * sizeof(uint16_t);
+  hipLaunchKernelGGL(k_router_mfma, dim3((L.E + 63) / 64 + 1, (T + 15) / 16), dim3(256), lds, st,
+                     L, xhi, need_lo, T, z);
   return hipGetLastError();
 }
 
@@ -275,9 +417,9 @@ __global__ __launch_bounds__(64) void k_router_select(const float* __restrict__ 
                                                        float* __restrict__ probs,
                                                        float* __restrict__ shg,
                                                        unsigned long long* status) {
-  extern __shared__ float sm[];  // p[E], then 2 scalars
+  extern __shared__ __attribute__((aligned(16))) float sm[];  // p[E], then 2 scalars
   float* pv = sm;
-  float* scal = sm + E;
+  float* scal = sm + ((E + 3) & ~3);
   const int t = blockIdx.x, lane = threadIdx.x;
   const float* zr = z + (size_t)t * ldz;
   float m = -__builtin_inff();
@@ -299,8 +441,7 @@ __global__ __launch_bounds__(64) void k_router_select(const float* __restrict__ 
   }
   __syncthreads();
   if (lane == 0) {
-    float s = 0.0f;
-    for (int e = 0; e < E; ++e) s = s + pv[e];
+    const float s = seq_sum(pv, E);
     if (!(s > 0.0f) || !finite_f(s)) record_err(status, err_key(kPhSoftmax, t, 0, 1 + E, 0));
     scal[0] = 1.0f / s;
   }
@@ -336,8 +477,7 @@ __global__ __launch_bounds__(64) void k_router_select(const float* __restrict__ 
   if (lane == 0) {
     if (sum_topk > 1.00001f) record_err(status, err_key(kPhTopk, t, 0, 0, kTkSum));
     if (K < E && __builtin_fabsf(sum_topk - 1.0f) < 1e-6f) {
-      float sum_all = 0.0f;
-      for (int e = 0; e < E; ++e) sum_all = sum_all + pv[e];
+      const float sum_all = seq_sum(pv, E);
       if (sum_all - sum_topk > 1e-5f) record_err(status, err_key(kPhTopk, t, 0, 0, kTkLeak));
     }
     if (has_sh) {
@@ -354,7 +494,7 @@ __global__ __launch_bounds__(64) void k_router_select(const float* __restrict__ 
 hipError_t launch_router_select(const float* z, int ldz, int T, int E, int K, int has_sh,
                                 int32_t* ids, float* probs, float* shg,
                                 unsigned long long* status, hipStream_t st) {
-  hipLaunchKernelGGL(k_router_select, dim3(T), dim3(64), (size_t)(E + 2) * sizeof(float), st, z,
+  hipLaunchKernelGGL(k_router_select, dim3(T), dim3(64), (size_t)(((E + 3) & ~3) + 2) * sizeof(float), st, z,
                      ldz, E, K, has_sh, ids, probs, shg, status);
   return hipGetLastError();
 }

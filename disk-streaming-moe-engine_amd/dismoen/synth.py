@@ -139,3 +139,38 @@ def algorithmic_bytes_per_token(H, E, K, I, Ish, G=32, x_bytes=4, y_bytes=4) -> 
     with fp16 group scales, the bf16 router and shared gate, x in, y out."""
     return (K * expert_bytes(H, I, G) + expert_bytes(H, Ish, G) + 2 * E * H + 2 * H
             + x_bytes * H + y_bytes * H)
+
+
+def make_layer_device(hidden: int, num_experts: int, top_k: int, inter: int, inter_sh: int,
+                      group_size: int = 32, seed: int = 0, device="cuda") -> dict:
+    """The same distributions as make_layer, drawn on the GPU with torch (for
+    many-layer workloads whose host generation would take minutes).  Returns
+    field name -> contiguous device tensor, for MoEBlock.upload_layer_device."""
+    import torch
+    H, E, I, Ish, G = hidden, num_experts, inter, inter_sh, group_size
+    g = torch.Generator(device=device)
+    g.manual_seed(seed)
+    lut = torch.from_numpy(_PAIR_LUT).to(device)
+
+    def bf16(n):
+        v = torch.randn(n, generator=g, device=device) * 0.02
+        return v.to(torch.bfloat16).view(torch.int16)
+
+    def scales(n):
+        v = (torch.randn(n, generator=g, device=device).abs() * 0.02 / 7.5).half()
+        b = v.view(torch.int16)
+        return torch.where(b == 0, torch.ones_like(b), b)
+
+    def codes(n):
+        out = torch.empty(n // 2, dtype=torch.uint8, device=device)
+        step = 1 << 26
+        for o in range(0, n // 2, step):
+            m = min(step, n // 2 - o)
+            out[o:o + m] = lut[torch.randint(0, 225, (m,), generator=g, device=device)]
+        return out
+
+    return {"router_bf16": bf16(E * H), "shgate_bf16": bf16(H),
+            "gu_scales": scales(E * 2 * I * H // G), "gu_packed": codes(E * 2 * I * H),
+            "d_scales": scales(E * H * I // G), "d_packed": codes(E * H * I),
+            "sh_gu_scales": scales(2 * Ish * H // G), "sh_gu_packed": codes(2 * Ish * H),
+            "sh_d_scales": scales(H * Ish // G), "sh_d_packed": codes(H * Ish)}

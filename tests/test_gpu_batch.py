@@ -122,3 +122,36 @@ def test_batch_overflow_error_matches_oracle(block, oracle):
             call()
         msgs.append(str(e.value))
     assert msgs[0] == msgs[1], msgs
+
+
+def test_many_tokens_matrix_core_router_vs_oracle(block, oracle, qwen):
+    """From 64 tokens on, bf16 activations are routed on the matrix cores
+    (one fp32 MFMA step per chain element): every token's ids and
+    probabilities bit-exact."""
+    T = 96
+    x = synth.make_activations(np.random.default_rng(310), (T, 2048))
+    pool = oracle.Pool(8)
+    try:
+        _check(block, oracle, qwen, 5, x, pool=pool)
+    finally:
+        pool.close()
+
+
+def test_many_tokens_fp32_activations_vs_oracle(block, oracle, qwen):
+    """Activations that are not bf16 values take the lane-chain router."""
+    T = 80
+    x = np.random.default_rng(311).standard_normal((T, 2048)).astype(np.float32)
+    pool = oracle.Pool(8)
+    try:
+        _check(block, oracle, qwen, 5, x, pool=pool)
+    finally:
+        pool.close()
+
+
+def test_many_tokens_toy_layer_vs_oracle(block, oracle):
+    """Fewer experts than one router workgroup covers (16 < 64), hidden 256."""
+    L = synth.make_layer(**synth.CONFIG_TOY, seed=8)
+    block.upload_layer(7, L)
+    x = synth.make_activations(np.random.default_rng(312), (70, 256))
+    _check(block, oracle, L, 7, x)
+    _check(block, oracle, L, 7, x, residual=x)

@@ -115,6 +115,35 @@ def test_stack_of_layers(block, oracle):
     assert ok, (err, rms)
 
 
+def test_device_generated_layers_stack_decode(block, oracle):
+    """Layers drawn on the GPU and uploaded from device pointers (the path of
+    the 40-layer workload), one decode token through two of them."""
+    import torch
+    cfg = synth.CONFIG_QWEN36
+    dims = (cfg["hidden"], cfg["num_experts"], cfg["top_k"], cfg["inter"], cfg["inter_sh"])
+    layers = []
+    for l in range(2):
+        W = synth.make_layer_device(**cfg, seed=500 + l, device="cuda")
+        torch.cuda.synchronize()
+        block.upload_layer_device(20 + l, dims, {k: v.data_ptr() for k, v in W.items()})
+        block.sync()
+        host = {k: v.cpu().numpy().view(np.uint16 if v.dtype == torch.int16 else np.uint8)
+                for k, v in W.items()}
+        layers.append(synth.MoELayerQ4(*dims, 32, **host))
+        del W
+    x = synth.make_activations(np.random.default_rng(108), (1, 2048))
+    out, ids, probs = block.forward_stack(x, 20, 2, 1, eps=1e-6)
+    oo, ido, po = oracle.moe_stack_q4(layers, x, 1, 1e-6)
+    assert np.array_equal(ids, ido)
+    # layer 0 routes the same input bits; deeper layers see the previous
+    # layer's output, equal only within the tolerance
+    assert np.array_equal(probs[0].view(np.uint32), po[0].view(np.uint32))
+    err, rms, ok = tol_check(out - x, oo - x)
+    assert ok, (err, rms)
+    block.free_layer(20)
+    block.free_layer(21)
+
+
 def test_interleaved_layers_of_different_shapes(block, oracle, toy, qwen):
     """Launches of layers with different workgroup counts alternate on one
     context (each layer keeps its own handoff counters)."""
