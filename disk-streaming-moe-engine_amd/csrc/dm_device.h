@@ -72,6 +72,10 @@ __device__ __forceinline__ float dm_silu(float z) {
   return z * dm_sigmoid(z);
 }
 
+// Wavefront-wide maxima from the ROCm device library (ockl).
+extern "C" __device__ __attribute__((const)) unsigned int __ockl_wfred_max_u32(unsigned int);
+extern "C" __device__ __attribute__((const)) float __ockl_wfred_max_f32(float);
+
 // Round-to-nearest-even fp32 -> bf16 pair packed as (lo, hi).
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));

@@ -638,10 +638,15 @@ hipError_t launch_experts_grouped(const LayerDev& L, const uint16_t* xhi, const 
                        hrh, hrl, hsh, hsl, r, rs, status};
   const int nu = group_units_max(T, L.K, L.E);
   const int imax = L.I > L.Ish ? L.I : L.Ish;
-  hipLaunchKernelGGL(k_gu_big, dim3(nu, (imax + 127) / 128), dim3(kGThreads), kBigLds, st, g);
+  // an expert holds at most T tokens (its ids per token are distinct), so
+  // units of more than 2 * kSmallMax tokens need T > 2 * kSmallMax
+  const bool big = T > 2 * kSmallMax;
+  if (big)
+    hipLaunchKernelGGL(k_gu_big, dim3(nu, (imax + 127) / 128), dim3(kGThreads), kBigLds, st, g);
   hipLaunchKernelGGL(k_gu_small, dim3(nu, (imax + kSmallGuCols - 1) / kSmallGuCols),
                      dim3(kGThreads), 0, st, g);
-  hipLaunchKernelGGL(k_down_big, dim3(nu, (L.H + 255) / 256), dim3(kGThreads), kBigLds, st, g);
+  if (big)
+    hipLaunchKernelGGL(k_down_big, dim3(nu, (L.H + 255) / 256), dim3(kGThreads), kBigLds, st, g);
   hipLaunchKernelGGL(k_down_small, dim3(nu, (L.H + kSmallDnRows - 1) / kSmallDnRows),
                      dim3(kGThreads), 0, st, g);
   return hipGetLastError();

@@ -411,33 +411,42 @@ __device__ __forceinline__ bool better(float va, int ia, float vb, int ib) {
   return va > vb || (va == vb && ia < ib);
 }
 
+// NE values per lane: element e = lane + 64 i.  Probabilities stay in
+// registers; each selection round is two wave-wide maxima: of the key
+// f2u(p) + 1 (p >= 0, so its bits order like p; 0 marks "no candidate") and,
+// among the lanes holding that key, of 0xFFFF - e (the lowest expert id).
+template <int NE>
 __global__ __launch_bounds__(64) void k_router_select(const float* __restrict__ z, int ldz, int E,
                                                        int K, int has_sh,
                                                        int32_t* __restrict__ ids,
                                                        float* __restrict__ probs,
                                                        float* __restrict__ shg,
                                                        unsigned long long* status) {
-  extern __shared__ __attribute__((aligned(16))) float sm[];  // p[E], then 2 scalars
+  extern __shared__ __attribute__((aligned(16))) float sm[];  // e[E] (padded), then 1/S
   float* pv = sm;
   float* scal = sm + ((E + 3) & ~3);
   const int t = blockIdx.x, lane = threadIdx.x;
   const float* zr = z + (size_t)t * ldz;
+  float zv[NE];
   float m = -__builtin_inff();
-  for (int e = lane; e < E; e += 64) {
-    const float v = zr[e];
-    if (!finite_f(v)) record_err(status, err_key(kPhLogit, t, 0, e, 0));
-    m = v > m ? v : m;
-  }
 #pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) {
-    const float other = __shfl_xor(m, o);
-    m = other > m ? other : m;
+  for (int i = 0; i < NE; ++i) {
+    const int e = lane + 64 * i;
+    zv[i] = e < E ? zr[e] : -__builtin_inff();
+    if (e < E && !finite_f(zv[i])) record_err(status, err_key(kPhLogit, t, 0, e, 0));
+    m = zv[i] > m ? zv[i] : m;
   }
+  m = __ockl_wfred_max_f32(m);
   if (lane == 0 && !finite_f(m)) record_err(status, err_key(kPhSoftmax, t, 0, 0, 0));
-  for (int e = lane; e < E; e += 64) {
-    const float ev = dm_expf(zr[e] - m);
-    if (!finite_f(ev)) record_err(status, err_key(kPhSoftmax, t, 0, 1 + e, 0));
-    pv[e] = ev;
+  float p[NE];
+#pragma unroll
+  for (int i = 0; i < NE; ++i) {
+    const int e = lane + 64 * i;
+    if (e < E) {
+      p[i] = dm_expf(zv[i] - m);
+      if (!finite_f(p[i])) record_err(status, err_key(kPhSoftmax, t, 0, 1 + e, 0));
+      pv[e] = p[i];
+    }
   }
   __syncthreads();
   if (lane == 0) {
@@ -447,31 +456,36 @@ __global__ __launch_bounds__(64) void k_router_select(const float* __restrict__ 
   }
   __syncthreads();
   const float inv = scal[0];
-  for (int e = lane; e < E; e += 64) pv[e] = pv[e] * inv;
-  __syncthreads();
-  // K rounds of wave-wide (p desc, id asc) argmax over unselected experts.
-  uint32_t taken = 0;  // bit i: element lane + 64*i selected (E <= 2048)
-  float sum_topk = 0.0f;
-  for (int i = 0; i < K; ++i) {
-    float bv = -1.0f;
-    int bi = 0x7FFFFFFF;
-    for (int e = lane, s = 0; e < E; e += 64, ++s) {
-      if (taken >> s & 1u) continue;
-      const float v = pv[e];
-      if (better(v, e, bv, bi)) { bv = v; bi = e; }
-    }
+  uint32_t key[NE];
 #pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) {
-      const float ov = __shfl_xor(bv, o);
-      const int oi = __shfl_xor(bi, o);
-      if (better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
-    }
-    if (bi < 0 || bi >= E) bi = 0;  // only reachable after a recorded error
-    if ((bi & 63) == lane) taken |= 1u << (bi >> 6);
+  for (int i = 0; i < NE; ++i) {
+    const int e = lane + 64 * i;
+    p[i] = p[i] * inv;
+    key[i] = e < E ? f2u(p[i]) + 1u : 0u;
+  }
+  __syncthreads();  // pv is rewritten with the probabilities for the leak check
+#pragma unroll
+  for (int i = 0; i < NE; ++i)
+    if (lane + 64 * i < E) pv[lane + 64 * i] = p[i];
+  float sum_topk = 0.0f;
+  for (int r = 0; r < K; ++r) {
+    uint32_t bk = 0;
+    int bi = 0xFFFF;
+#pragma unroll
+    for (int i = 0; i < NE; ++i)  // ascending e within the lane: first of equal keys wins
+      if (key[i] > bk) { bk = key[i]; bi = lane + 64 * i; }
+    const uint32_t mk = __ockl_wfred_max_u32(bk);
+    const uint32_t me = __ockl_wfred_max_u32(bk == mk && mk != 0u ? 0xFFFFu - (uint32_t)bi : 0u);
+    int win = (int)(0xFFFFu - me);
+    if (mk == 0u || win < 0 || win >= E) win = 0;  // only reachable after a recorded error
+    const float bv = u2f(mk - 1u);
+#pragma unroll
+    for (int i = 0; i < NE; ++i)
+      if (lane + 64 * i == win) key[i] = 0u;
     sum_topk = sum_topk + bv;
     if (lane == 0) {
-      ids[(size_t)t * K + i] = bi;
-      probs[(size_t)t * K + i] = bv;
+      ids[(size_t)t * K + r] = win;
+      probs[(size_t)t * K + r] = bv;
     }
   }
   if (lane == 0) {
@@ -494,8 +508,18 @@ __global__ __launch_bounds__(64) void k_router_select(const float* __restrict__ 
 hipError_t launch_router_select(const float* z, int ldz, int T, int E, int K, int has_sh,
                                 int32_t* ids, float* probs, float* shg,
                                 unsigned long long* status, hipStream_t st) {
-  hipLaunchKernelGGL(k_router_select, dim3(T), dim3(64), (size_t)(((E + 3) & ~3) + 2) * sizeof(float), st, z,
-                     ldz, E, K, has_sh, ids, probs, shg, status);
+  const size_t lds = (size_t)(((E + 3) & ~3) + 4) * sizeof(float);
+  const int ne = (E + 63) / 64;
+#define DM_SELECT(N)                                                                         \
+  hipLaunchKernelGGL(k_router_select<N>, dim3(T), dim3(64), lds, st, z, ldz, E, K, has_sh, ids, \
+                     probs, shg, status)
+  if (ne <= 1) DM_SELECT(1);
+  else if (ne <= 2) DM_SELECT(2);
+  else if (ne <= 4) DM_SELECT(4);
+  else if (ne <= 8) DM_SELECT(8);
+  else if (ne <= 16) DM_SELECT(16);
+  else DM_SELECT(32);
+#undef DM_SELECT
   return hipGetLastError();
 }
 
