@@ -198,15 +198,25 @@ void free_layer(Layer* Ly) {
 // activations); below it the lane-chain router is as fast.
 constexpr int kMfmaRouterMinTokens = 64;
 
+// norm_eps > 0: the block's input is RMSNorm(dx) (gamma = 1), computed inside
+// the fused decode kernel or by a separate kernel into ctx->xn.
 hipError_t run_block(dmh_ctx* ctx, Layer* Ly, int layer, const float* dx, const float* dres,
                      int T, float* dy, int32_t* dids, float* dprobs, float* dshg,
-                     bool allow_fused = true) {
+                     bool allow_fused = true, float norm_eps = 0.0f) {
   const LayerDev& L = Ly->dev;
   hipStream_t st = ctx->cur;
   unsigned long long* status = ctx->status + layer;
   const int ldh = L.I > L.Ish ? L.I : L.Ish;
   hipError_t e;
-  if (Ly->fused && allow_fused && T == 1) {
+  const bool fused = Ly->fused && allow_fused && T == 1;
+  if (norm_eps > 0.0f && !fused) {
+    if ((e = ctx->xn.ensure((size_t)T * L.H)) != hipSuccess) return e;
+    if ((e = dm::launch_rmsnorm_rows(dx, T, L.H, norm_eps, ctx->xn.p, nullptr, layer, st)) !=
+        hipSuccess)
+      return e;
+    dx = ctx->xn.p;
+  }
+  if (fused) {
     for (int t = 0; t < T; ++t) {
       if (Ly->launches >= (1u << 24) && (e = reset_counters(ctx, Ly)) != hipSuccess) return e;
       dm::DecodeSync S = dm::decode_sync_carve(L, Ly->sync);
@@ -214,7 +224,7 @@ hipError_t run_block(dmh_ctx* ctx, Layer* Ly, int layer, const float* dx, const 
       e = dm::launch_moe_decode(L, Ly->plan, dx + (size_t)t * L.H,
                                 dres ? dres + (size_t)t * L.H : nullptr, dy + (size_t)t * L.H,
                                 dids + (size_t)t * L.K, dprobs + (size_t)t * L.K, dshg + t, S,
-                                status, t, st);
+                                status, t, st, norm_eps);
       if (e != hipSuccess) return e;
     }
     return hipSuccess;
@@ -680,8 +690,7 @@ int dmh_moe_stack_forward(dmh_ctx* c, int first, int nl, float eps, const float*
     const int l = first + i;
     int32_t* dids = (own_ids ? c->ids.p : ids) + (size_t)i * TK;
     float* dprobs = (own_probs ? c->probs.p : probs) + (size_t)i * TK;
-    HIP_TRY(dm::launch_rmsnorm_rows(hA, T, H, eps, c->xn.p, nullptr, l, st));
-    HIP_TRY(run_block(c, c->layers[l], l, c->xn.p, hA, T, hB, dids, dprobs, c->shg.p));
+    HIP_TRY(run_block(c, c->layers[l], l, hA, hA, T, hB, dids, dprobs, c->shg.p, true, eps));
     c->last_ids[l] = dids;
     float* tmp = hA; hA = hB; hB = tmp;
   }

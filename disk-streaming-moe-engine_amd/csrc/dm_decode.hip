@@ -502,7 +502,8 @@ template <int GQW, int R>
 __global__ __launch_bounds__(kThreads) void k_moe_decode(
     LayerDev L, DecodePlan P, const float* __restrict__ x, const float* __restrict__ residual,
     float* __restrict__ y, int32_t* __restrict__ ids_out, float* __restrict__ probs_out,
-    float* __restrict__ shg_out, DecodeSync S, unsigned long long* status, int token) {
+    float* __restrict__ shg_out, DecodeSync S, unsigned long long* status, int token,
+    float norm_eps) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   float* xt = reinterpret_cast<float*>(smem + P.off_xt);
   uint4* xb2 = reinterpret_cast<uint4*>(smem + P.off_xb);
@@ -553,6 +554,46 @@ __global__ __launch_bounds__(kThreads) void k_moe_decode(
   const ExpertView sdv = {L.sd_nib, L.sd_sc, H, L.Ish};
   uint4 dw[kDownBatch];
   uint2 ds[kDownBatch];
+
+  // ---- optional RMSNorm of x with gamma = 1 (the layer-stack form): 256
+  // strided partial sums of squares, a halving tree, denominator
+  // sqrt(sum / H + eps), x / denominator; every workgroup computes it, while
+  // the weight loads above are in flight.  The B-block area holds the squares
+  // and the reduction area the partials until the staging below.
+  if (norm_eps > 0.0f) {
+    float* sq = reinterpret_cast<float*>(xb2);
+#pragma unroll
+    for (int ii = 0; ii < 2; ++ii) {
+      const int i = tid + kThreads * ii;
+      if (i < H / 8) {
+        const float4 a = xr[ii][0], c = xr[ii][1];
+        reinterpret_cast<float4*>(sq)[2 * i] = make_float4(a.x * a.x, a.y * a.y, a.z * a.z, a.w * a.w);
+        reinterpret_cast<float4*>(sq)[2 * i + 1] =
+            make_float4(c.x * c.x, c.y * c.y, c.z * c.z, c.w * c.w);
+      }
+    }
+    __syncthreads();
+    if (tid < 256) {
+      float a = 0.0f;
+      for (int k = tid; k < H; k += 256) a = a + sq[k];
+      red[tid] = a;
+    }
+#pragma unroll
+    for (int wd = 128; wd >= 1; wd >>= 1) {
+      __syncthreads();
+      if (tid < wd) red[tid] = red[tid] + red[tid + wd];
+    }
+    __syncthreads();
+    const float denom = __builtin_sqrtf(red[0] / (float)H + norm_eps);
+#pragma unroll
+    for (int ii = 0; ii < 2; ++ii) {
+      xr[ii][0] = make_float4(xr[ii][0].x / denom, xr[ii][0].y / denom, xr[ii][0].z / denom,
+                              xr[ii][0].w / denom);
+      xr[ii][1] = make_float4(xr[ii][1].x / denom, xr[ii][1].y / denom, xr[ii][1].z / denom,
+                              xr[ii][1].w / denom);
+    }
+    __syncthreads();  // the squares and partials are overwritten below
+  }
 
   // ---- stage x: transposed fp32 (router chains) and bf16 hi/lo B blocks -----
   {
@@ -866,7 +907,7 @@ hipError_t decode_occupancy(const LayerDev& L, const DecodePlan& P, int* blocks_
 hipError_t launch_moe_decode(const LayerDev& L, const DecodePlan& P, const float* x,
                              const float* residual, float* y, int32_t* ids, float* probs,
                              float* shg, const DecodeSync& S, unsigned long long* status, int token,
-                             hipStream_t st) {
+                             hipStream_t st, float norm_eps) {
   const void* fn = pick_kernel(L);
   if (!fn) return hipErrorInvalidValue;
   LayerDev Lc = L;
@@ -874,7 +915,7 @@ hipError_t launch_moe_decode(const LayerDev& L, const DecodePlan& P, const float
   DecodeSync Sc = S;
   const float* xc = x;
   const float* rc = residual;
-  void* args[] = {&Lc, &Pc, &xc, &rc, &y, &ids, &probs, &shg, &Sc, &status, &token};
+  void* args[] = {&Lc, &Pc, &xc, &rc, &y, &ids, &probs, &shg, &Sc, &status, &token, &norm_eps};
   return hipLaunchKernel(fn, dim3(P.grid), dim3(P.threads), args, P.lds_bytes, st);
 }
 
