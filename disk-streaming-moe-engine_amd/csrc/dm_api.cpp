@@ -676,10 +676,17 @@ int dmh_moe_stack_forward(dmh_ctx* c, int first, int nl, float eps, const float*
   hipStream_t st = c->cur;
   const size_t TH = (size_t)T * H, TK = (size_t)T * K;
   HIP_TRY(c->hstack.ensure(2 * TH));
-  HIP_TRY(c->xn.ensure(TH));
   float* hA = c->hstack.p;
   float* hB = c->hstack.p + TH;
-  HIP_TRY(hipMemcpyAsync(hA, x, TH * 4, dev ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice, st));
+  // device pointers: layer 0 reads x and the last layer writes out directly
+  // (unless they alias); host pointers: x goes through hA
+  const bool direct = dev && out != x;
+  const float* src = x;
+  if (!direct) {
+    HIP_TRY(hipMemcpyAsync(hA, x, TH * 4, dev ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice,
+                           st));
+    src = hA;
+  }
   const bool own_ids = !(dev && ids), own_probs = !(dev && probs);
   if (own_ids) HIP_TRY(c->ids.ensure(TK * nl));
   if (own_probs) HIP_TRY(c->probs.ensure(TK * nl));
@@ -690,12 +697,14 @@ int dmh_moe_stack_forward(dmh_ctx* c, int first, int nl, float eps, const float*
     const int l = first + i;
     int32_t* dids = (own_ids ? c->ids.p : ids) + (size_t)i * TK;
     float* dprobs = (own_probs ? c->probs.p : probs) + (size_t)i * TK;
-    HIP_TRY(run_block(c, c->layers[l], l, hA, hA, T, hB, dids, dprobs, c->shg.p, true, eps));
+    float* dst = (direct && i == nl - 1) ? out : (src == hA ? hB : hA);
+    HIP_TRY(run_block(c, c->layers[l], l, src, src, T, dst, dids, dprobs, c->shg.p, true, eps));
     c->last_ids[l] = dids;
-    float* tmp = hA; hA = hB; hB = tmp;
+    src = dst;
   }
-  HIP_TRY(hipMemcpyAsync(out, hA, TH * 4, dev ? hipMemcpyDeviceToDevice : hipMemcpyDeviceToHost,
-                         st));
+  if (src != out)
+    HIP_TRY(hipMemcpyAsync(out, src, TH * 4,
+                           dev ? hipMemcpyDeviceToDevice : hipMemcpyDeviceToHost, st));
   if (dev) return DMH_OK;
   std::vector<int32_t> hids(TK * nl);
   std::vector<unsigned long long> keys(nl);

@@ -140,6 +140,14 @@ def test_device_generated_layers_stack_decode(block, oracle):
     assert np.array_equal(probs[0].view(np.uint32), po[0].view(np.uint32))
     err, rms, ok = tol_check(out - x, oo - x)
     assert ok, (err, rms)
+    # the device-pointer form (layer 0 reads x, the last layer writes out) gives
+    # the same bits
+    xd = torch.from_numpy(x).to("cuda")
+    od = torch.empty_like(xd)
+    torch.cuda.synchronize()
+    block.forward_stack_device(xd.data_ptr(), 20, 2, 1, od.data_ptr(), eps=1e-6)
+    block.sync()
+    assert np.array_equal(od.cpu().numpy().view(np.uint32), out.view(np.uint32))
     block.free_layer(20)
     block.free_layer(21)
 
