@@ -15,7 +15,7 @@ DMH_F_DEVICE = 0x1
 
 ERROR_NAMES = {
     1: "INVALID_ARG", 2: "CONFIG", 3: "HIP", 4: "NO_MEMORY", 5: "DEQUANT", 6: "ACT",
-    7: "WEIGHT", 8: "ROUTER", 9: "EXPERT", 10: "SWIGLU", 11: "GATE", 12: "NORM",
+    7: "WEIGHT", 8: "ROUTER", 9: "EXPERT", 10: "SWIGLU", 11: "GATE", 12: "NORM", 13: "FORMAT",
 }
 
 # every symbol include/dismoen_hip.h declares
@@ -23,6 +23,10 @@ EXPORTS = (
     "dmh_version", "dmh_create", "dmh_destroy", "dmh_set_stream", "dmh_get_stream", "dmh_sync",
     "dmh_upload_moe_layer", "dmh_free_layer", "dmh_layer_bytes", "dmh_moe_forward",
     "dmh_moe_stack_forward", "dmh_router_forward", "dmh_dequant_q4_bf16",
+    "dmh_quant_open", "dmh_quant_close", "dmh_quant_num_tensors", "dmh_quant_find",
+    "dmh_quant_tensor_info", "dmh_quant_read", "dmh_st_open", "dmh_st_close",
+    "dmh_st_num_tensors", "dmh_st_find", "dmh_st_tensor_info", "dmh_st_read",
+    "dmh_upload_moe_layer_files",
 )
 
 
@@ -36,6 +40,13 @@ class DmhWeights(C.Structure):
     _fields_ = [(n, C.c_void_p) for n in (
         "router_bf16", "shgate_bf16", "gu_scales", "gu_packed", "d_scales", "d_packed",
         "sh_gu_scales", "sh_gu_packed", "sh_d_scales", "sh_d_packed")]
+
+
+class DmhTensorInfo(C.Structure):
+    _fields_ = [("name", C.c_char_p), ("dtype", C.c_char_p), ("ndim", C.c_int32),
+                ("shape", C.c_int64 * 8), ("group_size", C.c_int32), ("num_groups", C.c_int64),
+                ("scales_offset", C.c_int64), ("scales_bytes", C.c_int64),
+                ("data_offset", C.c_int64), ("data_bytes", C.c_int64)]
 
 
 class DismoenError(RuntimeError):
@@ -75,6 +86,17 @@ def lib():
     L.dmh_router_forward.argtypes = [vp, vp, vp, i32, i32, i32, i32, i32, i32, vp, vp, u32,
                                      C.c_char_p, sz]
     L.dmh_dequant_q4_bf16.argtypes = [vp, vp, i64, vp, i64, i64, i32, vp, u32, C.c_char_p, sz]
+    for pre in ("dmh_quant", "dmh_st"):
+        getattr(L, pre + "_open").argtypes = [C.c_char_p, C.POINTER(vp), C.c_char_p, sz]
+        getattr(L, pre + "_close").argtypes = [vp]
+        getattr(L, pre + "_close").restype = None
+        getattr(L, pre + "_num_tensors").argtypes = [vp]
+        getattr(L, pre + "_find").argtypes = [vp, C.c_char_p]
+        getattr(L, pre + "_tensor_info").argtypes = [vp, i32, C.POINTER(DmhTensorInfo)]
+    L.dmh_quant_read.argtypes = [vp, i32, vp, i64, vp, i64, C.c_char_p, sz]
+    L.dmh_st_read.argtypes = [vp, i32, vp, i64, C.c_char_p, sz]
+    L.dmh_upload_moe_layer_files.argtypes = [vp, i32, C.POINTER(DmhDims), vp, vp, i32, C.c_char_p,
+                                             sz]
     _lib = L
     return L
 

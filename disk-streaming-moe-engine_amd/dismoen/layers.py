@@ -144,6 +144,17 @@ class MoEBlock:
                                              DMH_F_DEVICE, e, len(e)), e)
         self.dims[layer_idx] = dims
 
+    def upload_layer_files(self, layer_idx: int, dims: tuple, quant, shard,
+                           model_layer: int = 0) -> None:
+        """Upload model layer model_layer from a quant model and a safetensors
+        shard (dismoen.formats.QuantModelIndex / SafetensorsShard)."""
+        H, E, K, I, Ish = dims
+        d = DmhDims(H, E, K, I, Ish, 32, 0)
+        e = errbuf()
+        check(self._lib.dmh_upload_moe_layer_files(self._h, layer_idx, C.byref(d), quant.handle,
+                                                   shard.handle, model_layer, e, len(e)), e)
+        self.dims[layer_idx] = dims
+
     def free_layer(self, layer_idx: int) -> None:
         self._lib.dmh_free_layer(self._h, layer_idx)
         self.dims.pop(layer_idx, None)

@@ -44,6 +44,7 @@ enum {
   DMH_ERR_SWIGLU = 10,      /* SWIGLU_ERROR */
   DMH_ERR_GATE = 11,        /* GATE_ERROR */
   DMH_ERR_NORM = 12,        /* NORM_ERROR */
+  DMH_ERR_FORMAT = 13,      /* a weight file fails its format checks */
 };
 
 #define DMH_F_DEVICE 0x1u   /* pointers are device memory; stream-ordered, no sync */
@@ -158,6 +159,66 @@ int dmh_dequant_q4_bf16(dmh_ctx* ctx, const uint16_t* scales, int64_t n_scales,
                         const uint8_t* packed, int64_t n_packed, int64_t num_elements,
                         int group_size, uint16_t* out, unsigned flags, char* err,
                         size_t errlen);
+
+/* ---- weight files ---------------------------------------------------------
+ * Readers of the reference's weight files on the host (no GPU needed), and
+ * the upload of one layer straight from them.  They replace, for this block,
+ * the per-use pread + dequant of src/layers/quant_loader.mojo and the
+ * router's safetensors load (src/layers/router.mojo:213-257). */
+typedef struct dmh_quant_file dmh_quant_file;
+typedef struct dmh_st_file dmh_st_file;
+
+/* One tensor of a weight file; name and dtype stay valid while the file
+ * handle is open.  Offsets are absolute file offsets. */
+typedef struct {
+  const char* name;
+  const char* dtype;        /* safetensors dtype, or the quant meta's "dtype" */
+  int32_t ndim;
+  int64_t shape[8];
+  int32_t group_size;       /* quant files */
+  int64_t num_groups;       /* quant files */
+  int64_t scales_offset;    /* quant files: fp16 LE group scales */
+  int64_t scales_bytes;
+  int64_t data_offset;      /* quant: packed codes; safetensors: the payload */
+  int64_t data_bytes;
+} dmh_tensor_info;
+
+/* scan_quant_file (src/format/quant_reader.mojo:487-662): header, every
+ * record and the SEC-4 checks; on failure err receives the reference's text
+ * ("scan_quant_file: ...") and DMH_ERR_FORMAT is returned. */
+int dmh_quant_open(const char* path, dmh_quant_file** out, char* err, size_t errlen);
+void dmh_quant_close(dmh_quant_file* f);
+int dmh_quant_num_tensors(const dmh_quant_file* f);
+/* QuantModelIndex.tensor_map lookup (quant_reader.mojo:631): index, or -1. */
+int dmh_quant_find(const dmh_quant_file* f, const char* name);
+int dmh_quant_tensor_info(const dmh_quant_file* f, int idx, dmh_tensor_info* info);
+/* pread_tensor_quant (quant_reader.mojo:665-692): fp16 scale bits
+ * [num_groups] and packed codes [data_bytes]. */
+int dmh_quant_read(const dmh_quant_file* f, int idx, uint16_t* scales, int64_t n_scales,
+                   uint8_t* packed, int64_t n_packed, char* err, size_t errlen);
+
+/* read_header (src/format/reader.mojo:21-297): safetensors header parse and
+ * the F15 checks (dtype, offsets, layout, no holes or overlap); errors are
+ * the reference's {"error_type","detail","shard","tensor_name"} objects. */
+int dmh_st_open(const char* path, dmh_st_file** out, char* err, size_t errlen);
+void dmh_st_close(dmh_st_file* f);
+int dmh_st_num_tensors(const dmh_st_file* f);
+int dmh_st_find(const dmh_st_file* f, const char* name);
+int dmh_st_tensor_info(const dmh_st_file* f, int idx, dmh_tensor_info* info);
+/* The payload bytes of tensor idx; bytes must equal its size. */
+int dmh_st_read(const dmh_st_file* f, int idx, void* out, int64_t bytes, char* err,
+                size_t errlen);
+
+/* dmh_upload_moe_layer from the files of model layer model_layer: routed
+ * experts model.layers.{l}.mlp.experts.{e}.{gate,up,down}_proj.weight and
+ * model.layers.{l}.mlp.shared_expert.{gate,up,down}_proj.weight from the
+ * quant model (src/layers/quant_loader.mojo:89-136); the router mlp.gate.weight
+ * (language-model prefix first, src/layers/router.mojo:234-247) and
+ * mlp.shared_expert_gate.weight as BF16 from the safetensors shard, the
+ * shared gate falling back to the quant model's 4-bit tensor. */
+int dmh_upload_moe_layer_files(dmh_ctx* ctx, int layer, const dmh_moe_dims* dims,
+                               const dmh_quant_file* quant, const dmh_st_file* shard,
+                               int model_layer, char* err, size_t errlen);
 
 #ifdef __cplusplus
 }

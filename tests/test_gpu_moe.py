@@ -188,3 +188,42 @@ def test_routing_near_ties_at_topk_boundary(block, oracle, gap_ulp):
     assert np.array_equal(probs.view(np.uint32), po.view(np.uint32))
     err, rms, ok = tol_check(y, yo)
     assert ok, (err, rms)
+
+
+@pytest.mark.parametrize("cfg", ["toy", "qwen"])
+def test_upload_from_reference_files(block, tmp_path, cfg):
+    """A layer written as the reference's quant model + safetensors shard and
+    uploaded from them computes the same bits as the same layer uploaded from
+    arrays (single token and a batch)."""
+    from dismoen import formats
+    c = synth.CONFIG_TOY if cfg == "toy" else synth.CONFIG_QWEN36
+    L = synth.make_layer(**c, seed=41)
+    qp, sp = str(tmp_path / "m.quant"), str(tmp_path / "m.safetensors")
+    formats.write_layer_files(qp, sp, L, model_layer=7)
+    dims = (c["hidden"], c["num_experts"], c["top_k"], c["inter"], c["inter_sh"])
+    with formats.scan_quant_file(qp) as q, formats.read_header(sp) as s:
+        block.upload_layer_files(30, dims, q, s, model_layer=7)
+    block.upload_layer(31, L)
+    x = synth.make_activations(np.random.default_rng(109), (3, c["hidden"]))
+    for T in (1, 3):
+        a = block.forward_arrays(30, x[:T], T)
+        b = block.forward_arrays(31, x[:T], T)
+        for u, v in zip(a, b):
+            assert np.array_equal(np.asarray(u).view(np.uint8), np.asarray(v).view(np.uint8))
+    block.free_layer(30)
+    block.free_layer(31)
+
+
+def test_upload_from_files_missing_expert(block, tmp_path):
+    from dismoen import DismoenError, formats
+    c = synth.CONFIG_TOY
+    L = synth.make_layer(**c, seed=42)
+    qp, sp = str(tmp_path / "m.quant"), str(tmp_path / "m.safetensors")
+    formats.write_layer_files(qp, sp, L, model_layer=0)
+    dims = (c["hidden"], c["num_experts"], c["top_k"], c["inter"], c["inter_sh"])
+    with formats.scan_quant_file(qp) as q, formats.read_header(sp) as s:
+        with pytest.raises(DismoenError) as ei:
+            block.upload_layer_files(32, dims, q, s, model_layer=1)
+    assert str(ei.value) == ('{"error_type":"WEIGHT_LOAD_FAILED","detail":"required router gate'
+                             ' tensor not in weight_map: model.layers.1.mlp.gate.weight",'
+                             '"shard":"","tensor_name":"model.layers.1.mlp.gate.weight"}')
