@@ -13,11 +13,11 @@
 //   P1     router rows (4 per router workgroup, the exact 16-lane order of
 //          router_project) -> z;  shared-expert gate/up tile -> h[K].
 //   P2     every workgroup polls z and selects the top-k itself on wave 0
-//          (identical everywhere, so no broadcast hand-off) while wave 1
+//          (identical everywhere, so no broadcast hand-off) while wave 7
 //          forms the softmax normaliser and the shared gate.
-//   P3     routed gate/up and down loads; wave 1 forms the probabilities
-//          while they are in flight; routed gate/up tile (slot, 16 rows) ->
-//          h[k], published with its bf16 hi/lo split.
+//   P3     routed gate/up and down loads; routed gate/up tile (slot, 16
+//          rows) -> h[k], published with its bf16 hi/lo split; then wave 7
+//          forms the probabilities (in workgroups with a down tile).
 //   P4     down tile (16 output rows, all K+1 slots): poll h, dequantize the
 //          down chunks meanwhile, MFMA per chunk scaled by its slot's weight
 //          (p_k, or the shared gate), residual, y.
@@ -47,7 +47,7 @@ constexpr int kRouterRows = 4;       // router rows per router workgroup (wave 0
 constexpr int kRwMax = 16;           // router chain chunks (8 bf16 each) held per lane
 constexpr int kDownBatch = 5;        // down chunks per wave held in registers
 constexpr int kHw = 10;              // h words per thread (all polled at once)
-constexpr int kNormWave = 1;          // forms the softmax normaliser during routing
+constexpr int kNormWave = 7;          // softmax normaliser during routing; probabilities after the gate/up tile
 
 // LDS state of the routing decision.
 struct SelState {
@@ -670,26 +670,31 @@ __global__ __launch_bounds__(kThreads) void k_moe_decode(
   uint4 gwg[GQW], gwu[GQW];
   uint2 gsg[GQW], gsu[GQW];
   ExpertView gv, uv;
-  if (b < K * nrb) {
-    gu_views(b, gv, uv);
-    gu_load<GQW, true>(gv, uv, b % nrb, gwg, gwu, gsg, gsu);
-  }
-  // down chunks of this workgroup's output tile (routed: non-temporal;
-  // shared: cached), unconditional with clamped indices
-  if (down_wg) {
+  // every address first, then all loads of the phase back to back: with
+  // address arithmetic between them the compiler waited for the gate/up
+  // loads before issuing the down loads
+  ExpertView dv[kDownBatch];
+  int dgq[kDownBatch];
 #pragma unroll
-    for (int i = 0; i < kDownBatch; ++i) {
-      const int c = min(w + kWaves * i, nch - 1);
-      const bool routed = c < nch_r;
-      const ExpertView v = routed ? down_view(c / nGQI) : sdv;
-      load_chunk_nt(v, b, routed ? c % nGQI : c - nch_r, lane, dw[i], ds[i]);
-    }
+  for (int i = 0; i < kDownBatch; ++i) {
+    const int c = min(w + kWaves * i, nch - 1);
+    const bool routed = c < nch_r;
+    dv[i] = routed ? down_view(c / nGQI) : sdv;
+    dgq[i] = routed ? c % nGQI : c - nch_r;
   }
-  // the probabilities while this wave's loads are in flight (published by
-  // the first barrier of the gate/up tile, or by the barrier below)
-  if (w == kNormWave)
-    finish_probs(E, K, st, red + kWaves * 32, b == 0, token, status, b == 0 ? ids_out : nullptr,
-                 probs_out, shg_out);
+  // (a workgroup past the routed tiles loads the last tile and ignores it)
+  const int t0 = min(b, K * nrb - 1);
+  gu_views(t0, gv, uv);
+  gu_load<GQW, true>(gv, uv, t0 % nrb, gwg, gwu, gsg, gsu);
+  // down chunks of this workgroup's output tile (routed: non-temporal;
+  // shared: cached).  Unconditional: loads under a branch left their
+  // registers to be copied at the join, which waited for every load in
+  // flight.  Workgroups without an output tile all read the first chunk of
+  // the shared down matrix (one cached line set) and ignore it.
+#pragma unroll
+  for (int i = 0; i < kDownBatch; ++i)
+    load_chunk_nt(down_wg ? dv[i] : sdv, down_wg ? b : 0, down_wg ? dgq[i] : 0, lane, dw[i],
+                  ds[i]);
   for (int t = b; t < K * nrb; t += nb) {
     if (t != b) {
       gu_views(t, gv, uv);
@@ -701,6 +706,13 @@ __global__ __launch_bounds__(kThreads) void k_moe_decode(
   }
   if (K * nrb <= b) __syncthreads();
   if (!down_wg) return;
+  // the probabilities, needed from the combine on (published by the barrier
+  // that ends the h staging below): done after the gate/up tile so that the
+  // tile's h is published without waiting for it, by a wave with one down
+  // chunk fewer than the others
+  if (w == kNormWave)
+    finish_probs(E, K, st, red + kWaves * 32, b == 0, token, status, b == 0 ? ids_out : nullptr,
+                 probs_out, shg_out);
 
   // ---- P4: down projection of this workgroup's 16 output rows ---------------
   // Issue the first poll of h (thread t reads words t, t + 512, ...), then
