@@ -16,10 +16,10 @@
 //          (identical everywhere, so no broadcast hand-off) while wave 7
 //          forms the softmax normaliser and the shared gate.
 //   P3     routed gate/up and down loads; routed gate/up tile (slot, 16
-//          rows) -> h[k], published with its bf16 hi/lo split; then wave 7
-//          forms the probabilities (in workgroups with a down tile).
+//          rows) -> h[k], published with its bf16 hi/lo split.
 //   P4     down tile (16 output rows, all K+1 slots): poll h, dequantize the
-//          down chunks meanwhile, MFMA per chunk scaled by its slot's weight
+//          down chunks and (wave 7) form the probabilities meanwhile, MFMA
+//          per chunk scaled by its slot's weight
 //          (p_k, or the shared gate), residual, y.
 //
 // Hand-offs are 64-bit (launch tag, value) words: the consumer polls the data
@@ -46,7 +46,7 @@ constexpr int kWaves = kThreads / 64;
 constexpr int kRouterRows = 4;       // router rows per router workgroup (wave 0)
 constexpr int kRwMax = 16;           // router chain chunks (8 bf16 each) held per lane
 constexpr int kDownBatch = 5;        // down chunks per wave held in registers
-constexpr int kHw = 10;              // h words per thread (all polled at once)
+constexpr int kHw = 5;               // h words per thread (all polled at once)
 constexpr int kNormWave = 7;          // softmax normaliser during routing; probabilities after the gate/up tile
 
 // LDS state of the routing decision.
@@ -57,6 +57,7 @@ struct SelState {
   int* rank;    // [32] position of each slot in the (p desc, id asc) order
   float* pw;    // [33] B-operand weight of slot s: p_s; slot K: the shared gate
   float* misc;  // [0] shared gate, [2] ok flag, [3] 1/S
+  float* scr;   // [64] p by slot, then p by rank (16-byte aligned)
 };
 
 // The wave index as a uniform (scalar) value: derived from threadIdx the
@@ -66,19 +67,17 @@ __device__ __forceinline__ int wave_id() {
 }
 
 // B operand of a 16x16x32 MFMA from split blocks blk2[2*b + {hi, lo}]:
-// lane (q, j) holds rows 8q..8q+7 of column j; columns 0/1 carry hi/lo, the
-// others are zero.
+// lane (q, j) holds rows 8q..8q+7 of column j; columns 0/1 carry hi/lo.  The
+// other columns repeat them: column j of the product depends on column j of
+// B only, and only columns 0 and 1 are ever read (fold_cols, then j == 0),
+// so they need no zeroing.
 __device__ __forceinline__ bf16x8 ld_b(const uint4* blk2, int blk, int j) {
-  uint4 v = blk2[2 * blk + (j & 1)];
-  if (j >= 2) v = make_uint4(0, 0, 0, 0);
-  return __builtin_bit_cast(bf16x8, v);
+  return __builtin_bit_cast(bf16x8, blk2[2 * blk + (j & 1)]);
 }
 
 // The same operand from separate bf16 arrays hi[] / lo[] (8 values per block).
 __device__ __forceinline__ bf16x8 ld_b2(const uint16_t* hi, const uint16_t* lo, int blk, int j) {
-  uint4 v = *reinterpret_cast<const uint4*>((j & 1 ? lo : hi) + 8 * blk);
-  if (j >= 2) v = make_uint4(0, 0, 0, 0);
-  return __builtin_bit_cast(bf16x8, v);
+  return __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>((j & 1 ? lo : hi) + 8 * blk));
 }
 
 // fp32 -> bf16 hi + bf16 lo (v ~= hi + lo within 2^-17 relative).
@@ -88,11 +87,27 @@ __device__ __forceinline__ void split1(float v, uint16_t& hi, uint16_t& lo) {
   lo = (uint16_t)(pack_bf16x2(v - u2f(h << 16), 0.0f) & 0xFFFFu);
 }
 
+// h hand-off word: two values (rows 2i and 2i+1 of a slot) and the low 16
+// bits of the launch tag, (tag16 << 48) | (v1 << 24) | v0, each value the top
+// 24 bits of its float encoding rounded to nearest (16 significant bits, the
+// precision of the bf16 hi + lo pair the down tile's MFMA operand is formed
+// from).  Half the words of a one-value-per-word hand-off, so each poll of h
+// moves half the bytes.
+__device__ __forceinline__ uint32_t h24(float v) { return (f2u(v) + 0x80u) >> 8; }
+__device__ __forceinline__ uint64_t pack_h2(unsigned tag, float v0, float v1) {
+  return ((uint64_t)(tag & 0xFFFFu) << 48) | ((uint64_t)h24(v1) << 24) | h24(v0);
+}
+__device__ __forceinline__ bool h2_current(uint64_t wd, unsigned tag) {
+  return (uint32_t)(wd >> 48) == (tag & 0xFFFFu);
+}
+__device__ __forceinline__ float h2_v0(uint64_t wd) { return u2f((uint32_t)wd << 8); }
+__device__ __forceinline__ float h2_v1(uint64_t wd) { return u2f((uint32_t)(wd >> 24) << 8); }
+
 // ---------------------------------------------------------------------------
 // Gate/up of one 16-row tile: h = SiLU(W_g x) * (W_u x) for rows 16rb..+15,
 // reduced over all H columns inside the workgroup (wave w owns the 128-column
 // chunks w, w+8, ...).  gu_load issues the loads; gu_compute consumes them and
-// stores the 16 h values as (tag, bf16 hi | bf16 lo << 16) words to hdst[row].
+// stores the 16 h values as 8 pack_h2 words to hdst[row / 2].
 template <int GQW, bool NT>
 __device__ __forceinline__ void gu_load(const ExpertView& gv, const ExpertView& uv, int rb,
                                         uint4 (&wg)[GQW], uint4 (&wu)[GQW], uint2 (&sg)[GQW],
@@ -165,10 +180,11 @@ __device__ __forceinline__ void gu_compute(const ExpertView& gv, int rb, const u
       else
         record_err(status, err_key(kPhExpert, token, 0, 0, kEkRecheck));
     }
-    // published as (tag, bf16 hi | bf16 lo << 16): the consumer's MFMA operand
-    uint16_t hh, hl;
-    split1(h, hh, hl);
-    st_coh_u64(hdst + row, ((uint64_t)tag << 32) | ((uint32_t)hl << 16) | hh);
+    // published in pairs of rows (2i, 2i+1) as one word (hand-off format
+    // of pack_h2); the partner's value comes from the neighbouring lane
+    const float hn = __builtin_bit_cast(
+        float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, h), 0xB1, 0xF, 0xF, true));
+    if ((r & 1) == 0) st_coh_u64(hdst + (row >> 1), pack_h2(tag, h, hn));
   }
   __syncthreads();
 }
@@ -395,13 +411,13 @@ __device__ __forceinline__ bool route(const uint64_t* zt, unsigned tag, int E, i
   return ok;
 }
 
-// The softmax normaliser on another wave while wave 0 selects: max, e =
-// exp(z - max) (zero-padded to 256R entries) and S summed sequentially in
-// expert order (src/layers/router.mojo:140-183), 1/S to misc[3]; and the
-// shared-expert gate to misc[0].
+// The softmax numerators on another wave while wave 0 selects: max, e =
+// exp(z - max) (zero-padded to 256R entries) to ev[] (src/layers/router.mojo:
+// 140-183), and the shared-expert gate to misc[0].  Their sum is formed later
+// (softmax_sum), off the routing path.
 template <int R>
-__device__ __forceinline__ void softmax_norm(const uint64_t* zt, unsigned tag, int E, SelState& st,
-                                             bool record, int token, unsigned long long* status) {
+__device__ __forceinline__ void softmax_exp(const uint64_t* zt, unsigned tag, int E, SelState& st,
+                                            bool record, int token, unsigned long long* status) {
   constexpr int NK = 4 * R;
   const int lane = threadIdx.x & 63;
   float z[NK];
@@ -425,13 +441,7 @@ __device__ __forceinline__ void softmax_norm(const uint64_t* zt, unsigned tag, i
     }
     st.ev[e] = ev;
   }
-  wait_lds();
-  __builtin_amdgcn_wave_barrier();
   if (lane == 0) {
-    const float s = seq_sum(st.ev, 256 * R);
-    if (record && (!(s > 0.0f) || !finite_f(s)))
-      record_err(status, err_key(kPhSoftmax, token, 0, 1 + E, 0));
-    st.misc[3] = 1.0f / s;
     // the shared-expert gate sigmoid(z_E) (src/layers/moe.mojo:70-100)
     if (record && !finite_f(gl)) record_err(status, err_key(kPhGate, token, 0, 0, kGkLogit));
     const float sg = dm_sigmoid(gl);
@@ -441,39 +451,61 @@ __device__ __forceinline__ void softmax_norm(const uint64_t* zt, unsigned tag, i
   }
 }
 
+// S = sum of ev[] in expert order (sequential, as src/layers/router.mojo:
+// 140-183 sums it) on every lane of one wave, 1/S to misc[3], and the slot
+// weights of the down tile: pw[k] = e_(ids[k]) / S (the routed probability
+// p_k) and pw[K] = the shared gate.  Published by the caller's next barrier.
+template <int R>
+__device__ __forceinline__ void softmax_sum(int E, int K, SelState& st, bool record, int token,
+                                            unsigned long long* status) {
+  const int lane = threadIdx.x & 63;
+  const float s = seq_sum(st.ev, 256 * R);
+  const float inv = 1.0f / s;
+  if (lane < K) st.pw[lane] = st.ev[st.ids[lane]] * inv;
+  if (lane == 0) {
+    if (record && (!(s > 0.0f) || !finite_f(s)))
+      record_err(status, err_key(kPhSoftmax, token, 0, 1 + E, 0));
+    st.misc[3] = inv;
+    st.pw[K] = st.misc[0];
+  }
+}
+
 // After routing, on one wave: the K probabilities p_k = e_k * (1/S), their
 // (p desc, id asc) order and the checks of src/layers/topk.mojo:109-128.
-// Lane k < K owns slot k; it reads every slot's (p, id) from LDS and counts
-// the slots ahead of it, which is its rank.  Writes the slot weights pw[]
-// (p_k; the shared gate for slot K) and ranks; `outputs` also writes ids /
-// probs / shared gate in the reference's order.
-__device__ __forceinline__ void finish_probs(int E, int K, SelState& st, float* scr, bool record,
-                                             int token, unsigned long long* status,
-                                             int32_t* ids_out, float* probs_out,
-                                             float* shg_out) {
+// Lane k < K owns slot k and counts the slots ahead of it, which is its
+// rank; the top-k sum is then formed in rank order.  Writes the ranks;
+// `outputs` also writes ids / probs / shared gate in the reference's order.
+// Runs in one workgroup after the gate/up tile.  Every slot's (p, id)
+// is read as broadcast LDS vectors, all reads before the compares: a round
+// trip per slot, or cross-lane reads into scalar registers, made this wave
+// the last to reach the down tile's barrier.
+__device__ __forceinline__ void finish_probs(int E, int K, SelState& st, bool record, int token,
+                                             unsigned long long* status, int32_t* ids_out,
+                                             float* probs_out, float* shg_out) {
   const int lane = threadIdx.x & 63;
   const float inv = st.misc[3];
   const int idk = lane < K ? st.ids[lane] : 0;
   const float pk = lane < K ? st.ev[idk] * inv : 0.0f;
-  float* ps = scr;       // [32] p by slot
-  int* is = reinterpret_cast<int*>(scr + 32);  // [32] id by slot
-  float* sorted = scr + 64;                    // [32] p by rank
-  if (lane < K) {
-    ps[lane] = pk;
-    is[lane] = idk;
-  }
+  float* ps = st.scr;           // [32] p by slot
+  float* sorted = st.scr + 32;  // [32] p by rank
+  if (lane < K) ps[lane] = pk;
   wait_lds();
   __builtin_amdgcn_wave_barrier();
   int rank = 0;
-  for (int j2 = 0; j2 < K; ++j2) {  // broadcast reads, independent compares
-    const float pj = ps[j2];
-    const int idj = is[j2];
-    rank += (pj > pk || (pj == pk && idj < idk)) ? 1 : 0;
+  for (int jb = 0; jb < K; jb += 8) {  // K <= 32; entries past K are masked
+    const float4 pa = *reinterpret_cast<const float4*>(ps + jb);
+    const float4 pb = *reinterpret_cast<const float4*>(ps + jb + 4);
+    const int4 ia = *reinterpret_cast<const int4*>(st.ids + jb);
+    const int4 ib = *reinterpret_cast<const int4*>(st.ids + jb + 4);
+    const float pj[8] = {pa.x, pa.y, pa.z, pa.w, pb.x, pb.y, pb.z, pb.w};
+    const int ij[8] = {ia.x, ia.y, ia.z, ia.w, ib.x, ib.y, ib.z, ib.w};
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      rank += (jb + u < K && (pj[u] > pk || (pj[u] == pk && ij[u] < idk))) ? 1 : 0;
   }
   if (lane < K) {
     sorted[rank] = pk;
     st.rank[lane] = rank;
-    st.pw[lane] = pk;
     if (ids_out) {
       ids_out[rank] = idk;
       probs_out[rank] = pk;
@@ -483,8 +515,14 @@ __device__ __forceinline__ void finish_probs(int E, int K, SelState& st, float* 
   __builtin_amdgcn_wave_barrier();
   if (lane == 0) {
     float sum_topk = 0.0f;  // in the reference's order
-    for (int r = 0; r < K; ++r) sum_topk = sum_topk + sorted[r];
-    st.pw[K] = st.misc[0];
+    for (int jb = 0; jb < K; jb += 8) {
+      const float4 sa = *reinterpret_cast<const float4*>(sorted + jb);
+      const float4 sb = *reinterpret_cast<const float4*>(sorted + jb + 4);
+      const float sv[8] = {sa.x, sa.y, sa.z, sa.w, sb.x, sb.y, sb.z, sb.w};
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        if (jb + u < K) sum_topk = sum_topk + sv[u];
+    }
     if (ids_out) shg_out[0] = st.misc[0];
     if (record) {
       if (sum_topk > 1.00001f) record_err(status, err_key(kPhTopk, token, 0, 0, kTkSum));
@@ -512,7 +550,8 @@ __global__ __launch_bounds__(kThreads) void k_moe_decode(
   unsigned char* sel = smem + P.off_sel;
   SelState st{reinterpret_cast<float*>(smem + P.off_zv), reinterpret_cast<float*>(smem + P.off_ev),
               reinterpret_cast<int*>(sel), reinterpret_cast<int*>(sel + 128),
-              reinterpret_cast<float*>(sel + 256), reinterpret_cast<float*>(sel + 400)};
+              reinterpret_cast<float*>(sel + 256), reinterpret_cast<float*>(sel + 400),
+              reinterpret_cast<float*>(sel + 512)};
 
   const int H = L.H, K = L.K, E = L.E;
   const int b = blockIdx.x, nb = gridDim.x;
@@ -640,22 +679,22 @@ __global__ __launch_bounds__(kThreads) void k_moe_decode(
   }
   for (int t = sh_tile; t < nsh; t += nb) {
     if (t != sh_tile) gu_load<GQW, false>(sgv, suv, t, swg, swu, ssg, ssu);
-    gu_compute<GQW>(sgv, t, swg, swu, ssg, ssu, xb2, red, S.ht + ((size_t)K << P.ldh_log2), n,
-                    kPhShared, token, status);
+    gu_compute<GQW>(sgv, t, swg, swu, ssg, ssu, xb2, red,
+                    S.ht + ((size_t)K << (P.ldh_log2 - 1)), n, kPhShared, token, status);
   }
 
-  // ---- P2: routing on wave 0, softmax normaliser on wave 1 (every workgroup
-  // computes the same result, so there is no broadcast hand-off) -------------
+  // ---- P2: routing on wave 0, softmax numerators on wave 7 (every
+  // workgroup computes the same result, so there is no broadcast hand-off) --
   if (w == 0) {
     const bool rok = route<R>(S.zt, n, E, K, st, b == 0, token, status);
     if (lane == 0) st.misc[2] = rok ? 1.0f : 0.0f;
   } else if (w == kNormWave) {
-    softmax_norm<R>(S.zt, n, E, st, b == 0, token, status);
+    softmax_exp<R>(S.zt, n, E, st, b == 0, token, status);
   }
   __syncthreads();
   const bool ok = st.misc[2] != 0.0f;
 
-  // ---- P3: routed loads; probabilities; routed gate/up tile -----------------
+  // ---- P3: routed loads; softmax sum and slot weights; routed gate/up tile --
   const size_t matI = (size_t)L.I * H;
   auto gu_views = [&](int t, ExpertView& gv, ExpertView& uv) {
     const int e = __builtin_amdgcn_readfirstlane(st.ids[t / nrb]);
@@ -674,23 +713,31 @@ __global__ __launch_bounds__(kThreads) void k_moe_decode(
   // address arithmetic between them the compiler waited for the gate/up
   // loads before issuing the down loads
   ExpertView dv[kDownBatch];
-  int dgq[kDownBatch];
+  int dgq[kDownBatch], dsl[kDownBatch];  // chunk within its slot; the slot (K: shared)
 #pragma unroll
   for (int i = 0; i < kDownBatch; ++i) {
     const int c = min(w + kWaves * i, nch - 1);
     const bool routed = c < nch_r;
     dv[i] = routed ? down_view(c / nGQI) : sdv;
     dgq[i] = routed ? c % nGQI : c - nch_r;
+    dsl[i] = routed ? c / nGQI : K;
   }
   // (a workgroup past the routed tiles loads the last tile and ignores it)
   const int t0 = min(b, K * nrb - 1);
   gu_views(t0, gv, uv);
   gu_load<GQW, true>(gv, uv, t0 % nrb, gwg, gwu, gsg, gsu);
-  // down chunks of this workgroup's output tile (routed: non-temporal;
-  // shared: cached).  Unconditional: loads under a branch left their
-  // registers to be copied at the join, which waited for every load in
-  // flight.  Workgroups without an output tile all read the first chunk of
-  // the shared down matrix (one cached line set) and ignore it.
+  // the softmax sum and the slot weights while the loads are in flight
+  // (published by the first barrier of the gate/up tile, or the one below)
+  if (w == kNormWave) softmax_sum<R>(E, K, st, b == 0, token, status);
+  // The down chunks of this workgroup's output tile only once this wave's
+  // gate/up bytes have landed: every workgroup's gate/up tile gates the h
+  // hand-off, while the down chunks are needed only after it, so they do
+  // not share the memory system with the gate/up loads (routed:
+  // non-temporal; shared: cached).  Unconditional: loads under a branch
+  // left their registers to be copied at the join, which waited for every
+  // load in flight.  Workgroups without an output tile all read the first
+  // chunk of the shared down matrix (one cached line set) and ignore it.
+  wait_vm();
 #pragma unroll
   for (int i = 0; i < kDownBatch; ++i)
     load_chunk_nt(down_wg ? dv[i] : sdv, down_wg ? b : 0, down_wg ? dgq[i] : 0, lane, dw[i],
@@ -701,65 +748,62 @@ __global__ __launch_bounds__(kThreads) void k_moe_decode(
       gu_load<GQW, true>(gv, uv, t % nrb, gwg, gwu, gsg, gsu);
     }
     const int k = t / nrb;
-    gu_compute<GQW>(gv, t % nrb, gwg, gwu, gsg, gsu, xb2, red, S.ht + ((size_t)k << P.ldh_log2), n,
-                    kPhExpert, token, status);
+    gu_compute<GQW>(gv, t % nrb, gwg, gwu, gsg, gsu, xb2, red,
+                    S.ht + ((size_t)k << (P.ldh_log2 - 1)), n, kPhExpert, token, status);
   }
   if (K * nrb <= b) __syncthreads();
-  if (!down_wg) return;
-  // the probabilities, needed from the combine on (published by the barrier
-  // that ends the h staging below): done after the gate/up tile so that the
-  // tile's h is published without waiting for it, by a wave with one down
-  // chunk fewer than the others
-  if (w == kNormWave)
-    finish_probs(E, K, st, red + kWaves * 32, b == 0, token, status, b == 0 ? ids_out : nullptr,
-                 probs_out, shg_out);
+  // the ranks, the outputs in the reference's order and the top-k checks:
+  // in the first workgroup without an output tile (idle from here on), or
+  // after the output tile in workgroup 0 when every workgroup has one
+  const int fin_wg = nb > H / kTileRows ? H / kTileRows : 0;
+  if (!down_wg) {
+    if (b == fin_wg && w == 0)
+      finish_probs(E, K, st, true, token, status, ids_out, probs_out, shg_out);
+    return;
+  }
 
   // ---- P4: down projection of this workgroup's 16 output rows ---------------
-  // Issue the first poll of h (thread t reads words t, t + 512, ...), then
-  // dequantize the down chunks while it is in flight.
+  // Dequantize the down chunks first, then poll h (thread t reads words t,
+  // t + 512, ...): the last gate/up tiles are published around the time the
+  // dequantization ends, and a poll issued earlier comes back stale and
+  // costs a round trip more.  (The empty asm statements pin the order: the
+  // compiler would otherwise sink the dequantization below the poll.)
   const int lg = P.ldh_log2, ldh = 1 << lg;
+  const int lgw = lg - 1;                                          // words per slot: ldh / 2
   uint16_t* hbh = reinterpret_cast<uint16_t*>(smem + P.off_hb);  // [K+1][ldh] bf16 hi
   uint16_t* hbl = hbh + ((size_t)(K + 1) << lg);                  // [K+1][ldh] bf16 lo
-  const int nwords = (K + 1) << lg;
-  uint64_t hv[kHw];
-#pragma unroll
-  for (int u = 0; u < kHw; ++u) {
-    hv[u] = ld_coh_u64(S.ht + min(tid + kThreads * u, nwords - 1));
-  }
-  // Dequantize the down chunks while the poll is in flight; a second poll
-  // is issued halfway, so that words still stale in the first one are
-  // usually current in the second.  (The empty asm statements pin the
-  // order: the compiler would otherwise hoist the dequantization.)
+  const int nwords = (K + 1) << lgw;
   auto pin = [&](int i) {
     asm volatile("" : "+v"(dw[i].x), "+v"(dw[i].y), "+v"(dw[i].z), "+v"(dw[i].w), "+v"(ds[i].x),
                  "+v"(ds[i].y)::"memory");
   };
   bf16x8 A[kDownBatch][4];
-  auto deq = [&](int i) {
+#pragma unroll
+  for (int i = 0; i < kDownBatch; ++i) pin(i);
+#pragma unroll
+  for (int i = 0; i < kDownBatch; ++i)
     if (i < my_chunks)
 #pragma unroll
       for (int c = 0; c < 4; ++c) A[i][c] = dequant8(word_of(dw[i], c), scale_of(ds[i], c));
-  };
-  constexpr int kHalf = (kDownBatch + 1) / 2;
 #pragma unroll
-  for (int i = 0; i < kHalf; ++i) pin(i);
+  for (int i = 0; i < kDownBatch; ++i)
 #pragma unroll
-  for (int i = 0; i < kHalf; ++i) deq(i);
-  uint64_t hv2[kHw];
+    for (int c = 0; c < 4; ++c) asm volatile("" : "+v"(A[i][c])::"memory");
+  uint64_t hv[kHw];
 #pragma unroll
-  for (int u = 0; u < kHw; ++u) hv2[u] = ld_coh_u64(S.ht + min(tid + kThreads * u, nwords - 1));
-#pragma unroll
-  for (int i = kHalf; i < kDownBatch; ++i) pin(i);
-#pragma unroll
-  for (int i = kHalf; i < kDownBatch; ++i) deq(i);
+  for (int u = 0; u < kHw; ++u) hv[u] = ld_coh_u64(S.ht + min(tid + kThreads * u, nwords - 1));
   {
-    // padding entries of a slot row are never written: they count as staged;
-    // each thread re-polls only its own stale words and the workgroup meets
-    // once at the end
+    // Each word carries rows 2i, 2i+1 of one slot; they are staged scaled by
+    // the slot's weight (p_k, or the shared gate) as bf16 hi / lo pairs, so
+    // every chunk of the tile accumulates into the same MFMA chains.
+    // Padding entries of a slot row are never written: they count as
+    // staged; each thread re-polls only its own stale words and the
+    // workgroup meets once at the end.
     uint32_t have = 0;
 #pragma unroll
     for (int u = 0; u < kHw; ++u) {
-      const int wd = min(tid + kThreads * u, nwords - 1), s2 = wd >> lg, idx = wd & (ldh - 1);
+      const int wd = min(tid + kThreads * u, nwords - 1), s2 = wd >> lgw;
+      const int idx = 2 * (wd & ((1 << lgw) - 1));
       if (idx >= (s2 < K ? L.I : L.Ish)) have |= 1u << u;
     }
     const uint32_t all = (1u << min(kHw, (nwords - tid + kThreads - 1) / kThreads)) - 1u;
@@ -769,19 +813,19 @@ __global__ __launch_bounds__(kThreads) void k_moe_decode(
       for (int u = 0; u < kHw; ++u) {
         if (!(have >> u & 1u) && (all >> u & 1u)) {
           const int wd = tid + kThreads * u;
-          if ((uint32_t)(hv[u] >> 32) == n) {
-            hbh[wd] = (uint16_t)hv[u];
-            hbl[wd] = (uint16_t)(hv[u] >> 16);
+          if (h2_current(hv[u], n)) {
+            const int s2 = wd >> lgw, at = (s2 << lg) + 2 * (wd & ((1 << lgw) - 1));
+            const float wgt = st.pw[s2];
+            uint16_t h0, l0, h1, l1;
+            split1(h2_v0(hv[u]) * wgt, h0, l0);
+            split1(h2_v1(hv[u]) * wgt, h1, l1);
+            *reinterpret_cast<uint32_t*>(hbh + at) = (uint32_t)h0 | ((uint32_t)h1 << 16);
+            *reinterpret_cast<uint32_t*>(hbl + at) = (uint32_t)l0 | ((uint32_t)l1 << 16);
             have |= 1u << u;
           }
         }
       }
       if (have == all) break;
-      if (spin == 0) {  // stale in the first poll: the later one (waited for only here)
-#pragma unroll
-        for (int u = 0; u < kHw; ++u) hv[u] = hv2[u];
-        continue;
-      }
       __builtin_amdgcn_s_sleep(1);
 #pragma unroll
       for (int u = 0; u < kHw; ++u)  // unconditional loads stay in flight together
@@ -790,47 +834,64 @@ __global__ __launch_bounds__(kThreads) void k_moe_decode(
     if (!__syncthreads_and(have == all || !ok) && tid == 0)
       record_err(status, err_key(kPhSync, 0, 0, 0, 0));
   }
-  // per chunk two MFMA chains over its four k-steps, then the slot weight:
-  // y = sum_k p_k (W_k h_k) + g (W_sh h_sh)
-  f32x4 acc = {0, 0, 0, 0};
-  for (int base = 0; base < my_chunks; base += kDownBatch) {
-    if (base > 0) {  // chunks beyond the register batch
+  // y = sum_k W_k (p_k h_k) + W_sh (g h_sh): every chunk of the wave into two
+  // MFMA chains (the weights are in the staged operand); the next chunk's B
+  // operand is read while the current one's products run
+  f32x4 acc0 = {0, 0, 0, 0}, acc1 = {0, 0, 0, 0};
+  auto ld_chunk_b = [&](int s, int gq, bf16x8 (&B)[4]) {
+    const uint16_t* hs = hbh + ((size_t)s << lg);
+    const uint16_t* ls = hbl + ((size_t)s << lg);
 #pragma unroll
-      for (int i = 0; i < kDownBatch; ++i) {
-        const int c = w + kWaves * (base + i);
-        if (base + i < my_chunks) {
-          const bool routed = c < nch_r;
-          const ExpertView v = routed ? down_view(c / nGQI) : sdv;
-          load_chunk_nt(v, b, routed ? c % nGQI : c - nch_r, lane, dw[i], ds[i]);
-        }
-      }
+    for (int cc = 0; cc < 4; ++cc) B[cc] = ld_b2(hs, ls, (gq * 4 + cc) * 4 + q, j);
+  };
+  bf16x8 Bb[2][4];
+  ld_chunk_b(dsl[0], dgq[0], Bb[0]);
 #pragma unroll
-      for (int i = 0; i < kDownBatch; ++i)
-        if (base + i < my_chunks)
-#pragma unroll
-          for (int c = 0; c < 4; ++c) A[i][c] = dequant8(word_of(dw[i], c), scale_of(ds[i], c));
+  for (int i = 0; i < kDownBatch; ++i) {
+    if (i < my_chunks) {
+      if (i + 1 < kDownBatch) ld_chunk_b(dsl[min(i + 1, kDownBatch - 1)],
+                                         dgq[min(i + 1, kDownBatch - 1)], Bb[(i + 1) & 1]);
+      const bf16x8(&B)[4] = Bb[i & 1];
+      acc0 = mfma16(A[i][0], B[0], acc0);
+      acc1 = mfma16(A[i][1], B[1], acc1);
+      acc0 = mfma16(A[i][2], B[2], acc0);
+      acc1 = mfma16(A[i][3], B[3], acc1);
     }
+  }
+  // chunks beyond the register batch (only when a wave has more than
+  // kDownBatch chunks)
+  for (int base = kDownBatch; base < my_chunks; base += kDownBatch) {
+#pragma unroll
+    for (int i = 0; i < kDownBatch; ++i) {
+      const int c = w + kWaves * (base + i);
+      if (base + i < my_chunks) {
+        const bool routed = c < nch_r;
+        const ExpertView v = routed ? down_view(c / nGQI) : sdv;
+        load_chunk_nt(v, b, routed ? c % nGQI : c - nch_r, lane, dw[i], ds[i]);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < kDownBatch; ++i)
+      if (base + i < my_chunks)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) A[i][c] = dequant8(word_of(dw[i], c), scale_of(ds[i], c));
 #pragma unroll
     for (int i = 0; i < kDownBatch; ++i) {
       if (base + i < my_chunks) {
         const int c = w + kWaves * (base + i);
         const int s = c < nch_r ? c / nGQI : K, gq = c < nch_r ? c % nGQI : c - nch_r;
-        const uint16_t* hs = hbh + ((size_t)s << lg);
-        const uint16_t* ls = hbl + ((size_t)s << lg);
-        const float wgt = st.pw[s];
         bf16x8 B[4];
-#pragma unroll
-        for (int cc = 0; cc < 4; ++cc) B[cc] = ld_b2(hs, ls, (gq * 4 + cc) * 4 + q, j);
-        f32x4 a0 = {0, 0, 0, 0}, a1 = {0, 0, 0, 0};
-        a0 = mfma16(A[i][0], B[0], a0);
-        a1 = mfma16(A[i][1], B[1], a1);
-        a0 = mfma16(A[i][2], B[2], a0);
-        a1 = mfma16(A[i][3], B[3], a1);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) acc[r] = acc[r] + wgt * (a0[r] + a1[r]);
+        ld_chunk_b(s, gq, B);
+        acc0 = mfma16(A[i][0], B[0], acc0);
+        acc1 = mfma16(A[i][1], B[1], acc1);
+        acc0 = mfma16(A[i][2], B[2], acc0);
+        acc1 = mfma16(A[i][3], B[3], acc1);
       }
     }
   }
+  f32x4 acc;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) acc[r] = acc0[r] + acc1[r];
   fold_cols(acc);
   if (j == 0) {
 #pragma unroll
@@ -847,6 +908,8 @@ __global__ __launch_bounds__(kThreads) void k_moe_decode(
     if (!finite_f(total)) record_err(status, err_key(kPhExpert, token, 0, 0, kEkRecheck));
     y[d] = total;
   }
+  if (b == fin_wg && fin_wg == 0 && w == 0)
+    finish_probs(E, K, st, true, token, status, ids_out, probs_out, shg_out);
 }
 
 static int ldh_log2_of(const LayerDev& L) {
@@ -888,7 +951,7 @@ DecodePlan make_decode_plan(const LayerDev& L, int num_cus) {
   P.off_zv = off; off += align16(4 * 256 * R);
   P.off_ev = off; off += align16(4 * 256 * R);
   P.off_sel = off; off += 768;
-  P.off_red = off; off += align16(kWaves * 2 * 16 * 4 + 96 * 4);  // + finish_probs scratch
+  P.off_red = off; off += align16(kWaves * 2 * 16 * 4);
   P.off_hb = off; off += align16(slots * ldh * 4);
   P.off_yred = off; off += align16(kWaves * 16 * 4);
   P.lds_bytes = off;
@@ -906,7 +969,7 @@ static const void* pick_kernel(const LayerDev& L) {
   const int gqw = (L.H / kQuadCols + kWaves - 1) / kWaves;
   const int R = (L.E + 255) / 256;
   const int ldh = 1 << ldh_log2_of(L);
-  if (R > 8 || L.K > 32 || (L.K + 1) * ldh > kHw * kThreads) return nullptr;
+  if (R > 8 || L.K > 32 || ldh < 2 || (L.K + 1) * (ldh / 2) > kHw * kThreads) return nullptr;
   return gqw <= 2 ? pick_r<2>(R) : gqw <= 8 ? pick_r<8>(R) : nullptr;
 }
 

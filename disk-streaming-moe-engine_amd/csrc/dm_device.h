@@ -165,6 +165,8 @@ __device__ __forceinline__ void st_coh_u64(void* p, uint64_t v) {
   __hip_atomic_store(reinterpret_cast<uint64_t*>(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ void wait_stores() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+// Every vector memory operation of this wave (loads and stores) complete.
+__device__ __forceinline__ void wait_vm() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
 // ---- wave-wide reductions with DPP (row shifts, then row broadcasts) --------
 // The result is exact for max/min (order independent), read from lane 63.
