@@ -330,7 +330,7 @@ __device__ __forceinline__ void wait_lds() { asm volatile("s_waitcnt lgkmcnt(0)"
 
 // Routing on wave 0.  Selects the K largest logits with unique 32-bit keys
 // (the high bits of the logit's order key, then the inverted expert id, so
-// one DPP max per round names the winner), then checks that the smallest
+// equal logits order by the lower id), then checks that the smallest
 // selected logit and the largest unselected one are far enough apart that
 // p = exp(z - max) * (1/S) keeps them strictly ordered; otherwise it forms S
 // and selects on the exact probabilities with the lowest-id tie-break.
@@ -345,7 +345,7 @@ __device__ __forceinline__ bool route(const uint64_t* zt, unsigned tag, int E, i
   float z[NK];
   const bool ok = poll_logits<R>(zt, tag, E, z, nullptr);
   if (!ok && lane == 0) record_err(status, err_key(kPhSync, 0, 0, 0, 0));
-  uint32_t fk[NK], key[NK], key0[NK];
+  uint32_t fk[NK], key[NK];
 #pragma unroll
   for (int i = 0; i < NK; ++i) {
     const int e = lane + 64 * i;
@@ -357,22 +357,51 @@ __device__ __forceinline__ bool route(const uint64_t* zt, unsigned tag, int E, i
       fk[i] = f2key(z[i]);
       key[i] = ((fk[i] >> IDB) << IDB) | (IDM - (uint32_t)e);
     }
-    key0[i] = key[i];
   }
   // K rounds: the largest remaining key; its low bits name the expert.  Lane
-  // `it` keeps the id of round it (no branches inside the loop).
+  // `it` keeps the id of round it (no branches inside the loop).  With four
+  // keys a lane sorts them once, so a round is one wave-wide max of the lane
+  // heads and a shift in the winning lane.
   int myid = 0;
   uint32_t gm = 0;
+  if constexpr (NK == 4) {
+    uint32_t k0 = key[0], k1 = key[1], k2 = key[2], k3 = key[3];
+    auto cx = [](uint32_t& a, uint32_t& b) {  // a >= b afterwards
+      const uint32_t hi = a > b ? a : b, lo = a > b ? b : a;
+      a = hi;
+      b = lo;
+    };
+    cx(k0, k1);
+    cx(k2, k3);
+    cx(k0, k2);
+    cx(k1, k3);
+    cx(k1, k2);
 #pragma unroll 8
-  for (int it = 0; it < K; ++it) {
-    uint32_t km = 0;
+    for (int it = 0; it < K; ++it) {
+      gm = wave_max_u32(k0);
+      const bool win = k0 == gm;
+      k0 = win ? k1 : k0;
+      k1 = win ? k2 : k1;
+      k2 = win ? k3 : k2;
+      k3 = win ? 0u : k3;
+      myid = lane == it ? (int)(IDM - (gm & IDM)) : myid;
+    }
+  } else {
+    uint32_t kw[NK];
 #pragma unroll
-    for (int i = 0; i < NK; ++i) km = key[i] > km ? key[i] : km;
-    gm = wave_max_u32(km);
+    for (int i = 0; i < NK; ++i) kw[i] = key[i];
+#pragma unroll 8
+    for (int it = 0; it < K; ++it) {
+      uint32_t km = 0;
 #pragma unroll
-    for (int i = 0; i < NK; ++i) key[i] = key[i] == gm ? 0u : key[i];
-    myid = lane == it ? (int)(IDM - (gm & IDM)) : myid;
+      for (int i = 0; i < NK; ++i) km = kw[i] > km ? kw[i] : km;
+      gm = wave_max_u32(km);
+#pragma unroll
+      for (int i = 0; i < NK; ++i) kw[i] = kw[i] == gm ? 0u : kw[i];
+      myid = lane == it ? (int)(IDM - (gm & IDM)) : myid;
+    }
   }
+  if (lane < K) st.ids[lane] = myid < E ? myid : E - 1;
   // selected = key at or above the last winner; exact max, smallest selected
   // and largest unselected logit in three independent reductions
   uint32_t lmax = 0, mins = 0xFFFFFFFFu, maxu = 0;
@@ -380,7 +409,7 @@ __device__ __forceinline__ bool route(const uint64_t* zt, unsigned tag, int E, i
   for (int i = 0; i < NK; ++i) {
     if (lane + 64 * i < E) {
       lmax = fk[i] > lmax ? fk[i] : lmax;
-      if (key0[i] >= gm) mins = fk[i] < mins ? fk[i] : mins;
+      if (key[i] >= gm) mins = fk[i] < mins ? fk[i] : mins;
       else maxu = fk[i] > maxu ? fk[i] : maxu;
     }
   }
@@ -392,7 +421,6 @@ __device__ __forceinline__ bool route(const uint64_t* zt, unsigned tag, int E, i
     const float ek = dm_expf(zs - m), en = dm_expf(zu - m);
     unsafe = !(ek > en + en * 0x1p-20f);
   }
-  if (lane < K) st.ids[lane] = myid < E ? myid : E - 1;
   if (unsafe) {  // select on the exact probabilities
     float ev[NK];
 #pragma unroll
