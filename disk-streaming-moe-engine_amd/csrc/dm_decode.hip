@@ -358,12 +358,19 @@ __device__ __forceinline__ bool route(const uint64_t* zt, unsigned tag, int E, i
       key[i] = ((fk[i] >> IDB) << IDB) | (IDM - (uint32_t)e);
     }
   }
+  // the exact maximum logit (independent of the selection below)
+  uint32_t lmax = 0;
+#pragma unroll
+  for (int i = 0; i < NK; ++i)
+    if (lane + 64 * i < E) lmax = fk[i] > lmax ? fk[i] : lmax;
+  const float m = key2f(wave_max_u32(lmax));
   // K rounds: the largest remaining key; its low bits name the expert.  Lane
   // `it` keeps the id of round it (no branches inside the loop).  With four
   // keys a lane sorts them once, so a round is one wave-wide max of the lane
-  // heads and a shift in the winning lane.
+  // heads and a shift in the winning lane.  A last max gives the largest
+  // unselected key.
   int myid = 0;
-  uint32_t gm = 0;
+  uint32_t gm = 0, gu = 0;
   if constexpr (NK == 4) {
     uint32_t k0 = key[0], k1 = key[1], k2 = key[2], k3 = key[3];
     auto cx = [](uint32_t& a, uint32_t& b) {  // a >= b afterwards
@@ -386,6 +393,7 @@ __device__ __forceinline__ bool route(const uint64_t* zt, unsigned tag, int E, i
       k3 = win ? 0u : k3;
       myid = lane == it ? (int)(IDM - (gm & IDM)) : myid;
     }
+    if (K < E) gu = wave_max_u32(k0);
   } else {
     uint32_t kw[NK];
 #pragma unroll
@@ -400,24 +408,23 @@ __device__ __forceinline__ bool route(const uint64_t* zt, unsigned tag, int E, i
       for (int i = 0; i < NK; ++i) kw[i] = kw[i] == gm ? 0u : kw[i];
       myid = lane == it ? (int)(IDM - (gm & IDM)) : myid;
     }
-  }
-  if (lane < K) st.ids[lane] = myid < E ? myid : E - 1;
-  // selected = key at or above the last winner; exact max, smallest selected
-  // and largest unselected logit in three independent reductions
-  uint32_t lmax = 0, mins = 0xFFFFFFFFu, maxu = 0;
+    if (K < E) {
+      uint32_t km = 0;
 #pragma unroll
-  for (int i = 0; i < NK; ++i) {
-    if (lane + 64 * i < E) {
-      lmax = fk[i] > lmax ? fk[i] : lmax;
-      if (key[i] >= gm) mins = fk[i] < mins ? fk[i] : mins;
-      else maxu = fk[i] > maxu ? fk[i] : maxu;
+      for (int i = 0; i < NK; ++i) km = kw[i] > km ? kw[i] : km;
+      gu = wave_max_u32(km);
     }
   }
-  const float m = key2f(wave_max_u32(lmax));
-  const float zs = key2f(wave_min_u32(mins)), zu = key2f(wave_max_u32(maxu));
+  if (lane < K) st.ids[lane] = myid < E ? myid : E - 1;
+  // Margin check on bounds from the keys: every selected logit is at least
+  // zs (the K-th key with its id bits cleared) and every unselected one at
+  // most zu (the largest unselected key with its id bits set), so
+  // e(zs) > e(zu) (1 + 2^-20) implies the same for the exact boundary logits
+  // (exp is monotone to within an ulp, far inside the 2^-20 margin).
   if (record && lane == 0 && !finite_f(m)) record_err(status, err_key(kPhSoftmax, token, 0, 0, 0));
   bool unsafe = false;
   if (K < E) {
+    const float zs = key2f(gm & ~IDM), zu = key2f(gu | IDM);
     const float ek = dm_expf(zs - m), en = dm_expf(zu - m);
     unsafe = !(ek > en + en * 0x1p-20f);
   }
