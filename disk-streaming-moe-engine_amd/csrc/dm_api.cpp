@@ -65,7 +65,7 @@ struct dmh_ctx {
   std::vector<Layer*> layers;
   // scratch
   DevBuf<float> x, res, y, z, probs, shg, h, xn, hstack;
-  DevBuf<int32_t> ids;
+  DevBuf<int32_t> ids, uids;  // uids: checked expert ids of dmh_experts_forward
   DevBuf<uint8_t> stage;
   // several tokens per call (grouped experts)
   DevBuf<int32_t> g_off, g_perm, g_meta, g_needlo;
@@ -135,6 +135,10 @@ int decode_key(uint64_t key, int layer, int expert_id, int E, char* err, size_t 
       if (kind == kEkGate) EJ(DMH_ERR_EXPERT, "EXPERT_ERROR", "non-finite in gate projection");
       if (kind == kEkUp) EJ(DMH_ERR_EXPERT, "EXPERT_ERROR", "non-finite in up projection");
       if (kind == kEkH) EJ(DMH_ERR_SWIGLU, "SWIGLU_ERROR", "non-finite in element-wise product");
+      if (kind == kEkBadId) {  // the id itself is the key's position (28-bit two's complement)
+        expert_id = (int)(pos << 4) >> 4;
+        EJ(DMH_ERR_INVALID_ARG, "EXPERT_ERROR", "expert id out of range");
+      }
       if (kind == kEkRecheck)
         RJ(DMH_ERR_EXPERT, "EXPERT_ERROR", "non-finite value in aggregation", "aggregation");
       EJ(DMH_ERR_EXPERT, "EXPERT_ERROR", "non-finite in down projection");
@@ -296,7 +300,7 @@ hipError_t run_block(dmh_ctx* ctx, Layer* Ly, int layer, const float* dx, const 
 
 // Host-side decode of a layer's status word after a synchronous call.
 int finish_status(dmh_ctx* ctx, Layer* Ly, int layer, uint64_t key, const int32_t* host_ids,
-                  char* err, size_t errlen) {
+                  char* err, size_t errlen, int ids_k = 0) {
   if (Ly && Ly->router_w_bad) {
     const uint64_t rk = dm::err_key(dm::kPhRouterW, 0, 0, 0, 0);
     if (rk < key) key = rk;
@@ -307,7 +311,7 @@ int finish_status(dmh_ctx* ctx, Layer* Ly, int layer, uint64_t key, const int32_
     (void)reset_counters(ctx, Ly);
   }
   int expert_id = -1;
-  const int K = Ly ? Ly->dims.top_k : 0;
+  const int K = ids_k > 0 ? ids_k : Ly ? Ly->dims.top_k : 0;
   if (dm::key_phase(key) == dm::kPhExpert && host_ids)
     expert_id = host_ids[(size_t)dm::key_token(key) * K + dm::key_slot(key)];
   return decode_key(key, layer, expert_id, Ly ? Ly->dims.num_experts : 0, err, errlen);
@@ -357,6 +361,7 @@ int dmh_destroy(dmh_ctx* c) {
   DevBuf<float>* fb[] = {&c->x, &c->res, &c->y, &c->z, &c->probs, &c->shg, &c->h, &c->xn, &c->hstack};
   for (auto* b : fb) b->release();
   c->ids.release();
+  c->uids.release();
   c->stage.release();
   c->g_off.release();
   c->g_perm.release();
@@ -398,14 +403,15 @@ int dmh_sync(dmh_ctx* c, char* err, size_t errlen) {
     uint64_t key = keys[l];
     if (key == dm::kNoError) continue;
     std::vector<int32_t> ids;
+    const int idk = c->last_k[l] > 0 ? c->last_k[l] : Ly ? Ly->dims.top_k : 0;
     if (dm::key_phase(key) == dm::kPhExpert && c->last_ids[l] && Ly) {
-      const size_t n = (size_t)(dm::key_token(key) + 1) * Ly->dims.top_k;
+      const size_t n = (size_t)(dm::key_token(key) + 1) * idk;
       ids.resize(n);
       if (hipMemcpy(ids.data(), c->last_ids[l], n * sizeof(int32_t), hipMemcpyDeviceToHost) !=
           hipSuccess)
         ids.clear();
     }
-    rc = finish_status(c, Ly, l, key, ids.empty() ? nullptr : ids.data(), err, errlen);
+    rc = finish_status(c, Ly, l, key, ids.empty() ? nullptr : ids.data(), err, errlen, idk);
   }
   HIP_TRY(hipMemset(c->status, 0xFF, sizeof(unsigned long long) * keys.size()));
   return rc;
@@ -623,6 +629,7 @@ int dmh_moe_forward(dmh_ctx* c, int layer, const float* x, const float* residual
   }
   HIP_TRY(run_block(c, Ly, layer, dx, dres, T, dy, dids, dprobs, dshg));
   c->last_ids[layer] = dids;
+  c->last_k[layer] = L.K;
   if (dev) return DMH_OK;
   std::vector<int32_t> hids(TK);
   unsigned long long key = 0;
@@ -700,6 +707,7 @@ int dmh_moe_stack_forward(dmh_ctx* c, int first, int nl, float eps, const float*
     float* dst = (direct && i == nl - 1) ? out : (src == hA ? hB : hA);
     HIP_TRY(run_block(c, c->layers[l], l, src, src, T, dst, dids, dprobs, c->shg.p, true, eps));
     c->last_ids[l] = dids;
+    c->last_k[l] = K;
     src = dst;
   }
   if (src != out)
@@ -830,6 +838,182 @@ int dmh_dequant_q4_bf16(dmh_ctx* c, const uint16_t* scales, int64_t n_scales,
                    (unsigned long long)(vk >> 1));
   return set_err(err, errlen, DMH_ERR_DEQUANT, "dequant_kernel: scale is NaN or Inf at group %llu",
                  (unsigned long long)(vk >> 1));
+}
+
+int dmh_experts_forward(dmh_ctx* c, int layer, const float* x, int T, const int32_t* ids,
+                        int K, float* out, float* shared_out, unsigned flags, char* err,
+                        size_t errlen) {
+  Layer* Ly = get_layer(c, layer);
+  if (!Ly)
+    return set_err(err, errlen, DMH_ERR_INVALID_ARG, "dmh_experts_forward: layer %d not uploaded",
+                   layer);
+  if (!x || !ids || !out)
+    return set_err(err, errlen, DMH_ERR_INVALID_ARG,
+                   "dmh_experts_forward: x, ids and out are required");
+  if (T <= 0 || K <= 0)
+    return set_err(err, errlen, DMH_ERR_EXPERT,
+                   "{\"error_type\":\"EXPERT_ERROR\",\"detail\":\"dimensions must be"
+                   " positive\",\"stage\":\"swiglu\",\"layer\":%d}", layer);
+  if (K > 64)
+    return set_err(err, errlen, DMH_ERR_INVALID_ARG,
+                   "dmh_experts_forward: top_k %d outside [1, 64]", K);
+  HIP_TRY(hipSetDevice(c->device));
+  const LayerDev& L = Ly->dev;
+  const bool dev = flags & DMH_F_DEVICE;
+  hipStream_t st = c->cur;
+  unsigned long long* status = c->status + layer;
+  const size_t TH = (size_t)T * L.H, TK = (size_t)T * K;
+  std::vector<int32_t> hids;
+  const float* dx = x;
+  HIP_TRY(c->uids.ensure(TK));
+  if (!dev) {
+    hids.assign(ids, ids + TK);
+    for (size_t i = 0; i < TK; ++i)
+      if (hids[i] < 0 || hids[i] >= L.E)
+        return set_err(err, errlen, DMH_ERR_INVALID_ARG,
+                       "{\"error_type\":\"EXPERT_ERROR\",\"detail\":\"expert id out of range\","
+                       "\"stage\":\"swiglu\",\"layer\":%d,\"expert_id\":%d}", layer, hids[i]);
+    HIP_TRY(c->x.ensure(TH));
+    HIP_TRY(hipMemcpyAsync(c->x.p, x, TH * 4, hipMemcpyHostToDevice, st));
+    dx = c->x.p;
+    HIP_TRY(reset_status(c, layer));
+    HIP_TRY(hipMemcpyAsync(c->uids.p, hids.data(), TK * 4, hipMemcpyHostToDevice, st));
+  } else {
+    HIP_TRY(dm::launch_check_ids(ids, T, K, L.E, c->uids.p, status, st));
+  }
+  // the grouped experts with K assignments per token
+  LayerDev Lk = L;
+  Lk.K = K;
+  HIP_TRY(c->g_off.ensure(L.E + 1));
+  HIP_TRY(c->g_perm.ensure(TK));
+  HIP_TRY(c->g_meta.ensure(2));
+  HIP_TRY(c->g_needlo.ensure(1));
+  HIP_TRY(c->g_units.ensure(dm::group_units_max(T, K, L.E)));
+  HIP_TRY(c->g_xhi.ensure(TH));
+  HIP_TRY(c->g_xlo.ensure(TH));
+  HIP_TRY(c->g_hr.ensure(2 * TK * L.I));
+  HIP_TRY(c->g_hs.ensure(2 * (size_t)T * L.Ish));
+  float* dout = dev ? out : nullptr;
+  if (!dout) { HIP_TRY(c->g_r.ensure(TK * L.H)); dout = c->g_r.p; }
+  HIP_TRY(c->g_rs.ensure(TH));
+  HIP_TRY(hipMemsetAsync(c->g_needlo.p, 0, sizeof(int), st));
+  HIP_TRY(dm::launch_split_rows(dx, (int64_t)TH, c->g_xhi.p, c->g_xlo.p, c->g_needlo.p, st));
+  HIP_TRY(dm::launch_group_build(c->uids.p, T, K, L.E, c->g_off.p, c->g_perm.p, c->g_units.p,
+                                 c->g_meta.p, st));
+  float* drs = (dev && shared_out) ? shared_out : c->g_rs.p;
+  HIP_TRY(dm::launch_experts_grouped(Lk, c->g_xhi.p, c->g_xlo.p, c->g_needlo.p, c->g_off.p,
+                                     c->g_perm.p, c->g_units.p, c->g_meta.p, T, c->g_hr.p,
+                                     c->g_hr.p + TK * L.I, c->g_hs.p,
+                                     c->g_hs.p + (size_t)T * L.Ish, dout, drs, status, st));
+  c->last_ids[layer] = c->uids.p;
+  c->last_k[layer] = K;
+  if (dev) return DMH_OK;
+  unsigned long long key = 0;
+  HIP_TRY(hipMemcpyAsync(out, dout, TK * L.H * 4, hipMemcpyDeviceToHost, st));
+  if (shared_out) HIP_TRY(hipMemcpyAsync(shared_out, drs, TH * 4, hipMemcpyDeviceToHost, st));
+  HIP_TRY(hipMemcpyAsync(&key, status, sizeof(key), hipMemcpyDeviceToHost, st));
+  HIP_TRY(hipStreamSynchronize(st));
+  int rc = finish_status(c, Ly, layer, key, hids.data(), err, errlen, K);
+  if (rc) HIP_TRY(reset_status(c, layer));
+  return rc;
+}
+
+int dmh_shared_gate_forward(dmh_ctx* c, int layer, const float* x, int T, float* scores,
+                            unsigned flags, char* err, size_t errlen) {
+  Layer* Ly = get_layer(c, layer);
+  if (!Ly)
+    return set_err(err, errlen, DMH_ERR_INVALID_ARG,
+                   "dmh_shared_gate_forward: layer %d not uploaded", layer);
+  if (!x || !scores)
+    return set_err(err, errlen, DMH_ERR_INVALID_ARG,
+                   "dmh_shared_gate_forward: x and scores are required");
+  if (T <= 0)
+    return set_err(err, errlen, DMH_ERR_GATE,
+                   "{\"error_type\":\"GATE_ERROR\",\"detail\":\"dimensions must be"
+                   " positive\",\"stage\":\"shared\",\"layer\":%d}", layer);
+  HIP_TRY(hipSetDevice(c->device));
+  const LayerDev& L = Ly->dev;
+  const bool dev = flags & DMH_F_DEVICE;
+  hipStream_t st = c->cur;
+  unsigned long long* status = c->status + layer;
+  const size_t TH = (size_t)T * L.H;
+  const float* dx = x;
+  float* ds = dev ? scores : nullptr;
+  if (!dev) {
+    HIP_TRY(c->x.ensure(TH));
+    HIP_TRY(hipMemcpyAsync(c->x.p, x, TH * 4, hipMemcpyHostToDevice, st));
+    dx = c->x.p;
+    HIP_TRY(c->shg.ensure(T));
+    ds = c->shg.p;
+    HIP_TRY(reset_status(c, layer));
+  }
+  // the gate vector is row E of the router layout: the lane-chain router on
+  // that one row gives the logit in the order of shared_gate_forward
+  // (src/layers/moe.mojo:64-81); the activation scan of that kernel goes to
+  // a scratch word, as shared_gate_forward has none
+  LayerDev Lg = L;
+  Lg.router = L.router + (size_t)L.E * L.H;
+  Lg.E = 0;
+  HIP_TRY(c->z.ensure(T));
+  HIP_TRY(dm::launch_router_dec(Lg, dx, T, c->z.p, c->vkey, st));
+  HIP_TRY(dm::launch_shared_gate_scores(c->z.p, 1, T, ds, status, st));
+  if (dev) return DMH_OK;
+  unsigned long long key = 0;
+  HIP_TRY(hipMemcpyAsync(scores, ds, (size_t)T * 4, hipMemcpyDeviceToHost, st));
+  HIP_TRY(hipMemcpyAsync(&key, status, sizeof(key), hipMemcpyDeviceToHost, st));
+  HIP_TRY(hipStreamSynchronize(st));
+  int rc = finish_status(c, Ly, layer, key, nullptr, err, errlen);
+  if (rc) HIP_TRY(reset_status(c, layer));
+  return rc;
+}
+
+int dmh_moe_aggregate(dmh_ctx* c, const float* residual, const float* routed, const float* probs,
+                      const float* shared_out, const float* shared_gates, int T, int H, int K,
+                      int layer, float* out, unsigned flags, char* err, size_t errlen) {
+  if (!c || !routed || !probs || !shared_out || !shared_gates || !out)
+    return set_err(err, errlen, DMH_ERR_INVALID_ARG, "dmh_moe_aggregate: NULL argument");
+  if (T <= 0 || H <= 0 || K < 0)
+    return set_err(err, errlen, DMH_ERR_EXPERT,
+                   "{\"error_type\":\"EXPERT_ERROR\",\"detail\":\"dimensions must be"
+                   " positive\",\"stage\":\"aggregation\",\"layer\":%d}", layer);
+  HIP_TRY(hipSetDevice(c->device));
+  const bool dev = flags & DMH_F_DEVICE;
+  hipStream_t st = c->cur;
+  unsigned long long* status = c->status + kMaxLayers;
+  const size_t TH = (size_t)T * H, TK = (size_t)T * K;
+  const float *dr = routed, *dp = probs, *dsh = shared_out, *dg = shared_gates, *dres = residual;
+  float* dy = out;
+  if (!dev) {
+    HIP_TRY(c->g_r.ensure(TK * H > 0 ? TK * H : 1));
+    HIP_TRY(c->g_rs.ensure(TH));
+    HIP_TRY(c->probs.ensure(TK > 0 ? TK : 1));
+    HIP_TRY(c->shg.ensure(T));
+    HIP_TRY(c->y.ensure(TH));
+    if (TK) HIP_TRY(hipMemcpyAsync(c->g_r.p, routed, TK * H * 4, hipMemcpyHostToDevice, st));
+    if (TK) HIP_TRY(hipMemcpyAsync(c->probs.p, probs, TK * 4, hipMemcpyHostToDevice, st));
+    HIP_TRY(hipMemcpyAsync(c->g_rs.p, shared_out, TH * 4, hipMemcpyHostToDevice, st));
+    HIP_TRY(hipMemcpyAsync(c->shg.p, shared_gates, (size_t)T * 4, hipMemcpyHostToDevice, st));
+    dr = c->g_r.p;
+    dp = c->probs.p;
+    dsh = c->g_rs.p;
+    dg = c->shg.p;
+    dy = c->y.p;
+    if (residual) {
+      HIP_TRY(c->res.ensure(TH));
+      HIP_TRY(hipMemcpyAsync(c->res.p, residual, TH * 4, hipMemcpyHostToDevice, st));
+      dres = c->res.p;
+    }
+    HIP_TRY(reset_status(c, kMaxLayers));
+  }
+  HIP_TRY(dm::launch_combine(dr, dsh, dp, dg, dres, T, H, K, dy, status, st));
+  if (dev) return DMH_OK;
+  unsigned long long key = 0;
+  HIP_TRY(hipMemcpyAsync(out, dy, TH * 4, hipMemcpyDeviceToHost, st));
+  HIP_TRY(hipMemcpyAsync(&key, status, sizeof(key), hipMemcpyDeviceToHost, st));
+  HIP_TRY(hipStreamSynchronize(st));
+  if (key == dm::kNoError) return DMH_OK;
+  HIP_TRY(reset_status(c, kMaxLayers));
+  return decode_key(key, layer, -1, 0, err, errlen);
 }
 
 }  // extern "C"

@@ -42,6 +42,16 @@ hipError_t launch_down_dec(const LayerDev& L, const float* h, int ldh, const int
                            const float* probs, const float* shg, const float* residual,
                            float* y, int token, unsigned long long* status, hipStream_t st);
 
+// Shared-expert gate scores from gate logits z[t] (ldz apart):
+// sigmoid(z) with the checks of shared_gate_forward (src/layers/moe.mojo:83-100).
+hipError_t launch_shared_gate_scores(const float* z, int ldz, int T, float* scores,
+                                     unsigned long long* status, hipStream_t st);
+// Expert ids [T][K] checked against [0, E): out-of-range entries are recorded
+// (kPhExpert, kEkBadId, the id's low 28 bits as the position) and replaced by
+// expert 0 in the copy out.
+hipError_t launch_check_ids(const int32_t* ids, int T, int K, int E, int32_t* out,
+                            unsigned long long* status, hipStream_t st);
+
 // ---- glue ----
 hipError_t launch_rmsnorm_rows(const float* x, int T, int H, float eps, float* out,
                                unsigned long long* status, int layer_tag, hipStream_t st);

@@ -721,4 +721,46 @@ hipError_t launch_rmsnorm_rows(const float* x, int T, int H, float eps, float* o
   return hipGetLastError();
 }
 
+// ---- shared gate scores and expert-id checks (unit entry points) ----------
+// One thread per token: sigmoid of the gate logit with the two checks of
+// shared_gate_forward (src/layers/moe.mojo:83-100) in its order.
+__global__ __launch_bounds__(256) void k_shared_gate_scores(const float* __restrict__ z, int ldz,
+                                                            int T, float* __restrict__ scores,
+                                                            unsigned long long* status) {
+  const int t = blockIdx.x * 256 + threadIdx.x;
+  if (t >= T) return;
+  const float logit = z[(size_t)t * ldz];
+  if (!finite_f(logit)) record_err(status, err_key(kPhGate, t, 0, 0, kGkLogit));
+  const float sg = dm_sigmoid(logit);
+  if (!finite_f(sg) || sg < 0.0f || sg > 1.0f)
+    record_err(status, err_key(kPhGate, t, 0, 0, kGkRange));
+  scores[t] = sg;
+}
+
+hipError_t launch_shared_gate_scores(const float* z, int ldz, int T, float* scores,
+                                     unsigned long long* status, hipStream_t st) {
+  hipLaunchKernelGGL(k_shared_gate_scores, dim3((T + 255) / 256), dim3(256), 0, st, z, ldz, T,
+                     scores, status);
+  return hipGetLastError();
+}
+
+__global__ __launch_bounds__(256) void k_check_ids(const int32_t* __restrict__ ids, int n, int K,
+                                                   int E, int32_t* __restrict__ out,
+                                                   unsigned long long* status) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i >= n) return;
+  const int32_t e = ids[i];
+  const bool ok = e >= 0 && e < E;
+  if (!ok) record_err(status, err_key(kPhExpert, i / K, i % K, (uint32_t)e & 0xFFFFFFFu, kEkBadId));
+  out[i] = ok ? e : 0;
+}
+
+hipError_t launch_check_ids(const int32_t* ids, int T, int K, int E, int32_t* out,
+                            unsigned long long* status, hipStream_t st) {
+  const int n = T * K;
+  hipLaunchKernelGGL(k_check_ids, dim3((n + 255) / 256), dim3(256), 0, st, ids, n, K, E, out,
+                     status);
+  return hipGetLastError();
+}
+
 }  // namespace dm

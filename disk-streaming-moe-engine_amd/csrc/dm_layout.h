@@ -84,6 +84,7 @@ enum : uint32_t {
 enum : uint32_t {  // kinds
   kTkSum = 0, kTkLeak = 1,                          // top-k
   kEkGate = 0, kEkUp = 1, kEkH = 2, kEkDown = 3,    // experts
+  kEkBadId = 4,     // an expert id outside [0, E) given to the experts entry point
   kEkRecheck = 15,  // fused decode: a non-finite output whose first failing check is re-derived
   kGkLogit = 0, kGkRange = 1,                       // shared gate
 };

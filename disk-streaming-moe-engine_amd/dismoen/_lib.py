@@ -26,7 +26,8 @@ EXPORTS = (
     "dmh_quant_open", "dmh_quant_close", "dmh_quant_num_tensors", "dmh_quant_find",
     "dmh_quant_tensor_info", "dmh_quant_read", "dmh_st_open", "dmh_st_close",
     "dmh_st_num_tensors", "dmh_st_find", "dmh_st_tensor_info", "dmh_st_read",
-    "dmh_upload_moe_layer_files",
+    "dmh_upload_moe_layer_files", "dmh_experts_forward", "dmh_shared_gate_forward",
+    "dmh_moe_aggregate",
 )
 
 
@@ -97,6 +98,10 @@ def lib():
     L.dmh_st_read.argtypes = [vp, i32, vp, i64, C.c_char_p, sz]
     L.dmh_upload_moe_layer_files.argtypes = [vp, i32, C.POINTER(DmhDims), vp, vp, i32, C.c_char_p,
                                              sz]
+    L.dmh_experts_forward.argtypes = [vp, i32, vp, i32, vp, i32, vp, vp, u32, C.c_char_p, sz]
+    L.dmh_shared_gate_forward.argtypes = [vp, i32, vp, i32, vp, u32, C.c_char_p, sz]
+    L.dmh_moe_aggregate.argtypes = [vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, vp, u32,
+                                    C.c_char_p, sz]
     _lib = L
     return L
 

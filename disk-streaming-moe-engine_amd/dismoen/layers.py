@@ -246,6 +246,91 @@ class MoEBlock:
                                            ids.ctypes.data, probs.ctypes.data, 0, e, len(e)), e)
         return RoutingInfo.from_arrays(ids.reshape(seq_len, K), probs.reshape(seq_len, K))
 
+    def experts_forward(self, x, ids, layer_idx: int, seq_len: int, with_shared: bool = False):
+        """The SwiGLU experts ids [seq_len][k] of an uploaded layer on x, unweighted:
+        (out [seq_len][k][H], shared [seq_len][H] or None)."""
+        H = self.dims[layer_idx][0]
+        x = _f32(x).reshape(-1)
+        ids = np.ascontiguousarray(ids, dtype=np.int32).reshape(seq_len, -1)
+        k = ids.shape[1]
+        out = np.empty(seq_len * k * H, np.float32)
+        sh = np.empty(seq_len * H, np.float32) if with_shared else None
+        e = errbuf()
+        check(self._lib.dmh_experts_forward(self._h, layer_idx, x.ctypes.data, seq_len,
+                                            ids.ctypes.data, k, out.ctypes.data, _ptr(sh), 0, e,
+                                            len(e)), e)
+        return out.reshape(seq_len, k, H), None if sh is None else sh.reshape(seq_len, H)
+
+    def parallel_moe_experts(self, x_tok, selected_experts, layer_idx: int) -> np.ndarray:
+        """WorkerPool.parallel_moe_experts for one token: out_routed [top_k*H]."""
+        out, _ = self.experts_forward(x_tok, np.asarray(selected_experts).reshape(1, -1),
+                                      layer_idx, 1)
+        return out.reshape(-1)
+
+    def swiglu_forward(self, x, seq_len: int, layer_idx: int = 0, expert_id: int = -1):
+        """swiglu_forward with an uploaded layer's expert expert_id (-1: the shared
+        expert): y [seq_len*H]."""
+        if expert_id < 0:
+            _, sh = self.experts_forward(x, np.zeros((seq_len, 1), np.int32), layer_idx,
+                                         seq_len, with_shared=True)
+            return sh.reshape(-1)
+        out, _ = self.experts_forward(x, np.full((seq_len, 1), expert_id, np.int32), layer_idx,
+                                      seq_len)
+        return out.reshape(-1)
+
+    def shared_gate_forward(self, x, seq_len: int, layer_idx: int = 0,
+                            gate_mode: str = "sigmoid") -> np.ndarray:
+        """shared_gate_forward with the uploaded layer's gate vector: scores [seq_len]."""
+        if gate_mode != "sigmoid":
+            raise DismoenError(11, '{"error_type":"GATE_ERROR","detail":"shared expert gate must'
+                                  ' be sigmoid; non-sigmoid gate forbidden (invariant #2)",'
+                                  f'"stage":"shared","layer":{layer_idx}}}')
+        x = _f32(x).reshape(-1)
+        scores = np.empty(max(seq_len, 1), np.float32)
+        e = errbuf()
+        check(self._lib.dmh_shared_gate_forward(self._h, layer_idx, x.ctypes.data, seq_len,
+                                                scores.ctypes.data, 0, e, len(e)), e)
+        return scores[:seq_len]
+
+    def _aggregate(self, x, routed_outputs, router_probs, shared_output, shared_gate_scores,
+                   seq_len: int, hidden_dim: int, layer_idx: int):
+        def err(detail):
+            return DismoenError(9, '{"error_type":"EXPERT_ERROR","detail":"' + detail +
+                                '","stage":"aggregation","layer":' + str(layer_idx) + "}")
+        if seq_len <= 0 or hidden_dim <= 0:
+            raise err("dimensions must be positive")
+        sh = _f32(shared_output).reshape(-1)
+        if (x is not None and _f32(x).size != seq_len * hidden_dim) or sh.size != seq_len * hidden_dim:
+            raise err("length mismatch in aggregation")
+        g = _f32(shared_gate_scores).reshape(-1)
+        if g.size != seq_len or len(routed_outputs) != seq_len:
+            raise err("sequence length mismatch")
+        probs = _f32(np.asarray(router_probs, dtype=np.float32).reshape(seq_len, -1))
+        k = probs.shape[1]
+        routed = _f32(np.asarray(routed_outputs, dtype=np.float32).reshape(seq_len, k * hidden_dim))
+        res = None if x is None else _f32(x).reshape(-1)
+        y = np.empty(seq_len * hidden_dim, np.float32)
+        e = errbuf()
+        check(self._lib.dmh_moe_aggregate(self._h, _ptr(res), routed.ctypes.data,
+                                          probs.ctypes.data, sh.ctypes.data, g.ctypes.data,
+                                          seq_len, hidden_dim, k, layer_idx, y.ctypes.data, 0, e,
+                                          len(e)), e)
+        return y
+
+    def moe_aggregate_forward(self, x, routed_outputs, router_probs, shared_output,
+                              shared_gate_scores, seq_len: int, hidden_dim: int,
+                              layer_idx: int = 0) -> np.ndarray:
+        """moe_aggregate_forward on given parts: y [seq_len*H]."""
+        return self._aggregate(x, routed_outputs, router_probs, shared_output,
+                               shared_gate_scores, seq_len, hidden_dim, layer_idx)
+
+    def combine_no_residual(self, routed_outputs, router_probs, shared_output,
+                            shared_gate_scores, seq_len: int, hidden_dim: int,
+                            layer_idx: int = 0) -> np.ndarray:
+        """moe_combine_no_residual (src/layers/forward_layer.mojo:181-247) on given parts."""
+        return self._aggregate(None, routed_outputs, router_probs, shared_output,
+                               shared_gate_scores, seq_len, hidden_dim, layer_idx)
+
     def dequant_kernel_simd(self, scales, packed_weights, num_elements: int,
                             group_size: int = 128) -> np.ndarray:
         """Returns bf16 bit patterns (uint16) of bf16(fp32(s_g) * q)."""

@@ -160,6 +160,36 @@ int dmh_dequant_q4_bf16(dmh_ctx* ctx, const uint16_t* scales, int64_t n_scales,
                         int group_size, uint16_t* out, unsigned flags, char* err,
                         size_t errlen);
 
+/* The SwiGLU experts of given assignments on an uploaded layer's 4-bit
+ * weights, unweighted: out[t][k][H] = W_down_e (SiLU(W_gate_e x_t) * (W_up_e
+ * x_t)) with e = ids[t][k], k < top_k (1..64; any expert ids in [0, E), repeats
+ * allowed).  Replaces WorkerPool.parallel_moe_experts
+ * (src/core/worker_pool.mojo:383-438, out_routed[k*H + d] for one token) and
+ * the per-(token, expert) swiglu_forward calls (src/layers/swiglu.mojo:52-230)
+ * of forward_moe_block.  shared_out [seq_len][H] (may be NULL) receives the
+ * shared expert's output.  A non-finite gate/up/product/output raises the
+ * EXPERT_ERROR / SWIGLU_ERROR text of swiglu_forward with the expert id; an id
+ * outside [0, E) raises EXPERT_ERROR "expert id out of range". */
+int dmh_experts_forward(dmh_ctx* ctx, int layer, const float* x, int seq_len,
+                        const int32_t* ids, int top_k, float* out, float* shared_out,
+                        unsigned flags, char* err, size_t errlen);
+
+/* shared_gate_forward (src/layers/moe.mojo:17-102) with gate_mode "sigmoid" and
+ * the uploaded layer's bf16 gate vector: scores[t] = sigmoid(w_sh . x_t), the
+ * dot product in the 16-lane order of the reference; GATE_ERROR texts. */
+int dmh_shared_gate_forward(dmh_ctx* ctx, int layer, const float* x, int seq_len,
+                            float* scores, unsigned flags, char* err, size_t errlen);
+
+/* moe_aggregate_forward (src/layers/moe.mojo:105-177) on given parts, or
+ * moe_combine_no_residual (src/layers/forward_layer.mojo:181-247) when
+ * residual is NULL: y[t][d] = (sum_k probs[t][k] routed[t][k][d]) +
+ * shared_gates[t] shared_out[t][d] (+ residual[t][d]), in that order.  layer
+ * is used in the error text only. */
+int dmh_moe_aggregate(dmh_ctx* ctx, const float* residual, const float* routed,
+                      const float* probs, const float* shared_out, const float* shared_gates,
+                      int seq_len, int hidden, int top_k, int layer, float* out,
+                      unsigned flags, char* err, size_t errlen);
+
 /* ---- weight files ---------------------------------------------------------
  * Readers of the reference's weight files on the host (no GPU needed), and
  * the upload of one layer straight from them.  They replace, for this block,
