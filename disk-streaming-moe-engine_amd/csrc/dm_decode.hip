@@ -602,15 +602,9 @@ __global__ __launch_bounds__(kThreads) void k_moe_decode(
   const bool router_wg = b < P.n_router_wg;
   const int sh_tile = (b + nb - P.n_router_wg % nb) % nb;
 
-  // ---- entry: x first (a wave's loads complete in order), then every load
-  // that depends on neither x nor routing
-  float4 xr[2][2];
-#pragma unroll
-  for (int ii = 0; ii < 2; ++ii) {
-    const int i = min(tid + kThreads * ii, H / 8 - 1);
-    xr[ii][0] = reinterpret_cast<const float4*>(x)[2 * i];
-    xr[ii][1] = reinterpret_cast<const float4*>(x)[2 * i + 1];
-  }
+  // ---- entry: the router rows first (their arrival gates the logits, the
+  // first hand-off), then x, then every other load that depends on neither
+  // x nor routing (a wave's loads complete in order)
   uint4 rw[kRwMax];
   const int re = b * kRouterRows + (tid >> 4);
   if (router_wg && tid < kRouterRows * 16) {
@@ -618,6 +612,13 @@ __global__ __launch_bounds__(kThreads) void k_moe_decode(
         reinterpret_cast<const uint4*>(L.router + r16_index(H, min(re, E), tid & 15));
 #pragma unroll
     for (int j8 = 0; j8 < kRwMax; ++j8) rw[j8] = wp[(size_t)min(j8, H / 128 - 1) * 16];
+  }
+  float4 xr[2][2];
+#pragma unroll
+  for (int ii = 0; ii < 2; ++ii) {
+    const int i = min(tid + kThreads * ii, H / 8 - 1);
+    xr[ii][0] = reinterpret_cast<const float4*>(x)[2 * i];
+    xr[ii][1] = reinterpret_cast<const float4*>(x)[2 * i + 1];
   }
   const size_t matS = (size_t)L.Ish * H;
   const ExpertView sgv = {L.sgu_nib, L.sgu_sc, L.Ish, H};
