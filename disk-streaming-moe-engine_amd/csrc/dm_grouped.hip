@@ -142,6 +142,22 @@ int group_units_max(int T, int K, int E) {
   return 2 * E + (T * K + kMT - 1) / kMT + (T + kMT - 1) / kMT + 2;
 }
 
+// Bounds of the two unit kinds, for the launch grids (the exact counts are
+// known on the device only).  Small units: each holds at least one
+// assignment and an expert has at most two (its remainder <= 32), the
+// shared expert at most two as well.  Big units: the full ones of all
+// assignments (routed and shared), plus at most one partial per expert with
+// more than 32 tokens in its remainder, and the shared expert's.
+static int small_units_max(int T, int K, int E) {
+  const long tk = (long)T * K;
+  return (int)(tk < 2L * E ? tk : 2L * E) + 2;
+}
+static int big_units_max(int T, int K, int E) {
+  const long tk = (long)T * K;
+  const long partial = tk / (2 * kSmallMax + 1);
+  return (int)(tk / kMT + T / kMT + (partial < E ? partial : E) + 1);
+}
+
 // ---------------------------------------------------------------------------
 // rows [T][n] fp32 -> bf16 hi / lo; *need_lo |= 1 when some lo part is nonzero.
 __global__ __launch_bounds__(256) void k_split_rows(const float* __restrict__ x, int64_t count8,
@@ -637,17 +653,23 @@ hipError_t launch_experts_grouped(const LayerDev& L, const uint16_t* xhi, const 
   const GroupArgs g = {L, xhi, xlo, need_lo, off, perm, units, meta, T,
                        hrh, hrl, hsh, hsl, r, rs, status};
   const int nu = group_units_max(T, L.K, L.E);
+  // grids sized by the bound of each unit kind, so that few workgroups
+  // start only to find no unit (each still costs a dispatch and its first
+  // instructions)
+  const int nbig = min(nu, big_units_max(T, L.K, L.E));
+  const int nsmall = min(nu, small_units_max(T, L.K, L.E));
   const int imax = L.I > L.Ish ? L.I : L.Ish;
   // an expert holds at most T tokens (its ids per token are distinct), so
   // units of more than 2 * kSmallMax tokens need T > 2 * kSmallMax
   const bool big = T > 2 * kSmallMax;
   if (big)
-    hipLaunchKernelGGL(k_gu_big, dim3(nu, (imax + 127) / 128), dim3(kGThreads), kBigLds, st, g);
-  hipLaunchKernelGGL(k_gu_small, dim3(nu, (imax + kSmallGuCols - 1) / kSmallGuCols),
+    hipLaunchKernelGGL(k_gu_big, dim3(nbig, (imax + 127) / 128), dim3(kGThreads), kBigLds, st, g);
+  hipLaunchKernelGGL(k_gu_small, dim3(nsmall, (imax + kSmallGuCols - 1) / kSmallGuCols),
                      dim3(kGThreads), 0, st, g);
   if (big)
-    hipLaunchKernelGGL(k_down_big, dim3(nu, (L.H + 255) / 256), dim3(kGThreads), kBigLds, st, g);
-  hipLaunchKernelGGL(k_down_small, dim3(nu, (L.H + kSmallDnRows - 1) / kSmallDnRows),
+    hipLaunchKernelGGL(k_down_big, dim3(nbig, (L.H + 255) / 256), dim3(kGThreads), kBigLds, st,
+                       g);
+  hipLaunchKernelGGL(k_down_small, dim3(nsmall, (L.H + kSmallDnRows - 1) / kSmallDnRows),
                      dim3(kGThreads), 0, st, g);
   return hipGetLastError();
 }
