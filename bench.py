@@ -266,6 +266,8 @@ def main():
         # the drop-in's host-pointer form: copy x in, run, copy y/ids/probs out
         # and synchronise, per token (reported beside value, never as value)
         nh = min(200, a.steps)
+        for t in range(min(5, a.warmup)):  # first calls size the staging buffers
+            blk.forward_arrays(0, x_host[t:t + 1], 1)
         t0 = time.perf_counter()
         for t in range(a.warmup, a.warmup + nh):
             blk.forward_arrays(0, x_host[t:t + 1], 1)

@@ -57,6 +57,27 @@ struct DevBuf {
   }
 };
 
+// Page-locked host memory for the host-pointer calls (hipHostMalloc), so
+// that the copies are single DMA transfers instead of staged ones.
+struct PinBuf {
+  uint8_t* p = nullptr;
+  size_t cap = 0;  // bytes
+  hipError_t ensure(size_t n) {
+    if (n <= cap) return hipSuccess;
+    if (p) (void)hipHostFree(p);
+    p = nullptr;
+    cap = 0;
+    hipError_t e = hipHostMalloc(reinterpret_cast<void**>(&p), n, hipHostMallocDefault);
+    if (e == hipSuccess) cap = n;
+    return e;
+  }
+  void release() {
+    if (p) (void)hipHostFree(p);
+    p = nullptr;
+    cap = 0;
+  }
+};
+
 }  // namespace
 
 struct dmh_ctx {
@@ -66,6 +87,11 @@ struct dmh_ctx {
   // scratch
   DevBuf<float> x, res, y, z, probs, shg, h, xn, hstack;
   DevBuf<int32_t> ids, uids;  // uids: checked expert ids of dmh_experts_forward
+  // host-pointer dmh_moe_forward: inputs [x | residual] and outputs
+  // [y | ids | probs | shared gate | status key], one block each on the
+  // device and page-locked on the host
+  DevBuf<uint8_t> io_in, io_out;
+  PinBuf pin;
   DevBuf<uint8_t> stage;
   // several tokens per call (grouped experts)
   DevBuf<int32_t> g_off, g_perm, g_meta, g_needlo;
@@ -362,6 +388,9 @@ int dmh_destroy(dmh_ctx* c) {
   for (auto* b : fb) b->release();
   c->ids.release();
   c->uids.release();
+  c->io_in.release();
+  c->io_out.release();
+  c->pin.release();
   c->stage.release();
   c->g_off.release();
   c->g_perm.release();
@@ -605,55 +634,68 @@ int dmh_moe_forward(dmh_ctx* c, int layer, const float* x, const float* residual
   const size_t TH = (size_t)T * L.H, TK = (size_t)T * L.K;
   const bool dev = flags & DMH_F_DEVICE;
   hipStream_t st = c->cur;
-  int32_t* dids = dev ? ids : nullptr;
-  float* dprobs = dev ? probs : nullptr;
-  float* dshg = dev ? shg : nullptr;
-  if (!dids) { HIP_TRY(c->ids.ensure(TK)); dids = c->ids.p; }
-  if (!dprobs) { HIP_TRY(c->probs.ensure(TK)); dprobs = c->probs.p; }
-  if (!dshg) { HIP_TRY(c->shg.ensure(T)); dshg = c->shg.p; }
-  const float* dx = x;
-  const float* dres = residual;
-  float* dy = y;
-  if (!dev) {
-    HIP_TRY(c->x.ensure(TH));
-    HIP_TRY(c->y.ensure(TH));
-    HIP_TRY(hipMemcpyAsync(c->x.p, x, TH * 4, hipMemcpyHostToDevice, st));
-    dx = c->x.p;
-    dy = c->y.p;
-    if (residual) {
-      HIP_TRY(c->res.ensure(TH));
-      HIP_TRY(hipMemcpyAsync(c->res.p, residual, TH * 4, hipMemcpyHostToDevice, st));
-      dres = c->res.p;
-    }
-    HIP_TRY(reset_status(c, layer));
+  if (dev) {
+    int32_t* dids = ids;
+    float* dprobs = probs;
+    float* dshg = shg;
+    if (!dids) { HIP_TRY(c->ids.ensure(TK)); dids = c->ids.p; }
+    if (!dprobs) { HIP_TRY(c->probs.ensure(TK)); dprobs = c->probs.p; }
+    if (!dshg) { HIP_TRY(c->shg.ensure(T)); dshg = c->shg.p; }
+    HIP_TRY(run_block(c, Ly, layer, x, residual, T, y, dids, dprobs, dshg));
+    c->last_ids[layer] = dids;
+    c->last_k[layer] = L.K;
+    return DMH_OK;
   }
-  HIP_TRY(run_block(c, Ly, layer, dx, dres, T, dy, dids, dprobs, dshg));
+  // Host pointers: the inputs go through one page-locked block and one
+  // copy, the outputs (with the status key) come back the same way.
+  const size_t in_bytes = align256(TH * 4) + (residual ? TH * 4 : 0);
+  const size_t o_y = 0, o_ids = align256(o_y + TH * 4), o_probs = align256(o_ids + TK * 4),
+               o_shg = align256(o_probs + TK * 4), o_key = align256(o_shg + (size_t)T * 4),
+               out_bytes = o_key + 8;
+  HIP_TRY(c->io_in.ensure(in_bytes));
+  HIP_TRY(c->io_out.ensure(out_bytes));
+  HIP_TRY(c->pin.ensure(align256(in_bytes) + out_bytes));
+  uint8_t* hin = c->pin.p;
+  uint8_t* hout = c->pin.p + align256(in_bytes);
+  memcpy(hin, x, TH * 4);
+  if (residual) memcpy(hin + align256(TH * 4), residual, TH * 4);
+  uint8_t* din = c->io_in.p;
+  uint8_t* dout = c->io_out.p;
+  const float* dx = reinterpret_cast<const float*>(din);
+  const float* dres = residual ? reinterpret_cast<const float*>(din + align256(TH * 4)) : nullptr;
+  float* dy = reinterpret_cast<float*>(dout + o_y);
+  int32_t* dids = reinterpret_cast<int32_t*>(dout + o_ids);
+  float* dprobs = reinterpret_cast<float*>(dout + o_probs);
+  float* dshg = reinterpret_cast<float*>(dout + o_shg);
+  HIP_TRY(hipMemcpyAsync(din, hin, in_bytes, hipMemcpyHostToDevice, st));
+  HIP_TRY(reset_status(c, layer));
+  auto run_and_fetch = [&](bool allow_fused) -> hipError_t {
+    hipError_t e = run_block(c, Ly, layer, dx, dres, T, dy, dids, dprobs, dshg, allow_fused);
+    if (e == hipSuccess)
+      e = hipMemcpyAsync(dout + o_key, c->status + layer, 8, hipMemcpyDeviceToDevice, st);
+    if (e == hipSuccess) e = hipMemcpyAsync(hout, dout, out_bytes, hipMemcpyDeviceToHost, st);
+    if (e == hipSuccess) e = hipStreamSynchronize(st);
+    return e;
+  };
+  HIP_TRY(run_and_fetch(true));
   c->last_ids[layer] = dids;
   c->last_k[layer] = L.K;
-  if (dev) return DMH_OK;
-  std::vector<int32_t> hids(TK);
-  unsigned long long key = 0;
-  HIP_TRY(hipMemcpyAsync(y, dy, TH * 4, hipMemcpyDeviceToHost, st));
-  HIP_TRY(hipMemcpyAsync(hids.data(), dids, TK * 4, hipMemcpyDeviceToHost, st));
-  if (probs) HIP_TRY(hipMemcpyAsync(probs, dprobs, TK * 4, hipMemcpyDeviceToHost, st));
-  if (shg) HIP_TRY(hipMemcpyAsync(shg, dshg, (size_t)T * 4, hipMemcpyDeviceToHost, st));
-  HIP_TRY(hipMemcpyAsync(&key, c->status + layer, sizeof(key), hipMemcpyDeviceToHost, st));
-  HIP_TRY(hipStreamSynchronize(st));
+  unsigned long long key;
+  memcpy(&key, hout + o_key, 8);
   if (dm::key_phase(key) == dm::kPhExpert && dm::key_kind(key) == dm::kEkRecheck) {
     // The fused kernel folds the routed and shared down projections into one
     // sum, so a non-finite output does not say which check of the reference
     // fires first; the multi-kernel path keeps them apart and re-derives it.
     HIP_TRY(reset_status(c, layer));
-    HIP_TRY(run_block(c, Ly, layer, dx, dres, T, dy, dids, dprobs, dshg, false));
-    HIP_TRY(hipMemcpyAsync(y, dy, TH * 4, hipMemcpyDeviceToHost, st));
-    HIP_TRY(hipMemcpyAsync(hids.data(), dids, TK * 4, hipMemcpyDeviceToHost, st));
-    if (probs) HIP_TRY(hipMemcpyAsync(probs, dprobs, TK * 4, hipMemcpyDeviceToHost, st));
-    if (shg) HIP_TRY(hipMemcpyAsync(shg, dshg, (size_t)T * 4, hipMemcpyDeviceToHost, st));
-    HIP_TRY(hipMemcpyAsync(&key, c->status + layer, sizeof(key), hipMemcpyDeviceToHost, st));
-    HIP_TRY(hipStreamSynchronize(st));
+    HIP_TRY(run_and_fetch(false));
+    memcpy(&key, hout + o_key, 8);
   }
-  if (ids) memcpy(ids, hids.data(), TK * 4);
-  int rc = finish_status(c, Ly, layer, key, hids.data(), err, errlen);
+  memcpy(y, hout + o_y, TH * 4);
+  if (ids) memcpy(ids, hout + o_ids, TK * 4);
+  if (probs) memcpy(probs, hout + o_probs, TK * 4);
+  if (shg) memcpy(shg, hout + o_shg, (size_t)T * 4);
+  int rc = finish_status(c, Ly, layer, key, reinterpret_cast<const int32_t*>(hout + o_ids), err,
+                         errlen);
   if (rc) HIP_TRY(reset_status(c, layer));
   return rc;
 }
