@@ -6,8 +6,13 @@ decode: every step is one token's full MoE block (router, 8 routed experts,
 shared expert, combine) with a fresh activation, launched in sequence.
 Inputs are resident in HBM before the timed region.  Prints one JSON line.
 
-  python bench.py [--steps K] [--warmup W] [--workload decode|toy|stack]
+  python bench.py [--steps K] [--warmup W] [--workload decode|toy|stack|gguf]
                   [--cpu-sample-s S] [--no-cpu]
+
+--workload gguf: one layer's routed expert projection in the reference's GGUF
+format (256 experts x 2048 x 512 weights, --gguf-type q3_k|q4_k|q8_0)
+dequantized to fp32 in HBM, the work src/layers/gguf_port_loader.mojo:217-236
+repeats for every layer of every token.
 """
 import argparse
 import json
@@ -23,11 +28,12 @@ HBM_PEAK_GBPS = 8000.0
 # HBM bytes per launch of the decode kernel from the rocprofv3 FETCH_SIZE and
 # WRITE_SIZE runs (scaled by a copy-kernel calibration) recorded in this file
 TRAFFIC_PROFILE = os.path.join("profiles", "k_moe_decode_qwen36_layer_decode.md")
+GGUF_PROFILE = os.path.join("profiles", "k_dequant_gguf_q3k_expert_layer.md")
 
 
-def profiled_traffic():
+def profiled_traffic(profile=TRAFFIC_PROFILE):
     try:
-        with open(os.path.join(ROOT, TRAFFIC_PROFILE)) as f:
+        with open(os.path.join(ROOT, profile)) as f:
             for line in f:
                 if line.startswith("traffic_bytes_per_launch:"):
                     return int(line.split(":")[1])
@@ -42,7 +48,7 @@ def parse():
     ap.add_argument("--steps", type=int, default=1000)
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--workload", default="decode",
-                    choices=["decode", "toy", "stack", "batch", "prefill", "copy"],
+                    choices=["decode", "toy", "stack", "batch", "prefill", "copy", "gguf"],
                     help="batch: --batch tokens per call (ragged small-batch decode); "
                          "prefill: --tokens per call with Zipf-skewed routing; "
                          "copy: a plain device copy of --copy-mib MiB, the calibration "
@@ -52,6 +58,7 @@ def parse():
     ap.add_argument("--zipf-s", type=float, default=1.1, help="prefill router skew exponent")
     ap.add_argument("--copy-mib", type=int, default=256)
     ap.add_argument("--layers", type=int, default=40, help="stack workload depth")
+    ap.add_argument("--gguf-type", default="q3_k", choices=["q3_k", "q4_k", "q8_0"])
     ap.add_argument("--cpu-sample-s", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--seed", type=int, default=1)
@@ -181,6 +188,70 @@ def grouped(a, blk, stream, dev):
     print(json.dumps(out))
 
 
+GGUF_TYPES = {"q3_k": (11, 256, 114, 112), "q4_k": (12, 256, 144, 0), "q8_0": (8, 32, 34, 0)}
+
+
+def gguf_layer(a, blk, stream, dev):
+    """256 experts x 2048 x 512 weights of one GGUF type -> fp32, resident in HBM."""
+    import numpy as np
+    import torch
+
+    from dismoen import gguf
+    t, bs, bpb, d_off = GGUF_TYPES[a.gguf_type]
+    E, H, I = 256, 2048, 512
+    n = E * H * I
+    nb = n // bs
+    g = torch.Generator(device=dev).manual_seed(a.seed)
+    raw = torch.randint(0, 256, (nb, bpb), dtype=torch.uint8, device=dev, generator=g)
+    raw[:, d_off + 1] %= 0x7C  # finite fp16 super-scales
+    out = torch.empty(n, dtype=torch.float32, device=dev)
+    torch.cuda.synchronize()
+
+    def launch():
+        gguf.dequantize_device(t, raw.data_ptr(), nb * bpb, n, out.data_ptr(), blk)
+
+    for _ in range(a.warmup):
+        launch()
+    blk.sync()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(a.steps):
+        launch()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    blk.sync()
+    ms = e0.elapsed_time(e1) / a.steps
+    alg = nb * bpb + n * 4
+    gbps = alg / (ms * 1e-3) / 1e9
+    rec = {"metric": f"GGUF {a.gguf_type.upper()} expert-layer dequant µs + achieved HBM GB/s",
+           "value": round(ms * 1e3, 2), "unit": "us/layer", "n_gpus": 1, "steps": a.steps,
+           "warmup": a.warmup, "ms_per_step": round(ms, 6), "higher_is_better": False,
+           "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+           "config": {"workload": f"gguf {a.gguf_type} dequant, 256 experts x 2048 x 512 "
+                                  "weights to fp32", "weights": n, "payload_bytes": nb * bpb},
+           "roofline": {"bound": "hbm", "kernel": f"k_dequant_gguf<{t}>", "achieved": round(gbps, 1),
+                        "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(gbps / HBM_PEAK_GBPS, 4),
+                        "traffic": profiled_traffic(GGUF_PROFILE) if t == 11 else None,
+                        "bytes_per_launch": alg}}
+    if not a.no_cpu:
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        import oracle as orc
+        host = raw[:max(1, nb // 32)].cpu().numpy()  # 8 of the 256 experts
+        t0 = time.perf_counter()
+        reps = 0
+        while True:
+            orc.dequant_gguf(t, host.ravel(), host.shape[0] * bs)
+            reps += 1
+            if time.perf_counter() - t0 > min(a.cpu_sample_s, 10.0):
+                break
+        per = (time.perf_counter() - t0) / reps * (nb / host.shape[0])
+        rec["cpu_baseline"] = {"value": round(per * 1e6, 1), "unit": "us/layer", "cores": 1,
+                               "kind": "port",
+                               "sample": f"{host.shape[0]} blocks (8 experts) x {reps} passes, "
+                                         "scaled to 256 experts"}
+    print(json.dumps(rec))
+
+
 def main():
     a = parse()
     if a.gpus != 1:
@@ -216,6 +287,10 @@ def main():
     blk = MoEBlock(0)
     # time on the library's own stream (the stream every launch goes to)
     stream = torch.cuda.ExternalStream(blk.stream(), device=dev)
+    if a.workload == "gguf":
+        gguf_layer(a, blk, stream, dev)
+        blk.close()
+        return
 
     if a.workload in ("decode", "toy"):
         cfg = synth.CONFIG_QWEN36 if a.workload == "decode" else synth.CONFIG_TOY

@@ -11,6 +11,7 @@
 
 #include "../../include/dismoen_hip.h"
 #include "dm_decode.h"
+#include "dm_gguf.h"
 #include "dm_grouped.h"
 #include "dm_kernels.h"
 #include "dm_layout.h"
@@ -880,6 +881,54 @@ int dmh_dequant_q4_bf16(dmh_ctx* c, const uint16_t* scales, int64_t n_scales,
                    (unsigned long long)(vk >> 1));
   return set_err(err, errlen, DMH_ERR_DEQUANT, "dequant_kernel: scale is NaN or Inf at group %llu",
                  (unsigned long long)(vk >> 1));
+}
+
+}  // extern "C"
+
+// GGUF payload -> fp32 on the context's stream; raw and out each in host or
+// device memory.  Shared by dmh_dequant_gguf and dmh_gguf_stream_tensor_f32.
+int dm::api_dequant_gguf(dmh_ctx* c, int t, const void* raw, bool raw_dev, int64_t raw_bytes,
+                         int64_t n, float* out, bool out_dev, int layout, char* err,
+                         size_t errlen) {
+  int bs = 0, bpb = 0;
+  if (dm::gguf_block_spec(t, &bs, &bpb))
+    return set_err(err, errlen, DMH_ERR_FORMAT, "GGUF_UNSUPPORTED_DTYPE: unsupported GGML type %d",
+                   t);
+  if (!c || !raw || !out || n < 0 || raw_bytes < 0)
+    return set_err(err, errlen, DMH_ERR_INVALID_ARG, "dmh_dequant_gguf: invalid argument");
+  if (n == 0) return DMH_OK;
+  const int64_t need = n / bs * bpb;
+  if (raw_bytes < need)
+    return set_err(err, errlen, DMH_ERR_INVALID_ARG,
+                   "dmh_dequant_gguf: %lld payload bytes < %lld for %lld weights",
+                   (long long)raw_bytes, (long long)need, (long long)n);
+  if ((raw_dev && ((uintptr_t)raw & 3)) || (out_dev && ((uintptr_t)out & 15)))
+    return set_err(err, errlen, DMH_ERR_INVALID_ARG,
+                   "dmh_dequant_gguf: device raw must be 4-byte and out 16-byte aligned");
+  HIP_TRY(hipSetDevice(c->device));
+  hipStream_t st = c->cur;
+  const size_t rb = raw_dev ? 0 : align256((size_t)(need > 0 ? need : 1));
+  HIP_TRY(c->stage.ensure(rb + (out_dev ? 0 : (size_t)n * 4)));
+  const uint8_t* draw = static_cast<const uint8_t*>(raw);
+  float* dout = out;
+  if (!raw_dev) {
+    if (need > 0) HIP_TRY(hipMemcpyAsync(c->stage.p, raw, (size_t)need, hipMemcpyHostToDevice, st));
+    draw = c->stage.p;
+  }
+  if (!out_dev) dout = reinterpret_cast<float*>(c->stage.p + rb);
+  HIP_TRY(dm::launch_dequant_gguf(t, draw, n, layout, dout, st));
+  if (!out_dev) HIP_TRY(hipMemcpyAsync(out, dout, (size_t)n * 4, hipMemcpyDeviceToHost, st));
+  if (!(raw_dev && out_dev)) HIP_TRY(hipStreamSynchronize(st));
+  return DMH_OK;
+}
+
+extern "C" {
+
+int dmh_dequant_gguf(dmh_ctx* c, int t, const void* raw, int64_t raw_bytes, int64_t n, float* out,
+                     unsigned flags, char* err, size_t errlen) {
+  const bool dev = flags & DMH_F_DEVICE;
+  return dm::api_dequant_gguf(c, t, raw, dev, raw_bytes, n, out, dev,
+                              (flags & DMH_F_Q4K_PY_SCALES) ? 1 : 0, err, errlen);
 }
 
 int dmh_experts_forward(dmh_ctx* c, int layer, const float* x, int T, const int32_t* ids,

@@ -8,12 +8,16 @@
 
 #include "../../include/dismoen_hip.h"
 #include "dm_formats.h"
+#include "dm_gguf.h"
 
 struct dmh_quant_file {
   dm::QuantFile f;
 };
 struct dmh_st_file {
   dm::SafetensorsFile f;
+};
+struct dmh_gguf_file {
+  dm::GgufFile f;
 };
 
 namespace {
@@ -265,6 +269,104 @@ int dmh_upload_moe_layer_files(dmh_ctx* ctx, int layer, const dmh_moe_dims* d,
   dmh_moe_weights w = {router.data(), shgate.data(), gus.data(), gup.data(), ds.data(),
                        dp.data(),     sgus.data(),   sgup.data(), sds.data(), sdp.data()};
   return dmh_upload_moe_layer(ctx, layer, d, &w, 0, err, errlen);
+}
+
+int dmh_gguf_open(const char* path, dmh_gguf_file** out, char* err, size_t errlen) {
+  if (!path || !out) return put_err(err, errlen, DMH_ERR_INVALID_ARG, "dmh_gguf_open: NULL argument");
+  *out = nullptr;
+  dmh_gguf_file* h = new dmh_gguf_file();
+  std::string e;
+  if (!dm::parse_gguf_index(path, &h->f, &e)) {
+    delete h;
+    return put_err(err, errlen, DMH_ERR_FORMAT, e);
+  }
+  *out = h;
+  return DMH_OK;
+}
+
+void dmh_gguf_close(dmh_gguf_file* f) { delete f; }
+
+int dmh_gguf_get_header(const dmh_gguf_file* f, dmh_gguf_header* h) {
+  if (!f || !h) return DMH_ERR_INVALID_ARG;
+  h->version = f->f.version;
+  h->tensor_count = f->f.tensor_count;
+  h->metadata_kv_count = f->f.metadata_kv_count;
+  h->data_section_offset = f->f.data_section_offset;
+  h->expected_file_size = f->f.expected_file_size;
+  h->alignment = f->f.alignment;
+  return DMH_OK;
+}
+
+int dmh_gguf_num_tensors(const dmh_gguf_file* f) { return f ? (int)f->f.tensors.size() : -1; }
+
+int dmh_gguf_find(const dmh_gguf_file* f, const char* name) {
+  return (f && name) ? f->f.find(name) : -1;
+}
+
+int dmh_gguf_tensor_info(const dmh_gguf_file* f, int idx, dmh_gguf_tensor* info) {
+  if (!f || !info || idx < 0 || idx >= (int)f->f.tensors.size()) return DMH_ERR_INVALID_ARG;
+  const dm::GgufTensor& t = f->f.tensors[idx];
+  memset(info, 0, sizeof(*info));
+  info->name = t.name.c_str();
+  info->ndim = (int32_t)t.dims.size();
+  for (size_t i = 0; i < t.dims.size() && i < 8; ++i) info->dims[i] = t.dims[i];
+  info->ggml_type = t.type;
+  info->offset = t.offset;
+  info->file_offset = f->f.data_section_offset + t.offset;
+  info->num_elements = t.num_elements;
+  info->raw_bytes = t.raw_bytes;
+  return DMH_OK;
+}
+
+const char* dmh_gguf_metadata(const dmh_gguf_file* f, const char* key) {
+  if (!f || !key) return nullptr;
+  const std::string* v = f->f.meta(key);
+  return v ? v->c_str() : nullptr;
+}
+
+int dmh_gguf_read(const dmh_gguf_file* f, int idx, void* out, int64_t bytes, char* err,
+                  size_t errlen) {
+  if (!f || !out || idx < 0 || idx >= (int)f->f.tensors.size())
+    return put_err(err, errlen, DMH_ERR_INVALID_ARG, "dmh_gguf_read: bad arguments");
+  const dm::GgufTensor& t = f->f.tensors[idx];
+  if (bytes != t.raw_bytes)
+    return put_err(err, errlen, DMH_ERR_INVALID_ARG,
+                   "dmh_gguf_read: buffer of " + std::to_string(bytes) + " bytes, tensor has " +
+                       std::to_string(t.raw_bytes));
+  std::vector<uint8_t> raw;
+  std::string e;
+  if (!dm::read_gguf_tensor(f->f, idx, &raw, &e)) return put_err(err, errlen, DMH_ERR_WEIGHT, e);
+  memcpy(out, raw.data(), raw.size());
+  return DMH_OK;
+}
+
+// stream_gguf_tensor_f32 (src/format/gguf.mojo:563-626): lookup, read, then
+// the type check, in the reference's order.
+int dmh_gguf_stream_tensor_f32(dmh_ctx* ctx, const dmh_gguf_file* f, const char* name, float* out,
+                               int64_t n_out, unsigned flags, char* err, size_t errlen) {
+  if (!ctx || !f || !name || !out)
+    return put_err(err, errlen, DMH_ERR_INVALID_ARG, "dmh_gguf_stream_tensor_f32: NULL argument");
+  const int idx = f->f.find(name);
+  if (idx < 0)
+    return put_err(err, errlen, DMH_ERR_WEIGHT,
+                   std::string("{\"error_type\":\"WEIGHT_LOAD_FAILED\",\"detail\":\"tensor not "
+                               "found in GGUF index\",\"tensor\":\"") + name + "\"}");
+  const dm::GgufTensor& t = f->f.tensors[idx];
+  std::vector<uint8_t> raw;
+  std::string e;
+  if (!dm::read_gguf_tensor(f->f, idx, &raw, &e)) return put_err(err, errlen, DMH_ERR_WEIGHT, e);
+  int bs, bpb;
+  if (dm::gguf_block_spec(t.type, &bs, &bpb))
+    return put_err(err, errlen, DMH_ERR_FORMAT,
+                   "GGUF_UNSUPPORTED_DTYPE: unsupported GGML type " + std::to_string(t.type) +
+                       " for tensor " + t.name);
+  if (n_out != t.num_elements)
+    return put_err(err, errlen, DMH_ERR_INVALID_ARG,
+                   "dmh_gguf_stream_tensor_f32: output of " + std::to_string(n_out) +
+                       " elements, tensor has " + std::to_string(t.num_elements));
+  return dm::api_dequant_gguf(ctx, t.type, raw.data(), false, (int64_t)raw.size(),
+                              t.num_elements, out, (flags & DMH_F_DEVICE) != 0,
+                              (flags & DMH_F_Q4K_PY_SCALES) ? 1 : 0, err, errlen);
 }
 
 }  // extern "C"

@@ -1,0 +1,69 @@
+// dm_gguf.h -- GGUF container index (host) and the payload dequantizer (GPU).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <string>
+#include <unordered_map>
+#include <utility>
+#include <vector>
+
+struct dmh_ctx;
+
+namespace dm {
+
+// GGML type codes of src/format/gguf.mojo:19-30 that have a dequantizer.
+constexpr int kGgmlF32 = 0;
+constexpr int kGgmlQ8_0 = 8;
+constexpr int kGgmlQ3_K = 11;
+constexpr int kGgmlQ4_K = 12;
+constexpr int kGgmlBF16 = 30;
+
+// (block_size, bytes_per_block) of a type with a dequantizer; -1 otherwise.
+int gguf_block_spec(int ggml_type, int* block_size, int* bytes_per_block);
+
+// out[0, n) = the fp32 values of the payload raw (device memory, 4-byte
+// aligned; out 16-byte aligned) of n weights of ggml_type; elements past the
+// last whole block are 0.0.  q4k_layout 1 selects the scale packing of the
+// reference's Python twin for Q4_K sub-blocks 4..7.
+hipError_t launch_dequant_gguf(int ggml_type, const uint8_t* raw, int64_t n, int q4k_layout,
+                               float* out, hipStream_t st);
+
+// GGUFTensorInfo (gguf.mojo:104-114); offset is relative to the data section.
+struct GgufTensor {
+  std::string name;
+  std::vector<int64_t> dims;
+  int type = 0;
+  int64_t offset = 0, num_elements = 0, raw_bytes = 0;
+};
+
+// GGUFIndex (gguf.mojo:117-141).
+struct GgufFile {
+  std::string path;
+  int64_t filesize = 0;
+  int version = 0;
+  int64_t tensor_count = 0, metadata_kv_count = 0;
+  int64_t data_section_offset = 0, expected_file_size = 0, alignment = 32;
+  std::vector<GgufTensor> tensors;
+  std::unordered_map<std::string, int> tensor_map;           // name -> last index
+  std::vector<std::pair<std::string, std::string>> metadata;  // first-seen order
+  std::unordered_map<std::string, size_t> meta_pos;
+  int find(const std::string& name) const;
+  const std::string* meta(const std::string& key) const;
+};
+
+// parse_gguf_index (gguf.mojo:257-411): header, metadata, tensor directory
+// and the exact-size rule; err receives the reference's text.
+bool parse_gguf_index(const std::string& path, GgufFile* out, std::string* err);
+
+// The raw payload of tensor idx (raw_bytes bytes) read from the file; the
+// truncated-read text of stream_gguf_tensor_f32 (gguf.mojo:586-596).
+bool read_gguf_tensor(const GgufFile& f, int idx, std::vector<uint8_t>* out, std::string* err);
+
+// The body of dmh_dequant_gguf with the memory kind of raw and out given
+// separately (defined in dm_api.cpp).
+int api_dequant_gguf(::dmh_ctx* c, int ggml_type, const void* raw, bool raw_dev,
+                     int64_t raw_bytes, int64_t n, float* out, bool out_dev, int q4k_layout,
+                     char* err, size_t errlen);
+
+}  // namespace dm

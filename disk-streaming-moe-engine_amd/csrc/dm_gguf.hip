@@ -1,0 +1,174 @@
+// dm_gguf.hip -- GGUF tensor payloads to fp32 on the GPU: the Q8_0, Q4_K and
+// Q3_K block layouts of src/format/gguf.mojo:414-560 and the F32 / BF16
+// branches of stream_gguf_tensor_f32 (gguf.mojo:598-613).
+//
+// Byte work, bound by HBM: per 256 weights a Q3_K block reads 114 B and
+// writes 1 KiB of fp32, so the stores are 90% of the traffic.  Each thread
+// produces 4 consecutive outputs and the lanes of a wave consecutive float4s,
+// so every (non-temporal) store instruction fills whole cache lines: with 8
+// outputs per thread as two float4 stores, each instruction left every line
+// half written and the kernel ran at a third of this rate.  The block header
+// bytes that neighbouring threads share come from the lines just fetched.
+// No status: the reference's dequantizers accept every byte pattern
+// (non-finite super-scales propagate as IEEE products).
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "dm_gguf.h"
+
+namespace dm {
+namespace {
+
+__device__ __forceinline__ float h2f(uint32_t h) {
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
+}
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// The 4 outputs at element e0 (a multiple of 4) of a type whose whole
+// blocks cover them.
+template <int T>
+__device__ __forceinline__ f32x4 values4(const uint8_t* raw, int64_t e0, int layout) {
+  f32x4 v;
+  if constexpr (T == kGgmlQ8_0) {
+    // 34-byte blocks: fp16 d, 32 int8 codes
+    const uint8_t* blk = raw + (e0 >> 5) * 34;
+    const uint16_t* h = reinterpret_cast<const uint16_t*>(blk);
+    const float d = h2f(h[0]);
+    const int r = (int)(e0 & 31);
+    const uint32_t w0 = h[1 + (r >> 1)], w1 = h[2 + (r >> 1)];
+    v.x = d * (float)(int8_t)(w0 & 0xFF);
+    v.y = d * (float)(int8_t)(w0 >> 8);
+    v.z = d * (float)(int8_t)(w1 & 0xFF);
+    v.w = d * (float)(int8_t)(w1 >> 8);
+  } else if constexpr (T == kGgmlQ4_K) {
+    // 144-byte blocks: fp16 d, fp16 dmin, 12 packed scale/min bytes, 128
+    // code bytes; sub-block j holds 32 weights in code bytes 16j..16j+15,
+    // the low nibbles first
+    const uint8_t* blk = raw + (e0 >> 8) * 144;
+    const uint32_t* w32 = reinterpret_cast<const uint32_t*>(blk);
+    const int e = (int)(e0 & 255), j = e >> 5, r = e & 31;
+    auto qb = [&](int i) -> int { return (int)((w32[1 + (i >> 2)] >> ((i & 3) * 8)) & 0xFF); };
+    int sc, mn;
+    if (j < 4) {
+      sc = qb(j) & 63;
+      mn = qb(j + 4) & 63;
+    } else {
+      // gguf.mojo:482-488 takes the low bits from byte j of the packed
+      // scales; the reference's Python twin (oracle_port.py:104-110) from j+4
+      const int lo = layout ? qb(j + 4) : qb(j);
+      sc = (lo & 15) | ((qb(j - 4) >> 6) << 4);
+      mn = (lo >> 4) | ((qb(j) >> 6) << 4);
+    }
+    const uint32_t hd = w32[0];
+    const float fs = (float)sc * h2f(hd & 0xFFFF);
+    const float fm = (float)mn * h2f(hd >> 16);
+    const uint32_t c = w32[(16 + j * 16 + (r & 15)) >> 2] >> (r < 16 ? 0 : 4);
+    v.x = fs * (float)(c & 15) - fm;
+    v.y = fs * (float)((c >> 8) & 15) - fm;
+    v.z = fs * (float)((c >> 16) & 15) - fm;
+    v.w = fs * (float)((c >> 24) & 15) - fm;
+  } else if constexpr (T == kGgmlQ3_K) {
+    // 114-byte blocks: hmask[32] (bit e of the 256), qs[64] (2 bits each),
+    // 16 scale bytes (value - 32), fp16 d at 112
+    const uint8_t* blk = raw + (e0 >> 8) * 114;
+    const int e = (int)(e0 & 255);
+    const uint32_t hm = blk[e >> 3] >> (e & 7);
+    const uint32_t qs = blk[32 + (e >> 2)];
+    const float fs = (float)((int)blk[96 + (e >> 4)] - 32) *
+                     h2f(reinterpret_cast<const uint16_t*>(blk)[56]);
+    v.x = fs * (float)((int)(((hm & 1) << 2) | (qs & 3)) - 4);
+    v.y = fs * (float)((int)((((hm >> 1) & 1) << 2) | ((qs >> 2) & 3)) - 4);
+    v.z = fs * (float)((int)((((hm >> 2) & 1) << 2) | ((qs >> 4) & 3)) - 4);
+    v.w = fs * (float)((int)((((hm >> 3) & 1) << 2) | ((qs >> 6) & 3)) - 4);
+  } else if constexpr (T == kGgmlBF16) {
+    const uint32_t* w = reinterpret_cast<const uint32_t*>(raw + e0 * 2);
+    const uint32_t a = w[0], b = w[1];
+    v.x = __builtin_bit_cast(float, a << 16);
+    v.y = __builtin_bit_cast(float, a & 0xFFFF0000u);
+    v.z = __builtin_bit_cast(float, b << 16);
+    v.w = __builtin_bit_cast(float, b & 0xFFFF0000u);
+  } else {  // F32
+    const float* f = reinterpret_cast<const float*>(raw) + e0;
+    v.x = f[0];
+    v.y = f[1];
+    v.z = f[2];
+    v.w = f[3];
+  }
+  return v;
+}
+
+// n outputs; whole blocks cover n_blk of them (a multiple of 32 for the
+// block types, n for F32 / BF16), the rest is 0.0.  Thread f writes elements
+// 4f .. 4f+3; the last float4 may be partial.
+template <int T>
+__global__ __launch_bounds__(256) void k_dequant_gguf(const uint8_t* __restrict__ raw,
+                                                      int64_t n, int64_t n_blk, int layout,
+                                                      float* __restrict__ out) {
+  // Workgroups are dispatched round-robin over the 8 XCDs, each with its own
+  // L2.  For the K-quant types give XCD x one contiguous run of the
+  // workgroup range, so that a 114- or 144-byte block straddling two
+  // workgroups' ranges is fetched once, not once per XCD (Q3_K: 1.26x ->
+  // 1.0x of the payload bytes; measured slower for Q8_0, which keeps the
+  // plain order).
+  uint32_t wg = blockIdx.x;
+  if constexpr (T == kGgmlQ3_K || T == kGgmlQ4_K) {
+    const uint32_t G = gridDim.x, q = G >> 3, r = G & 7;
+    const uint32_t x = blockIdx.x & 7, pos = blockIdx.x >> 3;
+    wg = x * q + (x < r ? x : r) + pos;
+  }
+  const int64_t f = (int64_t)wg * 256 + threadIdx.x;
+  const int64_t e0 = f * 4;
+  if (e0 >= n) return;
+  f32x4 v = {0.0f, 0.0f, 0.0f, 0.0f};
+  if (e0 + 4 <= n_blk) {
+    v = values4<T>(raw, e0, layout);
+  } else if (e0 < n_blk) {  // F32 / BF16 tail, element by element
+    for (int i = 0; i < 4 && e0 + i < n_blk; ++i) {
+      float x;
+      if constexpr (T == kGgmlBF16)
+        x = __builtin_bit_cast(float, (uint32_t)reinterpret_cast<const uint16_t*>(raw)[e0 + i] << 16);
+      else
+        x = reinterpret_cast<const float*>(raw)[e0 + i];
+      v[i] = x;
+    }
+  }
+  if (e0 + 4 <= n) {
+    __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(out + e0));
+  } else {
+    for (int i = 0; i < 4 && e0 + i < n; ++i) out[e0 + i] = v[i];
+  }
+}
+
+}  // namespace
+
+int gguf_block_spec(int t, int* bs, int* bpb) {
+  switch (t) {
+    case kGgmlF32: *bs = 1; *bpb = 4; return 0;
+    case kGgmlBF16: *bs = 1; *bpb = 2; return 0;
+    case kGgmlQ8_0: *bs = 32; *bpb = 34; return 0;
+    case kGgmlQ4_K: *bs = 256; *bpb = 144; return 0;
+    case kGgmlQ3_K: *bs = 256; *bpb = 114; return 0;
+    default: return -1;
+  }
+}
+
+hipError_t launch_dequant_gguf(int t, const uint8_t* raw, int64_t n, int layout, float* out,
+                               hipStream_t st) {
+  int bs = 0, bpb = 0;
+  if (gguf_block_spec(t, &bs, &bpb) || n <= 0) return hipErrorInvalidValue;
+  const int64_t n_blk = n / bs * bs;
+  const int64_t quads = (n + 3) / 4;
+  if ((quads + 255) / 256 > 0x7FFFFFFF) return hipErrorInvalidValue;
+  const dim3 grid((unsigned)((quads + 255) / 256)), block(256);
+  switch (t) {
+    case kGgmlQ8_0: k_dequant_gguf<kGgmlQ8_0><<<grid, block, 0, st>>>(raw, n, n_blk, layout, out); break;
+    case kGgmlQ4_K: k_dequant_gguf<kGgmlQ4_K><<<grid, block, 0, st>>>(raw, n, n_blk, layout, out); break;
+    case kGgmlQ3_K: k_dequant_gguf<kGgmlQ3_K><<<grid, block, 0, st>>>(raw, n, n_blk, layout, out); break;
+    case kGgmlBF16: k_dequant_gguf<kGgmlBF16><<<grid, block, 0, st>>>(raw, n, n_blk, layout, out); break;
+    default: k_dequant_gguf<kGgmlF32><<<grid, block, 0, st>>>(raw, n, n_blk, layout, out); break;
+  }
+  return hipGetLastError();
+}
+
+}  // namespace dm

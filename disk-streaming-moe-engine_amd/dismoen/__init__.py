@@ -5,4 +5,4 @@ package is the host-side binding that mirrors the reference's layer API.
 """
 from ._lib import DismoenError, LIB_PATH, lib  # noqa: F401
 from .layers import MoEBlock, RouterConfig, RoutingInfo  # noqa: F401
-from . import formats, synth  # noqa: F401
+from . import formats, gguf, synth  # noqa: F401

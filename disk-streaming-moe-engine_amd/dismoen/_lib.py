@@ -12,6 +12,7 @@ PKG_ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 LIB_PATH = os.path.join(PKG_ROOT, "libdismoen_hip.so")
 
 DMH_F_DEVICE = 0x1
+DMH_F_Q4K_PY_SCALES = 0x10
 
 ERROR_NAMES = {
     1: "INVALID_ARG", 2: "CONFIG", 3: "HIP", 4: "NO_MEMORY", 5: "DEQUANT", 6: "ACT",
@@ -27,7 +28,9 @@ EXPORTS = (
     "dmh_quant_tensor_info", "dmh_quant_read", "dmh_st_open", "dmh_st_close",
     "dmh_st_num_tensors", "dmh_st_find", "dmh_st_tensor_info", "dmh_st_read",
     "dmh_upload_moe_layer_files", "dmh_experts_forward", "dmh_shared_gate_forward",
-    "dmh_moe_aggregate",
+    "dmh_moe_aggregate", "dmh_gguf_open", "dmh_gguf_close", "dmh_gguf_get_header",
+    "dmh_gguf_num_tensors", "dmh_gguf_find", "dmh_gguf_tensor_info", "dmh_gguf_metadata",
+    "dmh_gguf_read", "dmh_dequant_gguf", "dmh_gguf_stream_tensor_f32",
 )
 
 
@@ -50,6 +53,18 @@ class DmhTensorInfo(C.Structure):
                 ("data_offset", C.c_int64), ("data_bytes", C.c_int64)]
 
 
+class DmhGgufTensor(C.Structure):
+    _fields_ = [("name", C.c_char_p), ("ndim", C.c_int32), ("dims", C.c_int64 * 8),
+                ("ggml_type", C.c_int32), ("offset", C.c_int64), ("file_offset", C.c_int64),
+                ("num_elements", C.c_int64), ("raw_bytes", C.c_int64)]
+
+
+class DmhGgufHeader(C.Structure):
+    _fields_ = [("version", C.c_int32), ("tensor_count", C.c_int64),
+                ("metadata_kv_count", C.c_int64), ("data_section_offset", C.c_int64),
+                ("expected_file_size", C.c_int64), ("alignment", C.c_int64)]
+
+
 class DismoenError(RuntimeError):
     """A nonzero status from the library; str() is the reference's error text."""
 
@@ -68,6 +83,14 @@ def lib():
         return _lib
     if not os.path.exists(LIB_PATH):
         raise RuntimeError(f"libdismoen_hip.so not built ({LIB_PATH}); run __graft_entry__.build()")
+    # One HIP runtime per process.  torch ships its own libamdhip64.so.7; the
+    # library binds to whichever copy of that soname is loaded first, and
+    # torch does not find a GPU through a runtime of another ROCm release.
+    # Loading torch first makes both share torch's.
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
     L = C.CDLL(LIB_PATH)
     vp, sz, i32, i64, u32 = C.c_void_p, C.c_size_t, C.c_int, C.c_int64, C.c_uint
     L.dmh_version.restype = C.c_char_p
@@ -102,6 +125,18 @@ def lib():
     L.dmh_shared_gate_forward.argtypes = [vp, i32, vp, i32, vp, u32, C.c_char_p, sz]
     L.dmh_moe_aggregate.argtypes = [vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, vp, u32,
                                     C.c_char_p, sz]
+    L.dmh_gguf_open.argtypes = [C.c_char_p, C.POINTER(vp), C.c_char_p, sz]
+    L.dmh_gguf_close.argtypes = [vp]
+    L.dmh_gguf_close.restype = None
+    L.dmh_gguf_get_header.argtypes = [vp, C.POINTER(DmhGgufHeader)]
+    L.dmh_gguf_num_tensors.argtypes = [vp]
+    L.dmh_gguf_find.argtypes = [vp, C.c_char_p]
+    L.dmh_gguf_tensor_info.argtypes = [vp, i32, C.POINTER(DmhGgufTensor)]
+    L.dmh_gguf_metadata.argtypes = [vp, C.c_char_p]
+    L.dmh_gguf_metadata.restype = C.c_char_p
+    L.dmh_gguf_read.argtypes = [vp, i32, vp, i64, C.c_char_p, sz]
+    L.dmh_dequant_gguf.argtypes = [vp, i32, vp, i64, i64, vp, u32, C.c_char_p, sz]
+    L.dmh_gguf_stream_tensor_f32.argtypes = [vp, vp, C.c_char_p, vp, i64, u32, C.c_char_p, sz]
     _lib = L
     return L
 

@@ -250,6 +250,80 @@ int dmh_upload_moe_layer_files(dmh_ctx* ctx, int layer, const dmh_moe_dims* dims
                                const dmh_quant_file* quant, const dmh_st_file* shard,
                                int model_layer, char* err, size_t errlen);
 
+/* ---- GGUF ------------------------------------------------------------------
+ * The container and the expert formats of the reference's Qwen3.6 port
+ * decode (src/format/gguf.mojo, read by src/layers/gguf_port_loader.mojo).
+ * GGML type codes with a dequantizer: */
+#define DMH_GGML_F32 0
+#define DMH_GGML_Q8_0 8   /* 32 weights in 34 bytes: fp16 d, 32 int8 */
+#define DMH_GGML_Q3_K 11  /* 256 weights in 114 bytes (the reference's layout) */
+#define DMH_GGML_Q4_K 12  /* 256 weights in 144 bytes (the reference's layout) */
+#define DMH_GGML_BF16 30
+/* Q4_K sub-blocks 4..7 with the scale/min packing of the reference's Python
+ * twin (tools/oracle/oracle_port.py:104-110) instead of gguf.mojo:482-488. */
+#define DMH_F_Q4K_PY_SCALES 0x10u
+
+typedef struct dmh_gguf_file dmh_gguf_file;
+
+/* GGUFTensorInfo (gguf.mojo:104-114); name valid while the file is open.
+ * offset is relative to the data section, file_offset absolute. */
+typedef struct {
+  const char* name;
+  int32_t ndim;
+  int64_t dims[8];
+  int32_t ggml_type;
+  int64_t offset;
+  int64_t file_offset;
+  int64_t num_elements;
+  int64_t raw_bytes;
+} dmh_gguf_tensor;
+
+/* The scalar fields of GGUFIndex (gguf.mojo:117-141). */
+typedef struct {
+  int32_t version;
+  int64_t tensor_count;
+  int64_t metadata_kv_count;
+  int64_t data_section_offset;
+  int64_t expected_file_size;
+  int64_t alignment;
+} dmh_gguf_header;
+
+/* parse_gguf_index (gguf.mojo:257-411): magic, version 2/3, metadata, tensor
+ * directory, general.alignment, and the exact file size rule (F11b); on
+ * failure err receives the reference's "GGUF..." text, DMH_ERR_FORMAT. */
+int dmh_gguf_open(const char* path, dmh_gguf_file** out, char* err, size_t errlen);
+void dmh_gguf_close(dmh_gguf_file* f);
+int dmh_gguf_get_header(const dmh_gguf_file* f, dmh_gguf_header* h);
+int dmh_gguf_num_tensors(const dmh_gguf_file* f);
+/* GGUFIndex.tensor_map lookup: the last tensor of that name, or -1. */
+int dmh_gguf_find(const dmh_gguf_file* f, const char* name);
+int dmh_gguf_tensor_info(const dmh_gguf_file* f, int idx, dmh_gguf_tensor* info);
+/* GGUFIndex.metadata[key] as text (scalars in decimal, arrays as
+ * "[Array of N elements]"), or NULL. */
+const char* dmh_gguf_metadata(const dmh_gguf_file* f, const char* key);
+/* The raw payload bytes of tensor idx; bytes must equal its raw_bytes. */
+int dmh_gguf_read(const dmh_gguf_file* f, int idx, void* out, int64_t bytes, char* err,
+                  size_t errlen);
+
+/* dequantize_q8_0 / dequantize_q4_k / dequantize_q3_k (gguf.mojo:414-560)
+ * and the F32 / BF16 copies of stream_gguf_tensor_f32 (:598-613) on the GPU:
+ * out[num_elements] fp32, elements past the last whole block 0.0.  raw holds
+ * at least the whole blocks.  flags: DMH_F_DEVICE (raw and out are device
+ * memory, raw 4-byte and out 16-byte aligned), DMH_F_Q4K_PY_SCALES.  Unknown
+ * types: "GGUF_UNSUPPORTED_DTYPE: unsupported GGML type T", DMH_ERR_FORMAT. */
+int dmh_dequant_gguf(dmh_ctx* ctx, int ggml_type, const void* raw, int64_t raw_bytes,
+                     int64_t num_elements, float* out, unsigned flags, char* err,
+                     size_t errlen);
+
+/* stream_gguf_tensor_f32 (gguf.mojo:563-626): read one tensor's bytes from
+ * the file and dequantize them on the GPU into out[n_out] (n_out must equal
+ * num_elements).  flags: DMH_F_DEVICE (out is device memory),
+ * DMH_F_Q4K_PY_SCALES.  Errors: WEIGHT_LOAD_FAILED (name not in the index),
+ * GGUF_READ_ERROR (truncated read), GGUF_UNSUPPORTED_DTYPE. */
+int dmh_gguf_stream_tensor_f32(dmh_ctx* ctx, const dmh_gguf_file* f, const char* name,
+                               float* out, int64_t n_out, unsigned flags, char* err,
+                               size_t errlen);
+
 #ifdef __cplusplus
 }
 #endif

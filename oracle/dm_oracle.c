@@ -22,6 +22,12 @@
  *       answers of tests/unit/test_moe.mojo:51-175 and a float64 numpy MoE.
  *   or_pool_*: partition_range invariants and serial == parallel bit-exact
  *       (tests/unit/test_m11_w1_workerpool.mojo:23-221).
+ *   or_dequant_gguf: the closed forms of the synthetic blocks of
+ *       fixtures/m9_port_mini.gguf (tools/fixtures/generate_m9_gguf_fixture.py:
+ *       47-91); vectors of the reference's Python twin tools/oracle/
+ *       oracle_port.py:68-160 on random blocks (Q8_0, Q3_K, Q4_K layout 1);
+ *       Q4_K layout 0 through the byte substitution that maps it onto layout
+ *       1 (bytes 12..15 := bytes 8..11, read from gguf.mojo:482-488).
  * Parity unpinned (no toolchain for the reference here): the exact bits of
  * Mojo's std.math.exp and the association order of SIMD.reduce_add; this file
  * fixes exp = or_expf and reduce_add = halving tree.
@@ -274,6 +280,86 @@ int or_dequant_q4_f32(const uint16_t* scales, int64_t n_scales,
     for (int64_t i = 0; i < num_elements; ++i) out[i] = or_bf16_to_f32(tmp[i]);
   free(tmp);
   return st;
+}
+
+/* ---- GGUF payloads ------------------------------------------------------- */
+/* get_ggml_block_specs, src/format/gguf.mojo:76-102, for the types that
+ * stream_gguf_tensor_f32 (gguf.mojo:598-626) dequantizes. */
+int or_gguf_block_spec(int t, int* bs, int* bpb) {
+  switch (t) {
+    case 0: *bs = 1; *bpb = 4; return 0;      /* F32 */
+    case 30: *bs = 1; *bpb = 2; return 0;     /* BF16 */
+    case 8: *bs = 32; *bpb = 34; return 0;    /* Q8_0 */
+    case 12: *bs = 256; *bpb = 144; return 0; /* Q4_K */
+    case 11: *bs = 256; *bpb = 114; return 0; /* Q3_K */
+    default: return -1;
+  }
+}
+
+static uint16_t rd_u16(const uint8_t* p) { return (uint16_t)(p[0] | (p[1] << 8)); }
+
+/* Scale code and min code of sub-block j of a Q4_K block (12 packed bytes
+ * q = block + 4).  layout 0: gguf.mojo:473-488 (for j >= 4 the low bits of
+ * both come from q[j]); layout 1: oracle_port.py:100-110 (from q[j + 4]). */
+static void q4k_scale_min(const uint8_t* q, int j, int layout, int* sc, int* mn) {
+  if (j < 4) {
+    *sc = q[j] & 63;
+    *mn = q[j + 4] & 63;
+    return;
+  }
+  const int lo = layout ? q[j + 4] : q[j];
+  *sc = (lo & 15) | ((q[j - 4] >> 6) << 4);
+  *mn = (lo >> 4) | ((q[j] >> 6) << 4);
+}
+
+/* dequantize_q8_0 (gguf.mojo:414-441), dequantize_q4_k (:444-506),
+ * dequantize_q3_k (:509-560) and the F32 / BF16 copies of
+ * stream_gguf_tensor_f32 (:598-613).  Each output is one fp32 product of
+ * exactly representable factors (Q4_K: minus the min, one rounding). */
+int or_dequant_gguf(int t, const uint8_t* raw, int64_t raw_bytes, int64_t n, int layout,
+                    float* out, char* err, size_t errlen) {
+  int bs, bpb;
+  if (or_gguf_block_spec(t, &bs, &bpb))
+    return seterr(err, errlen, "GGUF_UNSUPPORTED_DTYPE: unsupported GGML type %d", t);
+  if (n < 0) return seterr(err, errlen, "or_dequant_gguf: negative num_elements");
+  const int64_t nb = n / bs;
+  if (raw_bytes < nb * bpb)
+    return seterr(err, errlen, "or_dequant_gguf: %lld bytes < %lld blocks x %d",
+                  (long long)raw_bytes, (long long)nb, bpb);
+  for (int64_t i = nb * bs; i < n; ++i) out[i] = 0.0f;
+  for (int64_t b = 0; b < nb; ++b) {
+    const uint8_t* blk = raw + b * bpb;
+    float* o = out + b * bs;
+    if (t == 0) {
+      memcpy(o, blk, 4);
+    } else if (t == 30) {
+      o[0] = or_bf16_to_f32(rd_u16(blk));
+    } else if (t == 8) {
+      const float d = or_fp16_to_f32(rd_u16(blk));
+      for (int i = 0; i < 32; ++i) o[i] = d * (float)(int8_t)blk[2 + i];
+    } else if (t == 12) {
+      const float d = or_fp16_to_f32(rd_u16(blk));
+      const float dmin = or_fp16_to_f32(rd_u16(blk + 2));
+      for (int e = 0; e < 256; ++e) {
+        const int j = e >> 5, r = e & 31; /* sub-block, position in it */
+        int sc, mn;
+        q4k_scale_min(blk + 4, j, layout, &sc, &mn);
+        const uint8_t byte = blk[16 + j * 16 + (r & 15)];
+        const int q = r < 16 ? (byte & 15) : (byte >> 4);
+        const float fs = (float)sc * d, fm = (float)mn * dmin;
+        o[e] = fs * (float)q - fm;
+      }
+    } else { /* Q3_K: hmask [0,32), qs [32,96), scales [96,112), d [112,114) */
+      const float d = or_fp16_to_f32(rd_u16(blk + 112));
+      for (int e = 0; e < 256; ++e) {
+        const int hi = (blk[e >> 3] >> (e & 7)) & 1;
+        const int lo = (blk[32 + (e >> 2)] >> ((e & 3) * 2)) & 3;
+        const float fs = (float)((int)blk[96 + (e >> 4)] - 32) * d;
+        o[e] = fs * (float)((hi << 2 | lo) - 4);
+      }
+    }
+  }
+  return 0;
 }
 
 /* ---- router -------------------------------------------------------------- */

@@ -51,6 +51,18 @@ int or_dequant_q4_f32(const uint16_t* scales, int64_t n_scales,
                       int64_t num_elements, int group_size,
                       float* out_f32, char* err, size_t errlen);
 
+/* ---- GGUF tensor payloads -> fp32 (src/format/gguf.mojo:414-626) ----
+ * ggml_type: 0 F32, 30 BF16, 8 Q8_0 (32 weights / 34 B), 12 Q4_K (256 / 144 B),
+ * 11 Q3_K (256 / 114 B), the reference's own block layouts.  Elements past
+ * the last whole block stay 0.0, as in the reference.  q4k_layout 0 follows
+ * dequantize_q4_k of gguf.mojo:444-506; 1 follows the reference's Python twin
+ * (tools/oracle/oracle_port.py:86-127), which packs the scales and mins of
+ * sub-blocks 4..7 differently (gguf.mojo:482-488 vs oracle_port.py:104-110). */
+int or_gguf_block_spec(int ggml_type, int* block_size, int* bytes_per_block);
+int or_dequant_gguf(int ggml_type, const uint8_t* raw, int64_t raw_bytes,
+                    int64_t num_elements, int q4k_layout, float* out, char* err,
+                    size_t errlen);
+
 /* ---- router (src/layers/router.mojo, topk.mojo, router_types.mojo) ---- */
 int or_router_config_validate(int num_experts, int top_k, int norm_topk_prob,
                               char* err, size_t errlen);

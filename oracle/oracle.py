@@ -54,6 +54,8 @@ def lib():
         L.or_compute_fp16_scale_ceil.restype = C.c_uint16
         L.or_dequant_q4_bf16.argtypes = [U16P, C.c_int64, U8P, C.c_int64, C.c_int64,
                                          C.c_int, U16P, C.c_char_p, C.c_size_t]
+        L.or_dequant_gguf.argtypes = [C.c_int, U8P, C.c_int64, C.c_int64, C.c_int, F32P,
+                                      C.c_char_p, C.c_size_t]
         L.or_router_project.argtypes = [F32P, C.c_int64, F32P, C.c_int64, C.c_int, C.c_int,
                                         C.c_int, C.c_int, F32P, C.c_char_p, C.c_size_t]
         L.or_router_softmax.argtypes = [F32P, C.c_int64, C.c_int, C.c_int, C.c_int, F32P,
@@ -158,6 +160,23 @@ def dequant_q4_bf16(scales_u16, packed_u8, num_elements: int, group_size: int = 
     e = _errbuf()
     _check(lib().or_dequant_q4_bf16(s, s.size, p, p.size, num_elements, group_size, out,
                                     e, 1024), e)
+    return out[:num_elements]
+
+
+GGML_F32, GGML_Q8_0, GGML_Q3_K, GGML_Q4_K, GGML_BF16 = 0, 8, 11, 12, 30
+
+
+def dequant_gguf(ggml_type: int, raw, num_elements: int, q4k_layout: int = 0):
+    """GGUF payload -> fp32 (src/format/gguf.mojo:414-626)."""
+    r = np.frombuffer(bytes(raw), dtype=np.uint8) if not isinstance(raw, np.ndarray) else \
+        np.ascontiguousarray(raw, dtype=np.uint8).ravel()
+    nbytes = r.size
+    if r.size == 0:
+        r = np.zeros(1, np.uint8)
+    out = np.zeros(max(int(num_elements), 1), dtype=np.float32)
+    e = _errbuf()
+    _check(lib().or_dequant_gguf(ggml_type, r, nbytes, num_elements, q4k_layout, out, e,
+                                 1024), e)
     return out[:num_elements]
 
 
