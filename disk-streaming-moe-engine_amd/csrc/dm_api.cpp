@@ -21,6 +21,19 @@ using dm::LayerDev;
 namespace {
 
 constexpr int kMaxLayers = 4096;
+// first-error key slots: [0, kMaxLayers) uploaded 4-bit layers, kMaxLayers
+// the unit calls, then one per GGUF layer
+constexpr int kGgufSlot0 = kMaxLayers + 1;
+constexpr int kStatusSlots = kGgufSlot0 + kMaxLayers;
+
+// One MoE layer uploaded from a GGUF file: one device block holding the fp32
+// router and shared gate, the expert offset table and the expert payloads.
+struct GgufLayer {
+  dmh_moe_dims dims{};
+  void* buf = nullptr;
+  size_t bytes = 0;
+  dm::GgufMoeDev dev{};
+};
 
 struct Layer {
   dmh_moe_dims dims{};
@@ -100,7 +113,9 @@ struct dmh_ctx {
   DevBuf<uint16_t> g_xhi, g_xlo;
   DevBuf<uint16_t> g_hr, g_hs;  // bf16 hi parts, then lo parts
   DevBuf<float> g_r, g_rs;
-  unsigned long long* status = nullptr;  // [kMaxLayers + 1] first-error keys (last = unit calls)
+  std::vector<GgufLayer*> glayers;
+  DevBuf<float> gz;                      // shared-gate logits of the GGUF forward
+  unsigned long long* status = nullptr;  // [kStatusSlots] first-error keys
   unsigned long long* vkey = nullptr;    // upload validation key
   unsigned* flags = nullptr;             // upload flags
   // where to find the routing of the last device-mode call per layer
@@ -344,6 +359,58 @@ int finish_status(dmh_ctx* ctx, Layer* Ly, int layer, uint64_t key, const int32_
   return decode_key(key, layer, expert_id, Ly ? Ly->dims.num_experts : 0, err, errlen);
 }
 
+// The error text of a GGUF layer's first-error key.  forward_port_block
+// calls swiglu_forward(x, w, seq_len, hidden, inter) (port_scheduler.mojo:
+// 450-464), so the expert texts carry hidden as the layer and the
+// intermediate size as the expert id.
+int gguf_finish(dmh_ctx* c, int layer, uint64_t key, char* err, size_t errlen) {
+  GgufLayer* G = layer >= 0 && layer < (int)c->glayers.size() ? c->glayers[layer] : nullptr;
+  const int H = G ? G->dims.hidden : 0, E = G ? G->dims.num_experts : 0;
+  const uint32_t ph = dm::key_phase(key);
+  if (ph == dm::kPhExpert || ph == dm::kPhShared)
+    return decode_key(key, H, ph == dm::kPhShared ? (G ? G->dims.inter_sh : 0)
+                                                   : (G ? G->dims.inter : 0),
+                      E, err, errlen);
+  return decode_key(key, layer, -1, E, err, errlen);
+}
+
+GgufLayer* get_glayer(dmh_ctx* c, int layer) {
+  if (!c || layer < 0 || layer >= (int)c->glayers.size()) return nullptr;
+  return c->glayers[layer];
+}
+
+// The MoE section of forward_port_block on a GGUF layer, all on the device:
+// router (fp32 weights, router_forward's order), routed and shared experts
+// from their GGUF blocks, shared gate, moe_aggregate_forward.
+hipError_t run_gguf_block(dmh_ctx* c, GgufLayer* G, unsigned long long* status, const float* dx,
+                          const float* dres, int T, float* dy, int32_t* dids, float* dprobs,
+                          float* dshg) {
+  const dm::GgufMoeDev& L = G->dev;
+  hipStream_t st = c->cur;
+  hipError_t e;
+  const int ldh = L.I > L.Ish ? L.I : L.Ish;
+  if ((e = c->z.ensure((size_t)T * L.E)) != hipSuccess) return e;
+  if ((e = c->gz.ensure((size_t)T)) != hipSuccess) return e;
+  if ((e = c->h.ensure((size_t)T * (L.K + 1) * ldh)) != hipSuccess) return e;
+  if ((e = c->g_r.ensure((size_t)T * L.K * L.H)) != hipSuccess) return e;
+  if ((e = c->g_rs.ensure((size_t)T * L.H)) != hipSuccess) return e;
+  if ((e = dm::launch_router_generic(dx, L.router, T, L.H, L.E, c->z.p, status, st)) != hipSuccess)
+    return e;
+  if ((e = dm::launch_router_select(c->z.p, L.E, T, L.E, L.K, 0, dids, dprobs, dshg, status,
+                                    st)) != hipSuccess)
+    return e;
+  // the shared-gate logit in the same 16-lane order; its checks are the
+  // gate's own (GATE_ERROR), so the router kernel's records go to a sink
+  if ((e = dm::launch_router_generic(dx, L.shgate, T, L.H, 1, c->gz.p, c->vkey, st)) != hipSuccess)
+    return e;
+  if ((e = dm::launch_shared_gate_scores(c->gz.p, 1, T, dshg, status, st)) != hipSuccess) return e;
+  if ((e = dm::launch_gguf_gateup(L, dx, T, dids, c->h.p, ldh, status, st)) != hipSuccess) return e;
+  if ((e = dm::launch_gguf_down(L, c->h.p, ldh, T, dids, c->g_r.p, c->g_rs.p, status, st)) !=
+      hipSuccess)
+    return e;
+  return dm::launch_combine(c->g_r.p, c->g_rs.p, dprobs, dshg, dres, T, L.H, L.K, dy, status, st);
+}
+
 }  // namespace
 
 extern "C" {
@@ -362,11 +429,11 @@ int dmh_create(int device, dmh_ctx** out, char* err, size_t errlen) {
   dmh_ctx* c = new dmh_ctx();
   c->device = device;
   hipError_t e = hipStreamCreateWithFlags(&c->own, hipStreamNonBlocking);
-  if (e == hipSuccess) e = hipMalloc(&c->status, sizeof(unsigned long long) * (kMaxLayers + 1));
+  if (e == hipSuccess) e = hipMalloc(&c->status, sizeof(unsigned long long) * kStatusSlots);
   if (e == hipSuccess) e = hipMalloc(&c->vkey, sizeof(unsigned long long));
   if (e == hipSuccess) e = hipMalloc(&c->flags, sizeof(unsigned));
   if (e == hipSuccess)
-    e = hipMemset(c->status, 0xFF, sizeof(unsigned long long) * (kMaxLayers + 1));
+    e = hipMemset(c->status, 0xFF, sizeof(unsigned long long) * kStatusSlots);
   if (e != hipSuccess) {
     dmh_destroy(c);
     return set_err(err, errlen, DMH_ERR_HIP, "dmh_create: %s", hipGetErrorString(e));
@@ -376,6 +443,7 @@ int dmh_create(int device, dmh_ctx** out, char* err, size_t errlen) {
   if (hipGetDeviceProperties(&prop, device) == hipSuccess) c->num_cus = prop.multiProcessorCount;
   c->last_ids.assign(kMaxLayers + 1, nullptr);
   c->last_k.assign(kMaxLayers + 1, 0);
+  c->glayers.assign(kMaxLayers, nullptr);
   *out = c;
   return DMH_OK;
 }
@@ -385,7 +453,13 @@ int dmh_destroy(dmh_ctx* c) {
   (void)hipSetDevice(c->device);
   if (c->cur) (void)hipStreamSynchronize(c->cur);
   for (Layer* L : c->layers) free_layer(L);
-  DevBuf<float>* fb[] = {&c->x, &c->res, &c->y, &c->z, &c->probs, &c->shg, &c->h, &c->xn, &c->hstack};
+  for (GgufLayer* G : c->glayers)
+    if (G) {
+      if (G->buf) (void)hipFree(G->buf);
+      delete G;
+    }
+  DevBuf<float>* fb[] = {&c->x,  &c->res, &c->y,  &c->z,      &c->probs,
+                         &c->shg, &c->h,  &c->xn, &c->hstack, &c->gz};
   for (auto* b : fb) b->release();
   c->ids.release();
   c->uids.release();
@@ -424,10 +498,12 @@ int dmh_sync(dmh_ctx* c, char* err, size_t errlen) {
   if (!c) return set_err(err, errlen, DMH_ERR_INVALID_ARG, "dmh_sync: ctx is NULL");
   HIP_TRY(hipSetDevice(c->device));
   HIP_TRY(hipStreamSynchronize(c->cur));
-  std::vector<unsigned long long> keys(kMaxLayers + 1);
+  std::vector<unsigned long long> keys(kStatusSlots);
   HIP_TRY(hipMemcpy(keys.data(), c->status, sizeof(unsigned long long) * keys.size(),
                     hipMemcpyDeviceToHost));
   int rc = DMH_OK;
+  for (int l = kGgufSlot0; l < kStatusSlots && rc == DMH_OK; ++l)
+    if (keys[l] != dm::kNoError) rc = gguf_finish(c, l - kGgufSlot0, keys[l], err, errlen);
   for (int l = 0; l <= kMaxLayers && rc == DMH_OK; ++l) {
     Layer* Ly = l < (int)c->layers.size() ? c->layers[l] : nullptr;
     uint64_t key = keys[l];
@@ -1105,6 +1181,199 @@ int dmh_moe_aggregate(dmh_ctx* c, const float* residual, const float* routed, co
   if (key == dm::kNoError) return DMH_OK;
   HIP_TRY(reset_status(c, kMaxLayers));
   return decode_key(key, layer, -1, 0, err, errlen);
+}
+
+// load_port_block_from_gguf's MoE tensors (src/layers/gguf_port_loader.mojo:
+// 207-256) -> one GGUF layer in HBM.  Lookup, read, type and length checks
+// run in the loader's order with its texts.
+int dmh_upload_moe_layer_gguf(dmh_ctx* c, int layer, const dmh_moe_dims* d,
+                              const dmh_gguf_file* gf, int model_layer, unsigned flags, char* err,
+                              size_t errlen) {
+  if (!c || !d || !gf)
+    return set_err(err, errlen, DMH_ERR_INVALID_ARG, "dmh_upload_moe_layer_gguf: NULL argument");
+  if (layer < 0 || layer >= kMaxLayers)
+    return set_err(err, errlen, DMH_ERR_INVALID_ARG,
+                   "dmh_upload_moe_layer_gguf: layer %d outside [0, %d)", layer, kMaxLayers);
+  const int H = d->hidden, E = d->num_experts, K = d->top_k, I = d->inter, Ish = d->inter_sh;
+  int rc = router_config_check(E, K, d->norm_topk_prob, err, errlen);
+  if (rc) return rc;
+  if (H <= 0 || I <= 0 || Ish <= 0 || H % 4 || I % 4 || Ish % 4 || E > 2048 || K > 32)
+    return set_err(err, errlen, DMH_ERR_CONFIG,
+                   "{\"error_type\":\"CONFIG_ERROR\",\"detail\":\"GGUF layer needs hidden, inter"
+                   " and shared inter positive multiples of 4, num_experts <= 2048, top_k <= 32\""
+                   ",\"stage\":\"loader\",\"layer\":%d}", layer);
+  const dm::GgufFile& f = gf->f;
+  const std::string pfx = "blk." + std::to_string(model_layer) + ".";
+  // payload of one tensor, with the checks of stream_gguf_tensor_f32 and
+  // _expect_len (gguf_port_loader.mojo:55-67)
+  auto load = [&](const std::string& name, int64_t want, std::vector<uint8_t>* raw,
+                  int* type) -> int {
+    const int idx = f.find(name);
+    if (idx < 0)
+      return set_err(err, errlen, DMH_ERR_WEIGHT,
+                     "{\"error_type\":\"WEIGHT_LOAD_FAILED\",\"detail\":\"tensor not found in GGUF"
+                     " index\",\"tensor\":\"%s\"}", name.c_str());
+    std::string e;
+    if (!dm::read_gguf_tensor(f, idx, raw, &e)) return set_err(err, errlen, DMH_ERR_WEIGHT, "%s", e.c_str());
+    const dm::GgufTensor& t = f.tensors[idx];
+    int bs, bpb;
+    if (dm::gguf_block_spec(t.type, &bs, &bpb))
+      return set_err(err, errlen, DMH_ERR_FORMAT,
+                     "GGUF_UNSUPPORTED_DTYPE: unsupported GGML type %d for tensor %s", t.type,
+                     name.c_str());
+    if (t.num_elements != want)
+      return set_err(err, errlen, DMH_ERR_FORMAT,
+                     "GGUF_FILE_CORRUPT: dimension mismatch for tensor %s: expected %lld elements,"
+                     " got %lld", name.c_str(), (long long)want, (long long)t.num_elements);
+    *type = t.type;
+    return DMH_OK;
+  };
+  std::vector<uint8_t> router_raw, sg_raw, tmp;
+  int router_t = 0, sg_t = 0, exp_t = -1, ty = 0;
+  if ((rc = load(pfx + "ffn_gate_exps.weight", (int64_t)E * H, &router_raw, &router_t))) return rc;
+  // expert payloads back to back, each 256-byte aligned; row E = shared
+  std::vector<int64_t> off((size_t)(E + 1) * 3);
+  std::vector<uint8_t> payload;
+  auto append = [&](const std::string& name, int64_t want, int64_t* o) -> int {
+    int r = load(name, want, &tmp, &ty);
+    if (r) return r;
+    if (exp_t >= 0 && ty != exp_t)
+      return set_err(err, errlen, DMH_ERR_FORMAT,
+                     "dmh_upload_moe_layer_gguf: expert tensor %s has GGML type %d, the others %d",
+                     name.c_str(), ty, exp_t);
+    exp_t = ty;
+    *o = (int64_t)payload.size();
+    payload.insert(payload.end(), tmp.begin(), tmp.end());
+    payload.resize(align256(payload.size()), 0);
+    return DMH_OK;
+  };
+  const int64_t IH = (int64_t)I * H, ShH = (int64_t)Ish * H;
+  for (int e = 0; e < E; ++e) {
+    const std::string es = std::to_string(e);
+    if ((rc = append(pfx + "ffn_gate." + es + ".weight", IH, &off[(size_t)e * 3 + 0]))) return rc;
+    if ((rc = append(pfx + "ffn_up." + es + ".weight", IH, &off[(size_t)e * 3 + 1]))) return rc;
+    if ((rc = append(pfx + "ffn_down." + es + ".weight", IH, &off[(size_t)e * 3 + 2]))) return rc;
+  }
+  if ((rc = append(pfx + "ffn_shared_gate.weight", ShH, &off[(size_t)E * 3 + 0]))) return rc;
+  if ((rc = append(pfx + "ffn_shared_up.weight", ShH, &off[(size_t)E * 3 + 1]))) return rc;
+  if ((rc = append(pfx + "ffn_shared_down.weight", ShH, &off[(size_t)E * 3 + 2]))) return rc;
+  if ((rc = load(pfx + "shared_gate.weight", H, &sg_raw, &sg_t))) return rc;
+
+  HIP_TRY(hipSetDevice(c->device));
+  hipStream_t st = c->cur;
+  const size_t b_router = align256((size_t)E * H * 4), b_sg = align256((size_t)H * 4),
+               b_off = align256(off.size() * 8), b_rr = align256(router_raw.size()),
+               b_sr = align256(sg_raw.size());
+  const size_t bytes = b_router + b_sg + b_off + payload.size() + b_rr + b_sr;
+  GgufLayer* G = new GgufLayer();
+  if (hipMalloc(&G->buf, bytes) != hipSuccess) {
+    delete G;
+    return set_err(err, errlen, DMH_ERR_NO_MEMORY,
+                   "dmh_upload_moe_layer_gguf: cannot allocate %zu bytes", bytes);
+  }
+  uint8_t* b = static_cast<uint8_t*>(G->buf);
+  float* d_router = reinterpret_cast<float*>(b);
+  float* d_sg = reinterpret_cast<float*>(b + b_router);
+  int64_t* d_off = reinterpret_cast<int64_t*>(b + b_router + b_sg);
+  uint8_t* d_raw = b + b_router + b_sg + b_off;
+  // the raw router and gate sit at the end of the block until dequantized
+  uint8_t* d_rr = d_raw + payload.size();
+  uint8_t* d_sr = d_rr + b_rr;
+  const int layout = (flags & DMH_F_Q4K_PY_SCALES) ? 1 : 0;
+  hipError_t e = hipMemcpyAsync(d_off, off.data(), off.size() * 8, hipMemcpyHostToDevice, st);
+  if (e == hipSuccess && !payload.empty())
+    e = hipMemcpyAsync(d_raw, payload.data(), payload.size(), hipMemcpyHostToDevice, st);
+  if (e == hipSuccess)
+    e = hipMemcpyAsync(d_rr, router_raw.data(), router_raw.size(), hipMemcpyHostToDevice, st);
+  if (e == hipSuccess)
+    e = hipMemcpyAsync(d_sr, sg_raw.data(), sg_raw.size(), hipMemcpyHostToDevice, st);
+  if (e == hipSuccess) e = dm::launch_dequant_gguf(router_t, d_rr, (int64_t)E * H, layout, d_router, st);
+  if (e == hipSuccess) e = dm::launch_dequant_gguf(sg_t, d_sr, H, layout, d_sg, st);
+  if (e == hipSuccess) e = hipStreamSynchronize(st);
+  if (e != hipSuccess) {
+    (void)hipFree(G->buf);
+    delete G;
+    HIP_TRY(e);
+  }
+  G->dims = *d;
+  G->bytes = bytes;
+  G->dev = dm::GgufMoeDev{H, E, K, I, Ish, exp_t, layout, d_raw, d_off, d_router, d_sg};
+  if (GgufLayer* old = c->glayers[layer]) {
+    (void)hipFree(old->buf);
+    delete old;
+  }
+  c->glayers[layer] = G;
+  HIP_TRY(reset_status(c, kGgufSlot0 + layer));
+  return DMH_OK;
+}
+
+int dmh_free_layer_gguf(dmh_ctx* c, int layer) {
+  GgufLayer* G = get_glayer(c, layer);
+  if (!G) return DMH_ERR_INVALID_ARG;
+  (void)hipSetDevice(c->device);
+  (void)hipStreamSynchronize(c->cur);
+  (void)hipFree(G->buf);
+  delete G;
+  c->glayers[layer] = nullptr;
+  return DMH_OK;
+}
+
+int dmh_moe_forward_gguf(dmh_ctx* c, int layer, const float* x, const float* residual, int T,
+                         float* y, int32_t* ids, float* probs, float* shg, unsigned flags,
+                         char* err, size_t errlen) {
+  GgufLayer* G = get_glayer(c, layer);
+  if (!G)
+    return set_err(err, errlen, DMH_ERR_INVALID_ARG,
+                   "dmh_moe_forward_gguf: GGUF layer %d not uploaded", layer);
+  if (!x || !y)
+    return set_err(err, errlen, DMH_ERR_INVALID_ARG, "dmh_moe_forward_gguf: x and y are required");
+  if (T <= 0)
+    return set_err(err, errlen, DMH_ERR_ACT,
+                   "{\"error_type\":\"ACT_LOAD_FAILED\",\"detail\":\"dimensions must be"
+                   " positive\",\"stage\":\"router\",\"layer\":%d}", layer);
+  const bool dev = flags & DMH_F_DEVICE;
+  if (dev && (((uintptr_t)x & 15) || ((uintptr_t)y & 15) || ((uintptr_t)residual & 15)))
+    return set_err(err, errlen, DMH_ERR_INVALID_ARG,
+                   "dmh_moe_forward_gguf: device x, residual and y must be 16-byte aligned");
+  HIP_TRY(hipSetDevice(c->device));
+  const dm::GgufMoeDev& L = G->dev;
+  const size_t TH = (size_t)T * L.H, TK = (size_t)T * L.K;
+  hipStream_t st = c->cur;
+  unsigned long long* status = c->status + kGgufSlot0 + layer;
+  if (dev) {
+    int32_t* dids = ids;
+    float* dprobs = probs;
+    float* dshg = shg;
+    if (!dids) { HIP_TRY(c->ids.ensure(TK)); dids = c->ids.p; }
+    if (!dprobs) { HIP_TRY(c->probs.ensure(TK)); dprobs = c->probs.p; }
+    if (!dshg) { HIP_TRY(c->shg.ensure(T)); dshg = c->shg.p; }
+    HIP_TRY(run_gguf_block(c, G, status, x, residual, T, y, dids, dprobs, dshg));
+    return DMH_OK;
+  }
+  HIP_TRY(c->x.ensure(TH));
+  HIP_TRY(c->y.ensure(TH));
+  HIP_TRY(c->ids.ensure(TK));
+  HIP_TRY(c->probs.ensure(TK));
+  HIP_TRY(c->shg.ensure(T));
+  HIP_TRY(hipMemcpyAsync(c->x.p, x, TH * 4, hipMemcpyHostToDevice, st));
+  const float* dres = nullptr;
+  if (residual) {
+    HIP_TRY(c->res.ensure(TH));
+    HIP_TRY(hipMemcpyAsync(c->res.p, residual, TH * 4, hipMemcpyHostToDevice, st));
+    dres = c->res.p;
+  }
+  HIP_TRY(reset_status(c, kGgufSlot0 + layer));
+  HIP_TRY(run_gguf_block(c, G, status, c->x.p, dres, T, c->y.p, c->ids.p, c->probs.p, c->shg.p));
+  unsigned long long key = 0;
+  HIP_TRY(hipMemcpyAsync(y, c->y.p, TH * 4, hipMemcpyDeviceToHost, st));
+  if (ids) HIP_TRY(hipMemcpyAsync(ids, c->ids.p, TK * 4, hipMemcpyDeviceToHost, st));
+  if (probs) HIP_TRY(hipMemcpyAsync(probs, c->probs.p, TK * 4, hipMemcpyDeviceToHost, st));
+  if (shg) HIP_TRY(hipMemcpyAsync(shg, c->shg.p, (size_t)T * 4, hipMemcpyDeviceToHost, st));
+  HIP_TRY(hipMemcpyAsync(&key, status, 8, hipMemcpyDeviceToHost, st));
+  HIP_TRY(hipStreamSynchronize(st));
+  if (key == dm::kNoError) return DMH_OK;
+  HIP_TRY(reset_status(c, kGgufSlot0 + layer));
+  return gguf_finish(c, layer, key, err, errlen);
 }
 
 }  // extern "C"

@@ -804,7 +804,7 @@ __global__ __launch_bounds__(kThreads) void k_moe_decode(
   // dequantization ends, and a poll issued earlier comes back stale and
   // costs a round trip more.  (The empty asm statements pin the order: the
   // compiler would otherwise sink the dequantization below the poll.)
-  const int lg = P.ldh_log2, ldh = 1 << lg;
+  const int lg = P.ldh_log2;
   const int lgw = lg - 1;                                          // words per slot: ldh / 2
   uint16_t* hbh = reinterpret_cast<uint16_t*>(smem + P.off_hb);  // [K+1][ldh] bf16 hi
   uint16_t* hbl = hbh + ((size_t)(K + 1) << lg);                  // [K+1][ldh] bf16 lo

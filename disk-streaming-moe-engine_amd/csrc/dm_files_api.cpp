@@ -16,9 +16,7 @@ struct dmh_quant_file {
 struct dmh_st_file {
   dm::SafetensorsFile f;
 };
-struct dmh_gguf_file {
-  dm::GgufFile f;
-};
+
 
 namespace {
 

@@ -29,6 +29,31 @@ int gguf_block_spec(int ggml_type, int* block_size, int* bytes_per_block);
 hipError_t launch_dequant_gguf(int ggml_type, const uint8_t* raw, int64_t n, int q4k_layout,
                                float* out, hipStream_t st);
 
+// One MoE layer uploaded from GGUF (the tensors of
+// src/layers/gguf_port_loader.mojo:207-256): expert payloads stay in their
+// GGUF blocks in HBM, the router and the shared-expert gate are fp32.
+struct GgufMoeDev {
+  int H, E, K, I, Ish;
+  int type;            // GGML type of every expert tensor
+  int layout;          // Q4_K scale packing (see launch_dequant_gguf)
+  const uint8_t* raw;  // expert payloads
+  const int64_t* off;  // [E + 1][3] byte offsets of gate, up, down in raw; row E = shared expert
+  const float* router; // [E][H]
+  const float* shgate; // [H]
+};
+
+// h[t][s][i] = SiLU(W_gate x_t)_i * (W_up x_t)_i for slots s < K (expert
+// ids[t][s]) and s = K (the shared expert), rows i < I (Ish); ldh >= max(I,
+// Ish), a multiple of 4.  Non-finite gate / up / product values record the
+// first-error keys of swiglu_forward (phase expert or shared).
+hipError_t launch_gguf_gateup(const GgufMoeDev& L, const float* x, int T, const int32_t* ids,
+                              float* h, int ldh, unsigned long long* status, hipStream_t st);
+// routed[t][s][d] = (W_down h[t][s])_d for s < K and shared_out[t][d] for the
+// shared expert.
+hipError_t launch_gguf_down(const GgufMoeDev& L, const float* h, int ldh, int T,
+                            const int32_t* ids, float* routed, float* shared_out,
+                            unsigned long long* status, hipStream_t st);
+
 // GGUFTensorInfo (gguf.mojo:104-114); offset is relative to the data section.
 struct GgufTensor {
   std::string name;
@@ -67,3 +92,8 @@ int api_dequant_gguf(::dmh_ctx* c, int ggml_type, const void* raw, bool raw_dev,
                      char* err, size_t errlen);
 
 }  // namespace dm
+
+// The C ABI's GGUF file handle.
+struct dmh_gguf_file {
+  dm::GgufFile f;
+};

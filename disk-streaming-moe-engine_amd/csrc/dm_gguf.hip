@@ -14,7 +14,9 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "dm_device.h"
 #include "dm_gguf.h"
+#include "dm_layout.h"
 
 namespace dm {
 namespace {
@@ -140,6 +142,91 @@ __global__ __launch_bounds__(256) void k_dequant_gguf(const uint8_t* __restrict_
   }
 }
 
+
+// ---- MoE experts straight from GGUF blocks ---------------------------------
+// One wave per output row: the 64 lanes walk the row in float4 chunks (the
+// row's weights decoded from their blocks as in k_dequant_gguf), accumulate
+// in fp32 and reduce across the wave.  Decode reads each selected expert's
+// payload once (Q3_K: 0.445 B per weight) instead of converting the layer's
+// 256 experts to fp32 first.
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+__device__ __forceinline__ float dot4(f32x4 a, f32x4 b, float acc) {
+  acc = __builtin_fmaf(a.x, b.x, acc);
+  acc = __builtin_fmaf(a.y, b.y, acc);
+  acc = __builtin_fmaf(a.z, b.z, acc);
+  return __builtin_fmaf(a.w, b.w, acc);
+}
+
+template <int T>
+__global__ __launch_bounds__(256) void k_gguf_gateup(GgufMoeDev L, const float* __restrict__ x,
+                                                     const int32_t* __restrict__ ids,
+                                                     float* __restrict__ h, int ldh,
+                                                     unsigned long long* status) {
+  const int lane = threadIdx.x & 63;
+  const int slot = (int)(blockIdx.y % (unsigned)(L.K + 1)), t = (int)(blockIdx.y / (unsigned)(L.K + 1));
+  const bool sh = slot == L.K;
+  const int rows = sh ? L.Ish : L.I;
+  const int r = (int)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= rows) return;
+  const int e = sh ? L.E : ids[(size_t)t * L.K + slot];
+  const uint8_t* wg = L.raw + L.off[(size_t)e * 3 + 0];
+  const uint8_t* wu = L.raw + L.off[(size_t)e * 3 + 1];
+  const float* xt = x + (size_t)t * L.H;
+  const int64_t base = (int64_t)r * L.H;
+  float ag = 0.0f, au = 0.0f;
+  for (int c = lane * 4; c < L.H; c += 256) {
+    const f32x4 xv = *reinterpret_cast<const f32x4*>(xt + c);
+    ag = dot4(values4<T>(wg, base + c, L.layout), xv, ag);
+    au = dot4(values4<T>(wu, base + c, L.layout), xv, au);
+  }
+  ag = wave_sum(ag);
+  au = wave_sum(au);
+  if (lane == 0) {
+    const float hv = dm_silu(ag) * au;
+    const uint32_t ph = sh ? kPhShared : kPhExpert, sl = sh ? 0 : (uint32_t)slot;
+    if (!finite_f(ag)) record_err(status, err_key(ph, t, sl, r, kEkGate));
+    if (!finite_f(au)) record_err(status, err_key(ph, t, sl, r, kEkUp));
+    if (!finite_f(hv)) record_err(status, err_key(ph, t, sl, r, kEkH));
+    h[((size_t)t * (L.K + 1) + slot) * ldh + r] = hv;
+  }
+}
+
+template <int T>
+__global__ __launch_bounds__(256) void k_gguf_down(GgufMoeDev L, const float* __restrict__ h,
+                                                   int ldh, const int32_t* __restrict__ ids,
+                                                   float* __restrict__ routed,
+                                                   float* __restrict__ shared_out,
+                                                   unsigned long long* status) {
+  const int lane = threadIdx.x & 63;
+  const int slot = (int)(blockIdx.y % (unsigned)(L.K + 1)), t = (int)(blockIdx.y / (unsigned)(L.K + 1));
+  const bool sh = slot == L.K;
+  const int d = (int)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (d >= L.H) return;
+  const int n = sh ? L.Ish : L.I;
+  const int e = sh ? L.E : ids[(size_t)t * L.K + slot];
+  const uint8_t* wd = L.raw + L.off[(size_t)e * 3 + 2];
+  const float* hv = h + ((size_t)t * (L.K + 1) + slot) * ldh;
+  const int64_t base = (int64_t)d * n;
+  float a = 0.0f;
+  for (int c = lane * 4; c < n; c += 256)
+    a = dot4(values4<T>(wd, base + c, L.layout), *reinterpret_cast<const f32x4*>(hv + c), a);
+  a = wave_sum(a);
+  if (lane == 0) {
+    if (!finite_f(a))
+      record_err(status, err_key(sh ? kPhShared : kPhExpert, t, sh ? 0 : slot, n + d, kEkDown));
+    if (sh)
+      shared_out[(size_t)t * L.H + d] = a;
+    else
+      routed[((size_t)t * L.K + slot) * L.H + d] = a;
+  }
+}
+
 }  // namespace
 
 int gguf_block_spec(int t, int* bs, int* bpb) {
@@ -170,5 +257,35 @@ hipError_t launch_dequant_gguf(int t, const uint8_t* raw, int64_t n, int layout,
   }
   return hipGetLastError();
 }
+
+#define DM_GGUF_DISPATCH(KERNEL, GRID, ...)                                               \
+  switch (L.type) {                                                                       \
+    case kGgmlQ8_0: KERNEL<kGgmlQ8_0><<<GRID, 256, 0, st>>>(__VA_ARGS__); break;          \
+    case kGgmlQ4_K: KERNEL<kGgmlQ4_K><<<GRID, 256, 0, st>>>(__VA_ARGS__); break;          \
+    case kGgmlQ3_K: KERNEL<kGgmlQ3_K><<<GRID, 256, 0, st>>>(__VA_ARGS__); break;          \
+    case kGgmlBF16: KERNEL<kGgmlBF16><<<GRID, 256, 0, st>>>(__VA_ARGS__); break;          \
+    case kGgmlF32: KERNEL<kGgmlF32><<<GRID, 256, 0, st>>>(__VA_ARGS__); break;            \
+    default: return hipErrorInvalidValue;                                                 \
+  }
+
+hipError_t launch_gguf_gateup(const GgufMoeDev& L, const float* x, int T, const int32_t* ids,
+                              float* h, int ldh, unsigned long long* status, hipStream_t st) {
+  if (T <= 0 || L.H % 4 || L.I % 4 || L.Ish % 4 || ldh % 4 || ldh < L.I || ldh < L.Ish)
+    return hipErrorInvalidValue;
+  const int rows = L.I > L.Ish ? L.I : L.Ish;
+  const dim3 grid((unsigned)((rows + 3) / 4), (unsigned)(T * (L.K + 1)));
+  DM_GGUF_DISPATCH(k_gguf_gateup, grid, L, x, ids, h, ldh, status)
+  return hipGetLastError();
+}
+
+hipError_t launch_gguf_down(const GgufMoeDev& L, const float* h, int ldh, int T,
+                            const int32_t* ids, float* routed, float* shared_out,
+                            unsigned long long* status, hipStream_t st) {
+  if (T <= 0 || L.H % 4 || L.I % 4 || L.Ish % 4 || ldh % 4) return hipErrorInvalidValue;
+  const dim3 grid((unsigned)((L.H + 3) / 4), (unsigned)(T * (L.K + 1)));
+  DM_GGUF_DISPATCH(k_gguf_down, grid, L, h, ldh, ids, routed, shared_out, status)
+  return hipGetLastError();
+}
+#undef DM_GGUF_DISPATCH
 
 }  // namespace dm

@@ -31,6 +31,7 @@ EXPORTS = (
     "dmh_moe_aggregate", "dmh_gguf_open", "dmh_gguf_close", "dmh_gguf_get_header",
     "dmh_gguf_num_tensors", "dmh_gguf_find", "dmh_gguf_tensor_info", "dmh_gguf_metadata",
     "dmh_gguf_read", "dmh_dequant_gguf", "dmh_gguf_stream_tensor_f32",
+    "dmh_upload_moe_layer_gguf", "dmh_free_layer_gguf", "dmh_moe_forward_gguf",
 )
 
 
@@ -137,6 +138,10 @@ def lib():
     L.dmh_gguf_read.argtypes = [vp, i32, vp, i64, C.c_char_p, sz]
     L.dmh_dequant_gguf.argtypes = [vp, i32, vp, i64, i64, vp, u32, C.c_char_p, sz]
     L.dmh_gguf_stream_tensor_f32.argtypes = [vp, vp, C.c_char_p, vp, i64, u32, C.c_char_p, sz]
+    L.dmh_upload_moe_layer_gguf.argtypes = [vp, i32, C.POINTER(DmhDims), vp, i32, u32,
+                                            C.c_char_p, sz]
+    L.dmh_free_layer_gguf.argtypes = [vp, i32]
+    L.dmh_moe_forward_gguf.argtypes = [vp, i32, vp, vp, i32, vp, vp, vp, vp, u32, C.c_char_p, sz]
     _lib = L
     return L
 

@@ -96,6 +96,44 @@ def parse_gguf_index(file_path: str) -> GGUFIndex:
     return GGUFIndex(file_path)
 
 
+# ---- writer -----------------------------------------------------------------
+def write_gguf(path: str, tensors, metadata=None, alignment: int = 32, version: int = 3) -> None:
+    """A GGUF file as parse_gguf_index reads it: tensors is a list of (name,
+    dims, ggml_type, raw payload bytes), stored in order at `alignment`-byte
+    offsets of the data section; metadata maps keys to str or int (u32)."""
+    import struct
+    meta = dict(metadata or {})
+    if alignment != 32:
+        meta["general.alignment"] = alignment
+
+    def gstr(v: str) -> bytes:
+        b = v.encode()
+        return struct.pack("<Q", len(b)) + b
+
+    out = bytearray(b"GGUF" + struct.pack("<IQQ", version, len(tensors), len(meta)))
+    for k, v in meta.items():
+        out += gstr(k)
+        out += struct.pack("<I", 8) + gstr(v) if isinstance(v, str) else struct.pack("<II", 4, v)
+    off = 0
+    offs = []
+    for name, dims, ty, raw in tensors:
+        off = (off + alignment - 1) // alignment * alignment
+        offs.append(off)
+        out += gstr(name) + struct.pack("<I", len(dims))
+        out += b"".join(struct.pack("<Q", int(d)) for d in dims) + struct.pack("<IQ", ty, off)
+        off += len(raw)
+    out += b"\0" * ((-len(out)) % alignment)
+    base = len(out)
+    with open(path, "wb") as f:
+        f.write(out)
+        for (name, dims, ty, raw), o in zip(tensors, offs):
+            pos = base + o
+            cur = f.tell()
+            if pos > cur:
+                f.write(b"\0" * (pos - cur))
+            f.write(bytes(raw))
+
+
 def _flags(py_scales: bool) -> int:
     return DMH_F_Q4K_PY_SCALES if py_scales else 0
 

@@ -18,7 +18,8 @@ from dataclasses import dataclass, field
 
 import numpy as np
 
-from ._lib import (DMH_F_DEVICE, DismoenError, DmhDims, DmhWeights, check, errbuf, lib)
+from ._lib import (DMH_F_DEVICE, DMH_F_Q4K_PY_SCALES, DismoenError, DmhDims, DmhWeights, check,
+                   errbuf, lib)
 
 
 @dataclass
@@ -83,6 +84,7 @@ class MoEBlock:
         check(self._lib.dmh_create(device, C.byref(h), e, len(e)), e)
         self._h = h
         self.dims = {}
+        self.gguf_dims = {}
 
     # -- lifetime --------------------------------------------------------
     def close(self):
@@ -154,6 +156,50 @@ class MoEBlock:
         check(self._lib.dmh_upload_moe_layer_files(self._h, layer_idx, C.byref(d), quant.handle,
                                                    shard.handle, model_layer, e, len(e)), e)
         self.dims[layer_idx] = dims
+
+    # -- GGUF layers (slots of their own) ---------------------------------
+    def upload_layer_gguf(self, layer_idx: int, dims: tuple, index, model_layer: int = 0,
+                          py_scales: bool = False) -> None:
+        """load_port_block_from_gguf's MoE tensors of model layer model_layer
+        (src/layers/gguf_port_loader.mojo:207-256) from a dismoen.gguf.GGUFIndex;
+        dims = (hidden, num_experts, top_k, inter, inter_sh)."""
+        H, E, K, I, Ish = dims
+        d = DmhDims(H, E, K, I, Ish, 32, 0)
+        e = errbuf()
+        check(self._lib.dmh_upload_moe_layer_gguf(self._h, layer_idx, C.byref(d), index.handle,
+                                                  model_layer,
+                                                  DMH_F_Q4K_PY_SCALES if py_scales else 0, e,
+                                                  len(e)), e)
+        self.gguf_dims[layer_idx] = dims
+
+    def free_layer_gguf(self, layer_idx: int) -> None:
+        self._lib.dmh_free_layer_gguf(self._h, layer_idx)
+        self.gguf_dims.pop(layer_idx, None)
+
+    def forward_port_moe_gguf(self, norm_x, x_mid, layer_idx: int, seq_len: int):
+        """MoE section of forward_port_block (port_scheduler.mojo:381-482) on a
+        GGUF layer: (y [seq_len][H], ids, probs, shared gate) as numpy arrays."""
+        H, E, K, I, Ish = self.gguf_dims[layer_idx]
+        x = _f32(norm_x).reshape(-1)
+        res = None if x_mid is None else _f32(x_mid).reshape(-1)
+        y = np.empty(seq_len * H, np.float32)
+        ids = np.empty(seq_len * K, np.int32)
+        probs = np.empty(seq_len * K, np.float32)
+        shg = np.empty(seq_len, np.float32)
+        e = errbuf()
+        check(self._lib.dmh_moe_forward_gguf(self._h, layer_idx, x.ctypes.data, _ptr(res),
+                                             seq_len, y.ctypes.data, ids.ctypes.data,
+                                             probs.ctypes.data, shg.ctypes.data, 0, e, len(e)), e)
+        return (y.reshape(seq_len, H), ids.reshape(seq_len, K), probs.reshape(seq_len, K), shg)
+
+    def forward_gguf_device(self, layer_idx: int, x_ptr: int, seq_len: int, y_ptr: int,
+                            ids_ptr: int | None = None, probs_ptr: int | None = None,
+                            residual_ptr: int | None = None) -> None:
+        """Stream-ordered call on device buffers; errors are reported by sync()."""
+        e = errbuf()
+        check(self._lib.dmh_moe_forward_gguf(self._h, layer_idx, x_ptr, residual_ptr, seq_len,
+                                             y_ptr, ids_ptr, probs_ptr, None, DMH_F_DEVICE, e,
+                                             len(e)), e)
 
     def free_layer(self, layer_idx: int) -> None:
         self._lib.dmh_free_layer(self._h, layer_idx)

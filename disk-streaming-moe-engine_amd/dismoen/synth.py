@@ -174,3 +174,42 @@ def make_layer_device(hidden: int, num_experts: int, top_k: int, inter: int, int
             "d_scales": scales(E * H * I // G), "d_packed": codes(E * H * I),
             "sh_gu_scales": scales(2 * Ish * H // G), "sh_gu_packed": codes(2 * Ish * H),
             "sh_d_scales": scales(H * Ish // G), "sh_d_packed": codes(H * Ish)}
+
+
+# ---- GGUF layers ------------------------------------------------------------
+def gguf_payload(rng, ggml_type: int, n: int, scale: float = 1e-4) -> bytes:
+    """Random payload of n weights (a multiple of the block size) whose
+    super-scales are fp16 values near `scale` (Q8_0: 20 x scale)."""
+    import numpy as np
+    if ggml_type == 0:
+        return (rng.standard_normal(n) * scale * 100).astype("<f4").tobytes()
+    bs, bpb, d_off = {8: (32, 34, 0), 12: (256, 144, 0), 11: (256, 114, 112)}[ggml_type]
+    nb = n // bs
+    raw = rng.integers(0, 256, size=(nb, bpb), dtype=np.uint8)
+    d = (rng.uniform(0.5, 1.5, nb) * scale * (20 if ggml_type == 8 else 1)).astype(np.float16)
+    raw[:, d_off:d_off + 2] = d.view(np.uint8).reshape(nb, 2)
+    if ggml_type == 12:  # dmin
+        raw[:, 2:4] = (rng.uniform(0.5, 1.5, nb) * scale).astype(np.float16).view(np.uint8).reshape(nb, 2)
+    return raw.tobytes()
+
+
+def make_gguf_moe_layer(hidden: int, num_experts: int, inter: int, inter_sh: int, seed: int = 0,
+                        expert_type: int = 11, model_layer: int = 0):
+    """The MoE tensors of one layer under the names of
+    src/layers/gguf_port_loader.mojo:207-256, as (name, dims, type, raw)
+    for dismoen.gguf.write_gguf: router Q8_0, experts of expert_type,
+    shared-expert gate vector F32."""
+    import numpy as np
+    rng = np.random.default_rng(seed)
+    H, E, I, Ish = hidden, num_experts, inter, inter_sh
+    p = f"blk.{model_layer}."
+    ts = [(p + "ffn_gate_exps.weight", [H, E], 8, gguf_payload(rng, 8, E * H))]
+    for e in range(E):
+        ts.append((p + f"ffn_gate.{e}.weight", [H, I], expert_type, gguf_payload(rng, expert_type, I * H)))
+        ts.append((p + f"ffn_up.{e}.weight", [H, I], expert_type, gguf_payload(rng, expert_type, I * H)))
+        ts.append((p + f"ffn_down.{e}.weight", [I, H], expert_type, gguf_payload(rng, expert_type, I * H)))
+    ts.append((p + "ffn_shared_gate.weight", [H, Ish], expert_type, gguf_payload(rng, expert_type, Ish * H)))
+    ts.append((p + "ffn_shared_up.weight", [H, Ish], expert_type, gguf_payload(rng, expert_type, Ish * H)))
+    ts.append((p + "ffn_shared_down.weight", [Ish, H], expert_type, gguf_payload(rng, expert_type, Ish * H)))
+    ts.append((p + "shared_gate.weight", [H], 0, (rng.standard_normal(H) * 0.02).astype("<f4").tobytes()))
+    return ts

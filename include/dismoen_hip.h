@@ -324,6 +324,34 @@ int dmh_gguf_stream_tensor_f32(dmh_ctx* ctx, const dmh_gguf_file* f, const char*
                                float* out, int64_t n_out, unsigned flags, char* err,
                                size_t errlen);
 
+/* load_port_block_from_gguf's MoE tensors (src/layers/gguf_port_loader.mojo:
+ * 207-256) of model layer model_layer into GGUF layer slot `layer` (slots
+ * separate from dmh_upload_moe_layer's): router blk.{l}.ffn_gate_exps.weight
+ * [E*H] and shared gate blk.{l}.shared_gate.weight [H] dequantized to fp32;
+ * blk.{l}.ffn_{gate,up,down}.{e}.weight and blk.{l}.ffn_shared_{gate,up,down}
+ * .weight kept in their GGUF blocks in HBM (one GGML type for all of them).
+ * Errors: the loader's WEIGHT_LOAD_FAILED / GGUF_READ_ERROR /
+ * GGUF_UNSUPPORTED_DTYPE / "GGUF_FILE_CORRUPT: dimension mismatch" texts in
+ * its order.  dims: hidden, inter, inter_sh multiples of 4; group_size is
+ * ignored.  flags: DMH_F_Q4K_PY_SCALES. */
+int dmh_upload_moe_layer_gguf(dmh_ctx* ctx, int layer, const dmh_moe_dims* dims,
+                              const dmh_gguf_file* f, int model_layer, unsigned flags, char* err,
+                              size_t errlen);
+int dmh_free_layer_gguf(dmh_ctx* ctx, int layer);
+
+/* The MoE section of forward_port_block (src/layers/port_scheduler.mojo:
+ * 381-482) on a GGUF layer, as dmh_moe_forward: x is the post-attention
+ * RMSNorm output [seq_len][H], residual (x_mid, may be NULL) is added last;
+ * ids / probs [seq_len][K] and shg [seq_len] may be NULL.  Router, top-k,
+ * shared gate and aggregation are bit-exact with the reference's fp32
+ * order; the experts accumulate in fp32 in another order.  Expert error
+ * texts carry hidden as "layer" and the intermediate size as "expert_id", as
+ * forward_port_block's swiglu_forward calls do (port_scheduler.mojo:450-464).
+ * DMH_F_DEVICE: x, residual and y 16-byte aligned device memory. */
+int dmh_moe_forward_gguf(dmh_ctx* ctx, int layer, const float* x, const float* residual,
+                         int seq_len, float* y, int32_t* ids, float* probs, float* shg,
+                         unsigned flags, char* err, size_t errlen);
+
 #ifdef __cplusplus
 }
 #endif
