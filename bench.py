@@ -13,6 +13,11 @@ Inputs are resident in HBM before the timed region.  Prints one JSON line.
 format (256 experts x 2048 x 512 weights, --gguf-type q3_k|q4_k|q8_0)
 dequantized to fp32 in HBM, the work src/layers/gguf_port_loader.mojo:217-236
 repeats for every layer of every token.
+
+--workload gguf-moe: batch-1 decode of one Qwen3.6-shape MoE layer read from a
+GGUF file (Q8_0 router, 256 Q3_K experts and a Q3_K shared expert, written
+to TMPDIR with random payloads): the MoE section of forward_port_block with
+the experts kept in their GGUF blocks in HBM.
 """
 import argparse
 import json
@@ -48,7 +53,8 @@ def parse():
     ap.add_argument("--steps", type=int, default=1000)
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--workload", default="decode",
-                    choices=["decode", "toy", "stack", "batch", "prefill", "copy", "gguf"],
+                    choices=["decode", "toy", "stack", "batch", "prefill", "copy", "gguf",
+                             "gguf-moe"],
                     help="batch: --batch tokens per call (ragged small-batch decode); "
                          "prefill: --tokens per call with Zipf-skewed routing; "
                          "copy: a plain device copy of --copy-mib MiB, the calibration "
@@ -252,6 +258,104 @@ def gguf_layer(a, blk, stream, dev):
     print(json.dumps(rec))
 
 
+def gguf_moe(a, blk, stream, dev):
+    """Batch-1 decode of a Qwen3.6-shape GGUF MoE layer (Q3_K experts)."""
+    import tempfile
+
+    import numpy as np
+    import torch
+
+    from dismoen import gguf, synth
+    H, E, K, I, Ish = 2048, 256, 8, 512, 512
+    path = os.path.join(tempfile.gettempdir(), f"dismoen_bench_gguf_{os.getpid()}.gguf")
+    gguf.write_gguf(path, synth.make_gguf_moe_layer(H, E, I, Ish, seed=a.seed))
+    try:
+        with gguf.parse_gguf_index(path) as g:
+            blk.upload_layer_gguf(0, (H, E, K, I, Ish), g)
+            ntok = a.warmup + a.steps
+            rng = np.random.default_rng(a.seed)
+            xs = synth.make_activations(rng, (ntok, H))
+            xd = torch.from_numpy(xs).to(dev)
+            yd = torch.empty((ntok, H), dtype=torch.float32, device=dev)
+            idd = torch.empty((ntok, K), dtype=torch.int32, device=dev)
+            pd = torch.empty((ntok, K), dtype=torch.float32, device=dev)
+            torch.cuda.synchronize()
+            xp, yp, ip, pp = xd.data_ptr(), yd.data_ptr(), idd.data_ptr(), pd.data_ptr()
+            for t in range(a.warmup):
+                blk.forward_gguf_device(0, xp + t * H * 4, 1, yp + t * H * 4, ip + t * K * 4,
+                                        pp + t * K * 4)
+            blk.sync()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            for t in range(a.warmup, ntok):
+                blk.forward_gguf_device(0, xp + t * H * 4, 1, yp + t * H * 4, ip + t * K * 4,
+                                        pp + t * K * 4)
+            e1.record(stream)
+            torch.cuda.synchronize()
+            blk.sync()
+            ms = e0.elapsed_time(e1) / a.steps
+            blk_bytes = lambda n: n // 256 * 114  # Q3_K payload of n weights
+            alg = (E * H * 4 + H * 4 + (K + 1) * 3 * blk_bytes(I * H) + 2 * H * 4)
+            gbps = alg / (ms * 1e-3) / 1e9
+            rec = {"metric": "GGUF Q3_K MoE-layer decode µs/token + achieved HBM GB/s (batch 1)",
+                   "value": round(ms * 1e3, 3), "unit": "us/token", "n_gpus": 1,
+                   "steps": a.steps, "warmup": a.warmup, "ms_per_step": round(ms, 6),
+                   "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+                   "dtype": "f32", "data": "synthetic",
+                   "config": {"workload": "qwen3.6-35b-a3b moe layer from gguf (q8_0 router, "
+                                          "256 q3_k experts + q3_k shared), batch-1 decode",
+                              "hidden": H, "experts": E, "top_k": K, "inter": I,
+                              "inter_sh": Ish, "tokens": a.steps},
+                   "roofline": {"bound": "hbm", "kernel": "gguf moe block (5 launches)",
+                                "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS,
+                                "unit": "GB/s", "frac": round(gbps / HBM_PEAK_GBPS, 4),
+                                "traffic": None, "bytes_per_token": alg}}
+            if not a.no_cpu:
+                sys.path.insert(0, os.path.join(ROOT, "oracle"))
+                import oracle as orc
+                x = xs[-1:]
+                p = "blk.0."
+
+                def deq(name):
+                    t = g.tensors[g.tensor_map[p + name]]
+                    return orc.dequant_gguf(t.dtype, g.read_raw(p + name), t.num_elements)
+
+                # the reference dequantizes every expert of the layer per token
+                # (gguf_port_loader.mojo:217-236): timed on 8 of them, scaled
+                t0 = time.perf_counter()
+                for e in range(8):
+                    for nm in ("gate", "up", "down"):
+                        deq(f"ffn_{nm}.{e}.weight")
+                t_deq = (time.perf_counter() - t0) * E / 8
+                t0 = time.perf_counter()
+                ids, probs = orc.router_forward(x, deq("ffn_gate_exps.weight"), 1, H, E, K)
+                routed = np.zeros((1, K * H), np.float32)
+                for k in range(K):
+                    e = int(ids[0, k])
+                    routed[0, k * H:(k + 1) * H] = orc.swiglu_forward(
+                        x[0], deq(f"ffn_gate.{e}.weight"), deq(f"ffn_up.{e}.weight"),
+                        deq(f"ffn_down.{e}.weight"), 1, H, I)
+                sh = orc.swiglu_forward(x, deq("ffn_shared_gate.weight"),
+                                        deq("ffn_shared_up.weight"),
+                                        deq("ffn_shared_down.weight"), 1, H, Ish)
+                gt = orc.shared_gate_forward(x, deq("shared_gate.weight"), 1, H)
+                ref = orc.moe_aggregate(None, routed, probs, sh, gt, 1, H, K)
+                t_blk = time.perf_counter() - t0
+                y = yd[-1].cpu().numpy()
+                rms = float(np.sqrt(np.mean(ref.astype(np.float64) ** 2)))
+                rec["parity_last_token"] = {
+                    "ids_bit_exact": bool(np.array_equal(idd[-1].cpu().numpy(), ids[0])),
+                    "max_abs_over_rms": float(np.max(np.abs(y - ref)) / rms)}
+                rec["cpu_baseline"] = {"value": round((t_deq + t_blk) * 1e6, 1),
+                                       "unit": "us/token", "cores": 1, "kind": "port",
+                                       "sample": "dequant of 8 of the 256 experts scaled to 256 "
+                                                 "(the reference's per-token dequant) + one "
+                                                 "token's block, threads=1"}
+            print(json.dumps(rec))
+    finally:
+        os.unlink(path)
+
+
 def main():
     a = parse()
     if a.gpus != 1:
@@ -289,6 +393,10 @@ def main():
     stream = torch.cuda.ExternalStream(blk.stream(), device=dev)
     if a.workload == "gguf":
         gguf_layer(a, blk, stream, dev)
+        blk.close()
+        return
+    if a.workload == "gguf-moe":
+        gguf_moe(a, blk, stream, dev)
         blk.close()
         return
 

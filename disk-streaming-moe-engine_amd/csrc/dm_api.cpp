@@ -114,7 +114,6 @@ struct dmh_ctx {
   DevBuf<uint16_t> g_hr, g_hs;  // bf16 hi parts, then lo parts
   DevBuf<float> g_r, g_rs;
   std::vector<GgufLayer*> glayers;
-  DevBuf<float> gz;                      // shared-gate logits of the GGUF forward
   unsigned long long* status = nullptr;  // [kStatusSlots] first-error keys
   unsigned long long* vkey = nullptr;    // upload validation key
   unsigned* flags = nullptr;             // upload flags
@@ -389,21 +388,19 @@ hipError_t run_gguf_block(dmh_ctx* c, GgufLayer* G, unsigned long long* status, 
   hipStream_t st = c->cur;
   hipError_t e;
   const int ldh = L.I > L.Ish ? L.I : L.Ish;
-  if ((e = c->z.ensure((size_t)T * L.E)) != hipSuccess) return e;
-  if ((e = c->gz.ensure((size_t)T)) != hipSuccess) return e;
+  if ((e = c->z.ensure((size_t)T * (L.E + 1))) != hipSuccess) return e;
   if ((e = c->h.ensure((size_t)T * (L.K + 1) * ldh)) != hipSuccess) return e;
   if ((e = c->g_r.ensure((size_t)T * L.K * L.H)) != hipSuccess) return e;
   if ((e = c->g_rs.ensure((size_t)T * L.H)) != hipSuccess) return e;
-  if ((e = dm::launch_router_generic(dx, L.router, T, L.H, L.E, c->z.p, status, st)) != hipSuccess)
+  // router logits and, as column E, the shared-gate logit in the same
+  // 16-lane order; the selection kernel applies the gate's sigmoid and its
+  // GATE_ERROR checks
+  if ((e = dm::launch_router_generic(dx, L.router, T, L.H, L.E, c->z.p, status, st, L.shgate)) !=
+      hipSuccess)
     return e;
-  if ((e = dm::launch_router_select(c->z.p, L.E, T, L.E, L.K, 0, dids, dprobs, dshg, status,
+  if ((e = dm::launch_router_select(c->z.p, L.E + 1, T, L.E, L.K, 1, dids, dprobs, dshg, status,
                                     st)) != hipSuccess)
     return e;
-  // the shared-gate logit in the same 16-lane order; its checks are the
-  // gate's own (GATE_ERROR), so the router kernel's records go to a sink
-  if ((e = dm::launch_router_generic(dx, L.shgate, T, L.H, 1, c->gz.p, c->vkey, st)) != hipSuccess)
-    return e;
-  if ((e = dm::launch_shared_gate_scores(c->gz.p, 1, T, dshg, status, st)) != hipSuccess) return e;
   if ((e = dm::launch_gguf_gateup(L, dx, T, dids, c->h.p, ldh, status, st)) != hipSuccess) return e;
   if ((e = dm::launch_gguf_down(L, c->h.p, ldh, T, dids, c->g_r.p, c->g_rs.p, status, st)) !=
       hipSuccess)
@@ -458,8 +455,7 @@ int dmh_destroy(dmh_ctx* c) {
       if (G->buf) (void)hipFree(G->buf);
       delete G;
     }
-  DevBuf<float>* fb[] = {&c->x,  &c->res, &c->y,  &c->z,      &c->probs,
-                         &c->shg, &c->h,  &c->xn, &c->hstack, &c->gz};
+  DevBuf<float>* fb[] = {&c->x, &c->res, &c->y, &c->z, &c->probs, &c->shg, &c->h, &c->xn, &c->hstack};
   for (auto* b : fb) b->release();
   c->ids.release();
   c->uids.release();

@@ -22,8 +22,10 @@ hipError_t launch_repack_router(const uint16_t* router, const uint16_t* shgate, 
 hipError_t launch_dequant_ref(const uint16_t* scales, const uint8_t* packed, int64_t n,
                               int group, uint16_t* out, unsigned long long* vkey,
                               hipStream_t st);
+// z[T][E] (z[T][E + 1] with the shared-expert gate row w_sh as column E)
 hipError_t launch_router_generic(const float* x, const float* w, int T, int H, int E, float* z,
-                                 unsigned long long* status, hipStream_t st);
+                                 unsigned long long* status, hipStream_t st,
+                                 const float* w_sh = nullptr);
 
 // ---- decode path (one token per launch set) ----
 hipError_t launch_router_dec(const LayerDev& L, const float* x, int T, float* z,

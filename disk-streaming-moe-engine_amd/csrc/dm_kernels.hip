@@ -169,44 +169,68 @@ hipError_t launch_dequant_ref(const uint16_t* scales, const uint8_t* packed, int
 // sequentially, halving tree, scalar tail.
 // ===========================================================================
 
-// Generic form for the unit entry point: fp32 weights [E][H], any H.  One
-// thread per (token, expert) replays the 16 lanes in registers.
-__global__ __launch_bounds__(128) void k_router_generic(const float* __restrict__ x,
+// Generic form for the unit entry point: fp32 weights [E][H], any H.  Each
+// row's 16 lane partials (router.mojo:75-106) are 16 lanes of a wave: lane l
+// runs the chain k = l, l+16, ... with separate multiply and add, the
+// halving tree pairs lanes through shuffles inside the 16-lane group, and
+// lane 0 adds the tail.  A workgroup holds 16 rows of one token; every lane
+// checks the activations and weights it reads, which together cover x and w
+// (router.mojo:57-72).
+__global__ __launch_bounds__(256) void k_router_generic(const float* __restrict__ x,
                                                          const float* __restrict__ w, int T,
                                                          int H, int E, float* __restrict__ z,
-                                                         unsigned long long* status) {
-  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  // activation and weight scans (router.mojo:57-72)
-  for (int64_t i = gid; i < (int64_t)T * H; i += (int64_t)gridDim.x * blockDim.x)
-    if (!finite_f(x[i])) record_err(status, err_key(kPhX, 0, 0, 0, 0));
-  for (int64_t i = gid; i < (int64_t)E * H; i += (int64_t)gridDim.x * blockDim.x)
-    if (!finite_f(w[i])) record_err(status, err_key(kPhRouterW, 0, 0, 0, 0));
-  if (gid >= (int64_t)T * E) return;
-  const int t = (int)(gid / E), e = (int)(gid % E);
+                                                         unsigned long long* status, int t0,
+                                                         const float* __restrict__ w_sh) {
+  const int l = threadIdx.x & 15;
+  const int e = (int)blockIdx.x * 16 + (threadIdx.x >> 4);
+  const int t = t0 + (int)blockIdx.y;
+  // row E, when w_sh is given, is the shared-expert gate: same order, its
+  // checks are the gate's own and run where the logit is used
+  const int ldz = w_sh ? E + 1 : E;
+  const bool row = e < ldz, gate = e == E;
   const float* xr = x + (int64_t)t * H;
-  const float* wr = w + (int64_t)e * H;
-  float acc[16];
+  const float* wr = gate ? w_sh : w + (int64_t)(row ? e : 0) * H;
+  const int h16 = H & ~15;
+  float acc = 0.0f;
+  bool bad_x = false, bad_w = false;
+  if (row) {
+#pragma unroll 8
+    for (int k = l; k < h16; k += 16) {
+      const float xv = xr[k], wv = wr[k];
+      bad_x |= !finite_f(xv);
+      bad_w |= !finite_f(wv);
+      acc = acc + xv * wv;
+    }
+  }
 #pragma unroll
-  for (int l = 0; l < 16; ++l) acc[l] = 0.0f;
-  int k = 0;
-  for (; k + 16 <= H; k += 16)
-#pragma unroll
-    for (int l = 0; l < 16; ++l) acc[l] = acc[l] + xr[k + l] * wr[k + l];
-#pragma unroll
-  for (int wdt = 8; wdt >= 1; wdt >>= 1)
-#pragma unroll
-    for (int l = 0; l < wdt; ++l) acc[l] = acc[l] + acc[l + wdt];
-  float s = acc[0];
-  for (; k < H; ++k) s = s + xr[k] * wr[k];
-  if (!finite_f(s)) record_err(status, err_key(kPhLogit, t, 0, e, 0));
-  z[(int64_t)t * E + e] = s;
+  for (int wdt = 8; wdt >= 1; wdt >>= 1) {
+    const float o = __shfl_down(acc, wdt, 16);
+    if (l < wdt) acc = acc + o;
+  }
+  if (row && l == 0) {
+    float s = acc;
+    for (int k = h16; k < H; ++k) {
+      const float xv = xr[k], wv = wr[k];
+      bad_x |= !finite_f(xv);
+      bad_w |= !finite_f(wv);
+      s = s + xv * wv;
+    }
+    if (!gate && !finite_f(s)) record_err(status, err_key(kPhLogit, t, 0, e, 0));
+    z[(int64_t)t * ldz + e] = s;
+  }
+  if (bad_x) record_err(status, err_key(kPhX, 0, 0, 0, 0));
+  if (bad_w && !gate) record_err(status, err_key(kPhRouterW, 0, 0, 0, 0));
 }
 
 hipError_t launch_router_generic(const float* x, const float* w, int T, int H, int E, float* z,
-                                 unsigned long long* status, hipStream_t st) {
-  const int64_t n = (int64_t)T * E;
-  hipLaunchKernelGGL(k_router_generic, dim3((unsigned)((n + 127) / 128)), dim3(128), 0, st, x, w,
-                     T, H, E, z, status);
+                                 unsigned long long* status, hipStream_t st, const float* w_sh) {
+  if (T <= 0 || E <= 0) return hipErrorInvalidValue;
+  const int rows = w_sh ? E + 1 : E;
+  for (int t0 = 0; t0 < T; t0 += 65535) {  // grid.y holds at most 65535 tokens
+    const int n = T - t0 < 65535 ? T - t0 : 65535;
+    hipLaunchKernelGGL(k_router_generic, dim3((unsigned)((rows + 15) / 16), (unsigned)n),
+                       dim3(256), 0, st, x, w, T, H, E, z, status, t0, w_sh);
+  }
   return hipGetLastError();
 }
 
