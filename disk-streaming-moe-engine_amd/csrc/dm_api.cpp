@@ -378,9 +378,10 @@ GgufLayer* get_glayer(dmh_ctx* c, int layer) {
   return c->glayers[layer];
 }
 
-// The MoE section of forward_port_block on a GGUF layer, all on the device:
-// router (fp32 weights, router_forward's order), routed and shared experts
-// from their GGUF blocks, shared gate, moe_aggregate_forward.
+// The MoE section of forward_port_block on a GGUF layer, all on the device
+// in four launches: router and shared-gate logits (fp32 weights,
+// router_forward's order), selection and gate, gate/up of every slot, down
+// projections with moe_aggregate_forward.
 hipError_t run_gguf_block(dmh_ctx* c, GgufLayer* G, unsigned long long* status, const float* dx,
                           const float* dres, int T, float* dy, int32_t* dids, float* dprobs,
                           float* dshg) {
@@ -390,8 +391,6 @@ hipError_t run_gguf_block(dmh_ctx* c, GgufLayer* G, unsigned long long* status, 
   const int ldh = L.I > L.Ish ? L.I : L.Ish;
   if ((e = c->z.ensure((size_t)T * (L.E + 1))) != hipSuccess) return e;
   if ((e = c->h.ensure((size_t)T * (L.K + 1) * ldh)) != hipSuccess) return e;
-  if ((e = c->g_r.ensure((size_t)T * L.K * L.H)) != hipSuccess) return e;
-  if ((e = c->g_rs.ensure((size_t)T * L.H)) != hipSuccess) return e;
   // router logits and, as column E, the shared-gate logit in the same
   // 16-lane order; the selection kernel applies the gate's sigmoid and its
   // GATE_ERROR checks
@@ -402,10 +401,8 @@ hipError_t run_gguf_block(dmh_ctx* c, GgufLayer* G, unsigned long long* status, 
                                     st)) != hipSuccess)
     return e;
   if ((e = dm::launch_gguf_gateup(L, dx, T, dids, c->h.p, ldh, status, st)) != hipSuccess) return e;
-  if ((e = dm::launch_gguf_down(L, c->h.p, ldh, T, dids, c->g_r.p, c->g_rs.p, status, st)) !=
-      hipSuccess)
-    return e;
-  return dm::launch_combine(c->g_r.p, c->g_rs.p, dprobs, dshg, dres, T, L.H, L.K, dy, status, st);
+  return dm::launch_gguf_down_combine(L, c->h.p, ldh, T, dids, dprobs, dshg, dres, dy, status,
+                                      st);
 }
 
 }  // namespace

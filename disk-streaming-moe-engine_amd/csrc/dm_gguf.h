@@ -48,11 +48,13 @@ struct GgufMoeDev {
 // first-error keys of swiglu_forward (phase expert or shared).
 hipError_t launch_gguf_gateup(const GgufMoeDev& L, const float* x, int T, const int32_t* ids,
                               float* h, int ldh, unsigned long long* status, hipStream_t st);
-// routed[t][s][d] = (W_down h[t][s])_d for s < K and shared_out[t][d] for the
-// shared expert.
-hipError_t launch_gguf_down(const GgufMoeDev& L, const float* h, int ldh, int T,
-                            const int32_t* ids, float* routed, float* shared_out,
-                            unsigned long long* status, hipStream_t st);
+// y[t][d] = sum_k probs[t][k] (W_down h[t][k])_d + shg[t] (W_sh_down
+// h[t][K])_d (+ residual[t][d]): the down projections and
+// moe_aggregate_forward's order in one launch per 65535 tokens; K <= 32.
+hipError_t launch_gguf_down_combine(const GgufMoeDev& L, const float* h, int ldh, int T,
+                                    const int32_t* ids, const float* probs, const float* shg,
+                                    const float* residual, float* y, unsigned long long* status,
+                                    hipStream_t st);
 
 // GGUFTensorInfo (gguf.mojo:104-114); offset is relative to the data section.
 struct GgufTensor {

@@ -167,9 +167,10 @@ template <int T>
 __global__ __launch_bounds__(256) void k_gguf_gateup(GgufMoeDev L, const float* __restrict__ x,
                                                      const int32_t* __restrict__ ids,
                                                      float* __restrict__ h, int ldh,
-                                                     unsigned long long* status) {
+                                                     unsigned long long* status, int t0) {
   const int lane = threadIdx.x & 63;
-  const int slot = (int)(blockIdx.y % (unsigned)(L.K + 1)), t = (int)(blockIdx.y / (unsigned)(L.K + 1));
+  const int slot = (int)(blockIdx.y % (unsigned)(L.K + 1));
+  const int t = t0 + (int)(blockIdx.y / (unsigned)(L.K + 1));
   const bool sh = slot == L.K;
   const int rows = sh ? L.Ish : L.I;
   const int r = (int)blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -197,33 +198,44 @@ __global__ __launch_bounds__(256) void k_gguf_gateup(GgufMoeDev L, const float* 
   }
 }
 
+// Down projections and moe_aggregate_forward in one launch: workgroup (d, t)
+// computes output row d of every slot of token t (wave w takes slots w, w+4,
+// ...), then one thread combines them in the reference order, y = sum_k p_k
+// r_k + g r_sh (+ residual), with separate multiply and add.
 template <int T>
-__global__ __launch_bounds__(256) void k_gguf_down(GgufMoeDev L, const float* __restrict__ h,
-                                                   int ldh, const int32_t* __restrict__ ids,
-                                                   float* __restrict__ routed,
-                                                   float* __restrict__ shared_out,
-                                                   unsigned long long* status) {
-  const int lane = threadIdx.x & 63;
-  const int slot = (int)(blockIdx.y % (unsigned)(L.K + 1)), t = (int)(blockIdx.y / (unsigned)(L.K + 1));
-  const bool sh = slot == L.K;
-  const int d = (int)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (d >= L.H) return;
-  const int n = sh ? L.Ish : L.I;
-  const int e = sh ? L.E : ids[(size_t)t * L.K + slot];
-  const uint8_t* wd = L.raw + L.off[(size_t)e * 3 + 2];
-  const float* hv = h + ((size_t)t * (L.K + 1) + slot) * ldh;
-  const int64_t base = (int64_t)d * n;
-  float a = 0.0f;
-  for (int c = lane * 4; c < n; c += 256)
-    a = dot4(values4<T>(wd, base + c, L.layout), *reinterpret_cast<const f32x4*>(hv + c), a);
-  a = wave_sum(a);
-  if (lane == 0) {
-    if (!finite_f(a))
-      record_err(status, err_key(sh ? kPhShared : kPhExpert, t, sh ? 0 : slot, n + d, kEkDown));
-    if (sh)
-      shared_out[(size_t)t * L.H + d] = a;
-    else
-      routed[((size_t)t * L.K + slot) * L.H + d] = a;
+__global__ __launch_bounds__(256) void k_gguf_down_combine(
+    GgufMoeDev L, const float* __restrict__ h, int ldh, const int32_t* __restrict__ ids,
+    const float* __restrict__ probs, const float* __restrict__ shg,
+    const float* __restrict__ residual, float* __restrict__ y, unsigned long long* status,
+    int t0) {
+  __shared__ float part[33];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int d = (int)blockIdx.x, t = t0 + (int)blockIdx.y;
+  for (int slot = wave; slot <= L.K; slot += 4) {
+    const bool sh = slot == L.K;
+    const int n = sh ? L.Ish : L.I;
+    const int e = sh ? L.E : ids[(size_t)t * L.K + slot];
+    const uint8_t* wd = L.raw + L.off[(size_t)e * 3 + 2];
+    const float* hv = h + ((size_t)t * (L.K + 1) + slot) * ldh;
+    const int64_t base = (int64_t)d * n;
+    float a = 0.0f;
+    for (int c = lane * 4; c < n; c += 256)
+      a = dot4(values4<T>(wd, base + c, L.layout), *reinterpret_cast<const f32x4*>(hv + c), a);
+    a = wave_sum(a);
+    if (lane == 0) {
+      if (!finite_f(a))
+        record_err(status, err_key(sh ? kPhShared : kPhExpert, t, sh ? 0 : slot, n + d, kEkDown));
+      part[slot] = a;
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float acc = 0.0f;
+    for (int k = 0; k < L.K; ++k) acc = acc + probs[(size_t)t * L.K + k] * part[k];
+    float total = acc + shg[t] * part[L.K];
+    if (residual) total = total + residual[(size_t)t * L.H + d];
+    if (!finite_f(total)) record_err(status, err_key(kPhAgg, t, 0, d, 0));
+    y[(size_t)t * L.H + d] = total;
   }
 }
 
@@ -273,17 +285,26 @@ hipError_t launch_gguf_gateup(const GgufMoeDev& L, const float* x, int T, const 
   if (T <= 0 || L.H % 4 || L.I % 4 || L.Ish % 4 || ldh % 4 || ldh < L.I || ldh < L.Ish)
     return hipErrorInvalidValue;
   const int rows = L.I > L.Ish ? L.I : L.Ish;
-  const dim3 grid((unsigned)((rows + 3) / 4), (unsigned)(T * (L.K + 1)));
-  DM_GGUF_DISPATCH(k_gguf_gateup, grid, L, x, ids, h, ldh, status)
+  const int chunk = 65535 / (L.K + 1);  // tokens per launch: grid.y <= 65535
+  for (int t0 = 0; t0 < T; t0 += chunk) {
+    const int n = T - t0 < chunk ? T - t0 : chunk;
+    const dim3 grid((unsigned)((rows + 3) / 4), (unsigned)(n * (L.K + 1)));
+    DM_GGUF_DISPATCH(k_gguf_gateup, grid, L, x, ids, h, ldh, status, t0)
+  }
   return hipGetLastError();
 }
 
-hipError_t launch_gguf_down(const GgufMoeDev& L, const float* h, int ldh, int T,
-                            const int32_t* ids, float* routed, float* shared_out,
-                            unsigned long long* status, hipStream_t st) {
-  if (T <= 0 || L.H % 4 || L.I % 4 || L.Ish % 4 || ldh % 4) return hipErrorInvalidValue;
-  const dim3 grid((unsigned)((L.H + 3) / 4), (unsigned)(T * (L.K + 1)));
-  DM_GGUF_DISPATCH(k_gguf_down, grid, L, h, ldh, ids, routed, shared_out, status)
+hipError_t launch_gguf_down_combine(const GgufMoeDev& L, const float* h, int ldh, int T,
+                                    const int32_t* ids, const float* probs, const float* shg,
+                                    const float* residual, float* y, unsigned long long* status,
+                                    hipStream_t st) {
+  if (T <= 0 || L.K > 32 || L.H % 4 || L.I % 4 || L.Ish % 4 || ldh % 4)
+    return hipErrorInvalidValue;
+  for (int t0 = 0; t0 < T; t0 += 65535) {
+    const int n = T - t0 < 65535 ? T - t0 : 65535;
+    const dim3 grid((unsigned)L.H, (unsigned)n);
+    DM_GGUF_DISPATCH(k_gguf_down_combine, grid, L, h, ldh, ids, probs, shg, residual, y, status, t0)
+  }
   return hipGetLastError();
 }
 #undef DM_GGUF_DISPATCH
