@@ -1234,6 +1234,14 @@ int dmh_upload_moe_layer_gguf(dmh_ctx* c, int layer, const dmh_moe_dims* d,
       return set_err(err, errlen, DMH_ERR_FORMAT,
                      "dmh_upload_moe_layer_gguf: expert tensor %s has GGML type %d, the others %d",
                      name.c_str(), ty, exp_t);
+    // the reference leaves the weights of a partial last block at 0.0; the
+    // expert kernels decode whole blocks only
+    int bs = 1, bpb = 0;
+    dm::gguf_block_spec(ty, &bs, &bpb);
+    if (want % bs)
+      return set_err(err, errlen, DMH_ERR_FORMAT,
+                     "dmh_upload_moe_layer_gguf: expert tensor %s has %lld weights, not whole "
+                     "blocks of %d", name.c_str(), (long long)want, bs);
     exp_t = ty;
     *o = (int64_t)payload.size();
     payload.insert(payload.end(), tmp.begin(), tmp.end());

@@ -178,13 +178,13 @@ def make_layer_device(hidden: int, num_experts: int, top_k: int, inter: int, int
 
 # ---- GGUF layers ------------------------------------------------------------
 def gguf_payload(rng, ggml_type: int, n: int, scale: float = 1e-4) -> bytes:
-    """Random payload of n weights (a multiple of the block size) whose
-    super-scales are fp16 values near `scale` (Q8_0: 20 x scale)."""
+    """Random payload of n weights whose super-scales are fp16 values near
+    `scale` (Q8_0: 20 x scale)."""
     import numpy as np
     if ggml_type == 0:
         return (rng.standard_normal(n) * scale * 100).astype("<f4").tobytes()
     bs, bpb, d_off = {8: (32, 34, 0), 12: (256, 144, 0), 11: (256, 114, 112)}[ggml_type]
-    nb = n // bs
+    nb = -(-n // bs)  # a partial last block is stored whole
     raw = rng.integers(0, 256, size=(nb, bpb), dtype=np.uint8)
     d = (rng.uniform(0.5, 1.5, nb) * scale * (20 if ggml_type == 8 else 1)).astype(np.float16)
     raw[:, d_off:d_off + 2] = d.view(np.uint8).reshape(nb, 2)

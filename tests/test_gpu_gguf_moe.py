@@ -162,6 +162,25 @@ def test_loader_errors(block, tmp_path):
                                      "blk.0.ffn_down.1.weight has GGML type 12, the others 11")
 
 
+def test_partial_blocks_rejected(block, tmp_path):
+    # 100 x 36 Q8_0 weights are 112.5 blocks of 32 (F32 experts of that
+    # size, blocks of one weight, upload)
+    p = str(tmp_path / "f32.gguf")
+    gguf.write_gguf(p, synth.make_gguf_moe_layer(100, 2, 36, 36, seed=3, expert_type=0))
+    with gguf.parse_gguf_index(p) as g:
+        block.upload_layer_gguf(23, (100, 2, 1, 36, 36), g)
+    rng = np.random.default_rng(4)
+    ts = synth.make_gguf_moe_layer(100, 2, 36, 36, seed=4, expert_type=0)
+    ts = [(n, d, 8, synth.gguf_payload(rng, 8, -(-(36 * 100) // 32) * 32)) if ty == 0 and
+          "shared_gate.weight" != n.split(".", 2)[2] else (n, d, ty, raw) for n, d, ty, raw in ts]
+    p = str(tmp_path / "partial.gguf")
+    gguf.write_gguf(p, ts)
+    with gguf.parse_gguf_index(p) as g:
+        assert _upload_err(block, g, dims=(100, 2, 1, 36, 36)) == (
+            "dmh_upload_moe_layer_gguf: expert tensor blk.0.ffn_gate.0.weight has 3600 weights, "
+            "not whole blocks of 32")
+
+
 def test_forward_errors(block, tmp_path):
     dims = (128, 4, 2, 32, 32)
     g = _layer_file(tmp_path, "ok.gguf", lambda ts: ts)
