@@ -163,7 +163,31 @@ __device__ __forceinline__ float dot4(f32x4 a, f32x4 b, float acc) {
   return __builtin_fmaf(a.w, b.w, acc);
 }
 
-template <int T>
+// W consecutive weights at element e0 (a multiple of W, W in {4, 8}).  For
+// Q3_K eight weights share one hmask byte, two code bytes, the scale byte
+// and d, so the block header is decoded once per eight.
+template <int T, int W>
+__device__ __forceinline__ void valuesW(const uint8_t* raw, int64_t e0, int layout, f32x4 (&v)[W / 4]) {
+  if constexpr (T == kGgmlQ3_K && W == 8) {
+    const uint8_t* blk = raw + (e0 >> 8) * 114;
+    const int e = (int)(e0 & 255);
+    const uint16_t* h = reinterpret_cast<const uint16_t*>(blk);
+    const uint32_t hm = blk[e >> 3];
+    const uint32_t qs = h[16 + (e >> 3)];  // code bytes 32 + e/4 and the next
+    const float fs = (float)((int)blk[96 + (e >> 4)] - 32) * h2f(h[56]);
+    float w[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      w[i] = fs * (float)((int)((((hm >> i) & 1) << 2) | ((qs >> (2 * i)) & 3)) - 4);
+    v[0] = f32x4{w[0], w[1], w[2], w[3]};
+    v[1] = f32x4{w[4], w[5], w[6], w[7]};
+  } else {
+#pragma unroll
+    for (int j = 0; j < W / 4; ++j) v[j] = values4<T>(raw, e0 + 4 * j, layout);
+  }
+}
+
+template <int T, int W>
 __global__ __launch_bounds__(256) void k_gguf_gateup(GgufMoeDev L, const float* __restrict__ x,
                                                      const int32_t* __restrict__ ids,
                                                      float* __restrict__ h, int ldh,
@@ -181,10 +205,16 @@ __global__ __launch_bounds__(256) void k_gguf_gateup(GgufMoeDev L, const float* 
   const float* xt = x + (size_t)t * L.H;
   const int64_t base = (int64_t)r * L.H;
   float ag = 0.0f, au = 0.0f;
-  for (int c = lane * 4; c < L.H; c += 256) {
-    const f32x4 xv = *reinterpret_cast<const f32x4*>(xt + c);
-    ag = dot4(values4<T>(wg, base + c, L.layout), xv, ag);
-    au = dot4(values4<T>(wu, base + c, L.layout), xv, au);
+  for (int c = lane * W; c < L.H; c += 64 * W) {
+    f32x4 g4[W / 4], u4[W / 4];
+    valuesW<T, W>(wg, base + c, L.layout, g4);
+    valuesW<T, W>(wu, base + c, L.layout, u4);
+#pragma unroll
+    for (int j = 0; j < W / 4; ++j) {
+      const f32x4 xv = *reinterpret_cast<const f32x4*>(xt + c + 4 * j);
+      ag = dot4(g4[j], xv, ag);
+      au = dot4(u4[j], xv, au);
+    }
   }
   ag = wave_sum(ag);
   au = wave_sum(au);
@@ -202,7 +232,7 @@ __global__ __launch_bounds__(256) void k_gguf_gateup(GgufMoeDev L, const float* 
 // computes output row d of every slot of token t (wave w takes slots w, w+4,
 // ...), then one thread combines them in the reference order, y = sum_k p_k
 // r_k + g r_sh (+ residual), with separate multiply and add.
-template <int T>
+template <int T, int W>
 __global__ __launch_bounds__(256) void k_gguf_down_combine(
     GgufMoeDev L, const float* __restrict__ h, int ldh, const int32_t* __restrict__ ids,
     const float* __restrict__ probs, const float* __restrict__ shg,
@@ -219,8 +249,13 @@ __global__ __launch_bounds__(256) void k_gguf_down_combine(
     const float* hv = h + ((size_t)t * (L.K + 1) + slot) * ldh;
     const int64_t base = (int64_t)d * n;
     float a = 0.0f;
-    for (int c = lane * 4; c < n; c += 256)
-      a = dot4(values4<T>(wd, base + c, L.layout), *reinterpret_cast<const f32x4*>(hv + c), a);
+    for (int c = lane * W; c < n; c += 64 * W) {
+      f32x4 w4[W / 4];
+      valuesW<T, W>(wd, base + c, L.layout, w4);
+#pragma unroll
+      for (int j = 0; j < W / 4; ++j)
+        a = dot4(w4[j], *reinterpret_cast<const f32x4*>(hv + c + 4 * j), a);
+    }
     a = wave_sum(a);
     if (lane == 0) {
       if (!finite_f(a))
@@ -270,14 +305,21 @@ hipError_t launch_dequant_gguf(int t, const uint8_t* raw, int64_t n, int layout,
   return hipGetLastError();
 }
 
-#define DM_GGUF_DISPATCH(KERNEL, GRID, ...)                                               \
+// eight weights per lane when every row length allows it, else four
+#define DM_GGUF_DISPATCH_W(KERNEL, W, GRID, ...)                                          \
   switch (L.type) {                                                                       \
-    case kGgmlQ8_0: KERNEL<kGgmlQ8_0><<<GRID, 256, 0, st>>>(__VA_ARGS__); break;          \
-    case kGgmlQ4_K: KERNEL<kGgmlQ4_K><<<GRID, 256, 0, st>>>(__VA_ARGS__); break;          \
-    case kGgmlQ3_K: KERNEL<kGgmlQ3_K><<<GRID, 256, 0, st>>>(__VA_ARGS__); break;          \
-    case kGgmlBF16: KERNEL<kGgmlBF16><<<GRID, 256, 0, st>>>(__VA_ARGS__); break;          \
-    case kGgmlF32: KERNEL<kGgmlF32><<<GRID, 256, 0, st>>>(__VA_ARGS__); break;            \
+    case kGgmlQ8_0: KERNEL<kGgmlQ8_0, W><<<GRID, 256, 0, st>>>(__VA_ARGS__); break;       \
+    case kGgmlQ4_K: KERNEL<kGgmlQ4_K, W><<<GRID, 256, 0, st>>>(__VA_ARGS__); break;       \
+    case kGgmlQ3_K: KERNEL<kGgmlQ3_K, W><<<GRID, 256, 0, st>>>(__VA_ARGS__); break;       \
+    case kGgmlBF16: KERNEL<kGgmlBF16, W><<<GRID, 256, 0, st>>>(__VA_ARGS__); break;       \
+    case kGgmlF32: KERNEL<kGgmlF32, W><<<GRID, 256, 0, st>>>(__VA_ARGS__); break;         \
     default: return hipErrorInvalidValue;                                                 \
+  }
+#define DM_GGUF_DISPATCH(KERNEL, GRID, ...)                                               \
+  if (L.H % 8 == 0 && L.I % 8 == 0 && L.Ish % 8 == 0) {                                   \
+    DM_GGUF_DISPATCH_W(KERNEL, 8, GRID, __VA_ARGS__)                                      \
+  } else {                                                                                \
+    DM_GGUF_DISPATCH_W(KERNEL, 4, GRID, __VA_ARGS__)                                      \
   }
 
 hipError_t launch_gguf_gateup(const GgufMoeDev& L, const float* x, int T, const int32_t* ids,
@@ -308,5 +350,6 @@ hipError_t launch_gguf_down_combine(const GgufMoeDev& L, const float* h, int ldh
   return hipGetLastError();
 }
 #undef DM_GGUF_DISPATCH
+#undef DM_GGUF_DISPATCH_W
 
 }  // namespace dm

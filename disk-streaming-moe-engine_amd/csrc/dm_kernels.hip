@@ -222,14 +222,96 @@ __global__ __launch_bounds__(256) void k_router_generic(const float* __restrict_
   if (bad_w && !gate) record_err(status, err_key(kPhRouterW, 0, 0, 0, 0));
 }
 
+// The same rows with H <= 2048 staged in LDS first: a one-wave workgroup of
+// 4 rows loads them and x with 16-byte loads all in flight (one memory round
+// trip instead of one per step of the chains), checks every element once,
+// then runs the 16-lane chains from LDS.  Row stride H + 16 floats keeps the
+// two rows a half-wave reads on different banks.
+constexpr int kRouterLdsMaxH = 2048;
+__global__ __launch_bounds__(64) void k_router_lds(const float* __restrict__ x,
+                                                    const float* __restrict__ w, int T, int H,
+                                                    int E, float* __restrict__ z,
+                                                    unsigned long long* status, int t0,
+                                                    const float* __restrict__ w_sh) {
+  __shared__ __attribute__((aligned(16))) float sx[kRouterLdsMaxH];
+  __shared__ __attribute__((aligned(16))) float sw[4][kRouterLdsMaxH + 16];
+  const int tid = threadIdx.x;
+  const int t = t0 + (int)blockIdx.y;
+  const int ldz = w_sh ? E + 1 : E;
+  const int row0 = (int)blockIdx.x * 4;
+  const float* xr = x + (int64_t)t * H;
+  bool bad_x = false, bad_w = false;
+  // x and the 4 rows: lane tid takes columns 4 (tid + 64 j) of each, all
+  // 40 loads issued before the first LDS store
+  constexpr int kJ = kRouterLdsMaxH / 256;
+  f32x4 v[5][kJ];
+#pragma unroll
+  for (int r = 0; r < 5; ++r) {
+    const int e = row0 + r - 1;  // r = 0: x
+    const float* src = r == 0 ? xr : e == E ? w_sh : w + (int64_t)(e < ldz ? e : 0) * H;
+#pragma unroll
+    for (int j = 0; j < kJ; ++j) {
+      const int k = (tid + 64 * j) * 4;
+      v[r][j] = (k < H && (r == 0 || e < ldz)) ? *reinterpret_cast<const f32x4*>(src + k)
+                                               : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < 5; ++r) {
+    const int e = row0 + r - 1;
+#pragma unroll
+    for (int j = 0; j < kJ; ++j) {
+      const int k = (tid + 64 * j) * 4;
+      if (k >= H) continue;
+      const f32x4 q = v[r][j];
+      const bool bad = !finite_f(q.x) | !finite_f(q.y) | !finite_f(q.z) | !finite_f(q.w);
+      if (r == 0) {
+        bad_x |= bad;
+        *reinterpret_cast<f32x4*>(&sx[k]) = q;
+      } else if (e < ldz) {
+        if (e != E) bad_w |= bad;
+        *reinterpret_cast<f32x4*>(&sw[r - 1][k]) = q;
+      }
+    }
+  }
+  __syncthreads();
+  const int l = tid & 15, r = tid >> 4, e = row0 + r;
+  const bool row = e < ldz, gate = e == E;
+  const int h16 = H & ~15;
+  float acc = 0.0f;
+  if (row) {
+#pragma unroll 8
+    for (int k = l; k < h16; k += 16) acc = acc + sx[k] * sw[r][k];
+  }
+#pragma unroll
+  for (int wdt = 8; wdt >= 1; wdt >>= 1) {
+    const float o = __shfl_down(acc, wdt, 16);
+    if (l < wdt) acc = acc + o;
+  }
+  if (row && l == 0) {
+    float s = acc;
+    for (int k = h16; k < H; ++k) s = s + sx[k] * sw[r][k];
+    if (!gate && !finite_f(s)) record_err(status, err_key(kPhLogit, t, 0, e, 0));
+    z[(int64_t)t * ldz + e] = s;
+  }
+  if (bad_x) record_err(status, err_key(kPhX, 0, 0, 0, 0));
+  if (bad_w) record_err(status, err_key(kPhRouterW, 0, 0, 0, 0));
+}
+
 hipError_t launch_router_generic(const float* x, const float* w, int T, int H, int E, float* z,
                                  unsigned long long* status, hipStream_t st, const float* w_sh) {
   if (T <= 0 || E <= 0) return hipErrorInvalidValue;
   const int rows = w_sh ? E + 1 : E;
+  const bool lds = H <= kRouterLdsMaxH && H % 4 == 0 &&
+                   (((uintptr_t)x | (uintptr_t)w | (uintptr_t)w_sh) & 15) == 0;
   for (int t0 = 0; t0 < T; t0 += 65535) {  // grid.y holds at most 65535 tokens
     const int n = T - t0 < 65535 ? T - t0 : 65535;
-    hipLaunchKernelGGL(k_router_generic, dim3((unsigned)((rows + 15) / 16), (unsigned)n),
-                       dim3(256), 0, st, x, w, T, H, E, z, status, t0, w_sh);
+    if (lds)
+      hipLaunchKernelGGL(k_router_lds, dim3((unsigned)((rows + 3) / 4), (unsigned)n), dim3(64), 0,
+                         st, x, w, T, H, E, z, status, t0, w_sh);
+    else
+      hipLaunchKernelGGL(k_router_generic, dim3((unsigned)((rows + 15) / 16), (unsigned)n),
+                         dim3(256), 0, st, x, w, T, H, E, z, status, t0, w_sh);
   }
   return hipGetLastError();
 }

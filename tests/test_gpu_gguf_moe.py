@@ -162,13 +162,15 @@ def test_loader_errors(block, tmp_path):
                                      "blk.0.ffn_down.1.weight has GGML type 12, the others 11")
 
 
-def test_partial_blocks_rejected(block, tmp_path):
+def test_partial_blocks_rejected(block, oracle, tmp_path):
     # 100 x 36 Q8_0 weights are 112.5 blocks of 32 (F32 experts of that
     # size, blocks of one weight, upload)
     p = str(tmp_path / "f32.gguf")
     gguf.write_gguf(p, synth.make_gguf_moe_layer(100, 2, 36, 36, seed=3, expert_type=0))
     with gguf.parse_gguf_index(p) as g:
         block.upload_layer_gguf(23, (100, 2, 1, 36, 36), g)
+        # rows of 100 and 36: the kernels' four-weights-per-lane form
+        _check_layer(block, oracle, g, 0, (100, 2, 1, 36, 36), 23, T=3, seed=85)
     rng = np.random.default_rng(4)
     ts = synth.make_gguf_moe_layer(100, 2, 36, 36, seed=4, expert_type=0)
     ts = [(n, d, 8, synth.gguf_payload(rng, 8, -(-(36 * 100) // 32) * 32)) if ty == 0 and
