@@ -163,12 +163,26 @@ __device__ __forceinline__ float dot4(f32x4 a, f32x4 b, float acc) {
   return __builtin_fmaf(a.w, b.w, acc);
 }
 
-// W consecutive weights at element e0 (a multiple of W, W in {4, 8}).  For
-// Q3_K eight weights share one hmask byte, two code bytes, the scale byte
-// and d, so the block header is decoded once per eight.
+// W consecutive weights at element e0 (a multiple of W, W in {4, 8, 16}).
+// For Q3_K eight weights share one hmask byte, two code bytes, the scale
+// byte and d, so the block header is decoded once per eight (sixteen).
 template <int T, int W>
 __device__ __forceinline__ void valuesW(const uint8_t* raw, int64_t e0, int layout, f32x4 (&v)[W / 4]) {
-  if constexpr (T == kGgmlQ3_K && W == 8) {
+  if constexpr (T == kGgmlQ3_K && W == 16) {
+    // sixteen weights: two hmask bytes, four code bytes, one scale byte
+    const uint8_t* blk = raw + (e0 >> 8) * 114;
+    const int e = (int)(e0 & 255);
+    const uint16_t* h = reinterpret_cast<const uint16_t*>(blk);
+    const uint32_t hm = h[e >> 4];
+    const uint32_t qs = (uint32_t)h[16 + (e >> 3)] | ((uint32_t)h[17 + (e >> 3)] << 16);
+    const float fs = (float)((int)blk[96 + (e >> 4)] - 32) * h2f(h[56]);
+    float w[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+      w[i] = fs * (float)((int)((((hm >> i) & 1) << 2) | ((qs >> (2 * i)) & 3)) - 4);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[j] = f32x4{w[4 * j], w[4 * j + 1], w[4 * j + 2], w[4 * j + 3]};
+  } else if constexpr (T == kGgmlQ3_K && W == 8) {
     const uint8_t* blk = raw + (e0 >> 8) * 114;
     const int e = (int)(e0 & 255);
     const uint16_t* h = reinterpret_cast<const uint16_t*>(blk);
@@ -331,7 +345,11 @@ hipError_t launch_gguf_gateup(const GgufMoeDev& L, const float* x, int T, const 
   for (int t0 = 0; t0 < T; t0 += chunk) {
     const int n = T - t0 < chunk ? T - t0 : chunk;
     const dim3 grid((unsigned)((rows + 3) / 4), (unsigned)(n * (L.K + 1)));
-    DM_GGUF_DISPATCH(k_gguf_gateup, grid, L, x, ids, h, ldh, status, t0)
+    if (L.H % 16 == 0) {  // rows of H weights: sixteen per lane
+      DM_GGUF_DISPATCH_W(k_gguf_gateup, 16, grid, L, x, ids, h, ldh, status, t0)
+    } else {
+      DM_GGUF_DISPATCH(k_gguf_gateup, grid, L, x, ids, h, ldh, status, t0)
+    }
   }
   return hipGetLastError();
 }
