@@ -216,3 +216,20 @@ def test_forward_errors(block, tmp_path):
     # the layer recovers: the same layer, finite inputs, other weights fine
     block.upload_layer_gguf(25, dims, _layer_file(tmp_path, "ok2.gguf", lambda ts: ts))
     block.forward_port_moe_gguf(x, None, 25, 2)
+
+
+def test_many_tokens_cross_launch_chunks(block, tmp_path):
+    """65537 tokens: the router and down launches split at 65535 tokens, the
+    gate/up launch at 65535 / (K + 1); rows on either side of every split
+    equal the same tokens computed alone, bit for bit."""
+    dims = (128, 4, 2, 32, 32)
+    g = _layer_file(tmp_path, "many.gguf", lambda ts: ts)
+    block.upload_layer_gguf(26, dims, g)
+    T = 65537
+    x = synth.make_activations(np.random.default_rng(95), (T, 128))
+    y, ids, probs, shg = block.forward_port_moe_gguf(x, None, 26, T)
+    for t in (0, 21844, 21845, 43690, 43691, 65534, 65535, 65536):
+        y1, i1, p1, s1 = block.forward_port_moe_gguf(x[t:t + 1], None, 26, 1)
+        assert np.array_equal(y[t].view(np.uint32), y1[0].view(np.uint32)), t
+        assert np.array_equal(ids[t], i1[0]) and np.array_equal(probs[t], p1[0]), t
+        assert s1[0] == shg[t], t
