@@ -79,8 +79,8 @@ def _materialise(case, tmp_path):
 # The corpus drives the reference's CLI; cases 01, 02 and 04 are turned away
 # by its format detector before parse_gguf_index runs, and the name and dims
 # mutations that the index accepts fail later, when the loader looks the
-# tensor up or checks its shape.  These are the index's own verdicts.
-PARSE_VERDICT = {
+# tensor up or checks its shape.  These are the index's own results.
+PARSE_RESULT = {
     "FUZZ_01_CORRUPT_MAGIC": "GGUF_FILE_CORRUPT: invalid magic header (expected 'GGUF')",
     "FUZZ_02_UNSUPPORTED_VERSION": "GGUF_FILE_CORRUPT: unsupported version 99",
     "FUZZ_03_TRUNCATED_HEADER": "GGUF_FILE_CORRUPT: file size 12 too small for header",
@@ -103,11 +103,11 @@ RENAMED = {"FUZZ_13": "token_embd.weight", "FUZZ_16": "output.weight",
 def test_fuzz_corpus(case, tmp_path):
     path = _materialise(case, tmp_path)
     key = case["id"][:7]
-    if case["id"] in PARSE_VERDICT or key in BEYOND:
+    if case["id"] in PARSE_RESULT or key in BEYOND:
         with pytest.raises(DismoenError) as ei:
             gguf.parse_gguf_index(path)
         msg = str(ei.value)
-        want = PARSE_VERDICT.get(case["id"],
+        want = PARSE_RESULT.get(case["id"],
                                  "GGUF_FILE_CORRUPT: tensor extends beyond file boundary")
         assert msg == want
         if case["want_err"].startswith("GGUF"):
