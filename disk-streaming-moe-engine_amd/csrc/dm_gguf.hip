@@ -121,6 +121,24 @@ __global__ __launch_bounds__(256) void k_dequant_gguf(const uint8_t* __restrict_
   }
   const int64_t f = (int64_t)wg * 256 + threadIdx.x;
   const int64_t e0 = f * 4;
+  if constexpr (T == kGgmlQ4_K) {
+    // A workgroup's 1024 outputs are 4 whole Q4_K blocks, 576 contiguous
+    // bytes at a 4-byte aligned offset: load them with coalesced dwords into
+    // LDS and decode from there, instead of each lane issuing five dword
+    // loads into the same lines (Q4_K 203 -> 161 us per layer; the same for
+    // Q8_0's 1088 bytes measured slower, 251 -> 303 us).
+    constexpr int kBytes = 576;
+    __shared__ __attribute__((aligned(16))) uint32_t sblk[kBytes / 4];
+    const int64_t w0 = (int64_t)wg * 1024;  // first output of the workgroup
+    if (w0 + 1024 <= n_blk) {                // uniform over the workgroup
+      const uint32_t* src = reinterpret_cast<const uint32_t*>(raw + (w0 >> 8) * 144);
+      for (int i = threadIdx.x; i < kBytes / 4; i += 256) sblk[i] = src[i];
+      __syncthreads();
+      const f32x4 v = values4<T>(reinterpret_cast<const uint8_t*>(sblk), e0 - w0, layout);
+      __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(out + e0));
+      return;
+    }
+  }
   if (e0 >= n) return;
   f32x4 v = {0.0f, 0.0f, 0.0f, 0.0f};
   if (e0 + 4 <= n_blk) {
