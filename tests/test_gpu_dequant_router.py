@@ -66,7 +66,9 @@ def test_router_known_values(block):
 
 
 @pytest.mark.parametrize("T,H,E,K,scale", [(16, 256, 16, 4, 0.02), (1000, 2048, 256, 8, 0.02),
-                                           (64, 100, 60, 4, 0.05), (32, 2048, 256, 8, 0.0)])
+                                           (64, 100, 60, 4, 0.05), (32, 2048, 256, 8, 0.0),
+                                           # rows beyond the LDS form: H > 2048, H % 4 != 0
+                                           (8, 4096, 40, 4, 0.02), (8, 2050, 24, 4, 0.02)])
 def test_router_bit_exact_vs_oracle(block, oracle, T, H, E, K, scale):
     rng = np.random.default_rng(T + H)
     x = rng.standard_normal((T, H)).astype(np.float32)
