@@ -283,7 +283,13 @@ hipError_t run_block(dmh_ctx* ctx, Layer* Ly, int layer, const float* dx, const 
     if ((e = ctx->g_off.ensure(L.E + 1)) != hipSuccess) return e;
     if ((e = ctx->g_perm.ensure(TK)) != hipSuccess) return e;
     if ((e = ctx->g_meta.ensure(2)) != hipSuccess) return e;
+    // need-lo flag: zero between calls (set zero at allocation, cleared by
+    // the combine kernel that ends every call)
+    const size_t nl_cap = ctx->g_needlo.cap;
     if ((e = ctx->g_needlo.ensure(1)) != hipSuccess) return e;
+    if (ctx->g_needlo.cap != nl_cap &&
+        (e = hipMemsetAsync(ctx->g_needlo.p, 0, sizeof(int), st)) != hipSuccess)
+      return e;
     if ((e = ctx->g_units.ensure(dm::group_units_max(T, L.K, L.E))) != hipSuccess) return e;
     if ((e = ctx->g_xhi.ensure(TH)) != hipSuccess) return e;
     if ((e = ctx->g_xlo.ensure(TH)) != hipSuccess) return e;
@@ -291,7 +297,6 @@ hipError_t run_block(dmh_ctx* ctx, Layer* Ly, int layer, const float* dx, const 
     if ((e = ctx->g_hs.ensure(2 * (size_t)T * L.Ish)) != hipSuccess) return e;
     if ((e = ctx->g_r.ensure(TK * L.H)) != hipSuccess) return e;
     if ((e = ctx->g_rs.ensure(TH)) != hipSuccess) return e;
-    if ((e = hipMemsetAsync(ctx->g_needlo.p, 0, sizeof(int), st)) != hipSuccess) return e;
     if ((e = dm::launch_split_rows(dx, (int64_t)TH, ctx->g_xhi.p, ctx->g_xlo.p, ctx->g_needlo.p,
                                    st)) != hipSuccess)
       return e;
@@ -319,7 +324,7 @@ hipError_t run_block(dmh_ctx* ctx, Layer* Ly, int layer, const float* dx, const 
                                         ctx->g_rs.p, status, st)) != hipSuccess)
       return e;
     return dm::launch_combine(ctx->g_r.p, ctx->g_rs.p, dprobs, dshg, dres, T, L.H, L.K, dy, status,
-                              st);
+                              st, ctx->g_needlo.p);
   }
   if ((e = dm::launch_router_dec(L, dx, T, ctx->z.p, status, st)) != hipSuccess) return e;
   if ((e = dm::launch_router_select(ctx->z.p, L.E + 1, T, L.E, L.K, 1, dids, dprobs, dshg, status,
@@ -1065,6 +1070,8 @@ int dmh_experts_forward(dmh_ctx* c, int layer, const float* x, int T, const int3
                                      c->g_perm.p, c->g_units.p, c->g_meta.p, T, c->g_hr.p,
                                      c->g_hr.p + TK * L.I, c->g_hs.p,
                                      c->g_hs.p + (size_t)T * L.Ish, dout, drs, status, st));
+  // leave the need-lo flag zero, as the block forward expects between calls
+  HIP_TRY(hipMemsetAsync(c->g_needlo.p, 0, sizeof(int), st));
   c->last_ids[layer] = c->uids.p;
   c->last_k[layer] = K;
   if (dev) return DMH_OK;

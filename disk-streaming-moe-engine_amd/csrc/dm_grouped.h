@@ -31,6 +31,6 @@ hipError_t launch_experts_grouped(const LayerDev& L, const uint16_t* xhi, const 
 // y = sum_k p_k r_k + g rs (+ residual), per token in the reference order.
 hipError_t launch_combine(const float* r, const float* rs, const float* probs, const float* shg,
                           const float* residual, int T, int H, int K, float* y,
-                          unsigned long long* status, hipStream_t st);
+                          unsigned long long* status, hipStream_t st, int* clear_flag = nullptr);
 
 }  // namespace dm

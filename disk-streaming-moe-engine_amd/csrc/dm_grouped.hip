@@ -684,8 +684,11 @@ __global__ __launch_bounds__(256) void k_combine(const float* __restrict__ r,
                                                   const float* __restrict__ shg,
                                                   const float* __restrict__ residual, int H, int K,
                                                   float* __restrict__ y,
-                                                  unsigned long long* status) {
+                                                  unsigned long long* status,
+                                                  int* __restrict__ clear_flag) {
   const int t = blockIdx.y, d = blockIdx.x * 256 + threadIdx.x;
+  // the last kernel of a call clears the call's need-lo flag for the next
+  if (clear_flag && t == 0 && d == 0) *clear_flag = 0;
   if (d >= H) return;
   float acc = 0.0f;
   for (int k = 0; k < K; ++k) acc = acc + probs[(size_t)t * K + k] * r[((size_t)t * K + k) * H + d];
@@ -697,9 +700,9 @@ __global__ __launch_bounds__(256) void k_combine(const float* __restrict__ r,
 
 hipError_t launch_combine(const float* r, const float* rs, const float* probs, const float* shg,
                           const float* residual, int T, int H, int K, float* y,
-                          unsigned long long* status, hipStream_t st) {
+                          unsigned long long* status, hipStream_t st, int* clear_flag) {
   hipLaunchKernelGGL(k_combine, dim3((H + 255) / 256, T), dim3(256), 0, st, r, rs, probs, shg,
-                     residual, H, K, y, status);
+                     residual, H, K, y, status, clear_flag);
   return hipGetLastError();
 }
 
