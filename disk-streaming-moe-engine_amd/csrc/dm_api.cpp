@@ -6,10 +6,14 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <algorithm>
+#include <new>
+#include <stdexcept>
 #include <string>
 #include <vector>
 
 #include "../../include/dismoen_hip.h"
+#include "dm_api_internal.h"
 #include "dm_decode.h"
 #include "dm_gguf.h"
 #include "dm_grouped.h"
@@ -49,6 +53,9 @@ struct Layer {
   void* sync = nullptr;
   size_t sync_bytes = 0;
   unsigned launches = 0;
+  // post_attention_layernorm gamma [H] fp32 of the block-edge RMSNorm
+  // (dmh_set_layer_norm); nullptr: gamma = 1
+  float* gamma = nullptr;
 };
 
 template <typename T>
@@ -121,6 +128,8 @@ struct dmh_ctx {
   std::vector<const int32_t*> last_ids;
   std::vector<int> last_k;
   int num_cus = 0;
+  float* ones = nullptr;          // [kNormMaxH] 1.0f: gamma of layers without one
+  hipEvent_t switch_ev = nullptr;  // orders a stream switch after queued work
 };
 
 namespace {
@@ -216,6 +225,28 @@ int router_config_check(int E, int K, int norm, char* err, size_t errlen) {
   return DMH_OK;
 }
 
+}  // namespace
+
+// The dimensions the 4-bit block supports, checked before any arithmetic
+// or allocation that depends on them.  group_size: the reference's allowed
+// sizes (src/format/half_float.mojo:24-31, is_allowed_group_size).
+int dm::api_moe_dims_check(const dmh_moe_dims* d, int layer, char* err, size_t errlen) {
+  const int H = d->hidden, E = d->num_experts, K = d->top_k, I = d->inter, Ish = d->inter_sh;
+  const int G = d->group_size;
+  const bool g_ok = G == 32 || G == 64 || G == 128 || G == 256;
+  if (!g_ok || E <= 0 || K <= 0 || H <= 0 || I <= 0 || Ish <= 0 || H % 128 || I % 128 ||
+      Ish % 128 || E > 2048 || K + 1 > 33 || H > 8192 || I > 8192 || Ish > 8192 ||
+      (size_t)(K + 1) * (I > Ish ? I : Ish) * 6 > 65536)
+    return set_err(err, errlen, DMH_ERR_CONFIG,
+                   "{\"error_type\":\"CONFIG_ERROR\",\"detail\":\"unsupported MoE dims: G=%d H=%d"
+                   " E=%d K=%d I=%d Ish=%d (need G in {32, 64, 128, 256}, H/I/Ish multiples of"
+                   " 128, E<=2048, K<=32, H/I/Ish<=8192)\",\"stage\":\"config\",\"layer\":%d}",
+                   G, H, E, K, I, Ish, layer);
+  return DMH_OK;
+}
+
+namespace {
+
 Layer* get_layer(dmh_ctx* ctx, int layer) {
   if (!ctx || layer < 0 || layer >= (int)ctx->layers.size()) return nullptr;
   return ctx->layers[layer];
@@ -236,29 +267,40 @@ void free_layer(Layer* Ly) {
   if (!Ly) return;
   if (Ly->buf) (void)hipFree(Ly->buf);
   if (Ly->sync) (void)hipFree(Ly->sync);
+  if (Ly->gamma) (void)hipFree(Ly->gamma);
   delete Ly;
+}
+
+// The block-edge norm of a layer: its gamma, or the context's ones.
+dm::NormSpec layer_norm(const dmh_ctx* ctx, const Layer* Ly, float eps, bool tree) {
+  return dm::NormSpec{eps, Ly->gamma ? Ly->gamma : ctx->ones, tree ? 0 : 1};
 }
 
 // Token counts from which the router runs on the matrix cores (bf16
 // activations); below it the lane-chain router is as fast.
 constexpr int kMfmaRouterMinTokens = 64;
 
-// norm_eps > 0: the block's input is RMSNorm(dx) (gamma = 1), computed inside
-// the fused decode kernel or by a separate kernel into ctx->xn.
+// nm (may be NULL): the block's input is rmsnorm(dx, nm->gamma, nm->eps),
+// computed inside the fused decode kernel or by a separate kernel into ctx->xn.
+// Under stream capture the fused kernel is not used: its launch tag is fixed
+// on the host, so every replay of a captured launch would carry the same tag
+// and its waits would pass on the previous replay's data.
 hipError_t run_block(dmh_ctx* ctx, Layer* Ly, int layer, const float* dx, const float* dres,
                      int T, float* dy, int32_t* dids, float* dprobs, float* dshg,
-                     bool allow_fused = true, float norm_eps = 0.0f) {
+                     bool allow_fused = true, const dm::NormSpec* nm = nullptr) {
   const LayerDev& L = Ly->dev;
   hipStream_t st = ctx->cur;
   unsigned long long* status = ctx->status + layer;
   const int ldh = L.I > L.Ish ? L.I : L.Ish;
   hipError_t e;
-  const bool fused = Ly->fused && allow_fused && T == 1;
-  if (norm_eps > 0.0f && !fused) {
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  if ((e = hipStreamIsCapturing(st, &cap)) != hipSuccess) return e;
+  const bool fused = Ly->fused && allow_fused && T == 1 && cap == hipStreamCaptureStatusNone;
+  const dm::NormSpec no_norm{0.0f, nullptr, 0};
+  const bool norm = nm && nm->eps > 0.0f;
+  if (norm && !fused) {
     if ((e = ctx->xn.ensure((size_t)T * L.H)) != hipSuccess) return e;
-    if ((e = dm::launch_rmsnorm_rows(dx, T, L.H, norm_eps, ctx->xn.p, nullptr, layer, st)) !=
-        hipSuccess)
-      return e;
+    if ((e = dm::launch_rmsnorm_rows(dx, T, L.H, *nm, ctx->xn.p, st)) != hipSuccess) return e;
     dx = ctx->xn.p;
   }
   if (fused) {
@@ -269,7 +311,7 @@ hipError_t run_block(dmh_ctx* ctx, Layer* Ly, int layer, const float* dx, const 
       e = dm::launch_moe_decode(L, Ly->plan, dx + (size_t)t * L.H,
                                 dres ? dres + (size_t)t * L.H : nullptr, dy + (size_t)t * L.H,
                                 dids + (size_t)t * L.K, dprobs + (size_t)t * L.K, dshg + t, S,
-                                status, t, st, norm_eps);
+                                status, t, st, norm ? *nm : no_norm);
       if (e != hipSuccess) return e;
     }
     return hipSuccess;
@@ -433,6 +475,12 @@ int dmh_create(int device, dmh_ctx** out, char* err, size_t errlen) {
   if (e == hipSuccess) e = hipMalloc(&c->flags, sizeof(unsigned));
   if (e == hipSuccess)
     e = hipMemset(c->status, 0xFF, sizeof(unsigned long long) * kStatusSlots);
+  if (e == hipSuccess) e = hipMalloc(&c->ones, sizeof(float) * dm::kNormMaxH);
+  if (e == hipSuccess) {
+    const std::vector<float> one(dm::kNormMaxH, 1.0f);
+    e = hipMemcpy(c->ones, one.data(), sizeof(float) * one.size(), hipMemcpyHostToDevice);
+  }
+  if (e == hipSuccess) e = hipEventCreateWithFlags(&c->switch_ev, hipEventDisableTiming);
   if (e != hipSuccess) {
     dmh_destroy(c);
     return set_err(err, errlen, DMH_ERR_HIP, "dmh_create: %s", hipGetErrorString(e));
@@ -477,6 +525,8 @@ int dmh_destroy(dmh_ctx* c) {
   c->g_r.release();
   c->g_rs.release();
   if (c->status) (void)hipFree(c->status);
+  if (c->ones) (void)hipFree(c->ones);
+  if (c->switch_ev) (void)hipEventDestroy(c->switch_ev);
   if (c->vkey) (void)hipFree(c->vkey);
   if (c->flags) (void)hipFree(c->flags);
   if (c->own) (void)hipStreamDestroy(c->own);
@@ -484,9 +534,17 @@ int dmh_destroy(dmh_ctx* c) {
   return DMH_OK;
 }
 
+// Work queued on the old stream is ordered before everything issued on the
+// new one (an event recorded on the old stream, waited for by the new), so
+// two launches of one layer never interleave their hand-off words.
 int dmh_set_stream(dmh_ctx* c, void* s) {
   if (!c) return DMH_ERR_INVALID_ARG;
-  c->cur = s ? (hipStream_t)s : c->own;
+  hipStream_t nx = s ? (hipStream_t)s : c->own;
+  if (nx == c->cur) return DMH_OK;
+  if (hipSetDevice(c->device) != hipSuccess || hipEventRecord(c->switch_ev, c->cur) != hipSuccess ||
+      hipStreamWaitEvent(nx, c->switch_ev, 0) != hipSuccess)
+    return DMH_ERR_HIP;
+  c->cur = nx;
   return DMH_OK;
 }
 
@@ -531,19 +589,14 @@ int dmh_upload_moe_layer(dmh_ctx* c, int layer, const dmh_moe_dims* d, const dmh
   int rc = router_config_check(d->num_experts, d->top_k, d->norm_topk_prob, err, errlen);
   if (rc) return rc;
   const int H = d->hidden, E = d->num_experts, K = d->top_k, I = d->inter, Ish = d->inter_sh;
-  if (d->group_size != 32 || H <= 0 || I <= 0 || Ish <= 0 || H % 128 || I % 128 || Ish % 128 ||
-      E > 2048 || K + 1 > 33 || (size_t)(K + 1) * (I > Ish ? I : Ish) * 6 > 65536 || H > 8192)
-    return set_err(err, errlen, DMH_ERR_CONFIG,
-                   "{\"error_type\":\"CONFIG_ERROR\",\"detail\":\"unsupported MoE dims: G=%d H=%d"
-                   " E=%d K=%d I=%d Ish=%d (need G=32, H/I/Ish multiples of 128, E<=2048,"
-                   " K<=32, H<=8192)\",\"stage\":\"config\",\"layer\":%d}",
-                   d->group_size, H, E, K, I, Ish, layer);
+  if ((rc = dm::api_moe_dims_check(d, layer, err, errlen)) != DMH_OK) return rc;
   if (!w->router_bf16 || !w->shgate_bf16 || !w->gu_scales || !w->gu_packed || !w->d_scales ||
       !w->d_packed || !w->sh_gu_scales || !w->sh_gu_packed || !w->sh_d_scales || !w->sh_d_packed)
     return set_err(err, errlen, DMH_ERR_INVALID_ARG, "dmh_upload_moe_layer: NULL weight pointer");
   HIP_TRY(hipSetDevice(c->device));
   hipStream_t st = c->cur;
-  const size_t G = 32;
+  // G: one scale per 32 columns on the device; Gs: the source group size
+  const size_t G = 32, Gs = (size_t)d->group_size;
   const size_t n_gu = (size_t)E * 2 * I * H, n_d = (size_t)E * H * I;
   const size_t n_sgu = (size_t)2 * Ish * H, n_sd = (size_t)H * Ish;
   // device layout sizes
@@ -584,8 +637,12 @@ int dmh_upload_moe_layer(dmh_ctx* c, int layer, const dmh_moe_dims* d, const dmh
   if (e != hipSuccess) return fail(DMH_ERR_HIP, "memset", e);
 
   const bool dev = flags & DMH_F_DEVICE;
-  // staging: one tensor group (scales + codes) at a time
-  const size_t stage_bytes = align256(n_gu / 2) + align256(n_gu / G * 2) + 2 * b_router;
+  // staging: one tensor group (scales + codes) at a time, sized for the
+  // largest of the four groups (the shared expert can outgrow the routed
+  // ones), and for the router and shared gate
+  size_t stage_bytes = 2 * b_router;
+  for (size_t n : {n_gu, n_d, n_sgu, n_sd})
+    stage_bytes = std::max(stage_bytes, align256(n / 2) + align256(n / Gs * 2));
   if (!dev && (e = c->stage.ensure(stage_bytes)) != hipSuccess)
     return fail(DMH_ERR_NO_MEMORY, "staging", e);
   auto src = [&](const void* hp, size_t bytes, size_t off, const void** dp) -> hipError_t {
@@ -619,7 +676,7 @@ int dmh_upload_moe_layer(dmh_ctx* c, int layer, const dmh_moe_dims* d, const dmh
   };
   for (const Mat& m : mats) {
     if ((e = src(m.nib, m.n / 2, 0, &s_nib)) != hipSuccess ||
-        (e = src(m.sc, m.n / G * 2, align256(m.n / 2), &s_sc)) != hipSuccess)
+        (e = src(m.sc, m.n / Gs * 2, align256(m.n / 2), &s_sc)) != hipSuccess)
       return fail(DMH_ERR_HIP, "weight copy", e);
     // per-matrix launches keep the tensor index of the validation key in the
     // reference's load order (gate, up, down of expert 0, then expert 1, ...)
@@ -627,8 +684,8 @@ int dmh_upload_moe_layer(dmh_ctx* c, int layer, const dmh_moe_dims* d, const dmh
     for (int i = 0; i < m.nmat; ++i) {
       const int tens = m.tbase + (i / m.per) * 3 + (i % m.per);
       e = dm::launch_repack_a16((const uint8_t*)s_nib + i * (mn / 2),
-                                (const uint16_t*)s_sc + i * (mn / G), m.dn + i * (mn / 2),
-                                m.ds + i * (mn / G), m.R, m.C, 1, tens, c->vkey, st);
+                                (const uint16_t*)s_sc + i * (mn / Gs), m.dn + i * (mn / 2),
+                                m.ds + i * (mn / G), m.R, m.C, 1, tens, (int)Gs, c->vkey, st);
       if (e != hipSuccess) return fail(DMH_ERR_HIP, "repack", e);
     }
     if (!dev && (e = hipStreamSynchronize(st)) != hipSuccess) return fail(DMH_ERR_HIP, "sync", e);
@@ -691,9 +748,15 @@ int dmh_layer_bytes(dmh_ctx* c, int layer, int64_t* bytes) {
   return DMH_OK;
 }
 
-int dmh_moe_forward(dmh_ctx* c, int layer, const float* x, const float* residual, int T,
-                    float* y, int32_t* ids, float* probs, float* shg, unsigned flags, char* err,
-                    size_t errlen) {
+}  // extern "C"
+
+namespace {
+
+// dmh_moe_forward and dmh_port_moe_forward: nm (may be NULL) normalises the
+// block input first.
+int moe_forward_impl(dmh_ctx* c, int layer, const float* x, const float* residual, int T,
+                     float* y, int32_t* ids, float* probs, float* shg, unsigned flags,
+                     const dm::NormSpec* nm, char* err, size_t errlen) {
   Layer* Ly = get_layer(c, layer);
   if (!Ly)
     return set_err(err, errlen, DMH_ERR_INVALID_ARG, "dmh_moe_forward: layer %d not uploaded",
@@ -716,7 +779,7 @@ int dmh_moe_forward(dmh_ctx* c, int layer, const float* x, const float* residual
     if (!dids) { HIP_TRY(c->ids.ensure(TK)); dids = c->ids.p; }
     if (!dprobs) { HIP_TRY(c->probs.ensure(TK)); dprobs = c->probs.p; }
     if (!dshg) { HIP_TRY(c->shg.ensure(T)); dshg = c->shg.p; }
-    HIP_TRY(run_block(c, Ly, layer, x, residual, T, y, dids, dprobs, dshg));
+    HIP_TRY(run_block(c, Ly, layer, x, residual, T, y, dids, dprobs, dshg, true, nm));
     c->last_ids[layer] = dids;
     c->last_k[layer] = L.K;
     return DMH_OK;
@@ -745,7 +808,7 @@ int dmh_moe_forward(dmh_ctx* c, int layer, const float* x, const float* residual
   HIP_TRY(hipMemcpyAsync(din, hin, in_bytes, hipMemcpyHostToDevice, st));
   HIP_TRY(reset_status(c, layer));
   auto run_and_fetch = [&](bool allow_fused) -> hipError_t {
-    hipError_t e = run_block(c, Ly, layer, dx, dres, T, dy, dids, dprobs, dshg, allow_fused);
+    hipError_t e = run_block(c, Ly, layer, dx, dres, T, dy, dids, dprobs, dshg, allow_fused, nm);
     if (e == hipSuccess)
       e = hipMemcpyAsync(dout + o_key, c->status + layer, 8, hipMemcpyDeviceToDevice, st);
     if (e == hipSuccess) e = hipMemcpyAsync(hout, dout, out_bytes, hipMemcpyDeviceToHost, st);
@@ -775,15 +838,73 @@ int dmh_moe_forward(dmh_ctx* c, int layer, const float* x, const float* residual
   return rc;
 }
 
+// rmsnorm's eps check (src/layers/rmsnorm.mojo:36-41).
+int eps_check(float eps, char* err, size_t errlen) {
+  if (eps != eps || eps <= 0.0f || eps > 3.0e38f)
+    return set_err(err, errlen, DMH_ERR_CONFIG,
+                   "{\"error_type\":\"CONFIG_ERROR\",\"detail\":\"rms_norm_eps must be finite"
+                   " and > 0\",\"stage\":\"config\"}");
+  return DMH_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int dmh_moe_forward(dmh_ctx* c, int layer, const float* x, const float* residual, int T,
+                    float* y, int32_t* ids, float* probs, float* shg, unsigned flags, char* err,
+                    size_t errlen) {
+  return moe_forward_impl(c, layer, x, residual, T, y, ids, probs, shg, flags, nullptr, err,
+                          errlen);
+}
+
+int dmh_port_moe_forward(dmh_ctx* c, int layer, const float* x_mid, int T, float eps, float* y,
+                         int32_t* ids, float* probs, float* shg, unsigned flags, char* err,
+                         size_t errlen) {
+  Layer* Ly = get_layer(c, layer);
+  if (!Ly)
+    return set_err(err, errlen, DMH_ERR_INVALID_ARG, "dmh_port_moe_forward: layer %d not uploaded",
+                   layer);
+  if (T <= 0)
+    return set_err(err, errlen, DMH_ERR_NORM,
+                   "{\"error_type\":\"NORM_ERROR\",\"detail\":\"empty input\",\"stage\":"
+                   "\"rmsnorm\"}");
+  int rc = eps_check(eps, err, errlen);
+  if (rc) return rc;
+  const dm::NormSpec nm = layer_norm(c, Ly, eps, (flags & DMH_F_NORM_TREE) != 0);
+  return moe_forward_impl(c, layer, x_mid, x_mid, T, y, ids, probs, shg, flags, &nm, err, errlen);
+}
+
+int dmh_set_layer_norm(dmh_ctx* c, int layer, const float* gamma, int hidden, unsigned flags,
+                       char* err, size_t errlen) {
+  Layer* Ly = get_layer(c, layer);
+  if (!Ly)
+    return set_err(err, errlen, DMH_ERR_INVALID_ARG, "dmh_set_layer_norm: layer %d not uploaded",
+                   layer);
+  if (hidden != Ly->dims.hidden)
+    return set_err(err, errlen, DMH_ERR_NORM,
+                   "{\"error_type\":\"NORM_ERROR\",\"detail\":\"length mismatch\",\"stage\":"
+                   "\"rmsnorm\"}");
+  HIP_TRY(hipSetDevice(c->device));
+  HIP_TRY(hipStreamSynchronize(c->cur));
+  if (!gamma) {
+    if (Ly->gamma) HIP_TRY(hipFree(Ly->gamma));
+    Ly->gamma = nullptr;
+    return DMH_OK;
+  }
+  if (!Ly->gamma) HIP_TRY(hipMalloc(&Ly->gamma, sizeof(float) * (size_t)hidden));
+  HIP_TRY(hipMemcpy(Ly->gamma, gamma, sizeof(float) * (size_t)hidden,
+                    (flags & DMH_F_DEVICE) ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice));
+  return DMH_OK;
+}
+
 int dmh_moe_stack_forward(dmh_ctx* c, int first, int nl, float eps, const float* x, int T,
                           float* out, int32_t* ids, float* probs, unsigned flags, char* err,
                           size_t errlen) {
   if (!c || !x || !out || nl <= 0 || T <= 0)
     return set_err(err, errlen, DMH_ERR_INVALID_ARG, "dmh_moe_stack_forward: bad arguments");
-  if (eps != eps || eps <= 0.0f || eps > 3.0e38f)
-    return set_err(err, errlen, DMH_ERR_CONFIG,
-                   "{\"error_type\":\"CONFIG_ERROR\",\"detail\":\"rms_norm_eps must be finite"
-                   " and > 0\",\"stage\":\"config\"}");
+  int rc0 = eps_check(eps, err, errlen);
+  if (rc0) return rc0;
   Layer* L0 = get_layer(c, first);
   if (!L0)
     return set_err(err, errlen, DMH_ERR_INVALID_ARG, "dmh_moe_stack_forward: layer %d missing",
@@ -822,7 +943,8 @@ int dmh_moe_stack_forward(dmh_ctx* c, int first, int nl, float eps, const float*
     int32_t* dids = (own_ids ? c->ids.p : ids) + (size_t)i * TK;
     float* dprobs = (own_probs ? c->probs.p : probs) + (size_t)i * TK;
     float* dst = (direct && i == nl - 1) ? out : (src == hA ? hB : hA);
-    HIP_TRY(run_block(c, c->layers[l], l, src, src, T, dst, dids, dprobs, c->shg.p, true, eps));
+    const dm::NormSpec nm = layer_norm(c, c->layers[l], eps, (flags & DMH_F_NORM_TREE) != 0);
+    HIP_TRY(run_block(c, c->layers[l], l, src, src, T, dst, dids, dprobs, c->shg.p, true, &nm));
     c->last_ids[l] = dids;
     c->last_k[l] = K;
     src = dst;
@@ -1186,9 +1308,26 @@ int dmh_moe_aggregate(dmh_ctx* c, const float* residual, const float* routed, co
 // load_port_block_from_gguf's MoE tensors (src/layers/gguf_port_loader.mojo:
 // 207-256) -> one GGUF layer in HBM.  Lookup, read, type and length checks
 // run in the loader's order with its texts.
+static int upload_gguf_body(dmh_ctx* c, int layer, const dmh_moe_dims* d,
+                            const dmh_gguf_file* gf, int model_layer, unsigned flags, char* err,
+                            size_t errlen);
+
+// Host vectors grow with the file's payload: nothing may throw across the ABI.
 int dmh_upload_moe_layer_gguf(dmh_ctx* c, int layer, const dmh_moe_dims* d,
                               const dmh_gguf_file* gf, int model_layer, unsigned flags, char* err,
                               size_t errlen) {
+  try {
+    return upload_gguf_body(c, layer, d, gf, model_layer, flags, err, errlen);
+  } catch (const std::bad_alloc&) {
+    return set_err(err, errlen, DMH_ERR_NO_MEMORY, "dmh_upload_moe_layer_gguf: out of host memory");
+  } catch (const std::exception& ex) {
+    return set_err(err, errlen, DMH_ERR_NO_MEMORY, "dmh_upload_moe_layer_gguf: %s", ex.what());
+  }
+}
+
+static int upload_gguf_body(dmh_ctx* c, int layer, const dmh_moe_dims* d,
+                            const dmh_gguf_file* gf, int model_layer, unsigned flags, char* err,
+                            size_t errlen) {
   if (!c || !d || !gf)
     return set_err(err, errlen, DMH_ERR_INVALID_ARG, "dmh_upload_moe_layer_gguf: NULL argument");
   if (layer < 0 || layer >= kMaxLayers)

@@ -29,11 +29,11 @@ DecodeSync decode_sync_carve(const LayerDev& L, void* base);
 
 DecodePlan make_decode_plan(const LayerDev& L, int num_cus);
 hipError_t decode_occupancy(const LayerDev& L, const DecodePlan& P, int* blocks_per_cu);
-// norm_eps > 0: the router and experts see RMSNorm(x) (gamma = 1, the
-// layer-stack form: 256 strided partial sums of squares and a halving tree).
+// nm.eps > 0: the router and experts see rmsnorm(x, nm.gamma, nm.eps) in the
+// order nm.seq selects (NormSpec).
 hipError_t launch_moe_decode(const LayerDev& L, const DecodePlan& P, const float* x,
                              const float* residual, float* y, int32_t* ids, float* probs,
                              float* shg, const DecodeSync& S, unsigned long long* status, int token,
-                             hipStream_t st, float norm_eps = 0.0f);
+                             hipStream_t st, const NormSpec& nm);
 
 }  // namespace dm

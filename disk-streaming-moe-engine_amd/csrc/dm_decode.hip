@@ -571,12 +571,15 @@ __device__ __forceinline__ void finish_probs(int E, int K, SelState& st, bool re
 }
 
 // ---------------------------------------------------------------------------
-template <int GQW, int R>
+// NORM: 0 the block input is x; 1 / 2 it is rmsnorm(x, gamma, eps) with the
+// sum of squares as a 256-partial tree (1) or in element order (2, the
+// reference's order, src/layers/rmsnorm.mojo:41-44).
+template <int GQW, int R, int NORM>
 __global__ __launch_bounds__(kThreads) void k_moe_decode(
     LayerDev L, DecodePlan P, const float* __restrict__ x, const float* __restrict__ residual,
     float* __restrict__ y, int32_t* __restrict__ ids_out, float* __restrict__ probs_out,
     float* __restrict__ shg_out, DecodeSync S, unsigned long long* status, int token,
-    float norm_eps) {
+    NormSpec nm) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   float* xt = reinterpret_cast<float*>(smem + P.off_xt);
   uint4* xb2 = reinterpret_cast<uint4*>(smem + P.off_xb);
@@ -620,6 +623,15 @@ __global__ __launch_bounds__(kThreads) void k_moe_decode(
     xr[ii][0] = reinterpret_cast<const float4*>(x)[2 * i];
     xr[ii][1] = reinterpret_cast<const float4*>(x)[2 * i + 1];
   }
+  [[maybe_unused]] float4 gr[2][2];  // gamma of the same columns (the norm forms only)
+  if constexpr (NORM != 0) {
+#pragma unroll
+    for (int ii = 0; ii < 2; ++ii) {
+      const int i = min(tid + kThreads * ii, H / 8 - 1);
+      gr[ii][0] = reinterpret_cast<const float4*>(nm.gamma)[2 * i];
+      gr[ii][1] = reinterpret_cast<const float4*>(nm.gamma)[2 * i + 1];
+    }
+  }
   const size_t matS = (size_t)L.Ish * H;
   const ExpertView sgv = {L.sgu_nib, L.sgu_sc, L.Ish, H};
   const ExpertView suv = {L.sgu_nib + matS / 2, L.sgu_sc + matS / kGroup, L.Ish, H};
@@ -630,12 +642,14 @@ __global__ __launch_bounds__(kThreads) void k_moe_decode(
   uint4 dw[kDownBatch];
   uint2 ds[kDownBatch];
 
-  // ---- optional RMSNorm of x with gamma = 1 (the layer-stack form): 256
-  // strided partial sums of squares, a halving tree, denominator
-  // sqrt(sum / H + eps), x / denominator; every workgroup computes it, while
-  // the weight loads above are in flight.  The B-block area holds the squares
-  // and the reduction area the partials until the staging below.
-  if (norm_eps > 0.0f) {
+  // ---- optional RMSNorm of x (the port block's post-attention norm,
+  // src/layers/port_scheduler.mojo:383-385): every workgroup forms the sum of
+  // squares itself while the weight loads above are in flight, then
+  // x / denominator * gamma.  NORM 1: 256 strided partials and a halving tree;
+  // NORM 2: one lane adds the squares in element order (rmsnorm.mojo:41-44).
+  // The B-block area holds the squares and the reduction area the partials
+  // until the staging below.
+  if constexpr (NORM != 0) {
     float* sq = reinterpret_cast<float*>(xb2);
 #pragma unroll
     for (int ii = 0; ii < 2; ++ii) {
@@ -648,24 +662,46 @@ __global__ __launch_bounds__(kThreads) void k_moe_decode(
       }
     }
     __syncthreads();
-    if (tid < 256) {
-      float a = 0.0f;
-      for (int k = tid; k < H; k += 256) a = a + sq[k];
-      red[tid] = a;
-    }
+    if constexpr (NORM == 1) {
+      if (tid < 256) {
+        float a = 0.0f;
+        for (int k = tid; k < H; k += 256) a = a + sq[k];
+        red[tid] = a;
+      }
 #pragma unroll
-    for (int wd = 128; wd >= 1; wd >>= 1) {
-      __syncthreads();
-      if (tid < wd) red[tid] = red[tid] + red[tid + wd];
+      for (int wd = 128; wd >= 1; wd >>= 1) {
+        __syncthreads();
+        if (tid < wd) red[tid] = red[tid] + red[tid + wd];
+      }
+    } else {
+      if (tid == 0) {
+        const float4* s4 = reinterpret_cast<const float4*>(sq);
+        float a = 0.0f;
+        for (int k = 0; k < H / 4; k += 8) {  // H % 128 == 0; reads 8 ahead of the adds
+          float4 v[8];
+#pragma unroll
+          for (int u = 0; u < 8; ++u) v[u] = s4[k + u];
+#pragma unroll
+          for (int u = 0; u < 8; ++u) {
+            a = a + v[u].x;
+            a = a + v[u].y;
+            a = a + v[u].z;
+            a = a + v[u].w;
+          }
+        }
+        red[0] = a;
+      }
     }
     __syncthreads();
-    const float denom = __builtin_sqrtf(red[0] / (float)H + norm_eps);
+    const float denom = __builtin_sqrtf(red[0] / (float)H + nm.eps);
+    auto nrm = [&](float4 v, float4 g) {
+      return make_float4((v.x / denom) * g.x, (v.y / denom) * g.y, (v.z / denom) * g.z,
+                         (v.w / denom) * g.w);
+    };
 #pragma unroll
     for (int ii = 0; ii < 2; ++ii) {
-      xr[ii][0] = make_float4(xr[ii][0].x / denom, xr[ii][0].y / denom, xr[ii][0].z / denom,
-                              xr[ii][0].w / denom);
-      xr[ii][1] = make_float4(xr[ii][1].x / denom, xr[ii][1].y / denom, xr[ii][1].z / denom,
-                              xr[ii][1].w / denom);
+      xr[ii][0] = nrm(xr[ii][0], gr[ii][0]);
+      xr[ii][1] = nrm(xr[ii][1], gr[ii][1]);
     }
     __syncthreads();  // the squares and partials are overwritten below
   }
@@ -996,38 +1032,63 @@ DecodePlan make_decode_plan(const LayerDev& L, int num_cus) {
   return P;
 }
 
-template <int GQW>
+template <int GQW, int NORM>
 static const void* pick_r(int R) {
-  return R <= 1 ? (const void*)k_moe_decode<GQW, 1> : (const void*)k_moe_decode<GQW, 8>;
+  return R <= 1 ? (const void*)k_moe_decode<GQW, 1, NORM>
+                : (const void*)k_moe_decode<GQW, 8, NORM>;
 }
 
-static const void* pick_kernel(const LayerDev& L) {
+template <int NORM>
+static const void* pick_gqw(int gqw, int R) {
+  return gqw <= 2 ? pick_r<2, NORM>(R) : gqw <= 8 ? pick_r<8, NORM>(R) : nullptr;
+}
+
+static int norm_mode(const NormSpec& nm) { return nm.eps > 0.0f ? (nm.seq ? 2 : 1) : 0; }
+
+static const void* pick_kernel(const LayerDev& L, int norm) {
   const int gqw = (L.H / kQuadCols + kWaves - 1) / kWaves;
   const int R = (L.E + 255) / 256;
   const int ldh = 1 << ldh_log2_of(L);
   if (R > 8 || L.K > 32 || ldh < 2 || (L.K + 1) * (ldh / 2) > kHw * kThreads) return nullptr;
-  return gqw <= 2 ? pick_r<2>(R) : gqw <= 8 ? pick_r<8>(R) : nullptr;
+  return norm == 0 ? pick_gqw<0>(gqw, R) : norm == 1 ? pick_gqw<1>(gqw, R) : pick_gqw<2>(gqw, R);
 }
 
 hipError_t decode_occupancy(const LayerDev& L, const DecodePlan& P, int* blocks_per_cu) {
-  const void* fn = pick_kernel(L);
-  if (!fn) return hipErrorInvalidValue;
-  return hipOccupancyMaxActiveBlocksPerMultiprocessor(blocks_per_cu, fn, P.threads, P.lds_bytes);
+  // every norm form must fit: the launch picks one per call
+  int best = 1 << 30;
+  for (int norm = 0; norm < 3; ++norm) {
+    const void* fn = pick_kernel(L, norm);
+    if (!fn) return hipErrorInvalidValue;
+    int b = 0;
+    const hipError_t e =
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&b, fn, P.threads, P.lds_bytes);
+    if (e != hipSuccess) return e;
+    best = b < best ? b : best;
+  }
+  *blocks_per_cu = best;
+  return hipSuccess;
 }
 
 hipError_t launch_moe_decode(const LayerDev& L, const DecodePlan& P, const float* x,
                              const float* residual, float* y, int32_t* ids, float* probs,
                              float* shg, const DecodeSync& S, unsigned long long* status, int token,
-                             hipStream_t st, float norm_eps) {
-  const void* fn = pick_kernel(L);
+                             hipStream_t st, const NormSpec& nm) {
+  const int norm = norm_mode(nm);
+  if (norm != 0 && !nm.gamma) return hipErrorInvalidValue;
+  const void* fn = pick_kernel(L, norm);
   if (!fn) return hipErrorInvalidValue;
   LayerDev Lc = L;
   DecodePlan Pc = P;
   DecodeSync Sc = S;
+  NormSpec nc = nm;
   const float* xc = x;
   const float* rc = residual;
-  void* args[] = {&Lc, &Pc, &xc, &rc, &y, &ids, &probs, &shg, &Sc, &status, &token, &norm_eps};
-  return hipLaunchKernel(fn, dim3(P.grid), dim3(P.threads), args, P.lds_bytes, st);
+  void* args[] = {&Lc, &Pc, &xc, &rc, &y, &ids, &probs, &shg, &Sc, &status, &token, &nc};
+  // Every workgroup waits for words other workgroups publish, so all of them
+  // must be resident at once: a cooperative launch guarantees it or fails at
+  // launch (instead of leaving workgroups unscheduled behind other work and
+  // the waits running into their spin limit).
+  return hipLaunchCooperativeKernel(fn, dim3(P.grid), dim3(P.threads), args, P.lds_bytes, st);
 }
 
 }  // namespace dm

@@ -3,10 +3,13 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <new>
+#include <stdexcept>
 #include <string>
 #include <vector>
 
 #include "../../include/dismoen_hip.h"
+#include "dm_api_internal.h"
 #include "dm_formats.h"
 #include "dm_gguf.h"
 
@@ -42,6 +45,9 @@ void fill_info(const dm::FileTensor& t, dmh_tensor_info* info) {
   info->data_offset = t.data_offset;
   info->data_bytes = t.data_bytes;
 }
+
+int upload_files(dmh_ctx* ctx, int layer, const dmh_moe_dims* d, const dm::QuantFile& q,
+                 const dm::SafetensorsFile& s, int model_layer, char* err, size_t errlen);
 
 std::string not_in_quant(const std::string& name) {  // src/layers/quant_loader.mojo:33-40
   return "{\"error_type\":\"WEIGHT_LOAD_FAILED\",\"detail\":\"tensor not found in quant model\","
@@ -184,14 +190,32 @@ int dmh_st_read(const dmh_st_file* f, int idx, void* out, int64_t bytes, char* e
 int dmh_upload_moe_layer_files(dmh_ctx* ctx, int layer, const dmh_moe_dims* d,
                                const dmh_quant_file* qf, const dmh_st_file* sf, int model_layer,
                                char* err, size_t errlen) {
-  if (!ctx || !d || !qf || !sf)
+  if (!d || !qf || !sf)
     return put_err(err, errlen, DMH_ERR_INVALID_ARG, "dmh_upload_moe_layer_files: NULL argument");
-  const dm::QuantFile& q = qf->f;
-  const dm::SafetensorsFile& s = sf->f;
+  // the dims are checked before any size arithmetic (a zero or negative
+  // group size would divide by zero below) and nothing throws across the ABI
+  const int rc = dm::api_moe_dims_check(d, layer, err, errlen);
+  if (rc != DMH_OK) return rc;
+  if (!ctx)
+    return put_err(err, errlen, DMH_ERR_INVALID_ARG, "dmh_upload_moe_layer_files: NULL context");
+  try {
+    return upload_files(ctx, layer, d, qf->f, sf->f, model_layer, err, errlen);
+  } catch (const std::bad_alloc&) {
+    return put_err(err, errlen, DMH_ERR_NO_MEMORY, "dmh_upload_moe_layer_files: out of host memory");
+  } catch (const std::exception& ex) {
+    return put_err(err, errlen, DMH_ERR_NO_MEMORY,
+                   std::string("dmh_upload_moe_layer_files: ") + ex.what());
+  }
+}
+
+}  // extern "C"
+
+namespace {
+
+int upload_files(dmh_ctx* ctx, int layer, const dmh_moe_dims* d, const dm::QuantFile& q,
+                 const dm::SafetensorsFile& s, int model_layer, char* err, size_t errlen) {
   const int64_t H = d->hidden, E = d->num_experts, I = d->inter, Ish = d->inter_sh;
   const int G = d->group_size;
-  if (H <= 0 || E <= 0 || I <= 0 || Ish <= 0)
-    return put_err(err, errlen, DMH_ERR_CONFIG, "dmh_upload_moe_layer_files: bad dims");
   const std::string L = std::to_string(model_layer);
   // router gate (src/layers/router.mojo:234-247): language-model prefix first
   std::vector<uint16_t> router, shgate;
@@ -268,6 +292,10 @@ int dmh_upload_moe_layer_files(dmh_ctx* ctx, int layer, const dmh_moe_dims* d,
                        dp.data(),     sgus.data(),   sgup.data(), sds.data(), sdp.data()};
   return dmh_upload_moe_layer(ctx, layer, d, &w, 0, err, errlen);
 }
+
+}  // namespace
+
+extern "C" {
 
 int dmh_gguf_open(const char* path, dmh_gguf_file** out, char* err, size_t errlen) {
   if (!path || !out) return put_err(err, errlen, DMH_ERR_INVALID_ARG, "dmh_gguf_open: NULL argument");

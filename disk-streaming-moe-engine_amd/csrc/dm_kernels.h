@@ -8,10 +8,11 @@
 namespace dm {
 
 // ---- upload-time re-tiling and validation ----
-// nmat matrices [R][C] in the reference 4-bit layout -> A16.  Invalid scales
-// or reserved codes record (tensor << 34 | sub) into *vkey (atomicMin).
+// nmat matrices [R][C] in the reference 4-bit layout with source group size
+// gsrc (32, 64, 128 or 256) -> A16 with one scale per 32 columns.  Invalid
+// scales or reserved codes record (tensor << 34 | sub) into *vkey (atomicMin).
 hipError_t launch_repack_a16(const uint8_t* src_nib, const uint16_t* src_sc, uint8_t* dst_nib,
-                             uint16_t* dst_sc, int R, int C, int nmat, int tensor_base,
+                             uint16_t* dst_sc, int R, int C, int nmat, int tensor_base, int gsrc,
                              unsigned long long* vkey, hipStream_t st);
 // router [E][H] bf16 + shared gate [H] bf16 -> R16 (E+1 rows).  Non-finite
 // router weights set bit 0 of *flags.
@@ -55,7 +56,8 @@ hipError_t launch_check_ids(const int32_t* ids, int T, int K, int E, int32_t* ou
                             unsigned long long* status, hipStream_t st);
 
 // ---- glue ----
-hipError_t launch_rmsnorm_rows(const float* x, int T, int H, float eps, float* out,
-                               unsigned long long* status, int layer_tag, hipStream_t st);
+// rmsnorm of T rows [T][H] (H <= 8192) into out, in the order nm.seq selects.
+hipError_t launch_rmsnorm_rows(const float* x, int T, int H, const NormSpec& nm, float* out,
+                               hipStream_t st);
 
 }  // namespace dm

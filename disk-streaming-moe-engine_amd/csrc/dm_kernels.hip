@@ -17,14 +17,21 @@ namespace dm {
 // src/quant/dequant_kernel.mojo:68-108 (scale NaN/Inf, scale <= 0, code -8).
 // One thread per (matrix, tile, lane): reads 4 aligned words of the source
 // row (32 codes per word group), writes 16 bytes; q == 0 lanes move scales.
+// The source group size gsrc is any of {32, 64, 128, 256}: groups run over
+// the flattened row-major index (quant_format.md:117-161), every 32-column
+// chunk of a row lies inside one source group (row * C and the chunk start
+// are multiples of 32), and that group's scale is written for the chunk.
+// bf16(fp32(s) * q) depends on s and q only, so the tiles compute the same
+// values at every source group size.
 // Validation key: tensor << 34 | (2*group + kind) for scale errors
-// (kind 0 NaN/Inf, 1 non-positive), tensor << 34 | 1 << 33 for code -8.
+// (kind 0 NaN/Inf, 1 non-positive; group in the source numbering),
+// tensor << 34 | 1 << 33 for code -8.
 // ===========================================================================
 __global__ __launch_bounds__(256) void k_repack_a16(const uint8_t* __restrict__ src_nib,
                                                      const uint16_t* __restrict__ src_sc,
                                                      uint8_t* __restrict__ dst_nib,
                                                      uint16_t* __restrict__ dst_sc, int R, int C,
-                                                     int nmat, int tensor_base,
+                                                     int nmat, int tensor_base, int gsrc,
                                                      unsigned long long* vkey) {
   const int nRB = R / kTileRows, nGQ = C / kQuadCols;
   const int64_t per_mat = (int64_t)nRB * nGQ * 64;
@@ -40,7 +47,7 @@ __global__ __launch_bounds__(256) void k_repack_a16(const uint8_t* __restrict__ 
   const int row = rb * kTileRows + r;
   const size_t mat_nib = (size_t)R * C / 2, mat_sc = (size_t)R * C / kGroup;
   const uint8_t* sn = src_nib + (size_t)m * mat_nib;
-  const uint16_t* ss = src_sc + (size_t)m * mat_sc;
+  const uint16_t* ss = src_sc + (size_t)m * ((size_t)R * C / gsrc);
   uint32_t out[4];
   bool reserved = false;
 #pragma unroll
@@ -67,7 +74,8 @@ __global__ __launch_bounds__(256) void k_repack_a16(const uint8_t* __restrict__ 
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       const int g = gq * 4 + c;
-      const size_t gidx = (size_t)row * (C / kGroup) + g;  // group index inside the tensor
+      // source group index inside the tensor
+      const size_t gidx = ((size_t)row * C + (size_t)g * kGroup) / (size_t)gsrc;
       const uint16_t u = ss[gidx];
       sv[c] = u;
       uint64_t k2 = kNoError;
@@ -83,13 +91,14 @@ __global__ __launch_bounds__(256) void k_repack_a16(const uint8_t* __restrict__ 
 }
 
 hipError_t launch_repack_a16(const uint8_t* src_nib, const uint16_t* src_sc, uint8_t* dst_nib,
-                             uint16_t* dst_sc, int R, int C, int nmat, int tensor_base,
+                             uint16_t* dst_sc, int R, int C, int nmat, int tensor_base, int gsrc,
                              unsigned long long* vkey, hipStream_t st) {
+  if (gsrc != 32 && gsrc != 64 && gsrc != 128 && gsrc != 256) return hipErrorInvalidValue;
   const int64_t n = (int64_t)(R / kTileRows) * (C / kQuadCols) * 64 * nmat;
   if (n <= 0) return hipSuccess;
   const int64_t blocks = (n + 255) / 256;
   hipLaunchKernelGGL(k_repack_a16, dim3((unsigned)blocks), dim3(256), 0, st, src_nib, src_sc,
-                     dst_nib, dst_sc, R, C, nmat, tensor_base, vkey);
+                     dst_nib, dst_sc, R, C, nmat, tensor_base, gsrc, vkey);
   return hipGetLastError();
 }
 
@@ -264,7 +273,7 @@ __global__ __launch_bounds__(64) void k_router_lds(const float* __restrict__ x,
       const int k = (tid + 64 * j) * 4;
       if (k >= H) continue;
       const f32x4 q = v[r][j];
-      const bool bad = !finite_f(q.x) | !finite_f(q.y) | !finite_f(q.z) | !finite_f(q.w);
+      const bool bad = !finite_f(q.x) || !finite_f(q.y) || !finite_f(q.z) || !finite_f(q.w);
       if (r == 0) {
         bad_x |= bad;
         *reinterpret_cast<f32x4*>(&sx[k]) = q;
@@ -800,30 +809,59 @@ hipError_t launch_down_dec(const LayerDev& L, const float* h, int ldh, const int
 }
 
 // ===========================================================================
-// RMSNorm per token with gamma = 1 (src/layers/rmsnorm.mojo:41-48), used by
-// the layer-stack entry point.  The sum of squares is reduced as 256 strided
-// partials then a halving tree (a fixed order shared with the oracle's stack).
+// RMSNorm per token (src/layers/rmsnorm.mojo:41-48): out = x / denom *
+// gamma, denom = sqrt(sum(x * x) / H + eps), for the block-edge norm of
+// several tokens.  SEQ: the squares staged in LDS and added in element order
+// by one lane, the reference's order; otherwise 256 strided partials and a
+// halving tree (the order of the fused decode kernel's tree mode).
 // ===========================================================================
+template <bool SEQ>
 __global__ __launch_bounds__(256) void k_rmsnorm_rows(const float* __restrict__ x, int H,
-                                                       float eps, float* __restrict__ out) {
-  __shared__ float part[256];
+                                                       float eps, const float* __restrict__ gamma,
+                                                       float* __restrict__ out) {
+  __shared__ float part[SEQ ? kNormMaxH : 256];
   const int t = blockIdx.x;
   const float* xr = x + (size_t)t * H;
-  float acc = 0.0f;
-  for (int i = threadIdx.x; i < H; i += 256) acc = acc + xr[i] * xr[i];
-  part[threadIdx.x] = acc;
-  __syncthreads();
-  for (int wdt = 128; wdt >= 1; wdt >>= 1) {
-    if ((int)threadIdx.x < wdt) part[threadIdx.x] = part[threadIdx.x] + part[threadIdx.x + wdt];
+  if (SEQ) {
+    for (int i = threadIdx.x; i < H; i += 256) part[i] = xr[i] * xr[i];
     __syncthreads();
+    if (threadIdx.x == 0) {
+      float a = 0.0f;
+      int i = 0;
+      for (; i + 8 <= H; i += 8) {  // reads 8 ahead of the adds
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = part[i + u];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) a = a + v[u];
+      }
+      for (; i < H; ++i) a = a + part[i];
+      part[0] = a;
+    }
+    __syncthreads();
+  } else {
+    float acc = 0.0f;
+    for (int i = threadIdx.x; i < H; i += 256) acc = acc + xr[i] * xr[i];
+    part[threadIdx.x] = acc;
+    __syncthreads();
+    for (int wdt = 128; wdt >= 1; wdt >>= 1) {
+      if ((int)threadIdx.x < wdt) part[threadIdx.x] = part[threadIdx.x] + part[threadIdx.x + wdt];
+      __syncthreads();
+    }
   }
   const float denom = __builtin_sqrtf(part[0] / (float)H + eps);
-  for (int i = threadIdx.x; i < H; i += 256) out[(size_t)t * H + i] = xr[i] / denom;
+  for (int i = threadIdx.x; i < H; i += 256) out[(size_t)t * H + i] = (xr[i] / denom) * gamma[i];
 }
 
-hipError_t launch_rmsnorm_rows(const float* x, int T, int H, float eps, float* out,
-                               unsigned long long*, int, hipStream_t st) {
-  hipLaunchKernelGGL(k_rmsnorm_rows, dim3(T), dim3(256), 0, st, x, H, eps, out);
+hipError_t launch_rmsnorm_rows(const float* x, int T, int H, const NormSpec& nm, float* out,
+                               hipStream_t st) {
+  if (H <= 0 || H > kNormMaxH || !nm.gamma) return hipErrorInvalidValue;
+  if (nm.seq)
+    hipLaunchKernelGGL(k_rmsnorm_rows<true>, dim3(T), dim3(256), 0, st, x, H, nm.eps, nm.gamma,
+                       out);
+  else
+    hipLaunchKernelGGL(k_rmsnorm_rows<false>, dim3(T), dim3(256), 0, st, x, H, nm.eps, nm.gamma,
+                       out);
   return hipGetLastError();
 }
 

@@ -4,10 +4,12 @@
 // The caller hands weights over in the reference's 4-bit layout
 // (src/format/quant_reader.mojo:171-341): per tensor, fp16 group scales
 // [N/G] and packed bytes [N/2], element i in byte i/2 (low nibble = even i),
-// groups of G = 32 consecutive elements along the input dimension, codes
-// signed int4 in [-7, 7].  At upload each matrix is re-tiled once into the
-// "A16" layout below so that one 16-byte load per lane feeds four MFMA
-// k-steps and one 8-byte load carries the matching four fp16 scales.
+// groups of G in {32, 64, 128, 256} consecutive elements along the flattened
+// row-major index, codes signed int4 in [-7, 7].  At upload each matrix is
+// re-tiled once into the "A16" layout below, with one scale per 32 columns
+// (a source group's scale repeated over its 32-column chunks), so that one
+// 16-byte load per lane feeds four MFMA k-steps and one 8-byte load carries
+// the matching four fp16 scales.
 #pragma once
 #include <stddef.h>
 #include <stdint.h>
@@ -66,6 +68,17 @@ struct LayerDev {
   const uint16_t* sgu_sc;
   const uint8_t* sd_nib;    // shared expert: A16 down [H][Ish]
   const uint16_t* sd_sc;
+};
+
+// ---- RMSNorm at the block edge ---------------------------------------------
+// rmsnorm (src/layers/rmsnorm.mojo:10-48) of the block input:
+// out = x / sqrt(sum(x * x) / H + eps) * gamma, each step rounded as written.
+constexpr int kNormMaxH = 8192;  // largest H of the block-edge norm
+struct NormSpec {
+  float eps;           // > 0: the block sees the normalised input; 0: no norm
+  const float* gamma;  // [H] fp32 post_attention_layernorm gamma (ones when unset)
+  int seq;             // 1: the sum of squares in element order, as the reference
+                       // sums it; 0: 256 strided partials and a halving tree
 };
 
 // ---- first-error keys ------------------------------------------------------

@@ -13,6 +13,7 @@ LIB_PATH = os.path.join(PKG_ROOT, "libdismoen_hip.so")
 
 DMH_F_DEVICE = 0x1
 DMH_F_Q4K_PY_SCALES = 0x10
+DMH_F_NORM_TREE = 0x20
 
 ERROR_NAMES = {
     1: "INVALID_ARG", 2: "CONFIG", 3: "HIP", 4: "NO_MEMORY", 5: "DEQUANT", 6: "ACT",
@@ -32,6 +33,7 @@ EXPORTS = (
     "dmh_gguf_num_tensors", "dmh_gguf_find", "dmh_gguf_tensor_info", "dmh_gguf_metadata",
     "dmh_gguf_read", "dmh_dequant_gguf", "dmh_gguf_stream_tensor_f32",
     "dmh_upload_moe_layer_gguf", "dmh_free_layer_gguf", "dmh_moe_forward_gguf",
+    "dmh_set_layer_norm", "dmh_port_moe_forward",
 )
 
 
@@ -142,6 +144,9 @@ def lib():
                                             C.c_char_p, sz]
     L.dmh_free_layer_gguf.argtypes = [vp, i32]
     L.dmh_moe_forward_gguf.argtypes = [vp, i32, vp, vp, i32, vp, vp, vp, vp, u32, C.c_char_p, sz]
+    L.dmh_set_layer_norm.argtypes = [vp, i32, vp, i32, u32, C.c_char_p, sz]
+    L.dmh_port_moe_forward.argtypes = [vp, i32, vp, i32, C.c_float, vp, vp, vp, vp, u32,
+                                       C.c_char_p, sz]
     _lib = L
     return L
 

@@ -18,8 +18,8 @@ from dataclasses import dataclass, field
 
 import numpy as np
 
-from ._lib import (DMH_F_DEVICE, DMH_F_Q4K_PY_SCALES, DismoenError, DmhDims, DmhWeights, check,
-                   errbuf, lib)
+from ._lib import (DMH_F_DEVICE, DMH_F_NORM_TREE, DMH_F_Q4K_PY_SCALES, DismoenError, DmhDims,
+                   DmhWeights, check, errbuf, lib)
 
 
 @dataclass
@@ -136,10 +136,11 @@ class MoEBlock:
                                              len(e)), e)
         self.dims[layer_idx] = (L.hidden, L.num_experts, L.top_k, L.inter, L.inter_sh)
 
-    def upload_layer_device(self, layer_idx: int, dims: tuple, ptrs: dict) -> None:
+    def upload_layer_device(self, layer_idx: int, dims: tuple, ptrs: dict,
+                            group_size: int = 32) -> None:
         """Upload from device buffers (ptrs: field name -> device address)."""
         H, E, K, I, Ish = dims
-        d = DmhDims(H, E, K, I, Ish, 32, 0)
+        d = DmhDims(H, E, K, I, Ish, group_size, 0)
         w = DmhWeights(**ptrs)
         e = errbuf()
         check(self._lib.dmh_upload_moe_layer(self._h, layer_idx, C.byref(d), C.byref(w),
@@ -147,11 +148,12 @@ class MoEBlock:
         self.dims[layer_idx] = dims
 
     def upload_layer_files(self, layer_idx: int, dims: tuple, quant, shard,
-                           model_layer: int = 0) -> None:
+                           model_layer: int = 0, group_size: int = 32) -> None:
         """Upload model layer model_layer from a quant model and a safetensors
-        shard (dismoen.formats.QuantModelIndex / SafetensorsShard)."""
+        shard (dismoen.formats.QuantModelIndex / SafetensorsShard); group_size is
+        the group size of the quant model's expert tensors (32, 64, 128 or 256)."""
         H, E, K, I, Ish = dims
-        d = DmhDims(H, E, K, I, Ish, 32, 0)
+        d = DmhDims(H, E, K, I, Ish, group_size, 0)
         e = errbuf()
         check(self._lib.dmh_upload_moe_layer_files(self._h, layer_idx, C.byref(d), quant.handle,
                                                    shard.handle, model_layer, e, len(e)), e)
@@ -254,8 +256,45 @@ class MoEBlock:
         check(self._lib.dmh_moe_forward(self._h, layer_idx, x_ptr, residual_ptr, seq_len, y_ptr,
                                         ids_ptr, probs_ptr, shg_ptr, DMH_F_DEVICE, e, len(e)), e)
 
+    # -- the port block's MoE section with its RMSNorm ----------------------
+    def set_layer_norm(self, layer_idx: int, gamma) -> None:
+        """post_attention_layernorm_gamma of layer layer_idx (None: gamma = 1)."""
+        H = self.dims[layer_idx][0]
+        g = None if gamma is None else _f32(gamma).reshape(-1)
+        e = errbuf()
+        check(self._lib.dmh_set_layer_norm(self._h, layer_idx, _ptr(g),
+                                           H if g is None else g.size, 0, e, len(e)), e)
+
+    def forward_port_moe_norm(self, x_mid, layer_idx: int, seq_len: int, eps: float = 1e-6,
+                              tree: bool = False):
+        """MoE section of forward_port_block including its RMSNorm
+        (port_scheduler.mojo:381-482): (y = x_mid + MoE(rmsnorm(x_mid)), ids,
+        probs, shared gate) as numpy arrays."""
+        H, E, K, I, Ish = self.dims[layer_idx]
+        x = _f32(x_mid).reshape(-1)
+        y = np.empty(seq_len * H, np.float32)
+        ids = np.empty(seq_len * K, np.int32)
+        probs = np.empty(seq_len * K, np.float32)
+        shg = np.empty(seq_len, np.float32)
+        e = errbuf()
+        check(self._lib.dmh_port_moe_forward(self._h, layer_idx, x.ctypes.data, seq_len, eps,
+                                             y.ctypes.data, ids.ctypes.data, probs.ctypes.data,
+                                             shg.ctypes.data, DMH_F_NORM_TREE if tree else 0, e,
+                                             len(e)), e)
+        return (y.reshape(seq_len, H), ids.reshape(seq_len, K), probs.reshape(seq_len, K), shg)
+
+    def forward_port_moe_norm_device(self, layer_idx: int, x_ptr: int, seq_len: int, y_ptr: int,
+                                     eps: float = 1e-6, ids_ptr=None, probs_ptr=None,
+                                     shg_ptr=None, tree: bool = False) -> None:
+        e = errbuf()
+        fl = DMH_F_DEVICE | (DMH_F_NORM_TREE if tree else 0)
+        check(self._lib.dmh_port_moe_forward(self._h, layer_idx, x_ptr, seq_len, eps, y_ptr,
+                                             ids_ptr, probs_ptr, shg_ptr, fl, e, len(e)), e)
+
     def forward_stack(self, x, first_layer: int, num_layers: int, seq_len: int,
-                      eps: float = 1e-6):
+                      eps: float = 1e-6, tree: bool = False):
+        """num_layers port MoE sections in sequence (identity mixers); tree=True
+        sums the norm's squares in the fast tree order."""
         H, E, K, I, Ish = self.dims[first_layer]
         x = _f32(x).reshape(-1)
         out = np.empty(seq_len * H, np.float32)
@@ -264,16 +303,19 @@ class MoEBlock:
         e = errbuf()
         check(self._lib.dmh_moe_stack_forward(self._h, first_layer, num_layers, eps,
                                               x.ctypes.data, seq_len, out.ctypes.data,
-                                              ids.ctypes.data, probs.ctypes.data, 0, e, len(e)),
+                                              ids.ctypes.data, probs.ctypes.data,
+                                              DMH_F_NORM_TREE if tree else 0, e, len(e)),
               e)
         return (out.reshape(seq_len, H), ids.reshape(num_layers, seq_len, K),
                 probs.reshape(num_layers, seq_len, K))
 
     def forward_stack_device(self, x_ptr: int, first_layer: int, num_layers: int, seq_len: int,
-                             out_ptr: int, eps: float = 1e-6, ids_ptr=None, probs_ptr=None):
+                             out_ptr: int, eps: float = 1e-6, ids_ptr=None, probs_ptr=None,
+                             tree: bool = False):
         e = errbuf()
+        fl = DMH_F_DEVICE | (DMH_F_NORM_TREE if tree else 0)
         check(self._lib.dmh_moe_stack_forward(self._h, first_layer, num_layers, eps, x_ptr,
-                                              seq_len, out_ptr, ids_ptr, probs_ptr, DMH_F_DEVICE,
+                                              seq_len, out_ptr, ids_ptr, probs_ptr, fl,
                                               e, len(e)), e)
 
     # -- unit entry points ---------------------------------------------

@@ -48,12 +48,18 @@ enum {
 };
 
 #define DMH_F_DEVICE 0x1u   /* pointers are device memory; stream-ordered, no sync */
+/* Block-edge RMSNorm in the library's fast order: the sum of squares as 256
+ * strided partials and a halving tree.  Without it the squares are added in
+ * element order, as rmsnorm does (src/layers/rmsnorm.mojo:41-44). */
+#define DMH_F_NORM_TREE 0x20u
 
 typedef struct dmh_ctx dmh_ctx;
 
 /* Fields of ModelConfig that the block uses (src/core/config.mojo:11-174,
- * src/layers/router_types.mojo:9-44).  group_size must be 32; hidden, inter
- * and inter_sh must be multiples of 128; norm_topk_prob must be 0. */
+ * src/layers/router_types.mojo:9-44).  group_size is one of the quantizer's
+ * sizes {32, 64, 128, 256} (src/format/half_float.mojo:9,24-31; the format's
+ * default is 128); hidden, inter and inter_sh must be multiples of 128;
+ * norm_topk_prob must be 0. */
 typedef struct {
   int32_t hidden;          /* H */
   int32_t num_experts;     /* E */
@@ -97,7 +103,12 @@ int dmh_create(int device, dmh_ctx** out, char* err, size_t errlen);
 int dmh_destroy(dmh_ctx* ctx);
 
 /* Use another HIP stream (a hipStream_t) for subsequent calls; NULL restores
- * the context's own stream. */
+ * the context's own stream.  Work already queued on the previous stream is
+ * ordered before anything issued on the new one.  Calls made while the
+ * stream is being captured into a HIP graph take the multi-kernel path (the
+ * single-launch decode kernel tags its hand-offs per launch on the host, so
+ * a replayed capture would repeat a tag); buffers a call allocates on first
+ * use must be allocated by an uncaptured call first. */
 int dmh_set_stream(dmh_ctx* ctx, void* hip_stream);
 void* dmh_get_stream(dmh_ctx* ctx);
 
@@ -138,10 +149,30 @@ int dmh_moe_forward(dmh_ctx* ctx, int layer, const float* x, const float* residu
                     int seq_len, float* y, int32_t* ids, float* probs,
                     float* shared_gate, unsigned flags, char* err, size_t errlen);
 
+/* The post-attention RMSNorm weight of an uploaded layer: gamma [hidden] fp32
+ * (PortBlockWeights.post_attention_layernorm_gamma,
+ * src/layers/port_scheduler.mojo:65-86, used at :383-385), copied to the
+ * device; NULL restores gamma = 1.  hidden must equal the layer's (else the
+ * NORM_ERROR "length mismatch" of rmsnorm.mojo:31-35).  flags & DMH_F_DEVICE:
+ * gamma is device memory. */
+int dmh_set_layer_norm(dmh_ctx* ctx, int layer, const float* gamma, int hidden,
+                       unsigned flags, char* err, size_t errlen);
+
+/* The MoE section of forward_port_block (src/layers/port_scheduler.mojo:
+ * 381-482) with its RMSNorm: xn = rmsnorm(x_mid, gamma, eps)
+ * (apply_rmsnorm_sequence, :383-385, gamma the layer's), y = MoE(xn) +
+ * x_mid.  Outputs as dmh_moe_forward.  eps NaN/Inf/<= 0 gives rmsnorm's
+ * CONFIG_ERROR.  flags: DMH_F_DEVICE, DMH_F_NORM_TREE. */
+int dmh_port_moe_forward(dmh_ctx* ctx, int layer, const float* x_mid, int seq_len, float eps,
+                         float* y, int32_t* ids, float* probs, float* shared_gate,
+                         unsigned flags, char* err, size_t errlen);
+
 /* num_layers consecutive uploaded layers, token mixer replaced by identity:
- * per layer h <- moe_aggregate_forward(h, MoE(RMSNorm_{gamma=1,eps}(h))), the
- * composition of src/layers/port_scheduler.mojo:381-482.  ids/probs
- * [num_layers][seq_len][K] may be NULL. */
+ * per layer h <- dmh_port_moe_forward(h), i.e. h + MoE(rmsnorm(h, gamma_l,
+ * eps)), the composition of src/layers/port_scheduler.mojo:381-482 with
+ * gamma_l each layer's (dmh_set_layer_norm).  ids/probs
+ * [num_layers][seq_len][K] may be NULL.  flags: DMH_F_DEVICE,
+ * DMH_F_NORM_TREE. */
 int dmh_moe_stack_forward(dmh_ctx* ctx, int first_layer, int num_layers, float eps,
                           const float* x, int seq_len, float* out, int32_t* ids,
                           float* probs, unsigned flags, char* err, size_t errlen);

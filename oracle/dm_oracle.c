@@ -717,13 +717,14 @@ int or_rmsnorm(const float* x, const float* gamma, int n, float eps, float* out,
   return 0;
 }
 
-/* The RMSNorm of the layer-stack composition (gamma = 1): the arithmetic of
- * src/layers/rmsnorm.mojo:41-48 except that the sum of squares is reduced as
- * 256 strided partials (partial i sums x[i], x[i+256], ... in order) and a
- * halving tree, the order the GPU stack kernel uses.  The reference sums
- * sequentially; the two agree to a few ulp (tests/test_oracle_moe.py). */
-int or_rmsnorm_tree256(const float* x, int n, float eps, float* out, char* err,
-                       size_t errlen) {
+/* The fast-mode RMSNorm of the library: the arithmetic of
+ * src/layers/rmsnorm.mojo:41-48 (x / denom * gamma, gamma NULL = 1) except
+ * that the sum of squares is reduced as 256 strided partials (partial i sums
+ * x[i], x[i+256], ... in order) and a halving tree, the order of the GPU's
+ * tree mode.  The reference sums sequentially (or_rmsnorm); the two agree to
+ * a few ulp (tests/test_oracle_moe.py). */
+int or_rmsnorm_tree256(const float* x, const float* gamma, int n, float eps, float* out,
+                       char* err, size_t errlen) {
   if (n <= 0)
     return seterr(err, errlen,
                   "{\"error_type\":\"NORM_ERROR\",\"detail\":\"empty input\",\"stage\":\"rmsnorm\"}");
@@ -743,7 +744,10 @@ int or_rmsnorm_tree256(const float* x, int n, float eps, float* out, char* err,
   for (int w = 128; w >= 1; w >>= 1)
     for (int i = 0; i < w; ++i) part[i] = part[i] + part[i + w];
   float denom = sqrtf(part[0] / (float)n + eps);
-  for (int i = 0; i < n; ++i) out[i] = x[i] / denom;
+  for (int i = 0; i < n; ++i) {
+    float q = x[i] / denom;
+    out[i] = q * (gamma ? gamma[i] : 1.0f);
+  }
   return 0;
 }
 
@@ -987,8 +991,10 @@ int or_moe_layer_q4(const or_layer_q4* L, const or_layer_cache* cache,
   int H = L->hidden, E = L->num_experts, K = L->top_k, I = L->inter, Ish = L->inter_sh;
   int st = 0;
   if (or_router_config_validate(E, K, 0, err, errlen)) return 1;
+  /* each tensor is dequantized as one flat array (quant_loader.mojo:27-41,
+   * dequant_kernel.mojo:40-46): N % G == 0, a group may span two rows */
   if (T <= 0 || H <= 0 || I <= 0 || Ish <= 0 || !or_is_allowed_group_size(L->group_size) ||
-      H % L->group_size || I % L->group_size || Ish % L->group_size)
+      ((int64_t)I * H) % L->group_size || ((int64_t)Ish * H) % L->group_size)
     return seterr(err, errlen,
                   "{\"error_type\":\"CONFIG_ERROR\",\"detail\":\"invalid MoE layer"
                   " dimensions\",\"stage\":\"moe\",\"layer\":%d}", layer);
@@ -1077,10 +1083,13 @@ done:
 
 /* Stack of MoE blocks with the token mixer replaced by identity: the MoE
  * section of forward_port_block (src/layers/port_scheduler.mojo:381-482):
- * x_norm = RMSNorm(h) with gamma = 1 (or_rmsnorm_tree256);
- * h <- moe_aggregate_forward(h, ...). */
-int or_moe_stack_q4(const or_layer_q4* layers, int nl, or_pool* pool,
-                    const float* x, int T, float eps, float* out, int32_t* ids,
+ * x_norm = rmsnorm(h, gamma_l, eps) (apply_rmsnorm_sequence, :383-385;
+ * gammas[l] NULL or gammas NULL: gamma = 1), then
+ * h <- moe_aggregate_forward(h, MoE(x_norm)) (:469-479).  tree != 0 reduces
+ * the sum of squares in the library's fast-mode order (or_rmsnorm_tree256)
+ * instead of the reference's sequential order (or_rmsnorm). */
+int or_moe_stack_q4(const or_layer_q4* layers, int nl, const float* const* gammas, int tree,
+                    or_pool* pool, const float* x, int T, float eps, float* out, int32_t* ids,
                     float* probs, char* err, size_t errlen) {
   int H = layers[0].hidden;
   int64_t TH = (int64_t)T * H;
@@ -1091,8 +1100,11 @@ int or_moe_stack_q4(const or_layer_q4* layers, int nl, or_pool* pool,
   if (!st) memcpy(h, x, sizeof(float) * (size_t)TH);
   for (int l = 0; l < nl && !st; ++l) {
     int K = layers[l].top_k;
+    const float* g = gammas ? gammas[l] : NULL;
     for (int t = 0; t < T && !st; ++t)
-      st = or_rmsnorm_tree256(h + (int64_t)t * H, H, eps, xn + (int64_t)t * H, err, errlen);
+      st = tree ? or_rmsnorm_tree256(h + (int64_t)t * H, g, H, eps, xn + (int64_t)t * H, err,
+                                     errlen)
+                : or_rmsnorm(h + (int64_t)t * H, g, H, eps, xn + (int64_t)t * H, err, errlen);
     if (!st)
       st = or_moe_layer_q4(&layers[l], NULL, pool, xn, h, T, l, nh,
                            ids ? ids + (int64_t)l * T * K : NULL,

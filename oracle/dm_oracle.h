@@ -101,7 +101,7 @@ int or_moe_aggregate(const float* residual, const float* routed,
 /* ---- glue (src/layers/rmsnorm.mojo, residual.mojo) ---- */
 int or_rmsnorm(const float* x, const float* gamma, int n, float eps, float* out,
                char* err, size_t errlen);
-int or_rmsnorm_tree256(const float* x, int n, float eps, float* out, char* err,
+int or_rmsnorm_tree256(const float* x, const float* gamma, int n, float eps, float* out, char* err,
                        size_t errlen);
 int or_add_residual(const float* y, const float* x, int64_t n, int layer,
                     float* out, char* err, size_t errlen);
@@ -151,8 +151,11 @@ int or_moe_layer_q4(const or_layer_q4* L, const or_layer_cache* cache,
                     int seq_len, int layer, float* y, int32_t* ids,
                     float* probs, float* shgate, char* err, size_t errlen);
 
-/* 40-layer style stack: h <- h + MoE_l(RMSNorm_{gamma=1,eps}(h)). */
-int or_moe_stack_q4(const or_layer_q4* layers, int num_layers, or_pool* pool,
+/* 40-layer style stack: h <- h + MoE_l(RMSNorm_{gamma_l,eps}(h)), the norm
+ * in the reference's sequential order, or the tree order when tree != 0.
+ * gammas: [num_layers] pointers to [H] (NULL entries or NULL: gamma = 1). */
+int or_moe_stack_q4(const or_layer_q4* layers, int num_layers,
+                    const float* const* gammas, int tree, or_pool* pool,
                     const float* x, int seq_len, float eps, float* out,
                     int32_t* ids, float* probs, char* err, size_t errlen);
 

@@ -90,8 +90,11 @@ def lib():
         L.or_moe_layer_q4.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, F32P, C.c_void_p,
                                       C.c_int, C.c_int, F32P, I32P, F32P, F32P, C.c_char_p,
                                       C.c_size_t]
-        L.or_moe_stack_q4.argtypes = [C.c_void_p, C.c_int, C.c_void_p, F32P, C.c_int,
-                                      C.c_float, F32P, I32P, F32P, C.c_char_p, C.c_size_t]
+        L.or_rmsnorm_tree256.argtypes = [F32P, C.c_void_p, C.c_int, C.c_float, F32P,
+                                         C.c_char_p, C.c_size_t]
+        L.or_moe_stack_q4.argtypes = [C.c_void_p, C.c_int, C.c_void_p, C.c_int, C.c_void_p,
+                                      F32P, C.c_int, C.c_float, F32P, I32P, F32P, C.c_char_p,
+                                      C.c_size_t]
         _lib = L
     return _lib
 
@@ -251,13 +254,16 @@ def moe_aggregate(residual, routed, probs, shared_out, gates, seq_len, hidden, t
     return out[: seq_len * hidden]
 
 
-def rmsnorm(x, gamma, eps):
+def rmsnorm(x, gamma, eps, tree: bool = False):
+    """rmsnorm (src/layers/rmsnorm.mojo:10-48); tree=True: the sum of squares
+    in the library's fast-mode order (256 strided partials, halving tree)."""
     x = _f32(x)
     gm = None if gamma is None else _f32(gamma)
     out = np.zeros(max(x.size, 1), np.float32)
     e = _errbuf()
     gp = None if gm is None else gm.ctypes.data_as(C.c_void_p)
-    _check(lib().or_rmsnorm(x, gp, x.size, eps, out, e, 1024), e)
+    fn = lib().or_rmsnorm_tree256 if tree else lib().or_rmsnorm
+    _check(fn(x, gp, x.size, eps, out, e, 1024), e)
     return out[: x.size]
 
 
@@ -370,16 +376,27 @@ def moe_layer_q4(L, x, seq_len, residual=None, pool: Pool | None = None,
     return y.reshape(seq_len, H), ids.reshape(seq_len, K), probs.reshape(seq_len, K), shg
 
 
-def moe_stack_q4(layers, x, seq_len, eps=1e-6, pool: Pool | None = None):
+def moe_stack_q4(layers, x, seq_len, eps=1e-6, pool: Pool | None = None, gammas=None,
+                 tree: bool = False):
+    """The port block's MoE section stacked with identity mixers: per layer
+    h <- h + MoE_l(rmsnorm(h, gamma_l, eps)); gammas: per-layer [H] arrays (or
+    None entries: gamma = 1); tree=True: the fast-mode norm order."""
     arr = (_LayerQ4 * len(layers))(*[_layer_struct(L) for L in layers])
     x = _f32(x)
     H, K = layers[0].hidden, layers[0].top_k
     out = np.zeros(seq_len * H, np.float32)
     ids = np.zeros(len(layers) * seq_len * K, np.int32)
     probs = np.zeros(len(layers) * seq_len * K, np.float32)
+    gkeep = None
+    gp = None
+    if gammas is not None:
+        gkeep = [None if g is None else _f32(g) for g in gammas]
+        gp = (C.c_void_p * len(layers))(*[None if g is None else g.ctypes.data for g in gkeep])
     e = _errbuf()
     _check(lib().or_moe_stack_q4(C.cast(arr, C.c_void_p), len(layers),
+                                 None if gp is None else C.cast(gp, C.c_void_p), int(tree),
                                  pool.h if pool else None, x, seq_len, eps, out, ids, probs,
                                  e, 1024), e)
+    del gkeep
     return (out.reshape(seq_len, H), ids.reshape(len(layers), seq_len, K),
             probs.reshape(len(layers), seq_len, K))

@@ -211,3 +211,24 @@ def test_written_layer_reads_back(tmp_path):
         assert np.array_equal(pk, L.gu_packed.reshape(E, 2, -1)[5, 1])
         r = s.read(s.find("model.layers.3.mlp.gate.weight"))
         assert np.array_equal(np.frombuffer(r, "<u2"), L.router_bf16)
+
+
+@pytest.mark.parametrize("G", [0, -1, 48])
+def test_file_upload_rejects_group_size_before_reading(tmp_path, G):
+    """dmh_upload_moe_layer_files checks the dims (group size in {32, 64,
+    128, 256}) before any arithmetic or allocation on them: a zero or
+    negative group size is a CONFIG_ERROR, not a division by zero, and no
+    device is needed to reach the check."""
+    import ctypes as C
+    from dismoen._lib import DmhDims, lib
+    c = synth.CONFIG_TOY
+    L = synth.make_layer(**c, seed=70)
+    qp, sp = str(tmp_path / "m.quant"), str(tmp_path / "m.safetensors")
+    formats.write_layer_files(qp, sp, L, model_layer=0)
+    d = DmhDims(c["hidden"], c["num_experts"], c["top_k"], c["inter"], c["inter_sh"], G, 0)
+    e = C.create_string_buffer(1024)
+    with formats.scan_quant_file(qp) as q, formats.read_header(sp) as s:
+        rc = lib().dmh_upload_moe_layer_files(None, 0, C.byref(d), q.handle, s.handle, 0, e,
+                                              len(e))
+    assert rc == 2, e.value
+    assert b'"error_type":"CONFIG_ERROR"' in e.value and b"G=%d" % G in e.value

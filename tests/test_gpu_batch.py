@@ -155,3 +155,48 @@ def test_many_tokens_toy_layer_vs_oracle(block, oracle):
     x = synth.make_activations(np.random.default_rng(312), (70, 256))
     _check(block, oracle, L, 7, x)
     _check(block, oracle, L, 7, x, residual=x)
+
+
+def test_prefill_2048_zipf_skew_vs_oracle(block, oracle):
+    """The Zipf(1.1)-skewed 2048-token prefill: a router bias folded into
+    router column 0 with activation feature 0 = 1.0 (synth.with_router_bias),
+    so hot experts get hundreds of tokens and their full 128-token units run.
+    Every token's ids and probabilities are compared with the oracle's
+    router_forward (topk.mojo:79-96, lowest id on ties); outputs on a sample
+    holding tokens of the hottest expert and of experts with 1-5 tokens."""
+    E, H, K, T = 256, 2048, 8, 2048
+    L = synth.with_router_bias(synth.make_layer(**synth.CONFIG_QWEN36, seed=13),
+                               synth.zipf_router_bias(E, 1.1, seed=7))
+    block.upload_layer(8, L)
+    x = synth.bias_feature(synth.make_activations(np.random.default_rng(320), (T, H)))
+    y, ids, probs, shg = block.forward_arrays(8, x, T)
+    counts = np.bincount(ids.reshape(-1), minlength=E)
+    hot = int(np.argmax(counts))
+    # the routed full-unit path of the grouped kernels (more than one
+    # 128-token unit for a routed expert) is exercised
+    assert counts[hot] > 128, counts[hot]
+    w = synth.bf16_bits_to_f32(L.router_bf16).reshape(E, H)
+    ido, po = oracle.router_forward(x, w, T, H, E, K)
+    assert np.array_equal(ids, ido)
+    assert np.array_equal(probs.view(np.uint32), po.view(np.uint32))
+    rng = np.random.default_rng(321)
+    hot_tokens = np.nonzero((ids == hot).any(axis=1))[0]
+    sample = list(rng.choice(hot_tokens, 8, replace=False))
+    cold = [e for e in range(E) if 1 <= counts[e] <= 5]
+    assert cold, "no expert with 1-5 tokens"
+    for e in cold[:16]:
+        t = int(np.nonzero((ids == e).any(axis=1))[0][0])
+        if t not in sample:
+            sample.append(t)
+    sample = np.array(sample)
+    pool = oracle.Pool(8)
+    try:
+        yo, ido2, po2, so = oracle.moe_layer_q4(L, x[sample], len(sample), pool=pool)
+    finally:
+        pool.close()
+    assert np.array_equal(ids[sample], ido2)
+    assert np.array_equal(shg[sample].view(np.uint32), so.view(np.uint32))
+    for i, t in enumerate(sample):
+        err, rms, ok = tol_check(y[t], yo[i])
+        assert ok, (int(t), err, rms)
+    block.free_layer(8)

@@ -172,15 +172,71 @@ def test_rmsnorm_and_residual(oracle):
 
 
 def test_stack_composition(oracle):
+    """The oracle's stack is the chain of port MoE sections: per layer
+    xn = rmsnorm(h, gamma_l, eps), h <- h + MoE_l(xn), with ids and
+    probabilities of every layer and the output equal bit for bit, in both
+    norm orders."""
+    rng = np.random.default_rng(5)
     layers = [synth.make_layer(**synth.CONFIG_TOY, seed=10 + l) for l in range(3)]
-    x = synth.make_activations(np.random.default_rng(5), (2, 256))
-    out, ids, probs = oracle.moe_stack_q4(layers, x, 2, 1e-6)
-    h = x.copy()
-    for l, L in enumerate(layers):
-        xn = np.stack([oracle.rmsnorm(h[t], None, 1e-6) for t in range(2)])
-        y, lid, _, _ = oracle.moe_layer_q4(L, xn, 2, residual=h)
-        if np.array_equal(lid, ids[l]):
-            pass
-        h = y
-    # tree-ordered glue RMSNorm vs the sequential one: a few ulp apart
-    assert np.max(np.abs(out - h)) <= 1e-4 * np.sqrt(np.mean(h ** 2))
+    gammas = [(1.0 + 0.25 * rng.standard_normal(256)).astype(np.float32) for _ in layers]
+    gammas[1] = None  # gamma = 1
+    x = synth.make_activations(rng, (2, 256))
+    outs = {}
+    for tree in (False, True):
+        out, ids, probs = oracle.moe_stack_q4(layers, x, 2, 1e-6, gammas=gammas, tree=tree)
+        h = x.copy()
+        for l, L in enumerate(layers):
+            xn = np.stack([oracle.rmsnorm(h[t], gammas[l], 1e-6, tree=tree) for t in range(2)])
+            y, lid, lp, _ = oracle.moe_layer_q4(L, xn, 2, residual=h)
+            assert np.array_equal(lid, ids[l]), (tree, l)
+            assert np.array_equal(lp.view(np.uint32), probs[l].view(np.uint32)), (tree, l)
+            h = y
+        assert np.array_equal(out.view(np.uint32), h.view(np.uint32))
+        outs[tree] = out
+    # the two norm orders agree within a few ulp, so the stacks within the bar
+    rms = np.sqrt(np.mean((outs[False] - x).astype(np.float64) ** 2))
+    assert np.max(np.abs(outs[True] - outs[False])) <= 1e-4 * rms
+
+
+def test_rmsnorm_with_gamma_closed_form(oracle):
+    """rmsnorm(x, gamma, eps) against float64 for both orders; and with
+    integer x (every partial sum of squares exact in fp32, so both orders give
+    the same sum S) bit-exactly against out = (x / denom) * gamma with
+    denom = sqrt(S / n + eps), each step one correctly rounded fp32 operation
+    (src/layers/rmsnorm.mojo:44-47)."""
+    rng = np.random.default_rng(11)
+    for n in (256, 2048, 4096):
+        x = (rng.standard_normal(n) * 3).astype(np.float32)
+        g = (1 + 0.5 * rng.standard_normal(n)).astype(np.float32)
+        ref = x / np.sqrt(np.mean(x.astype(np.float64) ** 2) + 1e-6) * g
+        for tree in (False, True):
+            a = oracle.rmsnorm(x, g, 1e-6, tree=tree)
+            assert np.max(np.abs(a - ref)) <= 1e-5 * np.max(np.abs(ref))
+        xi = rng.integers(-20, 21, n).astype(np.float32)
+        S = np.float32(np.sum(xi.astype(np.int64) ** 2))
+        eps = np.float32(1e-5)
+        denom = np.sqrt(np.float32(S / np.float32(n)) + eps, dtype=np.float32)
+        want = (xi / denom) * g
+        for tree in (False, True):
+            assert np.array_equal(oracle.rmsnorm(xi, g, float(eps), tree=tree), want)
+
+
+def test_rmsnorm_order_closed_form(oracle):
+    """The two summation orders differ where fp32 rounding tells them apart:
+    x[0]^2 = 2^24 and every other square 1.  Added in element order each 1
+    is lost (2^24 + 1 rounds to 2^24, ties to even), so the sum stays 2^24
+    and denom = sqrt(2^24 / n + eps); the tree adds the ones among
+    themselves first and keeps them."""
+    for n in (256, 2048):
+        x = np.ones(n, np.float32)
+        x[0] = 4096.0
+        eps = np.float32(1e-6)
+        denom = np.sqrt(np.float32(np.float32(2.0 ** 24) / np.float32(n)) + eps, dtype=np.float32)
+        seq = oracle.rmsnorm(x, None, float(eps))
+        assert np.array_equal(seq, x / denom)
+        tree = oracle.rmsnorm(x, None, float(eps), tree=True)
+        assert not np.array_equal(tree, seq)
+        # the tree keeps the ones: its sum is 2^24 + n - 1 within one ulp (2)
+        dt = np.float32(x[1] / tree[1])
+        s_tree = (np.float64(dt) ** 2 - 1e-6) * n
+        assert abs(s_tree - (2.0 ** 24 + n - 1)) <= 2 * n * 2.0 ** -20 * 2.0 ** 24 / n + 4
