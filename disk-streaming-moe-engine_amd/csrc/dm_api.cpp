@@ -7,6 +7,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <atomic>
 #include <new>
 #include <stdexcept>
 #include <string>
@@ -25,6 +26,15 @@ using dm::LayerDev;
 namespace {
 
 constexpr int kMaxLayers = 4096;
+constexpr int kMaxDevices = 64;
+// Live contexts per device in this process.  The single-launch decode
+// kernel needs all its workgroups resident at once; with one context its
+// launches are stream-ordered and a plain launch suffices, with several the
+// grids of two contexts could each hold part of the device and wait for
+// each other, so their launches are cooperative (the runtime then keeps each
+// grid whole).
+std::atomic<int> g_live_ctx[kMaxDevices];
+
 // first-error key slots: [0, kMaxLayers) uploaded 4-bit layers, kMaxLayers
 // the unit calls, then one per GGUF layer
 constexpr int kGgufSlot0 = kMaxLayers + 1;
@@ -128,6 +138,7 @@ struct dmh_ctx {
   std::vector<const int32_t*> last_ids;
   std::vector<int> last_k;
   int num_cus = 0;
+  bool counted = false;           // counted in g_live_ctx
   float* ones = nullptr;          // [kNormMaxH] 1.0f: gamma of layers without one
   hipEvent_t switch_ev = nullptr;  // orders a stream switch after queued work
 };
@@ -280,14 +291,115 @@ dm::NormSpec layer_norm(const dmh_ctx* ctx, const Layer* Ly, float eps, bool tre
 // activations); below it the lane-chain router is as fast.
 constexpr int kMfmaRouterMinTokens = 64;
 
+// Device scratch of one run_block call.  Which buffers a call touches
+// depends on its path: the fused decode kernel none of them; the
+// multi-kernel single-token path z and h; several tokens z and the g_*
+// buffers; xn when the input is normalised outside the fused kernel.
+struct BlockScratch {
+  float* z = nullptr;         // [T][E+1] logits (and the shared-gate logit)
+  float* h = nullptr;         // [K+1][ldh] h of one token
+  float* xn = nullptr;        // [T][H] normalised input
+  int32_t* off = nullptr;     // [E+1] expert offsets
+  int32_t* perm = nullptr;    // [T*K] assignments in expert order
+  int32_t* meta = nullptr;    // [2] unit counts
+  int32_t* needlo = nullptr;  // [1] zero on entry; the combine clears it again
+  int2* units = nullptr;      // [group_units_max(T, K, E)]
+  uint16_t* xhi = nullptr;    // [T][H] bf16 hi parts of x
+  uint16_t* xlo = nullptr;    // [T][H] bf16 lo parts
+  uint16_t* hr = nullptr;     // [2][T*K][I] routed h, hi then lo
+  uint16_t* hs = nullptr;     // [2][T][Ish] shared h, hi then lo
+  float* r = nullptr;         // [T*K][H] routed down outputs
+  float* rs = nullptr;        // [T][H] shared down outputs
+};
+
+// Byte offsets of the scratch of T tokens carved from one block (each
+// buffer 256-byte aligned); returns the total.
+size_t scratch_carve(const LayerDev& L, int T, bool norm, uint8_t* base, BlockScratch* s) {
+  const size_t TK = (size_t)T * L.K, TH = (size_t)T * L.H;
+  const size_t ldh = (size_t)(L.I > L.Ish ? L.I : L.Ish);
+  size_t off = 0;
+  auto take = [&](size_t bytes) -> uint8_t* {
+    uint8_t* p = base ? base + off : nullptr;
+    off += align256(bytes);
+    return p;
+  };
+  BlockScratch t;
+  t.z = (float*)take((size_t)T * (L.E + 1) * 4);
+  t.h = (float*)take((size_t)(L.K + 1) * ldh * 4);
+  t.xn = norm ? (float*)take(TH * 4) : nullptr;
+  if (T > 1) {
+    t.off = (int32_t*)take((size_t)(L.E + 1) * 4);
+    t.perm = (int32_t*)take(TK * 4);
+    t.meta = (int32_t*)take(2 * 4);
+    t.needlo = (int32_t*)take(4);
+    t.units = (int2*)take((size_t)dm::group_units_max(T, L.K, L.E) * sizeof(int2));
+    t.xhi = (uint16_t*)take(TH * 2);
+    t.xlo = (uint16_t*)take(TH * 2);
+    t.hr = (uint16_t*)take(2 * TK * L.I * 2);
+    t.hs = (uint16_t*)take(2 * (size_t)T * L.Ish * 2);
+    t.r = (float*)take(TK * L.H * 4);
+    t.rs = (float*)take(TH * 4);
+  }
+  if (s) *s = t;
+  return off;
+}
+
+// The scratch of a call from the context's buffers, grown on demand (the
+// need-lo flag is zeroed when it is allocated and cleared by the combine
+// kernel that ends every call).
+hipError_t ctx_scratch(dmh_ctx* ctx, const LayerDev& L, int T, bool norm, BlockScratch* s) {
+  const size_t TK = (size_t)T * L.K, TH = (size_t)T * L.H;
+  const int ldh = L.I > L.Ish ? L.I : L.Ish;
+  hipError_t e;
+  if (norm) {
+    if ((e = ctx->xn.ensure(TH)) != hipSuccess) return e;
+    s->xn = ctx->xn.p;
+  }
+  if ((e = ctx->z.ensure((size_t)T * (L.E + 1))) != hipSuccess) return e;
+  if ((e = ctx->h.ensure((size_t)(L.K + 1) * ldh)) != hipSuccess) return e;
+  s->z = ctx->z.p;
+  s->h = ctx->h.p;
+  if (T <= 1) return hipSuccess;
+  if ((e = ctx->g_off.ensure(L.E + 1)) != hipSuccess) return e;
+  if ((e = ctx->g_perm.ensure(TK)) != hipSuccess) return e;
+  if ((e = ctx->g_meta.ensure(2)) != hipSuccess) return e;
+  const size_t nl_cap = ctx->g_needlo.cap;
+  if ((e = ctx->g_needlo.ensure(1)) != hipSuccess) return e;
+  if (ctx->g_needlo.cap != nl_cap &&
+      (e = hipMemsetAsync(ctx->g_needlo.p, 0, sizeof(int), ctx->cur)) != hipSuccess)
+    return e;
+  if ((e = ctx->g_units.ensure(dm::group_units_max(T, L.K, L.E))) != hipSuccess) return e;
+  if ((e = ctx->g_xhi.ensure(TH)) != hipSuccess) return e;
+  if ((e = ctx->g_xlo.ensure(TH)) != hipSuccess) return e;
+  if ((e = ctx->g_hr.ensure(2 * TK * L.I)) != hipSuccess) return e;
+  if ((e = ctx->g_hs.ensure(2 * (size_t)T * L.Ish)) != hipSuccess) return e;
+  if ((e = ctx->g_r.ensure(TK * L.H)) != hipSuccess) return e;
+  if ((e = ctx->g_rs.ensure(TH)) != hipSuccess) return e;
+  s->off = ctx->g_off.p;
+  s->perm = ctx->g_perm.p;
+  s->meta = ctx->g_meta.p;
+  s->needlo = ctx->g_needlo.p;
+  s->units = ctx->g_units.p;
+  s->xhi = ctx->g_xhi.p;
+  s->xlo = ctx->g_xlo.p;
+  s->hr = ctx->g_hr.p;
+  s->hs = ctx->g_hs.p;
+  s->r = ctx->g_r.p;
+  s->rs = ctx->g_rs.p;
+  return hipSuccess;
+}
+
 // nm (may be NULL): the block's input is rmsnorm(dx, nm->gamma, nm->eps),
-// computed inside the fused decode kernel or by a separate kernel into ctx->xn.
-// Under stream capture the fused kernel is not used: its launch tag is fixed
-// on the host, so every replay of a captured launch would carry the same tag
-// and its waits would pass on the previous replay's data.
+// computed inside the fused decode kernel or by a separate kernel into
+// scratch xn.  sc (may be NULL): the scratch to use instead of the
+// context's buffers.  Under stream capture the fused kernel is not used: its
+// launch tag is fixed on the host, so every replay of a captured launch
+// would carry the same tag and its waits would pass on the previous replay's
+// data.
 hipError_t run_block(dmh_ctx* ctx, Layer* Ly, int layer, const float* dx, const float* dres,
                      int T, float* dy, int32_t* dids, float* dprobs, float* dshg,
-                     bool allow_fused = true, const dm::NormSpec* nm = nullptr) {
+                     bool allow_fused = true, const dm::NormSpec* nm = nullptr,
+                     const BlockScratch* sc = nullptr) {
   const LayerDev& L = Ly->dev;
   hipStream_t st = ctx->cur;
   unsigned long long* status = ctx->status + layer;
@@ -298,11 +410,6 @@ hipError_t run_block(dmh_ctx* ctx, Layer* Ly, int layer, const float* dx, const 
   const bool fused = Ly->fused && allow_fused && T == 1 && cap == hipStreamCaptureStatusNone;
   const dm::NormSpec no_norm{0.0f, nullptr, 0};
   const bool norm = nm && nm->eps > 0.0f;
-  if (norm && !fused) {
-    if ((e = ctx->xn.ensure((size_t)T * L.H)) != hipSuccess) return e;
-    if ((e = dm::launch_rmsnorm_rows(dx, T, L.H, *nm, ctx->xn.p, st)) != hipSuccess) return e;
-    dx = ctx->xn.p;
-  }
   if (fused) {
     for (int t = 0; t < T; ++t) {
       if (Ly->launches >= (1u << 24) && (e = reset_counters(ctx, Ly)) != hipSuccess) return e;
@@ -311,73 +418,61 @@ hipError_t run_block(dmh_ctx* ctx, Layer* Ly, int layer, const float* dx, const 
       e = dm::launch_moe_decode(L, Ly->plan, dx + (size_t)t * L.H,
                                 dres ? dres + (size_t)t * L.H : nullptr, dy + (size_t)t * L.H,
                                 dids + (size_t)t * L.K, dprobs + (size_t)t * L.K, dshg + t, S,
-                                status, t, st, norm ? *nm : no_norm);
+                                status, t, st, norm ? *nm : no_norm,
+                                g_live_ctx[ctx->device].load(std::memory_order_relaxed) > 1);
       if (e != hipSuccess) return e;
     }
     return hipSuccess;
   }
-  if ((e = ctx->z.ensure((size_t)T * (L.E + 1))) != hipSuccess) return e;
-  if ((e = ctx->h.ensure((size_t)(L.K + 1) * ldh)) != hipSuccess) return e;
+  BlockScratch own;
+  if (!sc) {
+    if ((e = ctx_scratch(ctx, L, T, norm, &own)) != hipSuccess) return e;
+    sc = &own;
+  }
+  if (norm) {
+    if ((e = dm::launch_rmsnorm_rows(dx, T, L.H, *nm, sc->xn, st)) != hipSuccess) return e;
+    dx = sc->xn;
+  }
   if (T > 1) {
     // several tokens: route, group the assignments by expert and run each
     // expert's tokens together as a grouped GEMM
     const size_t TK = (size_t)T * L.K, TH = (size_t)T * L.H;
-    if ((e = ctx->g_off.ensure(L.E + 1)) != hipSuccess) return e;
-    if ((e = ctx->g_perm.ensure(TK)) != hipSuccess) return e;
-    if ((e = ctx->g_meta.ensure(2)) != hipSuccess) return e;
-    // need-lo flag: zero between calls (set zero at allocation, cleared by
-    // the combine kernel that ends every call)
-    const size_t nl_cap = ctx->g_needlo.cap;
-    if ((e = ctx->g_needlo.ensure(1)) != hipSuccess) return e;
-    if (ctx->g_needlo.cap != nl_cap &&
-        (e = hipMemsetAsync(ctx->g_needlo.p, 0, sizeof(int), st)) != hipSuccess)
-      return e;
-    if ((e = ctx->g_units.ensure(dm::group_units_max(T, L.K, L.E))) != hipSuccess) return e;
-    if ((e = ctx->g_xhi.ensure(TH)) != hipSuccess) return e;
-    if ((e = ctx->g_xlo.ensure(TH)) != hipSuccess) return e;
-    if ((e = ctx->g_hr.ensure(2 * TK * L.I)) != hipSuccess) return e;
-    if ((e = ctx->g_hs.ensure(2 * (size_t)T * L.Ish)) != hipSuccess) return e;
-    if ((e = ctx->g_r.ensure(TK * L.H)) != hipSuccess) return e;
-    if ((e = ctx->g_rs.ensure(TH)) != hipSuccess) return e;
-    if ((e = dm::launch_split_rows(dx, (int64_t)TH, ctx->g_xhi.p, ctx->g_xlo.p, ctx->g_needlo.p,
-                                   st)) != hipSuccess)
+    if ((e = dm::launch_split_rows(dx, (int64_t)TH, sc->xhi, sc->xlo, sc->needlo, st)) !=
+        hipSuccess)
       return e;
     if (T >= kMfmaRouterMinTokens) {
       // bf16 activations: matrix-core router; otherwise the lane-chain router
-      if ((e = dm::launch_router_mfma(L, ctx->g_xhi.p, ctx->g_needlo.p, T, ctx->z.p, st)) !=
-          hipSuccess)
+      if ((e = dm::launch_router_mfma(L, sc->xhi, sc->needlo, T, sc->z, st)) != hipSuccess)
         return e;
-      if ((e = dm::launch_router_dec(L, dx, T, ctx->z.p, status, st, ctx->g_needlo.p)) !=
-          hipSuccess)
+      if ((e = dm::launch_router_dec(L, dx, T, sc->z, status, st, sc->needlo)) != hipSuccess)
         return e;
-    } else if ((e = dm::launch_router_dec(L, dx, T, ctx->z.p, status, st)) != hipSuccess) {
+    } else if ((e = dm::launch_router_dec(L, dx, T, sc->z, status, st)) != hipSuccess) {
       return e;
     }
-    if ((e = dm::launch_router_select(ctx->z.p, L.E + 1, T, L.E, L.K, 1, dids, dprobs, dshg,
+    if ((e = dm::launch_router_select(sc->z, L.E + 1, T, L.E, L.K, 1, dids, dprobs, dshg,
                                       status, st)) != hipSuccess)
       return e;
-    if ((e = dm::launch_group_build(dids, T, L.K, L.E, ctx->g_off.p, ctx->g_perm.p,
-                                    ctx->g_units.p, ctx->g_meta.p, st)) != hipSuccess)
+    if ((e = dm::launch_group_build(dids, T, L.K, L.E, sc->off, sc->perm, sc->units, sc->meta,
+                                    st)) != hipSuccess)
       return e;
-    if ((e = dm::launch_experts_grouped(L, ctx->g_xhi.p, ctx->g_xlo.p, ctx->g_needlo.p,
-                                        ctx->g_off.p, ctx->g_perm.p, ctx->g_units.p,
-                                        ctx->g_meta.p, T, ctx->g_hr.p, ctx->g_hr.p + TK * L.I,
-                                        ctx->g_hs.p, ctx->g_hs.p + (size_t)T * L.Ish, ctx->g_r.p,
-                                        ctx->g_rs.p, status, st)) != hipSuccess)
+    if ((e = dm::launch_experts_grouped(L, sc->xhi, sc->xlo, sc->needlo, sc->off, sc->perm,
+                                        sc->units, sc->meta, T, sc->hr, sc->hr + TK * L.I, sc->hs,
+                                        sc->hs + (size_t)T * L.Ish, sc->r, sc->rs, status, st)) !=
+        hipSuccess)
       return e;
-    return dm::launch_combine(ctx->g_r.p, ctx->g_rs.p, dprobs, dshg, dres, T, L.H, L.K, dy, status,
-                              st, ctx->g_needlo.p);
+    return dm::launch_combine(sc->r, sc->rs, dprobs, dshg, dres, T, L.H, L.K, dy, status, st,
+                              sc->needlo);
   }
-  if ((e = dm::launch_router_dec(L, dx, T, ctx->z.p, status, st)) != hipSuccess) return e;
-  if ((e = dm::launch_router_select(ctx->z.p, L.E + 1, T, L.E, L.K, 1, dids, dprobs, dshg, status,
+  if ((e = dm::launch_router_dec(L, dx, T, sc->z, status, st)) != hipSuccess) return e;
+  if ((e = dm::launch_router_select(sc->z, L.E + 1, T, L.E, L.K, 1, dids, dprobs, dshg, status,
                                     st)) != hipSuccess)
     return e;
   for (int t = 0; t < T; ++t) {
     const float* xt = dx + (size_t)t * L.H;
-    if ((e = dm::launch_gateup_dec(L, xt, dids + (size_t)t * L.K, ctx->h.p, ldh, t, status, st)) !=
+    if ((e = dm::launch_gateup_dec(L, xt, dids + (size_t)t * L.K, sc->h, ldh, t, status, st)) !=
         hipSuccess)
       return e;
-    if ((e = dm::launch_down_dec(L, ctx->h.p, ldh, dids + (size_t)t * L.K,
+    if ((e = dm::launch_down_dec(L, sc->h, ldh, dids + (size_t)t * L.K,
                                  dprobs + (size_t)t * L.K, dshg + t,
                                  dres ? dres + (size_t)t * L.H : nullptr, dy + (size_t)t * L.H, t,
                                  status, st)) != hipSuccess)
@@ -466,6 +561,9 @@ int dmh_create(int device, dmh_ctx** out, char* err, size_t errlen) {
   if (device < 0 || device >= n)
     return set_err(err, errlen, DMH_ERR_INVALID_ARG, "dmh_create: no HIP device %d (%d present)",
                    device, n);
+  if (device >= kMaxDevices)
+    return set_err(err, errlen, DMH_ERR_INVALID_ARG, "dmh_create: device %d >= %d", device,
+                   kMaxDevices);
   HIP_TRY(hipSetDevice(device));
   dmh_ctx* c = new dmh_ctx();
   c->device = device;
@@ -491,6 +589,8 @@ int dmh_create(int device, dmh_ctx** out, char* err, size_t errlen) {
   c->last_ids.assign(kMaxLayers + 1, nullptr);
   c->last_k.assign(kMaxLayers + 1, 0);
   c->glayers.assign(kMaxLayers, nullptr);
+  g_live_ctx[device].fetch_add(1);
+  c->counted = true;
   *out = c;
   return DMH_OK;
 }
@@ -530,6 +630,7 @@ int dmh_destroy(dmh_ctx* c) {
   if (c->vkey) (void)hipFree(c->vkey);
   if (c->flags) (void)hipFree(c->flags);
   if (c->own) (void)hipStreamDestroy(c->own);
+  if (c->counted) g_live_ctx[c->device].fetch_sub(1);
   delete c;
   return DMH_OK;
 }

@@ -30,10 +30,12 @@ DecodeSync decode_sync_carve(const LayerDev& L, void* base);
 DecodePlan make_decode_plan(const LayerDev& L, int num_cus);
 hipError_t decode_occupancy(const LayerDev& L, const DecodePlan& P, int* blocks_per_cu);
 // nm.eps > 0: the router and experts see rmsnorm(x, nm.gamma, nm.eps) in the
-// order nm.seq selects (NormSpec).
+// order nm.seq selects (NormSpec).  cooperative: launch with
+// hipLaunchCooperativeKernel, which guarantees that every workgroup is
+// resident (slower; for devices shared by several contexts).
 hipError_t launch_moe_decode(const LayerDev& L, const DecodePlan& P, const float* x,
                              const float* residual, float* y, int32_t* ids, float* probs,
                              float* shg, const DecodeSync& S, unsigned long long* status, int token,
-                             hipStream_t st, const NormSpec& nm);
+                             hipStream_t st, const NormSpec& nm, bool cooperative);
 
 }  // namespace dm

@@ -227,3 +227,23 @@ def test_upload_from_files_missing_expert(block, tmp_path):
     assert str(ei.value) == ('{"error_type":"WEIGHT_LOAD_FAILED","detail":"required router gate'
                              ' tensor not in weight_map: model.layers.1.mlp.gate.weight",'
                              '"shard":"","tensor_name":"model.layers.1.mlp.gate.weight"}')
+
+
+def test_two_contexts_on_one_device(block, oracle, qwen):
+    """With a second live context on the device the single-launch decode
+    kernel is launched cooperatively (every workgroup resident); both
+    contexts still route and compute as the oracle does."""
+    from dismoen import MoEBlock
+    x = synth.make_activations(np.random.default_rng(113), (2, 2048))
+    with MoEBlock(0) as other:
+        other.upload_layer(0, qwen)
+        for t in range(2):
+            y2, ids2, p2, s2 = other.forward_arrays(0, x[t:t + 1], 1)
+            check_layer(block, oracle, qwen, 1, x[t:t + 1])
+            yo, ido, po, so = oracle.moe_layer_q4(qwen, x[t:t + 1], 1)
+            assert np.array_equal(ids2, ido)
+            assert np.array_equal(p2.view(np.uint32), po.view(np.uint32))
+            err, rms, ok = tol_check(y2, yo)
+            assert ok, (err, rms)
+    # back to one context: the plain launch
+    check_layer(block, oracle, qwen, 1, x[:1])
