@@ -8,6 +8,7 @@
 
 #include <algorithm>
 #include <atomic>
+#include <mutex>
 #include <new>
 #include <stdexcept>
 #include <string>
@@ -35,6 +36,16 @@ constexpr int kMaxDevices = 64;
 // grid whole).
 std::atomic<int> g_live_ctx[kMaxDevices];
 
+// Scratch of dmh_moe_forward_noalloc: a file-scope device array, one copy
+// per GPU the library runs on, held until the process ends.  Host code never
+// uses the array's name as an address: dmh_create resolves each device's
+// copy once (hipGetSymbolAddress with that device current) into
+// g_scratch_dev[device], and only that pointer reaches kernels.  Every call
+// of the entry point on a device shares that device's copy.
+constexpr size_t kNoAllocScratchBytes = (size_t)8 << 20;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+void* g_scratch_dev[kMaxDevices];
+std::mutex g_scratch_mu;
 // first-error key slots: [0, kMaxLayers) uploaded 4-bit layers, kMaxLayers
 // the unit calls, then one per GGUF layer
 constexpr int kGgufSlot0 = kMaxLayers + 1;
@@ -589,6 +600,20 @@ int dmh_create(int device, dmh_ctx** out, char* err, size_t errlen) {
   c->last_ids.assign(kMaxLayers + 1, nullptr);
   c->last_k.assign(kMaxLayers + 1, 0);
   c->glayers.assign(kMaxLayers, nullptr);
+  {
+    // this device's copy of the no-allocation scratch, resolved once
+    std::lock_guard<std::mutex> g(g_scratch_mu);
+    if (!g_scratch_dev[device]) {
+      void* p = nullptr;
+      e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+      if (e != hipSuccess || !p) {
+        dmh_destroy(c);
+        return set_err(err, errlen, DMH_ERR_HIP, "dmh_create: scratch address: %s",
+                       hipGetErrorString(e));
+      }
+      g_scratch_dev[device] = p;
+    }
+  }
   g_live_ctx[device].fetch_add(1);
   c->counted = true;
   *out = c;
@@ -957,6 +982,54 @@ int dmh_moe_forward(dmh_ctx* c, int layer, const float* x, const float* residual
                     size_t errlen) {
   return moe_forward_impl(c, layer, x, residual, T, y, ids, probs, shg, flags, nullptr, err,
                           errlen);
+}
+
+// dmh_moe_forward with every buffer of the call in this device's static
+// scratch: no allocation of any kind.
+int dmh_moe_forward_noalloc(dmh_ctx* c, int layer, const float* x, const float* residual, int T,
+                            float* y, int32_t* ids, float* probs, float* shg, unsigned flags,
+                            char* err, size_t errlen) {
+  Layer* Ly = get_layer(c, layer);
+  if (!Ly)
+    return set_err(err, errlen, DMH_ERR_INVALID_ARG,
+                   "dmh_moe_forward_noalloc: layer %d not uploaded", layer);
+  if (!(flags & DMH_F_DEVICE))
+    return set_err(err, errlen, DMH_ERR_INVALID_ARG,
+                   "dmh_moe_forward_noalloc: needs DMH_F_DEVICE (host pointers are staged "
+                   "through allocated buffers)");
+  if (!x || !y)
+    return set_err(err, errlen, DMH_ERR_INVALID_ARG,
+                   "dmh_moe_forward_noalloc: x and y are required");
+  if (T <= 0)
+    return set_err(err, errlen, DMH_ERR_ACT,
+                   "{\"error_type\":\"ACT_LOAD_FAILED\",\"detail\":\"dimensions must be"
+                   " positive\",\"stage\":\"router\",\"layer\":%d}", layer);
+  const LayerDev& L = Ly->dev;
+  const size_t TK = (size_t)T * L.K;
+  // scratch: the path's buffers, then ids / probs / shared gate when the
+  // caller passes none
+  const size_t need = scratch_carve(L, T, false, nullptr, nullptr) + (ids ? 0 : align256(TK * 4)) +
+                      (probs ? 0 : align256(TK * 4)) + (shg ? 0 : align256((size_t)T * 4));
+  if (need > kNoAllocScratchBytes)
+    return set_err(err, errlen, DMH_ERR_INVALID_ARG,
+                   "dmh_moe_forward_noalloc: seq_len %d needs %zu bytes of scratch, more than the"
+                   " %zu bytes held per device", T, need, kNoAllocScratchBytes);
+  HIP_TRY(hipSetDevice(c->device));
+  uint8_t* base = (uint8_t*)g_scratch_dev[c->device];
+  if (!base)
+    return set_err(err, errlen, DMH_ERR_HIP, "dmh_moe_forward_noalloc: no scratch on device %d",
+                   c->device);
+  BlockScratch sc;
+  size_t off = scratch_carve(L, T, false, base, &sc);
+  if (!ids) { ids = (int32_t*)(base + off); off += align256(TK * 4); }
+  if (!probs) { probs = (float*)(base + off); off += align256(TK * 4); }
+  if (!shg) { shg = (float*)(base + off); off += align256((size_t)T * 4); }
+  // the need-lo flag starts at zero (a call that failed may have left it set)
+  if (sc.needlo) HIP_TRY(dm::launch_fill_i32(sc.needlo, 1, 0, c->cur));
+  HIP_TRY(run_block(c, Ly, layer, x, residual, T, y, ids, probs, shg, true, nullptr, &sc));
+  c->last_ids[layer] = ids;
+  c->last_k[layer] = L.K;
+  return DMH_OK;
 }
 
 int dmh_port_moe_forward(dmh_ctx* c, int layer, const float* x_mid, int T, float eps, float* y,

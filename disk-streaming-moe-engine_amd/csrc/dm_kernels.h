@@ -56,6 +56,8 @@ hipError_t launch_check_ids(const int32_t* ids, int T, int K, int E, int32_t* ou
                             unsigned long long* status, hipStream_t st);
 
 // ---- glue ----
+// p[0..n) = v (a kernel, so that it can be captured into a graph).
+hipError_t launch_fill_i32(int32_t* p, int n, int32_t v, hipStream_t st);
 // rmsnorm of T rows [T][H] (H <= 8192) into out, in the order nm.seq selects.
 hipError_t launch_rmsnorm_rows(const float* x, int T, int H, const NormSpec& nm, float* out,
                                hipStream_t st);

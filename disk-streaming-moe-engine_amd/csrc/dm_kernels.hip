@@ -865,6 +865,20 @@ hipError_t launch_rmsnorm_rows(const float* x, int T, int H, const NormSpec& nm,
   return hipGetLastError();
 }
 
+// ---- a small fill kernel ---------------------------------------------------
+// Clears flags and counters in code a caller may capture into a HIP graph
+// (a kernel node instead of a memset node).
+__global__ __launch_bounds__(256) void k_fill_i32(int32_t* __restrict__ p, int n, int32_t v) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i < n) p[i] = v;
+}
+
+hipError_t launch_fill_i32(int32_t* p, int n, int32_t v, hipStream_t st) {
+  if (n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(k_fill_i32, dim3((n + 255) / 256), dim3(256), 0, st, p, n, v);
+  return hipGetLastError();
+}
+
 // ---- shared gate scores and expert-id checks (unit entry points) ----------
 // One thread per token: sigmoid of the gate logit with the two checks of
 // shared_gate_forward (src/layers/moe.mojo:83-100) in its order.

@@ -33,7 +33,7 @@ EXPORTS = (
     "dmh_gguf_num_tensors", "dmh_gguf_find", "dmh_gguf_tensor_info", "dmh_gguf_metadata",
     "dmh_gguf_read", "dmh_dequant_gguf", "dmh_gguf_stream_tensor_f32",
     "dmh_upload_moe_layer_gguf", "dmh_free_layer_gguf", "dmh_moe_forward_gguf",
-    "dmh_set_layer_norm", "dmh_port_moe_forward",
+    "dmh_set_layer_norm", "dmh_port_moe_forward", "dmh_moe_forward_noalloc",
 )
 
 
@@ -108,6 +108,8 @@ def lib():
     L.dmh_free_layer.argtypes = [vp, i32]
     L.dmh_layer_bytes.argtypes = [vp, i32, C.POINTER(C.c_int64)]
     L.dmh_moe_forward.argtypes = [vp, i32, vp, vp, i32, vp, vp, vp, vp, u32, C.c_char_p, sz]
+    L.dmh_moe_forward_noalloc.argtypes = [vp, i32, vp, vp, i32, vp, vp, vp, vp, u32, C.c_char_p,
+                                          sz]
     L.dmh_moe_stack_forward.argtypes = [vp, i32, i32, C.c_float, vp, i32, vp, vp, vp, u32,
                                         C.c_char_p, sz]
     L.dmh_router_forward.argtypes = [vp, vp, vp, i32, i32, i32, i32, i32, i32, vp, vp, u32,

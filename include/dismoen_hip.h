@@ -149,6 +149,22 @@ int dmh_moe_forward(dmh_ctx* ctx, int layer, const float* x, const float* residu
                     int seq_len, float* y, int32_t* ids, float* probs,
                     float* shared_gate, unsigned flags, char* err, size_t errlen);
 
+/* dmh_moe_forward that allocates nothing: no counterpart in the reference;
+ * for callers that cannot allocate device or host memory during a call
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  DMH_F_DEVICE is required (host pointers would need staging
+ * buffers).  Every buffer of the call (logits, grouping, h, partial outputs,
+ * and ids / probs / shared_gate when NULL) is carved from one static 8 MiB
+ * array per device that the library holds until the process ends; a call
+ * that needs more (about 80 tokens at the Qwen3.6 layer shape) fails with
+ * DMH_ERR_INVALID_ARG and changes nothing.  All calls on a device share its
+ * array, which keeps the last call's contents: calls that overlap on one
+ * device (several streams or contexts) race and must be serialised by the
+ * caller.  Outputs equal dmh_moe_forward's bit for bit. */
+int dmh_moe_forward_noalloc(dmh_ctx* ctx, int layer, const float* x, const float* residual,
+                            int seq_len, float* y, int32_t* ids, float* probs,
+                            float* shared_gate, unsigned flags, char* err, size_t errlen);
+
 /* The post-attention RMSNorm weight of an uploaded layer: gamma [hidden] fp32
  * (PortBlockWeights.post_attention_layernorm_gamma,
  * src/layers/port_scheduler.mojo:65-86, used at :383-385), copied to the
