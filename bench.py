@@ -71,18 +71,69 @@ def parse():
     return ap.parse_args()
 
 
+def cpu_info():
+    """Host cores this process may use and the CPU model name."""
+    model = None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        n = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        n = os.cpu_count()
+    return n, model
+
+
 def cpu_baseline(L, x_tokens, budget_s):
-    """The oracle (CPU restatement of the reference composition: per-use dequant
-    of the selected experts, fp32 SwiGLU, one thread) on a bounded token sample."""
+    """The oracle (CPU restatement of the reference composition) on bounded
+    token samples of the same layer, in the reference's four CPU modes:
+    threads=1 (its verdict mode) and threads=min(K, cores) through the
+    worker-pool partition of parallel_moe_experts (router and shared expert
+    serial), each with per-use dequantization of the selected experts (the
+    reference's quant_loader) and with every expert pre-dequantized to fp32
+    (a compute-only bound).  value: threads=1, dequant-per-use."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as O
-    n, t0 = 0, time.perf_counter()
-    while n < len(x_tokens) and (time.perf_counter() - t0) < budget_s:
-        O.moe_layer_q4(L, x_tokens[n:n + 1], 1)
-        n += 1
-    dt = time.perf_counter() - t0
-    return {"value": round(dt / n * 1e6, 1), "unit": "us/token", "cores": 1, "kind": "port",
-            "sample": f"{n} decode tokens of the same layer, dequant-per-use, threads=1"}
+    ncores, model = cpu_info()
+    nthr = max(1, min(L.top_k, ncores))
+
+    def timed(budget, pool=None, cache=None):
+        n, t0 = 0, time.perf_counter()
+        while n < len(x_tokens) and (time.perf_counter() - t0) < budget:
+            O.moe_layer_q4(L, x_tokens[n:n + 1], 1, pool=pool, cache=cache)
+            n += 1
+        return (time.perf_counter() - t0) / n * 1e6, n
+
+    per_use_1, n1 = timed(budget_s * 0.4)
+    pool = O.Pool(nthr)
+    try:
+        per_use_k, nk = timed(budget_s * 0.2, pool=pool)
+        t0 = time.perf_counter()
+        cache = O.LayerCache(L, threads=ncores)
+        build_s = time.perf_counter() - t0
+        cached_1, nc1 = timed(budget_s * 0.2, cache=cache)
+        cached_k, nck = timed(budget_s * 0.2, pool=pool, cache=cache)
+        del cache
+    finally:
+        pool.close()
+    return {"value": round(per_use_1, 1), "unit": "us/token", "cores": 1, "kind": "port",
+            "sample": f"{n1} decode tokens of the same layer, dequant-per-use, threads=1",
+            "nproc": ncores, "cpu_model": model,
+            "variants": {
+                "threads1_dequant_per_use": {"us_per_token": round(per_use_1, 1), "tokens": n1},
+                f"threads{nthr}_dequant_per_use": {"us_per_token": round(per_use_k, 1),
+                                                    "tokens": nk},
+                "threads1_predequantized_fp32": {"us_per_token": round(cached_1, 1),
+                                                 "tokens": nc1},
+                f"threads{nthr}_predequantized_fp32": {"us_per_token": round(cached_k, 1),
+                                                       "tokens": nck},
+                "predequantize_build_s": round(build_s, 2),
+                "predequantize_build_threads": ncores}}
 
 
 MFMA_BF16_PEAK_TFLOPS = 2500.0

@@ -961,15 +961,54 @@ static int load_expert(const or_layer_q4* L, int e, expert_f32* out, char* err,
   return st;
 }
 
-or_layer_cache* or_layer_cache_build(const or_layer_q4* L, char* err, size_t errlen) {
+/* The cache is built by nthreads threads (experts split by partition_range,
+ * the shared expert on thread 0); every expert's dequantization is the same
+ * single-threaded routine, so the contents do not depend on nthreads. */
+typedef struct {
+  const or_layer_q4* L;
+  or_layer_cache* c;
+  int tid, n, st;
+  char err[256];
+} cache_job;
+
+static void* cache_worker(void* arg) {
+  cache_job* j = (cache_job*)arg;
+  int64_t b, e;
+  or_partition_range(j->c->E, j->tid, j->n, &b, &e);
+  for (int64_t x = b; x < e && !j->st; ++x)
+    j->st = load_expert(j->L, (int)x, &j->c->ex[x], j->err, sizeof(j->err));
+  if (!j->st && j->tid == 0) j->st = load_expert(j->L, -1, &j->c->sh, j->err, sizeof(j->err));
+  return NULL;
+}
+
+or_layer_cache* or_layer_cache_build_mt(const or_layer_q4* L, int nthreads, char* err,
+                                        size_t errlen) {
   or_layer_cache* c = (or_layer_cache*)calloc(1, sizeof(or_layer_cache));
   if (!c) return NULL;
   c->E = L->num_experts;
   c->ex = (expert_f32*)calloc((size_t)c->E, sizeof(expert_f32));
-  for (int e = 0; e < c->E; ++e)
-    if (load_expert(L, e, &c->ex[e], err, errlen)) { or_layer_cache_free(c); return NULL; }
-  if (load_expert(L, -1, &c->sh, err, errlen)) { or_layer_cache_free(c); return NULL; }
+  if (nthreads < 1) nthreads = 1;
+  if (nthreads > 64) nthreads = 64;
+  cache_job jobs[64];
+  pthread_t th[64];
+  for (int t = 0; t < nthreads; ++t) {
+    jobs[t].L = L; jobs[t].c = c; jobs[t].tid = t; jobs[t].n = nthreads; jobs[t].st = 0;
+    jobs[t].err[0] = 0;
+    if (t > 0) pthread_create(&th[t], NULL, cache_worker, &jobs[t]);
+  }
+  cache_worker(&jobs[0]);
+  for (int t = 1; t < nthreads; ++t) pthread_join(th[t], NULL);
+  for (int t = 0; t < nthreads; ++t)
+    if (jobs[t].st) {
+      if (err && errlen) snprintf(err, errlen, "%s", jobs[t].err);
+      or_layer_cache_free(c);
+      return NULL;
+    }
   return c;
+}
+
+or_layer_cache* or_layer_cache_build(const or_layer_q4* L, char* err, size_t errlen) {
+  return or_layer_cache_build_mt(L, 1, err, errlen);
 }
 
 void or_layer_cache_free(or_layer_cache* c) {

@@ -141,6 +141,9 @@ typedef struct {
 typedef struct or_layer_cache or_layer_cache;
 or_layer_cache* or_layer_cache_build(const or_layer_q4* L, char* err,
                                      size_t errlen);
+/* The same cache built by nthreads threads (identical contents). */
+or_layer_cache* or_layer_cache_build_mt(const or_layer_q4* L, int nthreads, char* err,
+                                        size_t errlen);
 void or_layer_cache_free(or_layer_cache* c);
 
 /* forward_moe_block for the 4-bit layer.  residual == NULL gives the

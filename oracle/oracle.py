@@ -86,6 +86,8 @@ def lib():
                                                    C.c_void_p]
         L.or_layer_cache_build.argtypes = [C.c_void_p, C.c_char_p, C.c_size_t]
         L.or_layer_cache_build.restype = C.c_void_p
+        L.or_layer_cache_build_mt.argtypes = [C.c_void_p, C.c_int, C.c_char_p, C.c_size_t]
+        L.or_layer_cache_build_mt.restype = C.c_void_p
         L.or_layer_cache_free.argtypes = [C.c_void_p]
         L.or_moe_layer_q4.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, F32P, C.c_void_p,
                                       C.c_int, C.c_int, F32P, I32P, F32P, F32P, C.c_char_p,
@@ -343,11 +345,11 @@ def _layer_struct(L):
 class LayerCache:
     """Every expert of a layer dequantized once to fp32 (compute-only bound)."""
 
-    def __init__(self, L):
+    def __init__(self, L, threads: int = 1):
         self._s = _layer_struct(L)
         self._keep = L
         e = _errbuf()
-        self.h = lib().or_layer_cache_build(C.byref(self._s), e, 1024)
+        self.h = lib().or_layer_cache_build_mt(C.byref(self._s), threads, e, 1024)
         if not self.h:
             raise OracleError(e.value.decode())
 

@@ -240,3 +240,20 @@ def test_rmsnorm_order_closed_form(oracle):
         dt = np.float32(x[1] / tree[1])
         s_tree = (np.float64(dt) ** 2 - 1e-6) * n
         assert abs(s_tree - (2.0 ** 24 + n - 1)) <= 2 * n * 2.0 ** -20 * 2.0 ** 24 / n + 4
+
+def test_layer_cache_threads_and_pool_bit_exact(oracle):
+    """The pre-dequantized fp32 cache built by several threads, the pool of
+    parallel_moe_experts and dequant-per-use all give the same bits (the CPU
+    baseline's four modes compute one result)."""
+    L = synth.make_layer(**synth.CONFIG_TOY, seed=12)
+    x = synth.make_activations(np.random.default_rng(13), (3, 256))
+    ref = oracle.moe_layer_q4(L, x, 3)
+    pool = oracle.Pool(4)
+    try:
+        for cache in (oracle.LayerCache(L, 1), oracle.LayerCache(L, 5)):
+            for p in (None, pool):
+                got = oracle.moe_layer_q4(L, x, 3, cache=cache, pool=p)
+                for u, v in zip(ref, got):
+                    assert np.array_equal(np.asarray(u).view(np.uint8), np.asarray(v).view(np.uint8))
+    finally:
+        pool.close()
