@@ -99,23 +99,28 @@ struct DevBuf {
   }
 };
 
-// Page-locked host memory for the host-pointer calls (hipHostMalloc), so
-// that the copies are single DMA transfers instead of staged ones.
+// Page-locked host memory for the host-pointer calls (hipHostMalloc): the
+// copies are single DMA transfers instead of staged ones, and kernels can
+// read and write it directly through its device address d.
 struct PinBuf {
   uint8_t* p = nullptr;
+  uint8_t* d = nullptr;
   size_t cap = 0;  // bytes
   hipError_t ensure(size_t n) {
     if (n <= cap) return hipSuccess;
-    if (p) (void)hipHostFree(p);
-    p = nullptr;
-    cap = 0;
+    release();
     hipError_t e = hipHostMalloc(reinterpret_cast<void**>(&p), n, hipHostMallocDefault);
-    if (e == hipSuccess) cap = n;
-    return e;
+    if (e == hipSuccess) e = hipHostGetDevicePointer(reinterpret_cast<void**>(&d), p, 0);
+    if (e != hipSuccess) {
+      release();
+      return e;
+    }
+    cap = n;
+    return hipSuccess;
   }
   void release() {
     if (p) (void)hipHostFree(p);
-    p = nullptr;
+    p = d = nullptr;
     cap = 0;
   }
 };
@@ -143,6 +148,9 @@ struct dmh_ctx {
   DevBuf<float> g_r, g_rs;
   std::vector<GgufLayer*> glayers;
   unsigned long long* status = nullptr;  // [kStatusSlots] first-error keys
+  // status_clean[l]: slot l holds no error and nothing has run on it since
+  // a host-pointer call read it back, so the next one need not reset it
+  std::vector<uint8_t> status_clean;
   unsigned long long* vkey = nullptr;    // upload validation key
   unsigned* flags = nullptr;             // upload flags
   // where to find the routing of the last device-mode call per layer
@@ -410,10 +418,12 @@ hipError_t ctx_scratch(dmh_ctx* ctx, const LayerDev& L, int T, bool norm, BlockS
 hipError_t run_block(dmh_ctx* ctx, Layer* Ly, int layer, const float* dx, const float* dres,
                      int T, float* dy, int32_t* dids, float* dprobs, float* dshg,
                      bool allow_fused = true, const dm::NormSpec* nm = nullptr,
-                     const BlockScratch* sc = nullptr) {
+                     const BlockScratch* sc = nullptr, unsigned long long* status_out = nullptr,
+                     bool* exported = nullptr) {
   const LayerDev& L = Ly->dev;
   hipStream_t st = ctx->cur;
   unsigned long long* status = ctx->status + layer;
+  ctx->status_clean[layer] = 0;
   const int ldh = L.I > L.Ish ? L.I : L.Ish;
   hipError_t e;
   hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
@@ -430,9 +440,11 @@ hipError_t run_block(dmh_ctx* ctx, Layer* Ly, int layer, const float* dx, const 
                                 dres ? dres + (size_t)t * L.H : nullptr, dy + (size_t)t * L.H,
                                 dids + (size_t)t * L.K, dprobs + (size_t)t * L.K, dshg + t, S,
                                 status, t, st, norm ? *nm : no_norm,
-                                g_live_ctx[ctx->device].load(std::memory_order_relaxed) > 1);
+                                g_live_ctx[ctx->device].load(std::memory_order_relaxed) > 1,
+                                status_out);
       if (e != hipSuccess) return e;
     }
+    if (exported) *exported = status_out != nullptr;
     return hipSuccess;
   }
   BlockScratch own;
@@ -599,6 +611,7 @@ int dmh_create(int device, dmh_ctx** out, char* err, size_t errlen) {
   if (hipGetDeviceProperties(&prop, device) == hipSuccess) c->num_cus = prop.multiProcessorCount;
   c->last_ids.assign(kMaxLayers + 1, nullptr);
   c->last_k.assign(kMaxLayers + 1, 0);
+  c->status_clean.assign(kMaxLayers, 0);
   c->glayers.assign(kMaxLayers, nullptr);
   {
     // this device's copy of the no-allocation scratch, resolved once
@@ -878,6 +891,78 @@ int dmh_layer_bytes(dmh_ctx* c, int layer, int64_t* bytes) {
 
 namespace {
 
+// One token with host pointers, the drop-in's decode call.  The kernels read
+// x and the residual from, and write y, ids, probs and the shared gate into,
+// the page-locked block through its device address, so the call is one
+// launch and one synchronisation (every workgroup of the fused kernel stores
+// the status key into the block as it ends, the call's key is their
+// minimum; other paths read it back), and the key's reset is skipped while
+// the previous host call left it clean.
+int moe_forward_host1(dmh_ctx* c, Layer* Ly, int layer, const float* x, const float* residual,
+                      float* y, int32_t* ids, float* probs, float* shg, const dm::NormSpec* nm,
+                      char* err, size_t errlen) {
+  const LayerDev& L = Ly->dev;
+  const size_t H = (size_t)L.H, K = (size_t)L.K;
+  const size_t o_x = 0, o_res = align256(H * 4), o_y = o_res + (residual ? align256(H * 4) : 0),
+               o_ids = o_y + align256(H * 4), o_probs = o_ids + align256(K * 4),
+               o_shg = o_probs + align256(K * 4), o_key = o_shg + 256,
+               nkey = (size_t)(Ly->fused ? Ly->plan.grid : 1), bytes = o_key + nkey * 8;
+  hipStream_t st = c->cur;
+  HIP_TRY(c->pin.ensure(bytes));
+  uint8_t* hb = c->pin.p;
+  uint8_t* db = c->pin.d;
+  memcpy(hb + o_x, x, H * 4);
+  if (residual) memcpy(hb + o_res, residual, H * 4);
+  const float* dx = reinterpret_cast<const float*>(db + o_x);
+  const float* dres = residual ? reinterpret_cast<const float*>(db + o_res) : nullptr;
+  float* dy = reinterpret_cast<float*>(db + o_y);
+  int32_t* dids = reinterpret_cast<int32_t*>(db + o_ids);
+  float* dprobs = reinterpret_cast<float*>(db + o_probs);
+  float* dshg = reinterpret_cast<float*>(db + o_shg);
+  if (!c->status_clean[layer]) HIP_TRY(reset_status(c, layer));
+  size_t nk = 1;  // status words the last run left in the block
+  auto run_and_fetch = [&](bool allow_fused) -> hipError_t {
+    // the fused kernel's workgroups write the key into the block themselves
+    bool exported = false;
+    hipError_t e = run_block(c, Ly, layer, dx, dres, 1, dy, dids, dprobs, dshg, allow_fused, nm,
+                             nullptr, reinterpret_cast<unsigned long long*>(db + o_key), &exported);
+    if (e == hipSuccess && !exported)
+      e = hipMemcpyAsync(hb + o_key, c->status + layer, 8, hipMemcpyDeviceToHost, st);
+    if (e == hipSuccess) e = hipStreamSynchronize(st);
+    nk = exported ? nkey : 1;
+    return e;
+  };
+  auto key_of = [&]() {
+    unsigned long long k = ~0ull, v;
+    for (size_t i = 0; i < nk; ++i) {
+      memcpy(&v, hb + o_key + i * 8, 8);
+      k = v < k ? v : k;
+    }
+    return k;
+  };
+  HIP_TRY(run_and_fetch(true));
+  c->last_ids[layer] = nullptr;  // the block is rewritten by the next call
+  c->last_k[layer] = L.K;
+  unsigned long long key = key_of();
+  if (dm::key_phase(key) == dm::kPhExpert && dm::key_kind(key) == dm::kEkRecheck) {
+    // see moe_forward_impl: the multi-kernel path names the failing check
+    HIP_TRY(reset_status(c, layer));
+    HIP_TRY(run_and_fetch(false));
+    key = key_of();
+  }
+  memcpy(y, hb + o_y, H * 4);
+  if (ids) memcpy(ids, hb + o_ids, K * 4);
+  if (probs) memcpy(probs, hb + o_probs, K * 4);
+  if (shg) memcpy(shg, hb + o_shg, 4);
+  int rc = finish_status(c, Ly, layer, key, reinterpret_cast<const int32_t*>(hb + o_ids), err,
+                         errlen);
+  if (rc)
+    HIP_TRY(reset_status(c, layer));
+  else
+    c->status_clean[layer] = 1;
+  return rc;
+}
+
 // dmh_moe_forward and dmh_port_moe_forward: nm (may be NULL) normalises the
 // block input first.
 int moe_forward_impl(dmh_ctx* c, int layer, const float* x, const float* residual, int T,
@@ -910,8 +995,11 @@ int moe_forward_impl(dmh_ctx* c, int layer, const float* x, const float* residua
     c->last_k[layer] = L.K;
     return DMH_OK;
   }
-  // Host pointers: the inputs go through one page-locked block and one
-  // copy, the outputs (with the status key) come back the same way.
+  if (T == 1) return moe_forward_host1(c, Ly, layer, x, residual, y, ids, probs, shg, nm, err,
+                                       errlen);
+  // Host pointers, several tokens: the inputs go through one page-locked
+  // block and one copy, the outputs (with the status key) come back the
+  // same way.
   const size_t in_bytes = align256(TH * 4) + (residual ? TH * 4 : 0);
   const size_t o_y = 0, o_ids = align256(o_y + TH * 4), o_probs = align256(o_ids + TK * 4),
                o_shg = align256(o_probs + TK * 4), o_key = align256(o_shg + (size_t)T * 4),
@@ -1323,6 +1411,7 @@ int dmh_experts_forward(dmh_ctx* c, int layer, const float* x, int T, const int3
   const bool dev = flags & DMH_F_DEVICE;
   hipStream_t st = c->cur;
   unsigned long long* status = c->status + layer;
+  c->status_clean[layer] = 0;
   const size_t TH = (size_t)T * L.H, TK = (size_t)T * K;
   std::vector<int32_t> hids;
   const float* dx = x;
@@ -1399,6 +1488,7 @@ int dmh_shared_gate_forward(dmh_ctx* c, int layer, const float* x, int T, float*
   const bool dev = flags & DMH_F_DEVICE;
   hipStream_t st = c->cur;
   unsigned long long* status = c->status + layer;
+  c->status_clean[layer] = 0;
   const size_t TH = (size_t)T * L.H;
   const float* dx = x;
   float* ds = dev ? scores : nullptr;

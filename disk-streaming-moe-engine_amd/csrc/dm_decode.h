@@ -32,10 +32,14 @@ hipError_t decode_occupancy(const LayerDev& L, const DecodePlan& P, int* blocks_
 // nm.eps > 0: the router and experts see rmsnorm(x, nm.gamma, nm.eps) in the
 // order nm.seq selects (NormSpec).  cooperative: launch with
 // hipLaunchCooperativeKernel, which guarantees that every workgroup is
-// resident (slower; for devices shared by several contexts).
+// resident (slower; for devices shared by several contexts).  status_out
+// (may be NULL): P.grid words; each workgroup stores the status key there
+// as it ends, and the launch's key is their minimum, so a caller waiting for
+// the launch needs no separate read-back.
 hipError_t launch_moe_decode(const LayerDev& L, const DecodePlan& P, const float* x,
                              const float* residual, float* y, int32_t* ids, float* probs,
                              float* shg, const DecodeSync& S, unsigned long long* status, int token,
-                             hipStream_t st, const NormSpec& nm, bool cooperative);
+                             hipStream_t st, const NormSpec& nm, bool cooperative,
+                             unsigned long long* status_out);
 
 }  // namespace dm

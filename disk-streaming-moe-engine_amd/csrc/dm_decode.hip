@@ -570,6 +570,20 @@ __device__ __forceinline__ void finish_probs(int E, int K, SelState& st, bool re
   }
 }
 
+// The end of a workgroup when status_out is set: once this workgroup's own
+// error records (atomicMin on *status) have completed, thread 0 reads the
+// key and stores it to status_out[blockIdx.x].  Each entry is the minimum of
+// a set of records that holds at least the workgroup's own, so the minimum
+// over all entries is the launch's first-error key: no counter, no atomic
+// shared by the grid.  Launches without status_out pay nothing.
+__device__ __forceinline__ void end_workgroup(const unsigned long long* status,
+                                              unsigned long long* status_out) {
+  if (!status_out) return;
+  wait_vm();
+  __syncthreads();
+  if (threadIdx.x == 0) status_out[blockIdx.x] = ld_coh_u64(status);
+}
+
 // ---------------------------------------------------------------------------
 // NORM: 0 the block input is x; 1 / 2 it is rmsnorm(x, gamma, eps) with the
 // sum of squares as a 256-partial tree (1) or in element order (2, the
@@ -579,7 +593,7 @@ __global__ __launch_bounds__(kThreads) void k_moe_decode(
     LayerDev L, DecodePlan P, const float* __restrict__ x, const float* __restrict__ residual,
     float* __restrict__ y, int32_t* __restrict__ ids_out, float* __restrict__ probs_out,
     float* __restrict__ shg_out, DecodeSync S, unsigned long long* status, int token,
-    NormSpec nm) {
+    NormSpec nm, unsigned long long* status_out) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   float* xt = reinterpret_cast<float*>(smem + P.off_xt);
   uint4* xb2 = reinterpret_cast<uint4*>(smem + P.off_xb);
@@ -831,6 +845,7 @@ __global__ __launch_bounds__(kThreads) void k_moe_decode(
   if (!down_wg) {
     if (b == fin_wg && w == 0)
       finish_probs(E, K, st, true, token, status, ids_out, probs_out, shg_out);
+    end_workgroup(status, status_out);
     return;
   }
 
@@ -982,6 +997,7 @@ __global__ __launch_bounds__(kThreads) void k_moe_decode(
   }
   if (b == fin_wg && fin_wg == 0 && w == 0)
     finish_probs(E, K, st, true, token, status, ids_out, probs_out, shg_out);
+  end_workgroup(status, status_out);
 }
 
 static int ldh_log2_of(const LayerDev& L) {
@@ -1072,7 +1088,8 @@ hipError_t decode_occupancy(const LayerDev& L, const DecodePlan& P, int* blocks_
 hipError_t launch_moe_decode(const LayerDev& L, const DecodePlan& P, const float* x,
                              const float* residual, float* y, int32_t* ids, float* probs,
                              float* shg, const DecodeSync& S, unsigned long long* status, int token,
-                             hipStream_t st, const NormSpec& nm, bool cooperative) {
+                             hipStream_t st, const NormSpec& nm, bool cooperative,
+                             unsigned long long* status_out) {
   const int norm = norm_mode(nm);
   if (norm != 0 && !nm.gamma) return hipErrorInvalidValue;
   const void* fn = pick_kernel(L, norm);
@@ -1083,7 +1100,8 @@ hipError_t launch_moe_decode(const LayerDev& L, const DecodePlan& P, const float
   NormSpec nc = nm;
   const float* xc = x;
   const float* rc = residual;
-  void* args[] = {&Lc, &Pc, &xc, &rc, &y, &ids, &probs, &shg, &Sc, &status, &token, &nc};
+  void* args[] = {&Lc, &Pc,     &xc,    &rc, &y,         &ids, &probs,
+                  &shg, &Sc, &status, &token, &nc, &status_out};
   // Every workgroup waits for words other workgroups publish, so all of them
   // must be resident at once.  A cooperative launch guarantees it (or fails
   // at launch) but costs about 18 us more per launch than the plain one on

@@ -74,6 +74,9 @@ def _f32(a):
     return np.ascontiguousarray(a, dtype=np.float32)
 
 
+_F32, _I32 = np.dtype(np.float32), np.dtype(np.int32)
+
+
 class MoEBlock:
     """One device context: uploaded layers + the block entry points."""
 
@@ -85,6 +88,7 @@ class MoEBlock:
         self._h = h
         self.dims = {}
         self.gguf_dims = {}
+        self._ebuf = None  # error buffer reused by forward_into
 
     # -- lifetime --------------------------------------------------------
     def close(self):
@@ -247,6 +251,25 @@ class MoEBlock:
     def forward_arrays(self, layer_idx: int, x, seq_len: int, residual=None):
         """(y, ids, probs, shared_gate) as numpy arrays."""
         return self._forward(layer_idx, x, residual, seq_len)
+
+    def forward_into(self, layer_idx: int, x, seq_len: int, y, ids=None, probs=None, shg=None,
+                     residual=None) -> None:
+        """Host-pointer call into caller-owned outputs, as a compiled caller
+        makes it: x, residual, y, probs, shg C-contiguous float32, ids int32,
+        of the call's sizes (checked here); nothing is allocated per call."""
+        H, E, K, I, Ish = self.dims[layer_idx]
+        nh, nk = seq_len * H, seq_len * K
+        for a, dt, n in ((x, _F32, nh), (y, _F32, nh), (residual, _F32, nh), (ids, _I32, nk),
+                         (probs, _F32, nk), (shg, _F32, seq_len)):
+            if a is not None and (a.dtype != dt or a.size < n or not a.flags.c_contiguous):
+                raise ValueError(f"forward_into: arrays must be C-contiguous {np.dtype(dt)}"
+                                 f" with at least {n} elements")
+        e = self._ebuf
+        if e is None:
+            e = self._ebuf = errbuf()
+        check(self._lib.dmh_moe_forward(self._h, layer_idx, x.ctypes.data, _ptr(residual), seq_len,
+                                        y.ctypes.data, _ptr(ids), _ptr(probs), _ptr(shg), 0, e,
+                                        len(e)), e)
 
     def forward_device(self, layer_idx: int, x_ptr: int, seq_len: int, y_ptr: int,
                        ids_ptr: int | None = None, probs_ptr: int | None = None,

@@ -11,7 +11,10 @@
  * dequant strings, so a Mojo shim can `raise Error(String(err))` unchanged.
  *
  * Memory: by default every pointer is host memory and the call is
- * synchronous.  With DMH_F_DEVICE every activation/output pointer is device
+ * synchronous (a single token's block runs with x and the outputs in a
+ * page-locked block of the context that the kernel reads and writes itself:
+ * one launch and one synchronisation per call, no copy operations).  With
+ * DMH_F_DEVICE every activation/output pointer is device
  * memory, the call is ordered on the context's stream and returns at once;
  * errors found on the device are then sticky and reported by dmh_sync().
  *

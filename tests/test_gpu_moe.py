@@ -90,6 +90,83 @@ def test_nonfinite_activation_error_matches_oracle(block, oracle, toy):
     check_layer(block, oracle, toy, 0, x)
 
 
+def test_single_token_host_pointers_match_device_and_oracle(block, oracle, qwen):
+    """The single-token host-pointer call (the kernel reads x and the
+    residual from, and writes the outputs into, page-locked host memory, and
+    its last workgroup writes the status key there) gives the device-pointer
+    call's bits, with and without a residual, and the oracle's routing."""
+    import torch
+    dev = torch.device("cuda:0")
+    H, K = 2048, 8
+    x = synth.make_activations(np.random.default_rng(110), (4, H))
+    for t in range(4):
+        for res in (None, x[t]):
+            y = np.empty(H, np.float32)
+            ids = np.empty(K, np.int32)
+            probs = np.empty(K, np.float32)
+            shg = np.empty(1, np.float32)
+            block.forward_into(1, x[t], 1, y, ids, probs, shg, residual=res)
+            xd = torch.from_numpy(x[t].copy()).to(dev)
+            rd = None if res is None else torch.from_numpy(res.copy()).to(dev)
+            yd = torch.empty(H, dtype=torch.float32, device=dev)
+            idd = torch.empty(K, dtype=torch.int32, device=dev)
+            pd = torch.empty(K, dtype=torch.float32, device=dev)
+            sd = torch.empty(1, dtype=torch.float32, device=dev)
+            torch.cuda.synchronize()  # made on torch's stream, read on the library's
+            block.forward_device(1, xd.data_ptr(), 1, yd.data_ptr(), idd.data_ptr(),
+                                 pd.data_ptr(), sd.data_ptr(),
+                                 None if rd is None else rd.data_ptr())
+            block.sync()
+            assert np.array_equal(y.view(np.uint32), yd.cpu().numpy().view(np.uint32))
+            assert np.array_equal(ids, idd.cpu().numpy())
+            assert np.array_equal(probs.view(np.uint32), pd.cpu().numpy().view(np.uint32))
+            assert np.array_equal(shg.view(np.uint32), sd.cpu().numpy().view(np.uint32))
+            yo, ido, po, so = oracle.moe_layer_q4(qwen, x[t:t + 1], 1,
+                                                  residual=None if res is None else res[None])
+            assert np.array_equal(ids, ido.reshape(-1))
+            assert np.array_equal(probs.view(np.uint32), po.reshape(-1).view(np.uint32))
+    with pytest.raises(ValueError):
+        block.forward_into(1, x[0].astype(np.float64), 1, np.empty(H, np.float32))
+
+
+def test_single_token_host_errors_and_recovery(block, oracle, toy):
+    """Errors of single-token host-pointer calls (the status key comes back
+    from the kernel itself, or from the multi-kernel replay that names the
+    failing check) match the oracle's texts, and the call after an error,
+    and after a device-pointer call that failed, computes normally."""
+    import torch
+    x = synth.make_activations(np.random.default_rng(111), (1, 256))
+    good = block.forward_arrays(0, x, 1)
+    for scale in (1e15, 1e17, 1e19, 1e21, 3e37):
+        xs = (x * np.float32(scale)).astype(np.float32)
+        msgs = []
+        for call in (lambda: block.forward_arrays(0, xs, 1),
+                     lambda: oracle.moe_layer_q4(toy, xs, 1)):
+            try:
+                call()
+                msgs.append(None)
+            except (DismoenError, oracle.OracleError) as e:
+                msgs.append(str(e))
+        assert msgs[0] == msgs[1], (scale, msgs)
+        again = block.forward_arrays(0, x, 1)
+        for u, v in zip(good, again):
+            assert np.array_equal(np.asarray(u).view(np.uint8), np.asarray(v).view(np.uint8))
+    xn = x.copy()
+    xn[0, 3] = np.inf
+    with pytest.raises(DismoenError):
+        block.forward_arrays(0, xn, 1)
+    # a failing device-pointer call leaves a sticky error for sync(); the
+    # next host call resets the key first and reports only its own result
+    xd = torch.from_numpy(xn).to("cuda:0")
+    yd = torch.empty(256, dtype=torch.float32, device="cuda:0")
+    torch.cuda.synchronize()
+    block.forward_device(0, xd.data_ptr(), 1, yd.data_ptr())
+    again = block.forward_arrays(0, x, 1)
+    for u, v in zip(good, again):
+        assert np.array_equal(np.asarray(u).view(np.uint8), np.asarray(v).view(np.uint8))
+    block.sync()
+
+
 def test_upload_rejects_reserved_code_and_bad_scale(block):
     L = synth.make_layer(**synth.CONFIG_TOY, seed=7)
     L.d_packed = L.d_packed.copy()
