@@ -16,6 +16,8 @@
 
 #include "../../include/dismoen_hip.h"
 #include "dm_api_internal.h"
+#include <cstdlib>
+
 #include "dm_decode.h"
 #include "dm_gguf.h"
 #include "dm_grouped.h"
@@ -157,6 +159,7 @@ struct dmh_ctx {
   std::vector<const int32_t*> last_ids;
   std::vector<int> last_k;
   int num_cus = 0;
+  int xcd_nx = 0;  // XCDs when workgroup b runs on XCD b % xcd_nx (probed), else 0
   bool counted = false;           // counted in g_live_ctx
   float* ones = nullptr;          // [kNormMaxH] 1.0f: gamma of layers without one
   hipEvent_t switch_ev = nullptr;  // orders a stream switch after queued work
@@ -226,7 +229,12 @@ int decode_key(uint64_t key, int layer, int expert_id, int E, char* err, size_t 
       if (kind == kGkLogit) RJ(DMH_ERR_GATE, "GATE_ERROR", "non-finite shared gate logit", "shared");
       RJ(DMH_ERR_GATE, "GATE_ERROR", "shared gate score outside (0, 1)", "shared");
     case kPhSync:
-      RJ(DMH_ERR_HIP, "HIP_ERROR", "cross-workgroup handoff timed out in the decode kernel", "hip");
+      if (pos == 1)
+        RJ(DMH_ERR_HIP, "HIP_ERROR", "decode kernel workgroup ran on an unexpected XCD", "hip");
+      return set_err(err, errlen, DMH_ERR_HIP,
+                     "{\"error_type\":\"HIP_ERROR\",\"detail\":\"cross-workgroup handoff timed "
+                     "out in the decode kernel (wait %u)\",\"stage\":\"hip\",\"layer\":%d}",
+                     pos, layer);
     default:
       RJ(DMH_ERR_EXPERT, "EXPERT_ERROR", "non-finite value in aggregation", "aggregation");
   }
@@ -434,7 +442,7 @@ hipError_t run_block(dmh_ctx* ctx, Layer* Ly, int layer, const float* dx, const 
   if (fused) {
     for (int t = 0; t < T; ++t) {
       if (Ly->launches >= (1u << 24) && (e = reset_counters(ctx, Ly)) != hipSuccess) return e;
-      dm::DecodeSync S = dm::decode_sync_carve(L, Ly->sync);
+      dm::DecodeSync S = dm::decode_sync_carve(L, Ly->plan, Ly->sync);
       S.n = ++Ly->launches;
       e = dm::launch_moe_decode(L, Ly->plan, dx + (size_t)t * L.H,
                                 dres ? dres + (size_t)t * L.H : nullptr, dy + (size_t)t * L.H,
@@ -609,6 +617,12 @@ int dmh_create(int device, dmh_ctx** out, char* err, size_t errlen) {
   c->cur = c->own;
   hipDeviceProp_t prop;
   if (hipGetDeviceProperties(&prop, device) == hipSuccess) c->num_cus = prop.multiProcessorCount;
+  // where the dispatcher spreads a grid over the XCDs in rotation, the
+  // decode kernel can keep hand-offs inside one XCD (its XCD-sliced form);
+  // DMH_NO_XCD_SLICING set in the environment keeps the original form
+  if (std::getenv("DMH_NO_XCD_SLICING") == nullptr &&
+      dm::probe_xcd_map(c->num_cus, &c->xcd_nx) != hipSuccess)
+    c->xcd_nx = 0;
   c->last_ids.assign(kMaxLayers + 1, nullptr);
   c->last_k.assign(kMaxLayers + 1, 0);
   c->status_clean.assign(kMaxLayers, 0);
@@ -851,10 +865,10 @@ int dmh_upload_moe_layer(dmh_ctx* c, int layer, const dmh_moe_dims* d, const dmh
   }
   Ly->router_w_bad = fl & 1u;
   // fused decode kernel: all workgroups must be co-resident
-  Ly->plan = dm::make_decode_plan(Ly->dev, c->num_cus);
+  Ly->plan = dm::make_decode_plan(Ly->dev, c->num_cus, c->xcd_nx);
   {
     int per_cu = 0;
-    Ly->sync_bytes = dm::decode_sync_bytes(Ly->dev);
+    Ly->sync_bytes = dm::decode_sync_bytes(Ly->dev, Ly->plan);
     if (dm::decode_occupancy(Ly->dev, Ly->plan, &per_cu) == hipSuccess && c->num_cus > 0 &&
         per_cu * c->num_cus >= Ly->plan.grid && Ly->plan.lds_bytes <= 65536 && K + 1 <= 64 &&
         hipMalloc(&Ly->sync, Ly->sync_bytes) == hipSuccess &&

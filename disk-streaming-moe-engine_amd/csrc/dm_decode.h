@@ -15,19 +15,42 @@ struct DecodePlan {
   int off_xt, off_xb, off_zv, off_ev, off_sel, off_red, off_hb, off_yred;
   int n_router_wg;  // router workgroups (4 rows each)
   int ldh_log2;     // row stride of h: the power of two >= max(I, Ish)
+  // XCD-sliced form (xs != 0): the grid is spread over xs_nx XCDs in
+  // rotation, num_cus / xs_nx workgroups on each.  The
+  // expert work is cut into pairs (slot, 128-row slice of I); XCD x owns the
+  // pairs p = x, x + nx, ...: their gate/up tiles and the matching 128
+  // columns of their down matrices, so h never leaves the XCD.  Each XCD
+  // publishes one partial output vector; the partials are summed at the end.
+  int xs;
+  int xs_nx;    // XCDs
+  int xs_rpw;   // 16-row output tiles of the down partial per workgroup (1, 2, 4 or 8)
+  int xs_rpf;   // output rows per workgroup in the final sum
+  int xs_npx;   // most pairs on one XCD
+  int xs_nrw;   // waves per workgroup holding router rows (each XCD forms all logits)
+  int off_fin;  // LDS: the final sum's gathered partials
 };
 
 // Cross-workgroup state of one layer: tagged words carry the launch index in
 // their high half, so a consumer polls the data itself.
 struct DecodeSync {
   uint64_t* zt;  // [256*ceil(E/256) + 64] (tag, logit); entry E = shared-expert gate
+                 // (XCD-sliced form: one such vector per XCD)
   uint64_t* ht;  // [K+1][ldh] (tag, h), ldh = 2^ldh_log2 >= max(I, Ish)
+  uint64_t* hl;  // XCD-sliced form: [pairs][64] packed h words (pack_h2), XCD-local
+  uint64_t* pt;  // XCD-sliced form: [nx][H] (tag, partial output)
   unsigned n;    // launch index, >= 1 (the tag of this launch)
 };
-size_t decode_sync_bytes(const LayerDev& L);
-DecodeSync decode_sync_carve(const LayerDev& L, void* base);
+size_t decode_sync_bytes(const LayerDev& L, const DecodePlan& P);
+DecodeSync decode_sync_carve(const LayerDev& L, const DecodePlan& P, void* base);
 
-DecodePlan make_decode_plan(const LayerDev& L, int num_cus);
+// nx > 0: the XCD count, when the workgroups b of a num_cus grid were seen
+// on XCD (b + r) % nx for one r (probed on the device); then the XCD-sliced
+// form is planned
+// where the layer's shape allows it.  nx = 0: the original form only.
+DecodePlan make_decode_plan(const LayerDev& L, int num_cus, int nx = 0);
+// Launches one workgroup per CU that records the XCD it runs on; *nx = the
+// XCD count when the workgroups were placed on the XCDs in rotation, else 0.
+hipError_t probe_xcd_map(int num_cus, int* nx);
 hipError_t decode_occupancy(const LayerDev& L, const DecodePlan& P, int* blocks_per_cu);
 // nm.eps > 0: the router and experts see rmsnorm(x, nm.gamma, nm.eps) in the
 // order nm.seq selects (NormSpec).  cooperative: launch with

@@ -36,6 +36,8 @@
 // p (descending, lowest id first), as select_topk does (src/layers/topk.mojo:79-128).
 #include <hip/hip_runtime.h>
 
+#include <vector>
+
 #include "dm_decode.h"
 #include "dm_device.h"
 
@@ -129,7 +131,9 @@ __device__ __forceinline__ void gu_load(const ExpertView& gv, const ExpertView& 
   }
 }
 
-template <int GQW>
+// hdst: the tile's 8 hand-off words.  LOCAL: plain stores, read only by
+// workgroups on the same XCD (through its L2); otherwise agent-scope stores.
+template <int GQW, bool LOCAL = false>
 __device__ __forceinline__ void gu_compute(const ExpertView& gv, int rb, const uint4 (&wg)[GQW],
                                            const uint4 (&wu)[GQW], const uint2 (&sg)[GQW],
                                            const uint2 (&su)[GQW], const uint4* xb2, float* red,
@@ -184,7 +188,12 @@ __device__ __forceinline__ void gu_compute(const ExpertView& gv, int rb, const u
     // of pack_h2); the partner's value comes from the neighbouring lane
     const float hn = __builtin_bit_cast(
         float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, h), 0xB1, 0xF, 0xF, true));
-    if ((r & 1) == 0) st_coh_u64(hdst + (row >> 1), pack_h2(tag, h, hn));
+    if ((r & 1) == 0) {
+      if (LOCAL)
+        st_l2_u64(hdst + (r >> 1), pack_h2(tag, h, hn));
+      else
+        st_coh_u64(hdst + (r >> 1), pack_h2(tag, h, hn));
+    }
   }
   __syncthreads();
 }
@@ -196,6 +205,7 @@ __device__ __forceinline__ void gu_compute(const ExpertView& gv, int rb, const u
 // preloaded, the rest loaded here), the halving tree over the 16 chains, and
 // the (tag, logit) word stored to zt[e].  xt = x transposed: xt[l*xts + j] =
 // x[16j + l], row stride xts = H/16 + 4 floats.
+template <bool LOCAL = false>
 __device__ __forceinline__ void router_compute(const LayerDev& L, uint4 (&rw)[kRwMax], int e,
                                                const float* xt, uint64_t* zt, unsigned tag) {
   const int l = threadIdx.x & 15;
@@ -232,7 +242,12 @@ __device__ __forceinline__ void router_compute(const LayerDev& L, uint4 (&rw)[kR
   acc = acc + __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, acc), 0x104, 0xF, 0xF, true));
   acc = acc + __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, acc), 0x102, 0xF, 0xF, true));
   acc = acc + __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, acc), 0x101, 0xF, 0xF, true));
-  if (l == 0 && e <= L.E) st_coh_u64(zt + e, ((uint64_t)tag << 32) | f2u(acc));
+  if (l == 0 && e <= L.E) {
+    if (LOCAL)
+      st_l2_u64(zt + e, ((uint64_t)tag << 32) | f2u(acc));
+    else
+      st_coh_u64(zt + e, ((uint64_t)tag << 32) | f2u(acc));
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -766,7 +781,8 @@ __global__ __launch_bounds__(kThreads) void k_moe_decode(
   for (int t = sh_tile; t < nsh; t += nb) {
     if (t != sh_tile) gu_load<GQW, false>(sgv, suv, t, swg, swu, ssg, ssu);
     gu_compute<GQW>(sgv, t, swg, swu, ssg, ssu, xb2, red,
-                    S.ht + ((size_t)K << (P.ldh_log2 - 1)), n, kPhShared, token, status);
+                    S.ht + ((size_t)K << (P.ldh_log2 - 1)) + (size_t)t * (kTileRows / 2), n,
+                    kPhShared, token, status);
   }
 
   // ---- P2: routing on wave 0, softmax numerators on wave 7 (every
@@ -835,7 +851,8 @@ __global__ __launch_bounds__(kThreads) void k_moe_decode(
     }
     const int k = t / nrb;
     gu_compute<GQW>(gv, t % nrb, gwg, gwu, gsg, gsu, xb2, red,
-                    S.ht + ((size_t)k << (P.ldh_log2 - 1)), n, kPhExpert, token, status);
+                    S.ht + ((size_t)k << (P.ldh_log2 - 1)) + (size_t)(t % nrb) * (kTileRows / 2),
+                    n, kPhExpert, token, status);
   }
   if (K * nrb <= b) __syncthreads();
   // the ranks, the outputs in the reference's order and the top-k checks:
@@ -1000,6 +1017,471 @@ __global__ __launch_bounds__(kThreads) void k_moe_decode(
   end_workgroup(status, status_out);
 }
 
+// ---------------------------------------------------------------------------
+// The XCD-sliced form of the same launch.  The dispatcher places the
+// workgroups of a launch on the nx XCDs in rotation (b on XCD (b + r) % nx,
+// with r varying between launches), so every XCD holds nb / nx of them; each
+// workgroup reads its XCD from the hardware.  Hand-offs between workgroups
+// of one XCD go
+// through that XCD's L2 (plain stores, agent-scope polls: about a quarter of
+// the round trip of a hand-off through memory), so the expert work is cut
+// along XCDs:
+//
+//   pair p = (slot k, 128-row slice c of I) for the K routed slots, then the
+//   shared expert's slices.  XCD x owns the pairs p = x, x + nx, ...:
+//   - their gate/up tiles (8 tiles of 16 rows per pair, one per workgroup of
+//     the XCD at the Qwen3.6 shape), h published XCD-locally;
+//   - columns 128c..128c+127 of their down matrices for every output row:
+//     workgroup m of the XCD owns output tiles m*rpw..m*rpw+rpw-1, and its
+//     waves take the (tile, pair) A16 tiles, so each wave accumulates one
+//     output tile over its pairs.
+//   The XCD's partial output vector (its pairs' share of sum_k p_k W_k h_k +
+//   g W_sh h_sh) is published once; the final sum of the nx partials (XCD
+//   order) plus the residual forms y, rows spread over all workgroups.
+//
+// Every XCD forms all E+1 router logits itself (its workgroups share the
+// rows) and hands them on through its L2, so routing needs no hand-off
+// between XCDs; every workgroup then selects the same top-k as in the
+// original form.  The shared expert needs no routing: its h rows are formed
+// before the routing decision, two per workgroup, and handed to the XCDs
+// holding its slices through memory.
+constexpr int kXsR = 2;   // routed (output tile, pair) down tiles per wave, A operands in registers
+constexpr int kXsS = 1;   // shared-expert down tiles per wave
+constexpr int kXsHw = 2;     // XCD-local h words per thread
+constexpr int kXsRouterWaves = 4;  // waves holding router rows (4 rows each)
+
+__device__ __forceinline__ unsigned xcc_id() {
+  unsigned v;
+  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(v));
+  return v & 0xFu;
+}
+
+template <int GQW, int R, int NORM>
+__global__ __launch_bounds__(kThreads) void k_moe_decode_xs(
+    LayerDev L, DecodePlan P, const float* __restrict__ x, const float* __restrict__ residual,
+    float* __restrict__ y, int32_t* __restrict__ ids_out, float* __restrict__ probs_out,
+    float* __restrict__ shg_out, DecodeSync S, unsigned long long* status, int token,
+    NormSpec nm, unsigned long long* status_out) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  float* xt = reinterpret_cast<float*>(smem + P.off_xt);
+  uint4* xb2 = reinterpret_cast<uint4*>(smem + P.off_xb);
+  float* red = reinterpret_cast<float*>(smem + P.off_red);
+  float* yred = reinterpret_cast<float*>(smem + P.off_yred);
+  float* fin = reinterpret_cast<float*>(smem + P.off_fin);
+  uint16_t* hbh = reinterpret_cast<uint16_t*>(smem + P.off_hb);  // [npx][128] bf16 hi
+  uint16_t* hbl = hbh + (size_t)P.xs_npx * kQuadCols;             // [npx][128] bf16 lo
+  unsigned char* sel = smem + P.off_sel;
+  SelState st{reinterpret_cast<float*>(smem + P.off_zv), reinterpret_cast<float*>(smem + P.off_ev),
+              reinterpret_cast<int*>(sel), reinterpret_cast<int*>(sel + 128),
+              reinterpret_cast<float*>(sel + 256), reinterpret_cast<float*>(sel + 400),
+              reinterpret_cast<float*>(sel + 512)};
+
+  const int H = L.H, K = L.K, E = L.E;
+  const int b = blockIdx.x, nb = gridDim.x;
+  const int tid = threadIdx.x, w = wave_id(), lane = tid & 63;
+  const int q = lane >> 4, j = lane & 15;
+  const unsigned n = S.n;
+  // The dispatcher hands workgroups to the XCDs in rotation, starting at an
+  // XCD that varies from launch to launch: the XCD a workgroup runs on is
+  // read from the hardware, and b / nx numbers the workgroups of one XCD.
+  const int nx = P.xs_nx, nmx = nb / nx;
+  const int xc = (int)xcc_id(), m = b / nx;
+  const int nT = L.I / kQuadCols, KT = K * nT, NP = KT + L.Ish / kQuadCols;
+  const int npx = NP > xc ? (NP - xc + nx - 1) / nx : 0;   // pairs of this XCD
+  const int nrpx = KT > xc ? (KT - xc + nx - 1) / nx : 0;  // routed ones (they come first)
+  const int ntr = nrpx * 8;  // routed gate/up tiles of 16 rows on this XCD
+  const int rpw = P.xs_rpw, rb0 = m * rpw, nrt = H / kTileRows;
+  const int my_rt = max(0, min(rpw, nrt - rb0));  // output tiles of this workgroup
+  // this wave's down tiles: items jj = 0, 1, ...: output tile rb0 + ri of
+  // pair lp0 + lstep*jj (rpw divides the wave count, so ri is fixed)
+  const int ri = w & (rpw - 1), lp0 = w / rpw, lstep = kWaves / rpw;
+  const int nit = (ri < my_rt && lp0 < npx) ? (npx - lp0 + lstep - 1) / lstep : 0;
+  const int nit_r = (ri < my_rt && lp0 < nrpx) ? min(nit, (nrpx - lp0 + lstep - 1) / lstep) : 0;
+  const int nit_s = nit - nit_r;  // the plan keeps nit_r <= kXsR and nit_s <= kXsS
+  const int rbc = min(rb0 + ri, nrt - 1);  // a valid output tile for unused load slots
+  // router rows of this workgroup: every XCD forms all E+1 logits itself, so
+  // routing needs no hand-off between XCDs; wave w < nrw, lane group g owns
+  // row m + nmx*(4w + g)
+  const int nrw = P.xs_nrw;
+  const int zs = 256 * R + 64;            // logit words per XCD
+  uint64_t* zl = S.zt + (size_t)xc * zs;  // this XCD's logits
+  if (xc >= nx) {  // (never: the count was probed on this device)
+    if (tid == 0) record_err(status, err_key(kPhSync, 0, 0, 1, 0));
+    end_workgroup(status, status_out);
+    return;
+  }
+
+  // ---- entry: router rows, x, gamma -----------------------------------------
+  uint4 rw[kRwMax];
+  const int re = m + nmx * (4 * w + (lane >> 4));
+  if (w < nrw) {
+    const uint4* wp =
+        reinterpret_cast<const uint4*>(L.router + r16_index(H, min(re, E), lane & 15));
+#pragma unroll
+    for (int j8 = 0; j8 < kRwMax; ++j8) rw[j8] = wp[(size_t)min(j8, H / 128 - 1) * 16];
+  }
+  float4 xr[2][2];
+#pragma unroll
+  for (int ii = 0; ii < 2; ++ii) {
+    const int i = min(tid + kThreads * ii, H / 8 - 1);
+    xr[ii][0] = reinterpret_cast<const float4*>(x)[2 * i];
+    xr[ii][1] = reinterpret_cast<const float4*>(x)[2 * i + 1];
+  }
+  [[maybe_unused]] float4 gr[2][2];
+  if constexpr (NORM != 0) {
+#pragma unroll
+    for (int ii = 0; ii < 2; ++ii) {
+      const int i = min(tid + kThreads * ii, H / 8 - 1);
+      gr[ii][0] = reinterpret_cast<const float4*>(nm.gamma)[2 * i];
+      gr[ii][1] = reinterpret_cast<const float4*>(nm.gamma)[2 * i + 1];
+    }
+  }
+  const size_t matS = (size_t)L.Ish * H;
+  const ExpertView sgv = {L.sgu_nib, L.sgu_sc, L.Ish, H};
+  const ExpertView suv = {L.sgu_nib + matS / 2, L.sgu_sc + matS / kGroup, L.Ish, H};
+  const ExpertView sdv = {L.sd_nib, L.sd_sc, H, L.Ish};
+  // down A operands: routed tiles jr (pair lp0 + lstep*jr), then the shared
+  // tile (pair lp0 + lstep*nit_r).  Every load slot is always issued (an
+  // unused slot re-reads a valid tile): loads under a branch make the
+  // compiler wait for every load in flight before their first use.
+  uint4 dwr[kXsR], dws;
+  uint2 dsr[kXsR], dss;
+  bf16x8 Ar[kXsR][4], As[4];
+  // The shared expert's h: workgroup b forms rows 2b and 2b+1 (one hand-off
+  // word) as four wave-level dot products on waves 3..6 (gate row 0, gate
+  // row 1, up row 0, up row 1: none of them holds router rows or routes),
+  // lane = one 16-byte piece of the row (groups 4gq..4gq+3, columns
+  // 8q..8q+7 of each).  Spread over every workgroup it costs each one a few
+  // hundred instructions before routing.
+  const bool shw = w >= 3 && w <= 6;
+  const int sidx = w - 3;  // helper index on shw waves (others load a valid dummy)
+  const int nGQs = H / kQuadCols;
+  uint4 shc;
+  uint2 shs;
+  {
+    const int r = min(2 * b + (sidx & 1), L.Ish - 1);
+    const ExpertView& v = (sidx & 2) ? suv : sgv;
+    const int pc = min(lane, nGQs * 4 - 1);
+    shc = *reinterpret_cast<const uint4*>(
+        v.nib + a16_nib_offset(nGQs, r >> 4, pc >> 2, (pc & 3) * 16 + (r & 15)));
+    shs = *reinterpret_cast<const uint2*>(v.sc + a16_sc_offset(nGQs, r >> 4, pc >> 2, r & 15));
+  }
+  // the shared down operand (dequantized after routing)
+  load_chunk(sdv, rbc, nit_s > 0 ? xc + nx * (lp0 + lstep * nit_r) - KT : 0, lane, dws, dss);
+  float* shv = reinterpret_cast<float*>(sel + 448);  // [4] the four dot products
+
+  // ---- optional RMSNorm of x (as in the original form) ---------------------
+  if constexpr (NORM != 0) {
+    float* sq = reinterpret_cast<float*>(xb2);
+#pragma unroll
+    for (int ii = 0; ii < 2; ++ii) {
+      const int i = tid + kThreads * ii;
+      if (i < H / 8) {
+        const float4 a = xr[ii][0], c = xr[ii][1];
+        reinterpret_cast<float4*>(sq)[2 * i] = make_float4(a.x * a.x, a.y * a.y, a.z * a.z, a.w * a.w);
+        reinterpret_cast<float4*>(sq)[2 * i + 1] =
+            make_float4(c.x * c.x, c.y * c.y, c.z * c.z, c.w * c.w);
+      }
+    }
+    __syncthreads();
+    if constexpr (NORM == 1) {
+      if (tid < 256) {
+        float a = 0.0f;
+        for (int k = tid; k < H; k += 256) a = a + sq[k];
+        red[tid] = a;
+      }
+#pragma unroll
+      for (int wd = 128; wd >= 1; wd >>= 1) {
+        __syncthreads();
+        if (tid < wd) red[tid] = red[tid] + red[tid + wd];
+      }
+    } else {
+      if (tid == 0) {
+        const float4* s4 = reinterpret_cast<const float4*>(sq);
+        float a = 0.0f;
+        for (int k = 0; k < H / 4; k += 8) {
+          float4 v[8];
+#pragma unroll
+          for (int u = 0; u < 8; ++u) v[u] = s4[k + u];
+#pragma unroll
+          for (int u = 0; u < 8; ++u) {
+            a = a + v[u].x;
+            a = a + v[u].y;
+            a = a + v[u].z;
+            a = a + v[u].w;
+          }
+        }
+        red[0] = a;
+      }
+    }
+    __syncthreads();
+    const float denom = __builtin_sqrtf(red[0] / (float)H + nm.eps);
+    auto nrm = [&](float4 v, float4 g) {
+      return make_float4((v.x / denom) * g.x, (v.y / denom) * g.y, (v.z / denom) * g.z,
+                         (v.w / denom) * g.w);
+    };
+#pragma unroll
+    for (int ii = 0; ii < 2; ++ii) {
+      xr[ii][0] = nrm(xr[ii][0], gr[ii][0]);
+      xr[ii][1] = nrm(xr[ii][1], gr[ii][1]);
+    }
+    __syncthreads();
+  }
+
+  // ---- stage x --------------------------------------------------------------
+  {
+    bool bad = false;
+#pragma unroll
+    for (int ii = 0; ii < 2; ++ii) {
+      const int i = tid + kThreads * ii;
+      if (i < H / 8) {
+        const float f[8] = {xr[ii][0].x, xr[ii][0].y, xr[ii][0].z, xr[ii][0].w,
+                            xr[ii][1].x, xr[ii][1].y, xr[ii][1].z, xr[ii][1].w};
+#pragma unroll
+        for (int k2 = 0; k2 < 8; ++k2) bad |= !finite_f(f[k2]);
+        {
+          const int xts = H / 16 + 4;
+          float* dst = xt + (8 * (i & 1)) * xts + (i >> 1);
+#pragma unroll
+          for (int k2 = 0; k2 < 8; ++k2) dst[k2 * xts] = f[k2];
+        }
+        uint4 hi, lo;
+        split8(f, hi, lo);
+        xb2[2 * i + 0] = hi;
+        xb2[2 * i + 1] = lo;
+      }
+    }
+    if (bad && b == 0) record_err(status, err_key(kPhX, 0, 0, 0, 0));
+  }
+  __syncthreads();
+
+  // ---- router rows (XCD-local logits), the shared expert's rows ---------------
+  if (w < nrw) router_compute<true>(L, rw, re, xt, zl, n);
+  if (shw) {
+    float a = 0.0f;
+    if (lane < nGQs * 4) {
+      const int gq = lane >> 2, q = lane & 3;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const uint4 wv = __builtin_bit_cast(uint4, dequant8(word_of(shc, c), scale_of(shs, c)));
+        const int blk = (4 * gq + c) * 4 + q;  // x columns 32(4gq+c) + 8q .. +7
+        const uint4 xh = xb2[2 * blk], xl = xb2[2 * blk + 1];
+        const uint32_t wd[4] = {wv.x, wv.y, wv.z, wv.w};
+        const uint32_t hd[4] = {xh.x, xh.y, xh.z, xh.w};
+        const uint32_t ld[4] = {xl.x, xl.y, xl.z, xl.w};
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          a = __builtin_fmaf(bf16lo(wd[u]), bf16lo(hd[u]) + bf16lo(ld[u]), a);
+          a = __builtin_fmaf(bf16hi(wd[u]), bf16hi(hd[u]) + bf16hi(ld[u]), a);
+        }
+      }
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) a = a + __shfl_xor(a, off);
+    if (lane == 0) shv[sidx] = a;
+  }
+
+  // ---- routing (as in the original form) ------------------------------------
+  if (w == 0) {
+    const bool rok = route<R>(zl, n, E, K, st, b == 0, token, status);
+    if (lane == 0) st.misc[2] = rok ? 1.0f : 0.0f;
+  } else if (w == kNormWave) {
+    softmax_exp<R>(zl, n, E, st, b == 0, token, status);
+  }
+  __syncthreads();
+  const bool ok = st.misc[2] != 0.0f;
+  if (tid == 64 && 2 * b < L.Ish) {
+    // h of shared rows 2b, 2b+1 (swiglu_forward's gate, up, product checks)
+    const int r0 = 2 * b;
+    const float g0 = shv[0], g1 = shv[1], u0 = shv[2], u1 = shv[3];
+    const float h0 = dm_silu(g0) * u0, h1 = dm_silu(g1) * u1;
+    auto chk = [&](int r, float g, float u, float hh) {
+      if (!finite_f(g) || !finite_f(u) || !finite_f(hh))
+        record_err(status, err_key(kPhShared, token, 0, r,
+                                   !finite_f(g) ? kEkGate : !finite_f(u) ? kEkUp : kEkH));
+    };
+    chk(r0, g0, u0, h0);
+    chk(r0 + 1, g1, u1, h1);
+    // read by the XCD holding the shared slice r0 / 128 (any XCD): agent scope
+    st_coh_u64(S.hl + (size_t)(KT + r0 / kQuadCols) * 64 + (r0 % kQuadCols) / 2,
+               pack_h2(n, h0, h1));
+  }
+
+  // ---- routed loads: this workgroup's gate/up tile, this wave's down tiles ---
+  const size_t matI = (size_t)L.I * H, matD = (size_t)H * L.I;
+  auto task_views = [&](int tr, ExpertView& gv, ExpertView& uv) -> int {
+    const int p = xc + nx * (tr / 8);
+    const int e = __builtin_amdgcn_readfirstlane(st.ids[p / nT]);
+    gv = {L.gu_nib + (size_t)e * matI, L.gu_sc + (size_t)e * 2 * (matI / kGroup), L.I, H};
+    uv = {gv.nib + matI / 2, gv.sc + matI / kGroup, L.I, H};
+    return (p % nT) * 8 + tr % 8;
+  };
+  uint4 gwg[GQW], gwu[GQW];
+  uint2 gsg[GQW], gsu[GQW];
+  ExpertView gv = sgv, uv = suv;
+  int grb = 0;
+  if (ntr > 0) grb = task_views(min(m, ntr - 1), gv, uv);  // (a spare workgroup re-reads a tile)
+  gu_load<GQW, true>(gv, uv, grb, gwg, gwu, gsg, gsu);
+#pragma unroll
+  for (int jr = 0; jr < kXsR; ++jr) {
+    ExpertView dv = sdv;
+    int gq = 0;
+    if (nit_r > 0) {
+      const int p = xc + nx * (lp0 + lstep * min(jr, nit_r - 1));
+      const int e = __builtin_amdgcn_readfirstlane(st.ids[p / nT]);
+      dv = {L.d_nib + (size_t)e * (matD / 2), L.d_sc + (size_t)e * (matD / kGroup), H, L.I};
+      gq = p % nT;
+    }
+    load_chunk_nt(dv, rbc, gq, lane, dwr[jr], dsr[jr]);
+  }
+  // the shared down operand (its bytes landed before routing) while the
+  // routed loads are in flight
+#pragma unroll
+  for (int c = 0; c < 4; ++c) As[c] = dequant8(word_of(dws, c), scale_of(dss, c));
+  // the softmax sum and slot weights while the loads are in flight; the
+  // ranks and outputs in the reference's order in one workgroup
+  const int fin_wg = nb - 1;
+  if (w == kNormWave) {
+    softmax_sum<R>(E, K, st, b == 0, token, status);
+    if (b == fin_wg) finish_probs(E, K, st, true, token, status, ids_out, probs_out, shg_out);
+  }
+  for (int tr = m; tr < ntr; tr += nmx) {
+    if (tr != m) {
+      grb = task_views(tr, gv, uv);
+      gu_load<GQW, true>(gv, uv, grb, gwg, gwu, gsg, gsu);
+    }
+    const int p = xc + nx * (tr / 8);
+    gu_compute<GQW, true>(gv, grb, gwg, gwu, gsg, gsu, xb2, red,
+                          S.hl + (size_t)p * 64 + (tr % 8) * 8, n, kPhExpert, token, status);
+  }
+  if (m >= ntr) __syncthreads();  // publishes the slot weights
+
+  // ---- down: this XCD's pairs, columns of its slices, this workgroup's rows --
+  {
+    // h of every pair of the XCD, staged scaled by its slot's weight (p_k,
+    // or the shared gate) as bf16 hi / lo pairs.  The first poll goes out
+    // before the routed down tiles are dequantized (an XCD-local round trip
+    // is shorter than the dequantization), stale words are polled again.
+    const int nwords = my_rt > 0 ? npx * 64 : 0;
+    uint64_t hv[kXsHw];
+    uint32_t have = 0, all = 0;
+    if (nwords > 0) {
+#pragma unroll
+      for (int u = 0; u < kXsHw; ++u) {
+        const int wd = min(tid + kThreads * u, nwords - 1);
+        if (tid + kThreads * u < nwords) all |= 1u << u;
+        hv[u] = ld_coh_u64(S.hl + (size_t)(xc + nx * (wd >> 6)) * 64 + (wd & 63));
+      }
+    }
+    // (the empty asm statements order the dequantization after the poll and
+    // before the products: the compiler would otherwise move it)
+#pragma unroll
+    for (int jr = 0; jr < kXsR; ++jr)
+      asm volatile("" : "+v"(dwr[jr].x), "+v"(dwr[jr].y), "+v"(dwr[jr].z), "+v"(dwr[jr].w),
+                   "+v"(dsr[jr].x), "+v"(dsr[jr].y)::"memory");
+#pragma unroll
+    for (int jr = 0; jr < kXsR; ++jr)
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        Ar[jr][c] = dequant8(word_of(dwr[jr], c), scale_of(dsr[jr], c));
+#pragma unroll
+    for (int jr = 0; jr < kXsR; ++jr)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) asm volatile("" : "+v"(Ar[jr][c])::"memory");
+#pragma unroll
+    for (int c = 0; c < 4; ++c) asm volatile("" : "+v"(As[c])::"memory");
+    for (long spin = 0; spin < kSpinLimit && ok && have != all; ++spin) {
+#pragma unroll
+      for (int u = 0; u < kXsHw; ++u) {
+        if ((all >> u & 1u) && !(have >> u & 1u) && h2_current(hv[u], n)) {
+          const int wd = tid + kThreads * u, lp = wd >> 6, iw = wd & 63;
+          const int p = xc + nx * lp;
+          const float wgt = st.pw[p < KT ? p / nT : K];
+          uint16_t h0, l0, h1, l1;
+          split1(h2_v0(hv[u]) * wgt, h0, l0);
+          split1(h2_v1(hv[u]) * wgt, h1, l1);
+          const int at = lp * kQuadCols + 2 * iw;
+          *reinterpret_cast<uint32_t*>(hbh + at) = (uint32_t)h0 | ((uint32_t)h1 << 16);
+          *reinterpret_cast<uint32_t*>(hbl + at) = (uint32_t)l0 | ((uint32_t)l1 << 16);
+          have |= 1u << u;
+        }
+      }
+      if (have == all) break;
+      __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+      for (int u = 0; u < kXsHw; ++u) {
+        const int wd = min(tid + kThreads * u, nwords - 1);
+        hv[u] = ld_coh_u64(S.hl + (size_t)(xc + nx * (wd >> 6)) * 64 + (wd & 63));
+      }
+    }
+    if (!__syncthreads_and(have == all || !ok) && tid == 0)
+      record_err(status, err_key(kPhSync, 0, 0, 2, 0));
+  }
+  f32x4 acc0 = {0, 0, 0, 0}, acc1 = {0, 0, 0, 0};
+  auto tile_mfma = [&](const bf16x8 (&Aop)[4], int lp) {
+    const uint16_t* hs = hbh + lp * kQuadCols;
+    const uint16_t* ls = hbl + lp * kQuadCols;
+    bf16x8 B[4];
+#pragma unroll
+    for (int cc = 0; cc < 4; ++cc) B[cc] = ld_b2(hs, ls, cc * 4 + q, j);
+    acc0 = mfma16(Aop[0], B[0], acc0);
+    acc1 = mfma16(Aop[1], B[1], acc1);
+    acc0 = mfma16(Aop[2], B[2], acc0);
+    acc1 = mfma16(Aop[3], B[3], acc1);
+  };
+#pragma unroll
+  for (int jr = 0; jr < kXsR; ++jr)
+    if (jr < nit_r) tile_mfma(Ar[jr], lp0 + lstep * jr);
+  if (nit_s > 0) tile_mfma(As, lp0 + lstep * nit_r);
+  {
+    f32x4 acc;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) acc[r] = acc0[r] + acc1[r];
+    fold_cols(acc);
+    if (j == 0) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) yred[w * 16 + 4 * q + r] = acc[r];
+    }
+  }
+  __syncthreads();
+  if (npx > 0 && tid < kTileRows * my_rt) {
+    // the XCD's partial of rows (rb0 + tid/16)*16 + tid%16, waves in order
+    const int t2 = tid >> 4, r = tid & 15;
+    float s = 0.0f;
+    for (int w2 = t2; w2 < kWaves; w2 += rpw) s = s + yred[w2 * 16 + r];
+    st_coh_u64(S.pt + (size_t)xc * H + (rb0 + t2) * kTileRows + r, ((uint64_t)n << 32) | f2u(s));
+  }
+
+  // ---- the final sum: rows b*rpf .. b*rpf + rpf - 1 -------------------------
+  {
+    const int rpf = P.xs_rpf, nxa = min(nx, NP);
+    const int r0 = b * rpf, nfr = max(0, min(rpf, H - r0));
+    bool fok = true;
+    if (tid < nxa * rpf && tid % rpf < nfr) {
+      const int xx = tid / rpf, rr = tid % rpf;
+      const uint64_t* src = S.pt + (size_t)xx * H + r0 + rr;
+      uint64_t v = ld_coh_u64(src);
+      for (long spin = 0; spin < kSpinLimit && ok && (uint32_t)(v >> 32) != n; ++spin) {
+        __builtin_amdgcn_s_sleep(1);
+        v = ld_coh_u64(src);
+      }
+      fok = (uint32_t)(v >> 32) == n;
+      fin[xx * rpf + rr] = u2f((uint32_t)v);
+    }
+    if (!__syncthreads_and(fok || !ok) && tid == 0)
+      record_err(status, err_key(kPhSync, 0, 0, 3, 0));
+    if (tid < nfr) {
+      const int d = r0 + tid;
+      float total = 0.0f;
+      for (int xx = 0; xx < nxa; ++xx) total = total + fin[xx * rpf + tid];
+      if (residual) total = total + residual[d];
+      if (!finite_f(total)) record_err(status, err_key(kPhExpert, token, 0, 0, kEkRecheck));
+      y[d] = total;
+    }
+  }
+  end_workgroup(status, status_out);
+}
+
 static int ldh_log2_of(const LayerDev& L) {
   const int m = L.I > L.Ish ? L.I : L.Ish;
   int lg = 0;
@@ -1010,29 +1492,81 @@ static int ldh_log2_of(const LayerDev& L) {
 static int align16(int v) { return (v + 15) & ~15; }
 static size_t align256z(size_t v) { return (v + 255) & ~(size_t)255; }
 
-size_t decode_sync_bytes(const LayerDev& L) {
-  const size_t ldh = (size_t)1 << ldh_log2_of(L);
+static int xs_pairs(const LayerDev& L) { return L.K * (L.I / kQuadCols) + L.Ish / kQuadCols; }
+
+size_t decode_sync_bytes(const LayerDev& L, const DecodePlan& P) {
   const size_t R = (size_t)(L.E + 255) / 256;
-  return align256z((256 * R + 64) * 8) + align256z((size_t)(L.K + 1) * ldh * 8);
+  const size_t z = align256z((256 * R + 64) * 8 * (P.xs ? P.xs_nx : 1));
+  if (P.xs)
+    return z + align256z((size_t)xs_pairs(L) * 64 * 8) + align256z((size_t)P.xs_nx * L.H * 8);
+  const size_t ldh = (size_t)1 << ldh_log2_of(L);
+  return z + align256z((size_t)(L.K + 1) * ldh * 8);
 }
 
-DecodeSync decode_sync_carve(const LayerDev& L, void* base) {
+DecodeSync decode_sync_carve(const LayerDev& L, const DecodePlan& P, void* base) {
   const size_t R = (size_t)(L.E + 255) / 256;
   unsigned char* p = (unsigned char*)base;
   DecodeSync S{};
   S.zt = (uint64_t*)p;
-  p += align256z((256 * R + 64) * 8);
-  S.ht = (uint64_t*)p;
+  p += align256z((256 * R + 64) * 8 * (P.xs ? P.xs_nx : 1));
+  if (P.xs) {
+    S.hl = (uint64_t*)p;
+    p += align256z((size_t)xs_pairs(L) * 64 * 8);
+    S.pt = (uint64_t*)p;
+  } else {
+    S.ht = (uint64_t*)p;
+  }
   return S;
 }
 
-DecodePlan make_decode_plan(const LayerDev& L, int num_cus) {
+// The XCD-sliced form's geometry, when the layer's shape fits it.
+static bool plan_xs(const LayerDev& L, int num_cus, int nx, DecodePlan& P) {
+  if (nx <= 0 || num_cus < nx || num_cus % nx != 0) return false;
+  if (L.I % kQuadCols != 0 || L.Ish % kQuadCols != 0 || L.K > 32 || L.E > 2048) return false;
+  const int nmx = num_cus / nx, nrt = L.H / kTileRows;
+  const int need = (nrt + nmx - 1) / nmx;
+  int rpw = 1;
+  while (rpw < need) rpw *= 2;
+  if (rpw > kWaves) return false;
+  const int NP = xs_pairs(L), npx = (NP + nx - 1) / nx;
+  const int KT = L.K * (L.I / kQuadCols);
+  // down tiles per wave: routed ones in registers (kXsR), shared ones (kXsS)
+  for (int xc = 0; xc < nx; ++xc) {
+    const int np_x = NP > xc ? (NP - xc + nx - 1) / nx : 0;
+    const int nr_x = KT > xc ? (KT - xc + nx - 1) / nx : 0;
+    for (int w = 0; w < kWaves; ++w) {
+      const int lp0 = w / rpw, lstep = kWaves / rpw;
+      const int nit = lp0 < np_x ? (np_x - lp0 + lstep - 1) / lstep : 0;
+      const int nit_r = lp0 < nr_x ? (nr_x - lp0 + lstep - 1) / lstep : 0;
+      if (nit_r > kXsR || nit - nit_r > kXsS) return false;
+    }
+  }
+  const int rpf = (L.H + num_cus - 1) / num_cus;
+  const int nxa = nx < NP ? nx : NP;
+  if (npx * 64 > kXsHw * kThreads || rpf * nxa > kThreads) return false;
+  // the shared expert's rows: two per workgroup, one 16-byte piece per lane
+  if (L.Ish > 2 * num_cus || L.H / kQuadCols * 4 > 64) return false;
+  // every XCD forms all E+1 logits: rows per workgroup, four per wave
+  const int rows = (L.E + 1 + nmx - 1) / nmx;
+  const int nrw = (rows + 3) / 4;
+  if (nrw > kXsRouterWaves) return false;
+  P.xs_nrw = nrw;
+  P.xs = 1;
+  P.xs_nx = nx;
+  P.xs_rpw = rpw;
+  P.xs_rpf = rpf;
+  P.xs_npx = npx;
+  return true;
+}
+
+DecodePlan make_decode_plan(const LayerDev& L, int num_cus, int nx) {
   DecodePlan P{};
   P.ldh_log2 = ldh_log2_of(L);
   const int ldh = 1 << P.ldh_log2;
   P.n_router_wg = (L.E + 1 + kRouterRows - 1) / kRouterRows;
   const int R = (L.E + 255) / 256;
   const int slots = L.K + 1;
+  const bool xs = plan_xs(L, num_cus, nx, P);
   int off = 0;
   P.off_xt = off; off += align16(4 * 16 * (L.H / 16 + 4));  // 16 chains
   P.off_xb = off; off += align16(4 * L.H);
@@ -1040,40 +1574,52 @@ DecodePlan make_decode_plan(const LayerDev& L, int num_cus) {
   P.off_ev = off; off += align16(4 * 256 * R);
   P.off_sel = off; off += 768;
   P.off_red = off; off += align16(kWaves * 2 * 16 * 4);
-  P.off_hb = off; off += align16(slots * ldh * 4);
+  P.off_hb = off; off += align16(xs ? P.xs_npx * kQuadCols * 4 : slots * ldh * 4);
   P.off_yred = off; off += align16(kWaves * 16 * 4);
+  P.off_fin = off; off += align16(xs ? P.xs_rpf * (P.xs_nx < xs_pairs(L) ? P.xs_nx : xs_pairs(L)) * 4 : 0);
   P.lds_bytes = off;
   P.threads = kThreads;
-  P.grid = num_cus > L.H / kTileRows ? num_cus : L.H / kTileRows;
+  P.grid = xs ? num_cus : num_cus > L.H / kTileRows ? num_cus : L.H / kTileRows;
   return P;
 }
 
-template <int GQW, int NORM>
+template <int GQW, int NORM, bool XS>
 static const void* pick_r(int R) {
+  if (XS)
+    return R <= 1 ? (const void*)k_moe_decode_xs<GQW, 1, NORM>
+                  : (const void*)k_moe_decode_xs<GQW, 8, NORM>;
   return R <= 1 ? (const void*)k_moe_decode<GQW, 1, NORM>
                 : (const void*)k_moe_decode<GQW, 8, NORM>;
 }
 
-template <int NORM>
+template <int NORM, bool XS>
 static const void* pick_gqw(int gqw, int R) {
-  return gqw <= 2 ? pick_r<2, NORM>(R) : gqw <= 8 ? pick_r<8, NORM>(R) : nullptr;
+  return gqw <= 2 ? pick_r<2, NORM, XS>(R) : gqw <= 8 ? pick_r<8, NORM, XS>(R) : nullptr;
 }
 
 static int norm_mode(const NormSpec& nm) { return nm.eps > 0.0f ? (nm.seq ? 2 : 1) : 0; }
 
-static const void* pick_kernel(const LayerDev& L, int norm) {
+template <bool XS>
+static const void* pick_norm(int norm, int gqw, int R) {
+  return norm == 0 ? pick_gqw<0, XS>(gqw, R) : norm == 1 ? pick_gqw<1, XS>(gqw, R)
+                                                         : pick_gqw<2, XS>(gqw, R);
+}
+
+static const void* pick_kernel(const LayerDev& L, const DecodePlan& P, int norm) {
   const int gqw = (L.H / kQuadCols + kWaves - 1) / kWaves;
   const int R = (L.E + 255) / 256;
   const int ldh = 1 << ldh_log2_of(L);
-  if (R > 8 || L.K > 32 || ldh < 2 || (L.K + 1) * (ldh / 2) > kHw * kThreads) return nullptr;
-  return norm == 0 ? pick_gqw<0>(gqw, R) : norm == 1 ? pick_gqw<1>(gqw, R) : pick_gqw<2>(gqw, R);
+  if (R > 8 || L.K > 32 || ldh < 2) return nullptr;
+  if (P.xs) return pick_norm<true>(norm, gqw, R);
+  if ((L.K + 1) * (ldh / 2) > kHw * kThreads) return nullptr;
+  return pick_norm<false>(norm, gqw, R);
 }
 
 hipError_t decode_occupancy(const LayerDev& L, const DecodePlan& P, int* blocks_per_cu) {
   // every norm form must fit: the launch picks one per call
   int best = 1 << 30;
   for (int norm = 0; norm < 3; ++norm) {
-    const void* fn = pick_kernel(L, norm);
+    const void* fn = pick_kernel(L, P, norm);
     if (!fn) return hipErrorInvalidValue;
     int b = 0;
     const hipError_t e =
@@ -1092,7 +1638,7 @@ hipError_t launch_moe_decode(const LayerDev& L, const DecodePlan& P, const float
                              unsigned long long* status_out) {
   const int norm = norm_mode(nm);
   if (norm != 0 && !nm.gamma) return hipErrorInvalidValue;
-  const void* fn = pick_kernel(L, norm);
+  const void* fn = pick_kernel(L, P, norm);
   if (!fn) return hipErrorInvalidValue;
   LayerDev Lc = L;
   DecodePlan Pc = P;
@@ -1111,6 +1657,38 @@ hipError_t launch_moe_decode(const LayerDev& L, const DecodePlan& P, const float
   if (cooperative)
     return hipLaunchCooperativeKernel(fn, dim3(P.grid), dim3(P.threads), args, P.lds_bytes, st);
   return hipLaunchKernel(fn, dim3(P.grid), dim3(P.threads), args, P.lds_bytes, st);
+}
+
+}  // namespace dm
+
+namespace dm {
+
+__global__ void k_xcc_map(unsigned* out) {
+  if (threadIdx.x == 0) out[blockIdx.x] = xcc_id();
+}
+
+hipError_t probe_xcd_map(int num_cus, int* nx) {
+  *nx = 0;
+  if (num_cus <= 0) return hipSuccess;
+  unsigned* d = nullptr;
+  hipError_t e = hipMalloc(&d, sizeof(unsigned) * num_cus);
+  if (e != hipSuccess) return e;
+  std::vector<unsigned> h(num_cus, 0u);
+  hipLaunchKernelGGL(k_xcc_map, dim3(num_cus), dim3(64), 0, 0, d);
+  e = hipGetLastError();
+  if (e == hipSuccess) e = hipMemcpy(h.data(), d, sizeof(unsigned) * num_cus, hipMemcpyDeviceToHost);
+  (void)hipFree(d);
+  if (e != hipSuccess) return e;
+  unsigned mx = 0;
+  for (unsigned v : h) mx = v > mx ? v : mx;
+  const int n = (int)mx + 1;
+  if (num_cus % n != 0) return hipSuccess;
+  // a rotation: workgroup b on XCD (b + r) % n for one r
+  const unsigned r = (h[0] + (unsigned)n) % (unsigned)n;
+  for (int b = 0; b < num_cus; ++b)
+    if (h[b] != (unsigned)((b + (int)r) % n)) return hipSuccess;  // no sliced form
+  *nx = n;
+  return hipSuccess;
 }
 
 }  // namespace dm

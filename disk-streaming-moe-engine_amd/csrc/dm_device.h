@@ -164,6 +164,14 @@ __device__ __forceinline__ uint64_t ld_coh_u64(const void* p) {
 __device__ __forceinline__ void st_coh_u64(void* p, uint64_t v) {
   __hip_atomic_store(reinterpret_cast<uint64_t*>(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+// A plain store (no cache-control bits): it lands in the L2 of the XCD the
+// workgroup runs on, where agent-scope loads (ld_coh_u64) of workgroups on
+// the same XCD see it; workgroups on other XCDs do not see it before the
+// kernel ends.  For hand-offs whose producer and consumers share an XCD.
+__device__ __forceinline__ void st_l2_u64(void* p, uint64_t v) {
+  __hip_atomic_store(reinterpret_cast<uint64_t*>(p), v, __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_WAVEFRONT);
+}
 __device__ __forceinline__ void wait_stores() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 // Every vector memory operation of this wave (loads and stores) complete.
 __device__ __forceinline__ void wait_vm() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
