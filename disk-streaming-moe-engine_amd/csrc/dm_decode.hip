@@ -212,7 +212,37 @@ __device__ __forceinline__ void router_compute(const LayerDev& L, uint4 (&rw)[kR
   const int nj8 = L.H / 128;
   const float4* xr = reinterpret_cast<const float4*>(xt + l * (L.H / 16 + 4));
   float acc = 0.0f;
-  if (e <= L.E) {
+  if (e <= L.E && nj8 == kRwMax) {
+    // every chunk preloaded (H = 2048): one straight-line block, so the x
+    // reads from LDS are issued ahead of the chain instead of one chunk at a
+    // time behind a branch
+    // x of four chunks in flight ahead of the chain (the compiler otherwise
+    // reads each chunk just before its products and waits for it)
+    constexpr int kAhead = 4;
+    float4 xq[kAhead][2];
+#pragma unroll
+    for (int t = 0; t < kAhead; ++t) {
+      xq[t][0] = xr[2 * t];
+      xq[t][1] = xr[2 * t + 1];
+    }
+#pragma unroll
+    for (int j8 = 0; j8 < kRwMax; ++j8) {
+      const float4 xa = xq[j8 % kAhead][0], xc = xq[j8 % kAhead][1];
+      if (j8 + kAhead < kRwMax) {
+        xq[j8 % kAhead][0] = xr[2 * (j8 + kAhead)];
+        xq[j8 % kAhead][1] = xr[2 * (j8 + kAhead) + 1];
+      }
+      const uint4 ww = rw[j8];
+      acc = acc + xa.x * bf16lo(ww.x);
+      acc = acc + xa.y * bf16hi(ww.x);
+      acc = acc + xa.z * bf16lo(ww.y);
+      acc = acc + xa.w * bf16hi(ww.y);
+      acc = acc + xc.x * bf16lo(ww.z);
+      acc = acc + xc.y * bf16hi(ww.z);
+      acc = acc + xc.z * bf16lo(ww.w);
+      acc = acc + xc.w * bf16hi(ww.w);
+    }
+  } else if (e <= L.E) {
     const uint4* wp = reinterpret_cast<const uint4*>(L.router + r16_index(L.H, e, l));
     for (int base = 0; base < nj8; base += kRwMax) {
       if (base > 0) {
@@ -1148,23 +1178,26 @@ __global__ __launch_bounds__(kThreads) void k_moe_decode_xs(
   uint2 dsr[kXsR], dss;
   bf16x8 Ar[kXsR][4], As[4];
   // The shared expert's h: workgroup b forms rows 2b and 2b+1 (one hand-off
-  // word) as four wave-level dot products on waves 3..6 (gate row 0, gate
-  // row 1, up row 0, up row 1: none of them holds router rows or routes),
-  // lane = one 16-byte piece of the row (groups 4gq..4gq+3, columns
-  // 8q..8q+7 of each).  Spread over every workgroup it costs each one a few
-  // hundred instructions before routing.
-  const bool shw = w >= 3 && w <= 6;
-  const int sidx = w - 3;  // helper index on shw waves (others load a valid dummy)
+  // word) as wave-level dot products, wave 2 row 2b and wave 3 row 2b+1 (gate
+  // and up each; at the Qwen3.6 shape neither holds router rows outside
+  // workgroup 0), lane = one 16-byte piece of the row (groups 4gq..4gq+3,
+  // columns 8q..8q+7 of each).  Spread over every workgroup it costs each
+  // one a few hundred instructions before routing, on SIMDs the router
+  // chains do not use.
+  const bool shw = w == 2 || w == 3;
   const int nGQs = H / kQuadCols;
-  uint4 shc;
-  uint2 shs;
-  {
-    const int r = min(2 * b + (sidx & 1), L.Ish - 1);
-    const ExpertView& v = (sidx & 2) ? suv : sgv;
+  uint4 shc[2];
+  uint2 shs[2];
+  if (shw) {
+    const int r = min(2 * b + (w - 2), L.Ish - 1);
     const int pc = min(lane, nGQs * 4 - 1);
-    shc = *reinterpret_cast<const uint4*>(
-        v.nib + a16_nib_offset(nGQs, r >> 4, pc >> 2, (pc & 3) * 16 + (r & 15)));
-    shs = *reinterpret_cast<const uint2*>(v.sc + a16_sc_offset(nGQs, r >> 4, pc >> 2, r & 15));
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+      const ExpertView& v = mt ? suv : sgv;
+      shc[mt] = *reinterpret_cast<const uint4*>(
+          v.nib + a16_nib_offset(nGQs, r >> 4, pc >> 2, (pc & 3) * 16 + (r & 15)));
+      shs[mt] = *reinterpret_cast<const uint2*>(v.sc + a16_sc_offset(nGQs, r >> 4, pc >> 2, r & 15));
+    }
   }
   // the shared down operand (dequantized after routing)
   load_chunk(sdv, rbc, nit_s > 0 ? xc + nx * (lp0 + lstep * nit_r) - KT : 0, lane, dws, dss);
@@ -1258,27 +1291,37 @@ __global__ __launch_bounds__(kThreads) void k_moe_decode_xs(
   // ---- router rows (XCD-local logits), the shared expert's rows ---------------
   if (w < nrw) router_compute<true>(L, rw, re, xt, zl, n);
   if (shw) {
-    float a = 0.0f;
+    float a[2] = {0.0f, 0.0f};  // gate, up
     if (lane < nGQs * 4) {
       const int gq = lane >> 2, q = lane & 3;
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
-        const uint4 wv = __builtin_bit_cast(uint4, dequant8(word_of(shc, c), scale_of(shs, c)));
         const int blk = (4 * gq + c) * 4 + q;  // x columns 32(4gq+c) + 8q .. +7
         const uint4 xh = xb2[2 * blk], xl = xb2[2 * blk + 1];
-        const uint32_t wd[4] = {wv.x, wv.y, wv.z, wv.w};
         const uint32_t hd[4] = {xh.x, xh.y, xh.z, xh.w};
         const uint32_t ld[4] = {xl.x, xl.y, xl.z, xl.w};
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          a = __builtin_fmaf(bf16lo(wd[u]), bf16lo(hd[u]) + bf16lo(ld[u]), a);
-          a = __builtin_fmaf(bf16hi(wd[u]), bf16hi(hd[u]) + bf16hi(ld[u]), a);
+        for (int mt = 0; mt < 2; ++mt) {
+          const uint4 wv =
+              __builtin_bit_cast(uint4, dequant8(word_of(shc[mt], c), scale_of(shs[mt], c)));
+          const uint32_t wd[4] = {wv.x, wv.y, wv.z, wv.w};
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            a[mt] = __builtin_fmaf(bf16lo(wd[u]), bf16lo(hd[u]) + bf16lo(ld[u]), a[mt]);
+            a[mt] = __builtin_fmaf(bf16hi(wd[u]), bf16hi(hd[u]) + bf16hi(ld[u]), a[mt]);
+          }
         }
       }
     }
 #pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) a = a + __shfl_xor(a, off);
-    if (lane == 0) shv[sidx] = a;
+    for (int off = 32; off >= 1; off >>= 1) {
+      a[0] = a[0] + __shfl_xor(a[0], off);
+      a[1] = a[1] + __shfl_xor(a[1], off);
+    }
+    if (lane == 0) {
+      shv[w - 2] = a[0];      // gate of row 2b + (w - 2)
+      shv[2 + w - 2] = a[1];  // up
+    }
   }
 
   // ---- routing (as in the original form) ------------------------------------
@@ -1316,12 +1359,8 @@ __global__ __launch_bounds__(kThreads) void k_moe_decode_xs(
     uv = {gv.nib + matI / 2, gv.sc + matI / kGroup, L.I, H};
     return (p % nT) * 8 + tr % 8;
   };
-  uint4 gwg[GQW], gwu[GQW];
-  uint2 gsg[GQW], gsu[GQW];
-  ExpertView gv = sgv, uv = suv;
-  int grb = 0;
-  if (ntr > 0) grb = task_views(min(m, ntr - 1), gv, uv);  // (a spare workgroup re-reads a tile)
-  gu_load<GQW, true>(gv, uv, grb, gwg, gwu, gsg, gsu);
+  // this wave's routed down tiles first: they are few bytes, land first and
+  // are dequantized while the gate/up bytes are still in flight
 #pragma unroll
   for (int jr = 0; jr < kXsR; ++jr) {
     ExpertView dv = sdv;
@@ -1334,6 +1373,13 @@ __global__ __launch_bounds__(kThreads) void k_moe_decode_xs(
     }
     load_chunk_nt(dv, rbc, gq, lane, dwr[jr], dsr[jr]);
   }
+  uint4 gwg[GQW], gwu[GQW];
+  uint2 gsg[GQW], gsu[GQW];
+  ExpertView gv = sgv, uv = suv;
+  int grb = 0;
+  if (ntr > 0) grb = task_views(min(m, ntr - 1), gv, uv);  // (a spare workgroup re-reads a tile)
+  gu_load<GQW, true>(gv, uv, grb, gwg, gwu, gsg, gsu);
+
   // the shared down operand (its bytes landed before routing) while the
   // routed loads are in flight
 #pragma unroll
@@ -1345,6 +1391,18 @@ __global__ __launch_bounds__(kThreads) void k_moe_decode_xs(
     softmax_sum<R>(E, K, st, b == 0, token, status);
     if (b == fin_wg) finish_probs(E, K, st, true, token, status, ids_out, probs_out, shg_out);
   }
+#pragma unroll
+  for (int jr = 0; jr < kXsR; ++jr)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) Ar[jr][c] = dequant8(word_of(dwr[jr], c), scale_of(dsr[jr], c));
+  // (the empty asm statements keep the dequantization here, ahead of the
+  // gate/up tile; the compiler would otherwise sink it to the products)
+#pragma unroll
+  for (int jr = 0; jr < kXsR; ++jr)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) asm volatile("" : "+v"(Ar[jr][c])::"memory");
+#pragma unroll
+  for (int c = 0; c < 4; ++c) asm volatile("" : "+v"(As[c])::"memory");
   for (int tr = m; tr < ntr; tr += nmx) {
     if (tr != m) {
       grb = task_views(tr, gv, uv);
@@ -1359,9 +1417,8 @@ __global__ __launch_bounds__(kThreads) void k_moe_decode_xs(
   // ---- down: this XCD's pairs, columns of its slices, this workgroup's rows --
   {
     // h of every pair of the XCD, staged scaled by its slot's weight (p_k,
-    // or the shared gate) as bf16 hi / lo pairs.  The first poll goes out
-    // before the routed down tiles are dequantized (an XCD-local round trip
-    // is shorter than the dequantization), stale words are polled again.
+    // or the shared gate) as bf16 hi / lo pairs; stale words are polled
+    // again.
     const int nwords = my_rt > 0 ? npx * 64 : 0;
     uint64_t hv[kXsHw];
     uint32_t have = 0, all = 0;
@@ -1373,23 +1430,6 @@ __global__ __launch_bounds__(kThreads) void k_moe_decode_xs(
         hv[u] = ld_coh_u64(S.hl + (size_t)(xc + nx * (wd >> 6)) * 64 + (wd & 63));
       }
     }
-    // (the empty asm statements order the dequantization after the poll and
-    // before the products: the compiler would otherwise move it)
-#pragma unroll
-    for (int jr = 0; jr < kXsR; ++jr)
-      asm volatile("" : "+v"(dwr[jr].x), "+v"(dwr[jr].y), "+v"(dwr[jr].z), "+v"(dwr[jr].w),
-                   "+v"(dsr[jr].x), "+v"(dsr[jr].y)::"memory");
-#pragma unroll
-    for (int jr = 0; jr < kXsR; ++jr)
-#pragma unroll
-      for (int c = 0; c < 4; ++c)
-        Ar[jr][c] = dequant8(word_of(dwr[jr], c), scale_of(dsr[jr], c));
-#pragma unroll
-    for (int jr = 0; jr < kXsR; ++jr)
-#pragma unroll
-      for (int c = 0; c < 4; ++c) asm volatile("" : "+v"(Ar[jr][c])::"memory");
-#pragma unroll
-    for (int c = 0; c < 4; ++c) asm volatile("" : "+v"(As[c])::"memory");
     for (long spin = 0; spin < kSpinLimit && ok && have != all; ++spin) {
 #pragma unroll
       for (int u = 0; u < kXsHw; ++u) {
