@@ -325,6 +325,38 @@ __device__ __forceinline__ void select_keys(const uint32_t (&key)[NK], int round
   }
 }
 
+// One step of a wave-wide top-8 reduction: every lane holds 8 keys in
+// descending order; it takes the 8 keys of the lane the DPP control names
+// (in reverse order), keeps the elementwise maxima (a bitonic sequence that
+// holds the 8 largest of the 16) and sorts them with a bitonic network.
+// Lanes without a source lane take zeros (no keys).  The shift and row
+// broadcast controls of the usual reduction leave the top 8 of all lanes in
+// lane 63.
+template <int CTRL, int RM>
+__device__ __forceinline__ void top8_step(uint32_t (&a)[8]) {
+  uint32_t c[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const uint32_t bv = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)a[7 - i], CTRL, RM, 0xF, false);
+    c[i] = a[i] > bv ? a[i] : bv;
+  }
+  auto cx = [](uint32_t& p, uint32_t& q) {  // p >= q afterwards
+    const uint32_t hi = p > q ? p : q, lo = p > q ? q : p;
+    p = hi;
+    q = lo;
+  };
+#pragma unroll
+  for (int i = 0; i < 4; ++i) cx(c[i], c[i + 4]);
+  cx(c[0], c[2]);
+  cx(c[1], c[3]);
+  cx(c[4], c[6]);
+  cx(c[5], c[7]);
+#pragma unroll
+  for (int i = 0; i < 8; i += 2) cx(c[i], c[i + 1]);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) a[i] = c[i];
+}
+
 template <int R>
 __device__ __forceinline__ void issue_logits(const uint64_t* zt, int E, bool gate,
                                              uint64_t (&v)[4 * R + 1]) {
@@ -390,32 +422,33 @@ __device__ __forceinline__ bool route(const uint64_t* zt, unsigned tag, int E, i
   float z[NK];
   const bool ok = poll_logits<R>(zt, tag, E, z, nullptr);
   if (!ok && lane == 0) record_err(status, err_key(kPhSync, 0, 0, 0, 0));
+  // keys, branch-free (entries past E: key 0, never selected); the
+  // non-finite logits are recorded on a separate, rarely taken path
   uint32_t fk[NK], key[NK];
+  bool bad = false;
 #pragma unroll
   for (int i = 0; i < NK; ++i) {
     const int e = lane + 64 * i;
-    fk[i] = 0;
-    key[i] = 0;
-    if (e < E) {
-      st.zv[e] = z[i];
-      if (record && !finite_f(z[i])) record_err(status, err_key(kPhLogit, token, 0, e, 0));
-      fk[i] = f2key(z[i]);
-      key[i] = ((fk[i] >> IDB) << IDB) | (IDM - (uint32_t)e);
+    const bool in = e < E;
+    st.zv[min(e, 256 * R - 1)] = in ? z[i] : 0.0f;
+    bad |= in && !finite_f(z[i]);
+    fk[i] = in ? f2key(z[i]) : 0u;
+    key[i] = in ? (((fk[i] >> IDB) << IDB) | (IDM - (uint32_t)e)) : 0u;
+  }
+  if (record && __builtin_amdgcn_ballot_w64(bad) != 0) {
+#pragma unroll
+    for (int i = 0; i < NK; ++i) {
+      const int e = lane + 64 * i;
+      if (e < E && !finite_f(z[i])) record_err(status, err_key(kPhLogit, token, 0, e, 0));
     }
   }
-  // the exact maximum logit (independent of the selection below)
-  uint32_t lmax = 0;
-#pragma unroll
-  for (int i = 0; i < NK; ++i)
-    if (lane + 64 * i < E) lmax = fk[i] > lmax ? fk[i] : lmax;
-  const float m = key2f(wave_max_u32(lmax));
   // K rounds: the largest remaining key; its low bits name the expert.  Lane
   // `it` keeps the id of round it (no branches inside the loop).  With four
   // keys a lane sorts them once, so a round is one wave-wide max of the lane
   // heads and a shift in the winning lane.  A last max gives the largest
   // unselected key.
   int myid = 0;
-  uint32_t gm = 0, gu = 0;
+  uint32_t gm = 0, gu = 0, gtop = 0;
   if constexpr (NK == 4) {
     uint32_t k0 = key[0], k1 = key[1], k2 = key[2], k3 = key[3];
     auto cx = [](uint32_t& a, uint32_t& b) {  // a >= b afterwards
@@ -428,17 +461,46 @@ __device__ __forceinline__ bool route(const uint64_t* zt, unsigned tag, int E, i
     cx(k0, k2);
     cx(k1, k3);
     cx(k1, k2);
+    if (K <= 8) {
+      // one wave-wide top-8 reduction (bitonic merges along the DPP
+      // reduction tree) instead of K rounds of wave maxima
+      uint32_t a[8] = {k0, k1, k2, k3, 0u, 0u, 0u, 0u};
+      top8_step<0x111, 0xF>(a);
+      top8_step<0x112, 0xF>(a);
+      top8_step<0x114, 0xF>(a);
+      top8_step<0x118, 0xF>(a);
+      top8_step<0x142, 0xA>(a);
+      top8_step<0x143, 0xC>(a);
+      uint32_t T[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) T[i] = __builtin_amdgcn_readlane(a[i], 63);
+      gtop = T[0];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        if (i == K - 1) gm = T[i];
+        if (i == K && K < E) gu = T[i];
+        myid = lane == i ? (int)(IDM - (T[i] & IDM)) : myid;
+      }
+      if (K == 8 && K < E) {
+        // the largest key outside the top 8: each lane's first key below T7
+        const uint32_t t7 = T[7];
+        const uint32_t c = k0 < t7 ? k0 : k1 < t7 ? k1 : k2 < t7 ? k2 : k3 < t7 ? k3 : 0u;
+        gu = wave_max_u32(c);
+      }
+    } else {
 #pragma unroll 8
-    for (int it = 0; it < K; ++it) {
-      gm = wave_max_u32(k0);
-      const bool win = k0 == gm;
-      k0 = win ? k1 : k0;
-      k1 = win ? k2 : k1;
-      k2 = win ? k3 : k2;
-      k3 = win ? 0u : k3;
-      myid = lane == it ? (int)(IDM - (gm & IDM)) : myid;
+      for (int it = 0; it < K; ++it) {
+        gm = wave_max_u32(k0);
+        gtop = it == 0 ? gm : gtop;
+        const bool win = k0 == gm;
+        k0 = win ? k1 : k0;
+        k1 = win ? k2 : k1;
+        k2 = win ? k3 : k2;
+        k3 = win ? 0u : k3;
+        myid = lane == it ? (int)(IDM - (gm & IDM)) : myid;
+      }
+      if (K < E) gu = wave_max_u32(k0);
     }
-    if (K < E) gu = wave_max_u32(k0);
   } else {
     uint32_t kw[NK];
 #pragma unroll
@@ -449,6 +511,7 @@ __device__ __forceinline__ bool route(const uint64_t* zt, unsigned tag, int E, i
 #pragma unroll
       for (int i = 0; i < NK; ++i) km = kw[i] > km ? kw[i] : km;
       gm = wave_max_u32(km);
+      gtop = it == 0 ? gm : gtop;
 #pragma unroll
       for (int i = 0; i < NK; ++i) kw[i] = kw[i] == gm ? 0u : kw[i];
       myid = lane == it ? (int)(IDM - (gm & IDM)) : myid;
@@ -466,14 +529,32 @@ __device__ __forceinline__ bool route(const uint64_t* zt, unsigned tag, int E, i
   // most zu (the largest unselected key with its id bits set), so
   // e(zs) > e(zu) (1 + 2^-20) implies the same for the exact boundary logits
   // (exp is monotone to within an ulp, far inside the 2^-20 margin).
-  if (record && lane == 0 && !finite_f(m)) record_err(status, err_key(kPhSoftmax, token, 0, 0, 0));
+  // Fast sufficient test first: with zmax an upper bound of the largest
+  // logit (the top key with its id bits set), the rounded arguments zs - m
+  // and zu - m differ by at least (zs - zu) - 2^-23 (zmax - zu), and the
+  // computed exponentials (within 2^-21 relative of exp) keep their order by
+  // more than 2^-20 once that difference exceeds 2^-18; so when
+  // zs - zu > 2^-17 + 2^-21 (zmax - zu) and zmax - zs < 64 (no underflow of
+  // e(zs)) the exact maximum and both exponentials are not needed.  Any
+  // non-finite bound fails the test and takes the full check.
   bool unsafe = false;
   if (K < E) {
-    const float zs = key2f(gm & ~IDM), zu = key2f(gu | IDM);
-    const float ek = dm_expf(zs - m), en = dm_expf(zu - m);
-    unsafe = !(ek > en + en * 0x1p-20f);
+    const float zs = key2f(gm & ~IDM), zu = key2f(gu | IDM), zmax = key2f(gtop | IDM);
+    const bool clear = (zs - zu) > 0x1p-17f + (zmax - zu) * 0x1p-21f && (zmax - zs) < 64.0f;
+    if (!clear) {
+      uint32_t lmax = 0;
+#pragma unroll
+      for (int i = 0; i < NK; ++i) lmax = fk[i] > lmax ? fk[i] : lmax;
+      const float m = key2f(wave_max_u32(lmax));
+      const float ek = dm_expf(zs - m), en = dm_expf(zu - m);
+      unsafe = !(ek > en + en * 0x1p-20f);
+    }
   }
   if (unsafe) {  // select on the exact probabilities
+    uint32_t lmax = 0;
+#pragma unroll
+    for (int i = 0; i < NK; ++i) lmax = fk[i] > lmax ? fk[i] : lmax;
+    const float m = key2f(wave_max_u32(lmax));
     float ev[NK];
 #pragma unroll
     for (int i = 0; i < NK; ++i) {
@@ -511,6 +592,7 @@ __device__ __forceinline__ void softmax_exp(const uint64_t* zt, unsigned tag, in
       lm = k > lm ? k : lm;
     }
   const float m = key2f(wave_max_u32(lm));
+  if (record && lane == 0 && !finite_f(m)) record_err(status, err_key(kPhSoftmax, token, 0, 0, 0));
 #pragma unroll
   for (int i = 0; i < NK; ++i) {
     const int e = lane + 64 * i;
