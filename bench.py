@@ -64,6 +64,9 @@ def parse():
     ap.add_argument("--zipf-s", type=float, default=1.1, help="prefill router skew exponent")
     ap.add_argument("--copy-mib", type=int, default=256)
     ap.add_argument("--layers", type=int, default=40, help="stack workload depth")
+    ap.add_argument("--stack-norm", default="ref", choices=["ref", "tree"],
+                    help="stack workload: the RMSNorm's sum of squares in the reference's "
+                         "element order (ref) or as a 256-partial tree (tree)")
     ap.add_argument("--gguf-type", default="q3_k", choices=["q3_k", "q4_k", "q8_0"])
     ap.add_argument("--cpu-sample-s", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true")
@@ -569,14 +572,15 @@ def main():
         x = torch.from_numpy(x_host).to(dev)
         y = torch.empty((ntok, H), dtype=torch.float32, device=dev)
         xp, yp = x.data_ptr(), y.data_ptr()
+        tree = a.stack_norm == "tree"
         for t in range(a.warmup):
-            blk.forward_stack_device(xp + t * H * 4, 0, nl, 1, yp + t * H * 4)
+            blk.forward_stack_device(xp + t * H * 4, 0, nl, 1, yp + t * H * 4, tree=tree)
         torch.cuda.synchronize()
         blk.sync()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record(stream)
         for t in range(a.warmup, ntok):
-            blk.forward_stack_device(xp + t * H * 4, 0, nl, 1, yp + t * H * 4)
+            blk.forward_stack_device(xp + t * H * 4, 0, nl, 1, yp + t * H * 4, tree=tree)
         e1.record(stream)
         torch.cuda.synchronize()
         blk.sync()
@@ -590,7 +594,8 @@ def main():
             "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
             "data": "synthetic",
             "config": {"workload": f"{nl}-layer moe stack resident in HBM, batch-1 decode",
-                       "layers": nl, "hidden": H, "tokens": a.steps},
+                       "layers": nl, "hidden": H, "tokens": a.steps,
+                       "norm_order": "reference (sequential)" if not tree else "tree"},
             "roofline": {"bound": "hbm", "kernel": "moe stack", "achieved": round(gbps, 1),
                          "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                          "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None,

@@ -711,6 +711,28 @@ __device__ __forceinline__ void end_workgroup(const unsigned long long* status,
   if (threadIdx.x == 0) status_out[blockIdx.x] = ld_coh_u64(status);
 }
 
+// The sum of the squares sq[0..n) one after another (rmsnorm's order,
+// src/layers/rmsnorm.mojo:41-44) on one thread: a chain of n dependent adds
+// (about 6.7 us at n = 2048 on MI355X; a double-buffered variant of the LDS
+// reads measured slower).  n % 32 == 0.
+__device__ __forceinline__ float seq_sum_squares(const float* sq, int n) {
+  const float4* s4 = reinterpret_cast<const float4*>(sq);
+  float a = 0.0f;
+  for (int k = 0; k < n / 4; k += 8) {  // reads 8 float4 ahead of the adds
+    float4 v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = s4[k + u];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      a = a + v[u].x;
+      a = a + v[u].y;
+      a = a + v[u].z;
+      a = a + v[u].w;
+    }
+  }
+  return a;
+}
+
 // ---------------------------------------------------------------------------
 // NORM: 0 the block input is x; 1 / 2 it is rmsnorm(x, gamma, eps) with the
 // sum of squares as a 256-partial tree (1) or in element order (2, the
@@ -815,23 +837,7 @@ __global__ __launch_bounds__(kThreads) void k_moe_decode(
         if (tid < wd) red[tid] = red[tid] + red[tid + wd];
       }
     } else {
-      if (tid == 0) {
-        const float4* s4 = reinterpret_cast<const float4*>(sq);
-        float a = 0.0f;
-        for (int k = 0; k < H / 4; k += 8) {  // H % 128 == 0; reads 8 ahead of the adds
-          float4 v[8];
-#pragma unroll
-          for (int u = 0; u < 8; ++u) v[u] = s4[k + u];
-#pragma unroll
-          for (int u = 0; u < 8; ++u) {
-            a = a + v[u].x;
-            a = a + v[u].y;
-            a = a + v[u].z;
-            a = a + v[u].w;
-          }
-        }
-        red[0] = a;
-      }
+      if (tid == 0) red[0] = seq_sum_squares(sq, H);
     }
     __syncthreads();
     const float denom = __builtin_sqrtf(red[0] / (float)H + nm.eps);
@@ -1311,23 +1317,7 @@ __global__ __launch_bounds__(kThreads) void k_moe_decode_xs(
         if (tid < wd) red[tid] = red[tid] + red[tid + wd];
       }
     } else {
-      if (tid == 0) {
-        const float4* s4 = reinterpret_cast<const float4*>(sq);
-        float a = 0.0f;
-        for (int k = 0; k < H / 4; k += 8) {
-          float4 v[8];
-#pragma unroll
-          for (int u = 0; u < 8; ++u) v[u] = s4[k + u];
-#pragma unroll
-          for (int u = 0; u < 8; ++u) {
-            a = a + v[u].x;
-            a = a + v[u].y;
-            a = a + v[u].z;
-            a = a + v[u].w;
-          }
-        }
-        red[0] = a;
-      }
+      if (tid == 0) red[0] = seq_sum_squares(sq, H);
     }
     __syncthreads();
     const float denom = __builtin_sqrtf(red[0] / (float)H + nm.eps);
@@ -1415,22 +1405,6 @@ __global__ __launch_bounds__(kThreads) void k_moe_decode_xs(
   }
   __syncthreads();
   const bool ok = st.misc[2] != 0.0f;
-  if (tid == 64 && 2 * b < L.Ish) {
-    // h of shared rows 2b, 2b+1 (swiglu_forward's gate, up, product checks)
-    const int r0 = 2 * b;
-    const float g0 = shv[0], g1 = shv[1], u0 = shv[2], u1 = shv[3];
-    const float h0 = dm_silu(g0) * u0, h1 = dm_silu(g1) * u1;
-    auto chk = [&](int r, float g, float u, float hh) {
-      if (!finite_f(g) || !finite_f(u) || !finite_f(hh))
-        record_err(status, err_key(kPhShared, token, 0, r,
-                                   !finite_f(g) ? kEkGate : !finite_f(u) ? kEkUp : kEkH));
-    };
-    chk(r0, g0, u0, h0);
-    chk(r0 + 1, g1, u1, h1);
-    // read by the XCD holding the shared slice r0 / 128 (any XCD): agent scope
-    st_coh_u64(S.hl + (size_t)(KT + r0 / kQuadCols) * 64 + (r0 % kQuadCols) / 2,
-               pack_h2(n, h0, h1));
-  }
 
   // ---- routed loads: this workgroup's gate/up tile, this wave's down tiles ---
   const size_t matI = (size_t)L.I * H, matD = (size_t)H * L.I;
@@ -1462,8 +1436,25 @@ __global__ __launch_bounds__(kThreads) void k_moe_decode_xs(
   if (ntr > 0) grb = task_views(min(m, ntr - 1), gv, uv);  // (a spare workgroup re-reads a tile)
   gu_load<GQW, true>(gv, uv, grb, gwg, gwu, gsg, gsu);
 
-  // the shared down operand (its bytes landed before routing) while the
-  // routed loads are in flight
+  // while the routed loads are in flight: the shared rows' h (its thread
+  // would otherwise issue its loads late) and the shared down operand
+  if (tid == 64 && 2 * b < L.Ish) {
+    // h of shared rows 2b, 2b+1 (swiglu_forward's gate, up, product checks)
+    const int r0 = 2 * b;
+    const float g0 = shv[0], g1 = shv[1], u0 = shv[2], u1 = shv[3];
+    const float h0 = dm_silu(g0) * u0, h1 = dm_silu(g1) * u1;
+    auto chk = [&](int r, float g, float u, float hh) {
+      if (!finite_f(g) || !finite_f(u) || !finite_f(hh))
+        record_err(status, err_key(kPhShared, token, 0, r,
+                                   !finite_f(g) ? kEkGate : !finite_f(u) ? kEkUp : kEkH));
+    };
+    chk(r0, g0, u0, h0);
+    chk(r0 + 1, g1, u1, h1);
+    // read by the XCD holding the shared slice r0 / 128 (any XCD): agent scope
+    st_coh_u64(S.hl + (size_t)(KT + r0 / kQuadCols) * 64 + (r0 % kQuadCols) / 2,
+               pack_h2(n, h0, h1));
+  }
+
 #pragma unroll
   for (int c = 0; c < 4; ++c) As[c] = dequant8(word_of(dws, c), scale_of(dss, c));
   // the softmax sum and slot weights while the loads are in flight; the
