@@ -15,10 +15,15 @@
 //                   expert E over all tokens.  Units of more than 16 tokens
 //                   ("big") come first, then the small ones.
 //   k_split_rows    activations -> bf16 hi / lo rows
-//   k_gu_big        h = SiLU(W_g x) * (W_u x) for big units: A = 4-bit weights
-//                   dequantised in registers (16 features x 32 k per MFMA),
-//                   B = the unit's token rows staged in LDS per 128-column
-//                   step (double-buffered, one barrier per step)
+//   k_gu_big2       h = SiLU(W_g x) * (W_u x) for big units of bf16
+//                   activations: token rows, 4-bit weights and scales all
+//                   staged in LDS by direct-to-LDS loads, three k-steps in
+//                   flight, weights dequantised from LDS (16 features x 32 k
+//                   per MFMA)
+//   k_gu_big        the same when activations carry lo parts: A = 4-bit
+//                   weights dequantised in registers, B = the unit's token
+//                   rows (hi and lo) staged in LDS per 128-column step
+//                   (double-buffered, one barrier per step)
 //   k_gu_small      the same for units of <= 16 tokens: B fragments straight
 //                   from memory, no LDS and no barriers, deeper prefetch
 //   k_down_big / k_down_small   r = W_d h, B = h as bf16 hi + lo parts
@@ -464,15 +469,36 @@ __device__ __forceinline__ void big_loop(uint16_t* lds, const ExpertView& v0,
   }
 }
 
+// Big-unit workgroups come in classes b % 8, and the dispatcher places all
+// workgroups of a class on one XCD (it hands a launch's workgroups to the
+// XCDs in rotation).  The big units are cut into 8 contiguous ranges (the
+// units of one expert are adjacent in the unit list) and range c runs in
+// class c with each unit's feature blocks next to each other: the blocks of
+// a unit share that XCD's L2 for the unit's token rows, and the units of an
+// expert share it for the expert's weights.  Item (unit u, block f) of
+// workgroup b; false when b has no item.
+__device__ __forceinline__ bool big_item(int b, int nbig, int nblk, int& u, int& f) {
+  const int c = b & 7, idx = b >> 3;
+  const int span = (nbig + 7) >> 3;
+  const int ul = idx / nblk;
+  u = c * span + ul;
+  f = idx - ul * nblk;
+  return ul < span && u < nbig;
+}
+static int big_grid(int nbig, int nblk) { return 8 * ((nbig + 7) / 8) * nblk; }
+
 __global__ __launch_bounds__(kGThreads) void k_gu_big(GroupArgs g) {
   extern __shared__ __attribute__((aligned(16))) uint16_t glds[];
-  if ((int)blockIdx.x >= g.meta[1]) return;
-  const UnitTokens ut = unit_tokens(g.units[blockIdx.x], g.off, g.L.E, g.T, kMT);
+  if (g.need_lo[0] == 0) return;  // bf16 activations: k_gu_big2
+  int ui, fb;
+  const int nblk = ((g.L.I > g.L.Ish ? g.L.I : g.L.Ish) + 127) / 128;
+  if (!big_item(blockIdx.x, g.meta[1], nblk, ui, fb)) return;
+  const UnitTokens ut = unit_tokens(g.units[ui], g.off, g.L.E, g.T, kMT);
   const LayerDev& L = g.L;
   const int H = L.H, K = L.K, I = ut.shared ? L.Ish : L.I;
-  if ((int)blockIdx.y * 128 >= I) return;  // uniform per workgroup
+  if (fb * 128 >= I) return;  // uniform per workgroup
   const int tid = threadIdx.x, w = gwave_id(), lane = tid & 63, q = lane >> 4, j = lane & 15;
-  const int f0 = blockIdx.y * 128 + 32 * w;
+  const int f0 = fb * 128 + 32 * w;
   const bool active = f0 < I;  // uniform per wave
   const int rb0 = active ? f0 / kTileRows : 0;
   const size_t mat = (size_t)I * H;
@@ -489,22 +515,143 @@ __global__ __launch_bounds__(kGThreads) void k_gu_big(GroupArgs g) {
     roff[i] = t * H + seg * 8;
   }
   f32x4 acc[4][kNCT];
-  const int ns = H / kQuadCols;
-  if (g.need_lo[0] != 0)
-    big_loop<true, true>(glds, gv, uv, rb0, active, g.xhi, g.xlo, roff, ns, acc);
-  else
-    big_loop<false, true>(glds, gv, uv, rb0, active, g.xhi, g.xlo, roff, ns, acc);
+  big_loop<true, true>(glds, gv, uv, rb0, active, g.xhi, g.xlo, roff, H / kQuadCols, acc);
   if (active) gu_epilogue<4, kNCT>(g, ut, I, f0, q, j, acc);
+}
+
+// ---------------------------------------------------------------------------
+// Big units for bf16 activations (no lo parts), gate/up: k_gu_big2.  The same
+// work item as k_gu_big (a unit of up to 128 tokens x 128 features), on 8
+// waves, with every operand staged in LDS by direct-to-LDS loads
+// (global_load_lds_dwordx4: 16 bytes per lane land in LDS without passing
+// through registers), three k-steps in flight:
+//   - token rows: 128 rows x 256 bytes per k-step, segment sigma of row r
+//     stored at position sigma ^ (r & 15) of its row, so that the 16 rows of
+//     one MFMA B operand read distinct LDS banks;
+//   - A: the 16 A16 chunks of the step (8 gate tiles, 8 up tiles of the
+//     workgroup's 128 features) as they lie in memory, and their scales.
+// Wave w owns gate tile w and up tile w (features 16w..16w+15 of the block)
+// and all 8 column tiles, so h = SiLU(g) * u is formed in its registers.
+// One barrier per k-step: after it, stage s is complete everywhere and the
+// buffer of stage s - 1 is free for stage s + 2.
+constexpr int kB2Threads = 512;
+constexpr int kB2Stages = 3;
+constexpr int kB2RowBytes = kQuadCols * 2;                // one token row of a k-step
+constexpr int kB2BBytes = kMT * kB2RowBytes;               // 32 KB
+constexpr int kB2ABytes = 16 * 1024;                       // 16 A16 chunks
+constexpr int kB2SBytes = 16 * 128;                        // their scales
+constexpr int kB2Stage = kB2BBytes + kB2ABytes + kB2SBytes;  // 51200 bytes
+constexpr size_t kB2Lds = (size_t)kB2Stages * kB2Stage;    // 153600 bytes
+constexpr int kB2DmaPerStage = 7;                          // DMA instructions per wave and stage
+
+typedef __attribute__((address_space(3))) void lptr_t;
+// 16 bytes per lane from p to LDS at dst + 16 * lane (dst uniform per wave).
+// Issued as inline assembly: the compiler, which cannot tell the stages of
+// one LDS array apart, would otherwise wait for every load in flight before
+// any LDS read.  The kernel counts these loads itself (s_waitcnt vmcnt); a
+// load the compiler tracks is only ever waited for longer because of them.
+__device__ __forceinline__ void dma16(const void* p, void* dst) {
+  const uint32_t m = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lptr_t*)dst);
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(p), "s"(m)
+               : "memory", "m0");
+}
+
+__global__ __launch_bounds__(kB2Threads) void k_gu_big2(GroupArgs g) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char lds2[];
+  if (g.need_lo[0] != 0) return;  // activations with lo parts: k_gu_big
+  int ui, fb;
+  const int nblk = ((g.L.I > g.L.Ish ? g.L.I : g.L.Ish) + 127) / 128;
+  if (!big_item(blockIdx.x, g.meta[1], nblk, ui, fb)) return;
+  const UnitTokens ut = unit_tokens(g.units[ui], g.off, g.L.E, g.T, kMT);
+  const LayerDev& L = g.L;
+  const int H = L.H, K = L.K, I = ut.shared ? L.Ish : L.I;
+  if (fb * 128 >= I) return;  // uniform per workgroup
+  const int tid = threadIdx.x, w = gwave_id(), lane = tid & 63, q = lane >> 4, j = lane & 15;
+  const int rb0 = fb * 8;  // first 16-row tile of the block (gate and up)
+  const int nGQ = H / kQuadCols, ns = nGQ;
+  const size_t mat = (size_t)I * H;
+  const ExpertView gv = ut.shared ? ExpertView{L.sgu_nib, L.sgu_sc, I, H}
+                                  : ExpertView{L.gu_nib + (size_t)ut.e * mat,
+                                               L.gu_sc + (size_t)ut.e * 2 * (mat / kGroup), I, H};
+  const ExpertView uv = {gv.nib + mat / 2, gv.sc + mat / kGroup, I, H};
+  // this lane's part of the DMA of a stage:
+  //   token rows: instructions i = w + 8 m (m < 4) carry rows 4i..4i+3, lane
+  //   L row 4i + L/16, stored segment L % 16 = global segment (L % 16) ^ (row & 15)
+  //   A: chunk w (gate tile rb0 + w) and chunk 8 + w (up tile rb0 + w)
+  //   scales: lanes 0..15 carry the 2 x 128 bytes of the same two chunks
+  const uint16_t* rowp[4];
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    const int r = 4 * (w + 8 * m) + (lane >> 4);
+    const int rc = min(r, ut.n - 1);
+    const int t = ut.shared ? ut.p0 + rc : g.perm[ut.p0 + rc] / K;
+    const int sg = (lane & 15) ^ (r & 15);
+    rowp[m] = g.xhi + (size_t)t * H + sg * 8;
+  }
+  const ExpertView& sv = lane < 8 ? gv : uv;  // scale piece owner (lanes 0..15)
+  auto issue = [&](int s, int buf) {
+    unsigned char* st = lds2 + buf * kB2Stage;
+#pragma unroll
+    for (int m = 0; m < 4; ++m) dma16(rowp[m] + s * kQuadCols, st + (w + 8 * m) * 1024);
+    dma16(gv.nib + a16_nib_offset(nGQ, rb0 + w, s, lane), st + kB2BBytes + w * 1024);
+    dma16(uv.nib + a16_nib_offset(nGQ, rb0 + w, s, lane), st + kB2BBytes + (8 + w) * 1024);
+    // scales of (gate tile w, up tile w): 128 bytes each, lanes 0..7 and 8..15
+    // (only 16 lanes write: 256 bytes at the wave's own place)
+    if (lane < 16)
+      dma16(reinterpret_cast<const unsigned char*>(sv.sc + a16_sc_offset(nGQ, rb0 + w, s, 0)) +
+                (lane & 7) * 16,
+            st + kB2BBytes + kB2ABytes + w * 256);
+  };
+  f32x4 acc[2][kNCT];
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int ct = 0; ct < kNCT; ++ct) acc[t][ct] = f32x4{0, 0, 0, 0};
+  issue(0, 0);
+  if (ns > 1) issue(1, 1);
+  for (int s = 0; s < ns; ++s) {
+    // this wave's loads of stage s have landed (one later stage may be in flight)
+    static_assert(kB2DmaPerStage == 7, "the wait below counts one stage of 7 loads");
+    if (s + 1 < ns)
+      asm volatile("s_waitcnt vmcnt(7)" ::: "memory");
+    else
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    // every wave's loads of stage s have landed, and every wave has finished
+    // reading stage s - 1 (whose buffer the next issue overwrites)
+    __builtin_amdgcn_s_barrier();
+    if (s + 2 < ns) issue(s + 2, (s + 2) % kB2Stages);
+    const unsigned char* st = lds2 + (s % kB2Stages) * kB2Stage;
+    const uint4 cg = *reinterpret_cast<const uint4*>(st + kB2BBytes + w * 1024 + lane * 16);
+    const uint4 cu = *reinterpret_cast<const uint4*>(st + kB2BBytes + (8 + w) * 1024 + lane * 16);
+    const uint2 sgs = *reinterpret_cast<const uint2*>(st + kB2BBytes + kB2ABytes + w * 256 + j * 8);
+    const uint2 sus =
+        *reinterpret_cast<const uint2*>(st + kB2BBytes + kB2ABytes + w * 256 + 128 + j * 8);
+#pragma unroll
+    for (int kk = 0; kk < kGroupsPerQuad; ++kk) {
+      const bf16x8 ag = dequant8(word_of(cg, kk), scale_of(sgs, kk));
+      const bf16x8 au = dequant8(word_of(cu, kk), scale_of(sus, kk));
+      const int sg = (4 * kk + q) ^ j;
+#pragma unroll
+      for (int ct = 0; ct < kNCT; ++ct) {
+        const bf16x8 b =
+            *reinterpret_cast<const bf16x8*>(st + (ct * 16 + j) * kB2RowBytes + sg * 16);
+        acc[0][ct] = mfma16(ag, b, acc[0][ct]);
+        acc[1][ct] = mfma16(au, b, acc[1][ct]);
+      }
+    }
+  }
+  gu_epilogue<2, kNCT>(g, ut, I, fb * 128 + 16 * w, q, j, acc);
 }
 
 __global__ __launch_bounds__(kGThreads) void k_down_big(GroupArgs g) {
   extern __shared__ __attribute__((aligned(16))) uint16_t glds[];
-  if ((int)blockIdx.x >= g.meta[1]) return;
-  const UnitTokens ut = unit_tokens(g.units[blockIdx.x], g.off, g.L.E, g.T, kMT);
+  int ui, rbk;
+  if (!big_item(blockIdx.x, g.meta[1], (g.L.H + 255) / 256, ui, rbk)) return;
+  const UnitTokens ut = unit_tokens(g.units[ui], g.off, g.L.E, g.T, kMT);
   const LayerDev& L = g.L;
   const int H = L.H, I = ut.shared ? L.Ish : L.I;
   const int tid = threadIdx.x, w = gwave_id(), lane = tid & 63, q = lane >> 4, j = lane & 15;
-  const int row0 = blockIdx.y * 256 + 64 * w;
+  const int row0 = rbk * 256 + 64 * w;
   const bool active = row0 < H;
   const int rb0 = active ? row0 / kTileRows : 0;
   const size_t mat = (size_t)H * I;
@@ -662,13 +809,23 @@ hipError_t launch_experts_grouped(const LayerDev& L, const uint16_t* xhi, const 
   // an expert holds at most T tokens (its ids per token are distinct), so
   // units of more than 2 * kSmallMax tokens need T > 2 * kSmallMax
   const bool big = T > 2 * kSmallMax;
-  if (big)
-    hipLaunchKernelGGL(k_gu_big, dim3(nbig, (imax + 127) / 128), dim3(kGThreads), kBigLds, st, g);
+  if (big) {
+    // I and Ish are multiples of 128 (checked at upload): every block of
+    // k_gu_big2 is a whole 128-feature block.  Exactly one of the two
+    // kernels does the work, chosen on the device by the need-lo flag.
+    static const hipError_t attr = hipFuncSetAttribute(
+        reinterpret_cast<const void*>(k_gu_big2), hipFuncAttributeMaxDynamicSharedMemorySize,
+        (int)kB2Lds);
+    if (attr != hipSuccess) return attr;
+    const int gsz = big_grid(nbig, (imax + 127) / 128);
+    hipLaunchKernelGGL(k_gu_big2, dim3(gsz), dim3(kB2Threads), kB2Lds, st, g);
+    hipLaunchKernelGGL(k_gu_big, dim3(gsz), dim3(kGThreads), kBigLds, st, g);
+  }
   hipLaunchKernelGGL(k_gu_small, dim3(nsmall, (imax + kSmallGuCols - 1) / kSmallGuCols),
                      dim3(kGThreads), 0, st, g);
   if (big)
-    hipLaunchKernelGGL(k_down_big, dim3(nbig, (L.H + 255) / 256), dim3(kGThreads), kBigLds, st,
-                       g);
+    hipLaunchKernelGGL(k_down_big, dim3(big_grid(nbig, (L.H + 255) / 256)), dim3(kGThreads),
+                       kBigLds, st, g);
   hipLaunchKernelGGL(k_down_small, dim3(nsmall, (L.H + kSmallDnRows - 1) / kSmallDnRows),
                      dim3(kGThreads), 0, st, g);
   return hipGetLastError();
