@@ -55,21 +55,19 @@ __device__ __forceinline__ float dm_expf(float x) {
   return nan ? x : res;
 }
 
-// sigmoid_f32 / silu_f32 of src/layers/swiglu.mojo:11-38
+// sigmoid_f32 / silu_f32 of src/layers/swiglu.mojo:11-38.  Both branches of
+// the reference share e = exp(-|z|): for z < 0 it is exp(z) and the result
+// e / (1 + e), otherwise exp(-z) and 1 / (1 + e).  One exponential and one
+// division per value, the special cases selected, so that lanes of a wave on
+// different branches do not each run both.
 __device__ __forceinline__ float dm_sigmoid(float z) {
-  if (z != z) return z;
-  if (z < -88.0f) return 0.0f;
-  if (z > 88.0f) return 1.0f;
-  if (z < 0.0f) {
-    float ez = dm_expf(z);
-    return ez / (1.0f + ez);
-  }
-  return 1.0f / (1.0f + dm_expf(-z));
+  const float e = dm_expf(-__builtin_fabsf(z));
+  const float r = (z < 0.0f ? e : 1.0f) / (1.0f + e);
+  return z != z ? z : z < -88.0f ? 0.0f : z > 88.0f ? 1.0f : r;
 }
 __device__ __forceinline__ float dm_silu(float z) {
-  if (z != z) return z;
-  if (!finite_f(z)) return z > 0.0f ? z : 0.0f;
-  return z * dm_sigmoid(z);
+  const float s = z * dm_sigmoid(z);
+  return z != z ? z : !finite_f(z) ? (z > 0.0f ? z : 0.0f) : s;
 }
 
 // Wavefront-wide maxima from the ROCm device library (ockl).

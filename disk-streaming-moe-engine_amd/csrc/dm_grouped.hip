@@ -15,24 +15,21 @@
 //                   expert E over all tokens.  Units of more than 16 tokens
 //                   ("big") come first, then the small ones.
 //   k_split_rows    activations -> bf16 hi / lo rows
-//   k_gu_big2       h = SiLU(W_g x) * (W_u x) for big units of bf16
-//                   activations: token rows, 4-bit weights and scales all
-//                   staged in LDS by direct-to-LDS loads, three k-steps in
-//                   flight, weights dequantised from LDS (16 features x 32 k
-//                   per MFMA)
-//   k_gu_big        the same when activations carry lo parts: A = 4-bit
-//                   weights dequantised in registers, B = the unit's token
-//                   rows (hi and lo) staged in LDS per 128-column step
-//                   (double-buffered, one barrier per step)
+//   k_big<true>     h = SiLU(W_g x) * (W_u x) for big units: token rows,
+//                   4-bit weights and scales all staged in LDS by
+//                   direct-to-LDS loads, three stages in flight, weights
+//                   dequantised from LDS (16 features x 32 k per MFMA)
 //   k_gu_small      the same for units of <= 16 tokens: B fragments straight
 //                   from memory, no LDS and no barriers, deeper prefetch
-//   k_down_big / k_down_small   r = W_d h, B = h as bf16 hi + lo parts
+//   k_big<false> / k_down_small   r = W_d h, B = h as bf16 hi + lo parts
 //   k_combine       y = sum_k p_k r_k + g r_sh (+ residual), reference order
 //
 // Each token's outputs depend only on its own column of the MFMA tiles, so
 // the placement of tokens inside an expert's tiles (atomic scatter) does not
 // change any result bit.
 #include <hip/hip_runtime.h>
+
+#include <atomic>
 
 #include "dm_device.h"
 #include "dm_grouped.h"
@@ -281,36 +278,63 @@ __device__ __forceinline__ void split4(const float* v, uint2& hi, uint2& lo) {
 // Gate/up: tile t < NT/2 holds gate features f0 + 16 t + 4q + i, tile
 // NT/2 + t the same up features; h = SiLU(g) * u with the reference's checks
 // (src/layers/swiglu.mojo:191-201), stored as bf16 hi / lo.
+// The assignment (token * K + slot; the token for the shared expert) of
+// column j of each of the unit's NC column tiles, all requested before the
+// first store: a load issued after stores waits for them to complete (one
+// counter covers both), which would serialise the epilogue on store latency.
+template <int NC>
+__device__ __forceinline__ void unit_assignments(const GroupArgs& g, const UnitTokens& ut, int j,
+                                                 int (&aa)[NC]) {
+// (The load is unconditional — perm has T * K >= T entries — so that no
+// path joins with loads of unknown count in flight.)
+#pragma unroll
+  for (int ct = 0; ct < NC; ++ct) {
+    const int p = ut.p0 + min(16 * ct + j, ut.n - 1);
+    const int a = g.perm[p];
+    aa[ct] = ut.shared ? p : a;
+  }
+}
+
 template <int NT, int NC>
 __device__ __forceinline__ void gu_epilogue(const GroupArgs& g, const UnitTokens& ut, int I,
                                             int f0, int q, int j, const f32x4 (&acc)[NT][NC]) {
   const int K = g.L.K;
+  int aa[NC];
+  unit_assignments<NC>(g, ut, j, aa);
 #pragma unroll
   for (int ct = 0; ct < NC; ++ct) {
     const int c = 16 * ct + j;
     if (c < ut.n) {
       const int p = ut.p0 + c;
-      const int a = ut.shared ? p : g.perm[p];
-      const int t = ut.shared ? p : a / K, k = ut.shared ? 0 : a % K;
 #pragma unroll
       for (int half = 0; half < NT / 2; ++half) {
         const int fr = f0 + 16 * half + 4 * q;
         float hv[4];
+        bool bad = false;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const float gg = acc[half][ct][i], u = acc[NT / 2 + half][ct][i];
           hv[i] = dm_silu(gg) * u;
-          if (!finite_f(gg) || !finite_f(u) || !finite_f(hv[i])) {
-            const uint32_t ph = ut.shared ? kPhShared : kPhExpert;
-            const uint32_t kind = !finite_f(gg) ? kEkGate : !finite_f(u) ? kEkUp : kEkH;
-            record_err(g.status, err_key(ph, t, k, fr + i, kind));
-          }
+          bad |= !finite_f(gg) || !finite_f(u) || !finite_f(hv[i]);
         }
         uint2 h2, l2;
         split4(hv, h2, l2);
         const size_t o = (size_t)p * I + fr;
         *reinterpret_cast<uint2*>((ut.shared ? g.hsh : g.hrh) + o) = h2;
         *reinterpret_cast<uint2*>((ut.shared ? g.hsl : g.hrl) + o) = l2;
+        if (bad) {  // the error key needs token and slot (a division by K): only here
+          const int a = aa[ct];
+          const int t = ut.shared ? p : a / K, k = ut.shared ? 0 : a % K;
+          const uint32_t ph = ut.shared ? kPhShared : kPhExpert;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float gg = acc[half][ct][i], u = acc[NT / 2 + half][ct][i];
+            if (!finite_f(gg) || !finite_f(u) || !finite_f(hv[i])) {
+              const uint32_t kind = !finite_f(gg) ? kEkGate : !finite_f(u) ? kEkUp : kEkH;
+              record_err(g.status, err_key(ph, t, k, fr + i, kind));
+            }
+          }
+        }
       }
     }
   }
@@ -322,153 +346,34 @@ __device__ __forceinline__ void down_epilogue(const GroupArgs& g, const UnitToke
                                               int row0, int q, int j,
                                               const f32x4 (&acc)[NT][NC]) {
   const int H = g.L.H, K = g.L.K;
+  int aa[NC];
+  unit_assignments<NC>(g, ut, j, aa);
 #pragma unroll
   for (int ct = 0; ct < NC; ++ct) {
     const int c = 16 * ct + j;
     if (c < ut.n) {
       const int p = ut.p0 + c;
-      const int a = ut.shared ? p : g.perm[p];
-      const int t = ut.shared ? p : a / K, k = ut.shared ? 0 : a % K;
-      float* dst = ut.shared ? g.rs + (size_t)t * H : g.r + (size_t)a * H;
+      const int a = aa[ct];
+      float* dst = ut.shared ? g.rs + (size_t)p * H : g.r + (size_t)a * H;
 #pragma unroll
       for (int tl = 0; tl < NT; ++tl) {
         const int d0 = row0 + 16 * tl + 4 * q;
-        float v[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          v[i] = acc[tl][ct][i];
-          if (!finite_f(v[i])) {
-            const uint32_t ph = ut.shared ? kPhShared : kPhExpert;
-            record_err(g.status, err_key(ph, t, k, I + d0 + i, kEkDown));
-          }
-        }
+        const float* v = reinterpret_cast<const float*>(&acc[tl][ct]);
         *reinterpret_cast<float4*>(dst + d0) = make_float4(v[0], v[1], v[2], v[3]);
+        if (!finite_f(v[0]) || !finite_f(v[1]) || !finite_f(v[2]) || !finite_f(v[3])) {
+          // the error key needs token and slot (a division by K): only here
+          const int t = ut.shared ? p : a / K, k = ut.shared ? 0 : a % K;
+          const uint32_t ph = ut.shared ? kPhShared : kPhExpert;
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (!finite_f(v[i])) record_err(g.status, err_key(ph, t, k, I + d0 + i, kEkDown));
+        }
       }
     }
   }
 }
 
 // ---------------------------------------------------------------------------
-// Big units.  A workgroup of 4 waves takes one unit (17..128 tokens) and
-// 128 features (gate/up: wave w owns features f0 = 128 blockIdx.y + 32 w ..
-// f0 + 31, i.e. gate tiles f0, f0 + 16 and the same up tiles) or 256 output
-// rows (down: wave w owns rows 256 blockIdx.y + 64 w .. + 63).  All 8 column
-// tiles are computed (columns past the unit's tokens are never stored).
-//
-// B staging: per k-step of 128 columns, the unit's 128 rows (row r clamped
-// to the last token) move global -> registers -> LDS: thread tid carries the
-// 16-byte segment tid & 15 of rows (tid >> 4) + 16 i.  Two LDS buffers: step
-// s computes from buffer s & 1 while the rows of step s + 1 are written to
-// the other and those of step s + 2 are in flight; one barrier per step.
-// Rows are padded to kBPitch elements so that the 16 rows of one MFMA operand
-// fetch (ds_read_b128 by lanes j = 0..15 at one q) fall on 16 distinct
-// 4-bank groups.  A: the chunks of step s + 2 are requested while step s
-// computes (kBigPre = 2, which also keeps the buffer index of each unrolled
-// step a constant).
-constexpr int kBPitch = kQuadCols + 8;
-constexpr int kBTile = kMT * kBPitch;  // elements per staged plane
-constexpr int kBigPre = 2;
-constexpr size_t kBigLds = 2 * 2 * kBTile * sizeof(uint16_t);  // 2 buffers x (hi, lo)
-
-__device__ __forceinline__ bf16x8 lds_b(const uint16_t* bs, int ct, int kk, int q, int j) {
-  return *reinterpret_cast<const bf16x8*>(bs + (ct * 16 + j) * kBPitch + kk * kGroup + 8 * q);
-}
-
-template <bool LO>
-__device__ __forceinline__ void rows_load(const uint16_t* __restrict__ sh,
-                                          const uint16_t* __restrict__ sl,
-                                          const int (&roff)[kNCT], int s, v4u (&bh)[kNCT],
-                                          v4u (&bl)[kNCT]) {
-#pragma unroll
-  for (int i = 0; i < kNCT; ++i) {
-    const uint32_t o = (uint32_t)roff[i] + (uint32_t)(s * kQuadCols);
-    bh[i] = *reinterpret_cast<const v4u*>(sh + o);
-    if (LO) bl[i] = *reinterpret_cast<const v4u*>(sl + o);
-  }
-}
-
-template <bool LO>
-__device__ __forceinline__ void rows_store(uint16_t* bs, int srow, int seg, const v4u (&bh)[kNCT],
-                                           const v4u (&bl)[kNCT]) {
-#pragma unroll
-  for (int i = 0; i < kNCT; ++i) {
-    const int o = (srow + 16 * i) * kBPitch + seg * 8;
-    *reinterpret_cast<v4u*>(bs + o) = bh[i];
-    if (LO) *reinterpret_cast<v4u*>(bs + kBTile + o) = bl[i];
-  }
-}
-
-// One k-step of a big unit: 4 k-groups x (4 A tiles x 8 column tiles).
-template <bool LO>
-__device__ __forceinline__ void big_step(const uint16_t* bs, const AChunks<4>& a, int q, int j,
-                                         f32x4 (&acc)[4][kNCT]) {
-#pragma unroll
-  for (int kk = 0; kk < kGroupsPerQuad; ++kk) {
-    bf16x8 av[4];
-    dequant_a<4>(a, kk, av);
-#pragma unroll
-    for (int ct = 0; ct < kNCT; ++ct) {
-      const bf16x8 b = lds_b(bs, ct, kk, q, j);
-#pragma unroll
-      for (int tl = 0; tl < 4; ++tl) acc[tl][ct] = mfma16(av[tl], b, acc[tl][ct]);
-      if (LO) {
-        const bf16x8 b2 = lds_b(bs + kBTile, ct, kk, q, j);
-#pragma unroll
-        for (int tl = 0; tl < 4; ++tl) acc[tl][ct] = mfma16(av[tl], b2, acc[tl][ct]);
-      }
-    }
-  }
-}
-
-// The k-loop of a big unit over ns steps (A views, staged rows from sh/sl).
-template <bool LO, bool GU>
-__device__ __forceinline__ void big_loop(uint16_t* lds, const ExpertView& v0,
-                                         const ExpertView& v1, int rb0, bool active,
-                                         const uint16_t* sh, const uint16_t* sl,
-                                         const int (&roff)[kNCT], int ns, f32x4 (&acc)[4][kNCT]) {
-  const int tid = threadIdx.x, lane = tid & 63, q = lane >> 4, j = lane & 15;
-  const int seg = tid & 15, srow = tid >> 4;
-  constexpr int kBuf = 2 * kBTile;  // elements per buffer (hi, lo planes)
-  v4u bh[kNCT], bl[kNCT];
-  rows_load<LO>(sh, sl, roff, 0, bh, bl);
-  rows_store<LO>(lds, srow, seg, bh, bl);
-  rows_load<LO>(sh, sl, roff, min(1, ns - 1), bh, bl);
-  AChunks<4> ring[kBigPre];
-  if (active) {
-#pragma unroll
-    for (int u = 0; u < kBigPre; ++u) load_a<4, GU>(v0, v1, rb0, min(u, ns - 1), lane, ring[u]);
-  }
-#pragma unroll
-  for (int tl = 0; tl < 4; ++tl)
-#pragma unroll
-    for (int ct = 0; ct < kNCT; ++ct) acc[tl][ct] = f32x4{0, 0, 0, 0};
-  __syncthreads();
-  int s0 = 0;
-  for (; s0 + kBigPre < ns; s0 += kBigPre) {
-#pragma unroll
-    for (int u = 0; u < kBigPre; ++u) {
-      const int s = s0 + u;
-      rows_store<LO>(lds + ((u + 1) & 1) * kBuf, srow, seg, bh, bl);
-      rows_load<LO>(sh, sl, roff, min(s + 2, ns - 1), bh, bl);
-      if (active) {
-        big_step<LO>(lds + (u & 1) * kBuf, ring[u], q, j, acc);
-        load_a<4, GU>(v0, v1, rb0, s + kBigPre, lane, ring[u]);
-      }
-      __syncthreads();
-    }
-  }
-  // the last 1..kBigPre steps: nothing left to request
-#pragma unroll
-  for (int u = 0; u < kBigPre; ++u) {
-    const int s = s0 + u;
-    if (s < ns) {
-      if (s + 1 < ns) rows_store<LO>(lds + ((u + 1) & 1) * kBuf, srow, seg, bh, bl);
-      if (active) big_step<LO>(lds + (u & 1) * kBuf, ring[u], q, j, acc);
-      __syncthreads();
-    }
-  }
-}
-
 // Big-unit workgroups come in classes b % 8, and the dispatcher places all
 // workgroups of a class on one XCD (it hands a launch's workgroups to the
 // XCDs in rotation).  The big units are cut into 8 contiguous ranges (the
@@ -487,52 +392,24 @@ __device__ __forceinline__ bool big_item(int b, int nbig, int nblk, int& u, int&
 }
 static int big_grid(int nbig, int nblk) { return 8 * ((nbig + 7) / 8) * nblk; }
 
-__global__ __launch_bounds__(kGThreads) void k_gu_big(GroupArgs g) {
-  extern __shared__ __attribute__((aligned(16))) uint16_t glds[];
-  if (g.need_lo[0] == 0) return;  // bf16 activations: k_gu_big2
-  int ui, fb;
-  const int nblk = ((g.L.I > g.L.Ish ? g.L.I : g.L.Ish) + 127) / 128;
-  if (!big_item(blockIdx.x, g.meta[1], nblk, ui, fb)) return;
-  const UnitTokens ut = unit_tokens(g.units[ui], g.off, g.L.E, g.T, kMT);
-  const LayerDev& L = g.L;
-  const int H = L.H, K = L.K, I = ut.shared ? L.Ish : L.I;
-  if (fb * 128 >= I) return;  // uniform per workgroup
-  const int tid = threadIdx.x, w = gwave_id(), lane = tid & 63, q = lane >> 4, j = lane & 15;
-  const int f0 = fb * 128 + 32 * w;
-  const bool active = f0 < I;  // uniform per wave
-  const int rb0 = active ? f0 / kTileRows : 0;
-  const size_t mat = (size_t)I * H;
-  const ExpertView gv = ut.shared ? ExpertView{L.sgu_nib, L.sgu_sc, I, H}
-                                  : ExpertView{L.gu_nib + (size_t)ut.e * mat,
-                                               L.gu_sc + (size_t)ut.e * 2 * (mat / kGroup), I, H};
-  const ExpertView uv = {gv.nib + mat / 2, gv.sc + mat / kGroup, I, H};
-  int roff[kNCT];
-  const int seg = tid & 15, srow = tid >> 4;
-#pragma unroll
-  for (int i = 0; i < kNCT; ++i) {
-    const int r = min(srow + 16 * i, ut.n - 1);
-    const int t = ut.shared ? ut.p0 + r : g.perm[ut.p0 + r] / K;
-    roff[i] = t * H + seg * 8;
-  }
-  f32x4 acc[4][kNCT];
-  big_loop<true, true>(glds, gv, uv, rb0, active, g.xhi, g.xlo, roff, H / kQuadCols, acc);
-  if (active) gu_epilogue<4, kNCT>(g, ut, I, f0, q, j, acc);
-}
-
 // ---------------------------------------------------------------------------
-// Big units for bf16 activations (no lo parts), gate/up: k_gu_big2.  The same
-// work item as k_gu_big (a unit of up to 128 tokens x 128 features), on 8
-// waves, with every operand staged in LDS by direct-to-LDS loads
-// (global_load_lds_dwordx4: 16 bytes per lane land in LDS without passing
-// through registers), three k-steps in flight:
-//   - token rows: 128 rows x 256 bytes per k-step, segment sigma of row r
-//     stored at position sigma ^ (r & 15) of its row, so that the 16 rows of
-//     one MFMA B operand read distinct LDS banks;
-//   - A: the 16 A16 chunks of the step (8 gate tiles, 8 up tiles of the
-//     workgroup's 128 features) as they lie in memory, and their scales.
-// Wave w owns gate tile w and up tile w (features 16w..16w+15 of the block)
-// and all 8 column tiles, so h = SiLU(g) * u is formed in its registers.
-// One barrier per k-step: after it, stage s is complete everywhere and the
+// Big units (17..128 tokens): k_big<GU>.  A workgroup of 8 waves takes one
+// unit and 128 features (gate/up: gate and up tiles rb0 + w of wave w, so
+// that h = SiLU(g) * u is formed in its registers) or 256 output rows (down:
+// tiles rb0 + 2w, rb0 + 2w + 1 of wave w), all 8 column tiles of the unit
+// (columns past its tokens are never stored).  Every operand is staged in
+// LDS by direct-to-LDS loads (global_load_lds_dwordx4: 16 bytes per lane
+// land in LDS without passing through registers), three stages in flight:
+//   - B rows: 128 rows x 256 bytes per k-step, segment sigma of row r stored
+//     at position sigma ^ (r & 15) of its row, so that the 16 rows of one
+//     MFMA B operand read distinct LDS banks;
+//   - A: the step's 16 A16 chunks (2 per wave) as they lie in memory, and
+//     their scales.
+// B rows are bf16 hi parts, and when the activations are not all bf16
+// values (h always; x when the need-lo flag is set) the lo parts too: then
+// a k-step is two stages, hi then lo, with the same A (read twice, the
+// second time from L2) and both products summed into the accumulators.
+// One barrier per stage: after it, stage s is complete everywhere and the
 // buffer of stage s - 1 is free for stage s + 2.
 constexpr int kB2Threads = 512;
 constexpr int kB2Stages = 3;
@@ -550,55 +427,120 @@ typedef __attribute__((address_space(3))) void lptr_t;
 // one LDS array apart, would otherwise wait for every load in flight before
 // any LDS read.  The kernel counts these loads itself (s_waitcnt vmcnt); a
 // load the compiler tracks is only ever waited for longer because of them.
+// M0 (the LDS address) is a register the compiler reserves: its value is
+// saved and restored around the load.
 __device__ __forceinline__ void dma16(const void* p, void* dst) {
   const uint32_t m = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lptr_t*)dst);
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(p), "s"(m)
-               : "memory", "m0");
+  uint32_t save;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %1, off\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(save)
+      : "v"(p), "s"(m)
+      : "memory");
 }
 
-__global__ __launch_bounds__(kB2Threads) void k_gu_big2(GroupArgs g) {
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const lptr_t*)p;
+}
+
+// The B fragments of 8 column tiles (rows 16 ct + j of a staged k-step,
+// 16 * 256 bytes apart) as 8 LDS reads in flight together.  Inline assembly
+// again: the compiler would otherwise sink each read next to its first use,
+// leaving two in flight.  Their registers are not valid before lds_wait8.
+__device__ __forceinline__ void lds_read8(uint32_t a, bf16x8 (&b)[kNCT]) {
+  static_assert(kNCT == 8 && 16 * kB2RowBytes == 4096, "offsets below");
+  asm volatile(
+      "ds_read_b128 %0, %8\n\tds_read_b128 %1, %8 offset:4096\n\t"
+      "ds_read_b128 %2, %8 offset:8192\n\tds_read_b128 %3, %8 offset:12288\n\t"
+      "ds_read_b128 %4, %8 offset:16384\n\tds_read_b128 %5, %8 offset:20480\n\t"
+      "ds_read_b128 %6, %8 offset:24576\n\tds_read_b128 %7, %8 offset:28672"
+      : "=&v"(b[0]), "=&v"(b[1]), "=&v"(b[2]), "=&v"(b[3]), "=&v"(b[4]), "=&v"(b[5]),
+        "=&v"(b[6]), "=&v"(b[7])
+      : "v"(a));
+}
+// Wait until at most N LDS operations are in flight (LDS operations complete
+// in order, so every read issued before the last N has landed); b's
+// registers are tied to the wait, so no use of them moves above it.
+template <int N>
+__device__ __forceinline__ void lds_wait8(bf16x8 (&b)[kNCT]) {
+  asm volatile("s_waitcnt lgkmcnt(%8)"
+               : "+v"(b[0]), "+v"(b[1]), "+v"(b[2]), "+v"(b[3]), "+v"(b[4]), "+v"(b[5]),
+                 "+v"(b[6]), "+v"(b[7])
+               : "n"(N));
+}
+
+// One workgroup per CU (its LDS), two waves per SIMD: registers up to 256
+// per lane, spent on keeping a whole k-group of B fragments in flight.
+template <bool GU>
+__global__ __launch_bounds__(kB2Threads) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void k_big(GroupArgs g) {
   extern __shared__ __attribute__((aligned(16))) unsigned char lds2[];
-  if (g.need_lo[0] != 0) return;  // activations with lo parts: k_gu_big
-  int ui, fb;
-  const int nblk = ((g.L.I > g.L.Ish ? g.L.I : g.L.Ish) + 127) / 128;
-  if (!big_item(blockIdx.x, g.meta[1], nblk, ui, fb)) return;
-  const UnitTokens ut = unit_tokens(g.units[ui], g.off, g.L.E, g.T, kMT);
   const LayerDev& L = g.L;
-  const int H = L.H, K = L.K, I = ut.shared ? L.Ish : L.I;
-  if (fb * 128 >= I) return;  // uniform per workgroup
+  const int H = L.H, K = L.K;
+  int ui, fb;
+  const int nblk = GU ? ((L.I > L.Ish ? L.I : L.Ish) + 127) / 128 : (H + 255) / 256;
+  if (!big_item(blockIdx.x, g.meta[1], nblk, ui, fb)) return;
+  const UnitTokens ut = unit_tokens(g.units[ui], g.off, L.E, g.T, kMT);
+  const int I = ut.shared ? L.Ish : L.I;
+  if (GU && fb * 128 >= I) return;  // uniform per workgroup
   const int tid = threadIdx.x, w = gwave_id(), lane = tid & 63, q = lane >> 4, j = lane & 15;
-  const int rb0 = fb * 8;  // first 16-row tile of the block (gate and up)
-  const int nGQ = H / kQuadCols, ns = nGQ;
-  const size_t mat = (size_t)I * H;
-  const ExpertView gv = ut.shared ? ExpertView{L.sgu_nib, L.sgu_sc, I, H}
-                                  : ExpertView{L.gu_nib + (size_t)ut.e * mat,
-                                               L.gu_sc + (size_t)ut.e * 2 * (mat / kGroup), I, H};
-  const ExpertView uv = {gv.nib + mat / 2, gv.sc + mat / kGroup, I, H};
+  const int KD = GU ? H : I;  // reduction length
+  const int nGQ = KD / kQuadCols;
+  const bool lo = GU ? g.need_lo[0] != 0 : true;
+  const int nst = lo ? 2 * nGQ : nGQ;  // stages
+  // A views and this wave's two tiles: (v0, t0) and (v1, t1)
+  ExpertView v0, v1;
+  int t0, t1;
+  if (GU) {
+    const size_t mat = (size_t)I * H;
+    v0 = ut.shared ? ExpertView{L.sgu_nib, L.sgu_sc, I, H}
+                   : ExpertView{L.gu_nib + (size_t)ut.e * mat,
+                                L.gu_sc + (size_t)ut.e * 2 * (mat / kGroup), I, H};
+    v1 = {v0.nib + mat / 2, v0.sc + mat / kGroup, I, H};
+    t0 = t1 = fb * 8 + w;
+  } else {
+    const size_t mat = (size_t)H * I;
+    v0 = ut.shared ? ExpertView{L.sd_nib, L.sd_sc, H, I}
+                   : ExpertView{L.d_nib + (size_t)ut.e * (mat / 2),
+                                L.d_sc + (size_t)ut.e * (mat / kGroup), H, I};
+    v1 = v0;
+    // H is a multiple of 128, so the last block may hold 128 rows: waves
+    // past H load tiles 0 and 1 (their share of the B rows is still needed)
+    // and store nothing
+    t0 = fb * 256 + 32 * w < H ? fb * 16 + 2 * w : 0;
+    t1 = t0 + 1;
+  }
+  const uint16_t* bhi = GU ? g.xhi : (ut.shared ? g.hsh : g.hrh);
+  const uint16_t* blo = GU ? g.xlo : (ut.shared ? g.hsl : g.hrl);
   // this lane's part of the DMA of a stage:
-  //   token rows: instructions i = w + 8 m (m < 4) carry rows 4i..4i+3, lane
+  //   B rows: instructions i = w + 8 m (m < 4) carry rows 4i..4i+3, lane
   //   L row 4i + L/16, stored segment L % 16 = global segment (L % 16) ^ (row & 15)
-  //   A: chunk w (gate tile rb0 + w) and chunk 8 + w (up tile rb0 + w)
+  //   A: chunk 2w (tile t0) and chunk 2w + 1 (tile t1)
   //   scales: lanes 0..15 carry the 2 x 128 bytes of the same two chunks
-  const uint16_t* rowp[4];
+  size_t rowo[4];
 #pragma unroll
   for (int m = 0; m < 4; ++m) {
     const int r = 4 * (w + 8 * m) + (lane >> 4);
-    const int rc = min(r, ut.n - 1);
-    const int t = ut.shared ? ut.p0 + rc : g.perm[ut.p0 + rc] / K;
+    const int p = ut.p0 + min(r, ut.n - 1);
     const int sg = (lane & 15) ^ (r & 15);
-    rowp[m] = g.xhi + (size_t)t * H + sg * 8;
+    const int row = !GU ? p : ut.shared ? p : g.perm[p] / K;  // h rows by position, x by token
+    rowo[m] = (size_t)row * KD + sg * 8;
   }
-  const ExpertView& sv = lane < 8 ? gv : uv;  // scale piece owner (lanes 0..15)
-  auto issue = [&](int s, int buf) {
+  const ExpertView& sv = lane < 8 ? v0 : v1;  // scale piece owner (lanes 0..15)
+  const int st_ = lane < 8 ? t0 : t1;
+  auto issue = [&](int ps, int buf) {
+    const int s = lo ? ps >> 1 : ps;
+    const uint16_t* src = (lo && (ps & 1)) ? blo : bhi;
     unsigned char* st = lds2 + buf * kB2Stage;
 #pragma unroll
-    for (int m = 0; m < 4; ++m) dma16(rowp[m] + s * kQuadCols, st + (w + 8 * m) * 1024);
-    dma16(gv.nib + a16_nib_offset(nGQ, rb0 + w, s, lane), st + kB2BBytes + w * 1024);
-    dma16(uv.nib + a16_nib_offset(nGQ, rb0 + w, s, lane), st + kB2BBytes + (8 + w) * 1024);
-    // scales of (gate tile w, up tile w): 128 bytes each, lanes 0..7 and 8..15
-    // (only 16 lanes write: 256 bytes at the wave's own place)
+    for (int m = 0; m < 4; ++m) dma16(src + rowo[m] + s * kQuadCols, st + (w + 8 * m) * 1024);
+    dma16(v0.nib + a16_nib_offset(nGQ, t0, s, lane), st + kB2BBytes + 2 * w * 1024);
+    dma16(v1.nib + a16_nib_offset(nGQ, t1, s, lane), st + kB2BBytes + (2 * w + 1) * 1024);
+    // scales of the two chunks: 128 bytes each, lanes 0..7 and 8..15 (only
+    // 16 lanes write: 256 bytes at the wave's own place)
     if (lane < 16)
-      dma16(reinterpret_cast<const unsigned char*>(sv.sc + a16_sc_offset(nGQ, rb0 + w, s, 0)) +
+      dma16(reinterpret_cast<const unsigned char*>(sv.sc + a16_sc_offset(nGQ, st_, s, 0)) +
                 (lane & 7) * 16,
             st + kB2BBytes + kB2ABytes + w * 256);
   };
@@ -608,64 +550,71 @@ __global__ __launch_bounds__(kB2Threads) void k_gu_big2(GroupArgs g) {
 #pragma unroll
     for (int ct = 0; ct < kNCT; ++ct) acc[t][ct] = f32x4{0, 0, 0, 0};
   issue(0, 0);
-  if (ns > 1) issue(1, 1);
-  for (int s = 0; s < ns; ++s) {
-    // this wave's loads of stage s have landed (one later stage may be in flight)
+  if (nst > 1) issue(1, 1);
+  for (int ps = 0; ps < nst; ++ps) {
+    // this wave's loads of stage ps have landed (one later stage may be in flight)
     static_assert(kB2DmaPerStage == 7, "the wait below counts one stage of 7 loads");
-    if (s + 1 < ns)
+    if (ps + 1 < nst)
       asm volatile("s_waitcnt vmcnt(7)" ::: "memory");
     else
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    // every wave's loads of stage s have landed, and every wave has finished
-    // reading stage s - 1 (whose buffer the next issue overwrites)
+    // every wave's loads of stage ps have landed, and every wave has finished
+    // reading stage ps - 1 (whose buffer the next issue overwrites)
     __builtin_amdgcn_s_barrier();
-    if (s + 2 < ns) issue(s + 2, (s + 2) % kB2Stages);
-    const unsigned char* st = lds2 + (s % kB2Stages) * kB2Stage;
-    const uint4 cg = *reinterpret_cast<const uint4*>(st + kB2BBytes + w * 1024 + lane * 16);
-    const uint4 cu = *reinterpret_cast<const uint4*>(st + kB2BBytes + (8 + w) * 1024 + lane * 16);
-    const uint2 sgs = *reinterpret_cast<const uint2*>(st + kB2BBytes + kB2ABytes + w * 256 + j * 8);
-    const uint2 sus =
+    if (ps + 2 < nst) issue(ps + 2, (ps + 2) % kB2Stages);
+    const unsigned char* st = lds2 + (ps % kB2Stages) * kB2Stage;
+    const uint4 c0 = *reinterpret_cast<const uint4*>(st + kB2BBytes + 2 * w * 1024 + lane * 16);
+    const uint4 c1 =
+        *reinterpret_cast<const uint4*>(st + kB2BBytes + (2 * w + 1) * 1024 + lane * 16);
+    const uint2 s0 = *reinterpret_cast<const uint2*>(st + kB2BBytes + kB2ABytes + w * 256 + j * 8);
+    const uint2 s1 =
         *reinterpret_cast<const uint2*>(st + kB2BBytes + kB2ABytes + w * 256 + 128 + j * 8);
+    // The 8 B fragments of k-group kk + 1 are read while kk computes.
+    bf16x8 bc[kNCT], bn[kNCT];
+    const uint32_t bp = lds_addr(st + j * kB2RowBytes);
+    lds_read8(bp + (q ^ j) * 16, bc);
 #pragma unroll
     for (int kk = 0; kk < kGroupsPerQuad; ++kk) {
-      const bf16x8 ag = dequant8(word_of(cg, kk), scale_of(sgs, kk));
-      const bf16x8 au = dequant8(word_of(cu, kk), scale_of(sus, kk));
-      const int sg = (4 * kk + q) ^ j;
+      if (kk + 1 < kGroupsPerQuad) lds_read8(bp + ((4 * (kk + 1) + q) ^ j) * 16, bn);
+      const bf16x8 a0 = dequant8(word_of(c0, kk), scale_of(s0, kk));
+      const bf16x8 a1 = dequant8(word_of(c1, kk), scale_of(s1, kk));
+      if (kk + 1 < kGroupsPerQuad)
+        lds_wait8<kNCT>(bc);
+      else
+        lds_wait8<0>(bc);
 #pragma unroll
       for (int ct = 0; ct < kNCT; ++ct) {
-        const bf16x8 b =
-            *reinterpret_cast<const bf16x8*>(st + (ct * 16 + j) * kB2RowBytes + sg * 16);
-        acc[0][ct] = mfma16(ag, b, acc[0][ct]);
-        acc[1][ct] = mfma16(au, b, acc[1][ct]);
+        acc[0][ct] = mfma16(a0, bc[ct], acc[0][ct]);
+        acc[1][ct] = mfma16(a1, bc[ct], acc[1][ct]);
+      }
+      if (kk + 1 < kGroupsPerQuad) {
+#pragma unroll
+        for (int ct = 0; ct < kNCT; ++ct) bc[ct] = bn[ct];
       }
     }
   }
-  gu_epilogue<2, kNCT>(g, ut, I, fb * 128 + 16 * w, q, j, acc);
+  if (GU)
+    gu_epilogue<2, kNCT>(g, ut, I, fb * 128 + 16 * w, q, j, acc);
+  else if (fb * 256 + 32 * w < H)
+    down_epilogue<2, kNCT>(g, ut, I, fb * 256 + 32 * w, q, j, acc);
 }
 
-__global__ __launch_bounds__(kGThreads) void k_down_big(GroupArgs g) {
-  extern __shared__ __attribute__((aligned(16))) uint16_t glds[];
-  int ui, rbk;
-  if (!big_item(blockIdx.x, g.meta[1], (g.L.H + 255) / 256, ui, rbk)) return;
-  const UnitTokens ut = unit_tokens(g.units[ui], g.off, g.L.E, g.T, kMT);
-  const LayerDev& L = g.L;
-  const int H = L.H, I = ut.shared ? L.Ish : L.I;
-  const int tid = threadIdx.x, w = gwave_id(), lane = tid & 63, q = lane >> 4, j = lane & 15;
-  const int row0 = rbk * 256 + 64 * w;
-  const bool active = row0 < H;
-  const int rb0 = active ? row0 / kTileRows : 0;
-  const size_t mat = (size_t)H * I;
-  const ExpertView dv = ut.shared ? ExpertView{L.sd_nib, L.sd_sc, H, I}
-                                  : ExpertView{L.d_nib + (size_t)ut.e * (mat / 2),
-                                               L.d_sc + (size_t)ut.e * (mat / kGroup), H, I};
-  int roff[kNCT];
-  const int seg = tid & 15, srow = tid >> 4;
-#pragma unroll
-  for (int i = 0; i < kNCT; ++i) roff[i] = (ut.p0 + min(srow + 16 * i, ut.n - 1)) * I + seg * 8;
-  f32x4 acc[4][kNCT];
-  big_loop<true, false>(glds, dv, dv, rb0, active, ut.shared ? g.hsh : g.hrh,
-                        ut.shared ? g.hsl : g.hrl, roff, I / kQuadCols, acc);
-  if (active) down_epilogue<4, kNCT>(g, ut, I, row0, q, j, acc);
+// k_big's LDS (150 KB) is above the default limit of a launch: raised once
+// per device.
+static hipError_t big_attrs() {
+  static std::atomic<uint64_t> done{0};
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  const uint64_t bit = dev < 64 ? 1ull << dev : 0;
+  if (bit && (done.load() & bit)) return hipSuccess;
+  e = hipFuncSetAttribute(reinterpret_cast<const void*>(k_big<true>),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)kB2Lds);
+  if (e == hipSuccess)
+    e = hipFuncSetAttribute(reinterpret_cast<const void*>(k_big<false>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)kB2Lds);
+  if (e == hipSuccess) done.fetch_or(bit);
+  return e;
 }
 
 // ---------------------------------------------------------------------------
@@ -810,22 +759,17 @@ hipError_t launch_experts_grouped(const LayerDev& L, const uint16_t* xhi, const 
   // units of more than 2 * kSmallMax tokens need T > 2 * kSmallMax
   const bool big = T > 2 * kSmallMax;
   if (big) {
-    // I and Ish are multiples of 128 (checked at upload): every block of
-    // k_gu_big2 is a whole 128-feature block.  Exactly one of the two
-    // kernels does the work, chosen on the device by the need-lo flag.
-    static const hipError_t attr = hipFuncSetAttribute(
-        reinterpret_cast<const void*>(k_gu_big2), hipFuncAttributeMaxDynamicSharedMemorySize,
-        (int)kB2Lds);
-    if (attr != hipSuccess) return attr;
-    const int gsz = big_grid(nbig, (imax + 127) / 128);
-    hipLaunchKernelGGL(k_gu_big2, dim3(gsz), dim3(kB2Threads), kB2Lds, st, g);
-    hipLaunchKernelGGL(k_gu_big, dim3(gsz), dim3(kGThreads), kBigLds, st, g);
+    const hipError_t e = big_attrs();
+    if (e != hipSuccess) return e;
   }
+  if (big)
+    hipLaunchKernelGGL(k_big<true>, dim3(big_grid(nbig, (imax + 127) / 128)), dim3(kB2Threads),
+                       kB2Lds, st, g);
   hipLaunchKernelGGL(k_gu_small, dim3(nsmall, (imax + kSmallGuCols - 1) / kSmallGuCols),
                      dim3(kGThreads), 0, st, g);
   if (big)
-    hipLaunchKernelGGL(k_down_big, dim3(big_grid(nbig, (L.H + 255) / 256)), dim3(kGThreads),
-                       kBigLds, st, g);
+    hipLaunchKernelGGL(k_big<false>, dim3(big_grid(nbig, (L.H + 255) / 256)), dim3(kB2Threads),
+                       kB2Lds, st, g);
   hipLaunchKernelGGL(k_down_small, dim3(nsmall, (L.H + kSmallDnRows - 1) / kSmallDnRows),
                      dim3(kGThreads), 0, st, g);
   return hipGetLastError();
