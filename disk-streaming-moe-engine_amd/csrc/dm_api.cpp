@@ -317,6 +317,8 @@ dm::NormSpec layer_norm(const dmh_ctx* ctx, const Layer* Ly, float eps, bool tre
 // Token counts from which the router runs on the matrix cores (bf16
 // activations); below it the lane-chain router is as fast.
 constexpr int kMfmaRouterMinTokens = 64;
+// need-lo flag, then the front end's token counter and per-token counters
+constexpr int kFlagInts = 2 + dm::kFrontMaxT + 1;
 
 // Device scratch of one run_block call.  Which buffers a call touches
 // depends on its path: the fused decode kernel none of them; the
@@ -329,7 +331,9 @@ struct BlockScratch {
   int32_t* off = nullptr;     // [E+1] expert offsets
   int32_t* perm = nullptr;    // [T*K] assignments in expert order
   int32_t* meta = nullptr;    // [2] unit counts
-  int32_t* needlo = nullptr;  // [1] zero on entry; the combine clears it again
+  int32_t* needlo = nullptr;  // [kFlagInts] zero on entry: the need-lo flag (the combine
+                              // clears it again) and the front-end arrival counters
+                              // (reset by the front-end kernel itself)
   int2* units = nullptr;      // [group_units_max(T, K, E)]
   uint16_t* xhi = nullptr;    // [T][H] bf16 hi parts of x
   uint16_t* xlo = nullptr;    // [T][H] bf16 lo parts
@@ -358,7 +362,7 @@ size_t scratch_carve(const LayerDev& L, int T, bool norm, uint8_t* base, BlockSc
     t.off = (int32_t*)take((size_t)(L.E + 1) * 4);
     t.perm = (int32_t*)take(TK * 4);
     t.meta = (int32_t*)take(2 * 4);
-    t.needlo = (int32_t*)take(4);
+    t.needlo = (int32_t*)take(kFlagInts * 4);
     t.units = (int2*)take((size_t)dm::group_units_max(T, L.K, L.E) * sizeof(int2));
     t.xhi = (uint16_t*)take(TH * 2);
     t.xlo = (uint16_t*)take(TH * 2);
@@ -391,9 +395,9 @@ hipError_t ctx_scratch(dmh_ctx* ctx, const LayerDev& L, int T, bool norm, BlockS
   if ((e = ctx->g_perm.ensure(TK)) != hipSuccess) return e;
   if ((e = ctx->g_meta.ensure(2)) != hipSuccess) return e;
   const size_t nl_cap = ctx->g_needlo.cap;
-  if ((e = ctx->g_needlo.ensure(1)) != hipSuccess) return e;
+  if ((e = ctx->g_needlo.ensure(kFlagInts)) != hipSuccess) return e;
   if (ctx->g_needlo.cap != nl_cap &&
-      (e = hipMemsetAsync(ctx->g_needlo.p, 0, sizeof(int), ctx->cur)) != hipSuccess)
+      (e = hipMemsetAsync(ctx->g_needlo.p, 0, kFlagInts * sizeof(int), ctx->cur)) != hipSuccess)
     return e;
   if ((e = ctx->g_units.ensure(dm::group_units_max(T, L.K, L.E))) != hipSuccess) return e;
   if ((e = ctx->g_xhi.ensure(TH)) != hipSuccess) return e;
@@ -468,6 +472,20 @@ hipError_t run_block(dmh_ctx* ctx, Layer* Ly, int layer, const float* dx, const 
     // several tokens: route, group the assignments by expert and run each
     // expert's tokens together as a grouped GEMM
     const size_t TK = (size_t)T * L.K, TH = (size_t)T * L.H;
+    if (T < kMfmaRouterMinTokens && dm::front_supported(L, T)) {
+      // split, router, selection and grouping in one launch
+      if ((e = dm::launch_front(L, dx, T, sc->z, sc->xhi, sc->xlo, sc->needlo, dids, dprobs, dshg,
+                                sc->off, sc->perm, sc->units, sc->meta, status, st)) !=
+          hipSuccess)
+        return e;
+      if ((e = dm::launch_experts_grouped(L, sc->xhi, sc->xlo, sc->needlo, sc->off, sc->perm,
+                                          sc->units, sc->meta, T, sc->hr, sc->hr + TK * L.I,
+                                          sc->hs, sc->hs + (size_t)T * L.Ish, sc->r, sc->rs,
+                                          status, st)) != hipSuccess)
+        return e;
+      return dm::launch_combine(sc->r, sc->rs, dprobs, dshg, dres, T, L.H, L.K, dy, status, st,
+                                sc->needlo);
+    }
     if ((e = dm::launch_split_rows(dx, (int64_t)TH, sc->xhi, sc->xlo, sc->needlo, st)) !=
         hipSuccess)
       return e;
@@ -1126,8 +1144,9 @@ int dmh_moe_forward_noalloc(dmh_ctx* c, int layer, const float* x, const float* 
   if (!ids) { ids = (int32_t*)(base + off); off += align256(TK * 4); }
   if (!probs) { probs = (float*)(base + off); off += align256(TK * 4); }
   if (!shg) { shg = (float*)(base + off); off += align256((size_t)T * 4); }
-  // the need-lo flag starts at zero (a call that failed may have left it set)
-  if (sc.needlo) HIP_TRY(dm::launch_fill_i32(sc.needlo, 1, 0, c->cur));
+  // the need-lo flag and the front-end counter start at zero (a call that
+  // failed may have left the flag set)
+  if (sc.needlo) HIP_TRY(dm::launch_fill_i32(sc.needlo, kFlagInts, 0, c->cur));
   HIP_TRY(run_block(c, Ly, layer, x, residual, T, y, ids, probs, shg, true, nullptr, &sc));
   c->last_ids[layer] = ids;
   c->last_k[layer] = L.K;

@@ -325,38 +325,6 @@ __device__ __forceinline__ void select_keys(const uint32_t (&key)[NK], int round
   }
 }
 
-// One step of a wave-wide top-8 reduction: every lane holds 8 keys in
-// descending order; it takes the 8 keys of the lane the DPP control names
-// (in reverse order), keeps the elementwise maxima (a bitonic sequence that
-// holds the 8 largest of the 16) and sorts them with a bitonic network.
-// Lanes without a source lane take zeros (no keys).  The shift and row
-// broadcast controls of the usual reduction leave the top 8 of all lanes in
-// lane 63.
-template <int CTRL, int RM>
-__device__ __forceinline__ void top8_step(uint32_t (&a)[8]) {
-  uint32_t c[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const uint32_t bv = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)a[7 - i], CTRL, RM, 0xF, false);
-    c[i] = a[i] > bv ? a[i] : bv;
-  }
-  auto cx = [](uint32_t& p, uint32_t& q) {  // p >= q afterwards
-    const uint32_t hi = p > q ? p : q, lo = p > q ? q : p;
-    p = hi;
-    q = lo;
-  };
-#pragma unroll
-  for (int i = 0; i < 4; ++i) cx(c[i], c[i + 4]);
-  cx(c[0], c[2]);
-  cx(c[1], c[3]);
-  cx(c[4], c[6]);
-  cx(c[5], c[7]);
-#pragma unroll
-  for (int i = 0; i < 8; i += 2) cx(c[i], c[i + 1]);
-#pragma unroll
-  for (int i = 0; i < 8; ++i) a[i] = c[i];
-}
-
 template <int R>
 __device__ __forceinline__ void issue_logits(const uint64_t* zt, int E, bool gate,
                                              uint64_t (&v)[4 * R + 1]) {

@@ -152,6 +152,12 @@ __device__ __forceinline__ void st_coh(float* p, float v) {
 __device__ __forceinline__ float ld_coh(const float* p) {
   return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+__device__ __forceinline__ void st_coh_i32(int32_t* p, int32_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ int32_t ld_coh_i32(const int32_t* p) {
+  return __hip_atomic_load(const_cast<int32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 __device__ __forceinline__ unsigned ld_coh_u32(const unsigned* p) {
   return __hip_atomic_load(const_cast<unsigned*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -223,22 +229,20 @@ __device__ __forceinline__ bool wait_count(const unsigned* c, unsigned target,
 __device__ __forceinline__ float seq_sum(const float* v, int n) {
   float s = 0.0f;
   const float4* v4 = reinterpret_cast<const float4*>(v);
-  const int n4 = n >> 2;
-  for (int b0 = 0; b0 < n4; b0 += 16) {
-    float4 t[16];
+  const int n32 = n & ~31;
+  for (int k = 0; k < n32 / 4; k += 8) {  // eight float4 read ahead of their adds
+    float4 t[8];
 #pragma unroll
-    for (int u = 0; u < 16; ++u) t[u] = b0 + u < n4 ? v4[b0 + u] : make_float4(0, 0, 0, 0);
+    for (int u = 0; u < 8; ++u) t[u] = v4[k + u];
 #pragma unroll
-    for (int u = 0; u < 16; ++u) {
-      if (b0 + u < n4) {
-        s = s + t[u].x;
-        s = s + t[u].y;
-        s = s + t[u].z;
-        s = s + t[u].w;
-      }
+    for (int u = 0; u < 8; ++u) {
+      s = s + t[u].x;
+      s = s + t[u].y;
+      s = s + t[u].z;
+      s = s + t[u].w;
     }
   }
-  for (int e = n4 * 4; e < n; ++e) s = s + v[e];
+  for (int e = n32; e < n; ++e) s = s + v[e];
   return s;
 }
 
@@ -308,6 +312,246 @@ __device__ __forceinline__ void fold_cols(f32x4& acc) {
         float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, true));
     acc[i] = v + o;
   }
+}
+
+// One step of a wave-wide top-8 reduction: every lane holds 8 keys in
+// descending order; it takes the 8 keys of the lane the DPP control names
+// (in reverse order), keeps the elementwise maxima (a bitonic sequence that
+// holds the 8 largest of the 16) and sorts them with a bitonic network.
+// Lanes without a source lane take zeros (no keys).  The shift and row
+// broadcast controls of the usual reduction leave the top 8 of all lanes in
+// lane 63.
+template <int CTRL, int RM>
+__device__ __forceinline__ void top8_step(uint32_t (&a)[8]) {
+  uint32_t c[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const uint32_t bv = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)a[7 - i], CTRL, RM, 0xF, false);
+    c[i] = a[i] > bv ? a[i] : bv;
+  }
+  auto cx = [](uint32_t& p, uint32_t& q) {  // p >= q afterwards
+    const uint32_t hi = p > q ? p : q, lo = p > q ? q : p;
+    p = hi;
+    q = lo;
+  };
+#pragma unroll
+  for (int i = 0; i < 4; ++i) cx(c[i], c[i + 4]);
+  cx(c[0], c[2]);
+  cx(c[1], c[3]);
+  cx(c[4], c[6]);
+  cx(c[5], c[7]);
+#pragma unroll
+  for (int i = 0; i < 8; i += 2) cx(c[i], c[i + 1]);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) a[i] = c[i];
+}
+
+// ---- softmax + top-k + shared gate of one token ------------------------------
+// router_softmax (src/layers/router.mojo:140-183: sequential max, exp, sum,
+// p = e * (1/sum)) and select_topk (src/layers/topk.mojo:79-128: largest p,
+// lowest expert id on ties, K rounds; sum and renormalisation-leak checks).
+__device__ __forceinline__ bool better(float va, int ia, float vb, int ib) {
+  return va > vb || (va == vb && ia < ib);
+}
+
+// NE values per lane: element e = lane + 64 i.  Probabilities stay in
+// registers; each selection round is two wave-wide maxima: of the key
+// f2u(p) + 1 (p >= 0, so its bits order like p; 0 marks "no candidate") and,
+// among the lanes holding that key, of 0xFFFF - e (the lowest expert id).
+// Token t on one wave (lane 0..63), with sm (((E + 3) & ~3) + 4 floats of
+// LDS) its own; sync() orders the wave's LDS writes before reads by other
+// lanes (a workgroup barrier when the wave is the whole workgroup).  COH:
+// the logits are read, and the ids written, with agent-scope accesses
+// (producer and consumer are other workgroups of the same launch).
+template <int NE, bool COH, class Sync>
+__device__ __forceinline__ void route_select_token(const float* __restrict__ z, int ldz, int E,
+                                                   int K, int has_sh, int t, int lane, float* sm,
+                                                   int32_t* __restrict__ ids,
+                                                   float* __restrict__ probs,
+                                                   float* __restrict__ shg,
+                                                   unsigned long long* status, Sync sync) {
+  float* pv = sm;
+  float* scal = sm + ((E + 3) & ~3);
+  const float* zr = z + (size_t)t * ldz;
+  // the shared-gate logit is requested with the others: a load issued after
+  // the stores below would wait for them
+  const float lg = has_sh && lane == 0 ? (COH ? ld_coh(zr + E) : zr[E]) : 0.0f;
+  float zv[NE];
+  float m = -__builtin_inff();
+#pragma unroll
+  for (int i = 0; i < NE; ++i) {
+    const int e = lane + 64 * i;
+    zv[i] = e < E ? (COH ? ld_coh(zr + e) : zr[e]) : -__builtin_inff();
+    if (e < E && !finite_f(zv[i])) record_err(status, err_key(kPhLogit, t, 0, e, 0));
+    m = zv[i] > m ? zv[i] : m;
+  }
+  m = __ockl_wfred_max_f32(m);
+  if (lane == 0 && !finite_f(m)) record_err(status, err_key(kPhSoftmax, t, 0, 0, 0));
+  float p[NE];
+#pragma unroll
+  for (int i = 0; i < NE; ++i) {
+    const int e = lane + 64 * i;
+    if (e < E) {
+      p[i] = dm_expf(zv[i] - m);
+      if (!finite_f(p[i])) record_err(status, err_key(kPhSoftmax, t, 0, 1 + e, 0));
+      pv[e] = p[i];
+    }
+  }
+  sync();
+  if (lane == 0) {
+    const float s = seq_sum(pv, E);
+    if (!(s > 0.0f) || !finite_f(s)) record_err(status, err_key(kPhSoftmax, t, 0, 1 + E, 0));
+    scal[0] = 1.0f / s;
+  }
+  sync();
+  const float inv = scal[0];
+  uint32_t key[NE];
+#pragma unroll
+  for (int i = 0; i < NE; ++i) {
+    const int e = lane + 64 * i;
+    p[i] = p[i] * inv;
+    key[i] = e < E ? f2u(p[i]) + 1u : 0u;
+  }
+  sync();  // pv is rewritten with the probabilities for the leak check
+#pragma unroll
+  for (int i = 0; i < NE; ++i)
+    if (lane + 64 * i < E) pv[lane + 64 * i] = p[i];
+  float sum_topk = 0.0f;
+  bool done = false;
+  if constexpr (NE <= 4) {
+    // Fast path (E <= 256, K <= 8): one wave-wide top-8 reduction of 32-bit
+    // keys, the probability bits with their low 8 bits replaced by 255 - e.
+    // It is the exact selection when the truncated probabilities of the K
+    // selected experts and of the best unselected one are strictly
+    // decreasing (no tie or near tie the truncation could reorder) and the
+    // K-th is nonzero; otherwise the K exact rounds below run.
+    if (K <= 8) {
+      uint32_t k4[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int e = lane + 64 * i;
+        k4[i] = i < NE && e < E ? ((key[i < NE ? i : 0] >> 8) << 8) | (255u - (uint32_t)e) : 0u;
+      }
+      auto cx = [](uint32_t& a, uint32_t& b) {  // a >= b afterwards
+        const uint32_t hi = a > b ? a : b, lo = a > b ? b : a;
+        a = hi;
+        b = lo;
+      };
+      cx(k4[0], k4[1]);
+      cx(k4[2], k4[3]);
+      cx(k4[0], k4[2]);
+      cx(k4[1], k4[3]);
+      cx(k4[1], k4[2]);
+      uint32_t a[8] = {k4[0], k4[1], k4[2], k4[3], 0u, 0u, 0u, 0u};
+      top8_step<0x111, 0xF>(a);
+      top8_step<0x112, 0xF>(a);
+      top8_step<0x114, 0xF>(a);
+      top8_step<0x118, 0xF>(a);
+      top8_step<0x142, 0xA>(a);
+      top8_step<0x143, 0xC>(a);
+      uint32_t T[9];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) T[i] = __builtin_amdgcn_readlane(a[i], 63);
+      T[8] = 0u;
+      if (K == 8 && K < E) {  // the largest key outside the top 8
+        const uint32_t t7 = T[7];
+        const uint32_t c = k4[0] < t7 ? k4[0] : k4[1] < t7 ? k4[1] : k4[2] < t7 ? k4[2]
+                         : k4[3] < t7 ? k4[3] : 0u;
+        T[8] = wave_max_u32(c);
+      }
+      bool clean = true;
+#pragma unroll
+      for (int r = 0; r < 8; ++r)
+        if (r < K) clean = clean && (T[r] >> 8) > (T[r + 1] >> 8);
+      if (clean) {
+        sync();  // pv (the probabilities) is read by other lanes
+        // lane r < K reads and writes rank r; lane 0 sums them in rank order
+        int win = 0;
+#pragma unroll
+        for (int r = 0; r < 8; ++r) win = lane == r ? 255 - (int)(T[r] & 255u) : win;
+        const float bv = lane < K ? pv[win] : 0.0f;
+        if (lane < K) {
+          if (COH)
+            st_coh_i32(ids + (size_t)t * K + lane, win);
+          else
+            ids[(size_t)t * K + lane] = win;
+          probs[(size_t)t * K + lane] = bv;
+        }
+#pragma unroll
+        for (int r = 0; r < 8; ++r)
+          if (r < K) sum_topk = sum_topk + u2f(__builtin_amdgcn_readlane(f2u(bv), r));
+        done = true;
+      }
+    }
+  }
+  for (int r = 0; r < K && !done; ++r) {
+    uint32_t bk = 0;
+    int bi = 0xFFFF;
+#pragma unroll
+    for (int i = 0; i < NE; ++i)  // ascending e within the lane: first of equal keys wins
+      if (key[i] > bk) { bk = key[i]; bi = lane + 64 * i; }
+    const uint32_t mk = __ockl_wfred_max_u32(bk);
+    const uint32_t me = __ockl_wfred_max_u32(bk == mk && mk != 0u ? 0xFFFFu - (uint32_t)bi : 0u);
+    int win = (int)(0xFFFFu - me);
+    if (mk == 0u || win < 0 || win >= E) win = 0;  // only reachable after a recorded error
+    const float bv = u2f(mk - 1u);
+#pragma unroll
+    for (int i = 0; i < NE; ++i)
+      if (lane + 64 * i == win) key[i] = 0u;
+    sum_topk = sum_topk + bv;
+    if (lane == 0) {
+      if (COH)
+        st_coh_i32(ids + (size_t)t * K + r, win);
+      else
+        ids[(size_t)t * K + r] = win;
+      probs[(size_t)t * K + r] = bv;
+    }
+  }
+  if (lane == 0) {
+    if (sum_topk > 1.00001f) record_err(status, err_key(kPhTopk, t, 0, 0, kTkSum));
+    if (K < E && __builtin_fabsf(sum_topk - 1.0f) < 1e-6f) {
+      const float sum_all = seq_sum(pv, E);
+      if (sum_all - sum_topk > 1e-5f) record_err(status, err_key(kPhTopk, t, 0, 0, kTkLeak));
+    }
+    if (has_sh) {
+      if (!finite_f(lg)) record_err(status, err_key(kPhGate, t, 0, 0, kGkLogit));
+      const float s = dm_sigmoid(lg);
+      if (!finite_f(s) || s < 0.0f || s > 1.0f)
+        record_err(status, err_key(kPhGate, t, 0, 0, kGkRange));
+      shg[t] = s;
+    }
+  }
+}
+
+
+// One router logit chain of the R16 layer form: row e, lane partial l of
+// router_project (src/layers/router.mojo:80-104): k = l, l + 16, ... with
+// separate multiply and add, x (one token, fp32) staged in LDS.
+// The weights are requested eight 128-column chunks at a time (clamped
+// loads, all in flight together) ahead of their multiply-adds.
+__device__ __forceinline__ float router_chain(const uint16_t* __restrict__ router, int H, int e,
+                                              int l, const float* xs) {
+  float acc = 0.0f;
+  const uint4* wp = reinterpret_cast<const uint4*>(router + r16_index(H, e, l));
+  const int nj8 = H / 128;
+  for (int j0 = 0; j0 < nj8; j0 += 8) {
+    uint4 w[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) w[u] = wp[(size_t)min(j0 + u, nj8 - 1) * 16];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      if (j0 + u < nj8) {  // uniform
+        const uint32_t ww[4] = {w[u].x, w[u].y, w[u].z, w[u].w};
+        const float* xc = xs + (j0 + u) * 128 + l;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          acc = acc + xc[(2 * i) * 16] * bf16lo(ww[i]);
+          acc = acc + xc[(2 * i + 1) * 16] * bf16hi(ww[i]);
+        }
+      }
+    }
+  }
+  return acc;
 }
 
 }  // namespace dm

@@ -14,6 +14,20 @@ int group_units_max(int T, int K, int E);
 hipError_t launch_group_build(const int32_t* ids, int T, int K, int E, int32_t* off,
                               int32_t* perm, int2* units, int32_t* meta, hipStream_t st);
 
+// The front end of a small batch in one launch: x -> bf16 hi / lo rows and
+// need-lo (flags[0]), router logits z [T][E+1] in the layer order, softmax /
+// top-k / shared gate (ids, probs, shg) and the grouping (off, perm, units,
+// meta) -- the work of launch_split_rows, launch_router_dec,
+// launch_router_select and launch_group_build.  flags[1 .. 2 + T) are
+// arrival counters that must be zero on entry and are zero again on exit.
+constexpr int kFrontMaxT = 63;
+constexpr int kFrontMaxE = 512;
+bool front_supported(const LayerDev& L, int T);
+hipError_t launch_front(const LayerDev& L, const float* x, int T, float* z, uint16_t* xhi,
+                        uint16_t* xlo, int* flags, int32_t* ids, float* probs, float* shg,
+                        int32_t* off, int32_t* perm, int2* units, int32_t* meta,
+                        unsigned long long* status, hipStream_t st);
+
 // n fp32 values (n % 8 == 0) -> bf16 hi / lo; *need_lo |= 1 if a lo part is nonzero
 // (the caller zeroes *need_lo first).
 hipError_t launch_split_rows(const float* x, int64_t n, uint16_t* hi, uint16_t* lo, int* need_lo,

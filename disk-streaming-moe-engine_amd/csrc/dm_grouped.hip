@@ -58,21 +58,37 @@ __device__ __forceinline__ void unit_split(int c, int& nf, int& pb, int& ps) {
   ps = (r > 0 && r <= 2 * kSmallMax) ? (r + kSmallMax - 1) / kSmallMax : 0;
 }
 
-__global__ __launch_bounds__(1024) void k_group_build(const int32_t* __restrict__ ids, int T, int K,
-                                                      int E, int32_t* __restrict__ off,
-                                                      int32_t* __restrict__ perm,
-                                                      int2* __restrict__ units,
-                                                      int32_t* __restrict__ meta) {
-  // cnt[E] | cur[E] | 4 scans of 1024: counts, full units, partial big, small
-  extern __shared__ int lds[];
+// The grouping on one workgroup of 1024 threads, lds: (2 E + 64) ints.
+// COH: ids are read with agent-scope loads (written in the same launch).
+template <bool COH>
+__device__ __forceinline__ void group_build_wg(const int32_t* __restrict__ ids, int T, int K, int E,
+                                               int32_t* __restrict__ off,
+                                               int32_t* __restrict__ perm,
+                                               int2* __restrict__ units,
+                                               int32_t* __restrict__ meta, int* lds) {
+  // cnt[E] | cur[E] | wave totals of the 4 scans (counts, full units,
+  // partial big, small units), 16 waves each
   int* cnt = lds;
   int* cur = lds + E;
   int* sc = lds + 2 * E;
   const int tid = threadIdx.x, TK = T * K;
   for (int e = tid; e < E; e += 1024) cnt[e] = 0;
   __syncthreads();
-  for (int a = tid; a < TK; a += 1024) {
-    const int e = min(max((int)ids[a], 0), E - 1);
+  // the first kCache expert ids of this thread stay in registers for the
+  // scatter below (a load issued after the stores of the units would wait
+  // for them)
+  constexpr int kCache = 16;
+  int ec[kCache];
+#pragma unroll
+  for (int i = 0; i < kCache; ++i) {
+    const int a = tid + 1024 * i;
+    ec[i] = a < TK ? min(max((int)(COH ? ld_coh_i32(ids + a) : ids[a]), 0), E - 1) : 0;
+  }
+#pragma unroll
+  for (int i = 0; i < kCache; ++i)
+    if (tid + 1024 * i < TK) atomicAdd(&cnt[ec[i]], 1);
+  for (int a = tid + 1024 * kCache; a < TK; a += 1024) {
+    const int e = min(max((int)(COH ? ld_coh_i32(ids + a) : ids[a]), 0), E - 1);
     atomicAdd(&cnt[e], 1);
   }
   __syncthreads();
@@ -87,24 +103,40 @@ __global__ __launch_bounds__(1024) void k_group_build(const int32_t* __restrict_
     v[2] += pb;
     v[3] += ps;
   }
+  // exclusive prefix sums of the four counts over the threads: inclusive
+  // scans inside each wave (shuffles), then the 16 wave totals from LDS
+  const int lane = tid & 63, wv = tid >> 6;
+  int incl[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) sc[i * 1024 + tid] = v[i];
-  __syncthreads();
-  for (int d = 1; d < 1024; d <<= 1) {  // inclusive Hillis-Steele scans
-    int a[4];
+  for (int i = 0; i < 4; ++i) {
+    int a = v[i];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) a[i] = tid >= d ? sc[i * 1024 + tid - d] : 0;
-    __syncthreads();
-#pragma unroll
-    for (int i = 0; i < 4; ++i) sc[i * 1024 + tid] += a[i];
-    __syncthreads();
+    for (int d = 1; d < 64; d <<= 1) {
+      const int o = __shfl_up(a, d, 64);
+      a += lane >= d ? o : 0;
+    }
+    incl[i] = a;
+    if (lane == 63) sc[i * 16 + wv] = a;
   }
-  const int nf = sc[1024 + 1023], npb = sc[2048 + 1023], nps = sc[3072 + 1023];
+  __syncthreads();
+  int pre[4], tot[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    int p = 0, t = 0;
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      const int wt = sc[i * 16 + u];
+      p += u < wv ? wt : 0;
+      t += wt;
+    }
+    pre[i] = p + incl[i] - v[i];
+    tot[i] = t;
+  }
+  const int nf = tot[1], npb = tot[2], nps = tot[3];
   int snf, spb, sps;
   unit_split(T, snf, spb, sps);
   const int pb0 = nf + snf, s0 = pb0 + npb + spb;
-  int base = sc[tid] - v[0], fb = sc[1024 + tid] - v[1], pb = pb0 + sc[2048 + tid] - v[2],
-      ps = s0 + sc[3072 + tid] - v[3];
+  int base = pre[0], fb = pre[1], pb = pb0 + pre[2], ps = s0 + pre[3];
   for (int e = e0; e < e1; ++e) {
     int nfe, pbe, pse;
     unit_split(cnt[e], nfe, pbe, pse);
@@ -118,8 +150,13 @@ __global__ __launch_bounds__(1024) void k_group_build(const int32_t* __restrict_
   }
   if (tid == 0) off[E] = TK;
   __syncthreads();
-  for (int a = tid; a < TK; a += 1024) {
-    const int e = min(max((int)ids[a], 0), E - 1);
+#pragma unroll
+  for (int i = 0; i < kCache; ++i) {
+    const int a = tid + 1024 * i;
+    if (a < TK) perm[atomicAdd(&cur[ec[i]], 1)] = a;
+  }
+  for (int a = tid + 1024 * kCache; a < TK; a += 1024) {
+    const int e = min(max((int)(COH ? ld_coh_i32(ids + a) : ids[a]), 0), E - 1);
     perm[atomicAdd(&cur[e], 1)] = a;
   }
   for (int i = tid; i < snf; i += 1024) units[nf + i] = make_int2(E, kMT * i);
@@ -131,11 +168,126 @@ __global__ __launch_bounds__(1024) void k_group_build(const int32_t* __restrict_
   }
 }
 
+__global__ __launch_bounds__(1024) void k_group_build(const int32_t* __restrict__ ids, int T, int K,
+                                                      int E, int32_t* __restrict__ off,
+                                                      int32_t* __restrict__ perm,
+                                                      int2* __restrict__ units,
+                                                      int32_t* __restrict__ meta) {
+  extern __shared__ int lds[];
+  group_build_wg<false>(ids, T, K, E, off, perm, units, meta, lds);
+}
+
 hipError_t launch_group_build(const int32_t* ids, int T, int K, int E, int32_t* off,
                               int32_t* perm, int2* units, int32_t* meta, hipStream_t st) {
-  const size_t lds = (size_t)(2 * E + 4096) * sizeof(int);
+  const size_t lds = (size_t)(2 * E + 64) * sizeof(int);
   hipLaunchKernelGGL(k_group_build, dim3(1), dim3(1024), lds, st, ids, T, K, E, off, perm, units,
                      meta);
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// The front end of a small batch in one launch (T tokens, 2 <= T < 64):
+// workgroup (b, t) stages token t's x in LDS, computes router rows
+// 64 b .. 64 b + 63 (16 lanes each, the chains of router_chain and the
+// halving tree of k_router_dec: the same logits bit for bit), and workgroup
+// (0, t) also writes t's bf16 hi / lo rows and the need-lo flag.  Each
+// workgroup then counts itself in token t's counter flags[2 + t]; the last
+// of them (the logits are written and read at the device-coherent level, so
+// that those of workgroups on other XCDs are visible) runs t's softmax /
+// top-k on one wave (route_select_token) and counts the token in flags[1];
+// the last token's workgroup groups the assignments (group_build_wg).  Each
+// counter is reset by the workgroup that saw it complete.  No workgroup
+// waits for another.
+template <int NE>
+__global__ __launch_bounds__(1024) void k_front(LayerDev L, const float* __restrict__ x, int T,
+                                                float* __restrict__ z, uint4* __restrict__ xhi,
+                                                uint4* __restrict__ xlo, int* flags,
+                                                int32_t* __restrict__ ids,
+                                                float* __restrict__ probs,
+                                                float* __restrict__ shg, int32_t* __restrict__ off,
+                                                int32_t* __restrict__ perm,
+                                                int2* __restrict__ units,
+                                                int32_t* __restrict__ meta,
+                                                unsigned long long* status) {
+  extern __shared__ __attribute__((aligned(16))) float fl[];
+  __shared__ int last, last_tok;
+  const int tid = threadIdx.x, H = L.H, E = L.E, t = blockIdx.y;
+  const float* xr = x + (size_t)t * H;
+  bool bad = false;
+  for (int i = tid; i < H; i += 1024) {
+    const float v = xr[i];
+    bad |= !finite_f(v);
+    fl[i] = v;
+  }
+  if (bad && blockIdx.x == 0) record_err(status, err_key(kPhX, 0, 0, 0, 0));
+  if (blockIdx.x == 0) {
+    bool nz = false;
+    for (int i = tid; i < H / 8; i += 1024) {
+      uint4 h, l;
+      split8(xr + 8 * i, h, l);
+      xhi[(size_t)t * (H / 8) + i] = h;
+      xlo[(size_t)t * (H / 8) + i] = l;
+      nz |= (l.x | l.y | l.z | l.w) != 0u;
+    }
+    if (__builtin_amdgcn_ballot_w64(nz) != 0 && (tid & 63) == 0) atomicOr(&flags[0], 1);
+  }
+  __syncthreads();
+  const int l = tid & 15, e = blockIdx.x * 64 + (tid >> 4);
+  float acc = e <= E ? router_chain(L.router, H, e, l, fl) : 0.0f;
+#pragma unroll
+  for (int wdt = 8; wdt >= 1; wdt >>= 1) acc = acc + __shfl_down(acc, wdt, 16);
+  // logits to the device-coherent level (agent-scope stores, complete before
+  // the count), read back by the last workgroup with agent-scope loads: no
+  // write-back or invalidation of the whole L2
+  if (l == 0 && e <= E) st_coh(z + (size_t)t * (E + 1) + e, acc);
+  wait_stores();
+  __syncthreads();
+  // the last of token t's workgroups selects its experts (wave 0) ...
+  if (tid == 0) last = atomicAdd(&flags[2 + t], 1) == (int)gridDim.x - 1;
+  __syncthreads();
+  if (!last) return;
+  const int lane = tid & 63;
+  if (tid < 64) {
+    if (tid == 0) atomicExch(&flags[2 + t], 0);
+    route_select_token<NE, true>(z, E + 1, E, L.K, 1, t, lane, fl, ids, probs, shg, status, [] {
+      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+    });
+    wait_stores();
+    // ... and the last token to be selected groups the assignments
+    if (tid == 0) last_tok = atomicAdd(&flags[1], 1) == T - 1;
+  }
+  __syncthreads();
+  if (!last_tok) return;
+  if (tid == 0) atomicExch(&flags[1], 0);
+  group_build_wg<true>(ids, T, L.K, E, off, perm, units, meta, reinterpret_cast<int*>(fl));
+}
+
+bool front_supported(const LayerDev& L, int T) {
+  return T >= 2 && T <= kFrontMaxT && L.E <= kFrontMaxE && L.H % 128 == 0;
+}
+
+hipError_t launch_front(const LayerDev& L, const float* x, int T, float* z, uint16_t* xhi,
+                        uint16_t* xlo, int* flags, int32_t* ids, float* probs, float* shg,
+                        int32_t* off, int32_t* perm, int2* units, int32_t* meta,
+                        unsigned long long* status, hipStream_t st) {
+  if (!front_supported(L, T)) return hipErrorInvalidValue;
+  const size_t sel = (size_t)(((L.E + 3) & ~3) + 4) * sizeof(float);
+  const size_t bld = (size_t)(2 * L.E + 64) * sizeof(int);
+  const size_t xs = (size_t)L.H * sizeof(float);
+  const size_t lds = sel > bld ? (sel > xs ? sel : xs) : (bld > xs ? bld : xs);
+  const dim3 grid((L.E + 1 + 63) / 64, T);
+  uint4* hi = reinterpret_cast<uint4*>(xhi);
+  uint4* lo = reinterpret_cast<uint4*>(xlo);
+  const int ne = (L.E + 63) / 64;
+#define DM_FRONT(N)                                                                             \
+  hipLaunchKernelGGL(k_front<N>, grid, dim3(1024), lds, st, L, x, T, z, hi, lo, flags, ids, probs, \
+                     shg, off, perm, units, meta, status)
+  if (ne <= 1) DM_FRONT(1);
+  else if (ne <= 2) DM_FRONT(2);
+  else if (ne <= 4) DM_FRONT(4);
+  else DM_FRONT(8);
+#undef DM_FRONT
   return hipGetLastError();
 }
 

@@ -350,21 +350,7 @@ __global__ __launch_bounds__(256) void k_router_dec(LayerDev L, const float* __r
     }
     if (bad && blockIdx.x == 0) record_err(status, err_key(kPhX, 0, 0, 0, 0));
     __syncthreads();
-    float acc = 0.0f;
-    if (e <= L.E) {
-      const uint4* wp = reinterpret_cast<const uint4*>(L.router + r16_index(H, e, l));
-      const int nj8 = H / 128;
-      for (int j8 = 0; j8 < nj8; ++j8) {
-        const uint4 w = wp[(size_t)j8 * 16];
-        const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
-        const float* xc = xs + j8 * 128 + l;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          acc = acc + xc[(2 * i) * 16] * bf16lo(ww[i]);
-          acc = acc + xc[(2 * i + 1) * 16] * bf16hi(ww[i]);
-        }
-      }
-    }
+    float acc = e <= L.E ? router_chain(L.router, H, e, l, xs) : 0.0f;
     // halving tree over the 16 chains of a row: lane l += lane l + w
 #pragma unroll
     for (int wdt = 8; wdt >= 1; wdt >>= 1) acc = acc + __shfl_down(acc, wdt, 16);
@@ -517,19 +503,9 @@ hipError_t launch_router_mfma(const LayerDev& L, const uint16_t* xhi, const int*
 }
 
 // ===========================================================================
-// Softmax + top-k + shared gate, one 64-lane wave per token:
-// router_softmax (src/layers/router.mojo:140-183: sequential max, exp, sum,
-// p = e * (1/sum)) and select_topk (src/layers/topk.mojo:79-128: largest p,
-// lowest expert id on ties, K rounds; sum and renormalisation-leak checks).
+// Softmax + top-k + shared gate, one 64-lane wave per token
+// (route_select_token).
 // ===========================================================================
-__device__ __forceinline__ bool better(float va, int ia, float vb, int ib) {
-  return va > vb || (va == vb && ia < ib);
-}
-
-// NE values per lane: element e = lane + 64 i.  Probabilities stay in
-// registers; each selection round is two wave-wide maxima: of the key
-// f2u(p) + 1 (p >= 0, so its bits order like p; 0 marks "no candidate") and,
-// among the lanes holding that key, of 0xFFFF - e (the lowest expert id).
 template <int NE>
 __global__ __launch_bounds__(64) void k_router_select(const float* __restrict__ z, int ldz, int E,
                                                        int K, int has_sh,
@@ -538,86 +514,8 @@ __global__ __launch_bounds__(64) void k_router_select(const float* __restrict__ 
                                                        float* __restrict__ shg,
                                                        unsigned long long* status) {
   extern __shared__ __attribute__((aligned(16))) float sm[];  // e[E] (padded), then 1/S
-  float* pv = sm;
-  float* scal = sm + ((E + 3) & ~3);
-  const int t = blockIdx.x, lane = threadIdx.x;
-  const float* zr = z + (size_t)t * ldz;
-  float zv[NE];
-  float m = -__builtin_inff();
-#pragma unroll
-  for (int i = 0; i < NE; ++i) {
-    const int e = lane + 64 * i;
-    zv[i] = e < E ? zr[e] : -__builtin_inff();
-    if (e < E && !finite_f(zv[i])) record_err(status, err_key(kPhLogit, t, 0, e, 0));
-    m = zv[i] > m ? zv[i] : m;
-  }
-  m = __ockl_wfred_max_f32(m);
-  if (lane == 0 && !finite_f(m)) record_err(status, err_key(kPhSoftmax, t, 0, 0, 0));
-  float p[NE];
-#pragma unroll
-  for (int i = 0; i < NE; ++i) {
-    const int e = lane + 64 * i;
-    if (e < E) {
-      p[i] = dm_expf(zv[i] - m);
-      if (!finite_f(p[i])) record_err(status, err_key(kPhSoftmax, t, 0, 1 + e, 0));
-      pv[e] = p[i];
-    }
-  }
-  __syncthreads();
-  if (lane == 0) {
-    const float s = seq_sum(pv, E);
-    if (!(s > 0.0f) || !finite_f(s)) record_err(status, err_key(kPhSoftmax, t, 0, 1 + E, 0));
-    scal[0] = 1.0f / s;
-  }
-  __syncthreads();
-  const float inv = scal[0];
-  uint32_t key[NE];
-#pragma unroll
-  for (int i = 0; i < NE; ++i) {
-    const int e = lane + 64 * i;
-    p[i] = p[i] * inv;
-    key[i] = e < E ? f2u(p[i]) + 1u : 0u;
-  }
-  __syncthreads();  // pv is rewritten with the probabilities for the leak check
-#pragma unroll
-  for (int i = 0; i < NE; ++i)
-    if (lane + 64 * i < E) pv[lane + 64 * i] = p[i];
-  float sum_topk = 0.0f;
-  for (int r = 0; r < K; ++r) {
-    uint32_t bk = 0;
-    int bi = 0xFFFF;
-#pragma unroll
-    for (int i = 0; i < NE; ++i)  // ascending e within the lane: first of equal keys wins
-      if (key[i] > bk) { bk = key[i]; bi = lane + 64 * i; }
-    const uint32_t mk = __ockl_wfred_max_u32(bk);
-    const uint32_t me = __ockl_wfred_max_u32(bk == mk && mk != 0u ? 0xFFFFu - (uint32_t)bi : 0u);
-    int win = (int)(0xFFFFu - me);
-    if (mk == 0u || win < 0 || win >= E) win = 0;  // only reachable after a recorded error
-    const float bv = u2f(mk - 1u);
-#pragma unroll
-    for (int i = 0; i < NE; ++i)
-      if (lane + 64 * i == win) key[i] = 0u;
-    sum_topk = sum_topk + bv;
-    if (lane == 0) {
-      ids[(size_t)t * K + r] = win;
-      probs[(size_t)t * K + r] = bv;
-    }
-  }
-  if (lane == 0) {
-    if (sum_topk > 1.00001f) record_err(status, err_key(kPhTopk, t, 0, 0, kTkSum));
-    if (K < E && __builtin_fabsf(sum_topk - 1.0f) < 1e-6f) {
-      const float sum_all = seq_sum(pv, E);
-      if (sum_all - sum_topk > 1e-5f) record_err(status, err_key(kPhTopk, t, 0, 0, kTkLeak));
-    }
-    if (has_sh) {
-      const float lg = zr[E];
-      if (!finite_f(lg)) record_err(status, err_key(kPhGate, t, 0, 0, kGkLogit));
-      const float s = dm_sigmoid(lg);
-      if (!finite_f(s) || s < 0.0f || s > 1.0f)
-        record_err(status, err_key(kPhGate, t, 0, 0, kGkRange));
-      shg[t] = s;
-    }
-  }
+  route_select_token<NE, false>(z, ldz, E, K, has_sh, (int)blockIdx.x, threadIdx.x, sm, ids, probs, shg,
+                         status, [] { __syncthreads(); });
 }
 
 hipError_t launch_router_select(const float* z, int ldz, int T, int E, int K, int has_sh,
