@@ -36,6 +36,40 @@ def _check(block, oracle, L, layer, x, residual=None, pool=None):
     assert ok, (err, rms)
 
 
+@pytest.mark.parametrize("cfg", ["toy", "qwen"])
+@pytest.mark.parametrize("gap_ulp", [0, 1, 3, 64, 4096])
+def test_batch_routing_near_ties_at_topk_boundary(block, oracle, cfg, gap_ulp):
+    """The K-th and (K+1)-th experts get logits gap_ulp fp32 ulp apart (0 =
+    exact tie, lowest id wins) in every token of a 3-token call: the batch
+    front end's top-k has a fast reduction on truncated probability keys and
+    must fall back to exact rounds when the truncation could reorder them.
+    ids and probabilities bit-exact against the oracle."""
+    c = synth.CONFIG_TOY if cfg == "toy" else synth.CONFIG_QWEN36
+    L = synth.make_layer(**c, seed=31)
+    H, E, K = L.hidden, L.num_experts, L.top_k
+    w = np.zeros((E, H), np.float32)
+    w[:, 0] = 0.5
+    for i in range(K - 1):
+        w[i, 0] = 2.0 - i * 0.125
+    w[K - 1, 0], w[K, 0] = 1.0, 1.0
+    w[K - 1, 1] = 1.0
+    w[K, 1] = 1.0 + gap_ulp * 2.0 ** -7  # z_K - z_{K-1} = gap_ulp * 2^-23
+    L.router_bf16 = synth.f32_to_bf16_bits(w).reshape(-1)
+    assert np.array_equal(synth.bf16_bits_to_f32(L.router_bf16).reshape(E, H)[:, :2], w[:, :2])
+    layer = 60 + (gap_ulp % 7) + (10 if cfg == "qwen" else 0)
+    block.upload_layer(layer, L)
+    x = np.zeros((3, H), np.float32)
+    x[:, 0], x[:, 1] = 1.0, 2.0 ** -16
+    x[1, 2] = 0.25  # a second row pattern: feature 2 adds nothing (w[:, 2] = 0)
+    y, ids, probs, shg = block.forward_arrays(layer, x, 3)
+    yo, ido, po, so = oracle.moe_layer_q4(L, x, 3)
+    assert np.array_equal(ids, ido), (ids, ido)
+    assert np.array_equal(probs.view(np.uint32), po.view(np.uint32))
+    err, rms, ok = tol_check(y, yo)
+    assert ok, (err, rms)
+    block.free_layer(layer)
+
+
 @pytest.mark.parametrize("T", [2, 8, 32])
 def test_small_batch_vs_oracle(block, oracle, qwen, T):
     x = synth.make_activations(np.random.default_rng(200 + T), (T, 2048))
