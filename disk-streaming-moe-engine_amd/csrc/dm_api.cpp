@@ -8,6 +8,7 @@
 
 #include <algorithm>
 #include <atomic>
+#include <chrono>
 #include <mutex>
 #include <new>
 #include <stdexcept>
@@ -930,6 +931,10 @@ namespace {
 // the status key into the block as it ends, the call's key is their
 // minimum; other paths read it back), and the key's reset is skipped while
 // the previous host call left it clean.
+// A status word no workgroup writes (phase 15 = sync keys carry token 0).
+constexpr unsigned long long kKeySentinel = 0xFFFFFFFFFFFFFFF0ull;
+constexpr std::chrono::milliseconds kHostPollLimit{200};
+
 int moe_forward_host1(dmh_ctx* c, Layer* Ly, int layer, const float* x, const float* residual,
                       float* y, int32_t* ids, float* probs, float* shg, const dm::NormSpec* nm,
                       char* err, size_t errlen) {
@@ -953,16 +958,35 @@ int moe_forward_host1(dmh_ctx* c, Layer* Ly, int layer, const float* x, const fl
   float* dshg = reinterpret_cast<float*>(db + o_shg);
   if (!c->status_clean[layer]) HIP_TRY(reset_status(c, layer));
   size_t nk = 1;  // status words the last run left in the block
+  volatile unsigned long long* keys = reinterpret_cast<unsigned long long*>(hb + o_key);
   auto run_and_fetch = [&](bool allow_fused) -> hipError_t {
-    // the fused kernel's workgroups write the key into the block themselves
+    // The fused kernel's workgroups write the key into the block themselves,
+    // each as its last store after its outputs have completed; the block is
+    // fine-grained host memory, so once every word has changed from the
+    // sentinel the outputs are in place, and the call returns without the
+    // runtime's stream synchronisation (a poll of the block instead).  A
+    // run that has not finished within kHostPollLimit is left to
+    // hipStreamSynchronize, which also reports a failed launch.
+    for (size_t i = 0; i < nkey; ++i) keys[i] = kKeySentinel;
     bool exported = false;
     hipError_t e = run_block(c, Ly, layer, dx, dres, 1, dy, dids, dprobs, dshg, allow_fused, nm,
                              nullptr, reinterpret_cast<unsigned long long*>(db + o_key), &exported);
-    if (e == hipSuccess && !exported)
-      e = hipMemcpyAsync(hb + o_key, c->status + layer, 8, hipMemcpyDeviceToHost, st);
-    if (e == hipSuccess) e = hipStreamSynchronize(st);
     nk = exported ? nkey : 1;
-    return e;
+    if (e != hipSuccess) return e;
+    if (!exported) {
+      e = hipMemcpyAsync(hb + o_key, c->status + layer, 8, hipMemcpyDeviceToHost, st);
+      return e == hipSuccess ? hipStreamSynchronize(st) : e;
+    }
+    const auto t0 = std::chrono::steady_clock::now();
+    for (size_t i = 0; i < nkey;) {
+      if (keys[i] != kKeySentinel) {
+        ++i;
+        continue;
+      }
+      if (std::chrono::steady_clock::now() - t0 > kHostPollLimit) return hipStreamSynchronize(st);
+    }
+    std::atomic_thread_fence(std::memory_order_acquire);
+    return hipSuccess;
   };
   auto key_of = [&]() {
     unsigned long long k = ~0ull, v;
