@@ -61,7 +61,20 @@ struct GgufLayer {
   void* buf = nullptr;
   size_t bytes = 0;
   dm::GgufMoeDev dev{};
+  // single-token form (dm::launch_gguf_one_token): its sync area, grid and
+  // launch count (the hand-off count only grows)
+  void* sync = nullptr;
+  size_t sync_bytes = 0;
+  int grid = 0;
+  unsigned launches = 0;
 };
+
+void free_glayer(GgufLayer* G) {
+  if (!G) return;
+  if (G->buf) (void)hipFree(G->buf);
+  if (G->sync) (void)hipFree(G->sync);
+  delete G;
+}
 
 struct Layer {
   dmh_moe_dims dims{};
@@ -558,6 +571,10 @@ int gguf_finish(dmh_ctx* c, int layer, uint64_t key, char* err, size_t errlen) {
   GgufLayer* G = layer >= 0 && layer < (int)c->glayers.size() ? c->glayers[layer] : nullptr;
   const int H = G ? G->dims.hidden : 0, E = G ? G->dims.num_experts : 0;
   const uint32_t ph = dm::key_phase(key);
+  if (ph == dm::kPhSync && G && G->sync) {  // a hand-off timed out: start the count again
+    (void)hipStreamSynchronize(c->cur);
+    if (hipMemsetAsync(G->sync, 0, G->sync_bytes, c->cur) == hipSuccess) G->launches = 0;
+  }
   if (ph == dm::kPhExpert || ph == dm::kPhShared)
     return decode_key(key, H, ph == dm::kPhShared ? (G ? G->dims.inter_sh : 0)
                                                    : (G ? G->dims.inter : 0),
@@ -570,8 +587,12 @@ GgufLayer* get_glayer(dmh_ctx* c, int layer) {
   return c->glayers[layer];
 }
 
-// The MoE section of forward_port_block on a GGUF layer, all on the device
-// in four launches: router and shared-gate logits (fp32 weights,
+// The MoE section of forward_port_block on a GGUF layer, all on the device:
+// one token in two launches (dm::launch_gguf_one_token) when the layer has
+// its sync area, no other context of the library lives on the device (its
+// persistent grids could hold CUs the experts launch waits for) and the
+// stream is not being captured (a replay would repeat the launch count);
+// otherwise four launches: router and shared-gate logits (fp32 weights,
 // router_forward's order), selection and gate, gate/up of every slot, down
 // projections with moe_aggregate_forward.
 hipError_t run_gguf_block(dmh_ctx* c, GgufLayer* G, unsigned long long* status, const float* dx,
@@ -580,6 +601,19 @@ hipError_t run_gguf_block(dmh_ctx* c, GgufLayer* G, unsigned long long* status, 
   const dm::GgufMoeDev& L = G->dev;
   hipStream_t st = c->cur;
   hipError_t e;
+  if (T == 1 && G->sync && G->grid > 0 &&
+      g_live_ctx[c->device].load(std::memory_order_relaxed) <= 1) {
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    if ((e = hipStreamIsCapturing(st, &cap)) != hipSuccess) return e;
+    if (cap == hipStreamCaptureStatusNone) {
+      if (G->launches >= (1u << 24)) {
+        if ((e = hipMemsetAsync(G->sync, 0, G->sync_bytes, st)) != hipSuccess) return e;
+        G->launches = 0;
+      }
+      return dm::launch_gguf_one_token(L, dx, dres, dy, dids, dprobs, dshg, G->sync,
+                                       ++G->launches, G->grid, status, st);
+    }
+  }
   const int ldh = L.I > L.Ish ? L.I : L.Ish;
   if ((e = c->z.ensure((size_t)T * (L.E + 1))) != hipSuccess) return e;
   if ((e = c->h.ensure((size_t)T * (L.K + 1) * ldh)) != hipSuccess) return e;
@@ -671,11 +705,7 @@ int dmh_destroy(dmh_ctx* c) {
   (void)hipSetDevice(c->device);
   if (c->cur) (void)hipStreamSynchronize(c->cur);
   for (Layer* L : c->layers) free_layer(L);
-  for (GgufLayer* G : c->glayers)
-    if (G) {
-      if (G->buf) (void)hipFree(G->buf);
-      delete G;
-    }
+  for (GgufLayer* G : c->glayers) free_glayer(G);
   DevBuf<float>* fb[] = {&c->x, &c->res, &c->y, &c->z, &c->probs, &c->shg, &c->h, &c->xn, &c->hstack};
   for (auto* b : fb) b->release();
   c->ids.release();
@@ -1765,10 +1795,30 @@ static int upload_gguf_body(dmh_ctx* c, int layer, const dmh_moe_dims* d,
   }
   G->dims = *d;
   G->bytes = bytes;
-  G->dev = dm::GgufMoeDev{H, E, K, I, Ish, exp_t, layout, d_raw, d_off, d_router, d_sg};
+  // routed expert tensors of one size, appended in order from offset 0:
+  // their offsets are (3e + k) * stride, no table lookup needed
+  int64_t estride = off.size() > 1 ? off[1] - off[0] : 0;
+  for (int i = 0; i < 3 * E && estride > 0; ++i)
+    if (off[i] != (int64_t)i * estride) estride = 0;
+  G->dev = dm::GgufMoeDev{H, E, K, I, Ish, exp_t, layout, d_raw, d_off, d_router, d_sg, estride};
+  // the single-token form when its experts launch fits the device at once
+  {
+    int per_cu = 0;
+    G->sync_bytes = dm::gguf_one_token_sync_bytes(G->dev);
+    if (dm::gguf_one_token_supported(G->dev) && c->num_cus > 0 &&
+        dm::gguf_experts_occupancy(G->dev, &per_cu) == 0 && per_cu >= 1 &&
+        hipMalloc(&G->sync, G->sync_bytes) == hipSuccess) {
+      if (hipMemsetAsync(G->sync, 0, G->sync_bytes, st) == hipSuccess) {
+        G->grid = c->num_cus;
+      } else {
+        (void)hipFree(G->sync);
+        G->sync = nullptr;
+      }
+    }
+  }
   if (GgufLayer* old = c->glayers[layer]) {
-    (void)hipFree(old->buf);
-    delete old;
+    (void)hipStreamSynchronize(st);
+    free_glayer(old);
   }
   c->glayers[layer] = G;
   HIP_TRY(reset_status(c, kGgufSlot0 + layer));
@@ -1780,8 +1830,7 @@ int dmh_free_layer_gguf(dmh_ctx* c, int layer) {
   if (!G) return DMH_ERR_INVALID_ARG;
   (void)hipSetDevice(c->device);
   (void)hipStreamSynchronize(c->cur);
-  (void)hipFree(G->buf);
-  delete G;
+  free_glayer(G);
   c->glayers[layer] = nullptr;
   return DMH_OK;
 }

@@ -40,6 +40,7 @@ struct GgufMoeDev {
   const int64_t* off;  // [E + 1][3] byte offsets of gate, up, down in raw; row E = shared expert
   const float* router; // [E][H]
   const float* shgate; // [H]
+  int64_t estride;     // > 0: off[3e + k] = (3e + k) * estride for the routed experts (else 0)
 };
 
 // h[t][s][i] = SiLU(W_gate x_t)_i * (W_up x_t)_i for slots s < K (expert
@@ -55,6 +56,22 @@ hipError_t launch_gguf_down_combine(const GgufMoeDev& L, const float* h, int ldh
                                     const int32_t* ids, const float* probs, const float* shg,
                                     const float* residual, float* y, unsigned long long* status,
                                     hipStream_t st);
+
+// One token in two launches: the router, the shared expert's h and the
+// softmax / top-k (front launch), then the routed experts, the down
+// projections and the combine (experts launch: grid workgroups of 512
+// threads that must all be resident, one hand-off of the routed h counted
+// per slot in the sync area).  sync: gguf_one_token_sync_bytes of device
+// memory, zero before the first launch; launch n of a layer (n = 1, 2, ...)
+// waits for n * I / 16 counts per slot (compared modulo 2^32), so the
+// caller keeps n per layer.
+bool gguf_one_token_supported(const GgufMoeDev& L);
+size_t gguf_one_token_sync_bytes(const GgufMoeDev& L);
+int gguf_experts_occupancy(const GgufMoeDev& L, int* per_cu);
+hipError_t launch_gguf_one_token(const GgufMoeDev& L, const float* x, const float* residual,
+                                 float* y, int32_t* ids, float* probs, float* shg, void* sync,
+                                 unsigned launch, int grid, unsigned long long* status,
+                                 hipStream_t st);
 
 // GGUFTensorInfo (gguf.mojo:104-114); offset is relative to the data section.
 struct GgufTensor {
