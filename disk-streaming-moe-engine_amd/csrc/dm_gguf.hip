@@ -507,7 +507,7 @@ __global__ __launch_bounds__(512) void k_gguf_experts(
     unsigned* hcnt, unsigned target, unsigned long long* status) {
   __shared__ float part[8][33];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int G = (int)gridDim.x, nw = G * 8, gw = (int)blockIdx.x * 8 + w;
+  const int G = (int)gridDim.x;
   const int H = L.H, E = L.E, K = L.K, I = L.I, Ish = L.Ish;
   // lane s < K: the payload offsets of routed slot s
   const int es = min(max((int)ids[min(lane, K - 1)], 0), E - 1);
