@@ -67,12 +67,14 @@ struct GgufLayer {
   size_t sync_bytes = 0;
   int grid = 0;
   unsigned launches = 0;
+  float* rchain = nullptr;  // the router in chain order (dev.rchain)
 };
 
 void free_glayer(GgufLayer* G) {
   if (!G) return;
   if (G->buf) (void)hipFree(G->buf);
   if (G->sync) (void)hipFree(G->sync);
+  if (G->rchain) (void)hipFree(G->rchain);
   delete G;
 }
 
@@ -1808,11 +1810,17 @@ static int upload_gguf_body(dmh_ctx* c, int layer, const dmh_moe_dims* d,
     if (dm::gguf_one_token_supported(G->dev) && c->num_cus > 0 &&
         dm::gguf_experts_occupancy(G->dev, &per_cu) == 0 && per_cu >= 1 &&
         hipMalloc(&G->sync, G->sync_bytes) == hipSuccess) {
-      if (hipMemsetAsync(G->sync, 0, G->sync_bytes, st) == hipSuccess) {
+      if (hipMalloc(&G->rchain, dm::gguf_chain_router_bytes(G->dev)) == hipSuccess &&
+          dm::launch_chain_router(G->dev, G->rchain, st) == hipSuccess &&
+          hipMemsetAsync(G->sync, 0, G->sync_bytes, st) == hipSuccess &&
+          hipStreamSynchronize(st) == hipSuccess) {
+        G->dev.rchain = G->rchain;
         G->grid = c->num_cus;
       } else {
         (void)hipFree(G->sync);
         G->sync = nullptr;
+        if (G->rchain) (void)hipFree(G->rchain);
+        G->rchain = nullptr;
       }
     }
   }

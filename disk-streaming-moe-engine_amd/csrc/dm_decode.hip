@@ -280,98 +280,6 @@ __device__ __forceinline__ void router_compute(const LayerDev& L, uint4 (&rw)[kR
   }
 }
 
-// ---------------------------------------------------------------------------
-// One selection round set over NK keys per lane (lane l owns experts
-// l + 64 i, i < NK): `rounds` times take the largest remaining key, the
-// lowest id on equal keys (lowest i first, then lowest lane).  Winners go to ids[].
-// Returns the key of each round through kr (kr[0] = first, kr[1] = last,
-// kr[2] = the best key left after `rounds` rounds when want_next).
-template <int NK>
-__device__ __forceinline__ void select_keys(const uint32_t (&key)[NK], int rounds, int E,
-                                            int* ids, bool want_next, uint32_t (&kr)[3]) {
-  const int lane = threadIdx.x & 63;
-  uint32_t taken = 0;
-  kr[0] = kr[1] = kr[2] = 0;
-  for (int it = 0; it <= rounds; ++it) {
-    uint32_t lm = 0;
-#pragma unroll
-    for (int i = 0; i < NK; ++i) {
-      const uint32_t kv = (taken >> i & 1u) ? 0u : key[i];
-      lm = kv > lm ? kv : lm;
-    }
-    const uint32_t gm = wave_max_u32(lm);
-    if (it == rounds) {
-      kr[2] = gm;
-      break;
-    }
-    if (it == 0) kr[0] = gm;
-    kr[1] = gm;
-    int wi = -1, wl = 0;
-#pragma unroll
-    for (int i = 0; i < NK; ++i) {
-      const uint64_t mk = __builtin_amdgcn_ballot_w64(!(taken >> i & 1u) && key[i] == gm);
-      if (wi < 0 && mk) {
-        wi = i;
-        wl = (int)__builtin_ctzll(mk);
-      }
-    }
-    if (wi < 0) wi = 0;
-    if (lane == wl) taken |= 1u << wi;
-    if (lane == 0) {
-      const int e = 64 * wi + wl;
-      ids[it] = e < E ? e : E - 1;
-    }
-    if (!want_next && it == rounds - 1) break;
-  }
-}
-
-template <int R>
-__device__ __forceinline__ void issue_logits(const uint64_t* zt, int E, bool gate,
-                                             uint64_t (&v)[4 * R + 1]) {
-  const int lane = threadIdx.x & 63;
-#pragma unroll
-  for (int i = 0; i < 4 * R; ++i) v[i] = ld_coh_u64(zt + min(lane + 64 * i, E - 1));
-  v[4 * R] = gate ? ld_coh_u64(zt + E) : 0;
-}
-template <int R>
-__device__ __forceinline__ bool logits_ready(const uint64_t (&v)[4 * R + 1], unsigned tag, int E,
-                                             bool gate, float (&z)[4 * R], float* gl) {
-  const int lane = threadIdx.x & 63;
-  bool ready = true;
-#pragma unroll
-  for (int i = 0; i < 4 * R; ++i) {
-    z[i] = 0.0f;
-    if (lane + 64 * i < E) {
-      z[i] = u2f((uint32_t)v[i]);
-      ready &= (uint32_t)(v[i] >> 32) == tag;
-    }
-  }
-  if (gate && lane == 0) {
-    *gl = u2f((uint32_t)v[4 * R]);
-    ready &= (uint32_t)(v[4 * R] >> 32) == tag;
-  }
-  return __builtin_amdgcn_ballot_w64(!ready) == 0;
-}
-
-// Poll the tagged logits until every entry carries this launch's tag.  Lane
-// l holds experts l + 64 i (coalesced loads); lane 0 also the shared-gate
-// logit (entry E) when gl is given.  One poll in flight at a time: loads
-// left in flight would stall the first later reuse of their registers.
-// Returns false on a timeout.
-template <int R>
-__device__ __forceinline__ bool poll_logits(const uint64_t* zt, unsigned tag, int E, float (&z)[4 * R],
-                                            float* gl) {
-  const bool gate = gl != nullptr;
-  uint64_t v[4 * R + 1];
-  for (long spin = 0; spin < kSpinLimit; ++spin) {
-    issue_logits<R>(zt, E, gate, v);
-    if (logits_ready<R>(v, tag, E, gate, z, gl)) return true;
-    __builtin_amdgcn_s_sleep(1);
-  }
-  return false;
-}
-
-__device__ __forceinline__ void wait_lds() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
 // Routing on wave 0.  Selects the K largest logits with unique 32-bit keys
 // (the high bits of the logit's order key, then the inverted expert id, so
@@ -384,15 +292,12 @@ template <int R>
 __device__ __forceinline__ bool route(const uint64_t* zt, unsigned tag, int E, int K, SelState& st,
                                       bool record, int token, unsigned long long* status) {
   constexpr int NK = 4 * R;
-  constexpr int IDB = R == 1 ? 8 : 11;  // id bits of a selection key
-  constexpr uint32_t IDM = (1u << IDB) - 1;
   const int lane = threadIdx.x & 63;
   float z[NK];
   const bool ok = poll_logits<R>(zt, tag, E, z, nullptr);
   if (!ok && lane == 0) record_err(status, err_key(kPhSync, 0, 0, 0, 0));
-  // keys, branch-free (entries past E: key 0, never selected); the
-  // non-finite logits are recorded on a separate, rarely taken path
-  uint32_t fk[NK], key[NK];
+  // the logits' copy for the exact path; non-finite logits are recorded on
+  // a separate, rarely taken path
   bool bad = false;
 #pragma unroll
   for (int i = 0; i < NK; ++i) {
@@ -400,8 +305,6 @@ __device__ __forceinline__ bool route(const uint64_t* zt, unsigned tag, int E, i
     const bool in = e < E;
     st.zv[min(e, 256 * R - 1)] = in ? z[i] : 0.0f;
     bad |= in && !finite_f(z[i]);
-    fk[i] = in ? f2key(z[i]) : 0u;
-    key[i] = in ? (((fk[i] >> IDB) << IDB) | (IDM - (uint32_t)e)) : 0u;
   }
   if (record && __builtin_amdgcn_ballot_w64(bad) != 0) {
 #pragma unroll
@@ -410,114 +313,10 @@ __device__ __forceinline__ bool route(const uint64_t* zt, unsigned tag, int E, i
       if (e < E && !finite_f(z[i])) record_err(status, err_key(kPhLogit, token, 0, e, 0));
     }
   }
-  // K rounds: the largest remaining key; its low bits name the expert.  Lane
-  // `it` keeps the id of round it (no branches inside the loop).  With four
-  // keys a lane sorts them once, so a round is one wave-wide max of the lane
-  // heads and a shift in the winning lane.  A last max gives the largest
-  // unselected key.
+  uint32_t fk[NK], key[NK];
   int myid = 0;
-  uint32_t gm = 0, gu = 0, gtop = 0;
-  if constexpr (NK == 4) {
-    uint32_t k0 = key[0], k1 = key[1], k2 = key[2], k3 = key[3];
-    auto cx = [](uint32_t& a, uint32_t& b) {  // a >= b afterwards
-      const uint32_t hi = a > b ? a : b, lo = a > b ? b : a;
-      a = hi;
-      b = lo;
-    };
-    cx(k0, k1);
-    cx(k2, k3);
-    cx(k0, k2);
-    cx(k1, k3);
-    cx(k1, k2);
-    if (K <= 8) {
-      // one wave-wide top-8 reduction (bitonic merges along the DPP
-      // reduction tree) instead of K rounds of wave maxima
-      uint32_t a[8] = {k0, k1, k2, k3, 0u, 0u, 0u, 0u};
-      top8_step<0x111, 0xF>(a);
-      top8_step<0x112, 0xF>(a);
-      top8_step<0x114, 0xF>(a);
-      top8_step<0x118, 0xF>(a);
-      top8_step<0x142, 0xA>(a);
-      top8_step<0x143, 0xC>(a);
-      uint32_t T[8];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) T[i] = __builtin_amdgcn_readlane(a[i], 63);
-      gtop = T[0];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        if (i == K - 1) gm = T[i];
-        if (i == K && K < E) gu = T[i];
-        myid = lane == i ? (int)(IDM - (T[i] & IDM)) : myid;
-      }
-      if (K == 8 && K < E) {
-        // the largest key outside the top 8: each lane's first key below T7
-        const uint32_t t7 = T[7];
-        const uint32_t c = k0 < t7 ? k0 : k1 < t7 ? k1 : k2 < t7 ? k2 : k3 < t7 ? k3 : 0u;
-        gu = wave_max_u32(c);
-      }
-    } else {
-#pragma unroll 8
-      for (int it = 0; it < K; ++it) {
-        gm = wave_max_u32(k0);
-        gtop = it == 0 ? gm : gtop;
-        const bool win = k0 == gm;
-        k0 = win ? k1 : k0;
-        k1 = win ? k2 : k1;
-        k2 = win ? k3 : k2;
-        k3 = win ? 0u : k3;
-        myid = lane == it ? (int)(IDM - (gm & IDM)) : myid;
-      }
-      if (K < E) gu = wave_max_u32(k0);
-    }
-  } else {
-    uint32_t kw[NK];
-#pragma unroll
-    for (int i = 0; i < NK; ++i) kw[i] = key[i];
-#pragma unroll 8
-    for (int it = 0; it < K; ++it) {
-      uint32_t km = 0;
-#pragma unroll
-      for (int i = 0; i < NK; ++i) km = kw[i] > km ? kw[i] : km;
-      gm = wave_max_u32(km);
-      gtop = it == 0 ? gm : gtop;
-#pragma unroll
-      for (int i = 0; i < NK; ++i) kw[i] = kw[i] == gm ? 0u : kw[i];
-      myid = lane == it ? (int)(IDM - (gm & IDM)) : myid;
-    }
-    if (K < E) {
-      uint32_t km = 0;
-#pragma unroll
-      for (int i = 0; i < NK; ++i) km = kw[i] > km ? kw[i] : km;
-      gu = wave_max_u32(km);
-    }
-  }
+  const bool unsafe = topk_on_logits<R>(z, E, K, lane, fk, myid);
   if (lane < K) st.ids[lane] = myid < E ? myid : E - 1;
-  // Margin check on bounds from the keys: every selected logit is at least
-  // zs (the K-th key with its id bits cleared) and every unselected one at
-  // most zu (the largest unselected key with its id bits set), so
-  // e(zs) > e(zu) (1 + 2^-20) implies the same for the exact boundary logits
-  // (exp is monotone to within an ulp, far inside the 2^-20 margin).
-  // Fast sufficient test first: with zmax an upper bound of the largest
-  // logit (the top key with its id bits set), the rounded arguments zs - m
-  // and zu - m differ by at least (zs - zu) - 2^-23 (zmax - zu), and the
-  // computed exponentials (within 2^-21 relative of exp) keep their order by
-  // more than 2^-20 once that difference exceeds 2^-18; so when
-  // zs - zu > 2^-17 + 2^-21 (zmax - zu) and zmax - zs < 64 (no underflow of
-  // e(zs)) the exact maximum and both exponentials are not needed.  Any
-  // non-finite bound fails the test and takes the full check.
-  bool unsafe = false;
-  if (K < E) {
-    const float zs = key2f(gm & ~IDM), zu = key2f(gu | IDM), zmax = key2f(gtop | IDM);
-    const bool clear = (zs - zu) > 0x1p-17f + (zmax - zu) * 0x1p-21f && (zmax - zs) < 64.0f;
-    if (!clear) {
-      uint32_t lmax = 0;
-#pragma unroll
-      for (int i = 0; i < NK; ++i) lmax = fk[i] > lmax ? fk[i] : lmax;
-      const float m = key2f(wave_max_u32(lmax));
-      const float ek = dm_expf(zs - m), en = dm_expf(zu - m);
-      unsafe = !(ek > en + en * 0x1p-20f);
-    }
-  }
   if (unsafe) {  // select on the exact probabilities
     uint32_t lmax = 0;
 #pragma unroll

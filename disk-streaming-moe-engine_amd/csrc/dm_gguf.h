@@ -41,6 +41,7 @@ struct GgufMoeDev {
   const float* router; // [E][H]
   const float* shgate; // [H]
   int64_t estride;     // > 0: off[3e + k] = (3e + k) * estride for the routed experts (else 0)
+  const float* rchain; // [E + 1][H] router and shared gate in chain order (one-token form), or null
 };
 
 // h[t][s][i] = SiLU(W_gate x_t)_i * (W_up x_t)_i for slots s < K (expert
@@ -57,15 +58,23 @@ hipError_t launch_gguf_down_combine(const GgufMoeDev& L, const float* h, int ldh
                                     const float* residual, float* y, unsigned long long* status,
                                     hipStream_t st);
 
-// One token in two launches: the router, the shared expert's h and the
-// softmax / top-k (front launch), then the routed experts, the down
-// projections and the combine (experts launch: grid workgroups of 512
-// threads that must all be resident, one hand-off of the routed h counted
-// per slot in the sync area).  sync: gguf_one_token_sync_bytes of device
+// One token in two launches: the router logits (tagged with the launch
+// number n), the shared expert's h, the top-k selection and the softmax
+// terms (front launch: two polling workgroups with the others resident),
+// then the routed experts, the down projections and the combine (experts
+// launch: grid workgroups of 512 threads that must all be resident, one
+// hand-off of the routed h counted per slot).  L.rchain must be set
+// (launch_chain_router).  sync: gguf_one_token_sync_bytes of device
 // memory, zero before the first launch; launch n of a layer (n = 1, 2, ...)
-// waits for n * I / 16 counts per slot (compared modulo 2^32), so the
-// caller keeps n per layer.
+// waits for logits tagged n and for n * I / 16 counts per slot (compared
+// modulo 2^32), so the caller keeps n per layer.
 bool gguf_one_token_supported(const GgufMoeDev& L);
+// rchain for the one-token form: row e's element c + 16 (4q + u) at
+// 4 (16 q + c) + u (the steps of router_project's lane chains, four per
+// float4; zero past H), rows 0 .. E - 1 the router, row E the shared gate;
+// out holds gguf_chain_router_bytes(L) bytes, H a multiple of 64.
+size_t gguf_chain_router_bytes(const GgufMoeDev& L);
+hipError_t launch_chain_router(const GgufMoeDev& L, float* out, hipStream_t st);
 size_t gguf_one_token_sync_bytes(const GgufMoeDev& L);
 int gguf_experts_occupancy(const GgufMoeDev& L, int* per_cu);
 hipError_t launch_gguf_one_token(const GgufMoeDev& L, const float* x, const float* residual,

@@ -360,31 +360,54 @@ __device__ __forceinline__ void q3_decode(const Q3Raw<W>& r, f32x4 (&v)[W / 4]) 
   for (int j = 0; j < W / 4; ++j) v[j] = f32x4{w[4 * j], w[4 * j + 1], w[4 * j + 2], w[4 * j + 3]};
 }
 
-// k_gguf_front: workgroups 0 .. nR - 1 (one wave each) form the router logits
-// of rows 2b and 2b + 1 (row E: the shared-expert gate) in router_project's
-// order (16 lane chains k = l, l + 16, ..., the halving tree, the tail on
-// lane 0: the order of the router kernels), and publish them at the
-// device-coherent level; the last of them to arrive runs the softmax / top-k
-// (route_select_token).  Workgroups nR .. nR + Ish - 1 form the shared
-// expert's h rows meanwhile (they do not depend on the routing).
+// k_gguf_front: workgroup 0 selects, workgroup 1 forms the softmax
+// normaliser, workgroups 2 .. nR + 1 the router logits, the rest the shared
+// expert's h rows (they do not depend on the routing).  A router workgroup
+// (one wave) forms rows 4 (b - 2) .. 4 (b - 2) + 3 (row E: the
+// shared-expert gate) in router_project's order: lane 16 r + c runs chain c
+// of row r (k = c, c + 16, ..., separate multiply and add), then the
+// halving tree of the router kernels.  The chain's weights come four steps
+// per float4 from the chain-ordered copy of the router (k_chain_router,
+// rows of kFrontMaxH floats, zero past H), x from LDS in chain order (zero
+// past H: the extra steps add +0.0 to a sum that is never -0.0, which leaves
+// it unchanged).  Each logit is published as a tagged word (launch << 32 |
+// bits) at the device-coherent level.  Workgroup 0 polls them (bounded),
+// selects the top K on the logits (topk_on_logits; the exact probabilities
+// on a near tie at the boundary) and writes the K experts, ordered by logit
+// (then id), to sel[].  Workgroup 1 polls them too and writes, for the
+// experts launch, max z, 1/S (S the sum of exp(z - max) in expert order)
+// and the shared gate to soft[] with router_softmax's and the gate's checks
+// (src/layers/router.mojo:140-183, src/layers/moe.mojo:70-100).
 constexpr int kFrontMaxH = 2048;
-constexpr size_t kSyncHead = 1024;  // counters: front at 0, slot s's h count at 128 + 64 s
-constexpr int kFrontRows = 2;
+// sync area head: slot s's h count at 128 + 64 s, the selected experts at
+// kSelOff, the exact path's probabilities at kSelOff + 64, the softmax
+// terms at kSelOff + 128; then the tagged logits, the shared expert's h and
+// the routed slots' h
+constexpr size_t kSyncHead = 1024;
+constexpr size_t kSelOff = 768;
+constexpr int kFrontRows = 4;
+constexpr int kChainS = kFrontMaxH / 16 + 4;  // LDS row of x in chain order (4 pad floats)
 
-template <int T, int W, int NE>
+// whether any of four values is not finite, without branches
+__device__ __forceinline__ bool nonfinite4(const f32x4& q) {
+  constexpr uint32_t e = 0x7F800000u;
+  const int n = ((f2u(q.x) & e) == e) + ((f2u(q.y) & e) == e) + ((f2u(q.z) & e) == e) +
+                ((f2u(q.w) & e) == e);
+  return n != 0;
+}
+
+template <int T, int W, int R>
 __global__ __launch_bounds__(64) void k_gguf_front(GgufMoeDev L, const float* __restrict__ x,
-                                                   int nR, float* __restrict__ z,
-                                                   float* __restrict__ h, int ldh,
-                                                   unsigned* front, int32_t* __restrict__ ids,
-                                                   float* __restrict__ probs,
-                                                   float* __restrict__ shg,
+                                                   int nR, uint64_t* zt, float* __restrict__ hsh,
+                                                   int32_t* sel, float* selp, float* soft,
+                                                   unsigned launch,
                                                    unsigned long long* status) {
-  __shared__ __attribute__((aligned(16))) float sx[kFrontMaxH];
-  __shared__ __attribute__((aligned(16))) float sw[kFrontRows][kFrontMaxH + 16];
-  const int lane = threadIdx.x, H = L.H, E = L.E;
-  if ((int)blockIdx.x >= nR) {
+  __shared__ __attribute__((aligned(16))) float xt[16 * kChainS];
+  const int lane = threadIdx.x, H = L.H, E = L.E, K = L.K;
+  const int b = (int)blockIdx.x;
+  if (b > nR + 1) {
     // the shared expert's gate / up row r (as k_gguf_gateup's slot K)
-    const int r = (int)blockIdx.x - nR;
+    const int r = b - 2 - nR;
     const uint8_t* wg = L.raw + L.off[(size_t)E * 3 + 0];
     const uint8_t* wu = L.raw + L.off[(size_t)E * 3 + 1];
     const int64_t base = (int64_t)r * H;
@@ -407,110 +430,272 @@ __global__ __launch_bounds__(64) void k_gguf_front(GgufMoeDev L, const float* __
       if (!finite_f(ag)) record_err(status, err_key(kPhShared, 0, 0, r, kEkGate));
       if (!finite_f(au)) record_err(status, err_key(kPhShared, 0, 0, r, kEkUp));
       if (!finite_f(hv)) record_err(status, err_key(kPhShared, 0, 0, r, kEkH));
-      h[(size_t)L.K * ldh + r] = hv;
+      hsh[r] = hv;
     }
     return;
   }
-  // x and the workgroup's rows to LDS, every value checked as it is read
-  const int row0 = (int)blockIdx.x * kFrontRows;
-  bool bad_x = false, bad_w = false;
-  {
-    // x and the rows: every load (clamped to the data) issued before the
-    // first LDS store
-    constexpr int kJ = kFrontMaxH / 256;
-    f32x4 v[kFrontRows + 1][kJ];
+  auto wave_sync = [] {
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+  };
+  if (b == 0) {
+    float z[4 * R];
+    if (!poll_logits<R>(zt, launch, E, z, nullptr) && lane == 0)
+      record_err(status, err_key(kPhSync, 0, 0, 0, 0));
+    uint32_t fk[4 * R];
+    int myid = 0;
+    if (!topk_on_logits<R>(z, E, K, lane, fk, myid)) {
+      // lane k < K: the k-th by key; ordered by (logit, then lower id), the
+      // order the softmax's probabilities keep unless two of them round to
+      // the same value (the experts launch orders by probability)
+      myid = min(max(myid, 0), E - 1);
+      // the logit of expert e sits in lane e & 63, entry e >> 6
+      float zk = 0.0f;
 #pragma unroll
-    for (int r = 0; r <= kFrontRows; ++r) {
-      const int e = min(row0 + r - 1, E);
-      const float* src = r == 0 ? x : e == E ? L.shgate : L.router + (int64_t)e * H;
+      for (int i = 0; i < 4 * R; ++i) {
+        const float zo = u2f((uint32_t)__builtin_amdgcn_ds_bpermute(4 * (myid & 63), (int)f2u(z[i])));
+        zk = (myid >> 6) == i ? zo : zk;
+      }
+      const uint32_t kk = f2key(zk);
+      int rank = 0;
 #pragma unroll
-      for (int j = 0; j < kJ; ++j)
-        v[r][j] = *reinterpret_cast<const f32x4*>(src + min(4 * lane + 256 * j, H - 4));
+      for (int j = 0; j < 8; ++j) {
+        const uint32_t kj = (uint32_t)__builtin_amdgcn_readlane((int)kk, j);
+        const int ij = __builtin_amdgcn_readlane(myid, j);
+        if (j < K && lane < K)
+          rank += (kj > kk || (kj == kk && (ij < myid || (ij == myid && j < lane)))) ? 1 : 0;
+      }
+      if (lane < K) sel[rank] = myid;
+    } else {
+      // a near tie at the top-k boundary: the exact probabilities decide
+      float* sz = xt;
+      float* sm = xt + 512;
+#pragma unroll
+      for (int i = 0; i < 4 * R; ++i)
+        if (lane + 64 * i < E) sz[lane + 64 * i] = z[i];
+      wave_sync();
+      route_select_token<4 * R, false>(sz, 0, E, K, 0, 0, lane, sm, sel, selp, nullptr, status,
+                                       wave_sync);
     }
+    return;
+  }
+  if (b == 1) {
+    float z[4 * R], gl = 0.0f;
+    if (!poll_logits<R>(zt, launch, E, z, &gl) && lane == 0)
+      record_err(status, err_key(kPhSync, 0, 0, 0, 0));
+    float m = -__builtin_inff();
 #pragma unroll
-    for (int r = 0; r <= kFrontRows; ++r) {
-      const int e = row0 + r - 1;
+    for (int i = 0; i < 4 * R; ++i)
+      if (lane + 64 * i < E) m = z[i] > m ? z[i] : m;
+    m = __ockl_wfred_max_f32(m);
+    if (lane == 0 && !finite_f(m)) record_err(status, err_key(kPhSoftmax, 0, 0, 0, 0));
 #pragma unroll
-      for (int j = 0; j < kJ; ++j) {
-        const int k = 4 * lane + 256 * j;
-        if (k >= H || (r > 0 && e > E)) continue;
-        const f32x4 q = v[r][j];
-        const bool bad = !finite_f(q.x) || !finite_f(q.y) || !finite_f(q.z) || !finite_f(q.w);
-        if (r == 0) {
-          bad_x |= bad;
-          *reinterpret_cast<f32x4*>(&sx[k]) = q;
-        } else {
-          if (e != E) bad_w |= bad;
-          *reinterpret_cast<f32x4*>(&sw[r - 1][k]) = q;
-        }
+    for (int i = 0; i < 4 * R; ++i) {
+      const int e = lane + 64 * i;
+      if (e < E) {
+        const float ev = dm_expf(z[i] - m);
+        if (!finite_f(ev)) record_err(status, err_key(kPhSoftmax, 0, 0, 1 + e, 0));
+        xt[e] = ev;
       }
     }
+    wave_sync();
+    if (lane == 0) {
+      const float s = seq_sum(xt, E);
+      if (!(s > 0.0f) || !finite_f(s)) record_err(status, err_key(kPhSoftmax, 0, 0, 1 + E, 0));
+      if (!finite_f(gl)) record_err(status, err_key(kPhGate, 0, 0, 0, kGkLogit));
+      const float g = dm_sigmoid(gl);
+      if (!finite_f(g) || g < 0.0f || g > 1.0f)
+        record_err(status, err_key(kPhGate, 0, 0, 0, kGkRange));
+      soft[0] = m;
+      soft[1] = 1.0f / s;
+      soft[2] = g;
+    }
+    return;
   }
+  // ---- router rows: every load (clamped to the data) before the first LDS store
+  const int r = lane >> 4, c = lane & 15;
+  const int e = (b - 2) * kFrontRows + r;
+  const bool row = e <= E, chk = row && e != E;
+  constexpr int kJ = kFrontMaxH / 256;  // float4 of x per lane
+  constexpr int kQ = kFrontMaxH / 64;   // float4 of a chain
+  f32x4 xv[kJ], wv[kQ];
+#pragma unroll
+  for (int j = 0; j < kJ; ++j)
+    xv[j] = *reinterpret_cast<const f32x4*>(x + min(4 * lane + 256 * j, H - 4));
+  const float* wr = L.rchain + (int64_t)min(e, E) * kFrontMaxH + 4 * c;
+#pragma unroll
+  for (int q = 0; q < kQ; ++q) wv[q] = *reinterpret_cast<const f32x4*>(wr + 64 * q);
+  if (H < kFrontMaxH) {  // steps past H read zeros
+    for (int i = lane; i < 16 * kChainS; i += 64) xt[i] = 0.0f;
+  }
+  // x to LDS in chain order (element k at (k & 15) kChainS + (k >> 4); the
+  // clamped duplicates past H to the pad columns), every value checked
+  bool bad_x = false, bad_w = false;
+#pragma unroll
+  for (int j = 0; j < kJ; ++j) {
+    const int k = 4 * lane + 256 * j;
+    const bool in = k < H;
+    const f32x4 q = xv[j];
+    bad_x |= in && nonfinite4(q);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int kk = k + u;
+      xt[(kk & 15) * kChainS + (in ? kk >> 4 : kFrontMaxH / 16 + ((kk >> 4) & 3))] = q[u];
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < kQ; ++q)
+    bad_w |= nonfinite4(wv[q]);
+  bad_w = bad_w && chk;
   if (bad_x) record_err(status, err_key(kPhX, 0, 0, 0, 0));
   if (bad_w) record_err(status, err_key(kPhRouterW, 0, 0, 0, 0));
   __syncthreads();
-  const int l = lane & 15, r = lane >> 4, e = row0 + r;
-  const bool row = r < kFrontRows && e <= E;
-  const int h16 = H & ~15;
   float acc = 0.0f;
-  if (row) {
-#pragma unroll 8
-    for (int k = l; k < h16; k += 16) acc = acc + sx[k] * sw[r][k];
+  const float* xc = xt + c * kChainS;
+#pragma unroll
+  for (int q = 0; q < kQ; ++q) {
+    const f32x4 xq = *reinterpret_cast<const f32x4*>(xc + 4 * q);
+    acc = acc + xq.x * wv[q].x;
+    acc = acc + xq.y * wv[q].y;
+    acc = acc + xq.z * wv[q].z;
+    acc = acc + xq.w * wv[q].w;
   }
 #pragma unroll
   for (int wdt = 8; wdt >= 1; wdt >>= 1) {
     const float o = __shfl_down(acc, wdt, 16);
-    if (l < wdt) acc = acc + o;
+    if (c < wdt) acc = acc + o;
   }
-  if (row && l == 0) {
-    float sv = acc;
-    for (int k = h16; k < H; ++k) sv = sv + sx[k] * sw[r][k];
-    if (e != E && !finite_f(sv)) record_err(status, err_key(kPhLogit, 0, 0, e, 0));
-    st_coh(z + e, sv);
+  if (row && c == 0) {
+    if (e != E && !finite_f(acc)) record_err(status, err_key(kPhLogit, 0, 0, e, 0));
+    st_coh_u64(zt + e, ((uint64_t)launch << 32) | f2u(acc));
   }
-  wait_stores();
-  __syncthreads();
-  unsigned last = 0;
-  if (lane == 0) last = atomicAdd(front, 1u) == (unsigned)(nR - 1);
-  last = __shfl(last, 0);
-  if (!last) return;
-  if (lane == 0) atomicExch(front, 0u);
-  route_select_token<NE, true>(z, E + 1, E, L.K, 1, 0, lane, &sw[0][0], ids, probs, shg, status,
-                               [] {
-                                 __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-                                 __builtin_amdgcn_wave_barrier();
-                               });
+}
+
+// The chain-ordered copy of the router and the shared gate for k_gguf_front:
+// rows of kFrontMaxH floats (row E: the shared gate) as float4 groups
+// g = 16 q + c holding the elements c + 16 (4q + u), u = 0..3 (chain c's
+// steps 4q .. 4q + 3; zero past H), so that group q of the 16 chains is one
+// contiguous 256-byte read.
+__global__ void k_chain_router(const float* __restrict__ router, const float* __restrict__ shgate,
+                               int E, int H, float* __restrict__ out) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (int64_t)(E + 1) * kFrontMaxH) return;
+  const int e = (int)(i / kFrontMaxH), p = (int)(i % kFrontMaxH);
+  const int q = p >> 6, c = (p >> 2) & 15, u = p & 3;
+  const int k = c + 64 * q + 16 * u;
+  const float* src = e == E ? shgate : router + (int64_t)e * H;
+  out[i] = k < H ? src[k] : 0.0f;
 }
 
 // k_gguf_experts: one workgroup of 8 waves per CU, all resident together.
 // Phase 1: the K x I routed (gate, up) row pairs in blocks of 16 per
 // workgroup, every weight chunk requested before the first is decoded; a
 // block's h goes to the device-coherent level as one write and the block is
-// counted in its slot's counter (hcnt[16 s]).  Phase 2: workgroup b owns output rows 8b .. 8b + 7 (and
-// 8b + 8G ..): wave w requests the chunks of row 8b + w of the shared
-// expert (whose h the front launch wrote) and of the 8 rows of routed slot
-// w, waits for slot w's count, and forms the dot products; eight lanes
+// counted in its slot's counter (hcnt[16 s]).  Phase 2: workgroup b owns
+// output rows 8b .. 8b + 7 (and 8b + 8G ..): wave w requests the chunks of
+// row 8b + w of the shared expert (whose h the front launch wrote) and of
+// the 8 rows of routed slot w, waits for slot w's count, and forms the dot
+// products; eight lanes
 // then combine each row in moe_aggregate_forward's order
-// (y = sum_k p_k r_k + g r_sh (+ residual)).  Q3_K experts take the
+// (y = sum_k p_k r_k + g r_sh (+ residual), k in probability order).
+// Wave kSoftWave forms the K probabilities and their order before phase 2
+// (gguf_slot_probs); workgroup 0 writes ids, probs and the shared gate.  Q3_K experts take the
 // separate-load path (q3_load / q3_decode); other types decode as they load.
+// Bounded poll until *c reaches target (wrap-safe); on reaching the limit
+// records a sync error and returns false, so that the caller skips later
+// waits and the grid drains.
+__device__ __forceinline__ bool wait_count(const unsigned* c, unsigned target,
+                                           unsigned long long* status) {
+  for (long i = 0; i < kSpinLimit; ++i) {
+    const unsigned v =
+        __hip_atomic_load(const_cast<unsigned*>(c), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if ((int)(v - target) >= 0) return true;
+    __builtin_amdgcn_s_sleep(1);
+  }
+  record_err(status, err_key(kPhSync, 0, 0, 0, 0));
+  return false;
+}
+
 __device__ __forceinline__ int64_t lane64(int64_t v, int l) {
   const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, l);
   const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)((uint64_t)v >> 32), l);
   return (int64_t)(((uint64_t)hi << 32) | lo);
 }
 
-template <int T>
+// p_k = exp(z_k - max) * (1/S) for the K experts of the token (lane k < K:
+// slot k's expert idk and its logit zk; max and 1/S from the front launch,
+// router_softmax's terms, src/layers/router.mojo:140-183), their
+// (p desc, id asc) order and select_topk's checks (src/layers/topk.mojo:
+// 109-128) on one wave.  To LDS: sp[r], sslot[r], sid[r] (probability, slot
+// and id of rank r).  Only the `record` workgroup writes error keys; the
+// renormalisation-leak check re-forms every probability from the tagged
+// logits.
+constexpr int kSoftWave = 7;
+template <int R>
+__device__ __forceinline__ void gguf_slot_probs(float zk, int idk, float m, float inv,
+                                                const uint64_t* zt, int E, int K, float* sev,
+                                                float* sp, int* sslot, int* sid, bool record,
+                                                unsigned long long* status) {
+  const int lane = threadIdx.x & 63;
+  auto wave_sync = [] {
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+  };
+  const float pk = lane < K ? dm_expf(zk - m) * inv : 0.0f;
+  // rank of slot k: (p desc, id asc; the slot breaks any remaining tie so
+  // that the ranks are a permutation whatever the inputs)
+  const uint32_t kk = f2key(pk);
+  int rank = 0;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const uint32_t kj = (uint32_t)__builtin_amdgcn_readlane((int)kk, j);
+    const int ij = __builtin_amdgcn_readlane(idk, j);
+    if (j < K && lane < K)
+      rank += (kj > kk || (kj == kk && (ij < idk || (ij == idk && j < lane)))) ? 1 : 0;
+  }
+  if (lane < K) {
+    sp[rank] = pk;
+    sslot[rank] = lane;
+    sid[rank] = idk;
+  }
+  if (!record) return;
+  wave_sync();
+  float sum_topk = 0.0f;
+#pragma unroll
+  for (int r = 0; r < 8; ++r)
+    if (r < K) sum_topk = sum_topk + sp[r];
+  if (lane == 0 && sum_topk > 1.00001f) record_err(status, err_key(kPhTopk, 0, 0, 0, kTkSum));
+  if (K < E && __builtin_fabsf(sum_topk - 1.0f) < 1e-6f) {
+#pragma unroll
+    for (int i = 0; i < 4 * R; ++i) {
+      const int e = lane + 64 * i;
+      if (e < E) sev[e] = dm_expf(u2f((uint32_t)zt[e]) - m) * inv;
+    }
+    wave_sync();
+    const float sum_all = seq_sum(sev, E);
+    if (lane == 0 && sum_all - sum_topk > 1e-5f)
+      record_err(status, err_key(kPhTopk, 0, 0, 0, kTkLeak));
+  }
+}
+
+template <int T, int R>
 __global__ __launch_bounds__(512) void k_gguf_experts(
-    GgufMoeDev L, const float* __restrict__ x, const int32_t* __restrict__ ids,
-    const float* __restrict__ probs, const float* __restrict__ shg,
-    const float* __restrict__ residual, float* __restrict__ y, float* __restrict__ h, int ldh,
-    unsigned* hcnt, unsigned target, unsigned long long* status) {
+    GgufMoeDev L, const float* __restrict__ x, const int32_t* __restrict__ sel,
+    const uint64_t* __restrict__ zt, const float* __restrict__ soft,
+    const float* __restrict__ residual, float* __restrict__ y,
+    int32_t* __restrict__ ids, float* __restrict__ probs, float* __restrict__ shg,
+    const float* __restrict__ hsh, float* __restrict__ h, int ldh, unsigned* hcnt,
+    unsigned target, unsigned long long* status) {
   __shared__ float part[8][33];
+  __shared__ float sev[256 * R];
+  __shared__ float sp[8];
+  __shared__ int sslot[8], sid[8];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int wid = __builtin_amdgcn_readfirstlane(w);  // w as a uniform value
   const int G = (int)gridDim.x;
   const int H = L.H, E = L.E, K = L.K, I = L.I, Ish = L.Ish;
-  // lane s < K: the payload offsets of routed slot s
-  const int es = min(max((int)ids[min(lane, K - 1)], 0), E - 1);
+  // lane s < K: the expert and payload offsets of routed slot s
+  const int es = min(max((int)sel[min(lane, K - 1)], 0), E - 1);
   int64_t og, ou, od;
   if (L.estride > 0) {
     og = (int64_t)(3 * es) * L.estride;
@@ -521,23 +706,14 @@ __global__ __launch_bounds__(512) void k_gguf_experts(
     ou = L.off[(size_t)es * 3 + 1];
     od = L.off[(size_t)es * 3 + 2];
   }
-  // what the combine reads, requested now: the K probabilities and the
-  // shared gate (every lane), the residual of this lane's row
-  float pk[8], g_sh = shg[0];
-#pragma unroll
-  for (int k = 0; k < 8; ++k) pk[k] = probs[min(k, K - 1)];
-  // phase 2's first rows: their down chunks requested before phase 1 (Q3_K)
+  // for the combine: the slot's logit and the front launch's softmax terms
+  // (requested after the offsets, so that waiting for those does not wait
+  // for these)
+  const float zk = reinterpret_cast<const float*>(zt)[2 * es];  // the word's low half
+  const float sm_max = soft[0], sm_inv = soft[1], sg = soft[2];
   const uint8_t* wsh = L.raw + L.off[(size_t)E * 3 + 2];
   const int cs = min(lane * 8, Ish - 8), cr = min(lane * 8, I - 8);
   const int dfirst = (int)blockIdx.x * 8;
-  Q3Raw<8> pre_s, pre_r[8];
-  if constexpr (T == kGgmlQ3_K) {
-    const uint8_t* wrd0 = L.raw + lane64(od, min(w, K - 1));
-    pre_s = q3_load<8>(wsh, (int64_t)min(dfirst + w, H - 1) * Ish + cs);
-#pragma unroll
-    for (int i = 0; i < 8; ++i)
-      pre_r[i] = q3_load<8>(wrd0, (int64_t)min(dfirst + i, H - 1) * I + cr);
-  }
   // ---- phase 1: routed gate / up.  Workgroup b takes blocks of 16 row
   // pairs (16 pb .. 16 pb + 15 of slot 16 pb / I; wave w rows 2w, 2w + 1),
   // publishes the block's 16 h values as one write and counts the block in
@@ -571,15 +747,20 @@ __global__ __launch_bounds__(512) void k_gguf_experts(
       for (int q = 0; q < 2; ++q) {
 #pragma unroll
         for (int j = 0; j < NJ; ++j) {
-          if (lane * 16 + 1024 * j >= H) continue;
+          // every chunk is decoded (an unused load left in flight would hold
+          // its registers); chunks past H do not enter the sums
+          const bool in = lane * 16 + 1024 * j < H;
           f32x4 g4[4], u4[4];
           q3_decode<16>(rg[q][j], g4);
           q3_decode<16>(ru[q][j], u4);
+          float a = ag[q], bu = au[q];
 #pragma unroll
           for (int u = 0; u < 4; ++u) {
-            ag[q] = dot4(g4[u], xv[j][u], ag[q]);
-            au[q] = dot4(u4[u], xv[j][u], au[q]);
+            a = dot4(g4[u], xv[j][u], a);
+            bu = dot4(u4[u], xv[j][u], bu);
           }
+          ag[q] = in ? a : ag[q];
+          au[q] = in ? bu : au[q];
         }
       }
     } else {
@@ -618,9 +799,21 @@ __global__ __launch_bounds__(512) void k_gguf_experts(
     __syncthreads();
     if (threadIdx.x == 0) atomicAdd(hcnt + 16 * slot, 1u);
   }
+  // phase 2's first rows: their down chunks requested now, in flight
+  // while the slots' h counts are awaited (Q3_K)
+  const uint8_t* wrd = L.raw + lane64(od, min(w, K - 1));
+  Q3Raw<8> pre_s, pre_r[8];
+  if constexpr (T == kGgmlQ3_K) {
+    pre_s = q3_load<8>(wsh, (int64_t)min(dfirst + w, H - 1) * Ish + cs);
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      pre_r[i] = q3_load<8>(wrd, (int64_t)min(dfirst + i, H - 1) * I + cr);
+  }
+  if (wid == kSoftWave)
+    gguf_slot_probs<R>(zk, es, sm_max, sm_inv, zt, E, K, sev, sp, sslot, sid, blockIdx.x == 0,
+                       status);
   // ---- phase 2: down projections and the combine
   bool ready = false;
-  const uint8_t* wrd = L.raw + lane64(od, min(w, K - 1));
   const bool ls = lane * 8 < Ish, lr = lane * 8 < I;
   for (int d0 = (int)blockIdx.x * 8; d0 < H; d0 += 8 * G) {
     const int nd = min(8, H - d0);
@@ -643,7 +836,7 @@ __global__ __launch_bounds__(512) void k_gguf_experts(
     }
     // the shared expert's row d0 + w (h written by the front launch)
     {
-      const float* hp = h + (size_t)K * ldh + cs;
+      const float* hp = hsh + cs;
       float a = dot4(ws[0], *reinterpret_cast<const f32x4*>(hp), 0.0f);
       a = dot4(ws[1], *reinterpret_cast<const f32x4*>(hp + 4), a);
       a = wave_sum_dpp(ls ? a : 0.0f);
@@ -680,11 +873,18 @@ __global__ __launch_bounds__(512) void k_gguf_experts(
       float acc = 0.0f;
 #pragma unroll
       for (int k = 0; k < 8; ++k)
-        if (k < K) acc = acc + pk[k] * part[i][k];
-      float total = acc + g_sh * part[i][K];
+        if (k < K) acc = acc + sp[k] * part[i][sslot[k]];
+      float total = acc + sg * part[i][K];
       if (residual) total = total + res;
       if (!finite_f(total)) record_err(status, err_key(kPhAgg, 0, 0, d, 0));
       y[d] = total;
+    }
+    if (blockIdx.x == 0 && d0 == 0) {
+      if ((int)threadIdx.x < K) {
+        ids[threadIdx.x] = sid[threadIdx.x];
+        probs[threadIdx.x] = sp[threadIdx.x];
+      }
+      if (threadIdx.x == 0) shg[0] = sg;
     }
     __syncthreads();
   }
@@ -773,23 +973,42 @@ hipError_t launch_gguf_down_combine(const GgufMoeDev& L, const float* h, int ldh
 #undef DM_GGUF_DISPATCH_W
 
 bool gguf_one_token_supported(const GgufMoeDev& L) {
-  return L.H % 16 == 0 && L.H <= kFrontMaxH && L.I % 16 == 0 && L.I <= 512 && L.Ish % 8 == 0 &&
+  return L.H % 64 == 0 && L.H <= kFrontMaxH && L.I % 16 == 0 && L.I <= 512 && L.Ish % 8 == 0 &&
          L.Ish <= 512 && L.K <= 8 && L.E + 1 <= 512 && L.type != kGgmlF32 && L.type != kGgmlBF16;
 }
 
+static size_t zt_bytes(const GgufMoeDev& L) { return ((size_t)(L.E + 1) * 8 + 255) & ~(size_t)255; }
+
+static size_t hsh_bytes(const GgufMoeDev& L) { return ((size_t)L.Ish * 4 + 255) & ~(size_t)255; }
+
 size_t gguf_one_token_sync_bytes(const GgufMoeDev& L) {
-  const int ldh = L.I > L.Ish ? L.I : L.Ish;
-  return kSyncHead + (((size_t)(L.E + 1) * 4 + 255) & ~(size_t)255) + (size_t)(L.K + 1) * ldh * 4;
+  return kSyncHead + zt_bytes(L) + hsh_bytes(L) + (size_t)L.K * L.I * 4;
+}
+
+size_t gguf_chain_router_bytes(const GgufMoeDev& L) {
+  return (size_t)(L.E + 1) * kFrontMaxH * sizeof(float);
+}
+
+hipError_t launch_chain_router(const GgufMoeDev& L, float* out, hipStream_t st) {
+  if (L.H % 64 || L.H > kFrontMaxH || L.E < 1) return hipErrorInvalidValue;
+  const int64_t n = (int64_t)(L.E + 1) * kFrontMaxH;
+  k_chain_router<<<(unsigned)((n + 255) / 256), 256, 0, st>>>(L.router, L.shgate, L.E, L.H, out);
+  return hipGetLastError();
 }
 
 int gguf_experts_occupancy(const GgufMoeDev& L, int* per_cu) {
   hipError_t e = hipErrorInvalidValue;
+  const bool r1 = L.E <= 256;
+#define DM_OCC(TY)                                                                                \
+  e = r1 ? hipOccupancyMaxActiveBlocksPerMultiprocessor(per_cu, k_gguf_experts<TY, 1>, 512, 0)   \
+         : hipOccupancyMaxActiveBlocksPerMultiprocessor(per_cu, k_gguf_experts<TY, 2>, 512, 0)
   switch (L.type) {
-    case kGgmlQ8_0: e = hipOccupancyMaxActiveBlocksPerMultiprocessor(per_cu, k_gguf_experts<kGgmlQ8_0>, 512, 0); break;
-    case kGgmlQ4_K: e = hipOccupancyMaxActiveBlocksPerMultiprocessor(per_cu, k_gguf_experts<kGgmlQ4_K>, 512, 0); break;
-    case kGgmlQ3_K: e = hipOccupancyMaxActiveBlocksPerMultiprocessor(per_cu, k_gguf_experts<kGgmlQ3_K>, 512, 0); break;
+    case kGgmlQ8_0: DM_OCC(kGgmlQ8_0); break;
+    case kGgmlQ4_K: DM_OCC(kGgmlQ4_K); break;
+    case kGgmlQ3_K: DM_OCC(kGgmlQ3_K); break;
     default: break;
   }
+#undef DM_OCC
   return e == hipSuccess ? 0 : -1;
 }
 
@@ -797,38 +1016,37 @@ hipError_t launch_gguf_one_token(const GgufMoeDev& L, const float* x, const floa
                                  float* y, int32_t* ids, float* probs, float* shg, void* sync,
                                  unsigned launch, int grid, unsigned long long* status,
                                  hipStream_t st) {
-  if (!gguf_one_token_supported(L) || grid <= 0 || launch == 0) return hipErrorInvalidValue;
-  const int ldh = L.I > L.Ish ? L.I : L.Ish;
+  if (!gguf_one_token_supported(L) || !L.rchain || grid <= 0 || launch == 0)
+    return hipErrorInvalidValue;
   uint8_t* sb = static_cast<uint8_t*>(sync);
-  unsigned* front = reinterpret_cast<unsigned*>(sb);
   unsigned* hcnt = reinterpret_cast<unsigned*>(sb + 128);  // slot s at 64 s bytes
-  float* z = reinterpret_cast<float*>(sb + kSyncHead);
-  float* h = reinterpret_cast<float*>(sb + kSyncHead + (((size_t)(L.E + 1) * 4 + 255) & ~(size_t)255));
+  int32_t* sel = reinterpret_cast<int32_t*>(sb + kSelOff);
+  float* selp = reinterpret_cast<float*>(sb + kSelOff + 64);
+  float* soft = reinterpret_cast<float*>(sb + kSelOff + 128);
+  uint64_t* zt = reinterpret_cast<uint64_t*>(sb + kSyncHead);
+  float* hsh = reinterpret_cast<float*>(sb + kSyncHead + zt_bytes(L));
+  float* h = reinterpret_cast<float*>(sb + kSyncHead + zt_bytes(L) + hsh_bytes(L));
   const int nR = (L.E + 1 + kFrontRows - 1) / kFrontRows;
-  const dim3 g1((unsigned)(nR + L.Ish)), g2((unsigned)grid);
+  const dim3 g1((unsigned)(2 + nR + L.Ish)), g2((unsigned)grid);
   const unsigned target = launch * (unsigned)(L.I / 16);  // blocks per slot
-  const int ne = (L.E + 63) / 64;
-#define DM_FRONT(TY, N)                                                                      \
-  k_gguf_front<TY, 16, N><<<g1, 64, 0, st>>>(L, x, nR, z, h, ldh, front, ids, probs, shg, status)
-#define DM_FRONT_NE(TY)              \
-  if (ne <= 1) DM_FRONT(TY, 1);      \
-  else if (ne <= 2) DM_FRONT(TY, 2); \
-  else if (ne <= 4) DM_FRONT(TY, 4); \
-  else DM_FRONT(TY, 8);
+#define DM_ONE(TY, R)                                                                       \
+  k_gguf_front<TY, 16, R><<<g1, 64, 0, st>>>(L, x, nR, zt, hsh, sel, selp, soft, launch, status); \
+  k_gguf_experts<TY, R><<<g2, 512, 0, st>>>(L, x, sel, zt, soft, residual, y, ids, probs, shg,   \
+                                            hsh, h, L.I, hcnt, target, status)
+#define DM_ONE_R(TY)    \
+  if (L.E <= 256) {     \
+    DM_ONE(TY, 1);      \
+  } else {              \
+    DM_ONE(TY, 2);      \
+  }
   switch (L.type) {
-    case kGgmlQ8_0: DM_FRONT_NE(kGgmlQ8_0)
-      k_gguf_experts<kGgmlQ8_0><<<g2, 512, 0, st>>>(L, x, ids, probs, shg, residual, y, h, ldh, hcnt, target, status);
-      break;
-    case kGgmlQ4_K: DM_FRONT_NE(kGgmlQ4_K)
-      k_gguf_experts<kGgmlQ4_K><<<g2, 512, 0, st>>>(L, x, ids, probs, shg, residual, y, h, ldh, hcnt, target, status);
-      break;
-    case kGgmlQ3_K: DM_FRONT_NE(kGgmlQ3_K)
-      k_gguf_experts<kGgmlQ3_K><<<g2, 512, 0, st>>>(L, x, ids, probs, shg, residual, y, h, ldh, hcnt, target, status);
-      break;
+    case kGgmlQ8_0: DM_ONE_R(kGgmlQ8_0) break;
+    case kGgmlQ4_K: DM_ONE_R(kGgmlQ4_K) break;
+    case kGgmlQ3_K: DM_ONE_R(kGgmlQ3_K) break;
     default: return hipErrorInvalidValue;
   }
-#undef DM_FRONT_NE
-#undef DM_FRONT
+#undef DM_ONE_R
+#undef DM_ONE
   return hipGetLastError();
 }
 

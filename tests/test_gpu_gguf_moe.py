@@ -183,14 +183,16 @@ def test_partial_blocks_rejected(block, oracle, tmp_path):
             "not whole blocks of 32")
 
 
-def test_forward_errors(block, tmp_path):
+@pytest.mark.parametrize("T", [2, 1])
+def test_forward_errors(block, tmp_path, T):
+    """Error texts of the block; T = 1 takes the two-launch single-token form."""
     dims = (128, 4, 2, 32, 32)
     g = _layer_file(tmp_path, "ok.gguf", lambda ts: ts)
     block.upload_layer_gguf(24, dims, g)
-    x = synth.make_activations(np.random.default_rng(90), (2, 128))
-    x[1, 3] = np.nan
+    x = synth.make_activations(np.random.default_rng(90), (T, 128))
+    x[T - 1, 3] = np.nan
     with pytest.raises(DismoenError) as ei:
-        block.forward_port_moe_gguf(x, None, 24, 2)
+        block.forward_port_moe_gguf(x, None, 24, T)
     assert json.loads(str(ei.value)) == {"error_type": "ACT_LOAD_FAILED",
                                          "detail": "non-finite value in activation",
                                          "stage": "router", "layer": 24}
@@ -207,15 +209,48 @@ def test_forward_errors(block, tmp_path):
         return out
     g = _layer_file(tmp_path, "inf.gguf", bad)
     block.upload_layer_gguf(25, dims, g)
-    x = synth.make_activations(np.random.default_rng(91), (2, 128))
+    x = synth.make_activations(np.random.default_rng(91), (T, 128))
     with pytest.raises(DismoenError) as ei:
-        block.forward_port_moe_gguf(x, None, 25, 2)
+        block.forward_port_moe_gguf(x, None, 25, T)
     j = json.loads(str(ei.value))
     assert j["error_type"] == "EXPERT_ERROR" and j["detail"] == "non-finite in gate projection"
     assert (j["layer"], j["expert_id"]) == (128, 32)
     # the layer recovers: the same layer, finite inputs, other weights fine
     block.upload_layer_gguf(25, dims, _layer_file(tmp_path, "ok2.gguf", lambda ts: ts))
-    block.forward_port_moe_gguf(x, None, 25, 2)
+    block.forward_port_moe_gguf(x, None, 25, T)
+
+
+def _tied_router(ts, E, H):
+    """Router rows 2i + 1 copied from rows 2i: every logit appears twice."""
+    out = list(ts)
+    i = [k for k, t in enumerate(out) if t[0].endswith("ffn_gate_exps.weight")][0]
+    raw = bytearray(out[i][3])
+    rb = H // 32 * 34  # one Q8_0 row
+    for e in range(0, E - 1, 2):
+        raw[(e + 1) * rb:(e + 2) * rb] = raw[e * rb:(e + 1) * rb]
+    out[i] = (out[i][0], out[i][1], out[i][2], bytes(raw))
+    return out
+
+
+@pytest.mark.parametrize("E,K,ties", [(256, 8, False), (256, 8, True), (256, 7, True),
+                                      (300, 8, False), (300, 5, True)])
+def test_single_token_routing(block, oracle, tmp_path, E, K, ties):
+    """Single-token calls (the two-launch form) on 256 and 300 experts: the
+    top-k on the logits; with duplicated router rows, equal probabilities
+    inside the selection (ordered by id) and, for odd K, a tie at the top-k
+    boundary (the exact-probability path)."""
+    H, I, Ish = 256, 32, 32
+    ts = synth.make_gguf_moe_layer(H, E, I, Ish, seed=E + K)
+    if ties:
+        ts = _tied_router(ts, E, H)
+    p = str(tmp_path / "r.gguf")
+    gguf.write_gguf(p, ts)
+    dims = (H, E, K, I, Ish)
+    with gguf.parse_gguf_index(p) as g:
+        block.upload_layer_gguf(27, dims, g)
+        for t in range(4):
+            print(f"E={E} K={K} ties={ties} token {t}", flush=True)
+            _check_layer(block, oracle, g, 0, dims, 27, T=1, seed=100 + t)
 
 
 def test_many_tokens_cross_launch_chunks(block, tmp_path):
