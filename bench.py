@@ -34,13 +34,14 @@ HBM_PEAK_GBPS = 8000.0
 # WRITE_SIZE runs (scaled by a copy-kernel calibration) recorded in this file
 TRAFFIC_PROFILE = os.path.join("profiles", "k_moe_decode_qwen36_layer_decode.md")
 GGUF_PROFILE = os.path.join("profiles", "k_dequant_gguf_q3k_expert_layer.md")
+GGUF_MOE_PROFILE = os.path.join("profiles", "gguf_moe_q3k_layer_decode.md")
 
 
-def profiled_traffic(profile=TRAFFIC_PROFILE):
+def profiled_traffic(profile=TRAFFIC_PROFILE, key="traffic_bytes_per_launch"):
     try:
         with open(os.path.join(ROOT, profile)) as f:
             for line in f:
-                if line.startswith("traffic_bytes_per_launch:"):
+                if line.startswith(key + ":"):
                     return int(line.split(":")[1])
     except OSError:
         pass
@@ -363,7 +364,9 @@ def gguf_moe(a, blk, stream, dev):
                    "roofline": {"bound": "hbm", "kernel": "gguf moe block (front + experts launches)",
                                 "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS,
                                 "unit": "GB/s", "frac": round(gbps / HBM_PEAK_GBPS, 4),
-                                "traffic": None, "bytes_per_token": alg}}
+                                "traffic": profiled_traffic(GGUF_MOE_PROFILE,
+                                                            "traffic_bytes_per_token"),
+                                "traffic_source": GGUF_MOE_PROFILE, "bytes_per_token": alg}}
             if not a.no_cpu:
                 sys.path.insert(0, os.path.join(ROOT, "oracle"))
                 import oracle as orc

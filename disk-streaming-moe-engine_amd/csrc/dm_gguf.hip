@@ -200,21 +200,8 @@ __device__ __forceinline__ float dot4(f32x4 a, f32x4 b, float acc) {
 // byte and d, so the block header is decoded once per eight (sixteen).
 template <int T, int W>
 __device__ __forceinline__ void valuesW(const uint8_t* raw, int64_t e0, int layout, f32x4 (&v)[W / 4]) {
-  if constexpr (T == kGgmlQ3_K && W == 16) {
-    // sixteen weights: two hmask bytes, four code bytes, one scale byte
-    const uint8_t* blk = raw + (e0 >> 8) * 114;
-    const int e = (int)(e0 & 255);
-    const uint16_t* h = reinterpret_cast<const uint16_t*>(blk);
-    const uint32_t hm = h[e >> 4];
-    const uint32_t qs = (uint32_t)h[16 + (e >> 3)] | ((uint32_t)h[17 + (e >> 3)] << 16);
-    const float fs = (float)((int)blk[96 + (e >> 4)] - 32) * h2f(h[56]);
-    float w[16];
-#pragma unroll
-    for (int i = 0; i < 16; ++i)
-      w[i] = fs * (float)((int)((((hm >> i) & 1) << 2) | ((qs >> (2 * i)) & 3)) - 4);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) v[j] = f32x4{w[4 * j], w[4 * j + 1], w[4 * j + 2], w[4 * j + 3]};
-  } else if constexpr (T == kGgmlQ3_K && W == 8) {
+  static_assert(!(T == kGgmlQ3_K && W == 16), "Q3_K gate/up rows go through gu_dot16");
+  if constexpr (T == kGgmlQ3_K && W == 8) {
     const uint8_t* blk = raw + (e0 >> 8) * 114;
     const int e = (int)(e0 & 255);
     const uint16_t* h = reinterpret_cast<const uint16_t*>(blk);
@@ -230,6 +217,98 @@ __device__ __forceinline__ void valuesW(const uint8_t* raw, int64_t e0, int layo
   } else {
 #pragma unroll
     for (int j = 0; j < W / 4; ++j) v[j] = values4<T>(raw, e0 + 4 * j, layout);
+  }
+}
+
+// The bytes of W consecutive Q3_K weights (W = 8 or 16, at an element that
+// is a multiple of W) as separate loads, so that a wave can request every
+// chunk it needs before decoding the first.
+template <int W>
+struct Q3Raw {
+  uint32_t hm, q0, q1, sc, d;
+};
+template <int W>
+__device__ __forceinline__ Q3Raw<W> q3_load(const uint8_t* raw, int64_t e0) {
+  const uint8_t* blk = raw + (e0 >> 8) * 114;
+  const int e = (int)(e0 & 255);
+  const uint16_t* h = reinterpret_cast<const uint16_t*>(blk);
+  Q3Raw<W> r;
+  if constexpr (W == 16) {
+    r.hm = h[e >> 4];
+    r.q0 = h[16 + (e >> 3)];
+    r.q1 = h[17 + (e >> 3)];
+  } else {
+    r.hm = blk[e >> 3];
+    r.q0 = h[16 + (e >> 3)];
+    r.q1 = 0;
+  }
+  r.sc = blk[96 + (e >> 4)];
+  r.d = h[56];
+  return r;
+}
+// the same values valuesW<kGgmlQ3_K, W> forms from these bytes
+template <int W>
+__device__ __forceinline__ void q3_decode(const Q3Raw<W>& r, f32x4 (&v)[W / 4]) {
+  const uint32_t qs = r.q0 | (r.q1 << 16);
+  const float fs = (float)((int)r.sc - 32) * h2f(r.d);
+  float w[W];
+#pragma unroll
+  for (int i = 0; i < W; ++i)
+    w[i] = fs * (float)((int)((((r.hm >> i) & 1) << 2) | ((qs >> (2 * i)) & 3)) - 4);
+#pragma unroll
+  for (int j = 0; j < W / 4; ++j) v[j] = f32x4{w[4 * j], w[4 * j + 1], w[4 * j + 2], w[4 * j + 3]};
+}
+
+// x[0] + x[1] + ... + x[15] in element order: the chunk term of q3_dot16.
+__device__ __forceinline__ float xsum16(const f32x4 (&x)[4]) {
+  float s = 0.0f;
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    s = s + x[u].x;
+    s = s + x[u].y;
+    s = s + x[u].z;
+    s = s + x[u].w;
+  }
+  return s;
+}
+
+// acc + sum_i w_i x_i over sixteen Q3_K weights w_i = fs (q_i - 4) of one
+// 16-weight scale group, formed as fs (sum_i q_i x_i - 4 xs) with xs =
+// xsum16(x): the 3-bit codes enter the products as they are, so a weight
+// costs two bit-field extractions, a conversion and a multiply-add.
+__device__ __forceinline__ float q3_dot16(const Q3Raw<16>& r, const f32x4 (&x)[4], float xs,
+                                          float acc) {
+  const uint32_t qs = r.q0 | (r.q1 << 16);
+  const float fs = (float)((int)r.sc - 32) * h2f(r.d);
+  float t = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const uint32_t q = __builtin_amdgcn_ubfe(qs, 2 * i, 2) | (__builtin_amdgcn_ubfe(r.hm, i, 1) << 2);
+    t = __builtin_fmaf((float)q, x[i >> 2][i & 3], t);
+  }
+  return __builtin_fmaf(fs, __builtin_fmaf(-4.0f, xs, t), acc);
+}
+
+// Gate and up dot-product terms of the sixteen weights at e0 of a row pair
+// (x: the sixteen activations): Q3_K through q3_dot16, the other types as
+// dequantised values.  Shared by every gate/up kernel, so that one token
+// gives the same bits whichever launch form computes it.
+template <int T>
+__device__ __forceinline__ void gu_dot16(const uint8_t* wg, const uint8_t* wu, int64_t e0,
+                                         int layout, const f32x4 (&xv)[4], float& ag, float& au) {
+  if constexpr (T == kGgmlQ3_K) {
+    const float xs = xsum16(xv);
+    ag = q3_dot16(q3_load<16>(wg, e0), xv, xs, ag);
+    au = q3_dot16(q3_load<16>(wu, e0), xv, xs, au);
+  } else {
+    f32x4 g4[4], u4[4];
+    valuesW<T, 16>(wg, e0, layout, g4);
+    valuesW<T, 16>(wu, e0, layout, u4);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      ag = dot4(g4[j], xv[j], ag);
+      au = dot4(u4[j], xv[j], au);
+    }
   }
 }
 
@@ -252,14 +331,21 @@ __global__ __launch_bounds__(256) void k_gguf_gateup(GgufMoeDev L, const float* 
   const int64_t base = (int64_t)r * L.H;
   float ag = 0.0f, au = 0.0f;
   for (int c = lane * W; c < L.H; c += 64 * W) {
-    f32x4 g4[W / 4], u4[W / 4];
-    valuesW<T, W>(wg, base + c, L.layout, g4);
-    valuesW<T, W>(wu, base + c, L.layout, u4);
+    if constexpr (W == 16) {
+      f32x4 xv[4];
 #pragma unroll
-    for (int j = 0; j < W / 4; ++j) {
-      const f32x4 xv = *reinterpret_cast<const f32x4*>(xt + c + 4 * j);
-      ag = dot4(g4[j], xv, ag);
-      au = dot4(u4[j], xv, au);
+      for (int j = 0; j < 4; ++j) xv[j] = *reinterpret_cast<const f32x4*>(xt + c + 4 * j);
+      gu_dot16<T>(wg, wu, base + c, L.layout, xv, ag, au);
+    } else {
+      f32x4 g4[W / 4], u4[W / 4];
+      valuesW<T, W>(wg, base + c, L.layout, g4);
+      valuesW<T, W>(wu, base + c, L.layout, u4);
+#pragma unroll
+      for (int j = 0; j < W / 4; ++j) {
+        const f32x4 xv = *reinterpret_cast<const f32x4*>(xt + c + 4 * j);
+        ag = dot4(g4[j], xv, ag);
+        au = dot4(u4[j], xv, au);
+      }
     }
   }
   ag = wave_sum_dpp(ag);
@@ -320,46 +406,6 @@ __global__ __launch_bounds__(256) void k_gguf_down_combine(
   }
 }
 
-// ---- one token in two launches ----------------------------------------------
-// The bytes of W consecutive Q3_K weights (W = 8 or 16, at an element that
-// is a multiple of W) as separate loads, so that a wave can request every
-// chunk it needs before decoding the first (valuesW decodes as it loads).
-template <int W>
-struct Q3Raw {
-  uint32_t hm, q0, q1, sc, d;
-};
-template <int W>
-__device__ __forceinline__ Q3Raw<W> q3_load(const uint8_t* raw, int64_t e0) {
-  const uint8_t* blk = raw + (e0 >> 8) * 114;
-  const int e = (int)(e0 & 255);
-  const uint16_t* h = reinterpret_cast<const uint16_t*>(blk);
-  Q3Raw<W> r;
-  if constexpr (W == 16) {
-    r.hm = h[e >> 4];
-    r.q0 = h[16 + (e >> 3)];
-    r.q1 = h[17 + (e >> 3)];
-  } else {
-    r.hm = blk[e >> 3];
-    r.q0 = h[16 + (e >> 3)];
-    r.q1 = 0;
-  }
-  r.sc = blk[96 + (e >> 4)];
-  r.d = h[56];
-  return r;
-}
-// the same values valuesW<kGgmlQ3_K, W> forms from these bytes
-template <int W>
-__device__ __forceinline__ void q3_decode(const Q3Raw<W>& r, f32x4 (&v)[W / 4]) {
-  const uint32_t qs = r.q0 | (r.q1 << 16);
-  const float fs = (float)((int)r.sc - 32) * h2f(r.d);
-  float w[W];
-#pragma unroll
-  for (int i = 0; i < W; ++i)
-    w[i] = fs * (float)((int)((((r.hm >> i) & 1) << 2) | ((qs >> (2 * i)) & 3)) - 4);
-#pragma unroll
-  for (int j = 0; j < W / 4; ++j) v[j] = f32x4{w[4 * j], w[4 * j + 1], w[4 * j + 2], w[4 * j + 3]};
-}
-
 // k_gguf_front: workgroup 0 selects, workgroup 1 forms the softmax
 // normaliser, workgroups 2 .. nR + 1 the router logits, the rest the shared
 // expert's h rows (they do not depend on the routing).  A router workgroup
@@ -412,16 +458,11 @@ __global__ __launch_bounds__(64) void k_gguf_front(GgufMoeDev L, const float* __
     const uint8_t* wu = L.raw + L.off[(size_t)E * 3 + 1];
     const int64_t base = (int64_t)r * H;
     float ag = 0.0f, au = 0.0f;
-    for (int c = lane * W; c < H; c += 64 * W) {
-      f32x4 g4[W / 4], u4[W / 4];
-      valuesW<T, W>(wg, base + c, L.layout, g4);
-      valuesW<T, W>(wu, base + c, L.layout, u4);
+    for (int c = lane * 16; c < H; c += 64 * 16) {
+      f32x4 xv[4];
 #pragma unroll
-      for (int j = 0; j < W / 4; ++j) {
-        const f32x4 xv = *reinterpret_cast<const f32x4*>(x + c + 4 * j);
-        ag = dot4(g4[j], xv, ag);
-        au = dot4(u4[j], xv, au);
-      }
+      for (int j = 0; j < 4; ++j) xv[j] = *reinterpret_cast<const f32x4*>(x + c + 4 * j);
+      gu_dot16<T>(wg, wu, base + c, L.layout, xv, ag, au);
     }
     ag = wave_sum_dpp(ag);
     au = wave_sum_dpp(au);
@@ -743,22 +784,18 @@ __global__ __launch_bounds__(512) void k_gguf_experts(
 #pragma unroll
         for (int u = 0; u < 4; ++u) xv[j][u] = *reinterpret_cast<const f32x4*>(x + c + 4 * u);
       }
+      float xs[NJ];
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) xs[j] = xsum16(xv[j]);
 #pragma unroll
       for (int q = 0; q < 2; ++q) {
 #pragma unroll
         for (int j = 0; j < NJ; ++j) {
-          // every chunk is decoded (an unused load left in flight would hold
+          // every chunk is used (an unused load left in flight would hold
           // its registers); chunks past H do not enter the sums
           const bool in = lane * 16 + 1024 * j < H;
-          f32x4 g4[4], u4[4];
-          q3_decode<16>(rg[q][j], g4);
-          q3_decode<16>(ru[q][j], u4);
-          float a = ag[q], bu = au[q];
-#pragma unroll
-          for (int u = 0; u < 4; ++u) {
-            a = dot4(g4[u], xv[j][u], a);
-            bu = dot4(u4[u], xv[j][u], bu);
-          }
+          const float a = q3_dot16(rg[q][j], xv[j], xs[j], ag[q]);
+          const float bu = q3_dot16(ru[q][j], xv[j], xs[j], au[q]);
           ag[q] = in ? a : ag[q];
           au[q] = in ? bu : au[q];
         }
