@@ -622,12 +622,29 @@ __device__ __forceinline__ void lds_wait8(bf16x8 (&b)[kNCT]) {
                : "n"(N));
 }
 
+__device__ __forceinline__ void gu_small_part(const GroupArgs& g, int bx, int by, int w);
+__device__ __forceinline__ void down_small_part(const GroupArgs& g, int bx, int by, int w);
+
 // One workgroup per CU (its LDS), two waves per SIMD: registers up to 256
 // per lane, spent on keeping a whole k-group of B fragments in flight.
+// Workgroups from big_wgs on run the small units of the same stage (sx x sy
+// four-wave parts, two per workgroup): dispatched after every big one, they
+// fill the CUs that the big units' last round leaves idle.
 template <bool GU>
 __global__ __launch_bounds__(kB2Threads) __attribute__((amdgpu_waves_per_eu(2, 2)))
-void k_big(GroupArgs g) {
+void k_big(GroupArgs g, int big_wgs, int sx, int sy) {
   extern __shared__ __attribute__((aligned(16))) unsigned char lds2[];
+  if ((int)blockIdx.x >= big_wgs) {
+    const int w = gwave_id();
+    const int s = 2 * ((int)blockIdx.x - big_wgs) + (w >> 2);
+    if (s < sx * sy) {
+      if (GU)
+        gu_small_part(g, s % sx, s / sx, w & 3);
+      else
+        down_small_part(g, s % sx, s / sx, w & 3);
+    }
+    return;
+  }
   const LayerDev& L = g.L;
   const int H = L.H, K = L.K;
   int ui, fb;
@@ -845,16 +862,18 @@ __device__ __forceinline__ void small_loop(const ExpertView& v0, const ExpertVie
 constexpr int kSmallGuCols = 4 * 16;   // features per small gate/up workgroup
 constexpr int kSmallDnRows = 4 * 32;   // output rows per small down workgroup
 
-__global__ __launch_bounds__(kGThreads) __attribute__((amdgpu_waves_per_eu(3))) void k_gu_small(
-    GroupArgs g) {
-  const int ui = g.meta[1] + blockIdx.x;
+// Small gate/up unit bx (of those after the big ones), features by * 64 ..,
+// on wave w of four; no barriers, so that four waves of a larger workgroup
+// can run it too.
+__device__ __forceinline__ void gu_small_part(const GroupArgs& g, int bx, int by, int w) {
+  const int ui = g.meta[1] + bx;
   if (ui >= g.meta[0]) return;
   const UnitTokens ut = unit_tokens(g.units[ui], g.off, g.L.E, g.T, kSmallMax);
   const LayerDev& L = g.L;
   const int H = L.H, K = L.K, I = ut.shared ? L.Ish : L.I;
-  const int w = gwave_id(), lane = threadIdx.x & 63, q = lane >> 4, j = lane & 15;
-  const int f0 = blockIdx.y * kSmallGuCols + 16 * w;
-  if (f0 >= I) return;  // uniform per wave; no barriers in this kernel
+  const int lane = threadIdx.x & 63, q = lane >> 4, j = lane & 15;
+  const int f0 = by * kSmallGuCols + 16 * w;
+  if (f0 >= I) return;  // uniform per wave
   const size_t mat = (size_t)I * H;
   const ExpertView gv = ut.shared ? ExpertView{L.sgu_nib, L.sgu_sc, I, H}
                                   : ExpertView{L.gu_nib + (size_t)ut.e * mat,
@@ -872,15 +891,15 @@ __global__ __launch_bounds__(kGThreads) __attribute__((amdgpu_waves_per_eu(3))) 
   gu_epilogue<kSmallTiles, 1>(g, ut, I, f0, q, j, acc);
 }
 
-__global__ __launch_bounds__(kGThreads) __attribute__((amdgpu_waves_per_eu(3))) void k_down_small(
-    GroupArgs g) {
-  const int ui = g.meta[1] + blockIdx.x;
+// Small down unit bx, output rows by * 128 .., on wave w of four.
+__device__ __forceinline__ void down_small_part(const GroupArgs& g, int bx, int by, int w) {
+  const int ui = g.meta[1] + bx;
   if (ui >= g.meta[0]) return;
   const UnitTokens ut = unit_tokens(g.units[ui], g.off, g.L.E, g.T, kSmallMax);
   const LayerDev& L = g.L;
   const int H = L.H, I = ut.shared ? L.Ish : L.I;
-  const int w = gwave_id(), lane = threadIdx.x & 63, q = lane >> 4, j = lane & 15;
-  const int row0 = blockIdx.y * kSmallDnRows + 32 * w;
+  const int lane = threadIdx.x & 63, q = lane >> 4, j = lane & 15;
+  const int row0 = by * kSmallDnRows + 32 * w;
   if (row0 >= H) return;
   const size_t mat = (size_t)H * I;
   const ExpertView dv = ut.shared ? ExpertView{L.sd_nib, L.sd_sc, H, I}
@@ -891,6 +910,16 @@ __global__ __launch_bounds__(kGThreads) __attribute__((amdgpu_waves_per_eu(3))) 
   small_loop<true, false, 2>(dv, dv, row0 / kTileRows, (ut.shared ? g.hsh : g.hrh) + o,
                              (ut.shared ? g.hsl : g.hrl) + o, I / kQuadCols, acc);
   down_epilogue<kSmallTiles, 1>(g, ut, I, row0, q, j, acc);
+}
+
+__global__ __launch_bounds__(kGThreads) __attribute__((amdgpu_waves_per_eu(3))) void k_gu_small(
+    GroupArgs g) {
+  gu_small_part(g, blockIdx.x, blockIdx.y, gwave_id());
+}
+
+__global__ __launch_bounds__(kGThreads) __attribute__((amdgpu_waves_per_eu(3))) void k_down_small(
+    GroupArgs g) {
+  down_small_part(g, blockIdx.x, blockIdx.y, gwave_id());
 }
 
 hipError_t launch_experts_grouped(const LayerDev& L, const uint16_t* xhi, const uint16_t* xlo,
@@ -914,16 +943,20 @@ hipError_t launch_experts_grouped(const LayerDev& L, const uint16_t* xhi, const 
     const hipError_t e = big_attrs();
     if (e != hipSuccess) return e;
   }
-  if (big)
-    hipLaunchKernelGGL(k_big<true>, dim3(big_grid(nbig, (imax + 127) / 128)), dim3(kB2Threads),
-                       kB2Lds, st, g);
-  hipLaunchKernelGGL(k_gu_small, dim3(nsmall, (imax + kSmallGuCols - 1) / kSmallGuCols),
-                     dim3(kGThreads), 0, st, g);
-  if (big)
-    hipLaunchKernelGGL(k_big<false>, dim3(big_grid(nbig, (L.H + 255) / 256)), dim3(kB2Threads),
-                       kB2Lds, st, g);
-  hipLaunchKernelGGL(k_down_small, dim3(nsmall, (L.H + kSmallDnRows - 1) / kSmallDnRows),
-                     dim3(kGThreads), 0, st, g);
+  const int gy = (imax + kSmallGuCols - 1) / kSmallGuCols, dy = (L.H + kSmallDnRows - 1) / kSmallDnRows;
+  if (big) {
+    // the small gate/up units ride in the big gate/up grid, after the big
+    // units, and fill the CUs its last round leaves idle; the down stage's
+    // big units run about five rounds, so its small units keep their own
+    // launch (dispatched after every big one they would add rounds)
+    const int bg = big_grid(nbig, (imax + 127) / 128), bd = big_grid(nbig, (L.H + 255) / 256);
+    hipLaunchKernelGGL(k_big<true>, dim3(bg + (nsmall * gy + 1) / 2), dim3(kB2Threads), kB2Lds,
+                       st, g, bg, nsmall, gy);
+    hipLaunchKernelGGL(k_big<false>, dim3(bd), dim3(kB2Threads), kB2Lds, st, g, bd, 0, 0);
+  } else {
+    hipLaunchKernelGGL(k_gu_small, dim3(nsmall, gy), dim3(kGThreads), 0, st, g);
+  }
+  hipLaunchKernelGGL(k_down_small, dim3(nsmall, dy), dim3(kGThreads), 0, st, g);
   return hipGetLastError();
 }
 
