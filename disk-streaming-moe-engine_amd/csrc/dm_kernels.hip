@@ -456,20 +456,54 @@ __global__ __launch_bounds__(256) void k_router_mfma(LayerDev L, const uint16_t*
   f32x16 acc[4];
 #pragma unroll
   for (int g = 0; g < 4; ++g) acc[g] = f32x16{};
-  for (int c = 0; c < ns / 8; ++c) {
+  // steps 8c .. 8c + 7 of the wave's chains: the router words two rounds
+  // ahead of their products (a ring of two, requests clamped to the last
+  // round), x from LDS one round ahead
+  const int nc = ns / 8;
+  uint4 wr[2][4], xr[2][4];
+  auto load_w = [&](int c, uint4 (&d)[4]) {
+    const int cc = min(c, nc - 1);
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      // chain 4g + b: steps 8c .. 8c + 7
-      const uint4 xv = *reinterpret_cast<const uint4*>(xa + 4 * g * ns + 8 * c);
-      const uint4 wv = *reinterpret_cast<const uint4*>(wb + (size_t)c * 128 + 4 * g * 8);
-      const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w}, ww[4] = {wv.x, wv.y, wv.z, wv.w};
+    for (int g = 0; g < 4; ++g)
+      d[g] = *reinterpret_cast<const uint4*>(wb + (size_t)cc * 128 + 4 * g * 8);
+  };
+  auto load_x = [&](int c, uint4 (&d)[4]) {
+    const int cc = min(c, nc - 1);
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        acc[g] = __builtin_amdgcn_mfma_f32_16x16x1f32(bf16lo(xw[u]), bf16lo(ww[u]), acc[g], 0, 0, 0);
-        acc[g] = __builtin_amdgcn_mfma_f32_16x16x1f32(bf16hi(xw[u]), bf16hi(ww[u]), acc[g], 0, 0, 0);
+    for (int g = 0; g < 4; ++g) d[g] = *reinterpret_cast<const uint4*>(xa + 4 * g * ns + 8 * cc);
+  };
+  // the four accumulators' steps interleaved (each one's steps in order),
+  // so that consecutive matrix instructions are independent
+  auto steps = [&](const uint4 (&xv)[4], const uint4 (&wv)[4]) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const uint32_t xw = u == 0 ? xv[g].x : u == 1 ? xv[g].y : u == 2 ? xv[g].z : xv[g].w;
+        const uint32_t ww = u == 0 ? wv[g].x : u == 1 ? wv[g].y : u == 2 ? wv[g].z : wv[g].w;
+        acc[g] = __builtin_amdgcn_mfma_f32_16x16x1f32(bf16lo(xw), bf16lo(ww), acc[g], 0, 0, 0);
+      }
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const uint32_t xw = u == 0 ? xv[g].x : u == 1 ? xv[g].y : u == 2 ? xv[g].z : xv[g].w;
+        const uint32_t ww = u == 0 ? wv[g].x : u == 1 ? wv[g].y : u == 2 ? wv[g].z : wv[g].w;
+        acc[g] = __builtin_amdgcn_mfma_f32_16x16x1f32(bf16hi(xw), bf16hi(ww), acc[g], 0, 0, 0);
       }
     }
+  };
+  load_w(0, wr[0]);
+  load_w(1, wr[1]);
+  load_x(0, xr[0]);
+  int c = 0;
+  for (; c + 1 < nc; c += 2) {
+    load_x(c + 1, xr[1]);
+    steps(xr[0], wr[0]);
+    load_w(c + 2, wr[0]);
+    load_x(c + 2, xr[0]);
+    steps(xr[1], wr[1]);
+    load_w(c + 3, wr[1]);
   }
+  if (c < nc) steps(xr[0], wr[0]);
   // lane holds tokens t0 + 4 b + r, expert e0 + jj; chain 4g + bb at acc[g][4 bb + r]
   const int e = e0 + jj;
 #pragma unroll
