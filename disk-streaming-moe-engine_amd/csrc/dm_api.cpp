@@ -590,9 +590,9 @@ GgufLayer* get_glayer(dmh_ctx* c, int layer) {
 }
 
 // The MoE section of forward_port_block on a GGUF layer, all on the device:
-// one token in two launches (dm::launch_gguf_one_token) when the layer has
+// one token in one launch (dm::launch_gguf_one_token) when the layer has
 // its sync area, no other context of the library lives on the device (its
-// persistent grids could hold CUs the experts launch waits for) and the
+// persistent grids could hold CUs the launch waits for) and the
 // stream is not being captured (a replay would repeat the launch count);
 // otherwise four launches: router and shared-gate logits (fp32 weights,
 // router_forward's order), selection and gate, gate/up of every slot, down
@@ -1803,11 +1803,11 @@ static int upload_gguf_body(dmh_ctx* c, int layer, const dmh_moe_dims* d,
   for (int i = 0; i < 3 * E && estride > 0; ++i)
     if (off[i] != (int64_t)i * estride) estride = 0;
   G->dev = dm::GgufMoeDev{H, E, K, I, Ish, exp_t, layout, d_raw, d_off, d_router, d_sg, estride};
-  // the single-token form when its experts launch fits the device at once
+  // the single-token form when its launch fits the device at once
   {
     int per_cu = 0;
     G->sync_bytes = dm::gguf_one_token_sync_bytes(G->dev);
-    if (dm::gguf_one_token_supported(G->dev) && c->num_cus > 0 &&
+    if (dm::gguf_one_token_supported(G->dev) && dm::gguf_one_token_grid_ok(G->dev, c->num_cus) &&
         dm::gguf_experts_occupancy(G->dev, &per_cu) == 0 && per_cu >= 1 &&
         hipMalloc(&G->sync, G->sync_bytes) == hipSuccess) {
       if (hipMalloc(&G->rchain, dm::gguf_chain_router_bytes(G->dev)) == hipSuccess &&

@@ -58,15 +58,15 @@ hipError_t launch_gguf_down_combine(const GgufMoeDev& L, const float* h, int ldh
                                     const float* residual, float* y, unsigned long long* status,
                                     hipStream_t st);
 
-// One token in two launches: the router logits (tagged with the launch
-// number n), the shared expert's h, the top-k selection and the softmax
-// terms (front launch: two polling workgroups with the others resident),
-// then the routed experts, the down projections and the combine (experts
-// launch: grid workgroups of 512 threads that must all be resident, one
-// hand-off of the routed h counted per slot).  L.rchain must be set
+// One token in one launch of grid workgroups of 512 threads that must all
+// be resident (gguf_experts_occupancy >= 1 per CU, gguf_one_token_grid_ok):
+// the router logits, the top-k selection, the softmax terms and the shared
+// expert's h as wave tasks handed over in words tagged with the launch
+// number n, then the routed experts (one hand-off of the routed h counted
+// per slot), the down projections and the combine.  L.rchain must be set
 // (launch_chain_router).  sync: gguf_one_token_sync_bytes of device
 // memory, zero before the first launch; launch n of a layer (n = 1, 2, ...)
-// waits for logits tagged n and for n * I / 16 counts per slot (compared
+// waits for words tagged n and for n * I / 16 counts per slot (compared
 // modulo 2^32), so the caller keeps n per layer.
 bool gguf_one_token_supported(const GgufMoeDev& L);
 // rchain for the one-token form: row e's element c + 16 (4q + u) at
@@ -76,6 +76,7 @@ bool gguf_one_token_supported(const GgufMoeDev& L);
 size_t gguf_chain_router_bytes(const GgufMoeDev& L);
 hipError_t launch_chain_router(const GgufMoeDev& L, float* out, hipStream_t st);
 size_t gguf_one_token_sync_bytes(const GgufMoeDev& L);
+bool gguf_one_token_grid_ok(const GgufMoeDev& L, int grid);
 int gguf_experts_occupancy(const GgufMoeDev& L, int* per_cu);
 hipError_t launch_gguf_one_token(const GgufMoeDev& L, const float* x, const float* residual,
                                  float* y, int32_t* ids, float* probs, float* shg, void* sync,

@@ -406,29 +406,19 @@ __global__ __launch_bounds__(256) void k_gguf_down_combine(
   }
 }
 
-// k_gguf_front: workgroup 0 selects, workgroup 1 forms the softmax
-// normaliser, workgroups 2 .. nR + 1 the router logits, the rest the shared
-// expert's h rows (they do not depend on the routing).  A router workgroup
-// (one wave) forms rows 4 (b - 2) .. 4 (b - 2) + 3 (row E: the
-// shared-expert gate) in router_project's order: lane 16 r + c runs chain c
-// of row r (k = c, c + 16, ..., separate multiply and add), then the
-// halving tree of the router kernels.  The chain's weights come four steps
-// per float4 from the chain-ordered copy of the router (k_chain_router,
-// rows of kFrontMaxH floats, zero past H), x from LDS in chain order (zero
-// past H: the extra steps add +0.0 to a sum that is never -0.0, which leaves
-// it unchanged).  Each logit is published as a tagged word (launch << 32 |
-// bits) at the device-coherent level.  Workgroup 0 polls them (bounded),
-// selects the top K on the logits (topk_on_logits; the exact probabilities
-// on a near tie at the boundary) and writes the K experts, ordered by logit
-// (then id), to sel[].  Workgroup 1 polls them too and writes, for the
-// experts launch, max z, 1/S (S the sum of exp(z - max) in expert order)
-// and the shared gate to soft[] with router_softmax's and the gate's checks
-// (src/layers/router.mojo:140-183, src/layers/moe.mojo:70-100).
+// ---- one token in one launch ------------------------------------------------
+// k_gguf_one: one workgroup of 8 waves per CU, all resident together.  The
+// routing runs as one task per wave (the tasks below): router groups on
+// wave 0 of workgroups 0 .. nR - 1, the selection on wave 1 of workgroup 0,
+// the softmax terms on wave 1 of workgroup 1, the shared expert's h rows on
+// waves 2 .. 7 (row r on wave 2 + r % 6 of workgroup r / 6); each result is
+// handed over as tagged words (launch << 32 | bits) at the device-coherent
+// level, and every wait on them is a bounded poll.
 constexpr int kFrontMaxH = 2048;
-// sync area head: slot s's h count at 128 + 64 s, the selected experts at
-// kSelOff, the exact path's probabilities at kSelOff + 64, the softmax
-// terms at kSelOff + 128; then the tagged logits, the shared expert's h and
-// the routed slots' h
+// sync area head: slot s's h count at 128 + 64 s, the selected experts as
+// tagged words at kSelOff, the softmax terms (max, 1/S, shared gate) as
+// tagged words at kSelOff + 64; then the tagged logits, the shared
+// expert's h as tagged words and the routed slots' h
 constexpr size_t kSyncHead = 1024;
 constexpr size_t kSelOff = 768;
 constexpr int kFrontRows = 4;
@@ -442,123 +432,61 @@ __device__ __forceinline__ bool nonfinite4(const f32x4& q) {
   return n != 0;
 }
 
-template <int T, int W, int R>
-__global__ __launch_bounds__(64) void k_gguf_front(GgufMoeDev L, const float* __restrict__ x,
-                                                   int nR, uint64_t* zt, float* __restrict__ hsh,
-                                                   int32_t* sel, float* selp, float* soft,
-                                                   unsigned launch,
-                                                   unsigned long long* status) {
-  __shared__ __attribute__((aligned(16))) float xt[16 * kChainS];
-  const int lane = threadIdx.x, H = L.H, E = L.E, K = L.K;
-  const int b = (int)blockIdx.x;
-  if (b > nR + 1) {
-    // the shared expert's gate / up row r (as k_gguf_gateup's slot K)
-    const int r = b - 2 - nR;
-    const uint8_t* wg = L.raw + L.off[(size_t)E * 3 + 0];
-    const uint8_t* wu = L.raw + L.off[(size_t)E * 3 + 1];
-    const int64_t base = (int64_t)r * H;
-    float ag = 0.0f, au = 0.0f;
-    for (int c = lane * 16; c < H; c += 64 * 16) {
-      f32x4 xv[4];
+__device__ __forceinline__ void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+}
+
+__device__ __forceinline__ uint64_t tagged(unsigned launch, float v) {
+  return ((uint64_t)launch << 32) | f2u(v);
+}
+
+// The shared expert's gate / up row r (as k_gguf_gateup's slot K) on one
+// wave, h published as a tagged word.
+template <int T>
+__device__ __forceinline__ void shared_row_task(const GgufMoeDev& L, const float* __restrict__ x,
+                                                int r, uint64_t* hsh, unsigned launch,
+                                                unsigned long long* status) {
+  const int lane = threadIdx.x & 63, H = L.H, E = L.E;
+  const uint8_t* wg = L.raw + L.off[(size_t)E * 3 + 0];
+  const uint8_t* wu = L.raw + L.off[(size_t)E * 3 + 1];
+  const int64_t base = (int64_t)r * H;
+  float ag = 0.0f, au = 0.0f;
+  for (int c = lane * 16; c < H; c += 64 * 16) {
+    f32x4 xv[4];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) xv[j] = *reinterpret_cast<const f32x4*>(x + c + 4 * j);
-      gu_dot16<T>(wg, wu, base + c, L.layout, xv, ag, au);
-    }
-    ag = wave_sum_dpp(ag);
-    au = wave_sum_dpp(au);
-    if (lane == 0) {
-      const float hv = dm_silu(ag) * au;
-      if (!finite_f(ag)) record_err(status, err_key(kPhShared, 0, 0, r, kEkGate));
-      if (!finite_f(au)) record_err(status, err_key(kPhShared, 0, 0, r, kEkUp));
-      if (!finite_f(hv)) record_err(status, err_key(kPhShared, 0, 0, r, kEkH));
-      hsh[r] = hv;
-    }
-    return;
+    for (int j = 0; j < 4; ++j) xv[j] = *reinterpret_cast<const f32x4*>(x + c + 4 * j);
+    gu_dot16<T>(wg, wu, base + c, L.layout, xv, ag, au);
   }
-  auto wave_sync = [] {
-    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-  };
-  if (b == 0) {
-    float z[4 * R];
-    if (!poll_logits<R>(zt, launch, E, z, nullptr) && lane == 0)
-      record_err(status, err_key(kPhSync, 0, 0, 0, 0));
-    uint32_t fk[4 * R];
-    int myid = 0;
-    if (!topk_on_logits<R>(z, E, K, lane, fk, myid)) {
-      // lane k < K: the k-th by key; ordered by (logit, then lower id), the
-      // order the softmax's probabilities keep unless two of them round to
-      // the same value (the experts launch orders by probability)
-      myid = min(max(myid, 0), E - 1);
-      // the logit of expert e sits in lane e & 63, entry e >> 6
-      float zk = 0.0f;
-#pragma unroll
-      for (int i = 0; i < 4 * R; ++i) {
-        const float zo = u2f((uint32_t)__builtin_amdgcn_ds_bpermute(4 * (myid & 63), (int)f2u(z[i])));
-        zk = (myid >> 6) == i ? zo : zk;
-      }
-      const uint32_t kk = f2key(zk);
-      int rank = 0;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const uint32_t kj = (uint32_t)__builtin_amdgcn_readlane((int)kk, j);
-        const int ij = __builtin_amdgcn_readlane(myid, j);
-        if (j < K && lane < K)
-          rank += (kj > kk || (kj == kk && (ij < myid || (ij == myid && j < lane)))) ? 1 : 0;
-      }
-      if (lane < K) sel[rank] = myid;
-    } else {
-      // a near tie at the top-k boundary: the exact probabilities decide
-      float* sz = xt;
-      float* sm = xt + 512;
-#pragma unroll
-      for (int i = 0; i < 4 * R; ++i)
-        if (lane + 64 * i < E) sz[lane + 64 * i] = z[i];
-      wave_sync();
-      route_select_token<4 * R, false>(sz, 0, E, K, 0, 0, lane, sm, sel, selp, nullptr, status,
-                                       wave_sync);
-    }
-    return;
+  ag = wave_sum_dpp(ag);
+  au = wave_sum_dpp(au);
+  if (lane == 0) {
+    const float hv = dm_silu(ag) * au;
+    if (!finite_f(ag)) record_err(status, err_key(kPhShared, 0, 0, r, kEkGate));
+    if (!finite_f(au)) record_err(status, err_key(kPhShared, 0, 0, r, kEkUp));
+    if (!finite_f(hv)) record_err(status, err_key(kPhShared, 0, 0, r, kEkH));
+    st_coh_u64(hsh + r, tagged(launch, hv));
   }
-  if (b == 1) {
-    float z[4 * R], gl = 0.0f;
-    if (!poll_logits<R>(zt, launch, E, z, &gl) && lane == 0)
-      record_err(status, err_key(kPhSync, 0, 0, 0, 0));
-    float m = -__builtin_inff();
-#pragma unroll
-    for (int i = 0; i < 4 * R; ++i)
-      if (lane + 64 * i < E) m = z[i] > m ? z[i] : m;
-    m = __ockl_wfred_max_f32(m);
-    if (lane == 0 && !finite_f(m)) record_err(status, err_key(kPhSoftmax, 0, 0, 0, 0));
-#pragma unroll
-    for (int i = 0; i < 4 * R; ++i) {
-      const int e = lane + 64 * i;
-      if (e < E) {
-        const float ev = dm_expf(z[i] - m);
-        if (!finite_f(ev)) record_err(status, err_key(kPhSoftmax, 0, 0, 1 + e, 0));
-        xt[e] = ev;
-      }
-    }
-    wave_sync();
-    if (lane == 0) {
-      const float s = seq_sum(xt, E);
-      if (!(s > 0.0f) || !finite_f(s)) record_err(status, err_key(kPhSoftmax, 0, 0, 1 + E, 0));
-      if (!finite_f(gl)) record_err(status, err_key(kPhGate, 0, 0, 0, kGkLogit));
-      const float g = dm_sigmoid(gl);
-      if (!finite_f(g) || g < 0.0f || g > 1.0f)
-        record_err(status, err_key(kPhGate, 0, 0, 0, kGkRange));
-      soft[0] = m;
-      soft[1] = 1.0f / s;
-      soft[2] = g;
-    }
-    return;
-  }
-  // ---- router rows: every load (clamped to the data) before the first LDS store
+}
+
+// Router rows 4 grp .. 4 grp + 3 (row E: the shared-expert gate) on one
+// wave: lane 16 r + c runs chain c of row r (k = c, c + 16, ..., separate
+// multiply and add), then the halving tree of the router kernels.  The
+// chain's weights come four steps per float4 from the chain-ordered copy of
+// the router (k_chain_router, rows of kFrontMaxH floats, zero past H), x
+// from xt (LDS, this wave's) in chain order (zero past H: the extra steps
+// add +0.0 to a sum that is never -0.0, which leaves it unchanged).  Each
+// logit is published as a tagged word.
+__device__ __forceinline__ void router_task(const GgufMoeDev& L, const float* __restrict__ x,
+                                            int grp, uint64_t* zt, unsigned launch, float* xt,
+                                            unsigned long long* status) {
+  const int lane = threadIdx.x & 63, H = L.H, E = L.E;
   const int r = lane >> 4, c = lane & 15;
-  const int e = (b - 2) * kFrontRows + r;
+  const int e = grp * kFrontRows + r;
   const bool row = e <= E, chk = row && e != E;
   constexpr int kJ = kFrontMaxH / 256;  // float4 of x per lane
   constexpr int kQ = kFrontMaxH / 64;   // float4 of a chain
+  // every load (clamped to the data) before the first LDS store
   f32x4 xv[kJ], wv[kQ];
 #pragma unroll
   for (int j = 0; j < kJ; ++j)
@@ -585,12 +513,11 @@ __global__ __launch_bounds__(64) void k_gguf_front(GgufMoeDev L, const float* __
     }
   }
 #pragma unroll
-  for (int q = 0; q < kQ; ++q)
-    bad_w |= nonfinite4(wv[q]);
+  for (int q = 0; q < kQ; ++q) bad_w |= nonfinite4(wv[q]);
   bad_w = bad_w && chk;
   if (bad_x) record_err(status, err_key(kPhX, 0, 0, 0, 0));
   if (bad_w) record_err(status, err_key(kPhRouterW, 0, 0, 0, 0));
-  __syncthreads();
+  wave_sync();
   float acc = 0.0f;
   const float* xc = xt + c * kChainS;
 #pragma unroll
@@ -608,11 +535,121 @@ __global__ __launch_bounds__(64) void k_gguf_front(GgufMoeDev L, const float* __
   }
   if (row && c == 0) {
     if (e != E && !finite_f(acc)) record_err(status, err_key(kPhLogit, 0, 0, e, 0));
-    st_coh_u64(zt + e, ((uint64_t)launch << 32) | f2u(acc));
+    st_coh_u64(zt + e, tagged(launch, acc));
   }
 }
 
-// The chain-ordered copy of the router and the shared gate for k_gguf_front:
+// The top K on one wave: poll the tagged logits (bounded), topk_on_logits
+// (on a near tie at the boundary the exact-probability rounds of
+// route_select_token, on scratch in LDS), and the K experts, ordered by
+// logit (then id), published as tagged words sel[k] (launch << 32 | id).
+template <int R>
+__device__ __forceinline__ void select_task(const GgufMoeDev& L, const uint64_t* zt,
+                                            unsigned launch, uint64_t* sel, float* scr,
+                                            unsigned long long* status) {
+  const int lane = threadIdx.x & 63, E = L.E, K = L.K;
+  float z[4 * R];
+  if (!poll_logits<R>(zt, launch, E, z, nullptr) && lane == 0)
+    record_err(status, err_key(kPhSync, 0, 0, 0, 0));
+  uint32_t fk[4 * R];
+  int myid = 0;
+  if (!topk_on_logits<R>(z, E, K, lane, fk, myid)) {
+    // lane k < K: the k-th by key; ordered by (logit, then lower id), the
+    // order the softmax's probabilities keep unless two of them round to
+    // the same value (the probabilities' own order is formed later)
+    myid = min(max(myid, 0), E - 1);
+    // the logit of expert e sits in lane e & 63, entry e >> 6
+    float zk = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4 * R; ++i) {
+      const float zo = u2f((uint32_t)__builtin_amdgcn_ds_bpermute(4 * (myid & 63), (int)f2u(z[i])));
+      zk = (myid >> 6) == i ? zo : zk;
+    }
+    const uint32_t kk = f2key(zk);
+    int rank = 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const uint32_t kj = (uint32_t)__builtin_amdgcn_readlane((int)kk, j);
+      const int ij = __builtin_amdgcn_readlane(myid, j);
+      if (j < K && lane < K)
+        rank += (kj > kk || (kj == kk && (ij < myid || (ij == myid && j < lane)))) ? 1 : 0;
+    }
+    if (lane < K) st_coh_u64(sel + rank, ((uint64_t)launch << 32) | (uint32_t)myid);
+  } else {
+    // a near tie at the top-k boundary: the exact probabilities decide
+    float* sz = scr;
+    float* sm = scr + 512;
+    int32_t* ids = reinterpret_cast<int32_t*>(scr + 1040);
+    float* pr = scr + 1048;
+#pragma unroll
+    for (int i = 0; i < 4 * R; ++i)
+      if (lane + 64 * i < E) sz[lane + 64 * i] = z[i];
+    wave_sync();
+    route_select_token<4 * R, false>(sz, 0, E, K, 0, 0, lane, sm, ids, pr, nullptr, status,
+                                     [] { wave_sync(); });
+    wave_sync();
+    if (lane < K)
+      st_coh_u64(sel + lane, ((uint64_t)launch << 32) | (uint32_t)min(max(ids[lane], 0), E - 1));
+  }
+}
+
+// The softmax terms on one wave: poll the tagged logits and the
+// shared-gate logit (bounded), then max z, 1/S (S the sum of
+// exp(z - max) in expert order) and the shared gate with router_softmax's
+// and the gate's checks (src/layers/router.mojo:140-183,
+// src/layers/moe.mojo:70-100), published as tagged words soft[0..2].
+template <int R>
+__device__ __forceinline__ void softmax_task(const GgufMoeDev& L, const uint64_t* zt,
+                                             unsigned launch, uint64_t* soft, float* scr,
+                                             unsigned long long* status) {
+  const int lane = threadIdx.x & 63, E = L.E;
+  float z[4 * R], gl = 0.0f;
+  if (!poll_logits<R>(zt, launch, E, z, &gl) && lane == 0)
+    record_err(status, err_key(kPhSync, 0, 0, 0, 0));
+  float m = -__builtin_inff();
+#pragma unroll
+  for (int i = 0; i < 4 * R; ++i)
+    if (lane + 64 * i < E) m = z[i] > m ? z[i] : m;
+  m = __ockl_wfred_max_f32(m);
+  if (lane == 0 && !finite_f(m)) record_err(status, err_key(kPhSoftmax, 0, 0, 0, 0));
+#pragma unroll
+  for (int i = 0; i < 4 * R; ++i) {
+    const int e = lane + 64 * i;
+    if (e < E) {
+      const float ev = dm_expf(z[i] - m);
+      if (!finite_f(ev)) record_err(status, err_key(kPhSoftmax, 0, 0, 1 + e, 0));
+      scr[e] = ev;
+    }
+  }
+  wave_sync();
+  if (lane == 0) {
+    const float s = seq_sum(scr, E);
+    if (!(s > 0.0f) || !finite_f(s)) record_err(status, err_key(kPhSoftmax, 0, 0, 1 + E, 0));
+    if (!finite_f(gl)) record_err(status, err_key(kPhGate, 0, 0, 0, kGkLogit));
+    const float g = dm_sigmoid(gl);
+    if (!finite_f(g) || g < 0.0f || g > 1.0f)
+      record_err(status, err_key(kPhGate, 0, 0, 0, kGkRange));
+    st_coh_u64(soft + 0, tagged(launch, m));
+    st_coh_u64(soft + 1, tagged(launch, 1.0f / s));
+    st_coh_u64(soft + 2, tagged(launch, g));
+  }
+}
+
+// Bounded poll of n (<= 64) tagged words, word l on lane l; their values
+// (as bits) to v.  False on reaching the limit.
+__device__ __forceinline__ bool poll_words(const uint64_t* p, int n, unsigned tag, long limit,
+                                           uint32_t& v) {
+  const int lane = threadIdx.x & 63;
+  for (long spin = 0; spin < limit; ++spin) {
+    const uint64_t wd = lane < n ? ld_coh_u64(p + lane) : 0;
+    v = (uint32_t)wd;
+    if (__builtin_amdgcn_ballot_w64(lane < n && (uint32_t)(wd >> 32) != tag) == 0) return true;
+    __builtin_amdgcn_s_sleep(1);
+  }
+  return false;
+}
+
+// The chain-ordered copy of the router and the shared gate for router_task:
 // rows of kFrontMaxH floats (row E: the shared gate) as float4 groups
 // g = 16 q + c holding the elements c + 16 (4q + u), u = 0..3 (chain c's
 // steps 4q .. 4q + 3; zero past H), so that group q of the 16 chains is one
@@ -628,20 +665,20 @@ __global__ void k_chain_router(const float* __restrict__ router, const float* __
   out[i] = k < H ? src[k] : 0.0f;
 }
 
-// k_gguf_experts: one workgroup of 8 waves per CU, all resident together.
-// Phase 1: the K x I routed (gate, up) row pairs in blocks of 16 per
-// workgroup, every weight chunk requested before the first is decoded; a
-// block's h goes to the device-coherent level as one write and the block is
-// counted in its slot's counter (hcnt[16 s]).  Phase 2: workgroup b owns
-// output rows 8b .. 8b + 7 (and 8b + 8G ..): wave w requests the chunks of
-// row 8b + w of the shared expert (whose h the front launch wrote) and of
-// the 8 rows of routed slot w, waits for slot w's count, and forms the dot
-// products; eight lanes
-// then combine each row in moe_aggregate_forward's order
-// (y = sum_k p_k r_k + g r_sh (+ residual), k in probability order).
-// Wave kSoftWave forms the K probabilities and their order before phase 2
-// (gguf_slot_probs); workgroup 0 writes ids, probs and the shared gate.  Q3_K experts take the
-// separate-load path (q3_load / q3_decode); other types decode as they load.
+// After the routing tasks every wave polls the selected experts.  Phase 1:
+// the K x I routed (gate, up) row pairs in blocks of 16 per workgroup, every
+// weight chunk requested before the first is used; a block's h goes to the
+// device-coherent level as one write and the block is counted in its slot's
+// counter (hcnt[16 s]).  Phase 2: workgroup b owns output rows 8b .. 8b + 7
+// (and 8b + 8G ..): wave w requests the chunks of row 8b + w of the shared
+// expert and of the 8 rows of routed slot w, polls the shared h, waits for
+// slot w's count, and forms the dot products; eight lanes then combine each
+// row in moe_aggregate_forward's order (y = sum_k p_k r_k + g r_sh
+// (+ residual), k in probability order).  Wave kSoftWave forms the K
+// probabilities and their order before phase 2 (gguf_slot_probs);
+// workgroup 0 writes ids, probs and the shared gate.  Q3_K experts take
+// the separate-load path (q3_load / q3_dot16); other types decode as they
+// load.
 // Bounded poll until *c reaches target (wrap-safe); on reaching the limit
 // records a sync error and returns false, so that the caller skips later
 // waits and the grid drains.
@@ -664,7 +701,7 @@ __device__ __forceinline__ int64_t lane64(int64_t v, int l) {
 }
 
 // p_k = exp(z_k - max) * (1/S) for the K experts of the token (lane k < K:
-// slot k's expert idk and its logit zk; max and 1/S from the front launch,
+// slot k's expert idk and its logit zk; max and 1/S from softmax_task,
 // router_softmax's terms, src/layers/router.mojo:140-183), their
 // (p desc, id asc) order and select_topk's checks (src/layers/topk.mojo:
 // 109-128) on one wave.  To LDS: sp[r], sslot[r], sid[r] (probability, slot
@@ -710,7 +747,7 @@ __device__ __forceinline__ void gguf_slot_probs(float zk, int idk, float m, floa
 #pragma unroll
     for (int i = 0; i < 4 * R; ++i) {
       const int e = lane + 64 * i;
-      if (e < E) sev[e] = dm_expf(u2f((uint32_t)zt[e]) - m) * inv;
+      if (e < E) sev[e] = dm_expf(u2f((uint32_t)ld_coh_u64(zt + e)) - m) * inv;
     }
     wave_sync();
     const float sum_all = seq_sum(sev, E);
@@ -719,24 +756,64 @@ __device__ __forceinline__ void gguf_slot_probs(float zk, int idk, float m, floa
   }
 }
 
+// Bounded poll of a lane's eight tagged words (launch << 32 | bits) until
+// every lane's words carry this launch's tag; false on reaching the limit.
+__device__ __forceinline__ bool poll8(const uint64_t* p, unsigned tag, long limit,
+                                      f32x4 (&v)[2]) {
+  for (long spin = 0; spin < limit; ++spin) {
+    uint64_t wd[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) wd[q] = ld_coh_u64(p + q);
+    bool ok = true;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      ok &= (uint32_t)(wd[q] >> 32) == tag;
+      v[q >> 2][q & 3] = u2f((uint32_t)wd[q]);
+    }
+    if (__builtin_amdgcn_ballot_w64(!ok) == 0) return true;
+    __builtin_amdgcn_s_sleep(1);
+  }
+  return false;
+}
+
 template <int T, int R>
-__global__ __launch_bounds__(512) void k_gguf_experts(
-    GgufMoeDev L, const float* __restrict__ x, const int32_t* __restrict__ sel,
-    const uint64_t* __restrict__ zt, const float* __restrict__ soft,
-    const float* __restrict__ residual, float* __restrict__ y,
+__global__ __launch_bounds__(512) void k_gguf_one(
+    GgufMoeDev L, const float* __restrict__ x, int nR, uint64_t* zt, uint64_t* sel,
+    uint64_t* soft, uint64_t* hsh, const float* __restrict__ residual, float* __restrict__ y,
     int32_t* __restrict__ ids, float* __restrict__ probs, float* __restrict__ shg,
-    const float* __restrict__ hsh, float* __restrict__ h, int ldh, unsigned* hcnt,
-    unsigned target, unsigned long long* status) {
+    float* __restrict__ h, int ldh, unsigned* hcnt, unsigned target, unsigned launch,
+    unsigned long long* status) {
+  __shared__ __attribute__((aligned(16))) float xt[16 * kChainS];
+  __shared__ __attribute__((aligned(16))) float scr[1056];
   __shared__ float part[8][33];
   __shared__ float sev[256 * R];
   __shared__ float sp[8];
   __shared__ int sslot[8], sid[8];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int wid = __builtin_amdgcn_readfirstlane(w);  // w as a uniform value
-  const int G = (int)gridDim.x;
+  const int G = (int)gridDim.x, b = (int)blockIdx.x;
   const int H = L.H, E = L.E, K = L.K, I = L.I, Ish = L.Ish;
+  // ---- the routing and the shared expert's h, one task per wave
+  if (wid == 0) {
+    if (b < nR) router_task(L, x, b, zt, launch, xt, status);
+  } else if (wid == 1) {
+    if (b == 0) select_task<R>(L, zt, launch, sel, scr, status);
+    if (b == 1) softmax_task<R>(L, zt, launch, soft, scr, status);
+  } else if (6 * b + wid - 2 < Ish) {
+    shared_row_task<T>(L, x, 6 * b + wid - 2, hsh, launch, status);
+  }
+  // the selected experts: one wave per workgroup polls them (a poll by
+  // every wave would crowd the memory the routing tasks are using)
+  __shared__ int sel_ids[8];
+  if (wid == 1) {
+    uint32_t sv = 0;
+    if (!poll_words(sel, K, launch, kSpinLimit, sv) && lane == 0)
+      record_err(status, err_key(kPhSync, 0, 0, 0, 0));
+    if (lane < K) sel_ids[lane] = min(max((int)sv, 0), E - 1);
+  }
+  __syncthreads();
   // lane s < K: the expert and payload offsets of routed slot s
-  const int es = min(max((int)sel[min(lane, K - 1)], 0), E - 1);
+  const int es = sel_ids[min(lane, K - 1)];
   int64_t og, ou, od;
   if (L.estride > 0) {
     og = (int64_t)(3 * es) * L.estride;
@@ -747,11 +824,9 @@ __global__ __launch_bounds__(512) void k_gguf_experts(
     ou = L.off[(size_t)es * 3 + 1];
     od = L.off[(size_t)es * 3 + 2];
   }
-  // for the combine: the slot's logit and the front launch's softmax terms
-  // (requested after the offsets, so that waiting for those does not wait
-  // for these)
-  const float zk = reinterpret_cast<const float*>(zt)[2 * es];  // the word's low half
-  const float sm_max = soft[0], sm_inv = soft[1], sg = soft[2];
+  // for the combine: the slot's logit (requested after the offsets, so
+  // that waiting for those does not wait for it)
+  const float zk = u2f((uint32_t)ld_coh_u64(zt + es));
   const uint8_t* wsh = L.raw + L.off[(size_t)E * 3 + 2];
   const int cs = min(lane * 8, Ish - 8), cr = min(lane * 8, I - 8);
   const int dfirst = (int)blockIdx.x * 8;
@@ -846,9 +921,28 @@ __global__ __launch_bounds__(512) void k_gguf_experts(
     for (int i = 0; i < 8; ++i)
       pre_r[i] = q3_load<8>(wrd, (int64_t)min(dfirst + i, H - 1) * I + cr);
   }
-  if (wid == kSoftWave)
-    gguf_slot_probs<R>(zk, es, sm_max, sm_inv, zt, E, K, sev, sp, sslot, sid, blockIdx.x == 0,
-                       status);
+  __shared__ float sg;  // the shared gate
+  // the shared expert's h, read once per workgroup into LDS (wave 0)
+  __shared__ __attribute__((aligned(16))) float hshl[512];
+  if (wid == 0) {
+    f32x4 hv[2];
+    if (!poll8(hsh + cs, launch, kSpinLimit, hv) && lane == 0)
+      record_err(status, err_key(kPhSync, 0, 0, 0, 0));
+    if (lane * 8 < Ish) {
+      *reinterpret_cast<f32x4*>(hshl + lane * 8) = hv[0];
+      *reinterpret_cast<f32x4*>(hshl + lane * 8 + 4) = hv[1];
+    }
+  }
+  if (wid == kSoftWave) {
+    uint32_t tv = 0;
+    if (!poll_words(soft, 3, launch, kSpinLimit, tv) && lane == 0)
+      record_err(status, err_key(kPhSync, 0, 0, 0, 0));
+    const float sm_max = u2f((uint32_t)__builtin_amdgcn_readlane((int)tv, 0));
+    const float sm_inv = u2f((uint32_t)__builtin_amdgcn_readlane((int)tv, 1));
+    if (lane == 2) sg = u2f(tv);
+    gguf_slot_probs<R>(zk, es, sm_max, sm_inv, zt, E, K, sev, sp, sslot, sid, b == 0, status);
+  }
+  __syncthreads();  // hshl
   // ---- phase 2: down projections and the combine
   bool ready = false;
   const bool ls = lane * 8 < Ish, lr = lane * 8 < I;
@@ -871,9 +965,9 @@ __global__ __launch_bounds__(512) void k_gguf_experts(
       for (int i = 0; i < 8; ++i)
         valuesW<T, 8>(wrd, (int64_t)min(d0 + i, H - 1) * I + cr, L.layout, wr[i]);
     }
-    // the shared expert's row d0 + w (h written by the front launch)
+    // the shared expert's row d0 + w
     {
-      const float* hp = hsh + cs;
+      const float* hp = hshl + cs;
       float a = dot4(ws[0], *reinterpret_cast<const f32x4*>(hp), 0.0f);
       a = dot4(ws[1], *reinterpret_cast<const f32x4*>(hp + 4), a);
       a = wave_sum_dpp(ls ? a : 0.0f);
@@ -1016,7 +1110,7 @@ bool gguf_one_token_supported(const GgufMoeDev& L) {
 
 static size_t zt_bytes(const GgufMoeDev& L) { return ((size_t)(L.E + 1) * 8 + 255) & ~(size_t)255; }
 
-static size_t hsh_bytes(const GgufMoeDev& L) { return ((size_t)L.Ish * 4 + 255) & ~(size_t)255; }
+static size_t hsh_bytes(const GgufMoeDev& L) { return ((size_t)L.Ish * 8 + 255) & ~(size_t)255; }
 
 size_t gguf_one_token_sync_bytes(const GgufMoeDev& L) {
   return kSyncHead + zt_bytes(L) + hsh_bytes(L) + (size_t)L.K * L.I * 4;
@@ -1033,12 +1127,17 @@ hipError_t launch_chain_router(const GgufMoeDev& L, float* out, hipStream_t st) 
   return hipGetLastError();
 }
 
+bool gguf_one_token_grid_ok(const GgufMoeDev& L, int grid) {
+  const int nR = (L.E + 1 + kFrontRows - 1) / kFrontRows;
+  return grid >= 2 && grid >= nR && 6 * grid >= L.Ish;
+}
+
 int gguf_experts_occupancy(const GgufMoeDev& L, int* per_cu) {
   hipError_t e = hipErrorInvalidValue;
   const bool r1 = L.E <= 256;
 #define DM_OCC(TY)                                                                                \
-  e = r1 ? hipOccupancyMaxActiveBlocksPerMultiprocessor(per_cu, k_gguf_experts<TY, 1>, 512, 0)   \
-         : hipOccupancyMaxActiveBlocksPerMultiprocessor(per_cu, k_gguf_experts<TY, 2>, 512, 0)
+  e = r1 ? hipOccupancyMaxActiveBlocksPerMultiprocessor(per_cu, k_gguf_one<TY, 1>, 512, 0)   \
+         : hipOccupancyMaxActiveBlocksPerMultiprocessor(per_cu, k_gguf_one<TY, 2>, 512, 0)
   switch (L.type) {
     case kGgmlQ8_0: DM_OCC(kGgmlQ8_0); break;
     case kGgmlQ4_K: DM_OCC(kGgmlQ4_K); break;
@@ -1053,23 +1152,21 @@ hipError_t launch_gguf_one_token(const GgufMoeDev& L, const float* x, const floa
                                  float* y, int32_t* ids, float* probs, float* shg, void* sync,
                                  unsigned launch, int grid, unsigned long long* status,
                                  hipStream_t st) {
-  if (!gguf_one_token_supported(L) || !L.rchain || grid <= 0 || launch == 0)
+  const int nR = (L.E + 1 + kFrontRows - 1) / kFrontRows;
+  if (!gguf_one_token_supported(L) || !L.rchain || !gguf_one_token_grid_ok(L, grid) ||
+      launch == 0)
     return hipErrorInvalidValue;
   uint8_t* sb = static_cast<uint8_t*>(sync);
   unsigned* hcnt = reinterpret_cast<unsigned*>(sb + 128);  // slot s at 64 s bytes
-  int32_t* sel = reinterpret_cast<int32_t*>(sb + kSelOff);
-  float* selp = reinterpret_cast<float*>(sb + kSelOff + 64);
-  float* soft = reinterpret_cast<float*>(sb + kSelOff + 128);
+  uint64_t* sel = reinterpret_cast<uint64_t*>(sb + kSelOff);
+  uint64_t* soft = reinterpret_cast<uint64_t*>(sb + kSelOff + 64);
   uint64_t* zt = reinterpret_cast<uint64_t*>(sb + kSyncHead);
-  float* hsh = reinterpret_cast<float*>(sb + kSyncHead + zt_bytes(L));
+  uint64_t* hsh = reinterpret_cast<uint64_t*>(sb + kSyncHead + zt_bytes(L));
   float* h = reinterpret_cast<float*>(sb + kSyncHead + zt_bytes(L) + hsh_bytes(L));
-  const int nR = (L.E + 1 + kFrontRows - 1) / kFrontRows;
-  const dim3 g1((unsigned)(2 + nR + L.Ish)), g2((unsigned)grid);
   const unsigned target = launch * (unsigned)(L.I / 16);  // blocks per slot
-#define DM_ONE(TY, R)                                                                       \
-  k_gguf_front<TY, 16, R><<<g1, 64, 0, st>>>(L, x, nR, zt, hsh, sel, selp, soft, launch, status); \
-  k_gguf_experts<TY, R><<<g2, 512, 0, st>>>(L, x, sel, zt, soft, residual, y, ids, probs, shg,   \
-                                            hsh, h, L.I, hcnt, target, status)
+#define DM_ONE(TY, R)                                                                          \
+  k_gguf_one<TY, R><<<grid, 512, 0, st>>>(L, x, nR, zt, sel, soft, hsh, residual, y, ids, probs, \
+                                          shg, h, L.I, hcnt, target, launch, status)
 #define DM_ONE_R(TY)    \
   if (L.E <= 256) {     \
     DM_ONE(TY, 1);      \
