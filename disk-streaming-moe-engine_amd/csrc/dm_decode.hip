@@ -1340,10 +1340,12 @@ __global__ __launch_bounds__(kThreads) void k_moe_decode_xs(
     if (tid < nxa * rpf && tid % rpf < nfr) {
       const int xx = tid / rpf, rr = tid % rpf;
       const uint64_t* src = S.pt + (size_t)xx * H + r0 + rr;
-      uint64_t v = ld_coh_u64(src);
+      // two polls in flight: while the older one is checked the newer one
+      // travels, so a partial is seen about half a round trip sooner
+      uint64_t v = ld_coh_u64(src), nv = ld_coh_u64(src);
       for (long spin = 0; spin < kSpinLimit && ok && (uint32_t)(v >> 32) != n; ++spin) {
-        __builtin_amdgcn_s_sleep(1);
-        v = ld_coh_u64(src);
+        v = nv;
+        nv = ld_coh_u64(src);
       }
       fok = (uint32_t)(v >> 32) == n;
       fin[xx * rpf + rr] = u2f((uint32_t)v);
