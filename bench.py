@@ -361,7 +361,7 @@ def gguf_moe(a, blk, stream, dev):
                                           "256 q3_k experts + q3_k shared), batch-1 decode",
                               "hidden": H, "experts": E, "top_k": K, "inter": I,
                               "inter_sh": Ish, "tokens": a.steps},
-                   "roofline": {"bound": "hbm", "kernel": "gguf moe block (front + experts launches)",
+                   "roofline": {"bound": "hbm", "kernel": "k_gguf_one (one launch per token)",
                                 "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS,
                                 "unit": "GB/s", "frac": round(gbps / HBM_PEAK_GBPS, 4),
                                 "traffic": profiled_traffic(GGUF_MOE_PROFILE,
