@@ -803,9 +803,11 @@ __global__ __launch_bounds__(512) void k_gguf_one(
     shared_row_task<T>(L, x, 6 * b + wid - 2, hsh, launch, status);
   }
   // the selected experts: one wave per workgroup polls them (a poll by
-  // every wave would crowd the memory the routing tasks are using)
+  // every wave would crowd the memory the routing tasks are using); wave 0,
+  // whose router task ends before the selection does (wave 1 of workgroup
+  // 1 forms the softmax terms until after the ids are out)
   __shared__ int sel_ids[8];
-  if (wid == 1) {
+  if (wid == 0) {
     uint32_t sv = 0;
     if (!poll_words(sel, K, launch, kSpinLimit, sv) && lane == 0)
       record_err(status, err_key(kPhSync, 0, 0, 0, 0));
@@ -830,6 +832,33 @@ __global__ __launch_bounds__(512) void k_gguf_one(
   const uint8_t* wsh = L.raw + L.off[(size_t)E * 3 + 2];
   const int cs = min(lane * 8, Ish - 8), cr = min(lane * 8, I - 8);
   const int dfirst = (int)blockIdx.x * 8;
+  // Done once, in the shadow of the first gate / up requests (or after phase
+  // 1 when the workgroup has no block): wave 0 reads the shared expert's h
+  // into LDS, wave kSoftWave forms the K probabilities and their order.
+  __shared__ float sg;  // the shared gate
+  __shared__ __attribute__((aligned(16))) float hshl[512];
+  bool side_done = false;
+  auto side_work = [&]() {
+    side_done = true;
+    if (wid == 0) {
+      f32x4 hv[2];
+      if (!poll8(hsh + cs, launch, kSpinLimit, hv) && lane == 0)
+        record_err(status, err_key(kPhSync, 0, 0, 0, 0));
+      if (lane * 8 < Ish) {
+        *reinterpret_cast<f32x4*>(hshl + lane * 8) = hv[0];
+        *reinterpret_cast<f32x4*>(hshl + lane * 8 + 4) = hv[1];
+      }
+    }
+    if (wid == kSoftWave) {
+      uint32_t tv = 0;
+      if (!poll_words(soft, 3, launch, kSpinLimit, tv) && lane == 0)
+        record_err(status, err_key(kPhSync, 0, 0, 0, 0));
+      const float sm_max = u2f((uint32_t)__builtin_amdgcn_readlane((int)tv, 0));
+      const float sm_inv = u2f((uint32_t)__builtin_amdgcn_readlane((int)tv, 1));
+      if (lane == 2) sg = u2f(tv);
+      gguf_slot_probs<R>(zk, es, sm_max, sm_inv, zt, E, K, sev, sp, sslot, sid, b == 0, status);
+    }
+  };
   // ---- phase 1: routed gate / up.  Workgroup b takes blocks of 16 row
   // pairs (16 pb .. 16 pb + 15 of slot 16 pb / I; wave w rows 2w, 2w + 1),
   // publishes the block's 16 h values as one write and counts the block in
@@ -859,6 +888,7 @@ __global__ __launch_bounds__(512) void k_gguf_one(
 #pragma unroll
         for (int u = 0; u < 4; ++u) xv[j][u] = *reinterpret_cast<const f32x4*>(x + c + 4 * u);
       }
+      if (!side_done) side_work();
       float xs[NJ];
 #pragma unroll
       for (int j = 0; j < NJ; ++j) xs[j] = xsum16(xv[j]);
@@ -921,28 +951,8 @@ __global__ __launch_bounds__(512) void k_gguf_one(
     for (int i = 0; i < 8; ++i)
       pre_r[i] = q3_load<8>(wrd, (int64_t)min(dfirst + i, H - 1) * I + cr);
   }
-  __shared__ float sg;  // the shared gate
-  // the shared expert's h, read once per workgroup into LDS (wave 0)
-  __shared__ __attribute__((aligned(16))) float hshl[512];
-  if (wid == 0) {
-    f32x4 hv[2];
-    if (!poll8(hsh + cs, launch, kSpinLimit, hv) && lane == 0)
-      record_err(status, err_key(kPhSync, 0, 0, 0, 0));
-    if (lane * 8 < Ish) {
-      *reinterpret_cast<f32x4*>(hshl + lane * 8) = hv[0];
-      *reinterpret_cast<f32x4*>(hshl + lane * 8 + 4) = hv[1];
-    }
-  }
-  if (wid == kSoftWave) {
-    uint32_t tv = 0;
-    if (!poll_words(soft, 3, launch, kSpinLimit, tv) && lane == 0)
-      record_err(status, err_key(kPhSync, 0, 0, 0, 0));
-    const float sm_max = u2f((uint32_t)__builtin_amdgcn_readlane((int)tv, 0));
-    const float sm_inv = u2f((uint32_t)__builtin_amdgcn_readlane((int)tv, 1));
-    if (lane == 2) sg = u2f(tv);
-    gguf_slot_probs<R>(zk, es, sm_max, sm_inv, zt, E, K, sev, sp, sslot, sid, b == 0, status);
-  }
-  __syncthreads();  // hshl
+  if (!side_done) side_work();
+  __syncthreads();  // hshl, sp, sslot, sid, sg
   // ---- phase 2: down projections and the combine
   bool ready = false;
   const bool ls = lane * 8 < Ish, lr = lane * 8 < I;
