@@ -972,22 +972,54 @@ __global__ __launch_bounds__(256) void k_combine(const float* __restrict__ r,
                                                   float* __restrict__ y,
                                                   unsigned long long* status,
                                                   int* __restrict__ clear_flag) {
-  const int t = blockIdx.y, d = blockIdx.x * 256 + threadIdx.x;
+  // four consecutive outputs per thread (H % 4 == 0); the slots' rows are
+  // requested eight at a time before their products
+  const int t = blockIdx.y, d = (blockIdx.x * 256 + threadIdx.x) * 4;
   // the last kernel of a call clears the call's need-lo flag for the next
   if (clear_flag && t == 0 && d == 0) *clear_flag = 0;
   if (d >= H) return;
-  float acc = 0.0f;
-  for (int k = 0; k < K; ++k) acc = acc + probs[(size_t)t * K + k] * r[((size_t)t * K + k) * H + d];
-  float total = acc + shg[t] * rs[(size_t)t * H + d];
-  if (residual) total = total + residual[(size_t)t * H + d];
-  if (!finite_f(total)) record_err(status, err_key(kPhAgg, t, 0, d, 0));
-  y[(size_t)t * H + d] = total;
+  const float* pt = probs + (size_t)t * K;
+  float a[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int k0 = 0; k0 < K; k0 += 8) {
+    float4 rv[8];
+    float pv[8];
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk) {
+      const int k = min(k0 + kk, K - 1);
+      rv[kk] = *reinterpret_cast<const float4*>(r + ((size_t)t * K + k) * H + d);
+      pv[kk] = pt[k];
+    }
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk) {
+      if (k0 + kk < K) {
+        a[0] = a[0] + pv[kk] * rv[kk].x;
+        a[1] = a[1] + pv[kk] * rv[kk].y;
+        a[2] = a[2] + pv[kk] * rv[kk].z;
+        a[3] = a[3] + pv[kk] * rv[kk].w;
+      }
+    }
+  }
+  const float g = shg[t];
+  const float4 sv = *reinterpret_cast<const float4*>(rs + (size_t)t * H + d);
+  float tot[4] = {a[0] + g * sv.x, a[1] + g * sv.y, a[2] + g * sv.z, a[3] + g * sv.w};
+  if (residual) {
+    const float4 rr = *reinterpret_cast<const float4*>(residual + (size_t)t * H + d);
+    tot[0] = tot[0] + rr.x;
+    tot[1] = tot[1] + rr.y;
+    tot[2] = tot[2] + rr.z;
+    tot[3] = tot[3] + rr.w;
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    if (!finite_f(tot[i])) record_err(status, err_key(kPhAgg, t, 0, d + i, 0));
+  *reinterpret_cast<float4*>(y + (size_t)t * H + d) = make_float4(tot[0], tot[1], tot[2], tot[3]);
 }
 
 hipError_t launch_combine(const float* r, const float* rs, const float* probs, const float* shg,
                           const float* residual, int T, int H, int K, float* y,
                           unsigned long long* status, hipStream_t st, int* clear_flag) {
-  hipLaunchKernelGGL(k_combine, dim3((H + 255) / 256, T), dim3(256), 0, st, r, rs, probs, shg,
+  if (H % 4) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_combine, dim3((H / 4 + 255) / 256, T), dim3(256), 0, st, r, rs, probs, shg,
                      residual, H, K, y, status, clear_flag);
   return hipGetLastError();
 }
