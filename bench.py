@@ -63,6 +63,9 @@ def parse():
     ap.add_argument("--batch", type=int, default=32, help="tokens per call, batch workload")
     ap.add_argument("--tokens", type=int, default=2048, help="tokens per call, prefill workload")
     ap.add_argument("--zipf-s", type=float, default=1.1, help="prefill router skew exponent")
+    ap.add_argument("--activations", default="bf16", choices=["bf16", "fp32"],
+                    help="batch / prefill inputs: bf16 values, or fp32 values that are not "
+                         "(hi and lo bf16 parts on the matrix cores, lane-chain router)")
     ap.add_argument("--copy-mib", type=int, default=256)
     ap.add_argument("--layers", type=int, default=40, help="stack workload depth")
     ap.add_argument("--stack-norm", default="ref", choices=["ref", "tree"],
@@ -165,6 +168,9 @@ def grouped(a, blk, stream, dev):
     nbuf = (a.warmup + a.steps) if not prefill else min(a.warmup + a.steps, 8)
     rng = np.random.default_rng(a.seed + 2000)
     x_host = synth.make_activations(rng, (nbuf, T, H))
+    if a.activations == "fp32":
+        # a scale that is not a power of two gives most values nonzero lo parts
+        x_host = (x_host * np.float32(1.0 + 2.0 ** -10)).astype(np.float32)
     if prefill:
         x_host = synth.bias_feature(x_host)
     x = torch.from_numpy(x_host).to(dev)
@@ -221,7 +227,7 @@ def grouped(a, blk, stream, dev):
                "us_per_step": round(us, 3), **common,
                "config": {"workload": f"qwen3.6-35b-a3b moe layer, batch-{T} decode",
                           "batch": T, "hidden": H, "experts": E, "top_k": K, "inter": I,
-                          "group": 32, "bits": 4},
+                          "group": 32, "bits": 4, "activations": a.activations},
                "expert_union_mean": round(u_mean, 2),
                "roofline": {"bound": "hbm", "kernel": "grouped path (router, build, gate/up, "
                             "down, combine)", "achieved": round(gbps, 1),
@@ -238,7 +244,7 @@ def grouped(a, blk, stream, dev):
                "config": {"workload": f"qwen3.6-35b-a3b moe layer, {T}-token prefill chunk, "
                                       f"zipf(s={a.zipf_s}) router bias",
                           "tokens": T, "hidden": H, "experts": E, "top_k": K, "inter": I,
-                          "group": 32, "bits": 4},
+                          "group": 32, "bits": 4, "activations": a.activations},
                "experts_touched": int((counts > 0).sum()),
                "hottest_expert_tokens": int(counts.max()),
                "roofline": {"bound": "mfma", "kernel": "grouped path (router, build, gate/up, "

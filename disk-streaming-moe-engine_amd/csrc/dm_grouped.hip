@@ -328,7 +328,9 @@ __global__ __launch_bounds__(256) void k_split_rows(const float* __restrict__ x,
     lo[i] = l;
     nz |= (l.x | l.y | l.z | l.w) != 0u;
   }
-  if (__builtin_amdgcn_ballot_w64(nz) != 0 && (threadIdx.x & 63) == 0) atomicOr(need_lo, 1);
+  // a plain store of 1, not an atomic: thousands of waves may set the flag,
+  // and same-address atomics would be serialised one after another
+  if (__builtin_amdgcn_ballot_w64(nz) != 0 && (threadIdx.x & 63) == 0) *need_lo = 1;
 }
 
 hipError_t launch_split_rows(const float* x, int64_t n, uint16_t* hi, uint16_t* lo, int* need_lo,

@@ -182,6 +182,29 @@ def test_many_tokens_fp32_activations_vs_oracle(block, oracle, qwen):
         pool.close()
 
 
+def test_fp32_prefill_301_tokens_vs_oracle(block, oracle, qwen):
+    """A 301-token chunk of activations that are not bf16 values (the
+    lane-chain router, hi and lo passes, the need-lo flag set by thousands of
+    waves): sampled tokens and the last five with ids, probabilities and
+    shared gates bit-exact."""
+    T = 301
+    x = np.random.default_rng(312).standard_normal((T, 2048)).astype(np.float32)
+    y, ids, probs, shg = block.forward_arrays(5, x, T)
+    sample = np.concatenate([np.random.default_rng(313).choice(296, 12, replace=False),
+                             np.arange(296, T)])
+    pool = oracle.Pool(8)
+    try:
+        yo, ido, po, so = oracle.moe_layer_q4(qwen, x[sample], len(sample), pool=pool)
+    finally:
+        pool.close()
+    assert np.array_equal(ids[sample], ido)
+    assert np.array_equal(probs[sample].view(np.uint32), po.view(np.uint32))
+    assert np.array_equal(shg[sample].view(np.uint32), so.view(np.uint32))
+    for i, t in enumerate(sample):
+        err, rms, ok = tol_check(y[t], yo[i])
+        assert ok, (t, err, rms)
+
+
 def test_many_tokens_toy_layer_vs_oracle(block, oracle):
     """Fewer experts than one router workgroup covers (16 < 64), hidden 256."""
     L = synth.make_layer(**synth.CONFIG_TOY, seed=8)
