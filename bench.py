@@ -37,6 +37,28 @@ GGUF_PROFILE = os.path.join("profiles", "k_dequant_gguf_q3k_expert_layer.md")
 GGUF_MOE_PROFILE = os.path.join("profiles", "gguf_moe_q3k_layer_decode.md")
 
 
+def f10_metrics(ref, cand):
+    """The reference's F10 comparison of a candidate output against a
+    reference output (tools/dismoen-tools/src/compare.rs:648-700): delta_max =
+    max |c - r|, epsilon_rel = sqrt(sum (c - r)^2 / sum r^2), cos_theta =
+    r.c / (|r| |c|), in float64; and the G-M3-1 gate of the MoE-layer
+    comparison (compare.rs:1041-1043): delta_max <= 1e-3 and
+    epsilon_rel <= 1e-4."""
+    import numpy as np
+    r = np.asarray(ref, dtype=np.float64).reshape(-1)
+    c = np.asarray(cand, dtype=np.float64).reshape(-1)
+    if r.size != c.size or r.size == 0 or not (np.isfinite(r).all() and np.isfinite(c).all()):
+        return {"error": "size mismatch, empty or non-finite"}
+    d = np.abs(c - r)
+    sr, sc = float(np.sum(r * r)), float(np.sum(c * c))
+    eps = float(np.sqrt(np.sum(d * d) / sr)) if sr > 0 else 0.0
+    nrm = np.sqrt(sr) * np.sqrt(sc)
+    cos = float(np.dot(r, c) / nrm) if nrm > 0 else 0.0
+    dmax = float(d.max())
+    return {"delta_max": dmax, "epsilon_rel": eps, "cos_theta": cos,
+            "g_m3_1_pass": bool(dmax <= 1e-3 and eps <= 1e-4)}
+
+
 def profiled_traffic(profile=TRAFFIC_PROFILE, key="traffic_bytes_per_launch"):
     try:
         with open(os.path.join(ROOT, profile)) as f:
@@ -217,7 +239,7 @@ def grouped(a, blk, stream, dev):
     common = {"n_gpus": 1, "steps": a.steps, "warmup": a.warmup, "ms_per_step": round(ms, 6),
               "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
               "parity_sample": {"tokens": len(smp), "ids_bit_exact": ids_ok,
-                                "max_abs_over_rms": rel}}
+                                "max_abs_over_rms": rel, "f10": f10_metrics(yo, yg)}}
     if not prefill:
         nbytes = u_mean * eb + synth.expert_bytes(H, Ish) + 2 * E * H + 2 * H + T * H * 8
         gbps = nbytes / (ms * 1e-3) / 1e9
@@ -408,7 +430,8 @@ def gguf_moe(a, blk, stream, dev):
                 rms = float(np.sqrt(np.mean(ref.astype(np.float64) ** 2)))
                 rec["parity_last_token"] = {
                     "ids_bit_exact": bool(np.array_equal(idd[-1].cpu().numpy(), ids[0])),
-                    "max_abs_over_rms": float(np.max(np.abs(y - ref)) / rms)}
+                    "max_abs_over_rms": float(np.max(np.abs(y - ref)) / rms),
+                    "f10": f10_metrics(ref, y)}
                 rec["cpu_baseline"] = {"value": round((t_deq + t_blk) * 1e6, 1),
                                        "unit": "us/token", "cores": 1, "kind": "port",
                                        "sample": "dequant of 8 of the 256 experts scaled to 256 "
@@ -508,6 +531,7 @@ def main():
         ids_ok = bool(np.array_equal(ids[t_last].cpu().numpy(), ido[0]))
         yl = y[t_last].cpu().numpy().astype(np.float64)
         rel = float(np.max(np.abs(yl - yo[0])) / np.sqrt(np.mean(yo[0].astype(np.float64) ** 2)))
+        f10 = f10_metrics(yo[0], yl)
         traffic = profiled_traffic() if a.workload == "decode" else None
         # the drop-in's host-pointer form, as a compiled caller makes it: x and
         # the outputs in the caller's own host arrays, one synchronous C call
@@ -549,12 +573,13 @@ def main():
                        "hidden": H, "experts": L.num_experts, "top_k": K, "inter": L.inter,
                        "inter_sh": L.inter_sh, "group": 32, "bits": 4, "tokens": a.steps},
             "achieved_gbps": round(gbps, 1),
-            "roofline": {"bound": "hbm", "kernel": "k_moe_decode (one fused launch per token)",
+            "roofline": {"bound": "hbm",
+                         "kernel": "k_moe_decode_xs (XCD-sliced fused launch per token)",
                          "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                          "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": traffic,
                          "traffic_source": TRAFFIC_PROFILE if traffic else None,
                          "bytes_per_token": bytes_tok},
-            "parity_last_token": {"ids_bit_exact": ids_ok, "max_abs_over_rms": rel},
+            "parity_last_token": {"ids_bit_exact": ids_ok, "max_abs_over_rms": rel, "f10": f10},
             "host_pointer_us_per_token": round(host_us, 2),
             "host_pointer_forward_into_us_per_token": round(host_into_us, 2),
             "host_pointer_forward_arrays_us_per_token": round(host_arrays_us, 2),

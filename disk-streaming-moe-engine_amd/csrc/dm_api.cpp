@@ -7,6 +7,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <cmath>
 #include <atomic>
 #include <chrono>
 #include <mutex>
@@ -44,10 +45,15 @@ std::atomic<int> g_live_ctx[kMaxDevices];
 // uses the array's name as an address: dmh_create resolves each device's
 // copy once (hipGetSymbolAddress with that device current) into
 // g_scratch_dev[device], and only that pointer reaches kernels.  Every call
-// of the entry point on a device shares that device's copy.
+// of the entry point on a device shares that device's copy, so the calls on
+// one device are put in one order: each call's stream waits for the event
+// the previous call (from any context) recorded after its kernels, and
+// records it again after its own (g_noalloc_ev, created with the address).
 constexpr size_t kNoAllocScratchBytes = (size_t)8 << 20;
 static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
 void* g_scratch_dev[kMaxDevices];
+hipEvent_t g_noalloc_ev[kMaxDevices];
+bool g_noalloc_recorded[kMaxDevices];
 std::mutex g_scratch_mu;
 // first-error key slots: [0, kMaxLayers) uploaded 4-bit layers, kMaxLayers
 // the unit calls, then one per GGUF layer
@@ -119,15 +125,21 @@ struct DevBuf {
 
 // Page-locked host memory for the host-pointer calls (hipHostMalloc): the
 // copies are single DMA transfers instead of staged ones, and kernels can
-// read and write it directly through its device address d.
+// read and write it directly through its device address d.  flags: the
+// single-token call's output block is coherent (fine-grained) memory, so the
+// fused decode kernel's stores reach it without staying in the GPU's caches,
+// and each workgroup's status key is a system-scope release after its
+// outputs: a host that sees the key sees the outputs.  Inputs stay in a
+// default block, which the GPU may cache (every workgroup reads all of x).
 struct PinBuf {
   uint8_t* p = nullptr;
   uint8_t* d = nullptr;
   size_t cap = 0;  // bytes
+  unsigned flags = hipHostMallocDefault;
   hipError_t ensure(size_t n) {
     if (n <= cap) return hipSuccess;
     release();
-    hipError_t e = hipHostMalloc(reinterpret_cast<void**>(&p), n, hipHostMallocDefault);
+    hipError_t e = hipHostMalloc(reinterpret_cast<void**>(&p), n, flags);
     if (e == hipSuccess) e = hipHostGetDevicePointer(reinterpret_cast<void**>(&d), p, 0);
     if (e != hipSuccess) {
       release();
@@ -157,6 +169,7 @@ struct dmh_ctx {
   // device and page-locked on the host
   DevBuf<uint8_t> io_in, io_out;
   PinBuf pin;
+  PinBuf pin_out{nullptr, nullptr, 0, hipHostMallocCoherent};
   DevBuf<uint8_t> stage;
   // several tokens per call (grouped experts)
   DevBuf<int32_t> g_off, g_perm, g_meta, g_needlo;
@@ -179,6 +192,10 @@ struct dmh_ctx {
   bool counted = false;           // counted in g_live_ctx
   float* ones = nullptr;          // [kNormMaxH] 1.0f: gamma of layers without one
   hipEvent_t switch_ev = nullptr;  // orders a stream switch after queued work
+  // polls of a persistent kernel's wait before it gives up (dmh_set_spin_limit)
+  long spin_limit = dm::kDefaultSpinLimit;
+  // host-pointer calls rerun through the multi-kernel path after a time-out
+  int64_t sync_fallbacks = 0;
 };
 
 namespace {
@@ -304,6 +321,11 @@ namespace {
 Layer* get_layer(dmh_ctx* ctx, int layer) {
   if (!ctx || layer < 0 || layer >= (int)ctx->layers.size()) return nullptr;
   return ctx->layers[layer];
+}
+
+// A first-error key that says a wait between workgroups gave up.
+bool sync_timeout(uint64_t key) {
+  return key != dm::kNoError && dm::key_phase(key) == dm::kPhSync;
 }
 
 hipError_t reset_status(dmh_ctx* ctx, int slot) {
@@ -464,6 +486,7 @@ hipError_t run_block(dmh_ctx* ctx, Layer* Ly, int layer, const float* dx, const 
       if (Ly->launches >= (1u << 24) && (e = reset_counters(ctx, Ly)) != hipSuccess) return e;
       dm::DecodeSync S = dm::decode_sync_carve(L, Ly->plan, Ly->sync);
       S.n = ++Ly->launches;
+      S.spin = ctx->spin_limit;
       e = dm::launch_moe_decode(L, Ly->plan, dx + (size_t)t * L.H,
                                 dres ? dres + (size_t)t * L.H : nullptr, dy + (size_t)t * L.H,
                                 dids + (size_t)t * L.K, dprobs + (size_t)t * L.K, dshg + t, S,
@@ -599,11 +622,11 @@ GgufLayer* get_glayer(dmh_ctx* c, int layer) {
 // projections with moe_aggregate_forward.
 hipError_t run_gguf_block(dmh_ctx* c, GgufLayer* G, unsigned long long* status, const float* dx,
                           const float* dres, int T, float* dy, int32_t* dids, float* dprobs,
-                          float* dshg) {
+                          float* dshg, bool allow_one = true) {
   const dm::GgufMoeDev& L = G->dev;
   hipStream_t st = c->cur;
   hipError_t e;
-  if (T == 1 && G->sync && G->grid > 0 &&
+  if (allow_one && T == 1 && G->sync && G->grid > 0 &&
       g_live_ctx[c->device].load(std::memory_order_relaxed) <= 1) {
     hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
     if ((e = hipStreamIsCapturing(st, &cap)) != hipSuccess) return e;
@@ -613,7 +636,7 @@ hipError_t run_gguf_block(dmh_ctx* c, GgufLayer* G, unsigned long long* status, 
         G->launches = 0;
       }
       return dm::launch_gguf_one_token(L, dx, dres, dy, dids, dprobs, dshg, G->sync,
-                                       ++G->launches, G->grid, status, st);
+                                       ++G->launches, G->grid, status, st, c->spin_limit);
     }
   }
   const int ldh = L.I > L.Ish ? L.I : L.Ish;
@@ -638,6 +661,22 @@ hipError_t run_gguf_block(dmh_ctx* c, GgufLayer* G, unsigned long long* status, 
 extern "C" {
 
 const char* dmh_version(void) { return "dismoen_hip 1 gfx950"; }
+
+int dmh_set_spin_limit(dmh_ctx* c, int64_t polls) {
+  if (!c) return DMH_ERR_INVALID_ARG;
+  c->spin_limit = polls >= 0 ? (long)polls : dm::kDefaultSpinLimit;
+  return DMH_OK;
+}
+
+int dmh_xcd_rotation(const uint32_t* xcd_of_workgroup, int num_workgroups) {
+  return dm::xcd_rotation(xcd_of_workgroup, num_workgroups);
+}
+
+int dmh_sync_fallbacks(dmh_ctx* c, int64_t* count) {
+  if (!c || !count) return DMH_ERR_INVALID_ARG;
+  *count = c->sync_fallbacks;
+  return DMH_OK;
+}
 
 int dmh_create(int device, dmh_ctx** out, char* err, size_t errlen) {
   if (!out) return set_err(err, errlen, DMH_ERR_INVALID_ARG, "dmh_create: out is NULL");
@@ -693,6 +732,14 @@ int dmh_create(int device, dmh_ctx** out, char* err, size_t errlen) {
         return set_err(err, errlen, DMH_ERR_HIP, "dmh_create: scratch address: %s",
                        hipGetErrorString(e));
       }
+      hipEvent_t ev = nullptr;
+      e = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
+      if (e != hipSuccess) {
+        dmh_destroy(c);
+        return set_err(err, errlen, DMH_ERR_HIP, "dmh_create: scratch event: %s",
+                       hipGetErrorString(e));
+      }
+      g_noalloc_ev[device] = ev;
       g_scratch_dev[device] = p;
     }
   }
@@ -715,6 +762,7 @@ int dmh_destroy(dmh_ctx* c) {
   c->io_in.release();
   c->io_out.release();
   c->pin.release();
+  c->pin_out.release();
   c->stage.release();
   c->g_off.release();
   c->g_perm.release();
@@ -963,7 +1011,8 @@ namespace {
 // the status key into the block as it ends, the call's key is their
 // minimum; other paths read it back), and the key's reset is skipped while
 // the previous host call left it clean.
-// A status word no workgroup writes (phase 15 = sync keys carry token 0).
+// A status word no workgroup writes (phase 15 is no phase; only the
+// no-error key, all ones, has it).
 constexpr unsigned long long kKeySentinel = 0xFFFFFFFFFFFFFFF0ull;
 constexpr std::chrono::milliseconds kHostPollLimit{200};
 
@@ -972,18 +1021,23 @@ int moe_forward_host1(dmh_ctx* c, Layer* Ly, int layer, const float* x, const fl
                       char* err, size_t errlen) {
   const LayerDev& L = Ly->dev;
   const size_t H = (size_t)L.H, K = (size_t)L.K;
-  const size_t o_x = 0, o_res = align256(H * 4), o_y = o_res + (residual ? align256(H * 4) : 0),
-               o_ids = o_y + align256(H * 4), o_probs = o_ids + align256(K * 4),
+  // inputs [x | residual] in one block, outputs [y | ids | probs | shared
+  // gate | status keys] in the coherent one
+  const size_t o_x = 0, o_res = align256(H * 4), in_bytes = o_res + (residual ? H * 4 : 0);
+  const size_t o_y = 0, o_ids = o_y + align256(H * 4), o_probs = o_ids + align256(K * 4),
                o_shg = o_probs + align256(K * 4), o_key = o_shg + 256,
                nkey = (size_t)(Ly->fused ? Ly->plan.grid : 1), bytes = o_key + nkey * 8;
   hipStream_t st = c->cur;
-  HIP_TRY(c->pin.ensure(bytes));
-  uint8_t* hb = c->pin.p;
-  uint8_t* db = c->pin.d;
-  memcpy(hb + o_x, x, H * 4);
-  if (residual) memcpy(hb + o_res, residual, H * 4);
-  const float* dx = reinterpret_cast<const float*>(db + o_x);
-  const float* dres = residual ? reinterpret_cast<const float*>(db + o_res) : nullptr;
+  HIP_TRY(c->pin.ensure(in_bytes));
+  HIP_TRY(c->pin_out.ensure(bytes));
+  uint8_t* hi = c->pin.p;
+  uint8_t* di = c->pin.d;
+  uint8_t* hb = c->pin_out.p;
+  uint8_t* db = c->pin_out.d;
+  memcpy(hi + o_x, x, H * 4);
+  if (residual) memcpy(hi + o_res, residual, H * 4);
+  const float* dx = reinterpret_cast<const float*>(di + o_x);
+  const float* dres = residual ? reinterpret_cast<const float*>(di + o_res) : nullptr;
   float* dy = reinterpret_cast<float*>(db + o_y);
   int32_t* dids = reinterpret_cast<int32_t*>(db + o_ids);
   float* dprobs = reinterpret_cast<float*>(db + o_probs);
@@ -992,13 +1046,13 @@ int moe_forward_host1(dmh_ctx* c, Layer* Ly, int layer, const float* x, const fl
   size_t nk = 1;  // status words the last run left in the block
   volatile unsigned long long* keys = reinterpret_cast<unsigned long long*>(hb + o_key);
   auto run_and_fetch = [&](bool allow_fused) -> hipError_t {
-    // The fused kernel's workgroups write the key into the block themselves,
-    // each as its last store after its outputs have completed; the block is
-    // fine-grained host memory, so once every word has changed from the
-    // sentinel the outputs are in place, and the call returns without the
-    // runtime's stream synchronisation (a poll of the block instead).  A
-    // run that has not finished within kHostPollLimit is left to
-    // hipStreamSynchronize, which also reports a failed launch.
+    // The fused kernel's workgroups write the outputs and then the status
+    // keys into the block themselves (fine-grained host memory), each key a
+    // system-scope release after that workgroup's outputs, so once every key
+    // word has changed from the sentinel the outputs are in place and the
+    // call returns without the runtime's stream synchronisation (a poll of
+    // the block instead).  A run that has not finished within kHostPollLimit
+    // is left to hipStreamSynchronize, which also reports a failed launch.
     for (size_t i = 0; i < nkey; ++i) keys[i] = kKeySentinel;
     bool exported = false;
     hipError_t e = run_block(c, Ly, layer, dx, dres, 1, dy, dids, dprobs, dshg, allow_fused, nm,
@@ -1037,6 +1091,16 @@ int moe_forward_host1(dmh_ctx* c, Layer* Ly, int layer, const float* x, const fl
     HIP_TRY(reset_status(c, layer));
     HIP_TRY(run_and_fetch(false));
     key = key_of();
+  } else if (sync_timeout(key)) {
+    // a wait of the persistent grid gave up (another process's kernels
+    // held CUs it needed): start the tags again and rerun the token on the
+    // multi-kernel path, which has no waits between workgroups
+    HIP_TRY(hipStreamSynchronize(c->cur));
+    HIP_TRY(reset_counters(c, Ly));
+    HIP_TRY(reset_status(c, layer));
+    HIP_TRY(run_and_fetch(false));
+    key = key_of();
+    ++c->sync_fallbacks;
   }
   memcpy(y, hb + o_y, H * 4);
   if (ids) memcpy(ids, hb + o_ids, K * 4);
@@ -1142,7 +1206,7 @@ int moe_forward_impl(dmh_ctx* c, int layer, const float* x, const float* residua
 
 // rmsnorm's eps check (src/layers/rmsnorm.mojo:36-41).
 int eps_check(float eps, char* err, size_t errlen) {
-  if (eps != eps || eps <= 0.0f || eps > 3.0e38f)
+  if (!std::isfinite(eps) || eps <= 0.0f)
     return set_err(err, errlen, DMH_ERR_CONFIG,
                    "{\"error_type\":\"CONFIG_ERROR\",\"detail\":\"rms_norm_eps must be finite"
                    " and > 0\",\"stage\":\"config\"}");
@@ -1200,10 +1264,24 @@ int dmh_moe_forward_noalloc(dmh_ctx* c, int layer, const float* x, const float* 
   if (!ids) { ids = (int32_t*)(base + off); off += align256(TK * 4); }
   if (!probs) { probs = (float*)(base + off); off += align256(TK * 4); }
   if (!shg) { shg = (float*)(base + off); off += align256((size_t)T * 4); }
+  // One call at a time on this device's scratch: wait for the previous
+  // call's kernels, whichever context queued them.  A stream being captured
+  // cannot wait on an event recorded outside its capture; a captured call is
+  // ordered only by the stream its graph is launched on.
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  HIP_TRY(hipStreamIsCapturing(c->cur, &cap));
+  const bool chain = cap == hipStreamCaptureStatusNone;
+  std::lock_guard<std::mutex> order(g_scratch_mu);
+  if (chain && g_noalloc_recorded[c->device])
+    HIP_TRY(hipStreamWaitEvent(c->cur, g_noalloc_ev[c->device], 0));
   // the need-lo flag and the front-end counter start at zero (a call that
   // failed may have left the flag set)
   if (sc.needlo) HIP_TRY(dm::launch_fill_i32(sc.needlo, kFlagInts, 0, c->cur));
   HIP_TRY(run_block(c, Ly, layer, x, residual, T, y, ids, probs, shg, true, nullptr, &sc));
+  if (chain) {
+    HIP_TRY(hipEventRecord(g_noalloc_ev[c->device], c->cur));
+    g_noalloc_recorded[c->device] = true;
+  }
   c->last_ids[layer] = ids;
   c->last_k[layer] = L.K;
   return DMH_OK;
@@ -1277,39 +1355,71 @@ int dmh_moe_stack_forward(dmh_ctx* c, int first, int nl, float eps, const float*
   // device pointers: layer 0 reads x and the last layer writes out directly
   // (unless they alias); host pointers: x goes through hA
   const bool direct = dev && out != x;
-  const float* src = x;
-  if (!direct) {
-    HIP_TRY(hipMemcpyAsync(hA, x, TH * 4, dev ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice,
-                           st));
-    src = hA;
-  }
   const bool own_ids = !(dev && ids), own_probs = !(dev && probs);
   if (own_ids) HIP_TRY(c->ids.ensure(TK * nl));
   if (own_probs) HIP_TRY(c->probs.ensure(TK * nl));
   HIP_TRY(c->shg.ensure(T));
-  if (!dev)
-    for (int l = first; l < first + nl; ++l) HIP_TRY(reset_status(c, l));
-  for (int i = 0; i < nl; ++i) {
-    const int l = first + i;
-    int32_t* dids = (own_ids ? c->ids.p : ids) + (size_t)i * TK;
-    float* dprobs = (own_probs ? c->probs.p : probs) + (size_t)i * TK;
-    float* dst = (direct && i == nl - 1) ? out : (src == hA ? hB : hA);
-    const dm::NormSpec nm = layer_norm(c, c->layers[l], eps, (flags & DMH_F_NORM_TREE) != 0);
-    HIP_TRY(run_block(c, c->layers[l], l, src, src, T, dst, dids, dprobs, c->shg.p, true, &nm));
-    c->last_ids[l] = dids;
-    c->last_k[l] = K;
-    src = dst;
-  }
-  if (src != out)
-    HIP_TRY(hipMemcpyAsync(out, src, TH * 4,
-                           dev ? hipMemcpyDeviceToDevice : hipMemcpyDeviceToHost, st));
+  auto run_stack = [&](bool allow_fused) -> hipError_t {
+    hipError_t e;
+    const float* src = x;
+    if (!direct) {
+      if ((e = hipMemcpyAsync(hA, x, TH * 4,
+                              dev ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice, st)) !=
+          hipSuccess)
+        return e;
+      src = hA;
+    }
+    if (!dev)
+      for (int l = first; l < first + nl; ++l)
+        if ((e = reset_status(c, l)) != hipSuccess) return e;
+    for (int i = 0; i < nl; ++i) {
+      const int l = first + i;
+      int32_t* dids = (own_ids ? c->ids.p : ids) + (size_t)i * TK;
+      float* dprobs = (own_probs ? c->probs.p : probs) + (size_t)i * TK;
+      float* dst = (direct && i == nl - 1) ? out : (src == hA ? hB : hA);
+      const dm::NormSpec nm = layer_norm(c, c->layers[l], eps, (flags & DMH_F_NORM_TREE) != 0);
+      if ((e = run_block(c, c->layers[l], l, src, src, T, dst, dids, dprobs, c->shg.p,
+                         allow_fused, &nm)) != hipSuccess)
+        return e;
+      c->last_ids[l] = dids;
+      c->last_k[l] = K;
+      src = dst;
+    }
+    if (src != out &&
+        (e = hipMemcpyAsync(out, src, TH * 4,
+                            dev ? hipMemcpyDeviceToDevice : hipMemcpyDeviceToHost, st)) !=
+            hipSuccess)
+      return e;
+    return hipSuccess;
+  };
+  HIP_TRY(run_stack(true));
   if (dev) return DMH_OK;
   std::vector<int32_t> hids(TK * nl);
   std::vector<unsigned long long> keys(nl);
-  HIP_TRY(hipMemcpyAsync(hids.data(), c->ids.p, TK * nl * 4, hipMemcpyDeviceToHost, st));
-  if (probs) HIP_TRY(hipMemcpyAsync(probs, c->probs.p, TK * nl * 4, hipMemcpyDeviceToHost, st));
-  HIP_TRY(hipMemcpyAsync(keys.data(), c->status + first, nl * 8, hipMemcpyDeviceToHost, st));
-  HIP_TRY(hipStreamSynchronize(st));
+  auto fetch = [&]() -> hipError_t {
+    hipError_t e;
+    if ((e = hipMemcpyAsync(hids.data(), c->ids.p, TK * nl * 4, hipMemcpyDeviceToHost, st)) !=
+        hipSuccess)
+      return e;
+    if (probs && (e = hipMemcpyAsync(probs, c->probs.p, TK * nl * 4, hipMemcpyDeviceToHost,
+                                     st)) != hipSuccess)
+      return e;
+    if ((e = hipMemcpyAsync(keys.data(), c->status + first, nl * 8, hipMemcpyDeviceToHost, st)) !=
+        hipSuccess)
+      return e;
+    return hipStreamSynchronize(st);
+  };
+  HIP_TRY(fetch());
+  bool timed_out = false;
+  for (int i = 0; i < nl; ++i) timed_out |= sync_timeout(keys[i]);
+  if (timed_out) {
+    // a wait of a persistent grid gave up: start every layer's tags again and
+    // rerun the stack on the multi-kernel path, which has no such waits
+    for (int l = first; l < first + nl; ++l) HIP_TRY(reset_counters(c, c->layers[l]));
+    HIP_TRY(run_stack(false));
+    HIP_TRY(fetch());
+    ++c->sync_fallbacks;
+  }
   if (ids) memcpy(ids, hids.data(), TK * nl * 4);
   for (int i = 0; i < nl; ++i) {
     int rc = finish_status(c, c->layers[first + i], first + i, keys[i], hids.data() + i * TK, err,
@@ -1890,6 +2000,20 @@ int dmh_moe_forward_gguf(dmh_ctx* c, int layer, const float* x, const float* res
   HIP_TRY(reset_status(c, kGgufSlot0 + layer));
   HIP_TRY(run_gguf_block(c, G, status, c->x.p, dres, T, c->y.p, c->ids.p, c->probs.p, c->shg.p));
   unsigned long long key = 0;
+  HIP_TRY(hipMemcpyAsync(&key, status, 8, hipMemcpyDeviceToHost, st));
+  HIP_TRY(hipStreamSynchronize(st));
+  if (sync_timeout(key)) {
+    // a wait of the single-token grid gave up: start its tags again and
+    // rerun the token on the four-launch path, which has no such waits
+    if (G->sync) {
+      HIP_TRY(hipMemsetAsync(G->sync, 0, G->sync_bytes, st));
+      G->launches = 0;
+    }
+    HIP_TRY(reset_status(c, kGgufSlot0 + layer));
+    HIP_TRY(run_gguf_block(c, G, status, c->x.p, dres, T, c->y.p, c->ids.p, c->probs.p, c->shg.p,
+                           false));
+    ++c->sync_fallbacks;
+  }
   HIP_TRY(hipMemcpyAsync(y, c->y.p, TH * 4, hipMemcpyDeviceToHost, st));
   if (ids) HIP_TRY(hipMemcpyAsync(ids, c->ids.p, TK * 4, hipMemcpyDeviceToHost, st));
   if (probs) HIP_TRY(hipMemcpyAsync(probs, c->probs.p, TK * 4, hipMemcpyDeviceToHost, st));

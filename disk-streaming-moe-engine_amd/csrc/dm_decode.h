@@ -39,6 +39,7 @@ struct DecodeSync {
   uint64_t* hl;  // XCD-sliced form: [pairs][64] packed h words (pack_h2), XCD-local
   uint64_t* pt;  // XCD-sliced form: [nx][H] (tag, partial output)
   unsigned n;    // launch index, >= 1 (the tag of this launch)
+  long spin;     // polls of a wait before it gives up with a sync error
 };
 size_t decode_sync_bytes(const LayerDev& L, const DecodePlan& P);
 DecodeSync decode_sync_carve(const LayerDev& L, const DecodePlan& P, void* base);
@@ -51,6 +52,10 @@ DecodePlan make_decode_plan(const LayerDev& L, int num_cus, int nx = 0);
 // Launches one workgroup per CU that records the XCD it runs on; *nx = the
 // XCD count when the workgroups were placed on the XCDs in rotation, else 0.
 hipError_t probe_xcd_map(int num_cus, int* nx);
+// The decision of probe_xcd_map on a recorded placement (xcd[b] = the XCD
+// workgroup b ran on): the XCD count n when xcd[b] = (b + r) % n for
+// one r and n divides nwg, else 0.
+int xcd_rotation(const unsigned* xcd, int nwg);
 hipError_t decode_occupancy(const LayerDev& L, const DecodePlan& P, int* blocks_per_cu);
 // nm.eps > 0: the router and experts see rmsnorm(x, nm.gamma, nm.eps) in the
 // order nm.seq selects (NormSpec).  cooperative: launch with

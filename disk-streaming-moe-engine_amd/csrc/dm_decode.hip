@@ -290,11 +290,12 @@ __device__ __forceinline__ void router_compute(const LayerDev& L, uint4 (&rw)[kR
 // Identical in every workgroup; only `record` workgroups write error keys.
 template <int R>
 __device__ __forceinline__ bool route(const uint64_t* zt, unsigned tag, int E, int K, SelState& st,
-                                      bool record, int token, unsigned long long* status) {
+                                      bool record, int token, unsigned long long* status,
+                                      long lim) {
   constexpr int NK = 4 * R;
   const int lane = threadIdx.x & 63;
   float z[NK];
-  const bool ok = poll_logits<R>(zt, tag, E, z, nullptr);
+  const bool ok = poll_logits<R>(zt, tag, E, z, nullptr, lim);
   if (!ok && lane == 0) record_err(status, err_key(kPhSync, 0, 0, 0, 0));
   // the logits' copy for the exact path; non-finite logits are recorded on
   // a separate, rarely taken path
@@ -345,12 +346,13 @@ __device__ __forceinline__ bool route(const uint64_t* zt, unsigned tag, int E, i
 // (softmax_sum), off the routing path.
 template <int R>
 __device__ __forceinline__ void softmax_exp(const uint64_t* zt, unsigned tag, int E, SelState& st,
-                                            bool record, int token, unsigned long long* status) {
+                                            bool record, int token, unsigned long long* status,
+                                            long lim) {
   constexpr int NK = 4 * R;
   const int lane = threadIdx.x & 63;
   float z[NK];
   float gl = 0.0f;
-  (void)poll_logits<R>(zt, tag, E, z, &gl);  // wave 0 reports a timeout
+  (void)poll_logits<R>(zt, tag, E, z, &gl, lim);  // wave 0 reports a timeout
   uint32_t lm = 0;
 #pragma unroll
   for (int i = 0; i < NK; ++i)
@@ -464,18 +466,31 @@ __device__ __forceinline__ void finish_probs(int E, int K, SelState& st, bool re
   }
 }
 
-// The end of a workgroup when status_out is set: once this workgroup's own
-// error records (atomicMin on *status) have completed, thread 0 reads the
-// key and stores it to status_out[blockIdx.x].  Each entry is the minimum of
-// a set of records that holds at least the workgroup's own, so the minimum
-// over all entries is the launch's first-error key: no counter, no atomic
-// shared by the grid.  Launches without status_out pay nothing.
+// The end of a workgroup when status_out is set (the host waits on these
+// words instead of synchronising the stream): once this workgroup's output
+// stores and its own error records (atomicMin on *status) have completed,
+// thread 0 reads the key and stores it to status_out[blockIdx.x].  Each
+// entry is the minimum of a set of records that holds at least the
+// workgroup's own, so the minimum over all entries is the launch's
+// first-error key: no counter, no atomic shared by the grid.  Launches
+// without status_out pay nothing.
+//
+// The key is a system-scope release: the workgroup's outputs (written
+// before the barrier by any of its waves) are visible to the host before the
+// key that says they are complete, whatever memory type the host block has.
+// It costs an L2 write-back per workgroup: the host-pointer call measured
+// about 4.8 us slower than with a plain store of the key, whose ordering
+// after the outputs the memory model does not promise.  (System-scope output
+// stores waited on before the key, and a host-side sentinel check of every
+// output word, measured as slow.)
 __device__ __forceinline__ void end_workgroup(const unsigned long long* status,
                                               unsigned long long* status_out) {
   if (!status_out) return;
   wait_vm();
   __syncthreads();
-  if (threadIdx.x == 0) status_out[blockIdx.x] = ld_coh_u64(status);
+  if (threadIdx.x == 0)
+    __hip_atomic_store(status_out + blockIdx.x, ld_coh_u64(status), __ATOMIC_RELEASE,
+                       __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
 // The sum of the squares sq[0..n) one after another (rmsnorm's order,
@@ -673,10 +688,10 @@ __global__ __launch_bounds__(kThreads) void k_moe_decode(
   // ---- P2: routing on wave 0, softmax numerators on wave 7 (every
   // workgroup computes the same result, so there is no broadcast hand-off) --
   if (w == 0) {
-    const bool rok = route<R>(S.zt, n, E, K, st, b == 0, token, status);
+    const bool rok = route<R>(S.zt, n, E, K, st, b == 0, token, status, S.spin);
     if (lane == 0) st.misc[2] = rok ? 1.0f : 0.0f;
   } else if (w == kNormWave) {
-    softmax_exp<R>(S.zt, n, E, st, b == 0, token, status);
+    softmax_exp<R>(S.zt, n, E, st, b == 0, token, status, S.spin);
   }
   __syncthreads();
   const bool ok = st.misc[2] != 0.0f;
@@ -797,7 +812,7 @@ __global__ __launch_bounds__(kThreads) void k_moe_decode(
     }
     const uint32_t all = (1u << min(kHw, (nwords - tid + kThreads - 1) / kThreads)) - 1u;
     have &= all;
-    for (long spin = 0; spin < kSpinLimit && ok; ++spin) {
+    for (long spin = 0; spin < S.spin && ok; ++spin) {
 #pragma unroll
       for (int u = 0; u < kHw; ++u) {
         if (!(have >> u & 1u) && (all >> u & 1u)) {
@@ -1165,10 +1180,10 @@ __global__ __launch_bounds__(kThreads) void k_moe_decode_xs(
 
   // ---- routing (as in the original form) ------------------------------------
   if (w == 0) {
-    const bool rok = route<R>(zl, n, E, K, st, b == 0, token, status);
+    const bool rok = route<R>(zl, n, E, K, st, b == 0, token, status, S.spin);
     if (lane == 0) st.misc[2] = rok ? 1.0f : 0.0f;
   } else if (w == kNormWave) {
-    softmax_exp<R>(zl, n, E, st, b == 0, token, status);
+    softmax_exp<R>(zl, n, E, st, b == 0, token, status, S.spin);
   }
   __syncthreads();
   const bool ok = st.misc[2] != 0.0f;
@@ -1229,7 +1244,8 @@ __global__ __launch_bounds__(kThreads) void k_moe_decode_xs(
   const int fin_wg = nb - 1;
   if (w == kNormWave) {
     softmax_sum<R>(E, K, st, b == 0, token, status);
-    if (b == fin_wg) finish_probs(E, K, st, true, token, status, ids_out, probs_out, shg_out);
+    if (b == fin_wg)
+      finish_probs(E, K, st, true, token, status, ids_out, probs_out, shg_out);
   }
 #pragma unroll
   for (int jr = 0; jr < kXsR; ++jr)
@@ -1270,7 +1286,7 @@ __global__ __launch_bounds__(kThreads) void k_moe_decode_xs(
         hv[u] = ld_coh_u64(S.hl + (size_t)(xc + nx * (wd >> 6)) * 64 + (wd & 63));
       }
     }
-    for (long spin = 0; spin < kSpinLimit && ok && have != all; ++spin) {
+    for (long spin = 0; spin < S.spin && ok && have != all; ++spin) {
 #pragma unroll
       for (int u = 0; u < kXsHw; ++u) {
         if ((all >> u & 1u) && !(have >> u & 1u) && h2_current(hv[u], n)) {
@@ -1343,7 +1359,7 @@ __global__ __launch_bounds__(kThreads) void k_moe_decode_xs(
       // two polls in flight: while the older one is checked the newer one
       // travels, so a partial is seen about half a round trip sooner
       uint64_t v = ld_coh_u64(src), nv = ld_coh_u64(src);
-      for (long spin = 0; spin < kSpinLimit && ok && (uint32_t)(v >> 32) != n; ++spin) {
+      for (long spin = 0; spin < S.spin && ok && (uint32_t)(v >> 32) != n; ++spin) {
         v = nv;
         nv = ld_coh_u64(src);
       }
@@ -1389,6 +1405,7 @@ DecodeSync decode_sync_carve(const LayerDev& L, const DecodePlan& P, void* base)
   const size_t R = (size_t)(L.E + 255) / 256;
   unsigned char* p = (unsigned char*)base;
   DecodeSync S{};
+  S.spin = kDefaultSpinLimit;
   S.zt = (uint64_t*)p;
   p += align256z((256 * R + 64) * 8 * (P.xs ? P.xs_nx : 1));
   if (P.xs) {
@@ -1561,16 +1578,22 @@ hipError_t probe_xcd_map(int num_cus, int* nx) {
   if (e == hipSuccess) e = hipMemcpy(h.data(), d, sizeof(unsigned) * num_cus, hipMemcpyDeviceToHost);
   (void)hipFree(d);
   if (e != hipSuccess) return e;
-  unsigned mx = 0;
-  for (unsigned v : h) mx = v > mx ? v : mx;
-  const int n = (int)mx + 1;
-  if (num_cus % n != 0) return hipSuccess;
-  // a rotation: workgroup b on XCD (b + r) % n for one r
-  const unsigned r = (h[0] + (unsigned)n) % (unsigned)n;
-  for (int b = 0; b < num_cus; ++b)
-    if (h[b] != (unsigned)((b + (int)r) % n)) return hipSuccess;  // no sliced form
-  *nx = n;
+  *nx = xcd_rotation(h.data(), num_cus);
   return hipSuccess;
+}
+
+int xcd_rotation(const unsigned* xcd, int nwg) {
+  if (!xcd || nwg <= 0) return 0;
+  unsigned mx = 0;
+  for (int b = 0; b < nwg; ++b) mx = xcd[b] > mx ? xcd[b] : mx;
+  if (mx >= 64) return 0;  // not an XCD number
+  const int n = (int)mx + 1;
+  if (nwg % n != 0) return 0;
+  // a rotation: workgroup b on XCD (b + r) % n for the one r of workgroup 0
+  const unsigned r = xcd[0];
+  for (int b = 0; b < nwg; ++b)
+    if (xcd[b] != (unsigned)((b + (int)r) % n)) return 0;
+  return n;
 }
 
 }  // namespace dm

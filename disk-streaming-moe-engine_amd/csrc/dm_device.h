@@ -207,10 +207,11 @@ __device__ __forceinline__ float key2f(uint32_t k) {
   return u2f((k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k);
 }
 
-// Polls between kernels' workgroups are bounded: about one second at the
-// limit, then the caller records a sync error and goes on, so that the grid
-// always drains.
-constexpr long kSpinLimit = 1l << 20;
+// Polls between kernels' workgroups are bounded (kDefaultSpinLimit polls
+// unless the context sets another bound), then the caller records a sync
+// error and goes on, so that the grid always drains.  The bound is a launch
+// argument: a context can lower it so that waits give up early (the tests of
+// the time-out path).
 
 // The softmax normaliser, summed sequentially in expert order
 // (src/layers/router.mojo:160-170), read from LDS in batches of 64 values.
@@ -411,13 +412,13 @@ __device__ __forceinline__ bool logits_ready(const uint64_t (&v)[4 * R + 1], uns
 // l holds experts l + 64 i (coalesced loads); lane 0 also the shared-gate
 // logit (entry E) when gl is given.  One poll in flight at a time: loads
 // left in flight would stall the first later reuse of their registers.
-// Returns false on a timeout.
+// Returns false after lim polls.
 template <int R>
 __device__ __forceinline__ bool poll_logits(const uint64_t* zt, unsigned tag, int E, float (&z)[4 * R],
-                                            float* gl) {
+                                            float* gl, long lim) {
   const bool gate = gl != nullptr;
   uint64_t v[4 * R + 1];
-  for (long spin = 0; spin < kSpinLimit; ++spin) {
+  for (long spin = 0; spin < lim; ++spin) {
     issue_logits<R>(zt, E, gate, v);
     if (logits_ready<R>(v, tag, E, gate, z, gl)) return true;
     __builtin_amdgcn_s_sleep(1);

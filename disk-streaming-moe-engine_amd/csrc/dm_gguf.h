@@ -81,7 +81,7 @@ int gguf_experts_occupancy(const GgufMoeDev& L, int* per_cu);
 hipError_t launch_gguf_one_token(const GgufMoeDev& L, const float* x, const float* residual,
                                  float* y, int32_t* ids, float* probs, float* shg, void* sync,
                                  unsigned launch, int grid, unsigned long long* status,
-                                 hipStream_t st);
+                                 hipStream_t st, long spin);
 
 // GGUFTensorInfo (gguf.mojo:104-114); offset is relative to the data section.
 struct GgufTensor {

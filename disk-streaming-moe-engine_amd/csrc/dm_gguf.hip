@@ -546,10 +546,10 @@ __device__ __forceinline__ void router_task(const GgufMoeDev& L, const float* __
 template <int R>
 __device__ __forceinline__ void select_task(const GgufMoeDev& L, const uint64_t* zt,
                                             unsigned launch, uint64_t* sel, float* scr,
-                                            unsigned long long* status) {
+                                            unsigned long long* status, long lim) {
   const int lane = threadIdx.x & 63, E = L.E, K = L.K;
   float z[4 * R];
-  if (!poll_logits<R>(zt, launch, E, z, nullptr) && lane == 0)
+  if (!poll_logits<R>(zt, launch, E, z, nullptr, lim) && lane == 0)
     record_err(status, err_key(kPhSync, 0, 0, 0, 0));
   uint32_t fk[4 * R];
   int myid = 0;
@@ -601,10 +601,10 @@ __device__ __forceinline__ void select_task(const GgufMoeDev& L, const uint64_t*
 template <int R>
 __device__ __forceinline__ void softmax_task(const GgufMoeDev& L, const uint64_t* zt,
                                              unsigned launch, uint64_t* soft, float* scr,
-                                             unsigned long long* status) {
+                                             unsigned long long* status, long lim) {
   const int lane = threadIdx.x & 63, E = L.E;
   float z[4 * R], gl = 0.0f;
-  if (!poll_logits<R>(zt, launch, E, z, &gl) && lane == 0)
+  if (!poll_logits<R>(zt, launch, E, z, &gl, lim) && lane == 0)
     record_err(status, err_key(kPhSync, 0, 0, 0, 0));
   float m = -__builtin_inff();
 #pragma unroll
@@ -683,8 +683,8 @@ __global__ void k_chain_router(const float* __restrict__ router, const float* __
 // records a sync error and returns false, so that the caller skips later
 // waits and the grid drains.
 __device__ __forceinline__ bool wait_count(const unsigned* c, unsigned target,
-                                           unsigned long long* status) {
-  for (long i = 0; i < kSpinLimit; ++i) {
+                                           unsigned long long* status, long lim) {
+  for (long i = 0; i < lim; ++i) {
     const unsigned v =
         __hip_atomic_load(const_cast<unsigned*>(c), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if ((int)(v - target) >= 0) return true;
@@ -782,7 +782,7 @@ __global__ __launch_bounds__(512) void k_gguf_one(
     uint64_t* soft, uint64_t* hsh, const float* __restrict__ residual, float* __restrict__ y,
     int32_t* __restrict__ ids, float* __restrict__ probs, float* __restrict__ shg,
     float* __restrict__ h, int ldh, unsigned* hcnt, unsigned target, unsigned launch,
-    unsigned long long* status) {
+    unsigned long long* status, long lim) {
   __shared__ __attribute__((aligned(16))) float xt[16 * kChainS];
   __shared__ __attribute__((aligned(16))) float scr[1056];
   __shared__ float part[8][33];
@@ -797,8 +797,8 @@ __global__ __launch_bounds__(512) void k_gguf_one(
   if (wid == 0) {
     if (b < nR) router_task(L, x, b, zt, launch, xt, status);
   } else if (wid == 1) {
-    if (b == 0) select_task<R>(L, zt, launch, sel, scr, status);
-    if (b == 1) softmax_task<R>(L, zt, launch, soft, scr, status);
+    if (b == 0) select_task<R>(L, zt, launch, sel, scr, status, lim);
+    if (b == 1) softmax_task<R>(L, zt, launch, soft, scr, status, lim);
   } else if (6 * b + wid - 2 < Ish) {
     shared_row_task<T>(L, x, 6 * b + wid - 2, hsh, launch, status);
   }
@@ -809,7 +809,7 @@ __global__ __launch_bounds__(512) void k_gguf_one(
   __shared__ int sel_ids[8];
   if (wid == 0) {
     uint32_t sv = 0;
-    if (!poll_words(sel, K, launch, kSpinLimit, sv) && lane == 0)
+    if (!poll_words(sel, K, launch, lim, sv) && lane == 0)
       record_err(status, err_key(kPhSync, 0, 0, 0, 0));
     if (lane < K) sel_ids[lane] = min(max((int)sv, 0), E - 1);
   }
@@ -842,7 +842,7 @@ __global__ __launch_bounds__(512) void k_gguf_one(
     side_done = true;
     if (wid == 0) {
       f32x4 hv[2];
-      if (!poll8(hsh + cs, launch, kSpinLimit, hv) && lane == 0)
+      if (!poll8(hsh + cs, launch, lim, hv) && lane == 0)
         record_err(status, err_key(kPhSync, 0, 0, 0, 0));
       if (lane * 8 < Ish) {
         *reinterpret_cast<f32x4*>(hshl + lane * 8) = hv[0];
@@ -851,7 +851,7 @@ __global__ __launch_bounds__(512) void k_gguf_one(
     }
     if (wid == kSoftWave) {
       uint32_t tv = 0;
-      if (!poll_words(soft, 3, launch, kSpinLimit, tv) && lane == 0)
+      if (!poll_words(soft, 3, launch, lim, tv) && lane == 0)
         record_err(status, err_key(kPhSync, 0, 0, 0, 0));
       const float sm_max = u2f((uint32_t)__builtin_amdgcn_readlane((int)tv, 0));
       const float sm_inv = u2f((uint32_t)__builtin_amdgcn_readlane((int)tv, 1));
@@ -987,7 +987,7 @@ __global__ __launch_bounds__(512) void k_gguf_one(
       }
     }
     if (w < K) {
-      if (!ready) ready = wait_count(hcnt + 16 * w, target, status);
+      if (!ready) ready = wait_count(hcnt + 16 * w, target, status, lim);
       f32x4 hv[2];
       const float* hp = h + (size_t)w * ldh + cr;
 #pragma unroll
@@ -1161,7 +1161,7 @@ int gguf_experts_occupancy(const GgufMoeDev& L, int* per_cu) {
 hipError_t launch_gguf_one_token(const GgufMoeDev& L, const float* x, const float* residual,
                                  float* y, int32_t* ids, float* probs, float* shg, void* sync,
                                  unsigned launch, int grid, unsigned long long* status,
-                                 hipStream_t st) {
+                                 hipStream_t st, long spin) {
   const int nR = (L.E + 1 + kFrontRows - 1) / kFrontRows;
   if (!gguf_one_token_supported(L) || !L.rchain || !gguf_one_token_grid_ok(L, grid) ||
       launch == 0)
@@ -1176,7 +1176,7 @@ hipError_t launch_gguf_one_token(const GgufMoeDev& L, const float* x, const floa
   const unsigned target = launch * (unsigned)(L.I / 16);  // blocks per slot
 #define DM_ONE(TY, R)                                                                          \
   k_gguf_one<TY, R><<<grid, 512, 0, st>>>(L, x, nR, zt, sel, soft, hsh, residual, y, ids, probs, \
-                                          shg, h, L.I, hcnt, target, launch, status)
+                                          shg, h, L.I, hcnt, target, launch, status, spin)
 #define DM_ONE_R(TY)    \
   if (L.E <= 256) {     \
     DM_ONE(TY, 1);      \

@@ -84,15 +84,18 @@ struct NormSpec {
 // ---- first-error keys ------------------------------------------------------
 // Every check in the kernels that would raise in the reference records a
 // 64-bit key with an integer atomicMin; the smallest key is the error the
-// reference would have raised first.  Its checks run: activation scan, router
+// reference would have raised first.  A sync key (a bounded wait that gave
+// up) sorts before all of them: the launch's outputs are then not valid and
+// no other key of it can be trusted.  Its checks run: activation scan, router
 // weight scan, logits (token, expert), softmax per token (max, exp per
 // expert, sum), top-k per token, routed experts per (token, k) with rows j
 // (gate, up, product) then outputs d, the shared expert per token, the shared
 // gate per token, and the aggregation per (token, d).
 //   [63:60] phase  [59:40] token  [39:32] slot  [31:4] pos  [3:0] kind
 enum : uint32_t {
-  kPhX = 0, kPhRouterW = 1, kPhLogit = 2, kPhSoftmax = 3, kPhTopk = 4,
-  kPhExpert = 5, kPhShared = 6, kPhGate = 7, kPhAgg = 8, kPhSync = 15,
+  kPhSync = 0,  // a wait between workgroups gave up: the outputs are not valid
+  kPhX = 1, kPhRouterW = 2, kPhLogit = 3, kPhSoftmax = 4, kPhTopk = 5,
+  kPhExpert = 6, kPhShared = 7, kPhGate = 8, kPhAgg = 9,
 };
 enum : uint32_t {  // kinds
   kTkSum = 0, kTkLeak = 1,                          // top-k
@@ -102,6 +105,11 @@ enum : uint32_t {  // kinds
   kGkLogit = 0, kGkRange = 1,                       // shared gate
 };
 constexpr uint64_t kNoError = ~0ull;
+
+// Every wait of a persistent kernel on another workgroup's word is bounded:
+// this many polls (each followed by s_sleep 1, about one second in all) by
+// default, then a sync error is recorded and the wait ends.
+constexpr long kDefaultSpinLimit = 1l << 20;
 
 DM_HD uint64_t err_key(uint32_t phase, uint32_t token, uint32_t slot, uint32_t pos,
                        uint32_t kind) {

@@ -34,6 +34,7 @@ EXPORTS = (
     "dmh_gguf_read", "dmh_dequant_gguf", "dmh_gguf_stream_tensor_f32",
     "dmh_upload_moe_layer_gguf", "dmh_free_layer_gguf", "dmh_moe_forward_gguf",
     "dmh_set_layer_norm", "dmh_port_moe_forward", "dmh_moe_forward_noalloc",
+    "dmh_set_spin_limit", "dmh_sync_fallbacks", "dmh_xcd_rotation",
 )
 
 
@@ -103,6 +104,9 @@ def lib():
     L.dmh_get_stream.argtypes = [vp]
     L.dmh_get_stream.restype = vp
     L.dmh_sync.argtypes = [vp, C.c_char_p, sz]
+    L.dmh_set_spin_limit.argtypes = [vp, i64]
+    L.dmh_sync_fallbacks.argtypes = [vp, C.POINTER(C.c_int64)]
+    L.dmh_xcd_rotation.argtypes = [vp, i32]
     L.dmh_upload_moe_layer.argtypes = [vp, i32, C.POINTER(DmhDims), C.POINTER(DmhWeights), u32,
                                        C.c_char_p, sz]
     L.dmh_free_layer.argtypes = [vp, i32]

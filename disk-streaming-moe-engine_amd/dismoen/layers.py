@@ -119,6 +119,22 @@ class MoEBlock:
         e = errbuf()
         check(self._lib.dmh_sync(self._h, e, len(e)), e)
 
+    def set_spin_limit(self, polls: int | None) -> None:
+        """Bound of every wait between the workgroups of the single-token
+        kernels (None: the default, 2^20 polls; 0: every wait gives up)."""
+        rc = self._lib.dmh_set_spin_limit(self._h, -1 if polls is None else int(polls))
+        if rc:
+            raise DismoenError(rc, "dmh_set_spin_limit failed")
+
+    def sync_fallbacks(self) -> int:
+        """Host-pointer calls rerun on the multi-kernel path after a wait
+        of a single-token kernel gave up."""
+        n = C.c_int64()
+        rc = self._lib.dmh_sync_fallbacks(self._h, C.byref(n))
+        if rc:
+            raise DismoenError(rc, "dmh_sync_fallbacks failed")
+        return int(n.value)
+
     # -- weights ---------------------------------------------------------
     def upload_layer(self, layer_idx: int, L, norm_topk_prob: bool = False) -> None:
         """Upload a layer given in the reference 4-bit layout (dismoen.synth.MoELayerQ4

@@ -119,6 +119,29 @@ void* dmh_get_stream(dmh_ctx* ctx);
  * the last dmh_sync (DMH_F_DEVICE calls), then clear it. */
 int dmh_sync(dmh_ctx* ctx, char* err, size_t errlen);
 
+/* The single-token kernels run all their workgroups at once and pass data
+ * between them through polled words; every such wait gives up after a bound
+ * of polls (default 2^20, about one second) and records a sync error.  A
+ * host-pointer call whose wait gave up (another process's kernels held CUs
+ * the grid needed) restarts the layer's tags and reruns the call on the
+ * multi-kernel path, which has no such waits; DMH_F_DEVICE calls report the
+ * error at dmh_sync.  dmh_set_spin_limit sets the bound: polls >= 0 polls
+ * (0: every wait gives up at once, for tests of this path), polls < 0 the
+ * default.  dmh_sync_fallbacks reports how many host-pointer calls of the
+ * context were rerun this way.  No counterpart in the reference (its block
+ * runs on CPU threads that do not wait on each other this way). */
+int dmh_set_spin_limit(dmh_ctx* ctx, int64_t polls);
+int dmh_sync_fallbacks(dmh_ctx* ctx, int64_t* count);
+
+/* The decision the library makes once per device at dmh_create: given the
+ * XCD each workgroup of a one-workgroup-per-CU launch ran on
+ * (xcd_of_workgroup[b], read from the hardware), the XCD count n when
+ * workgroup b ran on XCD (b + r) % n for a single r and n divides
+ * num_workgroups (the dispatcher's rotation the XCD-sliced decode kernel
+ * relies on), else 0 (that kernel form is not used).  No counterpart in the
+ * reference (a host-side diagnostic of the gfx950 launch geometry). */
+int dmh_xcd_rotation(const uint32_t* xcd_of_workgroup, int num_workgroups);
+
 /* Upload one layer once into HBM, re-tiled for the gfx950 kernels and
  * validated (reserved code 0x8, fp16 scale NaN/Inf or <= 0: the checks of
  * src/quant/dequant_kernel.mojo:68-108; non-finite router weights: the scan
@@ -161,9 +184,13 @@ int dmh_moe_forward(dmh_ctx* ctx, int layer, const float* x, const float* residu
  * array per device that the library holds until the process ends; a call
  * that needs more (about 80 tokens at the Qwen3.6 layer shape) fails with
  * DMH_ERR_INVALID_ARG and changes nothing.  All calls on a device share its
- * array, which keeps the last call's contents: calls that overlap on one
- * device (several streams or contexts) race and must be serialised by the
- * caller.  Outputs equal dmh_moe_forward's bit for bit. */
+ * array, which keeps the last call's contents, so the library puts them in
+ * one order: each call's stream waits for an event the device's previous
+ * call (from any context or stream) recorded after its kernels.  A call made
+ * while its stream is captured into a HIP graph is not chained that way (a
+ * capture cannot wait on outside work): replays of such a graph must not
+ * overlap other calls of this entry point on the device.  Outputs equal
+ * dmh_moe_forward's bit for bit. */
 int dmh_moe_forward_noalloc(dmh_ctx* ctx, int layer, const float* x, const float* residual,
                             int seq_len, float* y, int32_t* ids, float* probs,
                             float* shared_gate, unsigned flags, char* err, size_t errlen);

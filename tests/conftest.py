@@ -33,6 +33,23 @@ def block():
     b.close()
 
 
+def f10(ref, cand):
+    """The reference's F10 metrics of a candidate against a reference output
+    (tools/dismoen-tools/src/compare.rs:648-700: delta_max = max |c - r|,
+    epsilon_rel = sqrt(sum (c - r)^2 / sum r^2), float64) and its G-M3-1 gate
+    for MoE-layer outputs (compare.rs:1041-1043: delta_max <= 1e-3 and
+    epsilon_rel <= 1e-4)."""
+    import numpy as np
+    r = np.asarray(ref, dtype=np.float64).reshape(-1)
+    c = np.asarray(cand, dtype=np.float64).reshape(-1)
+    assert r.size == c.size and r.size > 0
+    assert np.isfinite(r).all() and np.isfinite(c).all()
+    d = np.abs(c - r)
+    dmax = float(d.max())
+    eps = float(np.sqrt(np.sum(d * d) / np.sum(r * r))) if np.any(r) else 0.0
+    return dmax, eps, dmax <= 1e-3 and eps <= 1e-4
+
+
 def tol_check(y, ref, factor=1e-3):
     """The parity bar: max-abs-err <= factor * RMS(ref) on the no-residual output."""
     import numpy as np

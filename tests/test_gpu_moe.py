@@ -6,7 +6,7 @@ output within max-abs-err <= 1e-3 x RMS(oracle output)."""
 import numpy as np
 import pytest
 
-from conftest import tol_check
+from conftest import f10, tol_check
 from dismoen import DismoenError, synth
 
 pytestmark = pytest.mark.gpu
@@ -67,6 +67,22 @@ def test_qwen_layer_decode_tokens(block, oracle, qwen):
     x = synth.make_activations(np.random.default_rng(103), (6, 2048))
     for t in range(6):
         check_layer(block, oracle, qwen, 1, x[t:t + 1])
+
+
+@pytest.mark.parametrize("T", [1, 8, 32])
+def test_qwen_layer_f10_gate(block, oracle, qwen, T):
+    """The reference's own MoE-layer comparison gate G-M3-1 (delta_max <= 1e-3,
+    epsilon_rel <= 1e-4 over the whole output, compare.rs:1041-1043) on the
+    decode kernel (16 single-token calls) and the grouped path (8 and 32
+    tokens per call)."""
+    x = synth.make_activations(np.random.default_rng(105 + T), (16 if T == 1 else T, 2048))
+    if T == 1:
+        y = np.concatenate([block.forward_arrays(1, x[t:t + 1], 1)[0] for t in range(16)])
+    else:
+        y = block.forward_arrays(1, x, T)[0]
+    yo = oracle.moe_layer_q4(qwen, x, x.shape[0])[0]
+    dmax, eps, ok = f10(yo, y)
+    assert ok, (dmax, eps)
 
 
 def test_deterministic_run_to_run(block, qwen):

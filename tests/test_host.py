@@ -53,3 +53,14 @@ def test_algorithmic_bytes():
     # 9 experts x 1 769 472 B + router 1 MiB + shared gate 4 KiB + x, y fp32
     b = synth.algorithmic_bytes_per_token(2048, 256, 8, 512, 512)
     assert b == 9 * 1769472 + 1048576 + 4096 + 8192 + 8192
+
+
+def test_f10_metrics_known_values():
+    """The F10 helper on values whose metrics are known in closed form
+    (compare.rs:648-700): ref (3, 4) has norm 5."""
+    from conftest import f10
+    dmax, eps, ok = f10([3.0, 4.0], [3.0, 4.0 + 2.0 ** -10])
+    assert dmax == 2.0 ** -10 and abs(eps - 2.0 ** -10 / 5.0) < 1e-18 and not ok
+    dmax, eps, ok = f10([3.0, 4.0], [3.0 + 2.0 ** -20, 4.0])
+    assert dmax == 2.0 ** -20 and ok
+    assert f10([1.0, -2.0], [1.0, -2.0]) == (0.0, 0.0, True)

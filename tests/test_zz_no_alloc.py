@@ -1,8 +1,12 @@
 """dmh_moe_forward_noalloc: the MoE block with every buffer of the call in the
 library's per-device static scratch (no allocation).  Checked through the C
 ABI against dmh_moe_forward on the same device buffers, on consecutive calls
-whose second input is smaller, single-token and several-token paths, with
-and without caller-provided routing outputs."""
+whose second input is smaller: the single-token path, the small-batch front
+end (T < 64), the split + matrix-core router path (T >= 64), with and without
+caller-provided routing outputs; two contexts calling it from two threads at
+once (the library orders the calls on the device's scratch); and the call
+captured into a HIP graph (the multi-kernel path) and replayed on fresh
+inputs with eager work between the replays."""
 import ctypes as C
 
 import numpy as np
@@ -41,7 +45,7 @@ def _call(fn, block, layer, xd, T, b, residual=None, with_routing=True):
     block.sync()
 
 
-@pytest.mark.parametrize("sizes", [(32, 8), (5, 1), (1, 1)])
+@pytest.mark.parametrize("sizes", [(32, 8), (5, 1), (1, 1), (72, 8)])
 def test_noalloc_matches_moe_forward(block, oracle, qwen_na, sizes):
     import torch
     L = lib()
@@ -95,3 +99,106 @@ def test_noalloc_rejects_what_it_cannot_do_without_allocating(block, qwen_na):
     rc = L.dmh_moe_forward_noalloc(block.handle, 90, xd.data_ptr(), None, T, yd.data_ptr(), None,
                                    None, None, DMH_F_DEVICE, e, len(e))
     assert rc == 1 and b"bytes of scratch, more than the" in e.value, e.value
+
+
+def test_noalloc_two_contexts_from_two_threads(block, oracle, qwen_na):
+    """Both contexts' calls share the device's scratch; the library orders
+    them on the device, so every output equals its context's
+    dmh_moe_forward result bit for bit."""
+    import threading
+
+    import torch
+    from dismoen import MoEBlock
+    L = lib()
+    T, N = 8, 6
+    rng = np.random.default_rng(920)
+    other = MoEBlock(0)
+    try:
+        other.upload_layer(90, qwen_na)
+        ctxs = (block, other)
+        xs = [[torch.from_numpy(synth.make_activations(rng, (T, 2048))).to("cuda")
+               for _ in range(N)] for _ in ctxs]
+        torch.cuda.synchronize()
+        refs = [[_bufs(T) for _ in range(N)] for _ in ctxs]
+        for c, blk in enumerate(ctxs):
+            for i in range(N):
+                _call(L.dmh_moe_forward, blk, 90, xs[c][i], T, refs[c][i])
+        outs = [[_bufs(T) for _ in range(N)] for _ in ctxs]
+        torch.cuda.synchronize()
+        errs = []
+
+        def run(c):
+            blk = ctxs[c]
+            for i in range(N):
+                e = errbuf()
+                b = outs[c][i]
+                rc = L.dmh_moe_forward_noalloc(blk.handle, 90, xs[c][i].data_ptr(), None, T,
+                                               b["y"].data_ptr(), b["ids"].data_ptr(),
+                                               b["probs"].data_ptr(), b["shg"].data_ptr(),
+                                               DMH_F_DEVICE, e, len(e))
+                if rc:
+                    errs.append(e.value)
+
+        th = [threading.Thread(target=run, args=(c,)) for c in range(2)]
+        for t in th:
+            t.start()
+        for t in th:
+            t.join()
+        assert not errs, errs
+        for blk in ctxs:
+            blk.sync()
+        for c in range(2):
+            for i in range(N):
+                for k in ("ids", "probs", "shg", "y"):
+                    assert np.array_equal(outs[c][i][k].cpu().numpy().view(np.uint8),
+                                          refs[c][i][k].cpu().numpy().view(np.uint8)), (c, i, k)
+    finally:
+        other.close()
+
+
+@pytest.mark.parametrize("T", [1, 8])
+def test_noalloc_captured_in_a_graph(block, oracle, qwen_na, T):
+    """Captured once, replayed on three fresh inputs with eager calls and
+    synchronisations between the replays; every replay against the oracle
+    (ids, probabilities and shared gate bit for bit, y within the bar) and
+    against an eager call of dmh_moe_forward on the same input."""
+    import torch
+    L = lib()
+    rng = np.random.default_rng(930 + T)
+    xs = torch.zeros((T, 2048), dtype=torch.float32, device="cuda")
+    b = _bufs(T)
+    s = torch.cuda.Stream()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    block.set_stream(s.cuda_stream)
+    try:
+        e = errbuf()
+        with torch.cuda.graph(g, stream=s):
+            rc = L.dmh_moe_forward_noalloc(block.handle, 90, xs.data_ptr(), None, T,
+                                           b["y"].data_ptr(), b["ids"].data_ptr(),
+                                           b["probs"].data_ptr(), b["shg"].data_ptr(),
+                                           DMH_F_DEVICE, e, len(e))
+        assert rc == 0, e.value
+    finally:
+        block.set_stream(None)
+    block.sync()
+    for r in range(3):
+        x = synth.make_activations(rng, (T, 2048))
+        xs.copy_(torch.from_numpy(x).to("cuda"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        got = {k: v.cpu().numpy().copy() for k, v in b.items()}
+        # eager work between replays: the same input through dmh_moe_forward
+        ref = _bufs(T)
+        _call(L.dmh_moe_forward, block, 90, xs, T, ref)
+        for k in ("ids", "probs", "shg"):
+            assert np.array_equal(got[k].view(np.uint8), ref[k].cpu().numpy().view(np.uint8)), (r, k)
+        yo, ido, po, so = oracle.moe_layer_q4(qwen_na, x, T)
+        assert np.array_equal(got["ids"], ido), r
+        assert np.array_equal(got["probs"].view(np.uint32), po.view(np.uint32)), r
+        err, rms, ok = tol_check(got["y"], yo)
+        assert ok, (r, err, rms)
+        if T > 1:  # the same grouped path eagerly: the same bits
+            assert np.array_equal(got["y"].view(np.uint8), ref["y"].cpu().numpy().view(np.uint8))
+    del g
