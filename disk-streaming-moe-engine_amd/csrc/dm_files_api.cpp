@@ -192,6 +192,11 @@ int dmh_upload_moe_layer_files(dmh_ctx* ctx, int layer, const dmh_moe_dims* d,
                                char* err, size_t errlen) {
   if (!d || !qf || !sf)
     return put_err(err, errlen, DMH_ERR_INVALID_ARG, "dmh_upload_moe_layer_files: NULL argument");
+  // group_size 0: the quant model's own, quantization.group_size of its
+  // header (docs/format/quant_format.md:76,212)
+  dmh_moe_dims dd = *d;
+  if (dd.group_size == 0) dd.group_size = qf->f.group_size;
+  d = &dd;
   // the dims are checked before any size arithmetic (a zero or negative
   // group size would divide by zero below) and nothing throws across the ABI
   const int rc = dm::api_moe_dims_check(d, layer, err, errlen);

@@ -171,7 +171,8 @@ class MoEBlock:
                            model_layer: int = 0, group_size: int = 32) -> None:
         """Upload model layer model_layer from a quant model and a safetensors
         shard (dismoen.formats.QuantModelIndex / SafetensorsShard); group_size is
-        the group size of the quant model's expert tensors (32, 64, 128 or 256)."""
+        the group size of the quant model's expert tensors (32, 64, 128 or 256;
+        0: quantization.group_size of the quant model's header)."""
         H, E, K, I, Ish = dims
         d = DmhDims(H, E, K, I, Ish, group_size, 0)
         e = errbuf()

@@ -322,7 +322,9 @@ int dmh_st_read(const dmh_st_file* f, int idx, void* out, int64_t bytes, char* e
  * quant model (src/layers/quant_loader.mojo:89-136); the router mlp.gate.weight
  * (language-model prefix first, src/layers/router.mojo:234-247) and
  * mlp.shared_expert_gate.weight as BF16 from the safetensors shard, the
- * shared gate falling back to the quant model's 4-bit tensor. */
+ * shared gate falling back to the quant model's 4-bit tensor.
+ * dims->group_size 0 takes the quant model's own group size,
+ * quantization.group_size of its header (docs/format/quant_format.md:76). */
 int dmh_upload_moe_layer_files(dmh_ctx* ctx, int layer, const dmh_moe_dims* dims,
                                const dmh_quant_file* quant, const dmh_st_file* shard,
                                int model_layer, char* err, size_t errlen);

@@ -213,12 +213,13 @@ def test_written_layer_reads_back(tmp_path):
         assert np.array_equal(np.frombuffer(r, "<u2"), L.router_bf16)
 
 
-@pytest.mark.parametrize("G", [0, -1, 48])
+@pytest.mark.parametrize("G", [-1, 48, 512])
 def test_file_upload_rejects_group_size_before_reading(tmp_path, G):
     """dmh_upload_moe_layer_files checks the dims (group size in {32, 64,
-    128, 256}) before any arithmetic or allocation on them: a zero or
-    negative group size is a CONFIG_ERROR, not a division by zero, and no
-    device is needed to reach the check."""
+    128, 256}) before any arithmetic or allocation on them: a negative or
+    unsupported group size is a CONFIG_ERROR, not a division by zero, and no
+    device is needed to reach the check.  Group size 0 takes the quant
+    model's header value instead (below)."""
     import ctypes as C
     from dismoen._lib import DmhDims, lib
     c = synth.CONFIG_TOY
@@ -232,3 +233,21 @@ def test_file_upload_rejects_group_size_before_reading(tmp_path, G):
                                               len(e))
     assert rc == 2, e.value
     assert b'"error_type":"CONFIG_ERROR"' in e.value and b"G=%d" % G in e.value
+
+
+def test_file_upload_group_size_zero_takes_the_header(tmp_path):
+    """Group size 0 in the dims means quantization.group_size of the quant
+    model's header (docs/format/quant_format.md:76): the dims check passes
+    (the header says 32), and the call goes on to the context check."""
+    import ctypes as C
+    from dismoen._lib import DmhDims, lib
+    c = synth.CONFIG_TOY
+    L = synth.make_layer(**c, seed=71)
+    qp, sp = str(tmp_path / "m.quant"), str(tmp_path / "m.safetensors")
+    formats.write_layer_files(qp, sp, L, model_layer=0)
+    d = DmhDims(c["hidden"], c["num_experts"], c["top_k"], c["inter"], c["inter_sh"], 0, 0)
+    e = C.create_string_buffer(1024)
+    with formats.scan_quant_file(qp) as q, formats.read_header(sp) as s:
+        rc = lib().dmh_upload_moe_layer_files(None, 0, C.byref(d), q.handle, s.handle, 0, e,
+                                              len(e))
+    assert rc == 1 and b"NULL context" in e.value, e.value

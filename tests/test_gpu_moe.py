@@ -340,3 +340,42 @@ def test_two_contexts_on_one_device(block, oracle, qwen):
             assert ok, (err, rms)
     # back to one context: the plain launch
     check_layer(block, oracle, qwen, 1, x[:1])
+
+
+def test_two_contexts_from_two_threads_at_once(block, oracle, qwen):
+    """Two contexts on one device, each driven by its own host thread at the
+    same time (single-token host-pointer calls: cooperative launches of the
+    fused decode kernel, which the runtime admits one grid at a time): every
+    token of both matches the oracle."""
+    import threading
+
+    from dismoen import MoEBlock
+    N = 24
+    xs = synth.make_activations(np.random.default_rng(114), (2, N, 2048))
+    outs = [[None] * N, [None] * N]
+    errs = []
+    with MoEBlock(0) as other:
+        other.upload_layer(1, qwen)
+        ctxs = (block, other)
+
+        def run(c):
+            try:
+                for t in range(N):
+                    outs[c][t] = ctxs[c].forward_arrays(1, xs[c, t:t + 1], 1)
+            except Exception as e:  # reported below, on the main thread
+                errs.append(repr(e))
+
+        th = [threading.Thread(target=run, args=(c,)) for c in range(2)]
+        for t in th:
+            t.start()
+        for t in th:
+            t.join()
+    assert not errs, errs
+    for c in range(2):
+        yo, ido, po, so = oracle.moe_layer_q4(qwen, xs[c], N)
+        for t in range(N):
+            y, ids, probs, shg = outs[c][t]
+            assert np.array_equal(ids[0], ido[t]), (c, t)
+            assert np.array_equal(probs[0].view(np.uint32), po[t].view(np.uint32)), (c, t)
+            err, rms, ok = tol_check(y[0], yo[t])
+            assert ok, (c, t, err, rms)

@@ -47,13 +47,15 @@ def test_qwen_layer_g128_arrays_and_files_vs_oracle(block, oracle, tmp_path):
     formats.write_layer_files(qp, sp, L, model_layer=3)
     with formats.scan_quant_file(qp) as q, formats.read_header(sp) as s:
         block.upload_layer_files(62, dims, q, s, model_layer=3, group_size=128)
+        # group size 0: the quant model's header's quantization.group_size
+        block.upload_layer_files(64, dims, q, s, model_layer=3, group_size=0)
     x = synth.make_activations(np.random.default_rng(610), (3, c["hidden"]))
-    for layer in (61, 62):
+    for layer in (61, 62, 64):
         for t in range(2):
             _check(block, oracle, L, layer, x[t:t + 1])
         _check(block, oracle, L, layer, x)
-    block.free_layer(61)
-    block.free_layer(62)
+    for layer in (61, 62, 64):
+        block.free_layer(layer)
 
 
 def test_toy_layer_g32_files_vs_oracle(block, oracle, tmp_path):
