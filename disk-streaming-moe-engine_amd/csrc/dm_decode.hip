@@ -515,6 +515,16 @@ __device__ __forceinline__ float seq_sum_squares(const float* sq, int n) {
   return a;
 }
 
+// A workgroup barrier for data passed through LDS only.  __syncthreads()
+// is a release and acquire at workgroup scope, and its release waits for
+// every global load the wave has in flight (s_waitcnt vmcnt(0)): for waves
+// holding cold weight loads that is microseconds.  Here each wave waits only
+// for its own LDS operations, so LDS written by any wave before the barrier
+// is visible to every wave after it.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 // The same sum on one wave, every lane holding per <= kSeqPerLane of the
 // squares in registers: lane l the elements l*per .. l*per + per - 1, read
 // from sqT[i * 64 + l] = element l*per + i.  Round l adds every lane's
@@ -548,7 +558,8 @@ __device__ __forceinline__ float seq_sum_wave_rounds(const float* sqT, int per) 
 }
 
 // The block-edge norm's sum of squares of x, left in red[0] (read by every
-// thread after the final barrier).  Thread tid holds x[8i .. 8i+7] for
+// thread after the final barrier; the barriers are LDS-only, so the weight
+// loads in flight go on landing while the sum runs).  Thread tid holds x[8i .. 8i+7] for
 // i = tid, tid + kThreads in xr.  sq: H floats of LDS.
 // NORM 1: 256 strided partials and a halving tree (partial t + partial
 //   t + wd, wd = 128 .. 1, the order of or_rmsnorm_tree256); the levels
@@ -581,16 +592,16 @@ __device__ __forceinline__ void norm_sum_squares(const float4 (&xr)[2][2], int H
       }
     }
   }
-  __syncthreads();
+  lds_barrier();
   if constexpr (NORM == 1) {
     if (tid < 256) {
       float a = 0.0f;
       for (int k = tid; k < H; k += 256) a = a + sq[k];
       red[tid] = a;
     }
-    __syncthreads();
+    lds_barrier();
     if (tid < 128) red[tid] = red[tid] + red[tid + 128];
-    __syncthreads();
+    lds_barrier();
     if (tid < 64) {
       float v = red[tid] + red[tid + 64];
 #pragma unroll
@@ -605,7 +616,7 @@ __device__ __forceinline__ void norm_sum_squares(const float4 (&xr)[2][2], int H
   } else {
     if (tid == 0) red[0] = seq_sum_squares(sq, H);
   }
-  __syncthreads();
+  lds_barrier();
 }
 
 // ---------------------------------------------------------------------------
@@ -645,15 +656,20 @@ __global__ __launch_bounds__(kThreads) void k_moe_decode(
 
   // ---- entry: the router rows first (their arrival gates the logits, the
   // first hand-off), then x, then every other load that depends on neither
-  // x nor routing (a wave's loads complete in order)
+  // x nor routing (a wave's loads complete in order).  With the norm, x and
+  // gamma come first instead: the norm's sum needs them, and runs while the
+  // router rows land.
   uint4 rw[kRwMax];
   const int re = b * kRouterRows + (tid >> 4);
-  if (router_wg && tid < kRouterRows * 16) {
-    const uint4* wp =
-        reinterpret_cast<const uint4*>(L.router + r16_index(H, min(re, E), tid & 15));
+  auto load_rw = [&]() {
+    if (router_wg && tid < kRouterRows * 16) {
+      const uint4* wp =
+          reinterpret_cast<const uint4*>(L.router + r16_index(H, min(re, E), tid & 15));
 #pragma unroll
-    for (int j8 = 0; j8 < kRwMax; ++j8) rw[j8] = wp[(size_t)min(j8, H / 128 - 1) * 16];
-  }
+      for (int j8 = 0; j8 < kRwMax; ++j8) rw[j8] = wp[(size_t)min(j8, H / 128 - 1) * 16];
+    }
+  };
+  if constexpr (NORM == 0) load_rw();
   float4 xr[2][2];
 #pragma unroll
   for (int ii = 0; ii < 2; ++ii) {
@@ -669,6 +685,7 @@ __global__ __launch_bounds__(kThreads) void k_moe_decode(
       gr[ii][0] = reinterpret_cast<const float4*>(nm.gamma)[2 * i];
       gr[ii][1] = reinterpret_cast<const float4*>(nm.gamma)[2 * i + 1];
     }
+    load_rw();
   }
   const size_t matS = (size_t)L.Ish * H;
   const ExpertView sgv = {L.sgu_nib, L.sgu_sc, L.Ish, H};
@@ -699,7 +716,7 @@ __global__ __launch_bounds__(kThreads) void k_moe_decode(
       xr[ii][0] = nrm(xr[ii][0], gr[ii][0]);
       xr[ii][1] = nrm(xr[ii][1], gr[ii][1]);
     }
-    __syncthreads();  // the squares and partials are overwritten below
+    lds_barrier();  // the squares and partials are overwritten below
   }
 
   // ---- stage x: transposed fp32 (router chains) and bf16 hi/lo B blocks -----
@@ -1078,15 +1095,19 @@ __global__ __launch_bounds__(kThreads) void k_moe_decode_xs(
     return;
   }
 
-  // ---- entry: router rows, x, gamma -----------------------------------------
+  // ---- entry: router rows, x, gamma (with the norm: x, gamma, router
+  // rows, as in the original form) ---------------------------------------------
   uint4 rw[kRwMax];
   const int re = m + nmx * (4 * w + (lane >> 4));
-  if (w < nrw) {
-    const uint4* wp =
-        reinterpret_cast<const uint4*>(L.router + r16_index(H, min(re, E), lane & 15));
+  auto load_rw = [&]() {
+    if (w < nrw) {
+      const uint4* wp =
+          reinterpret_cast<const uint4*>(L.router + r16_index(H, min(re, E), lane & 15));
 #pragma unroll
-    for (int j8 = 0; j8 < kRwMax; ++j8) rw[j8] = wp[(size_t)min(j8, H / 128 - 1) * 16];
-  }
+      for (int j8 = 0; j8 < kRwMax; ++j8) rw[j8] = wp[(size_t)min(j8, H / 128 - 1) * 16];
+    }
+  };
+  if constexpr (NORM == 0) load_rw();
   float4 xr[2][2];
 #pragma unroll
   for (int ii = 0; ii < 2; ++ii) {
@@ -1102,6 +1123,7 @@ __global__ __launch_bounds__(kThreads) void k_moe_decode_xs(
       gr[ii][0] = reinterpret_cast<const float4*>(nm.gamma)[2 * i];
       gr[ii][1] = reinterpret_cast<const float4*>(nm.gamma)[2 * i + 1];
     }
+    load_rw();
   }
   const size_t matS = (size_t)L.Ish * H;
   const ExpertView sgv = {L.sgu_nib, L.sgu_sc, L.Ish, H};
@@ -1153,7 +1175,7 @@ __global__ __launch_bounds__(kThreads) void k_moe_decode_xs(
       xr[ii][0] = nrm(xr[ii][0], gr[ii][0]);
       xr[ii][1] = nrm(xr[ii][1], gr[ii][1]);
     }
-    __syncthreads();
+    lds_barrier();  // the squares and partials are overwritten below
   }
 
   // ---- stage x --------------------------------------------------------------
