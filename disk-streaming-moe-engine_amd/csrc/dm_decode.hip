@@ -515,16 +515,6 @@ __device__ __forceinline__ float seq_sum_squares(const float* sq, int n) {
   return a;
 }
 
-// A workgroup barrier for data passed through LDS only.  __syncthreads()
-// is a release and acquire at workgroup scope, and its release waits for
-// every global load the wave has in flight (s_waitcnt vmcnt(0)): for waves
-// holding cold weight loads that is microseconds.  Here each wave waits only
-// for its own LDS operations, so LDS written by any wave before the barrier
-// is visible to every wave after it.
-__device__ __forceinline__ void lds_barrier() {
-  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-}
-
 // The same sum on one wave, every lane holding per <= kSeqPerLane of the
 // squares in registers: lane l the elements l*per .. l*per + per - 1, read
 // from sqT[i * 64 + l] = element l*per + i.  Round l adds every lane's

@@ -428,6 +428,16 @@ __device__ __forceinline__ bool poll_logits(const uint64_t* zt, unsigned tag, in
 
 __device__ __forceinline__ void wait_lds() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
+// A workgroup barrier for data passed through LDS only.  __syncthreads()
+// is a release and acquire at workgroup scope, and its release waits for
+// every global load the wave has in flight (s_waitcnt vmcnt(0)): for waves
+// holding cold weight loads that is microseconds.  Here each wave waits only
+// for its own LDS operations, so LDS written by any wave before the barrier
+// is visible to every wave after it.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 // Top-K of one token's router logits on one wave, the selection step of
 // router_forward (src/layers/router.mojo:188-210 with select_topk of
 // src/layers/topk.mojo:79-128) done on the logits: lane l holds z[i] of

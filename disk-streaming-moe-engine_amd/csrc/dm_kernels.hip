@@ -359,9 +359,151 @@ __global__ __launch_bounds__(256) void k_router_dec(LayerDev L, const float* __r
   }
 }
 
+// The same logits for many tokens: each thread keeps its chain's H / 16
+// router weights (bf16, 8 per register quad) in registers for all the tokens
+// of its workgroup, instead of reading the rows again for every token, and
+// runs kRdTok tokens per pass, whose activations are staged in LDS as
+// xs[k][token] (one 16-byte read gives a step's value for every token of the
+// pass).  Each token's 16 chains are the reference's, element for element:
+// acc_l = acc_l + x[16 s + l] * w[16 s + l] in s order, multiply and add
+// rounded separately, then the halving tree, so every logit has the bits of
+// k_router_dec's.
+// NJ8 = H / 128 words of 8 steps per chain (a compile-time count: the step
+// loop is straight-line code).  The activations of 4 steps (one 16-byte
+// read per step) are read by inline assembly one group ahead of their
+// products, with a wait tied to their registers: the compiler, left to
+// itself, hoisted every read of the loop to its start and spilled.  At
+// H = 2048 the kernel holds 127 registers, so four waves share a SIMD and
+// the ~1000 workgroups of the launch run in one round.
+constexpr int kRdTok = 4;
+// the 4 steps' reads: a, a + 256, a + 512, a + 768 (steps 16 floats x 4
+// tokens apart)
+__device__ __forceinline__ void lds_read_steps4(uint32_t a, f32x4 (&v)[4]) {
+  asm volatile(
+      "ds_read_b128 %0, %4\n\tds_read_b128 %1, %4 offset:256\n\t"
+      "ds_read_b128 %2, %4 offset:512\n\tds_read_b128 %3, %4 offset:768"
+      : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3])
+      : "v"(a));
+}
+// wait until at most N LDS operations are in flight (they complete in
+// order); v's registers are tied to the wait
+template <int N>
+__device__ __forceinline__ void lds_wait_steps4(f32x4 (&v)[4]) {
+  asm volatile("s_waitcnt lgkmcnt(%4)" : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]) : "n"(N));
+}
+template <int NJ8>
+__global__ __launch_bounds__(256) void k_router_rows(
+    LayerDev L, const float* __restrict__ x, int T,
+                                                     int tpw, float* __restrict__ z,
+                                                     unsigned long long* status,
+                                                     const int* __restrict__ gate) {
+  extern __shared__ __attribute__((aligned(16))) float xs4[];  // [H][kRdTok]
+  if (gate && gate[0] == 0) return;  // uniform: k_router_mfma computed these logits
+  constexpr int H = NJ8 * 128;
+  const int l = threadIdx.x & 15;
+  const int e = blockIdx.x * 16 + (threadIdx.x >> 4);
+  const bool wave_live = blockIdx.x * 16 + (threadIdx.x >> 6) * 4 <= L.E;  // uniform per wave
+  uint4 wr[NJ8];
+  {
+    const uint4* wp = reinterpret_cast<const uint4*>(L.router + r16_index(H, min(e, L.E), l));
+#pragma unroll
+    for (int u = 0; u < NJ8; ++u) wr[u] = wp[(size_t)u * 16];
+  }
+  const int tb = blockIdx.y * tpw, te = min(T, tb + tpw);
+  static_assert(kRdTok == 4, "the float4 staging below");
+  for (int t0 = tb; t0 < te; t0 += kRdTok) {
+    const int nt = min(kRdTok, te - t0);
+    bool bad = false;
+    for (int k = threadIdx.x; k < H; k += 256) {
+      float v[kRdTok];
+#pragma unroll
+      for (int tt = 0; tt < kRdTok; ++tt) {
+        v[tt] = x[(size_t)(t0 + min(tt, nt - 1)) * H + k];
+        bad |= tt < nt && !finite_f(v[tt]);
+      }
+      *reinterpret_cast<float4*>(xs4 + (size_t)k * kRdTok) = make_float4(v[0], v[1], v[2], v[3]);
+    }
+    if (bad && blockIdx.x == 0) record_err(status, err_key(kPhX, 0, 0, 0, 0));
+    __syncthreads();
+    // a wave whose four rows are all past row E (the last block's tail)
+    // only helps to stage the activations
+    if (wave_live) {
+      float acc[kRdTok] = {0.0f, 0.0f, 0.0f, 0.0f};
+      // group c of 4 steps: steps 4c .. 4c + 3, i.e. word u = c / 2, registers
+      // i = 2 (c % 2) and i + 1 (step 8u + 2i: low half, 8u + 2i + 1: high)
+      const uint32_t xa0 = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)(
+          xs4 + (size_t)l * kRdTok);
+      f32x4 xc[4], xn[4];
+      lds_read_steps4(xa0, xc);
+#pragma unroll
+      for (int c = 0; c < 2 * NJ8; ++c) {
+        if (c + 1 < 2 * NJ8) {
+          lds_read_steps4(xa0 + (c + 1) * 4 * 256, xn);
+          lds_wait_steps4<4>(xc);
+        } else {
+          lds_wait_steps4<0>(xc);
+        }
+        const int u = c >> 1;
+        // this group's two weight words pass through an empty asm, so their
+        // conversions stay in the group (hoisted to the top of the token loop as
+        // 128 floats they did not fit in the registers)
+        uint32_t wg[2] = {(c & 1) ? wr[u].z : wr[u].x, (c & 1) ? wr[u].w : wr[u].y};
+        asm volatile("" : "+v"(wg[0]), "+v"(wg[1]));
+#pragma unroll
+        for (int i2 = 0; i2 < 2; ++i2) {
+          const f32x4 xa = xc[2 * i2], xb = xc[2 * i2 + 1];
+          const float wl = bf16lo(wg[i2]), wh = bf16hi(wg[i2]);
+          acc[0] = acc[0] + xa[0] * wl;
+          acc[1] = acc[1] + xa[1] * wl;
+          acc[2] = acc[2] + xa[2] * wl;
+          acc[3] = acc[3] + xa[3] * wl;
+          acc[0] = acc[0] + xb[0] * wh;
+          acc[1] = acc[1] + xb[1] * wh;
+          acc[2] = acc[2] + xb[2] * wh;
+          acc[3] = acc[3] + xb[3] * wh;
+        }
+        // (the four chains are complete at every group: sunk below the
+        // first token's store, the others kept every read of the pass live)
+        asm volatile("" : "+v"(acc[0]), "+v"(acc[1]), "+v"(acc[2]), "+v"(acc[3]));
+        if (c + 1 < 2 * NJ8) {
+#pragma unroll
+          for (int k = 0; k < 4; ++k) xc[k] = xn[k];
+        }
+      }
+#pragma unroll
+      for (int tt = 0; tt < kRdTok; ++tt) {
+        // halving tree over the 16 chains of a row: lane l += lane l + w
+#pragma unroll
+        for (int wdt = 8; wdt >= 1; wdt >>= 1) acc[tt] = acc[tt] + __shfl_down(acc[tt], wdt, 16);
+        if (l == 0 && e <= L.E && tt < nt) z[(size_t)(t0 + tt) * (L.E + 1) + e] = acc[tt];
+      }
+    }
+    __syncthreads();  // xs4 is restaged for the next tokens
+  }
+}
+
 hipError_t launch_router_dec(const LayerDev& L, const float* x, int T, float* z,
                              unsigned long long* status, hipStream_t st, const int* gate) {
   const int blocks = (L.E + 1 + 15) / 16;
+  const int nj8 = L.H % 128 == 0 ? L.H / 128 : 0;
+  if (T >= 2 * kRdTok && (nj8 == 2 || nj8 == 4 || nj8 == 8 || nj8 == 16)) {
+    // tokens per workgroup: a multiple of kRdTok, about 1024 workgroups
+    const int want = (1024 + blocks - 1) / blocks;
+    int tpw = (T + want - 1) / want;
+    tpw = ((tpw + kRdTok - 1) / kRdTok) * kRdTok;
+    const int ty = (T + tpw - 1) / tpw;
+    const size_t lds = (size_t)L.H * kRdTok * sizeof(float);
+    const dim3 g(blocks, ty);
+    if (nj8 == 16)
+      hipLaunchKernelGGL(k_router_rows<16>, g, dim3(256), lds, st, L, x, T, tpw, z, status, gate);
+    else if (nj8 == 8)
+      hipLaunchKernelGGL(k_router_rows<8>, g, dim3(256), lds, st, L, x, T, tpw, z, status, gate);
+    else if (nj8 == 4)
+      hipLaunchKernelGGL(k_router_rows<4>, g, dim3(256), lds, st, L, x, T, tpw, z, status, gate);
+    else
+      hipLaunchKernelGGL(k_router_rows<2>, g, dim3(256), lds, st, L, x, T, tpw, z, status, gate);
+    return hipGetLastError();
+  }
   const int ty = T < 256 ? T : 256;  // workgroups loop over the tokens beyond
   hipLaunchKernelGGL(k_router_dec, dim3(blocks, ty), dim3(256), (size_t)L.H * sizeof(float), st, L,
                      x, T, z, status, gate);

@@ -205,6 +205,25 @@ def test_fp32_prefill_301_tokens_vs_oracle(block, oracle, qwen):
         assert ok, (t, err, rms)
 
 
+@pytest.mark.parametrize("slot,shape", [
+    (20, (256, 16, 4, 128, 128)),    # 2 words per chain; one live wave in the last row block
+    (21, (512, 40, 4, 128, 128)),    # 4 words; the last block's fourth wave has no rows
+    (22, (1024, 64, 6, 256, 256)),   # 8 words
+    (23, (384, 24, 4, 128, 128)),    # 3 words: the one-token-at-a-time lane-chain kernel
+])
+@pytest.mark.parametrize("T", [9, 37])
+def test_lane_chain_router_hidden_sizes_vs_oracle(block, oracle, slot, shape, T):
+    """Activations that are not bf16 values at several hidden sizes: the
+    register-resident lane-chain router (4 tokens a pass, a ragged last
+    pass) and its one-token fallback give bit-exact ids, probabilities and
+    shared gates."""
+    H, E, K, I, Ish = shape
+    L = synth.make_layer(H, E, K, I, Ish, seed=slot)
+    block.upload_layer(slot, L)
+    x = np.random.default_rng(400 + slot + T).standard_normal((T, H)).astype(np.float32)
+    _check(block, oracle, L, slot, x)
+
+
 def test_many_tokens_toy_layer_vs_oracle(block, oracle):
     """Fewer experts than one router workgroup covers (16 < 64), hidden 256."""
     L = synth.make_layer(**synth.CONFIG_TOY, seed=8)
