@@ -195,6 +195,26 @@ __device__ __forceinline__ float dot4(f32x4 a, f32x4 b, float acc) {
   return __builtin_fmaf(a.w, b.w, acc);
 }
 
+// The 3-bit codes of sixteen Q3_K weights (qs: their 2-bit low parts, code
+// i at bits 2i; hm: their high bits, bit i) as bytes, four weights per
+// word: byte m of qw[k] = code of weight 4m + k.  A word costs a shift, a
+// mask and a merge of each part (the high bits first moved so that nibble m
+// of hm is the low nibble of byte m), where a code taken alone costs two
+// bit-field extractions and a merge; a byte then converts in one
+// instruction (v_cvt_f32_ubyte0..3).
+__device__ __forceinline__ void q3_codes(uint32_t qs, uint32_t hm, uint32_t (&qw)[4]) {
+  uint32_t t = (hm | (hm << 8)) & 0x00FF00FFu;
+  const uint32_t hs = (t | (t << 4)) & 0x0F0F0F0Fu;  // bit k of byte m = hm bit 4m + k
+  qw[0] = ((hs << 2) & 0x04040404u) | (qs & 0x03030303u);
+  qw[1] = ((hs << 1) & 0x04040404u) | ((qs >> 2) & 0x03030303u);
+  qw[2] = (hs & 0x04040404u) | ((qs >> 4) & 0x03030303u);
+  qw[3] = ((hs >> 1) & 0x04040404u) | ((qs >> 6) & 0x03030303u);
+}
+// code i of q3_codes' words as a float
+__device__ __forceinline__ float q3_code(const uint32_t (&qw)[4], int i) {
+  return (float)((qw[i & 3] >> (8 * (i >> 2))) & 0xFFu);
+}
+
 // W consecutive weights at element e0 (a multiple of W, W in {4, 8, 16}).
 // For Q3_K eight weights share one hmask byte, two code bytes, the scale
 // byte and d, so the block header is decoded once per eight (sixteen).
@@ -208,10 +228,13 @@ __device__ __forceinline__ void valuesW(const uint8_t* raw, int64_t e0, int layo
     const uint32_t hm = blk[e >> 3];
     const uint32_t qs = h[16 + (e >> 3)];  // code bytes 32 + e/4 and the next
     const float fs = (float)((int)blk[96 + (e >> 4)] - 32) * h2f(h[56]);
+    // fs (q - 4) rounded once: fma(fs, q, -4 fs), -4 fs being exact
+    const float m4 = -4.0f * fs;
+    uint32_t qw[4];
+    q3_codes(qs, hm, qw);
     float w[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
-      w[i] = fs * (float)((int)((((hm >> i) & 1) << 2) | ((qs >> (2 * i)) & 3)) - 4);
+    for (int i = 0; i < 8; ++i) w[i] = __builtin_fmaf(fs, q3_code(qw, i), m4);
     v[0] = f32x4{w[0], w[1], w[2], w[3]};
     v[1] = f32x4{w[4], w[5], w[6], w[7]};
   } else {
@@ -251,10 +274,12 @@ template <int W>
 __device__ __forceinline__ void q3_decode(const Q3Raw<W>& r, f32x4 (&v)[W / 4]) {
   const uint32_t qs = r.q0 | (r.q1 << 16);
   const float fs = (float)((int)r.sc - 32) * h2f(r.d);
+  const float m4 = -4.0f * fs;  // fs (q - 4) rounded once, as valuesW forms it
+  uint32_t qw[4];
+  q3_codes(qs, r.hm, qw);
   float w[W];
 #pragma unroll
-  for (int i = 0; i < W; ++i)
-    w[i] = fs * (float)((int)((((r.hm >> i) & 1) << 2) | ((qs >> (2 * i)) & 3)) - 4);
+  for (int i = 0; i < W; ++i) w[i] = __builtin_fmaf(fs, q3_code(qw, i), m4);
 #pragma unroll
   for (int j = 0; j < W / 4; ++j) v[j] = f32x4{w[4 * j], w[4 * j + 1], w[4 * j + 2], w[4 * j + 3]};
 }
@@ -275,17 +300,16 @@ __device__ __forceinline__ float xsum16(const f32x4 (&x)[4]) {
 // acc + sum_i w_i x_i over sixteen Q3_K weights w_i = fs (q_i - 4) of one
 // 16-weight scale group, formed as fs (sum_i q_i x_i - 4 xs) with xs =
 // xsum16(x): the 3-bit codes enter the products as they are, so a weight
-// costs two bit-field extractions, a conversion and a multiply-add.
+// costs its share of q3_codes, a conversion and a multiply-add.
 __device__ __forceinline__ float q3_dot16(const Q3Raw<16>& r, const f32x4 (&x)[4], float xs,
                                           float acc) {
   const uint32_t qs = r.q0 | (r.q1 << 16);
   const float fs = (float)((int)r.sc - 32) * h2f(r.d);
+  uint32_t qw[4];
+  q3_codes(qs, r.hm, qw);
   float t = 0.0f;
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const uint32_t q = __builtin_amdgcn_ubfe(qs, 2 * i, 2) | (__builtin_amdgcn_ubfe(r.hm, i, 1) << 2);
-    t = __builtin_fmaf((float)q, x[i >> 2][i & 3], t);
-  }
+  for (int i = 0; i < 16; ++i) t = __builtin_fmaf(q3_code(qw, i), x[i >> 2][i & 3], t);
   return __builtin_fmaf(fs, __builtin_fmaf(-4.0f, xs, t), acc);
 }
 
