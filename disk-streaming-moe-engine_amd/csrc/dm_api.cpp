@@ -487,6 +487,7 @@ hipError_t run_block(dmh_ctx* ctx, Layer* Ly, int layer, const float* dx, const 
       dm::DecodeSync S = dm::decode_sync_carve(L, Ly->plan, Ly->sync);
       S.n = ++Ly->launches;
       S.spin = ctx->spin_limit;
+      S.trace = layer;
       e = dm::launch_moe_decode(L, Ly->plan, dx + (size_t)t * L.H,
                                 dres ? dres + (size_t)t * L.H : nullptr, dy + (size_t)t * L.H,
                                 dids + (size_t)t * L.K, dprobs + (size_t)t * L.K, dshg + t, S,

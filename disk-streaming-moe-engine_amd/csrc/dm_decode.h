@@ -40,7 +40,14 @@ struct DecodeSync {
   uint64_t* pt;  // XCD-sliced form: [nx][H] (tag, partial output)
   unsigned n;    // launch index, >= 1 (the tag of this launch)
   long spin;     // polls of a wait before it gives up with a sync error
+  int trace;     // phase-trace slot of the launch (the layer), -1: none; read only by
+                 // a tracing build (DM_PHASE_TRACE, `make trace`)
 };
+// Tracing build: phase timestamps of k_moe_decode_xs, kTraceSlots slots
+// (layers) x 256 workgroups x 8 points (wall_clock64, 100 MHz), fetched by
+// the extern "C" dmh_phase_trace_fetch of libdismoen_hip_trace.so.
+constexpr int kTraceSlots = 64;
+constexpr int kTracePoints = 8;
 size_t decode_sync_bytes(const LayerDev& L, const DecodePlan& P);
 DecodeSync decode_sync_carve(const LayerDev& L, const DecodePlan& P, void* base);
 

@@ -1030,6 +1030,24 @@ __device__ __forceinline__ unsigned xcc_id() {
   return v & 0xFu;
 }
 
+#ifdef DM_PHASE_TRACE
+// Tracing build: workgroup b (< 256) of a launch with S.trace = slot stores
+// wall_clock64() at point k to g_phase_trace[(slot * 256 + b) * 8 + k]:
+// 0 entry, 1 norm sum done, 2 x staged, 3 routing done, 4 h staged,
+// 5 partial published, 6 partials polled, 7 end.
+__device__ unsigned long long g_phase_trace[kTraceSlots * 256 * kTracePoints];
+#define DM_TR(k)                                                                      \
+  do {                                                                                \
+    if (S.trace >= 0 && S.trace < kTraceSlots && blockIdx.x < 256 && threadIdx.x == 0) \
+      g_phase_trace[((size_t)S.trace * 256 + blockIdx.x) * kTracePoints + (k)] =       \
+          wall_clock64();                                                             \
+  } while (0)
+#else
+#define DM_TR(k) \
+  do {           \
+  } while (0)
+#endif
+
 template <int GQW, int R, int NORM>
 __global__ __launch_bounds__(kThreads) void k_moe_decode_xs(
     LayerDev L, DecodePlan P, const float* __restrict__ x, const float* __restrict__ residual,
@@ -1037,6 +1055,7 @@ __global__ __launch_bounds__(kThreads) void k_moe_decode_xs(
     float* __restrict__ shg_out, DecodeSync S, unsigned long long* status, int token,
     NormSpec nm, unsigned long long* status_out) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  DM_TR(0);
   float* xt = reinterpret_cast<float*>(smem + P.off_xt);
   uint4* xb2 = reinterpret_cast<uint4*>(smem + P.off_xb);
   float* red = reinterpret_cast<float*>(smem + P.off_red);
@@ -1155,6 +1174,7 @@ __global__ __launch_bounds__(kThreads) void k_moe_decode_xs(
   // ---- optional RMSNorm of x (as in the original form) ---------------------
   if constexpr (NORM != 0) {
     norm_sum_squares<NORM>(xr, H, reinterpret_cast<float*>(xb2), red);
+    DM_TR(1);
     const float denom = __builtin_sqrtf(red[0] / (float)H + nm.eps);
     auto nrm = [&](float4 v, float4 g) {
       return make_float4((v.x / denom) * g.x, (v.y / denom) * g.y, (v.z / denom) * g.z,
@@ -1194,6 +1214,7 @@ __global__ __launch_bounds__(kThreads) void k_moe_decode_xs(
     if (bad && b == 0) record_err(status, err_key(kPhX, 0, 0, 0, 0));
   }
   __syncthreads();
+  DM_TR(2);
 
   // ---- router rows (XCD-local logits), the shared expert's rows ---------------
   if (w < nrw) router_compute<true>(L, rw, re, xt, zl, n);
@@ -1239,6 +1260,7 @@ __global__ __launch_bounds__(kThreads) void k_moe_decode_xs(
     softmax_exp<R>(zl, n, E, st, b == 0, token, status, S.spin);
   }
   __syncthreads();
+  DM_TR(3);
   const bool ok = st.misc[2] != 0.0f;
 
   // ---- routed loads: this workgroup's gate/up tile, this wave's down tiles ---
@@ -1366,6 +1388,7 @@ __global__ __launch_bounds__(kThreads) void k_moe_decode_xs(
     if (!__syncthreads_and(have == all || !ok) && tid == 0)
       record_err(status, err_key(kPhSync, 0, 0, 2, 0));
   }
+  DM_TR(4);
   f32x4 acc0 = {0, 0, 0, 0}, acc1 = {0, 0, 0, 0};
   auto tile_mfma = [&](const bf16x8 (&Aop)[4], int lp) {
     const uint16_t* hs = hbh + lp * kQuadCols;
@@ -1400,6 +1423,7 @@ __global__ __launch_bounds__(kThreads) void k_moe_decode_xs(
     for (int w2 = t2; w2 < kWaves; w2 += rpw) s = s + yred[w2 * 16 + r];
     st_coh_u64(S.pt + (size_t)xc * H + (rb0 + t2) * kTileRows + r, ((uint64_t)n << 32) | f2u(s));
   }
+  DM_TR(5);
 
   // ---- the final sum: rows b*rpf .. b*rpf + rpf - 1 -------------------------
   {
@@ -1421,6 +1445,7 @@ __global__ __launch_bounds__(kThreads) void k_moe_decode_xs(
     }
     if (!__syncthreads_and(fok || !ok) && tid == 0)
       record_err(status, err_key(kPhSync, 0, 0, 3, 0));
+    DM_TR(6);
     if (tid < nfr) {
       const int d = r0 + tid;
       float total = 0.0f;
@@ -1430,6 +1455,7 @@ __global__ __launch_bounds__(kThreads) void k_moe_decode_xs(
       y[d] = total;
     }
   }
+  DM_TR(7);
   end_workgroup(status, status_out);
 }
 
@@ -1459,6 +1485,7 @@ DecodeSync decode_sync_carve(const LayerDev& L, const DecodePlan& P, void* base)
   unsigned char* p = (unsigned char*)base;
   DecodeSync S{};
   S.spin = kDefaultSpinLimit;
+  S.trace = -1;
   S.zt = (uint64_t*)p;
   p += align256z((256 * R + 64) * 8 * (P.xs ? P.xs_nx : 1));
   if (P.xs) {
@@ -1650,3 +1677,15 @@ int xcd_rotation(const unsigned* xcd, int nwg) {
 }
 
 }  // namespace dm
+
+#ifdef DM_PHASE_TRACE
+// The phase timestamps of a tracing build (kTraceSlots x 256 x kTracePoints
+// 64-bit words, zero where no launch stored one); not in the normal build.
+extern "C" int dmh_phase_trace_fetch(void* dst, size_t bytes) {
+  if (!dst || bytes < sizeof(dm::g_phase_trace)) return 1;
+  return hipMemcpyFromSymbol(dst, HIP_SYMBOL(dm::g_phase_trace), sizeof(dm::g_phase_trace)) ==
+                 hipSuccess
+             ? 0
+             : 3;
+}
+#endif

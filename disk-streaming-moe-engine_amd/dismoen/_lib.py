@@ -9,7 +9,9 @@ import ctypes as C
 import os
 
 PKG_ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-LIB_PATH = os.path.join(PKG_ROOT, "libdismoen_hip.so")
+# DISMOEN_LIB names another build of the same library (the tracing build of
+# phase_trace.py); by default the in-tree libdismoen_hip.so
+LIB_PATH = os.environ.get("DISMOEN_LIB") or os.path.join(PKG_ROOT, "libdismoen_hip.so")
 
 DMH_F_DEVICE = 0x1
 DMH_F_Q4K_PY_SCALES = 0x10
