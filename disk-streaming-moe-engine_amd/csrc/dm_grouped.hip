@@ -449,12 +449,12 @@ __device__ __forceinline__ void unit_assignments(const GroupArgs& g, const UnitT
   }
 }
 
+// (aa: the unit's assignments of column j, unit_assignments)
 template <int NT, int NC>
 __device__ __forceinline__ void gu_epilogue(const GroupArgs& g, const UnitTokens& ut, int I,
-                                            int f0, int q, int j, const f32x4 (&acc)[NT][NC]) {
+                                            int f0, int q, int j, const f32x4 (&acc)[NT][NC],
+                                            const int (&aa)[NC]) {
   const int K = g.L.K;
-  int aa[NC];
-  unit_assignments<NC>(g, ut, j, aa);
 #pragma unroll
   for (int ct = 0; ct < NC; ++ct) {
     const int c = 16 * ct + j;
@@ -497,11 +497,9 @@ __device__ __forceinline__ void gu_epilogue(const GroupArgs& g, const UnitTokens
 // Down: tile tl holds output rows row0 + 16 tl + 4q + i of column j.
 template <int NT, int NC>
 __device__ __forceinline__ void down_epilogue(const GroupArgs& g, const UnitTokens& ut, int I,
-                                              int row0, int q, int j,
-                                              const f32x4 (&acc)[NT][NC]) {
+                                              int row0, int q, int j, const f32x4 (&acc)[NT][NC],
+                                              const int (&aa)[NC]) {
   const int H = g.L.H, K = g.L.K;
-  int aa[NC];
-  unit_assignments<NC>(g, ut, j, aa);
 #pragma unroll
   for (int ct = 0; ct < NC; ++ct) {
     const int c = 16 * ct + j;
@@ -627,14 +625,100 @@ __device__ __forceinline__ void lds_wait8(bf16x8 (&b)[kNCT]) {
 __device__ __forceinline__ void gu_small_part(const GroupArgs& g, int bx, int by, int w);
 __device__ __forceinline__ void down_small_part(const GroupArgs& g, int bx, int by, int w);
 
-// One workgroup per CU (its LDS), two waves per SIMD: registers up to 256
-// per lane, spent on keeping a whole k-group of B fragments in flight.
+// One big item (unit ui, feature / row block fb) as seen by one lane: what
+// the DMA of its stages needs (its A views and tiles, its B rows) and what
+// its epilogue needs.
+struct BigItem {
+  bool valid;
+  UnitTokens ut;
+  int I, fb, nst, nGQ, KD, t0, t1, st_;
+  bool lo;
+  ExpertView v0, v1;
+  const uint16_t* bhi;
+  const uint16_t* blo;
+  uint32_t rowo[4];  // this lane's B row offsets (elements) of the four DMA rows
+};
+
+template <bool GU>
+__device__ __forceinline__ BigItem big_item_state(const GroupArgs& g, int idx, int items,
+                                                  int nblk, int w, int lane) {
+  BigItem it;
+  it.valid = false;
+  int ui, fb;
+  if (idx >= items || !big_item(idx, g.meta[1], nblk, ui, fb)) return it;
+  const LayerDev& L = g.L;
+  const int H = L.H, K = L.K;
+  it.ut = unit_tokens(g.units[ui], g.off, L.E, g.T, kMT);
+  it.I = it.ut.shared ? L.Ish : L.I;
+  it.fb = fb;
+  if (GU && fb * 128 >= it.I) return it;  // uniform per workgroup
+  it.KD = GU ? H : it.I;  // reduction length
+  it.nGQ = it.KD / kQuadCols;
+  it.lo = GU ? g.need_lo[0] != 0 : true;
+  it.nst = it.lo ? 2 * it.nGQ : it.nGQ;
+  if (GU) {
+    const size_t mat = (size_t)it.I * H;
+    it.v0 = it.ut.shared ? ExpertView{L.sgu_nib, L.sgu_sc, it.I, H}
+                         : ExpertView{L.gu_nib + (size_t)it.ut.e * mat,
+                                      L.gu_sc + (size_t)it.ut.e * 2 * (mat / kGroup), it.I, H};
+    it.v1 = {it.v0.nib + mat / 2, it.v0.sc + mat / kGroup, it.I, H};
+    it.t0 = it.t1 = fb * 8 + w;
+  } else {
+    const size_t mat = (size_t)H * it.I;
+    it.v0 = it.ut.shared ? ExpertView{L.sd_nib, L.sd_sc, H, it.I}
+                         : ExpertView{L.d_nib + (size_t)it.ut.e * (mat / 2),
+                                      L.d_sc + (size_t)it.ut.e * (mat / kGroup), H, it.I};
+    it.v1 = it.v0;
+    // H is a multiple of 128, so the last block may hold 128 rows: waves
+    // past H load tiles 0 and 1 (their share of the B rows is still needed)
+    // and store nothing
+    it.t0 = fb * 256 + 32 * w < H ? fb * 16 + 2 * w : 0;
+    it.t1 = it.t0 + 1;
+  }
+  it.bhi = GU ? g.xhi : (it.ut.shared ? g.hsh : g.hrh);
+  it.blo = GU ? g.xlo : (it.ut.shared ? g.hsl : g.hrl);
+  // B rows: instructions i = w + 8 m (m < 4) carry rows 4i..4i+3, lane L
+  // row 4i + L/16, stored segment L % 16 = global segment (L % 16) ^ (row & 15)
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    const int r = 4 * (w + 8 * m) + (lane >> 4);
+    const int p = it.ut.p0 + min(r, it.ut.n - 1);
+    const int sg = (lane & 15) ^ (r & 15);
+    const int row = !GU ? p : it.ut.shared ? p : g.perm[p] / K;  // h rows by position, x by token
+    it.rowo[m] = (uint32_t)row * (uint32_t)it.KD + sg * 8;
+  }
+  it.st_ = lane < 8 ? it.t0 : it.t1;
+  it.valid = true;
+  return it;
+}
+
+// The first valid item at idx, idx + step, ... (idx advanced past it).
+template <bool GU>
+__device__ __forceinline__ BigItem big_next_item(const GroupArgs& g, int& idx, int step, int items,
+                                                 int nblk, int w, int lane) {
+  BigItem it;
+  it.valid = false;
+  while (idx < items) {
+    it = big_item_state<GU>(g, idx, items, nblk, w, lane);
+    idx += step;
+    if (it.valid) break;
+  }
+  return it;
+}
+
+// Workgroups 0 .. big_wgs - 1 are persistent: workgroup b takes the big
+// items (big_item index space 0 .. items - 1) b, b + big_wgs, ...; with
+// big_wgs a multiple of 8, every item of b is of class b % 8, on b's XCD.
+// The stage pipeline runs on across items: the first two stages of the
+// next item are requested during the last two stages of the current one,
+// so they land while its epilogue runs (the start latency of a workgroup,
+// ~3.4 us, is paid once per workgroup instead of once per item).
 // Workgroups from big_wgs on run the small units of the same stage (sx x sy
 // four-wave parts, two per workgroup): dispatched after every big one, they
-// fill the CUs that the big units' last round leaves idle.
+// fill the CUs the big items' last round leaves idle.
 template <bool GU>
 __global__ __launch_bounds__(kB2Threads) __attribute__((amdgpu_waves_per_eu(2, 2)))
-void k_big(GroupArgs g, int big_wgs, int sx, int sy) {
+void k_big(GroupArgs g, int items, int big_wgs, int sx, int sy) {
   extern __shared__ __attribute__((aligned(16))) unsigned char lds2[];
   if ((int)blockIdx.x >= big_wgs) {
     const int w = gwave_id();
@@ -648,126 +732,106 @@ void k_big(GroupArgs g, int big_wgs, int sx, int sy) {
     return;
   }
   const LayerDev& L = g.L;
-  const int H = L.H, K = L.K;
-  int ui, fb;
+  const int H = L.H;
   const int nblk = GU ? ((L.I > L.Ish ? L.I : L.Ish) + 127) / 128 : (H + 255) / 256;
-  if (!big_item(blockIdx.x, g.meta[1], nblk, ui, fb)) return;
-  const UnitTokens ut = unit_tokens(g.units[ui], g.off, L.E, g.T, kMT);
-  const int I = ut.shared ? L.Ish : L.I;
-  if (GU && fb * 128 >= I) return;  // uniform per workgroup
   const int tid = threadIdx.x, w = gwave_id(), lane = tid & 63, q = lane >> 4, j = lane & 15;
-  const int KD = GU ? H : I;  // reduction length
-  const int nGQ = KD / kQuadCols;
-  const bool lo = GU ? g.need_lo[0] != 0 : true;
-  const int nst = lo ? 2 * nGQ : nGQ;  // stages
-  // A views and this wave's two tiles: (v0, t0) and (v1, t1)
-  ExpertView v0, v1;
-  int t0, t1;
-  if (GU) {
-    const size_t mat = (size_t)I * H;
-    v0 = ut.shared ? ExpertView{L.sgu_nib, L.sgu_sc, I, H}
-                   : ExpertView{L.gu_nib + (size_t)ut.e * mat,
-                                L.gu_sc + (size_t)ut.e * 2 * (mat / kGroup), I, H};
-    v1 = {v0.nib + mat / 2, v0.sc + mat / kGroup, I, H};
-    t0 = t1 = fb * 8 + w;
-  } else {
-    const size_t mat = (size_t)H * I;
-    v0 = ut.shared ? ExpertView{L.sd_nib, L.sd_sc, H, I}
-                   : ExpertView{L.d_nib + (size_t)ut.e * (mat / 2),
-                                L.d_sc + (size_t)ut.e * (mat / kGroup), H, I};
-    v1 = v0;
-    // H is a multiple of 128, so the last block may hold 128 rows: waves
-    // past H load tiles 0 and 1 (their share of the B rows is still needed)
-    // and store nothing
-    t0 = fb * 256 + 32 * w < H ? fb * 16 + 2 * w : 0;
-    t1 = t0 + 1;
-  }
-  const uint16_t* bhi = GU ? g.xhi : (ut.shared ? g.hsh : g.hrh);
-  const uint16_t* blo = GU ? g.xlo : (ut.shared ? g.hsl : g.hrl);
+  int idx = blockIdx.x;
+  BigItem cur = big_next_item<GU>(g, idx, big_wgs, items, nblk, w, lane);
+  if (!cur.valid) return;  // uniform per workgroup
   // this lane's part of the DMA of a stage:
-  //   B rows: instructions i = w + 8 m (m < 4) carry rows 4i..4i+3, lane
-  //   L row 4i + L/16, stored segment L % 16 = global segment (L % 16) ^ (row & 15)
+  //   B rows: 4 instructions of 4 rows (rowo)
   //   A: chunk 2w (tile t0) and chunk 2w + 1 (tile t1)
   //   scales: lanes 0..15 carry the 2 x 128 bytes of the same two chunks
-  size_t rowo[4];
-#pragma unroll
-  for (int m = 0; m < 4; ++m) {
-    const int r = 4 * (w + 8 * m) + (lane >> 4);
-    const int p = ut.p0 + min(r, ut.n - 1);
-    const int sg = (lane & 15) ^ (r & 15);
-    const int row = !GU ? p : ut.shared ? p : g.perm[p] / K;  // h rows by position, x by token
-    rowo[m] = (size_t)row * KD + sg * 8;
-  }
-  const ExpertView& sv = lane < 8 ? v0 : v1;  // scale piece owner (lanes 0..15)
-  const int st_ = lane < 8 ? t0 : t1;
-  auto issue = [&](int ps, int buf) {
-    const int s = lo ? ps >> 1 : ps;
-    const uint16_t* src = (lo && (ps & 1)) ? blo : bhi;
+  auto issue = [&](const BigItem& it, int ps, int buf) {
+    const int s = it.lo ? ps >> 1 : ps;
+    const uint16_t* src = (it.lo && (ps & 1)) ? it.blo : it.bhi;
     unsigned char* st = lds2 + buf * kB2Stage;
 #pragma unroll
-    for (int m = 0; m < 4; ++m) dma16(src + rowo[m] + s * kQuadCols, st + (w + 8 * m) * 1024);
-    dma16(v0.nib + a16_nib_offset(nGQ, t0, s, lane), st + kB2BBytes + 2 * w * 1024);
-    dma16(v1.nib + a16_nib_offset(nGQ, t1, s, lane), st + kB2BBytes + (2 * w + 1) * 1024);
+    for (int m = 0; m < 4; ++m) dma16(src + it.rowo[m] + s * kQuadCols, st + (w + 8 * m) * 1024);
+    dma16(it.v0.nib + a16_nib_offset(it.nGQ, it.t0, s, lane), st + kB2BBytes + 2 * w * 1024);
+    dma16(it.v1.nib + a16_nib_offset(it.nGQ, it.t1, s, lane), st + kB2BBytes + (2 * w + 1) * 1024);
     // scales of the two chunks: 128 bytes each, lanes 0..7 and 8..15 (only
     // 16 lanes write: 256 bytes at the wave's own place)
     if (lane < 16)
-      dma16(reinterpret_cast<const unsigned char*>(sv.sc + a16_sc_offset(nGQ, st_, s, 0)) +
+      dma16(reinterpret_cast<const unsigned char*>((lane < 8 ? it.v0 : it.v1).sc +
+                                                   a16_sc_offset(it.nGQ, it.st_, s, 0)) +
                 (lane & 7) * 16,
             st + kB2BBytes + kB2ABytes + w * 256);
   };
-  f32x4 acc[2][kNCT];
+  issue(cur, 0, 0);
+  issue(cur, 1, 1);  // every item has at least two stages (checked at launch)
+  int gb = 0;        // stage count of the items before cur (buffer of its stage ps: (gb + ps) % 3)
+  while (true) {
+    // the next item's state (its loads wait, at the latest, for cur's first
+    // two stages, which stage 0 waits for anyway)
+    const BigItem nxt = big_next_item<GU>(g, idx, big_wgs, items, nblk, w, lane);
+    // the epilogue's assignments, requested now: a load issued after the next
+    // item's first stages would wait for them
+    int aa[kNCT];
+    unit_assignments<kNCT>(g, cur.ut, j, aa);
+    f32x4 acc[2][kNCT];
 #pragma unroll
-  for (int t = 0; t < 2; ++t)
+    for (int t = 0; t < 2; ++t)
 #pragma unroll
-    for (int ct = 0; ct < kNCT; ++ct) acc[t][ct] = f32x4{0, 0, 0, 0};
-  issue(0, 0);
-  if (nst > 1) issue(1, 1);
-  for (int ps = 0; ps < nst; ++ps) {
-    // this wave's loads of stage ps have landed (one later stage may be in flight)
-    static_assert(kB2DmaPerStage == 7, "the wait below counts one stage of 7 loads");
-    if (ps + 1 < nst)
-      asm volatile("s_waitcnt vmcnt(7)" ::: "memory");
-    else
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    // every wave's loads of stage ps have landed, and every wave has finished
-    // reading stage ps - 1 (whose buffer the next issue overwrites)
-    __builtin_amdgcn_s_barrier();
-    if (ps + 2 < nst) issue(ps + 2, (ps + 2) % kB2Stages);
-    const unsigned char* st = lds2 + (ps % kB2Stages) * kB2Stage;
-    const uint4 c0 = *reinterpret_cast<const uint4*>(st + kB2BBytes + 2 * w * 1024 + lane * 16);
-    const uint4 c1 =
-        *reinterpret_cast<const uint4*>(st + kB2BBytes + (2 * w + 1) * 1024 + lane * 16);
-    const uint2 s0 = *reinterpret_cast<const uint2*>(st + kB2BBytes + kB2ABytes + w * 256 + j * 8);
-    const uint2 s1 =
-        *reinterpret_cast<const uint2*>(st + kB2BBytes + kB2ABytes + w * 256 + 128 + j * 8);
-    // The 8 B fragments of k-group kk + 1 are read while kk computes.
-    bf16x8 bc[kNCT], bn[kNCT];
-    const uint32_t bp = lds_addr(st + j * kB2RowBytes);
-    lds_read8(bp + (q ^ j) * 16, bc);
-#pragma unroll
-    for (int kk = 0; kk < kGroupsPerQuad; ++kk) {
-      if (kk + 1 < kGroupsPerQuad) lds_read8(bp + ((4 * (kk + 1) + q) ^ j) * 16, bn);
-      const bf16x8 a0 = dequant8(word_of(c0, kk), scale_of(s0, kk));
-      const bf16x8 a1 = dequant8(word_of(c1, kk), scale_of(s1, kk));
-      if (kk + 1 < kGroupsPerQuad)
-        lds_wait8<kNCT>(bc);
+      for (int ct = 0; ct < kNCT; ++ct) acc[t][ct] = f32x4{0, 0, 0, 0};
+    for (int ps = 0; ps < cur.nst; ++ps) {
+      // this wave's loads of stage ps have landed (one later stage may be in flight)
+      // (the first stage of an item after the first: everything, since the
+      // previous epilogue's stores were issued after this stage's loads and
+      // a count of outstanding operations cannot tell them apart)
+      static_assert(kB2DmaPerStage == 7, "the wait below counts one stage of 7 loads");
+      if ((ps + 1 < cur.nst || nxt.valid) && !(ps == 0 && gb > 0))
+        asm volatile("s_waitcnt vmcnt(7)" ::: "memory");
       else
-        lds_wait8<0>(bc);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      // every wave's loads of stage ps have landed, and every wave has finished
+      // reading stage ps - 1 (whose buffer the next issue overwrites)
+      __builtin_amdgcn_s_barrier();
+      const int gs = gb + ps;
+      if (ps + 2 < cur.nst)
+        issue(cur, ps + 2, (gs + 2) % kB2Stages);
+      else if (nxt.valid)
+        issue(nxt, ps + 2 - cur.nst, (gs + 2) % kB2Stages);
+      const unsigned char* st = lds2 + (gs % kB2Stages) * kB2Stage;
+      const uint4 c0 = *reinterpret_cast<const uint4*>(st + kB2BBytes + 2 * w * 1024 + lane * 16);
+      const uint4 c1 =
+          *reinterpret_cast<const uint4*>(st + kB2BBytes + (2 * w + 1) * 1024 + lane * 16);
+      const uint2 s0 =
+          *reinterpret_cast<const uint2*>(st + kB2BBytes + kB2ABytes + w * 256 + j * 8);
+      const uint2 s1 =
+          *reinterpret_cast<const uint2*>(st + kB2BBytes + kB2ABytes + w * 256 + 128 + j * 8);
+      // The 8 B fragments of k-group kk + 1 are read while kk computes.
+      bf16x8 bc[kNCT], bn[kNCT];
+      const uint32_t bp = lds_addr(st + j * kB2RowBytes);
+      lds_read8(bp + (q ^ j) * 16, bc);
 #pragma unroll
-      for (int ct = 0; ct < kNCT; ++ct) {
-        acc[0][ct] = mfma16(a0, bc[ct], acc[0][ct]);
-        acc[1][ct] = mfma16(a1, bc[ct], acc[1][ct]);
-      }
-      if (kk + 1 < kGroupsPerQuad) {
+      for (int kk = 0; kk < kGroupsPerQuad; ++kk) {
+        if (kk + 1 < kGroupsPerQuad) lds_read8(bp + ((4 * (kk + 1) + q) ^ j) * 16, bn);
+        const bf16x8 a0 = dequant8(word_of(c0, kk), scale_of(s0, kk));
+        const bf16x8 a1 = dequant8(word_of(c1, kk), scale_of(s1, kk));
+        if (kk + 1 < kGroupsPerQuad)
+          lds_wait8<kNCT>(bc);
+        else
+          lds_wait8<0>(bc);
 #pragma unroll
-        for (int ct = 0; ct < kNCT; ++ct) bc[ct] = bn[ct];
+        for (int ct = 0; ct < kNCT; ++ct) {
+          acc[0][ct] = mfma16(a0, bc[ct], acc[0][ct]);
+          acc[1][ct] = mfma16(a1, bc[ct], acc[1][ct]);
+        }
+        if (kk + 1 < kGroupsPerQuad) {
+#pragma unroll
+          for (int ct = 0; ct < kNCT; ++ct) bc[ct] = bn[ct];
+        }
       }
     }
+    if (GU)
+      gu_epilogue<2, kNCT>(g, cur.ut, cur.I, cur.fb * 128 + 16 * w, q, j, acc, aa);
+    else if (cur.fb * 256 + 32 * w < H)
+      down_epilogue<2, kNCT>(g, cur.ut, cur.I, cur.fb * 256 + 32 * w, q, j, acc, aa);
+    if (!nxt.valid) break;  // uniform
+    gb += cur.nst;
+    cur = nxt;
   }
-  if (GU)
-    gu_epilogue<2, kNCT>(g, ut, I, fb * 128 + 16 * w, q, j, acc);
-  else if (fb * 256 + 32 * w < H)
-    down_epilogue<2, kNCT>(g, ut, I, fb * 256 + 32 * w, q, j, acc);
 }
 
 // k_big's LDS (150 KB) is above the default limit of a launch: raised once
@@ -786,6 +850,21 @@ static hipError_t big_attrs() {
                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)kB2Lds);
   if (e == hipSuccess) done.fetch_or(bit);
   return e;
+}
+
+// Persistent big workgroups of this device: its CU count rounded down to a
+// multiple of 8 (0 when it cannot be read).
+static int big_persistent_wgs() {
+  static std::atomic<int> cus[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  int n = cus[dev].load();
+  if (n == 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    n &= ~7;
+    cus[dev].store(n);
+  }
+  return n;
 }
 
 // ---------------------------------------------------------------------------
@@ -890,7 +969,9 @@ __device__ __forceinline__ void gu_small_part(const GroupArgs& g, int bx, int by
     small_loop<true, true, 2>(gv, uv, f0 / kTileRows, g.xhi + o, g.xlo + o, ns, acc);
   else
     small_loop<false, true, 4>(gv, uv, f0 / kTileRows, g.xhi + o, g.xlo + o, ns, acc);
-  gu_epilogue<kSmallTiles, 1>(g, ut, I, f0, q, j, acc);
+  int aa[1];
+  unit_assignments<1>(g, ut, j, aa);
+  gu_epilogue<kSmallTiles, 1>(g, ut, I, f0, q, j, acc, aa);
 }
 
 // Small down unit bx, output rows by * 128 .., on wave w of four.
@@ -911,7 +992,9 @@ __device__ __forceinline__ void down_small_part(const GroupArgs& g, int bx, int 
   f32x4 acc[kSmallTiles][1];
   small_loop<true, false, 2>(dv, dv, row0 / kTileRows, (ut.shared ? g.hsh : g.hrh) + o,
                              (ut.shared ? g.hsl : g.hrl) + o, I / kQuadCols, acc);
-  down_epilogue<kSmallTiles, 1>(g, ut, I, row0, q, j, acc);
+  int aa[1];
+  unit_assignments<1>(g, ut, j, aa);
+  down_epilogue<kSmallTiles, 1>(g, ut, I, row0, q, j, acc, aa);
 }
 
 __global__ __launch_bounds__(kGThreads) __attribute__((amdgpu_waves_per_eu(3))) void k_gu_small(
@@ -941,6 +1024,9 @@ hipError_t launch_experts_grouped(const LayerDev& L, const uint16_t* xhi, const 
   // an expert holds at most T tokens (its ids per token are distinct), so
   // units of more than 2 * kSmallMax tokens need T > 2 * kSmallMax
   const bool big = T > 2 * kSmallMax;
+  // the big items' B row offsets are 32-bit element offsets
+  if ((size_t)T * L.K * imax >= (1ull << 32) || (size_t)T * L.H >= (1ull << 32))
+    return hipErrorInvalidValue;
   if (big) {
     const hipError_t e = big_attrs();
     if (e != hipSuccess) return e;
@@ -952,9 +1038,14 @@ hipError_t launch_experts_grouped(const LayerDev& L, const uint16_t* xhi, const 
     // big units run about five rounds, so its small units keep their own
     // launch (dispatched after every big one they would add rounds)
     const int bg = big_grid(nbig, (imax + 127) / 128), bd = big_grid(nbig, (L.H + 255) / 256);
-    hipLaunchKernelGGL(k_big<true>, dim3(bg + (nsmall * gy + 1) / 2), dim3(kB2Threads), kB2Lds,
-                       st, g, bg, nsmall, gy);
-    hipLaunchKernelGGL(k_big<false>, dim3(bd), dim3(kB2Threads), kB2Lds, st, g, bd, 0, 0);
+    // persistent big workgroups: one per CU (150 KB of LDS each), a multiple
+    // of 8 so that an item keeps its class; every item needs two stages or
+    // more (gate/up: H / 128 of them, down: 2 I / 128)
+    const int pw = L.H >= 256 ? big_persistent_wgs() : 0;
+    const int wg_g = pw > 0 && pw < bg ? pw : bg, wg_d = pw > 0 && pw < bd ? pw : bd;
+    hipLaunchKernelGGL(k_big<true>, dim3(wg_g + (nsmall * gy + 1) / 2), dim3(kB2Threads), kB2Lds,
+                       st, g, bg, wg_g, nsmall, gy);
+    hipLaunchKernelGGL(k_big<false>, dim3(wg_d), dim3(kB2Threads), kB2Lds, st, g, bd, wg_d, 0, 0);
   } else {
     hipLaunchKernelGGL(k_gu_small, dim3(nsmall, gy), dim3(kGThreads), 0, st, g);
   }
