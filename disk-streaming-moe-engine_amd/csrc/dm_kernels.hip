@@ -542,27 +542,44 @@ __global__ __launch_bounds__(256) void k_router_mfma(LayerDev L, const uint16_t*
   const int pitch = 16 * ns + 8;  // elements per staged token (16 B of padding)
   const int t0 = blockIdx.y * 16, tid = threadIdx.x;
   // stage: thread item (token i, step pair sp) reads x[32 sp .. 32 sp + 31]
-  // and writes, for each chain l, steps 2 sp and 2 sp + 1 as one word
+  // and writes, for each chain l, steps 2 sp and 2 sp + 1 as one word.
+  // The reads of up to kStage items are all requested before the first
+  // write (one round trip instead of one per item: x was just written by
+  // another launch, so it comes from beyond this XCD's L2).
+  constexpr int kStage = 4;
   const int npair = ns / 2;
-  for (int idx = tid; idx < 16 * npair; idx += 256) {
-    const int i = idx / npair, sp = idx % npair;
-    uint32_t v[16];
-    if (t0 + i < T) {
-      const uint4* src = reinterpret_cast<const uint4*>(xhi + (size_t)(t0 + i) * H + 32 * sp);
+  for (int idx0 = tid; idx0 < 16 * npair; idx0 += 256 * kStage) {
+    uint4 xv[kStage][4];
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const uint4 u = src[c];
-        v[4 * c] = u.x; v[4 * c + 1] = u.y; v[4 * c + 2] = u.z; v[4 * c + 3] = u.w;
-      }
-    } else {
+    for (int it = 0; it < kStage; ++it) {
+      const int idx = min(idx0 + 256 * it, 16 * npair - 1);
+      const int i = idx / npair, sp = idx % npair;
+      const uint4* src =
+          reinterpret_cast<const uint4*>(xhi + (size_t)min(t0 + i, T - 1) * H + 32 * sp);
 #pragma unroll
-      for (int c = 0; c < 16; ++c) v[c] = 0;
+      for (int c = 0; c < 4; ++c) xv[it][c] = src[c];
     }
 #pragma unroll
-    for (int l = 0; l < 16; ++l) {
-      const uint32_t a = (v[l >> 1] >> (16 * (l & 1))) & 0xFFFFu;          // step 2 sp
-      const uint32_t bq = (v[8 + (l >> 1)] >> (16 * (l & 1))) & 0xFFFFu;   // step 2 sp + 1
-      *reinterpret_cast<uint32_t*>(xs + i * pitch + l * ns + 2 * sp) = a | (bq << 16);
+    for (int it = 0; it < kStage; ++it) {
+      const int idx = idx0 + 256 * it;
+      if (idx < 16 * npair) {
+        const int i = idx / npair, sp = idx % npair;
+        uint32_t v[16];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const bool in = t0 + i < T;  // tokens past T stage zeros
+          v[4 * c] = in ? xv[it][c].x : 0u;
+          v[4 * c + 1] = in ? xv[it][c].y : 0u;
+          v[4 * c + 2] = in ? xv[it][c].z : 0u;
+          v[4 * c + 3] = in ? xv[it][c].w : 0u;
+        }
+#pragma unroll
+        for (int l = 0; l < 16; ++l) {
+          const uint32_t a = (v[l >> 1] >> (16 * (l & 1))) & 0xFFFFu;          // step 2 sp
+          const uint32_t bq = (v[8 + (l >> 1)] >> (16 * (l & 1))) & 0xFFFFu;   // step 2 sp + 1
+          *reinterpret_cast<uint32_t*>(xs + i * pitch + l * ns + 2 * sp) = a | (bq << 16);
+        }
+      }
     }
   }
   __syncthreads();
@@ -573,14 +590,28 @@ __global__ __launch_bounds__(256) void k_router_mfma(LayerDev L, const uint16_t*
     const uint16_t* xr = xs + i * pitch + l * ns;
     const uint16_t* wr = L.router + r16_index(H, E, l);
     float acc = 0.0f;
-    for (int c = 0; c < ns / 8; ++c) {
-      const uint4 xv = *reinterpret_cast<const uint4*>(xr + 8 * c);
-      const uint4 wv = *reinterpret_cast<const uint4*>(wr + (size_t)c * 128);
-      const uint32_t xa[4] = {xv.x, xv.y, xv.z, xv.w}, wa[4] = {wv.x, wv.y, wv.z, wv.w};
+    // the chain's gate words sixteen rounds at a time, all requested before
+    // the first product (one round trip per sixteen rounds; requested one
+    // per round they made these workgroups the launch's longest)
+    constexpr int kGw = 16;
+    const int nc = ns / 8;
+    for (int c0 = 0; c0 < nc; c0 += kGw) {
+      uint4 wv[kGw];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        acc = acc + bf16lo(xa[u]) * bf16lo(wa[u]);
-        acc = acc + bf16hi(xa[u]) * bf16hi(wa[u]);
+      for (int u = 0; u < kGw; ++u)
+        wv[u] = *reinterpret_cast<const uint4*>(wr + (size_t)min(c0 + u, nc - 1) * 128);
+#pragma unroll
+      for (int u = 0; u < kGw; ++u) {
+        if (c0 + u < nc) {  // uniform
+          const uint4 xv = *reinterpret_cast<const uint4*>(xr + 8 * (c0 + u));
+          const uint32_t xa[4] = {xv.x, xv.y, xv.z, xv.w};
+          const uint32_t wa[4] = {wv[u].x, wv[u].y, wv[u].z, wv[u].w};
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            acc = acc + bf16lo(xa[k]) * bf16lo(wa[k]);
+            acc = acc + bf16hi(xa[k]) * bf16hi(wa[k]);
+          }
+        }
       }
     }
 #pragma unroll
