@@ -246,13 +246,113 @@ __global__ __launch_bounds__(1024) void k_front(LayerDev L, const float* __restr
   if (tid == 0) last = atomicAdd(&flags[2 + t], 1) == (int)gridDim.x - 1;
   __syncthreads();
   if (!last) return;
-  const int lane = tid & 63;
-  if (tid < 64) {
+  const int lane = tid & 63, w = tid >> 6, K = L.K;
+  auto wsync = [] {
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+  };
+  // Two waves at once: wave 0 picks the top K on the logits (topk_on_logits:
+  // the same set as the reference's rounds on the probabilities whenever its
+  // margin check passes), wave 1 forms the softmax terms (max, the
+  // exponentials, their sum in expert order) and the shared gate, as
+  // router_softmax does (src/layers/router.mojo:140-183).  Then wave 0
+  // forms the K probabilities e_k * (1/S) and orders them (p desc, id asc),
+  // as select_topk (src/layers/topk.mojo:79-128).  On a near tie at the
+  // boundary wave 0 runs the exact rounds (route_select_token) instead.
+  constexpr int R = NE <= 4 ? 1 : 2;
+  __shared__ float sm_terms[2];  // max, 1/S
+  __shared__ int sm_unsafe;
+  float* sev = fl;               // [E] exponentials (the staged x is no longer read)
+  const float* zr = z + (size_t)t * (E + 1);
+  int myid = 0;
+  float zk = 0.0f;
+  if (w == 0) {
     if (tid == 0) atomicExch(&flags[2 + t], 0);
-    route_select_token<NE, true>(z, E + 1, E, L.K, 1, t, lane, fl, ids, probs, shg, status, [] {
-      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-    });
+    float zv[4 * R];
+#pragma unroll
+    for (int i = 0; i < 4 * R; ++i) {
+      const int e = lane + 64 * i;
+      zv[i] = e < E ? ld_coh(zr + e) : -__builtin_inff();
+    }
+    uint32_t fk[4 * R];
+    const bool unsafe = topk_on_logits<R>(zv, E, K, lane, fk, myid);
+    myid = min(max(myid, 0), E - 1);
+    // the logit of expert myid sits in lane myid & 63, entry myid >> 6
+#pragma unroll
+    for (int i = 0; i < 4 * R; ++i) {
+      const float zo = u2f((uint32_t)__builtin_amdgcn_ds_bpermute(4 * (myid & 63), (int)f2u(zv[i])));
+      zk = (myid >> 6) == i ? zo : zk;
+    }
+    if (lane == 0) sm_unsafe = unsafe || K > 8 ? 1 : 0;  // (the ranks below take K <= 8)
+  } else if (w == 1) {
+    const float lg = lane == 0 ? ld_coh(zr + E) : 0.0f;
+    float zv[NE];
+    float m = -__builtin_inff();
+#pragma unroll
+    for (int i = 0; i < NE; ++i) {
+      const int e = lane + 64 * i;
+      zv[i] = e < E ? ld_coh(zr + e) : -__builtin_inff();
+      if (e < E && !finite_f(zv[i])) record_err(status, err_key(kPhLogit, t, 0, e, 0));
+      m = zv[i] > m ? zv[i] : m;
+    }
+    m = __ockl_wfred_max_f32(m);
+    if (lane == 0 && !finite_f(m)) record_err(status, err_key(kPhSoftmax, t, 0, 0, 0));
+#pragma unroll
+    for (int i = 0; i < NE; ++i) {
+      const int e = lane + 64 * i;
+      if (e < E) {
+        const float ev = dm_expf(zv[i] - m);
+        if (!finite_f(ev)) record_err(status, err_key(kPhSoftmax, t, 0, 1 + e, 0));
+        sev[e] = ev;
+      }
+    }
+    wsync();
+    if (lane == 0) {
+      const float sum = seq_sum(sev, E);
+      if (!(sum > 0.0f) || !finite_f(sum)) record_err(status, err_key(kPhSoftmax, t, 0, 1 + E, 0));
+      sm_terms[0] = m;
+      sm_terms[1] = 1.0f / sum;
+      if (!finite_f(lg)) record_err(status, err_key(kPhGate, t, 0, 0, kGkLogit));
+      const float g = dm_sigmoid(lg);
+      if (!finite_f(g) || g < 0.0f || g > 1.0f) record_err(status, err_key(kPhGate, t, 0, 0, kGkRange));
+      shg[t] = g;
+    }
+  }
+  __syncthreads();
+  if (w == 0) {
+    if (sm_unsafe) {
+      route_select_token<NE, true>(z, E + 1, E, K, 1, t, lane, fl, ids, probs, shg, status, wsync);
+    } else {
+      const float m = sm_terms[0], inv = sm_terms[1];
+      const float pk = lane < K ? dm_expf(zk - m) * inv : 0.0f;
+      // rank of slot k: (p desc, id asc); the ids are distinct
+      const uint32_t kk = f2key(pk);
+      int rank = 0;
+#pragma unroll
+      for (int jj = 0; jj < 8; ++jj) {
+        const uint32_t kj = (uint32_t)__builtin_amdgcn_readlane((int)kk, jj);
+        const int ij = __builtin_amdgcn_readlane(myid, jj);
+        if (jj < K && lane < K) rank += (kj > kk || (kj == kk && ij < myid)) ? 1 : 0;
+      }
+      if (lane < K) {
+        st_coh_i32(ids + (size_t)t * K + rank, myid);
+        probs[(size_t)t * K + rank] = pk;
+      }
+      // the checks of select_topk in rank order
+      float* sp = sev + ((E + 3) & ~3);  // [8] probabilities by rank
+      if (lane < K) sp[rank] = pk;
+      wsync();
+      if (lane == 0) {
+        float sum_topk = 0.0f;
+        for (int r = 0; r < K; ++r) sum_topk = sum_topk + sp[r];
+        if (sum_topk > 1.00001f) record_err(status, err_key(kPhTopk, t, 0, 0, kTkSum));
+        if (K < E && __builtin_fabsf(sum_topk - 1.0f) < 1e-6f) {
+          float sum_all = 0.0f;
+          for (int e = 0; e < E; ++e) sum_all = sum_all + sev[e] * inv;
+          if (sum_all - sum_topk > 1e-5f) record_err(status, err_key(kPhTopk, t, 0, 0, kTkLeak));
+        }
+      }
+    }
     wait_stores();
     // ... and the last token to be selected groups the assignments
     if (tid == 0) last_tok = atomicAdd(&flags[1], 1) == T - 1;
@@ -272,7 +372,7 @@ hipError_t launch_front(const LayerDev& L, const float* x, int T, float* z, uint
                         int32_t* off, int32_t* perm, int2* units, int32_t* meta,
                         unsigned long long* status, hipStream_t st) {
   if (!front_supported(L, T)) return hipErrorInvalidValue;
-  const size_t sel = (size_t)(((L.E + 3) & ~3) + 4) * sizeof(float);
+  const size_t sel = (size_t)(((L.E + 3) & ~3) + 8) * sizeof(float);
   const size_t bld = (size_t)(2 * L.E + 64) * sizeof(int);
   const size_t xs = (size_t)L.H * sizeof(float);
   const size_t lds = sel > bld ? (sel > xs ? sel : xs) : (bld > xs ? bld : xs);
