@@ -615,10 +615,12 @@ __device__ __forceinline__ void norm_sum_squares(const float4 (&xr)[2][2], int H
 // reference's order, src/layers/rmsnorm.mojo:41-44).
 template <int GQW, int R, int NORM>
 __global__ __launch_bounds__(kThreads) void k_moe_decode(
-    LayerDev L, DecodePlan P, const float* __restrict__ x, const float* __restrict__ residual,
-    float* __restrict__ y, int32_t* __restrict__ ids_out, float* __restrict__ probs_out,
-    float* __restrict__ shg_out, DecodeSync S, unsigned long long* status, int token,
-    NormSpec nm, unsigned long long* status_out) {
+    const float* __restrict__ x, const uint16_t* __restrict__ router,
+    const float* __restrict__ gamma, int H_, int E_, int nx_, int nrw_, int nb_, LayerDev L,
+    DecodePlan P,
+    const float* __restrict__ residual, float* __restrict__ y, int32_t* __restrict__ ids_out,
+    float* __restrict__ probs_out, float* __restrict__ shg_out, DecodeSync S,
+    unsigned long long* status, int token, NormSpec nm, unsigned long long* status_out) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   float* xt = reinterpret_cast<float*>(smem + P.off_xt);
   uint4* xb2 = reinterpret_cast<uint4*>(smem + P.off_xb);
@@ -630,7 +632,7 @@ __global__ __launch_bounds__(kThreads) void k_moe_decode(
               reinterpret_cast<float*>(sel + 256), reinterpret_cast<float*>(sel + 400),
               reinterpret_cast<float*>(sel + 512)};
 
-  const int H = L.H, K = L.K, E = L.E;
+  const int H = H_, K = L.K, E = E_;  // (preloaded entry arguments)
   const int b = blockIdx.x, nb = gridDim.x;
   const int tid = threadIdx.x, w = wave_id(), lane = tid & 63;
   const int q = lane >> 4, j = lane & 15;
@@ -654,7 +656,7 @@ __global__ __launch_bounds__(kThreads) void k_moe_decode(
   auto load_rw = [&]() {
     if (router_wg && tid < kRouterRows * 16) {
       const uint4* wp =
-          reinterpret_cast<const uint4*>(L.router + r16_index(H, min(re, E), tid & 15));
+          reinterpret_cast<const uint4*>(router + r16_index(H, min(re, E), tid & 15));
 #pragma unroll
       for (int j8 = 0; j8 < kRwMax; ++j8) rw[j8] = wp[(size_t)min(j8, H / 128 - 1) * 16];
     }
@@ -672,8 +674,8 @@ __global__ __launch_bounds__(kThreads) void k_moe_decode(
 #pragma unroll
     for (int ii = 0; ii < 2; ++ii) {
       const int i = min(tid + kThreads * ii, H / 8 - 1);
-      gr[ii][0] = reinterpret_cast<const float4*>(nm.gamma)[2 * i];
-      gr[ii][1] = reinterpret_cast<const float4*>(nm.gamma)[2 * i + 1];
+      gr[ii][0] = reinterpret_cast<const float4*>(gamma)[2 * i];
+      gr[ii][1] = reinterpret_cast<const float4*>(gamma)[2 * i + 1];
     }
     load_rw();
   }
@@ -745,7 +747,7 @@ __global__ __launch_bounds__(kThreads) void k_moe_decode(
       const int e2 = rr * kRouterRows + (tid >> 4);
       {
         const uint4* wp =
-            reinterpret_cast<const uint4*>(L.router + r16_index(H, min(e2, E), tid & 15));
+            reinterpret_cast<const uint4*>(router + r16_index(H, min(e2, E), tid & 15));
 #pragma unroll
         for (int j8 = 0; j8 < kRwMax; ++j8) rw[j8] = wp[(size_t)min(j8, H / 128 - 1) * 16];
       }
@@ -1050,68 +1052,34 @@ __device__ unsigned long long g_phase_trace[kTraceSlots * 256 * kTracePoints];
 
 template <int GQW, int R, int NORM>
 __global__ __launch_bounds__(kThreads) void k_moe_decode_xs(
-    LayerDev L, DecodePlan P, const float* __restrict__ x, const float* __restrict__ residual,
-    float* __restrict__ y, int32_t* __restrict__ ids_out, float* __restrict__ probs_out,
-    float* __restrict__ shg_out, DecodeSync S, unsigned long long* status, int token,
-    NormSpec nm, unsigned long long* status_out) {
+    const float* __restrict__ x, const uint16_t* __restrict__ router,
+    const float* __restrict__ gamma, int H_, int E_, int nx_, int nrw_, int nb_, LayerDev L,
+    DecodePlan P,
+    const float* __restrict__ residual, float* __restrict__ y, int32_t* __restrict__ ids_out,
+    float* __restrict__ probs_out, float* __restrict__ shg_out, DecodeSync S,
+    unsigned long long* status, int token, NormSpec nm, unsigned long long* status_out) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   DM_TR(0);
-  float* xt = reinterpret_cast<float*>(smem + P.off_xt);
-  uint4* xb2 = reinterpret_cast<uint4*>(smem + P.off_xb);
-  float* red = reinterpret_cast<float*>(smem + P.off_red);
-  float* yred = reinterpret_cast<float*>(smem + P.off_yred);
-  float* fin = reinterpret_cast<float*>(smem + P.off_fin);
-  uint16_t* hbh = reinterpret_cast<uint16_t*>(smem + P.off_hb);  // [npx][128] bf16 hi
-  uint16_t* hbl = hbh + (size_t)P.xs_npx * kQuadCols;             // [npx][128] bf16 lo
-  unsigned char* sel = smem + P.off_sel;
-  SelState st{reinterpret_cast<float*>(smem + P.off_zv), reinterpret_cast<float*>(smem + P.off_ev),
-              reinterpret_cast<int*>(sel), reinterpret_cast<int*>(sel + 128),
-              reinterpret_cast<float*>(sel + 256), reinterpret_cast<float*>(sel + 400),
-              reinterpret_cast<float*>(sel + 512)};
-
-  const int H = L.H, K = L.K, E = L.E;
-  const int b = blockIdx.x, nb = gridDim.x;
+  // ---- entry: router rows, x, gamma (with the norm: x, gamma, router
+  // rows, as in the original form), requested first, from the preloaded
+  // leading arguments only --------------------------------------------------
+  const int H = H_, E = E_;
+  const int b = blockIdx.x, nb = nb_;
   const int tid = threadIdx.x, w = wave_id(), lane = tid & 63;
-  const int q = lane >> 4, j = lane & 15;
-  const unsigned n = S.n;
   // The dispatcher hands workgroups to the XCDs in rotation, starting at an
   // XCD that varies from launch to launch: the XCD a workgroup runs on is
   // read from the hardware, and b / nx numbers the workgroups of one XCD.
-  const int nx = P.xs_nx, nmx = nb / nx;
-  const int xc = (int)xcc_id(), m = b / nx;
-  const int nT = L.I / kQuadCols, KT = K * nT, NP = KT + L.Ish / kQuadCols;
-  const int npx = NP > xc ? (NP - xc + nx - 1) / nx : 0;   // pairs of this XCD
-  const int nrpx = KT > xc ? (KT - xc + nx - 1) / nx : 0;  // routed ones (they come first)
-  const int ntr = nrpx * 8;  // routed gate/up tiles of 16 rows on this XCD
-  const int rpw = P.xs_rpw, rb0 = m * rpw, nrt = H / kTileRows;
-  const int my_rt = max(0, min(rpw, nrt - rb0));  // output tiles of this workgroup
-  // this wave's down tiles: items jj = 0, 1, ...: output tile rb0 + ri of
-  // pair lp0 + lstep*jj (rpw divides the wave count, so ri is fixed)
-  const int ri = w & (rpw - 1), lp0 = w / rpw, lstep = kWaves / rpw;
-  const int nit = (ri < my_rt && lp0 < npx) ? (npx - lp0 + lstep - 1) / lstep : 0;
-  const int nit_r = (ri < my_rt && lp0 < nrpx) ? min(nit, (nrpx - lp0 + lstep - 1) / lstep) : 0;
-  const int nit_s = nit - nit_r;  // the plan keeps nit_r <= kXsR and nit_s <= kXsS
-  const int rbc = min(rb0 + ri, nrt - 1);  // a valid output tile for unused load slots
+  const int nx = nx_, nmx = nb / nx, m = b / nx;
   // router rows of this workgroup: every XCD forms all E+1 logits itself, so
   // routing needs no hand-off between XCDs; wave w < nrw, lane group g owns
   // row m + nmx*(4w + g)
-  const int nrw = P.xs_nrw;
-  const int zs = 256 * R + 64;            // logit words per XCD
-  uint64_t* zl = S.zt + (size_t)xc * zs;  // this XCD's logits
-  if (xc >= nx) {  // (never: the count was probed on this device)
-    if (tid == 0) record_err(status, err_key(kPhSync, 0, 0, 1, 0));
-    end_workgroup(status, status_out);
-    return;
-  }
-
-  // ---- entry: router rows, x, gamma (with the norm: x, gamma, router
-  // rows, as in the original form) ---------------------------------------------
+  const int nrw = nrw_;
   uint4 rw[kRwMax];
   const int re = m + nmx * (4 * w + (lane >> 4));
   auto load_rw = [&]() {
     if (w < nrw) {
       const uint4* wp =
-          reinterpret_cast<const uint4*>(L.router + r16_index(H, min(re, E), lane & 15));
+          reinterpret_cast<const uint4*>(router + r16_index(H, min(re, E), lane & 15));
 #pragma unroll
       for (int j8 = 0; j8 < kRwMax; ++j8) rw[j8] = wp[(size_t)min(j8, H / 128 - 1) * 16];
     }
@@ -1129,11 +1097,49 @@ __global__ __launch_bounds__(kThreads) void k_moe_decode_xs(
 #pragma unroll
     for (int ii = 0; ii < 2; ++ii) {
       const int i = min(tid + kThreads * ii, H / 8 - 1);
-      gr[ii][0] = reinterpret_cast<const float4*>(nm.gamma)[2 * i];
-      gr[ii][1] = reinterpret_cast<const float4*>(nm.gamma)[2 * i + 1];
+      gr[ii][0] = reinterpret_cast<const float4*>(gamma)[2 * i];
+      gr[ii][1] = reinterpret_cast<const float4*>(gamma)[2 * i + 1];
     }
     load_rw();
   }
+  float* xt = reinterpret_cast<float*>(smem + P.off_xt);
+  uint4* xb2 = reinterpret_cast<uint4*>(smem + P.off_xb);
+  float* red = reinterpret_cast<float*>(smem + P.off_red);
+  float* yred = reinterpret_cast<float*>(smem + P.off_yred);
+  float* fin = reinterpret_cast<float*>(smem + P.off_fin);
+  uint16_t* hbh = reinterpret_cast<uint16_t*>(smem + P.off_hb);  // [npx][128] bf16 hi
+  uint16_t* hbl = hbh + (size_t)P.xs_npx * kQuadCols;             // [npx][128] bf16 lo
+  unsigned char* sel = smem + P.off_sel;
+  SelState st{reinterpret_cast<float*>(smem + P.off_zv), reinterpret_cast<float*>(smem + P.off_ev),
+              reinterpret_cast<int*>(sel), reinterpret_cast<int*>(sel + 128),
+              reinterpret_cast<float*>(sel + 256), reinterpret_cast<float*>(sel + 400),
+              reinterpret_cast<float*>(sel + 512)};
+
+  const int K = L.K;
+  const int q = lane >> 4, j = lane & 15;
+  const unsigned n = S.n;
+  const int xc = (int)xcc_id();
+  const int nT = L.I / kQuadCols, KT = K * nT, NP = KT + L.Ish / kQuadCols;
+  const int npx = NP > xc ? (NP - xc + nx - 1) / nx : 0;   // pairs of this XCD
+  const int nrpx = KT > xc ? (KT - xc + nx - 1) / nx : 0;  // routed ones (they come first)
+  const int ntr = nrpx * 8;  // routed gate/up tiles of 16 rows on this XCD
+  const int rpw = P.xs_rpw, rb0 = m * rpw, nrt = H / kTileRows;
+  const int my_rt = max(0, min(rpw, nrt - rb0));  // output tiles of this workgroup
+  // this wave's down tiles: items jj = 0, 1, ...: output tile rb0 + ri of
+  // pair lp0 + lstep*jj (rpw divides the wave count, so ri is fixed)
+  const int ri = w & (rpw - 1), lp0 = w / rpw, lstep = kWaves / rpw;
+  const int nit = (ri < my_rt && lp0 < npx) ? (npx - lp0 + lstep - 1) / lstep : 0;
+  const int nit_r = (ri < my_rt && lp0 < nrpx) ? min(nit, (nrpx - lp0 + lstep - 1) / lstep) : 0;
+  const int nit_s = nit - nit_r;  // the plan keeps nit_r <= kXsR and nit_s <= kXsS
+  const int rbc = min(rb0 + ri, nrt - 1);  // a valid output tile for unused load slots
+  const int zs = 256 * R + 64;            // logit words per XCD
+  uint64_t* zl = S.zt + (size_t)xc * zs;  // this XCD's logits
+  if (xc >= nx) {  // (never: the count was probed on this device)
+    if (tid == 0) record_err(status, err_key(kPhSync, 0, 0, 1, 0));
+    end_workgroup(status, status_out);
+    return;
+  }
+
   const size_t matS = (size_t)L.Ish * H;
   const ExpertView sgv = {L.sgu_nib, L.sgu_sc, L.Ish, H};
   const ExpertView suv = {L.sgu_nib + matS / 2, L.sgu_sc + matS / kGroup, L.Ish, H};
@@ -1625,8 +1631,16 @@ hipError_t launch_moe_decode(const LayerDev& L, const DecodePlan& P, const float
   NormSpec nc = nm;
   const float* xc = x;
   const float* rc = residual;
-  void* args[] = {&Lc, &Pc,     &xc,    &rc, &y,         &ids, &probs,
-                  &shg, &Sc, &status, &token, &nc, &status_out};
+  // The arguments every workgroup needs for its first loads come first:
+  // gfx950 preloads the leading kernel arguments into scalar registers
+  // (dm_decode.hip is compiled with -amdgpu-kernarg-preload-count), so the
+  // loads of x, gamma and the router rows are issued without waiting for a
+  // read of the argument segment, which the host has just written.
+  const uint16_t* router = L.router;
+  const float* gamma = nm.gamma;
+  int eH = L.H, eE = L.E, enx = P.xs_nx, enrw = P.xs_nrw, enb = P.grid;
+  void* args[] = {&xc,  &router, &gamma, &eH,    &eE,  &enx, &enrw,   &enb,   &Lc, &Pc,
+                  &rc,  &y,      &ids,   &probs, &shg, &Sc,  &status, &token, &nc, &status_out};
   // Every workgroup waits for words other workgroups publish, so all of them
   // must be resident at once.  A cooperative launch guarantees it (or fails
   // at launch) but costs about 18 us more per launch than the plain one on
