@@ -801,8 +801,14 @@ __device__ __forceinline__ bool poll8(const uint64_t* p, unsigned tag, long limi
 }
 
 template <int T, int R>
+// The leading arguments (what the routing and shared-expert tasks need for
+// their first loads) are preloaded into scalar registers at dispatch
+// (dm_gguf.hip is compiled with -amdgpu-kernarg-preload-count): those loads
+// are issued without waiting for a read of the argument segment.
 __global__ __launch_bounds__(512) void k_gguf_one(
-    GgufMoeDev L, const float* __restrict__ x, int nR, uint64_t* zt, uint64_t* sel,
+    const float* __restrict__ x, const float* __restrict__ rchain_, const uint8_t* raw_,
+    const int64_t* off_, int H_, int E_, int Ish_, int nR, GgufMoeDev Lk, uint64_t* zt,
+    uint64_t* sel,
     uint64_t* soft, uint64_t* hsh, const float* __restrict__ residual, float* __restrict__ y,
     int32_t* __restrict__ ids, float* __restrict__ probs, float* __restrict__ shg,
     float* __restrict__ h, int ldh, unsigned* hcnt, unsigned target, unsigned launch,
@@ -813,6 +819,13 @@ __global__ __launch_bounds__(512) void k_gguf_one(
   __shared__ float sev[256 * R];
   __shared__ float sp[8];
   __shared__ int sslot[8], sid[8];
+  GgufMoeDev L = Lk;  // the entry fields from the preloaded arguments
+  L.H = H_;
+  L.E = E_;
+  L.Ish = Ish_;
+  L.rchain = rchain_;
+  L.raw = raw_;
+  L.off = off_;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int wid = __builtin_amdgcn_readfirstlane(w);  // w as a uniform value
   const int G = (int)gridDim.x, b = (int)blockIdx.x;
@@ -1199,7 +1212,8 @@ hipError_t launch_gguf_one_token(const GgufMoeDev& L, const float* x, const floa
   float* h = reinterpret_cast<float*>(sb + kSyncHead + zt_bytes(L) + hsh_bytes(L));
   const unsigned target = launch * (unsigned)(L.I / 16);  // blocks per slot
 #define DM_ONE(TY, R)                                                                          \
-  k_gguf_one<TY, R><<<grid, 512, 0, st>>>(L, x, nR, zt, sel, soft, hsh, residual, y, ids, probs, \
+  k_gguf_one<TY, R><<<grid, 512, 0, st>>>(x, L.rchain, L.raw, L.off, L.H, L.E, L.Ish, nR, L, zt, \
+                                          sel, soft, hsh, residual, y, ids, probs,             \
                                           shg, h, L.I, hcnt, target, launch, status, spin)
 #define DM_ONE_R(TY)    \
   if (L.E <= 256) {     \
