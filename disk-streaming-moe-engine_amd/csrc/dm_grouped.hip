@@ -199,7 +199,9 @@ hipError_t launch_group_build(const int32_t* ids, int T, int K, int E, int32_t* 
 // counter is reset by the workgroup that saw it complete.  No workgroup
 // waits for another.
 template <int NE>
-__global__ __launch_bounds__(1024) void k_front(LayerDev L, const float* __restrict__ x, int T,
+__global__ __launch_bounds__(1024) void k_front(const float* __restrict__ x,
+                                                const uint16_t* __restrict__ router_, int H_,
+                                                int E_, LayerDev Lk, int T,
                                                 float* __restrict__ z, uint4* __restrict__ xhi,
                                                 uint4* __restrict__ xlo, int* flags,
                                                 int32_t* __restrict__ ids,
@@ -211,6 +213,10 @@ __global__ __launch_bounds__(1024) void k_front(LayerDev L, const float* __restr
                                                 unsigned long long* status) {
   extern __shared__ __attribute__((aligned(16))) float fl[];
   __shared__ int last, last_tok;
+  LayerDev L = Lk;  // the entry fields from the preloaded leading arguments
+  L.H = H_;
+  L.E = E_;
+  L.router = router_;
   const int tid = threadIdx.x, H = L.H, E = L.E, t = blockIdx.y;
   const float* xr = x + (size_t)t * H;
   bool bad = false;
@@ -381,8 +387,8 @@ hipError_t launch_front(const LayerDev& L, const float* x, int T, float* z, uint
   uint4* lo = reinterpret_cast<uint4*>(xlo);
   const int ne = (L.E + 63) / 64;
 #define DM_FRONT(N)                                                                             \
-  hipLaunchKernelGGL(k_front<N>, grid, dim3(1024), lds, st, L, x, T, z, hi, lo, flags, ids, probs, \
-                     shg, off, perm, units, meta, status)
+  hipLaunchKernelGGL(k_front<N>, grid, dim3(1024), lds, st, x, L.router, L.H, L.E, L, T, z, hi, \
+                     lo, flags, ids, probs, shg, off, perm, units, meta, status)
   if (ne <= 1) DM_FRONT(1);
   else if (ne <= 2) DM_FRONT(2);
   else if (ne <= 4) DM_FRONT(4);
@@ -1097,13 +1103,28 @@ __device__ __forceinline__ void down_small_part(const GroupArgs& g, int bx, int 
   down_epilogue<kSmallTiles, 1>(g, ut, I, row0, q, j, acc, aa);
 }
 
+// The grouping's arrays come first among the arguments: they start each
+// workgroup's chain of dependent loads (meta -> units -> off -> perm) and
+// are preloaded into scalar registers at dispatch.
 __global__ __launch_bounds__(kGThreads) __attribute__((amdgpu_waves_per_eu(3))) void k_gu_small(
-    GroupArgs g) {
+    const int32_t* meta, const int2* units, const int32_t* off, const int32_t* perm,
+    GroupArgs gk) {
+  GroupArgs g = gk;
+  g.meta = meta;
+  g.units = units;
+  g.off = off;
+  g.perm = perm;
   gu_small_part(g, blockIdx.x, blockIdx.y, gwave_id());
 }
 
 __global__ __launch_bounds__(kGThreads) __attribute__((amdgpu_waves_per_eu(3))) void k_down_small(
-    GroupArgs g) {
+    const int32_t* meta, const int2* units, const int32_t* off, const int32_t* perm,
+    GroupArgs gk) {
+  GroupArgs g = gk;
+  g.meta = meta;
+  g.units = units;
+  g.off = off;
+  g.perm = perm;
   down_small_part(g, blockIdx.x, blockIdx.y, gwave_id());
 }
 
@@ -1147,9 +1168,11 @@ hipError_t launch_experts_grouped(const LayerDev& L, const uint16_t* xhi, const 
                        st, g, bg, wg_g, nsmall, gy);
     hipLaunchKernelGGL(k_big<false>, dim3(wg_d), dim3(kB2Threads), kB2Lds, st, g, bd, wg_d, 0, 0);
   } else {
-    hipLaunchKernelGGL(k_gu_small, dim3(nsmall, gy), dim3(kGThreads), 0, st, g);
+    hipLaunchKernelGGL(k_gu_small, dim3(nsmall, gy), dim3(kGThreads), 0, st, meta, units, off, perm,
+                       g);
   }
-  hipLaunchKernelGGL(k_down_small, dim3(nsmall, dy), dim3(kGThreads), 0, st, g);
+  hipLaunchKernelGGL(k_down_small, dim3(nsmall, dy), dim3(kGThreads), 0, st, meta, units, off,
+                     perm, g);
   return hipGetLastError();
 }
 
