@@ -10,7 +10,10 @@ k_moe_decode_xs and prints, per layer and as medians over the layers, the
 time of each point from the layer's first workgroup start (median over the
 workgroups, and the last workgroup).
 
-    python3 disk-streaming-moe-engine_amd/phase_trace.py [--norm ref|tree] [--tokens N]
+    python3 disk-streaming-moe-engine_amd/phase_trace.py [--norm ref|tree|none] [--tokens N]
+
+--norm none traces the single-layer decode instead (one layer, no norm,
+dmh_moe_forward on device pointers, the bench's default workload).
 """
 import argparse
 import ctypes as C
@@ -30,7 +33,7 @@ CLOCK_MHZ = 100.0  # wall_clock64
 
 def main():
     ap = argparse.ArgumentParser()
-    ap.add_argument("--norm", default="ref", choices=["ref", "tree"])
+    ap.add_argument("--norm", default="ref", choices=["ref", "tree", "none"])
     ap.add_argument("--tokens", type=int, default=20)
     ap.add_argument("--layers", type=int, default=40)
     a = ap.parse_args()
@@ -49,7 +52,7 @@ def main():
     fetch.argtypes = [C.c_void_p, C.c_size_t]
     fetch.restype = C.c_int
     cfg = synth.CONFIG_QWEN36
-    nl = a.layers
+    nl = 1 if a.norm == "none" else a.layers
     dims = (cfg["hidden"], cfg["num_experts"], cfg["top_k"], cfg["inter"], cfg["inter_sh"])
     for l in range(nl):
         W = synth.make_layer_device(**cfg, seed=1000 + l, device=dev)
@@ -61,8 +64,18 @@ def main():
     x = torch.from_numpy(synth.make_activations(np.random.default_rng(7), (a.tokens, H))).to(dev)
     y = torch.empty_like(x)
     torch.cuda.synchronize()
-    for t in range(a.tokens):  # the last token's launches leave their stamps
-        blk.forward_stack_device(x[t].data_ptr(), 0, nl, 1, y[t].data_ptr(), tree=a.norm == "tree")
+    if a.norm == "none":
+        K = cfg["top_k"]
+        ids = torch.empty((a.tokens, K), dtype=torch.int32, device=dev)
+        pr = torch.empty((a.tokens, K), dtype=torch.float32, device=dev)
+        sg = torch.empty((a.tokens,), dtype=torch.float32, device=dev)
+        for t in range(a.tokens):
+            blk.forward_device(0, x[t].data_ptr(), 1, y[t].data_ptr(), ids[t].data_ptr(),
+                               pr[t].data_ptr(), sg[t].data_ptr())
+    else:
+        for t in range(a.tokens):  # the last token's launches leave their stamps
+            blk.forward_stack_device(x[t].data_ptr(), 0, nl, 1, y[t].data_ptr(),
+                                     tree=a.norm == "tree")
     blk.sync()
     buf = np.zeros(SLOTS * WGS * POINTS, np.uint64)
     rc = fetch(C.c_void_p(buf.ctypes.data), buf.nbytes)
@@ -71,9 +84,11 @@ def main():
     tr = buf.reshape(SLOTS, WGS, POINTS)[:nl].astype(np.int64)
     base = tr[:, :, 0].min(axis=1)
     rows = []
+    # points no launch stored (the norm's, without a norm) are left out
+    names = {k: nm for k, nm in NAMES.items() if (tr[:, :, k] > 0).all()}
     for l in range(nl):
         r = {"layer": l, "start_spread_us": round(float((tr[l, :, 0].max() - base[l]) / CLOCK_MHZ), 2)}
-        for k, nm in NAMES.items():
+        for k, nm in names.items():
             d = (tr[l, :, k] - base[l]) / CLOCK_MHZ
             r[nm] = [round(float(np.median(d)), 2), round(float(d.max()), 2)]
         if l + 1 < nl:
@@ -83,9 +98,10 @@ def main():
     for r in rows:
         print(json.dumps(r))
     lay = [r["layer_us"] for r in rows if "layer_us" in r]
-    print(f"median layer start-to-start us {np.median(lay):.2f}; first to last start "
-          f"{(base[-1] - base[0]) / CLOCK_MHZ:.2f} us")
-    for k, nm in NAMES.items():
+    if lay:
+        print(f"median layer start-to-start us {np.median(lay):.2f}; first to last start "
+              f"{(base[-1] - base[0]) / CLOCK_MHZ:.2f} us")
+    for k, nm in names.items():
         med = np.median([r[nm][0] for r in rows])
         mx = np.median([r[nm][1] for r in rows])
         print(f"{nm:>18}: median {med:.2f} us (median over layers of the last workgroup {mx:.2f})")
