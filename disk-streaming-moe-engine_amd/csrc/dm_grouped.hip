@@ -822,10 +822,19 @@ __device__ __forceinline__ BigItem big_next_item(const GroupArgs& g, int& idx, i
 // Workgroups from big_wgs on run the small units of the same stage (sx x sy
 // four-wave parts, two per workgroup): dispatched after every big one, they
 // fill the CUs the big items' last round leaves idle.
+// (The grouping's arrays lead the arguments, preloaded at dispatch: they
+// start each workgroup's chain of dependent loads.)
 template <bool GU>
 __global__ __launch_bounds__(kB2Threads) __attribute__((amdgpu_waves_per_eu(2, 2)))
-void k_big(GroupArgs g, int items, int big_wgs, int sx, int sy) {
+void k_big(int items, int big_wgs, const int32_t* meta, const int2* units, const int32_t* off,
+           const int32_t* perm, const int* need_lo, GroupArgs gk, int sx, int sy) {
   extern __shared__ __attribute__((aligned(16))) unsigned char lds2[];
+  GroupArgs g = gk;
+  g.meta = meta;
+  g.units = units;
+  g.off = off;
+  g.perm = perm;
+  g.need_lo = need_lo;
   if ((int)blockIdx.x >= big_wgs) {
     const int w = gwave_id();
     const int s = 2 * ((int)blockIdx.x - big_wgs) + (w >> 2);
@@ -1165,8 +1174,9 @@ hipError_t launch_experts_grouped(const LayerDev& L, const uint16_t* xhi, const 
     const int pw = L.H >= 256 ? big_persistent_wgs() : 0;
     const int wg_g = pw > 0 && pw < bg ? pw : bg, wg_d = pw > 0 && pw < bd ? pw : bd;
     hipLaunchKernelGGL(k_big<true>, dim3(wg_g + (nsmall * gy + 1) / 2), dim3(kB2Threads), kB2Lds,
-                       st, g, bg, wg_g, nsmall, gy);
-    hipLaunchKernelGGL(k_big<false>, dim3(wg_d), dim3(kB2Threads), kB2Lds, st, g, bd, wg_d, 0, 0);
+                       st, bg, wg_g, meta, units, off, perm, need_lo, g, nsmall, gy);
+    hipLaunchKernelGGL(k_big<false>, dim3(wg_d), dim3(kB2Threads), kB2Lds, st, bd, wg_d, meta,
+                       units, off, perm, need_lo, g, 0, 0);
   } else {
     hipLaunchKernelGGL(k_gu_small, dim3(nsmall, gy), dim3(kGThreads), 0, st, meta, units, off, perm,
                        g);

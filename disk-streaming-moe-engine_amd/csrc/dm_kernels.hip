@@ -393,10 +393,11 @@ __device__ __forceinline__ void lds_wait_steps4(f32x4 (&v)[4]) {
 }
 template <int NJ8>
 __global__ __launch_bounds__(256) void k_router_rows(
-    LayerDev L, const float* __restrict__ x, int T,
-                                                     int tpw, float* __restrict__ z,
-                                                     unsigned long long* status,
-                                                     const int* __restrict__ gate) {
+    const float* __restrict__ x, const int* __restrict__ gate, const uint16_t* __restrict__ router_,
+    int E_, int T, int tpw, LayerDev Lk, float* __restrict__ z, unsigned long long* status) {
+  LayerDev L = Lk;  // the entry fields from the preloaded leading arguments
+  L.router = router_;
+  L.E = E_;
   extern __shared__ __attribute__((aligned(16))) float xs4[];  // [H][kRdTok]
   if (gate && gate[0] == 0) return;  // uniform: k_router_mfma computed these logits
   constexpr int H = NJ8 * 128;
@@ -495,13 +496,17 @@ hipError_t launch_router_dec(const LayerDev& L, const float* x, int T, float* z,
     const size_t lds = (size_t)L.H * kRdTok * sizeof(float);
     const dim3 g(blocks, ty);
     if (nj8 == 16)
-      hipLaunchKernelGGL(k_router_rows<16>, g, dim3(256), lds, st, L, x, T, tpw, z, status, gate);
+      hipLaunchKernelGGL(k_router_rows<16>, g, dim3(256), lds, st, x, gate, L.router, L.E, T, tpw,
+                         L, z, status);
     else if (nj8 == 8)
-      hipLaunchKernelGGL(k_router_rows<8>, g, dim3(256), lds, st, L, x, T, tpw, z, status, gate);
+      hipLaunchKernelGGL(k_router_rows<8>, g, dim3(256), lds, st, x, gate, L.router, L.E, T, tpw,
+                         L, z, status);
     else if (nj8 == 4)
-      hipLaunchKernelGGL(k_router_rows<4>, g, dim3(256), lds, st, L, x, T, tpw, z, status, gate);
+      hipLaunchKernelGGL(k_router_rows<4>, g, dim3(256), lds, st, x, gate, L.router, L.E, T, tpw,
+                         L, z, status);
     else
-      hipLaunchKernelGGL(k_router_rows<2>, g, dim3(256), lds, st, L, x, T, tpw, z, status, gate);
+      hipLaunchKernelGGL(k_router_rows<2>, g, dim3(256), lds, st, x, gate, L.router, L.E, T, tpw,
+                         L, z, status);
     return hipGetLastError();
   }
   const int ty = T < 256 ? T : 256;  // workgroups loop over the tokens beyond
@@ -532,9 +537,15 @@ hipError_t launch_router_dec(const LayerDev& L, const float* x, int T, float* z,
 // ===========================================================================
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-__global__ __launch_bounds__(256) void k_router_mfma(LayerDev L, const uint16_t* __restrict__ xhi,
-                                                      const int* __restrict__ need_lo, int T,
+__global__ __launch_bounds__(256) void k_router_mfma(const uint16_t* __restrict__ xhi,
+                                                      const int* __restrict__ need_lo,
+                                                      const uint16_t* __restrict__ router_, int H_,
+                                                      int E_, int T, LayerDev Lk,
                                                       float* __restrict__ z) {
+  LayerDev L = Lk;  // the entry fields from the preloaded leading arguments
+  L.router = router_;
+  L.H = H_;
+  L.E = E_;
   extern __shared__ __attribute__((aligned(16))) uint16_t xs_chain[];
   uint16_t* xs = xs_chain;
   if (need_lo[0] != 0) return;  // uniform: k_router_dec takes these tokens
@@ -705,7 +716,7 @@ hipError_t launch_router_mfma(const LayerDev& L, const uint16_t* xhi, const int*
                               float* z, hipStream_t st) {
   const size_t lds = (size_t)16 * (16 * (L.H / 16) + 8) * sizeof(uint16_t);
   hipLaunchKernelGGL(k_router_mfma, dim3((L.E + 63) / 64 + 1, (T + 15) / 16), dim3(256), lds, st,
-                     L, xhi, need_lo, T, z);
+                     xhi, need_lo, L.router, L.H, L.E, T, L, z);
   return hipGetLastError();
 }
 
