@@ -481,6 +481,18 @@ hipError_t run_block(dmh_ctx* ctx, Layer* Ly, int layer, const float* dx, const 
   const bool fused = Ly->fused && allow_fused && T == 1 && cap == hipStreamCaptureStatusNone;
   const dm::NormSpec no_norm{0.0f, nullptr, 0};
   const bool norm = nm && nm->eps > 0.0f;
+  if (Ly->fused && allow_fused && cap == hipStreamCaptureStatusNone && !norm && T >= 2 &&
+      T <= dm::kTokMaxT && Ly->plan.tok && T <= Ly->plan.xs_nx &&
+      Ly->plan.tok_lds_bytes <= 65536) {
+    // a few tokens: each one's whole block on one XCD, in one launch
+    if (Ly->launches >= (1u << 24) && (e = reset_counters(ctx, Ly)) != hipSuccess) return e;
+    dm::DecodeSync S = dm::decode_sync_carve(L, Ly->plan, Ly->sync);
+    S.n = ++Ly->launches;
+    S.spin = ctx->spin_limit;
+    S.trace = layer;
+    return dm::launch_moe_tokens(L, Ly->plan, dx, T, dres, dy, dids, dprobs, dshg, S, status, st,
+                                 g_live_ctx[ctx->device].load(std::memory_order_relaxed) > 1);
+  }
   if (fused) {
     for (int t = 0; t < T; ++t) {
       if (Ly->launches >= (1u << 24) && (e = reset_counters(ctx, Ly)) != hipSuccess) return e;
@@ -1188,12 +1200,21 @@ int moe_forward_impl(dmh_ctx* c, int layer, const float* x, const float* residua
   unsigned long long key;
   memcpy(&key, hout + o_key, 8);
   if (dm::key_phase(key) == dm::kPhExpert && dm::key_kind(key) == dm::kEkRecheck) {
-    // The fused kernel folds the routed and shared down projections into one
+    // The fused kernels fold the routed and shared down projections into one
     // sum, so a non-finite output does not say which check of the reference
     // fires first; the multi-kernel path keeps them apart and re-derives it.
     HIP_TRY(reset_status(c, layer));
     HIP_TRY(run_and_fetch(false));
     memcpy(&key, hout + o_key, 8);
+  } else if (sync_timeout(key)) {
+    // a wait of the several-token launch gave up: start the tags again and
+    // rerun the tokens on the multi-kernel path (as the single-token call does)
+    HIP_TRY(hipStreamSynchronize(st));
+    HIP_TRY(reset_counters(c, Ly));
+    HIP_TRY(reset_status(c, layer));
+    HIP_TRY(run_and_fetch(false));
+    memcpy(&key, hout + o_key, 8);
+    ++c->sync_fallbacks;
   }
   memcpy(y, hout + o_y, TH * 4);
   if (ids) memcpy(ids, hout + o_ids, TK * 4);

@@ -28,7 +28,16 @@ struct DecodePlan {
   int xs_npx;   // most pairs on one XCD
   int xs_nrw;   // waves per workgroup holding router rows (each XCD forms all logits)
   int off_fin;  // LDS: the final sum's gathered partials
+  // Several tokens in one launch (tok != 0, on top of the XCD-sliced form):
+  // token t on XCD t % nx, its whole block on that XCD's workgroups
+  // (launch_moe_tokens).  LDS: the sliced form's carve-up up to off_hb, then
+  // every pair's h (bf16 hi / lo) and the down tile's reduction.
+  int tok;
+  int tok_off_hb, tok_off_yred, tok_lds_bytes;
 };
+
+// Most tokens of one launch_moe_tokens launch (and at most the XCD count).
+constexpr int kTokMaxT = 8;
 
 // Cross-workgroup state of one layer: tagged words carry the launch index in
 // their high half, so a consumer polls the data itself.
@@ -38,6 +47,7 @@ struct DecodeSync {
   uint64_t* ht;  // [K+1][ldh] (tag, h), ldh = 2^ldh_log2 >= max(I, Ish)
   uint64_t* hl;  // XCD-sliced form: [pairs][64] packed h words (pack_h2), XCD-local
   uint64_t* pt;  // XCD-sliced form: [nx][H] (tag, partial output)
+  uint64_t* htk; // several-token form: [kTokMaxT][pairs][128] (tag, h), XCD-local
   unsigned n;    // launch index, >= 1 (the tag of this launch)
   long spin;     // polls of a wait before it gives up with a sync error
   int trace;     // phase-trace slot of the launch (the layer), -1: none; read only by
@@ -64,6 +74,14 @@ hipError_t probe_xcd_map(int num_cus, int* nx);
 // one r and n divides nwg, else 0.
 int xcd_rotation(const unsigned* xcd, int nwg);
 hipError_t decode_occupancy(const LayerDev& L, const DecodePlan& P, int* blocks_per_cu);
+// T tokens (2 <= T <= min(kTokMaxT, P.xs_nx), P.tok) in one launch of the
+// XCD-sliced grid: token t's routing, experts and combine on XCD t % nx
+// (every hand-off stays in that XCD's L2, nothing is summed across XCDs).
+// x, residual, y: [T][H]; ids, probs: [T][K]; shg: [T].  No norm.
+hipError_t launch_moe_tokens(const LayerDev& L, const DecodePlan& P, const float* x, int T,
+                             const float* residual, float* y, int32_t* ids, float* probs,
+                             float* shg, const DecodeSync& S, unsigned long long* status,
+                             hipStream_t st, bool cooperative);
 // nm.eps > 0: the router and experts see rmsnorm(x, nm.gamma, nm.eps) in the
 // order nm.seq selects (NormSpec).  cooperative: launch with
 // hipLaunchCooperativeKernel, which guarantees that every workgroup is

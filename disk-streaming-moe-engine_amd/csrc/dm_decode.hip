@@ -133,7 +133,9 @@ __device__ __forceinline__ void gu_load(const ExpertView& gv, const ExpertView& 
 
 // hdst: the tile's 8 hand-off words.  LOCAL: plain stores, read only by
 // workgroups on the same XCD (through its L2); otherwise agent-scope stores.
-template <int GQW, bool LOCAL = false>
+// WIDE: 16 plain (XCD-local) stores instead, one value each with the whole
+// launch tag ((tag << 32) | bits).
+template <int GQW, bool LOCAL = false, bool WIDE = false>
 __device__ __forceinline__ void gu_compute(const ExpertView& gv, int rb, const uint4 (&wg)[GQW],
                                            const uint4 (&wu)[GQW], const uint2 (&sg)[GQW],
                                            const uint2 (&su)[GQW], const uint4* xb2, float* red,
@@ -188,7 +190,9 @@ __device__ __forceinline__ void gu_compute(const ExpertView& gv, int rb, const u
     // of pack_h2); the partner's value comes from the neighbouring lane
     const float hn = __builtin_bit_cast(
         float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, h), 0xB1, 0xF, 0xF, true));
-    if ((r & 1) == 0) {
+    if (WIDE) {
+      st_l2_u64(hdst + r, ((uint64_t)tag << 32) | f2u(h));
+    } else if ((r & 1) == 0) {
       if (LOCAL)
         st_l2_u64(hdst + (r >> 1), pack_h2(tag, h, hn));
       else
@@ -1465,6 +1469,283 @@ __global__ __launch_bounds__(kThreads) void k_moe_decode_xs(
   end_workgroup(status, status_out);
 }
 
+// ---------------------------------------------------------------------------
+// Several tokens in one launch (launch_moe_tokens): the XCD-sliced grid, XCD
+// c taking token c (T <= nx) and its whole block on its own nmx = nb / nx
+// workgroups (workgroup m = b / nx of the XCD), so every hand-off stays in
+// that XCD's L2 and no partial output crosses XCDs:
+//   routing  as in k_moe_decode_xs: the XCD forms all E+1 logits and every
+//            workgroup selects the top k itself;
+//   gate/up  the token's NP pairs (a routed slot's or the shared expert's
+//            128-row slice of I) x 8 tiles of 16 rows: tasks m, m + nmx, ...
+//            of workgroup m, each task's loads issued before the previous
+//            task's products; h published XCD-locally, one tagged word per
+//            value;
+//   down     workgroup m owns the output tiles m rpw ..; wave w takes tile
+//            w % rpw and the pairs w / rpw, + kWaves / rpw, ... (A16 chunks
+//            kTokRing ahead, the first ones requested right after routing),
+//            with h of every pair staged in LDS scaled by its slot's weight
+//            (p_k, or the shared gate); y = the waves' sums (+ residual).
+// Routing is bit for bit that of the single-token kernels (the same chains,
+// tree and selection); the expert sums run in another order, within the
+// same tolerance.  Loads past a workgroup's or wave's last task read fixed
+// bytes of the shared expert instead (every such request hits the same
+// lines), so that no load is issued under a branch.
+constexpr int kTokHw = 12;   // h words per thread in the staging poll
+constexpr int kTokRing = 4;  // down chunks per wave in flight
+
+template <int GQW, int R>
+__global__ __launch_bounds__(kThreads) void k_moe_tokens(
+    const float* __restrict__ x, const uint16_t* __restrict__ router, int H_, int E_, int nx_,
+    int nrw_, int nb_, int T, LayerDev L, DecodePlan P, const float* __restrict__ residual,
+    float* __restrict__ y, int32_t* __restrict__ ids_out, float* __restrict__ probs_out,
+    float* __restrict__ shg_out, DecodeSync S, unsigned long long* status) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  const int H = H_, E = E_;
+  const int b = blockIdx.x, nb = nb_;
+  const int tid = threadIdx.x, w = wave_id(), lane = tid & 63;
+  const int nx = nx_, nmx = nb / nx, m = b / nx;
+  // router rows of this workgroup (as in k_moe_decode_xs)
+  const int nrw = nrw_;
+  const int re = m + nmx * (4 * w + (lane >> 4));
+  float* xt = reinterpret_cast<float*>(smem + P.off_xt);
+  uint4* xb2 = reinterpret_cast<uint4*>(smem + P.off_xb);
+  float* red = reinterpret_cast<float*>(smem + P.off_red);
+  float* yred = reinterpret_cast<float*>(smem + P.tok_off_yred);
+  const int K = L.K;
+  const int nT = L.I / kQuadCols, KT = K * nT, NP = KT + L.Ish / kQuadCols;
+  uint16_t* hbh = reinterpret_cast<uint16_t*>(smem + P.tok_off_hb);  // [NP][128] bf16 hi
+  uint16_t* hbl = hbh + (size_t)NP * kQuadCols;                      // [NP][128] bf16 lo
+  unsigned char* sel = smem + P.off_sel;
+  SelState st{reinterpret_cast<float*>(smem + P.off_zv), reinterpret_cast<float*>(smem + P.off_ev),
+              reinterpret_cast<int*>(sel), reinterpret_cast<int*>(sel + 128),
+              reinterpret_cast<float*>(sel + 256), reinterpret_cast<float*>(sel + 400),
+              reinterpret_cast<float*>(sel + 512)};
+  const int q = lane >> 4, j = lane & 15;
+  const unsigned n = S.n;
+  const int xc = (int)xcc_id();
+  const int rpw = P.xs_rpw, rb0 = m * rpw, nrt = H / kTileRows;
+  const int my_rt = max(0, min(rpw, nrt - rb0));  // output tiles of this workgroup
+  const int ri = w & (rpw - 1), lp0 = w / rpw, lstep = kWaves / rpw;
+  const int nit = (ri < my_rt && lp0 < NP) ? (NP - lp0 + lstep - 1) / lstep : 0;
+  const int rbc = min(rb0 + ri, nrt - 1);
+  const int zs = 256 * R + 64;
+  const int ntask = NP * (kQuadCols / kTileRows);
+  const size_t matI = (size_t)L.I * H, matD = (size_t)H * L.I, matS = (size_t)L.Ish * H;
+  const ExpertView sgv = {L.sgu_nib, L.sgu_sc, L.Ish, H};
+  const ExpertView suv = {L.sgu_nib + matS / 2, L.sgu_sc + matS / kGroup, L.Ish, H};
+  const ExpertView sdv = {L.sd_nib, L.sd_sc, H, L.Ish};
+  if (xc >= nx) {  // (never: the count was probed on this device)
+    if (tid == 0) record_err(status, err_key(kPhSync, 0, 0, 1, 0));
+    return;
+  }
+  // token t = xc (T <= nx: at most one token per XCD; the other XCDs' workgroups end here)
+  const int t = xc;
+  if (t >= T) return;
+  {
+    uint4 rw[kRwMax];
+    if (w < nrw) {
+      const uint4* wp =
+          reinterpret_cast<const uint4*>(router + r16_index(H, min(re, E), lane & 15));
+#pragma unroll
+      for (int j8 = 0; j8 < kRwMax; ++j8) rw[j8] = wp[(size_t)min(j8, H / 128 - 1) * 16];
+    }
+    uint64_t* zl = S.zt + (size_t)t * zs;                    // token t's logits
+    uint64_t* hk = S.htk + (size_t)t * NP * kQuadCols;       // token t's h words
+    const float* xg = x + (size_t)t * H;
+
+    // ---- x staged (chains: transposed fp32; MFMA: bf16 hi / lo) -------------
+    {
+      bool bad = false;
+#pragma unroll
+      for (int ii = 0; ii < 2; ++ii) {
+        const int i = tid + kThreads * ii;
+        if (i < H / 8) {
+          const float4 a = reinterpret_cast<const float4*>(xg)[2 * i];
+          const float4 c = reinterpret_cast<const float4*>(xg)[2 * i + 1];
+          const float f[8] = {a.x, a.y, a.z, a.w, c.x, c.y, c.z, c.w};
+#pragma unroll
+          for (int k2 = 0; k2 < 8; ++k2) bad |= !finite_f(f[k2]);
+          const int xts = H / 16 + 4;
+          float* dst = xt + (8 * (i & 1)) * xts + (i >> 1);
+#pragma unroll
+          for (int k2 = 0; k2 < 8; ++k2) dst[k2 * xts] = f[k2];
+          uint4 hi, lo;
+          split8(f, hi, lo);
+          xb2[2 * i + 0] = hi;
+          xb2[2 * i + 1] = lo;
+        }
+      }
+      if (bad && m == 0) record_err(status, err_key(kPhX, 0, 0, 0, 0));
+    }
+    __syncthreads();
+
+    // ---- router rows, then routing (as in k_moe_decode_xs) ---------------------
+    if (w < nrw) router_compute<true>(L, rw, re, xt, zl, n);
+    if (w == 0) {
+      const bool rok = route<R>(zl, n, E, K, st, m == 0, t, status, S.spin);
+      if (lane == 0) st.misc[2] = rok ? 1.0f : 0.0f;
+    } else if (w == kNormWave) {
+      softmax_exp<R>(zl, n, E, st, m == 0, t, status, S.spin);
+    }
+    __syncthreads();
+    const bool ok = st.misc[2] != 0.0f;
+
+    // ---- this wave's first down chunks (they need the routing only) ----------
+    auto dload = [&](int i, uint4& wv, uint2& sv) {
+      ExpertView dv = sdv;
+      int gq = 0;
+      if (i < nit) {
+        const int p = lp0 + lstep * i;
+        if (p < KT) {
+          const int e = __builtin_amdgcn_readfirstlane(st.ids[p / nT]);
+          dv = {L.d_nib + (size_t)e * (matD / 2), L.d_sc + (size_t)e * (matD / kGroup), H, L.I};
+          gq = p % nT;
+        } else {
+          gq = p - KT;
+        }
+      }
+      load_chunk_nt(dv, i < nit ? rbc : 0, gq, lane, wv, sv);
+    };
+    uint4 dw[kTokRing];
+    uint2 ds[kTokRing];
+#pragma unroll
+    for (int u = 0; u < kTokRing; ++u) dload(u, dw[u], ds[u]);
+
+    // ---- slot weights; ids / probs / gate of the token in one workgroup ------
+    if (w == kNormWave) {
+      softmax_sum<R>(E, K, st, m == 0, t, status);
+      if (m == nmx - 1)
+        finish_probs(E, K, st, true, t, status, ids_out + (size_t)t * K,
+                     probs_out + (size_t)t * K, shg_out + t);
+    }
+
+    // ---- gate/up tasks, each one's loads in flight during the previous one ---
+    auto tview = [&](int tr, ExpertView& gv, ExpertView& uv, int& rb, uint32_t& ph) {
+      gv = sgv;
+      uv = suv;
+      rb = 0;
+      ph = kPhShared;
+      if (tr < ntask) {
+        const int p = tr >> 3, r = tr & 7;
+        if (p < KT) {
+          const int e = __builtin_amdgcn_readfirstlane(st.ids[p / nT]);
+          gv = {L.gu_nib + (size_t)e * matI, L.gu_sc + (size_t)e * 2 * (matI / kGroup), L.I, H};
+          uv = {gv.nib + matI / 2, gv.sc + matI / kGroup, L.I, H};
+          rb = (p % nT) * 8 + r;
+          ph = kPhExpert;
+        } else {
+          rb = (p - KT) * 8 + r;
+        }
+      }
+    };
+    {
+      uint4 gA[GQW], uA[GQW], gB[GQW], uB[GQW];
+      uint2 sgA[GQW], suA[GQW], sgB[GQW], suB[GQW];
+      ExpertView gvA, uvA, gvB, uvB;
+      int rbA, rbB;
+      uint32_t phA, phB;
+      tview(m, gvA, uvA, rbA, phA);
+      gu_load<GQW, true>(gvA, uvA, rbA, gA, uA, sgA, suA);
+      for (int tr = m; tr < ntask; tr += 2 * nmx) {
+        const int t1 = tr + nmx;
+        tview(t1, gvB, uvB, rbB, phB);
+        gu_load<GQW, true>(gvB, uvB, rbB, gB, uB, sgB, suB);
+        gu_compute<GQW, true, true>(gvA, rbA, gA, uA, sgA, suA, xb2, red,
+                                    hk + (size_t)tr * kTileRows, n, phA, t, status);
+        tview(t1 + nmx, gvA, uvA, rbA, phA);
+        gu_load<GQW, true>(gvA, uvA, rbA, gA, uA, sgA, suA);
+        if (t1 < ntask)
+          gu_compute<GQW, true, true>(gvB, rbB, gB, uB, sgB, suB, xb2, red,
+                                      hk + (size_t)t1 * kTileRows, n, phB, t, status);
+      }
+    }
+    __syncthreads();  // (a workgroup without tasks) publishes the slot weights
+
+    // ---- every pair's h, staged scaled by its slot's weight --------------------
+    {
+      const int nwords = NP * kQuadCols;
+      uint64_t hv[kTokHw];
+      uint32_t have = 0, all = 0;
+#pragma unroll
+      for (int u = 0; u < kTokHw; ++u) {
+        const int wd = tid + kThreads * u;
+        if (wd < nwords) all |= 1u << u;
+        hv[u] = ld_coh_u64(hk + min(wd, nwords - 1));
+      }
+      for (long spin = 0; spin < S.spin && ok && have != all; ++spin) {
+#pragma unroll
+        for (int u = 0; u < kTokHw; ++u) {
+          if ((all >> u & 1u) && !(have >> u & 1u) && (uint32_t)(hv[u] >> 32) == n) {
+            const int wd = tid + kThreads * u, p = wd / kQuadCols;
+            const float wgt = st.pw[p < KT ? p / nT : K];
+            uint16_t h0, l0;
+            split1(u2f((uint32_t)hv[u]) * wgt, h0, l0);
+            hbh[wd] = h0;
+            hbl[wd] = l0;
+            have |= 1u << u;
+          }
+        }
+        if (have == all) break;
+        __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+        for (int u = 0; u < kTokHw; ++u) {
+          const int wd = tid + kThreads * u;
+          hv[u] = ld_coh_u64(hk + min(wd, nwords - 1));
+        }
+      }
+      if (!__syncthreads_and(have == all || !ok) && tid == 0)
+        record_err(status, err_key(kPhSync, 0, 0, 2, 0));
+    }
+
+    // ---- down: this wave's tile over its pairs ------------------------------
+    f32x4 acc0 = {0, 0, 0, 0}, acc1 = {0, 0, 0, 0};
+    for (int i0 = 0; i0 < nit; i0 += kTokRing) {
+#pragma unroll
+      for (int u = 0; u < kTokRing; ++u) {
+        const int i = i0 + u;
+        if (i < nit) {
+          const int lp = lp0 + lstep * i;
+          bf16x8 A[4], B[4];
+#pragma unroll
+          for (int c = 0; c < 4; ++c) A[c] = dequant8(word_of(dw[u], c), scale_of(ds[u], c));
+          const uint16_t* hs = hbh + lp * kQuadCols;
+          const uint16_t* ls = hbl + lp * kQuadCols;
+#pragma unroll
+          for (int cc = 0; cc < 4; ++cc) B[cc] = ld_b2(hs, ls, cc * 4 + q, j);
+          acc0 = mfma16(A[0], B[0], acc0);
+          acc1 = mfma16(A[1], B[1], acc1);
+          acc0 = mfma16(A[2], B[2], acc0);
+          acc1 = mfma16(A[3], B[3], acc1);
+        }
+        dload(i + kTokRing, dw[u], ds[u]);
+      }
+    }
+    {
+      f32x4 acc;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[r] = acc0[r] + acc1[r];
+      fold_cols(acc);
+      if (j == 0) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) yred[w * 16 + 4 * q + r] = acc[r];
+      }
+    }
+    __syncthreads();
+    if (tid < kTileRows * my_rt) {
+      // rows (rb0 + t2) * 16 + r: the waves of tile t2 in order, the residual
+      const int t2 = tid >> 4, r = tid & 15;
+      float sum = 0.0f;
+      for (int w2 = t2; w2 < kWaves; w2 += rpw) sum = sum + yred[w2 * 16 + r];
+      const int d = (rb0 + t2) * kTileRows + r;
+      if (residual) sum = sum + residual[(size_t)t * H + d];
+      // a non-finite output: the host re-derives which check fires first
+      if (!finite_f(sum)) record_err(status, err_key(kPhExpert, t, 0, 0, kEkRecheck));
+      y[(size_t)t * H + d] = sum;
+    }
+  }
+}
+
 static int ldh_log2_of(const LayerDev& L) {
   const int m = L.I > L.Ish ? L.I : L.Ish;
   int lg = 0;
@@ -1481,7 +1762,8 @@ size_t decode_sync_bytes(const LayerDev& L, const DecodePlan& P) {
   const size_t R = (size_t)(L.E + 255) / 256;
   const size_t z = align256z((256 * R + 64) * 8 * (P.xs ? P.xs_nx : 1));
   if (P.xs)
-    return z + align256z((size_t)xs_pairs(L) * 64 * 8) + align256z((size_t)P.xs_nx * L.H * 8);
+    return z + align256z((size_t)xs_pairs(L) * 64 * 8) + align256z((size_t)P.xs_nx * L.H * 8) +
+           (P.tok ? align256z((size_t)kTokMaxT * xs_pairs(L) * kQuadCols * 8) : 0);
   const size_t ldh = (size_t)1 << ldh_log2_of(L);
   return z + align256z((size_t)(L.K + 1) * ldh * 8);
 }
@@ -1498,6 +1780,8 @@ DecodeSync decode_sync_carve(const LayerDev& L, const DecodePlan& P, void* base)
     S.hl = (uint64_t*)p;
     p += align256z((size_t)xs_pairs(L) * 64 * 8);
     S.pt = (uint64_t*)p;
+    p += align256z((size_t)P.xs_nx * L.H * 8);
+    if (P.tok) S.htk = (uint64_t*)p;
   } else {
     S.ht = (uint64_t*)p;
   }
@@ -1563,6 +1847,15 @@ DecodePlan make_decode_plan(const LayerDev& L, int num_cus, int nx) {
   P.off_yred = off; off += align16(kWaves * 16 * 4);
   P.off_fin = off; off += align16(xs ? P.xs_rpf * (P.xs_nx < xs_pairs(L) ? P.xs_nx : xs_pairs(L)) * 4 : 0);
   P.lds_bytes = off;
+  // the several-token form: every pair's h polled by the whole workgroup
+  // (kTokHw words per thread), the router rows as in the sliced form
+  if (xs && xs_pairs(L) * kQuadCols <= kTokHw * kThreads) {
+    P.tok = 1;
+    int o = P.off_hb;
+    P.tok_off_hb = o; o += align16(xs_pairs(L) * kQuadCols * 4);
+    P.tok_off_yred = o; o += align16(kWaves * 16 * 4);
+    P.tok_lds_bytes = o;
+  }
   P.threads = kThreads;
   P.grid = xs ? num_cus : num_cus > L.H / kTileRows ? num_cus : L.H / kTileRows;
   return P;
@@ -1614,6 +1907,40 @@ hipError_t decode_occupancy(const LayerDev& L, const DecodePlan& P, int* blocks_
   }
   *blocks_per_cu = best;
   return hipSuccess;
+}
+
+template <int GQW>
+static const void* pick_tok(int R) {
+  return R <= 1 ? (const void*)k_moe_tokens<GQW, 1> : (const void*)k_moe_tokens<GQW, 8>;
+}
+
+hipError_t launch_moe_tokens(const LayerDev& L, const DecodePlan& P, const float* x, int T,
+                             const float* residual, float* y, int32_t* ids, float* probs,
+                             float* shg, const DecodeSync& S, unsigned long long* status,
+                             hipStream_t st, bool cooperative) {
+  if (!P.xs || !P.tok || !S.htk || T < 2 || T > kTokMaxT || T > P.xs_nx)
+    return hipErrorInvalidValue;
+  const int gqw = (L.H / kQuadCols + kWaves - 1) / kWaves;
+  const int R = (L.E + 255) / 256;
+  if (R > 8 || L.K > 32) return hipErrorInvalidValue;
+  const void* fn = gqw <= 2 ? pick_tok<2>(R) : gqw <= 8 ? pick_tok<8>(R) : nullptr;
+  if (!fn) return hipErrorInvalidValue;
+  LayerDev Lc = L;
+  DecodePlan Pc = P;
+  DecodeSync Sc = S;
+  const float* xc = x;
+  const float* rc = residual;
+  // (leading arguments preloaded into scalar registers, as in launch_moe_decode)
+  const uint16_t* router = L.router;
+  int eH = L.H, eE = L.E, enx = P.xs_nx, enrw = P.xs_nrw, enb = P.grid, eT = T;
+  void* args[] = {&xc, &router, &eH, &eE, &enx,   &enrw, &enb,   &eT, &Lc,
+                  &Pc, &rc,     &y,  &ids, &probs, &shg,  &Sc, &status};
+  // every workgroup of an XCD waits for words its other workgroups publish:
+  // all must be resident at once (the rule of launch_moe_decode)
+  if (cooperative)
+    return hipLaunchCooperativeKernel(fn, dim3(P.grid), dim3(P.threads), args, P.tok_lds_bytes,
+                                      st);
+  return hipLaunchKernel(fn, dim3(P.grid), dim3(P.threads), args, P.tok_lds_bytes, st);
 }
 
 hipError_t launch_moe_decode(const LayerDev& L, const DecodePlan& P, const float* x,

@@ -185,7 +185,8 @@ def test_partial_blocks_rejected(block, oracle, tmp_path):
 
 @pytest.mark.parametrize("T", [2, 1])
 def test_forward_errors(block, tmp_path, T):
-    """Error texts of the block; T = 1 takes the two-launch single-token form."""
+    """Error texts of the block; T = 1 takes the single-launch one-token form
+    (k_gguf_one)."""
     dims = (128, 4, 2, 32, 32)
     g = _layer_file(tmp_path, "ok.gguf", lambda ts: ts)
     block.upload_layer_gguf(24, dims, g)
@@ -235,7 +236,7 @@ def _tied_router(ts, E, H):
 @pytest.mark.parametrize("E,K,ties", [(256, 8, False), (256, 8, True), (256, 7, True),
                                       (300, 8, False), (300, 5, True)])
 def test_single_token_routing(block, oracle, tmp_path, E, K, ties):
-    """Single-token calls (the two-launch form) on 256 and 300 experts: the
+    """Single-token calls (one k_gguf_one launch) on 256 and 300 experts: the
     top-k on the logits; with duplicated router rows, equal probabilities
     inside the selection (ordered by id) and, for odd K, a tie at the top-k
     boundary (the exact-probability path)."""

@@ -199,6 +199,9 @@ def test_noalloc_captured_in_a_graph(block, oracle, qwen_na, T):
         assert np.array_equal(got["probs"].view(np.uint32), po.view(np.uint32)), r
         err, rms, ok = tol_check(got["y"], yo)
         assert ok, (r, err, rms)
-        if T > 1:  # the same grouped path eagerly: the same bits
-            assert np.array_equal(got["y"].view(np.uint8), ref["y"].cpu().numpy().view(np.uint8))
+        # the eager call takes the fused kernels (one token, or a few tokens
+        # each on one XCD), which sum the experts in another order than the
+        # captured multi-kernel path: y within the bar of the eager result
+        err, rms, ok = tol_check(got["y"], ref["y"].cpu().numpy())
+        assert ok, (r, err, rms)
     del g
