@@ -482,8 +482,7 @@ hipError_t run_block(dmh_ctx* ctx, Layer* Ly, int layer, const float* dx, const 
   const dm::NormSpec no_norm{0.0f, nullptr, 0};
   const bool norm = nm && nm->eps > 0.0f;
   if (Ly->fused && allow_fused && cap == hipStreamCaptureStatusNone && !norm && T >= 2 &&
-      T <= dm::kTokMaxT && Ly->plan.tok && T <= Ly->plan.xs_nx &&
-      Ly->plan.tok_lds_bytes <= 65536) {
+      T <= dm::kTokMaxT && Ly->plan.tok && T <= Ly->plan.xs_nx) {
     // a few tokens: each one's whole block on one XCD, in one launch
     if (Ly->launches >= (1u << 24) && (e = reset_counters(ctx, Ly)) != hipSuccess) return e;
     dm::DecodeSync S = dm::decode_sync_carve(L, Ly->plan, Ly->sync);

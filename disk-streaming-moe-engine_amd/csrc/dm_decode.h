@@ -33,11 +33,13 @@ struct DecodePlan {
   // (launch_moe_tokens).  LDS: the sliced form's carve-up up to off_hb, then
   // every pair's h (bf16 hi / lo) and the down tile's reduction.
   int tok;
-  int tok_off_hb, tok_off_yred, tok_lds_bytes;
+  int tok_off_hb, tok_off_yred, tok_off_ring, tok_lds_bytes;
 };
 
-// Most tokens of one launch_moe_tokens launch (and at most the XCD count).
+// Most tokens of one launch_moe_tokens launch (and at most the XCD count),
+// and the most LDS it may take (one workgroup per CU).
 constexpr int kTokMaxT = 8;
+constexpr int kTokMaxLds = 150 * 1024;
 
 // Cross-workgroup state of one layer: tagged words carry the launch index in
 // their high half, so a consumer polls the data itself.

@@ -36,6 +36,7 @@
 // p (descending, lowest id first), as select_topk does (src/layers/topk.mojo:79-128).
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <vector>
 
 #include "dm_decode.h"
@@ -131,16 +132,14 @@ __device__ __forceinline__ void gu_load(const ExpertView& gv, const ExpertView& 
   }
 }
 
-// hdst: the tile's 8 hand-off words.  LOCAL: plain stores, read only by
-// workgroups on the same XCD (through its L2); otherwise agent-scope stores.
-// WIDE: 16 plain (XCD-local) stores instead, one value each with the whole
-// launch tag ((tag << 32) | bits).
-template <int GQW, bool LOCAL = false, bool WIDE = false>
-__device__ __forceinline__ void gu_compute(const ExpertView& gv, int rb, const uint4 (&wg)[GQW],
-                                           const uint4 (&wu)[GQW], const uint2 (&sg)[GQW],
-                                           const uint2 (&su)[GQW], const uint4* xb2, float* red,
-                                           uint64_t* hdst, unsigned tag, uint32_t phase,
-                                           uint32_t token, unsigned long long* status) {
+// The products of one 16-row tile for this wave's chunks (w, w+8, ...):
+// gate and up partial sums over its columns, folded to column 0, stored to
+// red[(w * 2 + {0: gate, 1: up}) * 16 + row].
+template <int GQW>
+__device__ __forceinline__ void gu_products(const ExpertView& gv, const uint4 (&wg)[GQW],
+                                            const uint4 (&wu)[GQW], const uint2 (&sg)[GQW],
+                                            const uint2 (&su)[GQW], const uint4* xb2,
+                                            float* red) {
   const int w = wave_id(), lane = threadIdx.x & 63;
   const int q = lane >> 4, j = lane & 15;
   const int nGQ = gv.cols / kQuadCols;
@@ -166,6 +165,17 @@ __device__ __forceinline__ void gu_compute(const ExpertView& gv, int rb, const u
       red[(w * 2 + 1) * 16 + 4 * q + i] = au[i];
     }
   }
+}
+
+// hdst: the tile's 8 hand-off words.  LOCAL: plain stores, read only by
+// workgroups on the same XCD (through its L2); otherwise agent-scope stores.
+template <int GQW, bool LOCAL = false>
+__device__ __forceinline__ void gu_compute(const ExpertView& gv, int rb, const uint4 (&wg)[GQW],
+                                           const uint4 (&wu)[GQW], const uint2 (&sg)[GQW],
+                                           const uint2 (&su)[GQW], const uint4* xb2, float* red,
+                                           uint64_t* hdst, unsigned tag, uint32_t phase,
+                                           uint32_t token, unsigned long long* status) {
+  gu_products<GQW>(gv, wg, wu, sg, su, xb2, red);
   __syncthreads();
   if (threadIdx.x < 16) {
     const int r = threadIdx.x, row = rb * kTileRows + r;
@@ -190,9 +200,7 @@ __device__ __forceinline__ void gu_compute(const ExpertView& gv, int rb, const u
     // of pack_h2); the partner's value comes from the neighbouring lane
     const float hn = __builtin_bit_cast(
         float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, h), 0xB1, 0xF, 0xF, true));
-    if (WIDE) {
-      st_l2_u64(hdst + r, ((uint64_t)tag << 32) | f2u(h));
-    } else if ((r & 1) == 0) {
+    if ((r & 1) == 0) {
       if (LOCAL)
         st_l2_u64(hdst + (r >> 1), pack_h2(tag, h, hn));
       else
@@ -1040,7 +1048,9 @@ __device__ __forceinline__ unsigned xcc_id() {
 // Tracing build: workgroup b (< 256) of a launch with S.trace = slot stores
 // wall_clock64() at point k to g_phase_trace[(slot * 256 + b) * 8 + k]:
 // 0 entry, 1 norm sum done, 2 x staged, 3 routing done, 4 h staged,
-// 5 partial published, 6 partials polled, 7 end.
+// 5 partial published, 6 partials polled, 7 end; in k_moe_tokens: 0 entry,
+// 1 x staged, 2 routing done, 3 gate/up tasks done, 4 h staged, 5 down
+// products done, 7 end.
 __device__ unsigned long long g_phase_trace[kTraceSlots * 256 * kTracePoints];
 #define DM_TR(k)                                                                      \
   do {                                                                                \
@@ -1478,9 +1488,10 @@ __global__ __launch_bounds__(kThreads) void k_moe_decode_xs(
 //            workgroup selects the top k itself;
 //   gate/up  the token's NP pairs (a routed slot's or the shared expert's
 //            128-row slice of I) x 8 tiles of 16 rows: tasks m, m + nmx, ...
-//            of workgroup m, each task's loads issued before the previous
-//            task's products; h published XCD-locally, one tagged word per
-//            value;
+//            of workgroup m, streamed through an LDS ring by direct-to-LDS
+//            loads; each wave's partial sums of every task kept in LDS, then
+//            one barrier and every task's h formed and published
+//            XCD-locally, one tagged word per value;
 //   down     workgroup m owns the output tiles m rpw ..; wave w takes tile
 //            w % rpw and the pairs w / rpw, + kWaves / rpw, ... (A16 chunks
 //            kTokRing ahead, the first ones requested right after routing),
@@ -1493,6 +1504,10 @@ __global__ __launch_bounds__(kThreads) void k_moe_decode_xs(
 // lines), so that no load is issued under a branch.
 constexpr int kTokHw = 12;   // h words per thread in the staging poll
 constexpr int kTokRing = 4;  // down chunks per wave in flight
+constexpr int kTokGu = 3;    // gate/up task slots of the LDS ring
+constexpr int kTokSlotW = 4 * 1024 + 4 * 128;  // one wave's part of a slot
+typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+typedef uint32_t v2u __attribute__((ext_vector_type(2)));
 
 template <int GQW, int R>
 __global__ __launch_bounds__(kThreads) void k_moe_tokens(
@@ -1501,6 +1516,7 @@ __global__ __launch_bounds__(kThreads) void k_moe_tokens(
     float* __restrict__ y, int32_t* __restrict__ ids_out, float* __restrict__ probs_out,
     float* __restrict__ shg_out, DecodeSync S, unsigned long long* status) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  DM_TR(0);
   const int H = H_, E = E_;
   const int b = blockIdx.x, nb = nb_;
   const int tid = threadIdx.x, w = wave_id(), lane = tid & 63;
@@ -1531,6 +1547,14 @@ __global__ __launch_bounds__(kThreads) void k_moe_tokens(
   const int rbc = min(rb0 + ri, nrt - 1);
   const int zs = 256 * R + 64;
   const int ntask = NP * (kQuadCols / kTileRows);
+  // pair p: the shared expert's slices first (their tasks need no routing,
+  // and task m of every workgroup is one of them), then the routed slots'
+  const int nGS = L.Ish / kQuadCols;
+  auto pair_of = [&](int p, int& shared, int& slot, int& slice) {
+    shared = p < nGS;
+    slot = shared ? K : (p - nGS) / nT;
+    slice = shared ? p : (p - nGS) % nT;
+  };
   const size_t matI = (size_t)L.I * H, matD = (size_t)H * L.I, matS = (size_t)L.Ish * H;
   const ExpertView sgv = {L.sgu_nib, L.sgu_sc, L.Ish, H};
   const ExpertView suv = {L.sgu_nib + matS / 2, L.sgu_sc + matS / kGroup, L.Ish, H};
@@ -1579,16 +1603,68 @@ __global__ __launch_bounds__(kThreads) void k_moe_tokens(
       if (bad && m == 0) record_err(status, err_key(kPhX, 0, 0, 0, 0));
     }
     __syncthreads();
+    DM_TR(1);
+
+    // ---- gate/up tasks (views, and their loads into the LDS ring) -----------
+    auto tview = [&](int tr, ExpertView& gv, ExpertView& uv, int& rb, uint32_t& ph) {
+      gv = sgv;
+      uv = suv;
+      rb = 0;
+      ph = kPhShared;
+      if (tr < ntask) {
+        int sh, slot, sli;
+        pair_of(tr >> 3, sh, slot, sli);
+        rb = sli * 8 + (tr & 7);
+        if (!sh) {
+          const int e = __builtin_amdgcn_readfirstlane(st.ids[slot]);
+          gv = {L.gu_nib + (size_t)e * matI, L.gu_sc + (size_t)e * 2 * (matI / kGroup), L.I, H};
+          uv = {gv.nib + matI / 2, gv.sc + matI / kGroup, L.I, H};
+          ph = kPhExpert;
+        }
+      }
+    };
+    static_assert(GQW == 2, "the ring holds two chunk pairs per wave");
+    // each task's partial sums: [task of this workgroup][wave][gate 16, up 16]
+    // in the h staging area (not used before the h poll)
+    float* rall = reinterpret_cast<float*>(smem + P.tok_off_hb);
+    const uint32_t ring = lds_u32(smem + P.tok_off_ring) + w * kTokSlotW;
+    auto issue = [&](int tr, int k) {
+      ExpertView gv, uv;
+      int rb;
+      uint32_t ph;
+      tview(tr, gv, uv, rb, ph);
+      const int nGQ = gv.cols / kQuadCols;
+      const uint32_t sl = ring + k * kWaves * kTokSlotW;
+#pragma unroll
+      for (int c = 0; c < 2 * GQW; ++c) {
+        const int gq = min(w + kWaves * (c >> 1), nGQ - 1);
+        dma16_lds(((c & 1) ? uv : gv).nib + a16_nib_offset(nGQ, rb, gq, lane), sl + c * 1024);
+      }
+      // the four chunks' scales: 128 bytes each, 8 lanes per chunk
+      if (lane < 8 * 2 * GQW) {
+        const int c = lane >> 3;
+        const int gq = min(w + kWaves * (c >> 1), nGQ - 1);
+        dma16_lds(reinterpret_cast<const unsigned char*>(((c & 1) ? uv : gv).sc +
+                                                         a16_sc_offset(nGQ, rb, gq, 0)) +
+                      (lane & 7) * 16,
+                  sl + 2 * GQW * 1024);
+      }
+    };
 
     // ---- router rows, then routing (as in k_moe_decode_xs) ---------------------
+    // task m is a shared slice's (m < 8 nGS): it needs no routing, so its
+    // loads go out now on the waves that neither poll nor select
+    const bool early = m < nGS * (kQuadCols / kTileRows);
     if (w < nrw) router_compute<true>(L, rw, re, xt, zl, n);
+    if (early && w != 0 && w != kNormWave) issue(m, 0);
     if (w == 0) {
       const bool rok = route<R>(zl, n, E, K, st, m == 0, t, status, S.spin);
       if (lane == 0) st.misc[2] = rok ? 1.0f : 0.0f;
     } else if (w == kNormWave) {
       softmax_exp<R>(zl, n, E, st, m == 0, t, status, S.spin);
     }
-    __syncthreads();
+    lds_barrier();  // the routing state (LDS); task m's loads stay in flight
+    DM_TR(2);
     const bool ok = st.misc[2] != 0.0f;
 
     // ---- this wave's first down chunks (they need the routing only) ----------
@@ -1596,13 +1672,12 @@ __global__ __launch_bounds__(kThreads) void k_moe_tokens(
       ExpertView dv = sdv;
       int gq = 0;
       if (i < nit) {
-        const int p = lp0 + lstep * i;
-        if (p < KT) {
-          const int e = __builtin_amdgcn_readfirstlane(st.ids[p / nT]);
+        int sh, slot, sli;
+        pair_of(lp0 + lstep * i, sh, slot, sli);
+        gq = sli;
+        if (!sh) {
+          const int e = __builtin_amdgcn_readfirstlane(st.ids[slot]);
           dv = {L.d_nib + (size_t)e * (matD / 2), L.d_sc + (size_t)e * (matD / kGroup), H, L.I};
-          gq = p % nT;
-        } else {
-          gq = p - KT;
         }
       }
       load_chunk_nt(dv, i < nit ? rbc : 0, gq, lane, wv, sv);
@@ -1620,47 +1695,83 @@ __global__ __launch_bounds__(kThreads) void k_moe_tokens(
                      probs_out + (size_t)t * K, shg_out + t);
     }
 
-    // ---- gate/up tasks, each one's loads in flight during the previous one ---
-    auto tview = [&](int tr, ExpertView& gv, ExpertView& uv, int& rb, uint32_t& ph) {
-      gv = sgv;
-      uv = suv;
-      rb = 0;
-      ph = kPhShared;
-      if (tr < ntask) {
-        const int p = tr >> 3, r = tr & 7;
-        if (p < KT) {
-          const int e = __builtin_amdgcn_readfirstlane(st.ids[p / nT]);
-          gv = {L.gu_nib + (size_t)e * matI, L.gu_sc + (size_t)e * 2 * (matI / kGroup), L.I, H};
-          uv = {gv.nib + matI / 2, gv.sc + matI / kGroup, L.I, H};
-          rb = (p % nT) * 8 + r;
-          ph = kPhExpert;
-        } else {
-          rb = (p - KT) * 8 + r;
+    {
+      // A ring of kTokGu task slots in LDS, filled by direct-to-LDS loads
+      // (loads into registers stall at a few tens of KB in flight per CU):
+      // wave w's part of a slot holds its 2 GQW chunks (gate, up of chunk
+      // w + 8 i) and their scales, and only wave w reads it, so the ring needs
+      // no barrier; the loads of the next kTokGu - 1 tasks are in flight
+      // while one task's products run.
+      static_assert(kTokGu == 3, "tasks m and m + nmx are the two issued ahead");
+      if (!early || w == 0 || w == kNormWave) issue(m, 0);
+      issue(m + nmx, 1);
+
+      for (int tr = m; tr < ntask; tr += kTokGu * nmx) {
+#pragma unroll
+        for (int k = 0; k < kTokGu; ++k) {
+          issue(tr + (k + kTokGu - 1) * nmx, (k + kTokGu - 1) % kTokGu);
+          const int tk = tr + k * nmx;
+          // this slot's loads have landed: only the later tasks' loads (five
+          // per task) may still be in flight
+          asm volatile("s_waitcnt vmcnt(%0)" ::"n"((kTokGu - 1) * (2 * GQW + 1)) : "memory");
+          if (tk < ntask) {
+            ExpertView gv, uv;
+            int rb;
+            uint32_t ph;
+            tview(tk, gv, uv, rb, ph);
+            (void)rb;
+            (void)ph;
+            const uint32_t sl = ring + k * kWaves * kTokSlotW;
+            uint4 wg[GQW], wu[GQW];
+            uint2 sg[GQW], su[GQW];
+#pragma unroll
+            for (int i = 0; i < GQW; ++i) {
+              const v4u a = *(const __attribute__((address_space(3))) v4u*)(size_t)(
+                  sl + (2 * i) * 1024 + lane * 16);
+              const v4u c = *(const __attribute__((address_space(3))) v4u*)(size_t)(
+                  sl + (2 * i + 1) * 1024 + lane * 16);
+              const v2u d = *(const __attribute__((address_space(3))) v2u*)(size_t)(
+                  sl + 2 * GQW * 1024 + (2 * i) * 128 + j * 8);
+              const v2u e2 = *(const __attribute__((address_space(3))) v2u*)(size_t)(
+                  sl + 2 * GQW * 1024 + (2 * i + 1) * 128 + j * 8);
+              wg[i] = make_uint4(a.x, a.y, a.z, a.w);
+              wu[i] = make_uint4(c.x, c.y, c.z, c.w);
+              sg[i] = make_uint2(d.x, d.y);
+              su[i] = make_uint2(e2.x, e2.y);
+            }
+            gu_products<GQW>(gv, wg, wu, sg, su, xb2, rall + (size_t)((tk - m) / nmx) * 256);
+          }
         }
       }
-    };
-    {
-      uint4 gA[GQW], uA[GQW], gB[GQW], uB[GQW];
-      uint2 sgA[GQW], suA[GQW], sgB[GQW], suB[GQW];
-      ExpertView gvA, uvA, gvB, uvB;
-      int rbA, rbB;
-      uint32_t phA, phB;
-      tview(m, gvA, uvA, rbA, phA);
-      gu_load<GQW, true>(gvA, uvA, rbA, gA, uA, sgA, suA);
-      for (int tr = m; tr < ntask; tr += 2 * nmx) {
-        const int t1 = tr + nmx;
-        tview(t1, gvB, uvB, rbB, phB);
-        gu_load<GQW, true>(gvB, uvB, rbB, gB, uB, sgB, suB);
-        gu_compute<GQW, true, true>(gvA, rbA, gA, uA, sgA, suA, xb2, red,
-                                    hk + (size_t)tr * kTileRows, n, phA, t, status);
-        tview(t1 + nmx, gvA, uvA, rbA, phA);
-        gu_load<GQW, true>(gvA, uvA, rbA, gA, uA, sgA, suA);
-        if (t1 < ntask)
-          gu_compute<GQW, true, true>(gvB, rbB, gB, uB, sgB, suB, xb2, red,
-                                      hk + (size_t)t1 * kTileRows, n, phB, t, status);
+      // every task's partials in LDS: one barrier, then 16 threads per task
+      // form its h (swiglu_forward's SiLU, product and checks) and publish it
+      lds_barrier();
+      const int ntk = m < ntask ? (ntask - m + nmx - 1) / nmx : 0;
+      if (tid < kTileRows * ntk) {
+        const int kt = tid >> 4, r = tid & 15, tk = m + kt * nmx;
+        const float* rp = rall + (size_t)kt * 256;
+        float g = 0.0f, u = 0.0f;
+#pragma unroll
+        for (int v = 0; v < kWaves; ++v) {
+          g = g + rp[v * 32 + r];
+          u = u + rp[v * 32 + 16 + r];
+        }
+        const float h = dm_silu(g) * u;
+        if (!finite_f(g) || !finite_f(u) || !finite_f(h)) {
+          // shared expert: the exact key; routed: the host re-derives it
+          int sh, slot, sli;
+          pair_of(tk >> 3, sh, slot, sli);
+          if (sh)
+            record_err(status, err_key(kPhShared, t, 0, (sli * 8 + (tk & 7)) * kTileRows + r,
+                                       !finite_f(g) ? kEkGate : !finite_f(u) ? kEkUp : kEkH));
+          else
+            record_err(status, err_key(kPhExpert, t, 0, 0, kEkRecheck));
+        }
+        st_l2_u64(hk + (size_t)tk * kTileRows + r, ((uint64_t)n << 32) | f2u(h));
       }
     }
     __syncthreads();  // (a workgroup without tasks) publishes the slot weights
+    DM_TR(3);
 
     // ---- every pair's h, staged scaled by its slot's weight --------------------
     {
@@ -1677,8 +1788,10 @@ __global__ __launch_bounds__(kThreads) void k_moe_tokens(
 #pragma unroll
         for (int u = 0; u < kTokHw; ++u) {
           if ((all >> u & 1u) && !(have >> u & 1u) && (uint32_t)(hv[u] >> 32) == n) {
-            const int wd = tid + kThreads * u, p = wd / kQuadCols;
-            const float wgt = st.pw[p < KT ? p / nT : K];
+            const int wd = tid + kThreads * u;
+            int sh, slot, sli;
+            pair_of(wd / kQuadCols, sh, slot, sli);
+            const float wgt = st.pw[slot];
             uint16_t h0, l0;
             split1(u2f((uint32_t)hv[u]) * wgt, h0, l0);
             hbh[wd] = h0;
@@ -1697,6 +1810,7 @@ __global__ __launch_bounds__(kThreads) void k_moe_tokens(
       if (!__syncthreads_and(have == all || !ok) && tid == 0)
         record_err(status, err_key(kPhSync, 0, 0, 2, 0));
     }
+    DM_TR(4);
 
     // ---- down: this wave's tile over its pairs ------------------------------
     f32x4 acc0 = {0, 0, 0, 0}, acc1 = {0, 0, 0, 0};
@@ -1721,6 +1835,7 @@ __global__ __launch_bounds__(kThreads) void k_moe_tokens(
         dload(i + kTokRing, dw[u], ds[u]);
       }
     }
+    DM_TR(5);
     {
       f32x4 acc;
 #pragma unroll
@@ -1743,6 +1858,7 @@ __global__ __launch_bounds__(kThreads) void k_moe_tokens(
       if (!finite_f(sum)) record_err(status, err_key(kPhExpert, t, 0, 0, kEkRecheck));
       y[(size_t)t * H + d] = sum;
     }
+    DM_TR(7);
   }
 }
 
@@ -1849,12 +1965,17 @@ DecodePlan make_decode_plan(const LayerDev& L, int num_cus, int nx) {
   P.lds_bytes = off;
   // the several-token form: every pair's h polled by the whole workgroup
   // (kTokHw words per thread), the router rows as in the sliced form
-  if (xs && xs_pairs(L) * kQuadCols <= kTokHw * kThreads) {
-    P.tok = 1;
+  // (H <= 2048: two chunk pairs per wave in the LDS ring of gate/up tasks)
+  if (xs && xs_pairs(L) * kQuadCols <= kTokHw * kThreads && L.H <= 2 * kWaves * kQuadCols) {
     int o = P.off_hb;
     P.tok_off_hb = o; o += align16(xs_pairs(L) * kQuadCols * 4);
     P.tok_off_yred = o; o += align16(kWaves * 16 * 4);
+    P.tok_off_ring = o; o += kTokGu * kWaves * kTokSlotW;
     P.tok_lds_bytes = o;
+    // each workgroup's task partials (1 KB per task) fit the h staging area
+    const int nmx = num_cus / nx;
+    const int ntk = (xs_pairs(L) * (kQuadCols / kTileRows) + nmx - 1) / nmx;
+    P.tok = o <= kTokMaxLds && ntk * 1024 <= xs_pairs(L) * kQuadCols * 4 ? 1 : 0;
   }
   P.threads = kThreads;
   P.grid = xs ? num_cus : num_cus > L.H / kTileRows ? num_cus : L.H / kTileRows;
@@ -1909,9 +2030,25 @@ hipError_t decode_occupancy(const LayerDev& L, const DecodePlan& P, int* blocks_
   return hipSuccess;
 }
 
-template <int GQW>
 static const void* pick_tok(int R) {
-  return R <= 1 ? (const void*)k_moe_tokens<GQW, 1> : (const void*)k_moe_tokens<GQW, 8>;
+  return R <= 1 ? (const void*)k_moe_tokens<2, 1> : (const void*)k_moe_tokens<2, 8>;
+}
+
+// the several-token kernel's LDS (its gate/up ring) is above the default
+// limit of a launch: raised once per device
+static hipError_t tok_attrs() {
+  static std::atomic<uint64_t> done{0};
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  const uint64_t bit = dev < 64 ? 1ull << dev : 0;
+  if (bit && (done.load() & bit)) return hipSuccess;
+  for (int r : {1, 8}) {
+    e = hipFuncSetAttribute(pick_tok(r), hipFuncAttributeMaxDynamicSharedMemorySize, kTokMaxLds);
+    if (e != hipSuccess) return e;
+  }
+  done.fetch_or(bit);
+  return hipSuccess;
 }
 
 hipError_t launch_moe_tokens(const LayerDev& L, const DecodePlan& P, const float* x, int T,
@@ -1920,11 +2057,12 @@ hipError_t launch_moe_tokens(const LayerDev& L, const DecodePlan& P, const float
                              hipStream_t st, bool cooperative) {
   if (!P.xs || !P.tok || !S.htk || T < 2 || T > kTokMaxT || T > P.xs_nx)
     return hipErrorInvalidValue;
-  const int gqw = (L.H / kQuadCols + kWaves - 1) / kWaves;
   const int R = (L.E + 255) / 256;
-  if (R > 8 || L.K > 32) return hipErrorInvalidValue;
-  const void* fn = gqw <= 2 ? pick_tok<2>(R) : gqw <= 8 ? pick_tok<8>(R) : nullptr;
-  if (!fn) return hipErrorInvalidValue;
+  if (R > 8 || L.K > 32 || L.H > 2 * kWaves * kQuadCols || P.tok_lds_bytes > kTokMaxLds)
+    return hipErrorInvalidValue;
+  const void* fn = pick_tok(R);
+  const hipError_t ea = tok_attrs();
+  if (ea != hipSuccess) return ea;
   LayerDev Lc = L;
   DecodePlan Pc = P;
   DecodeSync Sc = S;

@@ -149,6 +149,24 @@ __device__ __forceinline__ void record_err(unsigned long long* status, uint64_t 
   atomicMin(status, (unsigned long long)key);
 }
 
+// 16 bytes per lane from p to the LDS byte address m + 16 * lane (m uniform),
+// without passing through registers (global_load_lds_dwordx4).  Issued as
+// inline assembly: the caller counts these loads itself (s_waitcnt vmcnt); a
+// load the compiler tracks is only ever waited for longer because of them.
+// M0 (the LDS address) is saved and restored around the load.
+__device__ __forceinline__ void dma16_lds(const void* p, uint32_t m) {
+  uint32_t save;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %1, off\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(save)
+      : "v"(p), "s"(__builtin_amdgcn_readfirstlane(m))
+      : "memory");
+}
+// The LDS byte address of a __shared__ object: the low word of its generic
+// address (the shared aperture's base is a multiple of 2^32).
+__device__ __forceinline__ uint32_t lds_u32(const void* p) { return (uint32_t)(uintptr_t)p; }
+
 // ---- cross-workgroup handoff inside one launch -----------------------------
 // Data handed between workgroups is written and read with agent-scope relaxed
 // atomics: they go to the device-coherent level and bypass the per-XCD L2,
