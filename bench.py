@@ -251,8 +251,11 @@ def grouped(a, blk, stream, dev):
                           "batch": T, "hidden": H, "experts": E, "top_k": K, "inter": I,
                           "group": 32, "bits": 4, "activations": a.activations},
                "expert_union_mean": round(u_mean, 2),
-               "roofline": {"bound": "hbm", "kernel": "grouped path (router, build, gate/up, "
-                            "down, combine)", "achieved": round(gbps, 1),
+               "roofline": {"bound": "hbm",
+                            "kernel": ("k_moe_tokens (one launch, each token's block on one XCD)"
+                                       if 3 <= T <= 8 else
+                                       "grouped path (router, build, gate/up, down, combine)"),
+                            "achieved": round(gbps, 1),
                             "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                             "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None,
                             "bytes_per_step": int(nbytes)}}

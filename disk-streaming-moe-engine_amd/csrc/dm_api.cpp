@@ -465,6 +465,8 @@ hipError_t ctx_scratch(dmh_ctx* ctx, const LayerDev& L, int T, bool norm, BlockS
 // launch tag is fixed on the host, so every replay of a captured launch
 // would carry the same tag and its waits would pass on the previous replay's
 // data.
+constexpr int kTokMinT = 3;  // fewest tokens of the several-token launch
+
 hipError_t run_block(dmh_ctx* ctx, Layer* Ly, int layer, const float* dx, const float* dres,
                      int T, float* dy, int32_t* dids, float* dprobs, float* dshg,
                      bool allow_fused = true, const dm::NormSpec* nm = nullptr,
@@ -481,9 +483,11 @@ hipError_t run_block(dmh_ctx* ctx, Layer* Ly, int layer, const float* dx, const 
   const bool fused = Ly->fused && allow_fused && T == 1 && cap == hipStreamCaptureStatusNone;
   const dm::NormSpec no_norm{0.0f, nullptr, 0};
   const bool norm = nm && nm->eps > 0.0f;
-  if (Ly->fused && allow_fused && cap == hipStreamCaptureStatusNone && !norm && T >= 2 &&
-      T <= dm::kTokMaxT && Ly->plan.tok && T <= Ly->plan.xs_nx) {
-    // a few tokens: each one's whole block on one XCD, in one launch
+  if (Ly->fused && allow_fused && cap == hipStreamCaptureStatusNone && !norm &&
+      T >= kTokMinT && T <= dm::kTokMaxT && Ly->plan.tok && T <= Ly->plan.xs_nx) {
+    // a few tokens: each one's whole block on one XCD, in one launch (from
+    // three tokens on: with two, six XCDs would idle and the grouped path
+    // measured as fast)
     if (Ly->launches >= (1u << 24) && (e = reset_counters(ctx, Ly)) != hipSuccess) return e;
     dm::DecodeSync S = dm::decode_sync_carve(L, Ly->plan, Ly->sync);
     S.n = ++Ly->launches;

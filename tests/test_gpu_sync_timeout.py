@@ -1,7 +1,7 @@
-"""The time-out path of the single-token kernels' waits, forced from the host.
+"""The time-out path of the fused kernels' waits, forced from the host.
 
-The fused single-token kernels (the 4-bit decode kernel and the GGUF
-one-launch kernel) run every workgroup at once and pass data between them
+The fused kernels (the 4-bit decode kernel, the several-token launch and the
+GGUF one-launch kernel) run every workgroup at once and pass data between them
 through polled words.  Every such wait is bounded: after the context's bound
 of polls it records a sync error and the kernel runs on to its end, so the
 grid always drains.  A context whose bound is zero polls
@@ -17,8 +17,8 @@ outputs within max-abs-err <= 1e-3 x RMS):
 - a DMH_F_DEVICE call reports the hand-off error text at dmh_sync;
 - with the default bound restored, the next host and device calls run the
   fused kernel again and are correct;
-- the 40-layer stack's host call and the GGUF layer's host call fall back
-  the same way."""
+- the several-token launch, the 40-layer stack's host call and the GGUF
+  layer's host call fall back the same way."""
 import numpy as np
 import pytest
 
@@ -79,6 +79,61 @@ def test_decode_waits_give_up_then_fall_back(block, oracle, shape):
         _check(oracle, L, x[2:3], dy.cpu().numpy(), dids.cpu().numpy(), dpr.cpu().numpy(),
                dsg.cpu().numpy())
         _check(oracle, L, x[3:4], *block.forward_arrays(SLOT, x[3:4], 1))
+        assert block.sync_fallbacks() == n0 + 1
+    finally:
+        block.set_spin_limit(None)
+        block.free_layer(SLOT)
+
+
+def test_few_token_waits_give_up_then_fall_back(block, oracle):
+    """The several-token launch (each token's block on one XCD) under a
+    zero-poll bound: the host call is rerun on the grouped path and matches
+    the oracle, a device call reports the hand-off error at dmh_sync, and
+    with the default bound restored the launch is correct again."""
+    import torch
+    L = synth.make_layer(**synth.CONFIG_QWEN36, seed=97)
+    H, K, T = L.hidden, L.top_k, 4
+    x = synth.make_activations(np.random.default_rng(98), (4 * T, H))
+
+    def check(xs, y, ids, probs, shg):
+        yo, ido, po, so = oracle.moe_layer_q4(L, xs, T)
+        assert np.array_equal(ids, ido), (ids, ido)
+        assert np.array_equal(probs.view(np.uint32), po.view(np.uint32))
+        assert np.array_equal(np.asarray(shg, np.float32).view(np.uint32),
+                              np.asarray(so, np.float32).view(np.uint32))
+        err, rms, ok = tol_check(y, yo)
+        assert ok, (err, rms)
+
+    block.upload_layer(SLOT, L)
+    try:
+        print("[sync-timeout] few tokens: default bound", flush=True)
+        check(x[:T], *block.forward_arrays(SLOT, x[:T], T))
+        n0 = block.sync_fallbacks()
+        block.set_spin_limit(0)
+        print("[sync-timeout] few tokens: zero-poll bound, host call", flush=True)
+        check(x[T:2 * T], *block.forward_arrays(SLOT, x[T:2 * T], T))
+        assert block.sync_fallbacks() == n0 + 1
+        print("[sync-timeout] few tokens: zero-poll bound, device call", flush=True)
+        dev = torch.device("cuda:0")
+        dx = torch.from_numpy(x[2 * T:3 * T].copy()).to(dev)
+        dy = torch.empty((T, H), dtype=torch.float32, device=dev)
+        dids = torch.empty((T, K), dtype=torch.int32, device=dev)
+        dpr = torch.empty((T, K), dtype=torch.float32, device=dev)
+        dsg = torch.empty((T,), dtype=torch.float32, device=dev)
+        torch.cuda.synchronize()
+        block.forward_device(SLOT, dx.data_ptr(), T, dy.data_ptr(), dids.data_ptr(),
+                             dpr.data_ptr(), dsg.data_ptr())
+        with pytest.raises(DismoenError) as ei:
+            block.sync()
+        assert "cross-workgroup handoff timed out" in str(ei.value), str(ei.value)
+        block.set_spin_limit(None)
+        print("[sync-timeout] few tokens: default bound again", flush=True)
+        block.forward_device(SLOT, dx.data_ptr(), T, dy.data_ptr(), dids.data_ptr(),
+                             dpr.data_ptr(), dsg.data_ptr())
+        block.sync()
+        check(x[2 * T:3 * T], dy.cpu().numpy(), dids.cpu().numpy(), dpr.cpu().numpy(),
+              dsg.cpu().numpy())
+        check(x[3 * T:], *block.forward_arrays(SLOT, x[3 * T:], T))
         assert block.sync_fallbacks() == n0 + 1
     finally:
         block.set_spin_limit(None)
