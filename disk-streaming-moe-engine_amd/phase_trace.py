@@ -14,6 +14,13 @@ workgroups, and the last workgroup).
 
 --norm none traces the single-layer decode instead (one layer, no norm,
 dmh_moe_forward on device pointers, the bench's default workload).
+
+    python3 disk-streaming-moe-engine_amd/phase_trace.py --batch T
+
+traces the several-token launch of k_moe_tokens instead (T = 3 .. 8 tokens
+per call, one layer, device pointers, the last call's workgroups that hold a
+token): x staged, routing done, gate/up tasks done, h staged, down products
+done, end.
 """
 import argparse
 import ctypes as C
@@ -36,6 +43,8 @@ def main():
     ap.add_argument("--norm", default="ref", choices=["ref", "tree", "none"])
     ap.add_argument("--tokens", type=int, default=20)
     ap.add_argument("--layers", type=int, default=40)
+    ap.add_argument("--batch", type=int, default=0,
+                    help="trace the several-token launch with this many tokens per call")
     a = ap.parse_args()
     if not os.path.exists(TRACE_LIB):
         raise SystemExit(f"{TRACE_LIB} not built (make -C {HERE} trace)")
@@ -52,6 +61,8 @@ def main():
     fetch.argtypes = [C.c_void_p, C.c_size_t]
     fetch.restype = C.c_int
     cfg = synth.CONFIG_QWEN36
+    if a.batch:
+        return trace_batch(a, blk, fetch, cfg, dev)
     nl = 1 if a.norm == "none" else a.layers
     dims = (cfg["hidden"], cfg["num_experts"], cfg["top_k"], cfg["inter"], cfg["inter_sh"])
     for l in range(nl):
@@ -105,6 +116,44 @@ def main():
         med = np.median([r[nm][0] for r in rows])
         mx = np.median([r[nm][1] for r in rows])
         print(f"{nm:>18}: median {med:.2f} us (median over layers of the last workgroup {mx:.2f})")
+
+
+BATCH_NAMES = {1: "x staged", 2: "routing done", 3: "gate/up tasks done", 4: "h staged",
+               5: "down products done", 7: "end"}
+
+
+def trace_batch(a, blk, fetch, cfg, dev):
+    import torch
+    from dismoen import synth
+    T = a.batch
+    W = synth.make_layer_device(**cfg, seed=1000, device=dev)
+    torch.cuda.synchronize()
+    dims = (cfg["hidden"], cfg["num_experts"], cfg["top_k"], cfg["inter"], cfg["inter_sh"])
+    blk.upload_layer_device(0, dims, {k: v.data_ptr() for k, v in W.items()})
+    blk.sync()
+    del W
+    H, K = cfg["hidden"], cfg["top_k"]
+    x = torch.from_numpy(synth.make_activations(np.random.default_rng(7), (a.tokens, T, H))).to(dev)
+    y = torch.empty_like(x)
+    ids = torch.empty((a.tokens, T, K), dtype=torch.int32, device=dev)
+    pr = torch.empty((a.tokens, T, K), dtype=torch.float32, device=dev)
+    sg = torch.empty((a.tokens, T), dtype=torch.float32, device=dev)
+    torch.cuda.synchronize()
+    for i in range(a.tokens):  # the last call's launch leaves its stamps
+        blk.forward_device(0, x[i].data_ptr(), T, y[i].data_ptr(), ids[i].data_ptr(),
+                           pr[i].data_ptr(), sg[i].data_ptr())
+    blk.sync()
+    buf = np.zeros(SLOTS * WGS * POINTS, np.uint64)
+    rc = fetch(C.c_void_p(buf.ctypes.data), buf.nbytes)
+    if rc != 0:
+        raise SystemExit(f"dmh_phase_trace_fetch returned {rc}")
+    tr = buf.reshape(SLOTS, WGS, POINTS)[0].astype(np.int64)
+    tr = tr[tr[:, 7] > 0]  # the workgroups that held a token
+    base = tr[:, 0].min()
+    print(f"batch {T}, {len(tr)} workgroups with a token, call {a.tokens - 1}")
+    for k, nm in BATCH_NAMES.items():
+        d = (tr[:, k] - base) / CLOCK_MHZ
+        print(f"{nm:>20}: median {np.median(d):.2f} us (last workgroup {d.max():.2f})")
 
 
 if __name__ == "__main__":
