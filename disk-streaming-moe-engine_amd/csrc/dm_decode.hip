@@ -135,7 +135,8 @@ __device__ __forceinline__ void gu_load(const ExpertView& gv, const ExpertView& 
 // The products of one 16-row tile for this wave's chunks (w, w+8, ...):
 // gate and up partial sums over its columns, folded to column 0, stored to
 // red[(w * 2 + {0: gate, 1: up}) * 16 + row].
-template <int GQW>
+// kShifted: dequant8_shifted (the one-token kernels), else dequant8.
+template <int GQW, bool kShifted>
 __device__ __forceinline__ void gu_products(const ExpertView& gv, const uint4 (&wg)[GQW],
                                             const uint4 (&wu)[GQW], const uint2 (&sg)[GQW],
                                             const uint2 (&su)[GQW], const uint4* xb2,
@@ -151,8 +152,10 @@ __device__ __forceinline__ void gu_products(const ExpertView& gv, const uint4 (&
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
         const bf16x8 b = ld_b(xb2, (gq * 4 + c) * 4 + q, j);
-        ag = mfma16(dequant8(word_of(wg[i], c), scale_of(sg[i], c)), b, ag);
-        au = mfma16(dequant8(word_of(wu[i], c), scale_of(su[i], c)), b, au);
+        const uint32_t wgc = word_of(wg[i], c), wuc = word_of(wu[i], c);
+        const float sgc = scale_of(sg[i], c), suc = scale_of(su[i], c);
+        ag = mfma16(kShifted ? dequant8_shifted(wgc, sgc) : dequant8(wgc, sgc), b, ag);
+        au = mfma16(kShifted ? dequant8_shifted(wuc, suc) : dequant8(wuc, suc), b, au);
       }
     }
   }
@@ -175,7 +178,7 @@ __device__ __forceinline__ void gu_compute(const ExpertView& gv, int rb, const u
                                            const uint2 (&su)[GQW], const uint4* xb2, float* red,
                                            uint64_t* hdst, unsigned tag, uint32_t phase,
                                            uint32_t token, unsigned long long* status) {
-  gu_products<GQW>(gv, wg, wu, sg, su, xb2, red);
+  gu_products<GQW, true>(gv, wg, wu, sg, su, xb2, red);
   __syncthreads();
   if (threadIdx.x < 16) {
     const int r = threadIdx.x, row = rb * kTileRows + r;
@@ -876,7 +879,7 @@ __global__ __launch_bounds__(kThreads) void k_moe_decode(
   for (int i = 0; i < kDownBatch; ++i)
     if (i < my_chunks)
 #pragma unroll
-      for (int c = 0; c < 4; ++c) A[i][c] = dequant8(word_of(dw[i], c), scale_of(ds[i], c));
+      for (int c = 0; c < 4; ++c) A[i][c] = dequant8_shifted(word_of(dw[i], c), scale_of(ds[i], c));
 #pragma unroll
   for (int i = 0; i < kDownBatch; ++i)
 #pragma unroll
@@ -966,7 +969,7 @@ __global__ __launch_bounds__(kThreads) void k_moe_decode(
     for (int i = 0; i < kDownBatch; ++i)
       if (base + i < my_chunks)
 #pragma unroll
-        for (int c = 0; c < 4; ++c) A[i][c] = dequant8(word_of(dw[i], c), scale_of(ds[i], c));
+        for (int c = 0; c < 4; ++c) A[i][c] = dequant8_shifted(word_of(dw[i], c), scale_of(ds[i], c));
 #pragma unroll
     for (int i = 0; i < kDownBatch; ++i) {
       if (base + i < my_chunks) {
@@ -1251,7 +1254,7 @@ __global__ __launch_bounds__(kThreads) void k_moe_decode_xs(
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt) {
           const uint4 wv =
-              __builtin_bit_cast(uint4, dequant8(word_of(shc[mt], c), scale_of(shs[mt], c)));
+              __builtin_bit_cast(uint4, dequant8_shifted(word_of(shc[mt], c), scale_of(shs[mt], c)));
           const uint32_t wd[4] = {wv.x, wv.y, wv.z, wv.w};
 #pragma unroll
           for (int u = 0; u < 4; ++u) {
@@ -1333,7 +1336,7 @@ __global__ __launch_bounds__(kThreads) void k_moe_decode_xs(
   }
 
 #pragma unroll
-  for (int c = 0; c < 4; ++c) As[c] = dequant8(word_of(dws, c), scale_of(dss, c));
+  for (int c = 0; c < 4; ++c) As[c] = dequant8_shifted(word_of(dws, c), scale_of(dss, c));
   // the softmax sum and slot weights while the loads are in flight; the
   // ranks and outputs in the reference's order in one workgroup
   const int fin_wg = nb - 1;
@@ -1345,7 +1348,7 @@ __global__ __launch_bounds__(kThreads) void k_moe_decode_xs(
 #pragma unroll
   for (int jr = 0; jr < kXsR; ++jr)
 #pragma unroll
-    for (int c = 0; c < 4; ++c) Ar[jr][c] = dequant8(word_of(dwr[jr], c), scale_of(dsr[jr], c));
+    for (int c = 0; c < 4; ++c) Ar[jr][c] = dequant8_shifted(word_of(dwr[jr], c), scale_of(dsr[jr], c));
   // (the empty asm statements keep the dequantization here, ahead of the
   // gate/up tile; the compiler would otherwise sink it to the products)
 #pragma unroll
@@ -1739,7 +1742,7 @@ __global__ __launch_bounds__(kThreads) void k_moe_tokens(
               sg[i] = make_uint2(d.x, d.y);
               su[i] = make_uint2(e2.x, e2.y);
             }
-            gu_products<GQW>(gv, wg, wu, sg, su, xb2, rall + (size_t)((tk - m) / nmx) * 256);
+            gu_products<GQW, false>(gv, wg, wu, sg, su, xb2, rall + (size_t)((tk - m) / nmx) * 256);
           }
         }
       }

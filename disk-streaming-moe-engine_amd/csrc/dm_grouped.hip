@@ -679,29 +679,14 @@ constexpr int kB2Stage = kB2BBytes + kB2ABytes + kB2SBytes;  // 51200 bytes
 constexpr size_t kB2Lds = (size_t)kB2Stages * kB2Stage;    // 153600 bytes
 constexpr int kB2DmaPerStage = 7;                          // DMA instructions per wave and stage
 
-typedef __attribute__((address_space(3))) void lptr_t;
-// 16 bytes per lane from p to LDS at dst + 16 * lane (dst uniform per wave).
-// Issued as inline assembly: the compiler, which cannot tell the stages of
-// one LDS array apart, would otherwise wait for every load in flight before
-// any LDS read.  The kernel counts these loads itself (s_waitcnt vmcnt); a
-// load the compiler tracks is only ever waited for longer because of them.
-// M0 (the LDS address) is a register the compiler reserves: its value is
-// saved and restored around the load.
-__device__ __forceinline__ void dma16(const void* p, void* dst) {
-  const uint32_t m = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lptr_t*)dst);
-  uint32_t save;
-  asm volatile(
-      "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %1, off\n\t"
-      "s_mov_b32 m0, %0"
-      : "=&s"(save)
-      : "v"(p), "s"(m)
-      : "memory");
-}
-
-__device__ __forceinline__ uint32_t lds_addr(const void* p) {
-  return (uint32_t)(uintptr_t)(const lptr_t*)p;
-}
-
+// 16 bytes per lane from p to LDS at byte address m + 16 * lane (m uniform
+// per wave): dma16_lds, inline assembly.  The compiler, which cannot tell the
+// stages of one LDS array apart, would otherwise wait for every load in
+// flight before any LDS read.  The kernel counts these loads itself
+// (s_waitcnt vmcnt); a load the compiler tracks is only ever waited for longer
+// because of them.  LDS addresses are 32-bit offsets from lds_u32 of the
+// array: arithmetic on a generic pointer into LDS makes the compiler build
+// the 64-bit address, which it cannot always lower.
 // The B fragments of 8 column tiles (rows 16 ct + j of a staged k-step,
 // 16 * 256 bytes apart) as 8 LDS reads in flight together.  Inline assembly
 // again: the compiler would otherwise sink each read next to its first use,
@@ -860,18 +845,20 @@ void k_big(int items, int big_wgs, const int32_t* meta, const int2* units, const
   auto issue = [&](const BigItem& it, int ps, int buf) {
     const int s = it.lo ? ps >> 1 : ps;
     const uint16_t* src = (it.lo && (ps & 1)) ? it.blo : it.bhi;
-    unsigned char* st = lds2 + buf * kB2Stage;
+    const uint32_t st = lds_u32(lds2) + (uint32_t)(buf * kB2Stage);
 #pragma unroll
-    for (int m = 0; m < 4; ++m) dma16(src + it.rowo[m] + s * kQuadCols, st + (w + 8 * m) * 1024);
-    dma16(it.v0.nib + a16_nib_offset(it.nGQ, it.t0, s, lane), st + kB2BBytes + 2 * w * 1024);
-    dma16(it.v1.nib + a16_nib_offset(it.nGQ, it.t1, s, lane), st + kB2BBytes + (2 * w + 1) * 1024);
+    for (int m = 0; m < 4; ++m)
+      dma16_lds(src + it.rowo[m] + s * kQuadCols, st + (uint32_t)((w + 8 * m) * 1024));
+    dma16_lds(it.v0.nib + a16_nib_offset(it.nGQ, it.t0, s, lane), st + (uint32_t)(kB2BBytes + 2 * w * 1024));
+    dma16_lds(it.v1.nib + a16_nib_offset(it.nGQ, it.t1, s, lane),
+              st + (uint32_t)(kB2BBytes + (2 * w + 1) * 1024));
     // scales of the two chunks: 128 bytes each, lanes 0..7 and 8..15 (only
     // 16 lanes write: 256 bytes at the wave's own place)
     if (lane < 16)
-      dma16(reinterpret_cast<const unsigned char*>((lane < 8 ? it.v0 : it.v1).sc +
-                                                   a16_sc_offset(it.nGQ, it.st_, s, 0)) +
-                (lane & 7) * 16,
-            st + kB2BBytes + kB2ABytes + w * 256);
+      dma16_lds(reinterpret_cast<const unsigned char*>((lane < 8 ? it.v0 : it.v1).sc +
+                                                       a16_sc_offset(it.nGQ, it.st_, s, 0)) +
+                    (lane & 7) * 16,
+                st + (uint32_t)(kB2BBytes + kB2ABytes + w * 256));
   };
   issue(cur, 0, 0);
   issue(cur, 1, 1);  // every item has at least two stages (checked at launch)
@@ -917,7 +904,7 @@ void k_big(int items, int big_wgs, const int32_t* meta, const int2* units, const
           *reinterpret_cast<const uint2*>(st + kB2BBytes + kB2ABytes + w * 256 + 128 + j * 8);
       // The 8 B fragments of k-group kk + 1 are read while kk computes.
       bf16x8 bc[kNCT], bn[kNCT];
-      const uint32_t bp = lds_addr(st + j * kB2RowBytes);
+      const uint32_t bp = lds_u32(lds2) + (uint32_t)((gs % kB2Stages) * kB2Stage + j * kB2RowBytes);
       lds_read8(bp + (q ^ j) * 16, bc);
 #pragma unroll
       for (int kk = 0; kk < kGroupsPerQuad; ++kk) {
