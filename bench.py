@@ -94,6 +94,8 @@ def parse():
                     help="stack workload: the RMSNorm's sum of squares in the reference's "
                          "element order (ref) or as a 256-partial tree (tree)")
     ap.add_argument("--gguf-type", default="q3_k", choices=["q3_k", "q4_k", "q8_0"])
+    ap.add_argument("--gguf-tokens", type=int, default=1,
+                    help="tokens per call, gguf-moe workload (> 1: the grouped form)")
     ap.add_argument("--cpu-sample-s", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--seed", type=int, default=1)
@@ -344,6 +346,61 @@ def gguf_layer(a, blk, stream, dev):
     print(json.dumps(rec))
 
 
+def gguf_moe_tokens(a, blk, stream, dev, dims):
+    """Calls of a.gguf_tokens tokens on the uploaded GGUF layer: the grouped
+    form (tokens grouped by expert, each expert row read once per unit)."""
+    import numpy as np
+    import torch
+
+    from dismoen import synth
+    H, E, K, I, Ish = dims
+    T, nb = a.gguf_tokens, 8
+    xs = synth.make_activations(np.random.default_rng(a.seed), (nb, T, H))
+    xd = torch.from_numpy(xs).to(dev)
+    yd = torch.empty((nb, T, H), dtype=torch.float32, device=dev)
+    idd = torch.empty((nb, T, K), dtype=torch.int32, device=dev)
+    pd = torch.empty((nb, T, K), dtype=torch.float32, device=dev)
+    torch.cuda.synchronize()
+
+    def step(i):
+        b = i % nb
+        blk.forward_gguf_device(0, xd[b].data_ptr(), T, yd[b].data_ptr(), idd[b].data_ptr(),
+                                pd[b].data_ptr())
+
+    for i in range(a.warmup):
+        step(i)
+    blk.sync()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for i in range(a.steps):
+        step(a.warmup + i)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    blk.sync()
+    ms = e0.elapsed_time(e1) / a.steps
+    ids = idd.cpu().numpy()
+    uniq = float(np.mean([len(np.unique(ids[b])) for b in range(nb)]))
+    blk_bytes = lambda n: n // 256 * 114  # Q3_K payload of n weights
+    # router, the distinct routed experts and the shared one read once, x in, y out
+    alg = E * H * 4 + H * 4 + (uniq + 1) * 3 * blk_bytes(I * H) + 2 * T * H * 4
+    gbps = alg / (ms * 1e-3) / 1e9
+    rec = {"metric": f"GGUF Q3_K MoE-layer µs/token + achieved HBM GB/s ({T} tokens per call)",
+           "value": round(ms * 1e3 / T, 3), "unit": "us/token", "us_per_step": round(ms * 1e3, 3),
+           "n_gpus": 1, "steps": a.steps, "warmup": a.warmup, "ms_per_step": round(ms, 6),
+           "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+           "data": "synthetic",
+           "config": {"workload": f"qwen3.6-35b-a3b moe layer from gguf (256 q3_k experts + "
+                                  f"q3_k shared), {T} tokens per call", "hidden": H,
+                      "experts": E, "top_k": K, "inter": I, "inter_sh": Ish, "tokens": T},
+           "roofline": {"bound": "hbm", "kernel": "grouped gguf path (router, select, grouping, "
+                                                  "gate/up, down, combine)",
+                        "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                        "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None,
+                        "bytes_per_step": int(alg), "distinct_experts": uniq},
+           "cpu_baseline": None}
+    print(json.dumps(rec), flush=True)
+
+
 def gguf_moe(a, blk, stream, dev):
     """Batch-1 decode of a Qwen3.6-shape GGUF MoE layer (Q3_K experts)."""
     import tempfile
@@ -358,6 +415,8 @@ def gguf_moe(a, blk, stream, dev):
     try:
         with gguf.parse_gguf_index(path) as g:
             blk.upload_layer_gguf(0, (H, E, K, I, Ish), g)
+            if a.gguf_tokens > 1:
+                return gguf_moe_tokens(a, blk, stream, dev, (H, E, K, I, Ish))
             ntok = a.warmup + a.steps
             rng = np.random.default_rng(a.seed)
             xs = synth.make_activations(rng, (ntok, H))

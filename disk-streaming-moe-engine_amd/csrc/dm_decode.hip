@@ -1529,7 +1529,6 @@ __global__ __launch_bounds__(kThreads) void k_moe_tokens(
   const int re = m + nmx * (4 * w + (lane >> 4));
   float* xt = reinterpret_cast<float*>(smem + P.off_xt);
   uint4* xb2 = reinterpret_cast<uint4*>(smem + P.off_xb);
-  float* red = reinterpret_cast<float*>(smem + P.off_red);
   float* yred = reinterpret_cast<float*>(smem + P.tok_off_yred);
   const int K = L.K;
   const int nT = L.I / kQuadCols, KT = K * nT, NP = KT + L.Ish / kQuadCols;

@@ -58,6 +58,19 @@ hipError_t launch_gguf_down_combine(const GgufMoeDev& L, const float* h, int ldh
                                     const float* residual, float* y, unsigned long long* status,
                                     hipStream_t st);
 
+// The same outputs for T tokens grouped by expert (off, perm, units, meta
+// of launch_group_build on ids; nunits = group_units_max(T, K, E)): each
+// expert row is read once per unit of up to 128 tokens instead of once per
+// (token, slot).  Three launches: gate/up into h as launch_gguf_gateup, the
+// down projections into parts [T][K+1][H], then moe_aggregate_forward's
+// combine.  Every token's sums are formed by the same helpers in the same
+// order as launch_gguf_gateup / launch_gguf_down_combine: the same bits.
+hipError_t launch_gguf_units(const GgufMoeDev& L, const float* x, int T, const int32_t* off,
+                             const int32_t* perm, const int2* units, const int32_t* meta,
+                             int nunits, float* h, int ldh, float* parts, const float* probs,
+                             const float* shg, const float* residual, float* y,
+                             unsigned long long* status, hipStream_t st);
+
 // One token in one launch of grid workgroups of 512 threads that must all
 // be resident (gguf_experts_occupancy >= 1 per CU, gguf_one_token_grid_ok):
 // the router logits, the top-k selection, the softmax terms and the shared

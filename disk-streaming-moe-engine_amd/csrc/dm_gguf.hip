@@ -16,6 +16,7 @@
 
 #include "dm_device.h"
 #include "dm_gguf.h"
+#include "dm_grouped.h"
 #include "dm_layout.h"
 
 namespace dm {
@@ -428,6 +429,327 @@ __global__ __launch_bounds__(256) void k_gguf_down_combine(
     if (!finite_f(total)) record_err(status, err_key(kPhAgg, t, 0, d, 0));
     y[(size_t)t * L.H + d] = total;
   }
+}
+
+// ---- several tokens grouped by expert --------------------------------------
+// The units of launch_group_build: an expert's row is read once per unit (up
+// to 128 tokens) and its weights decoded once per pass of kGgufUnitTok
+// tokens.  Each token's lane sums and wave reductions are those of
+// k_gguf_gateup / k_gguf_down_combine (the same helpers, the same order), so
+// a token's outputs do not depend on the form that computed them.
+constexpr int kGgufUnitTok = 8;
+
+struct GgufUnit {
+  int e, p0, n;  // expert (E: shared), first position (shared: first token), tokens
+  bool sh;
+};
+__device__ __forceinline__ GgufUnit gguf_unit(const int2* units, const int32_t* meta,
+                                              const int32_t* off, int u, int E, int T) {
+  const int2 v = units[u];
+  const int size = u < meta[1] ? kUnitBig : kUnitSmall;
+  GgufUnit r;
+  r.sh = v.x >= E;
+  r.e = r.sh ? E : v.x;
+  r.p0 = r.sh ? v.y : off[v.x] + v.y;
+  r.n = min(size, (r.sh ? T : off[v.x + 1]) - r.p0);
+  return r;
+}
+// token and slot (K: the shared expert) of the unit's position i
+__device__ __forceinline__ void gguf_unit_pos(const GgufUnit& ut, const int32_t* perm, int K,
+                                              int i, int& t, int& slot) {
+  if (ut.sh) {
+    t = ut.p0 + i;
+    slot = K;
+  } else {
+    const int a = perm[ut.p0 + i];
+    t = a / K;
+    slot = a % K;
+  }
+}
+
+// Workgroup (rb, u): rows 4 rb + wave of unit u0 + u's expert, h as
+// k_gguf_gateup writes it.
+template <int T, int W>
+__global__ __launch_bounds__(256) void k_gguf_gateup_units(
+    GgufMoeDev L, const float* __restrict__ x, const int32_t* __restrict__ off,
+    const int32_t* __restrict__ perm, const int2* __restrict__ units,
+    const int32_t* __restrict__ meta, int ntok, float* __restrict__ h, int ldh,
+    unsigned long long* status, int u0) {
+  const int u = u0 + (int)blockIdx.y;
+  if (u >= meta[0]) return;
+  const GgufUnit ut = gguf_unit(units, meta, off, u, L.E, ntok);
+  const int rows = ut.sh ? L.Ish : L.I;
+  const int r = (int)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= rows || ut.n <= 0) return;
+  const int lane = threadIdx.x & 63;
+  const uint8_t* wg = L.raw + L.off[(size_t)ut.e * 3 + 0];
+  const uint8_t* wu = L.raw + L.off[(size_t)ut.e * 3 + 1];
+  const int64_t base = (int64_t)r * L.H;
+  for (int i0 = 0; i0 < ut.n; i0 += kGgufUnitTok) {
+    int tt[kGgufUnitTok], sl[kGgufUnitTok];
+    float ag[kGgufUnitTok], au[kGgufUnitTok];
+#pragma unroll
+    for (int k = 0; k < kGgufUnitTok; ++k) {
+      gguf_unit_pos(ut, perm, L.K, min(i0 + k, ut.n - 1), tt[k], sl[k]);
+      ag[k] = 0.0f;
+      au[k] = 0.0f;
+    }
+    const int nk = min(kGgufUnitTok, ut.n - i0);
+    for (int c = lane * W; c < L.H; c += 64 * W) {
+#pragma unroll
+      for (int k = 0; k < kGgufUnitTok; ++k) {
+        if (k >= nk) break;  // uniform per wave
+        const float* xt = x + (size_t)tt[k] * L.H;
+        if constexpr (W == 16) {
+          f32x4 xv[4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) xv[j] = *reinterpret_cast<const f32x4*>(xt + c + 4 * j);
+          gu_dot16<T>(wg, wu, base + c, L.layout, xv, ag[k], au[k]);
+        } else {
+          f32x4 g4[W / 4], u4[W / 4];
+          valuesW<T, W>(wg, base + c, L.layout, g4);
+          valuesW<T, W>(wu, base + c, L.layout, u4);
+#pragma unroll
+          for (int j = 0; j < W / 4; ++j) {
+            const f32x4 xv = *reinterpret_cast<const f32x4*>(xt + c + 4 * j);
+            ag[k] = dot4(g4[j], xv, ag[k]);
+            au[k] = dot4(u4[j], xv, au[k]);
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < kGgufUnitTok; ++k) {
+      if (i0 + k >= ut.n) break;  // uniform per wave
+      const float g = wave_sum_dpp(ag[k]), uu = wave_sum_dpp(au[k]);
+      if (lane == 0) {
+        const int t = tt[k], slot = sl[k];
+        const float hv = dm_silu(g) * uu;
+        const uint32_t ph = ut.sh ? kPhShared : kPhExpert, sp = ut.sh ? 0 : (uint32_t)slot;
+        if (!finite_f(g)) record_err(status, err_key(ph, t, sp, r, kEkGate));
+        if (!finite_f(uu)) record_err(status, err_key(ph, t, sp, r, kEkUp));
+        if (!finite_f(hv)) record_err(status, err_key(ph, t, sp, r, kEkH));
+        h[((size_t)t * (L.K + 1) + slot) * ldh + r] = hv;
+      }
+    }
+  }
+}
+
+// Workgroup (db, u): output rows 4 db + wave of unit u0 + u's down
+// projection, parts[t][slot][d] as k_gguf_down_combine forms part[slot].
+template <int T, int W>
+__global__ __launch_bounds__(256) void k_gguf_down_units(
+    GgufMoeDev L, const float* __restrict__ h, int ldh, const int32_t* __restrict__ off,
+    const int32_t* __restrict__ perm, const int2* __restrict__ units,
+    const int32_t* __restrict__ meta, int ntok, float* __restrict__ parts,
+    unsigned long long* status, int u0) {
+  const int u = u0 + (int)blockIdx.y;
+  if (u >= meta[0]) return;
+  const GgufUnit ut = gguf_unit(units, meta, off, u, L.E, ntok);
+  const int d = (int)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (d >= L.H || ut.n <= 0) return;
+  const int lane = threadIdx.x & 63;
+  const int n = ut.sh ? L.Ish : L.I;
+  const uint8_t* wd = L.raw + L.off[(size_t)ut.e * 3 + 2];
+  const int64_t base = (int64_t)d * n;
+  for (int i0 = 0; i0 < ut.n; i0 += kGgufUnitTok) {
+    int tt[kGgufUnitTok], sl[kGgufUnitTok];
+    float a[kGgufUnitTok];
+#pragma unroll
+    for (int k = 0; k < kGgufUnitTok; ++k) {
+      gguf_unit_pos(ut, perm, L.K, min(i0 + k, ut.n - 1), tt[k], sl[k]);
+      a[k] = 0.0f;
+    }
+    const int nk = min(kGgufUnitTok, ut.n - i0);
+    for (int c = lane * W; c < n; c += 64 * W) {
+      f32x4 w4[W / 4];
+      valuesW<T, W>(wd, base + c, L.layout, w4);
+#pragma unroll
+      for (int k = 0; k < kGgufUnitTok; ++k) {
+        if (k >= nk) break;  // uniform per wave
+        const float* hv = h + ((size_t)tt[k] * (L.K + 1) + sl[k]) * ldh;
+#pragma unroll
+        for (int j = 0; j < W / 4; ++j)
+          a[k] = dot4(w4[j], *reinterpret_cast<const f32x4*>(hv + c + 4 * j), a[k]);
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < kGgufUnitTok; ++k) {
+      if (i0 + k >= ut.n) break;  // uniform per wave
+      const float v = wave_sum_dpp(a[k]);
+      if (lane == 0) {
+        const int t = tt[k], slot = sl[k];
+        if (!finite_f(v))
+          record_err(status, err_key(ut.sh ? kPhShared : kPhExpert, t, ut.sh ? 0 : slot, n + d,
+                                     kEkDown));
+        parts[((size_t)t * (L.K + 1) + slot) * L.H + d] = v;
+      }
+    }
+  }
+}
+
+// Blocked forms (the common shapes): a wave keeps the activations of
+// kGgufBlkTok tokens in registers (its lane's chunks, at most kGgufBlkCh of
+// them) across rpw rows (1 .. kGgufBlkRowsMax, more when the units hold
+// more tokens), so that a row costs its weights and the
+// products, not another read of every token's x (or h) from the caches.
+// The lane sums run over the same chunks in the same order as above.
+constexpr int kGgufBlkTok = 4, kGgufBlkCh = 2, kGgufBlkRowsMax = 8;
+
+// gate/up, sixteen weights per lane (gu_dot16), H <= 64 * 16 * kGgufBlkCh
+template <int T>
+__global__ __launch_bounds__(256) void k_gguf_gateup_units_blk(
+    GgufMoeDev L, const float* __restrict__ x, const int32_t* __restrict__ off,
+    const int32_t* __restrict__ perm, const int2* __restrict__ units,
+    const int32_t* __restrict__ meta, int ntok, float* __restrict__ h, int ldh,
+    unsigned long long* status, int u0, int rpw) {
+  const int u = u0 + (int)blockIdx.y;
+  if (u >= meta[0]) return;
+  const GgufUnit ut = gguf_unit(units, meta, off, u, L.E, ntok);
+  const int rows = ut.sh ? L.Ish : L.I;
+  const int row0 = ((int)blockIdx.x * 4 + (threadIdx.x >> 6)) * rpw;
+  if (row0 >= rows || ut.n <= 0) return;
+  const int lane = threadIdx.x & 63;
+  const uint8_t* wg = L.raw + L.off[(size_t)ut.e * 3 + 0];
+  const uint8_t* wu = L.raw + L.off[(size_t)ut.e * 3 + 1];
+  for (int i0 = 0; i0 < ut.n; i0 += kGgufBlkTok) {
+    const int nk = min(kGgufBlkTok, ut.n - i0);
+    int tt[kGgufBlkTok], sl[kGgufBlkTok];
+    f32x4 xv[kGgufBlkTok][kGgufBlkCh][4];
+#pragma unroll
+    for (int k = 0; k < kGgufBlkTok; ++k) {
+      gguf_unit_pos(ut, perm, L.K, min(i0 + k, ut.n - 1), tt[k], sl[k]);
+      const float* xt = x + (size_t)tt[k] * L.H;
+#pragma unroll
+      for (int ch = 0; ch < kGgufBlkCh; ++ch) {
+        const int c = lane * 16 + 1024 * ch;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          xv[k][ch][j] = c < L.H ? *reinterpret_cast<const f32x4*>(xt + c + 4 * j)
+                                 : f32x4{0, 0, 0, 0};
+      }
+    }
+    for (int rr = 0; rr < rpw; ++rr) {
+      const int r = row0 + rr;
+      if (r >= rows) break;  // uniform per wave
+      const int64_t base = (int64_t)r * L.H;
+      float ag[kGgufBlkTok], au[kGgufBlkTok];
+#pragma unroll
+      for (int k = 0; k < kGgufBlkTok; ++k) ag[k] = au[k] = 0.0f;
+#pragma unroll
+      for (int ch = 0; ch < kGgufBlkCh; ++ch) {
+        const int c = lane * 16 + 1024 * ch;
+        if (c < L.H) {
+#pragma unroll
+          for (int k = 0; k < kGgufBlkTok; ++k)
+            if (k < nk) gu_dot16<T>(wg, wu, base + c, L.layout, xv[k][ch], ag[k], au[k]);
+        }
+      }
+#pragma unroll
+      for (int k = 0; k < kGgufBlkTok; ++k) {
+        if (k >= nk) break;  // uniform per wave
+        const float g = wave_sum_dpp(ag[k]), uu = wave_sum_dpp(au[k]);
+        if (lane == 0) {
+          const int t = tt[k], slot = sl[k];
+          const float hv = dm_silu(g) * uu;
+          const uint32_t ph = ut.sh ? kPhShared : kPhExpert, sp = ut.sh ? 0 : (uint32_t)slot;
+          if (!finite_f(g)) record_err(status, err_key(ph, t, sp, r, kEkGate));
+          if (!finite_f(uu)) record_err(status, err_key(ph, t, sp, r, kEkUp));
+          if (!finite_f(hv)) record_err(status, err_key(ph, t, sp, r, kEkH));
+          h[((size_t)t * (L.K + 1) + slot) * ldh + r] = hv;
+        }
+      }
+    }
+  }
+}
+
+// down, eight weights per lane, I and Ish <= 64 * 8 * kGgufBlkCh
+template <int T>
+__global__ __launch_bounds__(256) void k_gguf_down_units_blk(
+    GgufMoeDev L, const float* __restrict__ h, int ldh, const int32_t* __restrict__ off,
+    const int32_t* __restrict__ perm, const int2* __restrict__ units,
+    const int32_t* __restrict__ meta, int ntok, float* __restrict__ parts,
+    unsigned long long* status, int u0, int rpw) {
+  const int u = u0 + (int)blockIdx.y;
+  if (u >= meta[0]) return;
+  const GgufUnit ut = gguf_unit(units, meta, off, u, L.E, ntok);
+  const int d0 = ((int)blockIdx.x * 4 + (threadIdx.x >> 6)) * rpw;
+  if (d0 >= L.H || ut.n <= 0) return;
+  const int lane = threadIdx.x & 63;
+  const int n = ut.sh ? L.Ish : L.I;
+  const uint8_t* wd = L.raw + L.off[(size_t)ut.e * 3 + 2];
+  for (int i0 = 0; i0 < ut.n; i0 += kGgufBlkTok) {
+    const int nk = min(kGgufBlkTok, ut.n - i0);
+    int tt[kGgufBlkTok], sl[kGgufBlkTok];
+    f32x4 hv[kGgufBlkTok][kGgufBlkCh][2];
+#pragma unroll
+    for (int k = 0; k < kGgufBlkTok; ++k) {
+      gguf_unit_pos(ut, perm, L.K, min(i0 + k, ut.n - 1), tt[k], sl[k]);
+      const float* ht = h + ((size_t)tt[k] * (L.K + 1) + sl[k]) * ldh;
+#pragma unroll
+      for (int ch = 0; ch < kGgufBlkCh; ++ch) {
+        const int c = lane * 8 + 512 * ch;
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          hv[k][ch][j] = c < n ? *reinterpret_cast<const f32x4*>(ht + c + 4 * j)
+                               : f32x4{0, 0, 0, 0};
+      }
+    }
+    for (int rr = 0; rr < rpw; ++rr) {
+      const int d = d0 + rr;
+      if (d >= L.H) break;  // uniform per wave
+      const int64_t base = (int64_t)d * n;
+      float a[kGgufBlkTok];
+#pragma unroll
+      for (int k = 0; k < kGgufBlkTok; ++k) a[k] = 0.0f;
+#pragma unroll
+      for (int ch = 0; ch < kGgufBlkCh; ++ch) {
+        const int c = lane * 8 + 512 * ch;
+        if (c < n) {
+          f32x4 w4[2];
+          valuesW<T, 8>(wd, base + c, L.layout, w4);
+#pragma unroll
+          for (int k = 0; k < kGgufBlkTok; ++k)
+            if (k < nk) {
+#pragma unroll
+              for (int j = 0; j < 2; ++j) a[k] = dot4(w4[j], hv[k][ch][j], a[k]);
+            }
+        }
+      }
+#pragma unroll
+      for (int k = 0; k < kGgufBlkTok; ++k) {
+        if (k >= nk) break;  // uniform per wave
+        const float v = wave_sum_dpp(a[k]);
+        if (lane == 0) {
+          const int t = tt[k], slot = sl[k];
+          if (!finite_f(v))
+            record_err(status, err_key(ut.sh ? kPhShared : kPhExpert, t, ut.sh ? 0 : slot,
+                                       n + d, kEkDown));
+          parts[((size_t)t * (L.K + 1) + slot) * L.H + d] = v;
+        }
+      }
+    }
+  }
+}
+
+// y[t][d] from parts[t][0..K][d]: k_gguf_down_combine's combine, thread per (t, d).
+__global__ __launch_bounds__(256) void k_gguf_combine_parts(int K, int H, int ntok,
+                                                            const float* __restrict__ parts,
+                                                            const float* __restrict__ probs,
+                                                            const float* __restrict__ shg,
+                                                            const float* __restrict__ residual,
+                                                            float* __restrict__ y,
+                                                            unsigned long long* status) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (int64_t)ntok * H) return;
+  const int t = (int)(i / H), d = (int)(i % H);
+  const float* pp = parts + (size_t)t * (K + 1) * H + d;
+  float acc = 0.0f;
+  for (int k = 0; k < K; ++k) acc = acc + probs[(size_t)t * K + k] * pp[(size_t)k * H];
+  float total = acc + shg[t] * pp[(size_t)K * H];
+  if (residual) total = total + residual[(size_t)t * H + d];
+  if (!finite_f(total)) record_err(status, err_key(kPhAgg, t, 0, d, 0));
+  y[(size_t)t * H + d] = total;
 }
 
 // ---- one token in one launch ------------------------------------------------
@@ -1109,6 +1431,15 @@ hipError_t launch_dequant_gguf(int t, const uint8_t* raw, int64_t n, int layout,
     case kGgmlF32: KERNEL<kGgmlF32, W><<<GRID, 256, 0, st>>>(__VA_ARGS__); break;         \
     default: return hipErrorInvalidValue;                                                 \
   }
+#define DM_GGUF_DISPATCH_T(KERNEL, GRID, ...)                                             \
+  switch (L.type) {                                                                       \
+    case kGgmlQ8_0: KERNEL<kGgmlQ8_0><<<GRID, 256, 0, st>>>(__VA_ARGS__); break;          \
+    case kGgmlQ4_K: KERNEL<kGgmlQ4_K><<<GRID, 256, 0, st>>>(__VA_ARGS__); break;          \
+    case kGgmlQ3_K: KERNEL<kGgmlQ3_K><<<GRID, 256, 0, st>>>(__VA_ARGS__); break;          \
+    case kGgmlBF16: KERNEL<kGgmlBF16><<<GRID, 256, 0, st>>>(__VA_ARGS__); break;          \
+    case kGgmlF32: KERNEL<kGgmlF32><<<GRID, 256, 0, st>>>(__VA_ARGS__); break;            \
+    default: return hipErrorInvalidValue;                                                 \
+  }
 #define DM_GGUF_DISPATCH(KERNEL, GRID, ...)                                               \
   if (L.H % 8 == 0 && L.I % 8 == 0 && L.Ish % 8 == 0) {                                   \
     DM_GGUF_DISPATCH_W(KERNEL, 8, GRID, __VA_ARGS__)                                      \
@@ -1147,8 +1478,55 @@ hipError_t launch_gguf_down_combine(const GgufMoeDev& L, const float* h, int ldh
   }
   return hipGetLastError();
 }
+hipError_t launch_gguf_units(const GgufMoeDev& L, const float* x, int T, const int32_t* off,
+                             const int32_t* perm, const int2* units, const int32_t* meta,
+                             int nunits, float* h, int ldh, float* parts, const float* probs,
+                             const float* shg, const float* residual, float* y,
+                             unsigned long long* status, hipStream_t st) {
+  if (T <= 0 || nunits <= 0 || L.K <= 0 || L.H % 4 || L.I % 4 || L.Ish % 4 || ldh % 4 ||
+      ldh < L.I || ldh < L.Ish)
+    return hipErrorInvalidValue;
+  const int rows = L.I > L.Ish ? L.I : L.Ish;
+  // rows per wave of the blocked forms: one for few tokens (the units hold
+  // one or two, and more waves hide more latency), up to eight as the units fill
+  const int rpw = T >= 512 ? kGgufBlkRowsMax : T >= 128 ? 4 : T >= 32 ? 2 : 1;  // (T >= 128 in use)
+  for (int u0 = 0; u0 < nunits; u0 += 65535) {
+    const int n = nunits - u0 < 65535 ? nunits - u0 : 65535;
+    const dim3 grid((unsigned)((rows + 3) / 4), (unsigned)n);
+    if (L.H % 16 == 0 && L.H <= 64 * 16 * kGgufBlkCh) {  // as launch_gguf_gateup: W = 16
+      const dim3 gb((unsigned)((rows + 4 * rpw - 1) / (4 * rpw)), (unsigned)n);
+      DM_GGUF_DISPATCH_T(k_gguf_gateup_units_blk, gb, L, x, off, perm, units, meta, T, h, ldh,
+                         status, u0, rpw)
+    } else if (L.H % 16 == 0) {
+      DM_GGUF_DISPATCH_W(k_gguf_gateup_units, 16, grid, L, x, off, perm, units, meta, T, h, ldh,
+                         status, u0)
+    } else {
+      DM_GGUF_DISPATCH(k_gguf_gateup_units, grid, L, x, off, perm, units, meta, T, h, ldh, status,
+                       u0)
+    }
+  }
+  for (int u0 = 0; u0 < nunits; u0 += 65535) {
+    const int n = nunits - u0 < 65535 ? nunits - u0 : 65535;
+    const dim3 grid((unsigned)((L.H + 3) / 4), (unsigned)n);
+    const int nmax = L.I > L.Ish ? L.I : L.Ish;
+    if (L.H % 8 == 0 && L.I % 8 == 0 && L.Ish % 8 == 0 && nmax <= 64 * 8 * kGgufBlkCh) {
+      // as launch_gguf_down_combine: W = 8
+      const dim3 gb((unsigned)((L.H + 4 * rpw - 1) / (4 * rpw)), (unsigned)n);
+      DM_GGUF_DISPATCH_T(k_gguf_down_units_blk, gb, L, h, ldh, off, perm, units, meta, T, parts,
+                         status, u0, rpw)
+    } else {
+      DM_GGUF_DISPATCH(k_gguf_down_units, grid, L, h, ldh, off, perm, units, meta, T, parts,
+                       status, u0)
+    }
+  }
+  const int64_t nt = (int64_t)T * L.H;
+  hipLaunchKernelGGL(k_gguf_combine_parts, dim3((unsigned)((nt + 255) / 256)), dim3(256), 0, st,
+                     L.K, L.H, T, parts, probs, shg, residual, y, status);
+  return hipGetLastError();
+}
 #undef DM_GGUF_DISPATCH
 #undef DM_GGUF_DISPATCH_W
+#undef DM_GGUF_DISPATCH_T
 
 bool gguf_one_token_supported(const GgufMoeDev& L) {
   return L.H % 64 == 0 && L.H <= kFrontMaxH && L.I % 16 == 0 && L.I <= 512 && L.Ish % 8 == 0 &&

@@ -10,6 +10,13 @@ namespace dm {
 // Upper bound of the work units for T tokens (size of the units buffer).
 int group_units_max(int T, int K, int E);
 
+// Tokens per work unit of launch_group_build: units[0 .. meta[1]) hold up to
+// kUnitBig of their expert's positions, units[meta[1] .. meta[0]) up to
+// kUnitSmall.  A unit is (expert, first position within the expert); the
+// expert E is the shared one, whose positions are the tokens.
+constexpr int kUnitBig = 128;
+constexpr int kUnitSmall = 16;
+
 // Group the T*K assignments by expert: off [E+1], perm [T*K], units, meta[0].
 hipError_t launch_group_build(const int32_t* ids, int T, int K, int E, int32_t* off,
                               int32_t* perm, int2* units, int32_t* meta, hipStream_t st);

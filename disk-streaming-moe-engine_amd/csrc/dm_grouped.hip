@@ -1042,6 +1042,7 @@ __device__ __forceinline__ void small_loop(const ExpertView& v0, const ExpertVie
     if (s0 + u < ns) small_step<LO>(ring[u], acc);
 }
 
+static_assert(kMT == kUnitBig && kSmallMax == kUnitSmall, "unit sizes of dm_grouped.h");
 constexpr int kSmallGuCols = 4 * 16;   // features per small gate/up workgroup
 constexpr int kSmallDnRows = 4 * 32;   // output rows per small down workgroup
 

@@ -96,6 +96,24 @@ def test_qwen_shape_q3_k(block, oracle, qwen_gguf):
         _check_layer(block, oracle, g, 3, dims, 20, T=5, seed=61)
 
 
+def test_many_tokens_grouped_qwen_shape(block, oracle, qwen_gguf):
+    """130 tokens on 16 experts: the grouped form's big units (more than 32
+    of an expert's tokens, the shared expert's 128 + 2) and small units,
+    against the oracle, and rows equal to the same tokens computed alone,
+    bit for bit."""
+    dims = (2048, 16, 8, 512, 512)
+    with gguf.parse_gguf_index(qwen_gguf) as g:
+        block.upload_layer_gguf(22, dims, g, model_layer=3)
+        print("qwen-shape q3_k layer uploaded (grouped form)", flush=True)
+        _check_layer(block, oracle, g, 3, dims, 22, T=130, seed=64)
+    x = synth.make_activations(np.random.default_rng(65), (130, 2048))
+    y, ids, probs, shg = block.forward_port_moe_gguf(x, None, 22, 130)
+    for t in (0, 1, 63, 127, 128, 129):
+        y1, i1, p1, s1 = block.forward_port_moe_gguf(x[t:t + 1], None, 22, 1)
+        assert np.array_equal(y[t].view(np.uint32), y1[0].view(np.uint32)), t
+        assert np.array_equal(ids[t], i1[0]) and np.array_equal(probs[t], p1[0]), t
+
+
 @pytest.mark.parametrize("ty", [12, 8, 0])
 def test_other_expert_types(block, oracle, tmp_path, ty):
     dims = (256, 8, 4, 64, 96)
