@@ -629,6 +629,18 @@ __global__ __launch_bounds__(256) void k_gguf_gateup_units_blk(
                                  : f32x4{0, 0, 0, 0};
       }
     }
+    // Q3_K: the next row's bytes are requested before this row's products
+    // (q3_dot16 on them is gu_dot16's arithmetic)
+    Q3Raw<16> pg[kGgufBlkCh], pu[kGgufBlkCh];
+    auto q3_fetch = [&](int r) {
+#pragma unroll
+      for (int ch = 0; ch < kGgufBlkCh; ++ch) {
+        const int c = min(lane * 16 + 1024 * ch, L.H - 16);
+        pg[ch] = q3_load<16>(wg, (int64_t)r * L.H + c);
+        pu[ch] = q3_load<16>(wu, (int64_t)r * L.H + c);
+      }
+    };
+    if constexpr (T == kGgmlQ3_K) q3_fetch(row0);
     for (int rr = 0; rr < rpw; ++rr) {
       const int r = row0 + rr;
       if (r >= rows) break;  // uniform per wave
@@ -636,13 +648,36 @@ __global__ __launch_bounds__(256) void k_gguf_gateup_units_blk(
       float ag[kGgufBlkTok], au[kGgufBlkTok];
 #pragma unroll
       for (int k = 0; k < kGgufBlkTok; ++k) ag[k] = au[k] = 0.0f;
+      if constexpr (T == kGgmlQ3_K) {
+        Q3Raw<16> cg[kGgufBlkCh], cu[kGgufBlkCh];
 #pragma unroll
-      for (int ch = 0; ch < kGgufBlkCh; ++ch) {
-        const int c = lane * 16 + 1024 * ch;
-        if (c < L.H) {
+        for (int ch = 0; ch < kGgufBlkCh; ++ch) {
+          cg[ch] = pg[ch];
+          cu[ch] = pu[ch];
+        }
+        if (rr + 1 < rpw && r + 1 < rows) q3_fetch(r + 1);
 #pragma unroll
-          for (int k = 0; k < kGgufBlkTok; ++k)
-            if (k < nk) gu_dot16<T>(wg, wu, base + c, L.layout, xv[k][ch], ag[k], au[k]);
+        for (int ch = 0; ch < kGgufBlkCh; ++ch) {
+          const int c = lane * 16 + 1024 * ch;
+          if (c < L.H) {
+#pragma unroll
+            for (int k = 0; k < kGgufBlkTok; ++k)
+              if (k < nk) {
+                const float xs = xsum16(xv[k][ch]);
+                ag[k] = q3_dot16(cg[ch], xv[k][ch], xs, ag[k]);
+                au[k] = q3_dot16(cu[ch], xv[k][ch], xs, au[k]);
+              }
+          }
+        }
+      } else {
+#pragma unroll
+        for (int ch = 0; ch < kGgufBlkCh; ++ch) {
+          const int c = lane * 16 + 1024 * ch;
+          if (c < L.H) {
+#pragma unroll
+            for (int k = 0; k < kGgufBlkTok; ++k)
+              if (k < nk) gu_dot16<T>(wg, wu, base + c, L.layout, xv[k][ch], ag[k], au[k]);
+          }
         }
       }
 #pragma unroll
@@ -695,6 +730,15 @@ __global__ __launch_bounds__(256) void k_gguf_down_units_blk(
                                : f32x4{0, 0, 0, 0};
       }
     }
+    // Q3_K: the next row's bytes are requested before this row's products
+    // (q3_decode on them forms valuesW's values)
+    Q3Raw<8> pd[kGgufBlkCh];
+    auto q3_fetch = [&](int d) {
+#pragma unroll
+      for (int ch = 0; ch < kGgufBlkCh; ++ch)
+        pd[ch] = q3_load<8>(wd, (int64_t)d * n + min(lane * 8 + 512 * ch, n - 8));
+    };
+    if constexpr (T == kGgmlQ3_K) q3_fetch(d0);
     for (int rr = 0; rr < rpw; ++rr) {
       const int d = d0 + rr;
       if (d >= L.H) break;  // uniform per wave
@@ -702,12 +746,21 @@ __global__ __launch_bounds__(256) void k_gguf_down_units_blk(
       float a[kGgufBlkTok];
 #pragma unroll
       for (int k = 0; k < kGgufBlkTok; ++k) a[k] = 0.0f;
+      Q3Raw<8> cd[kGgufBlkCh];
+      if constexpr (T == kGgmlQ3_K) {
+#pragma unroll
+        for (int ch = 0; ch < kGgufBlkCh; ++ch) cd[ch] = pd[ch];
+        if (rr + 1 < rpw && d + 1 < L.H) q3_fetch(d + 1);
+      }
 #pragma unroll
       for (int ch = 0; ch < kGgufBlkCh; ++ch) {
         const int c = lane * 8 + 512 * ch;
         if (c < n) {
           f32x4 w4[2];
-          valuesW<T, 8>(wd, base + c, L.layout, w4);
+          if constexpr (T == kGgmlQ3_K)
+            q3_decode<8>(cd[ch], w4);
+          else
+            valuesW<T, 8>(wd, base + c, L.layout, w4);
 #pragma unroll
           for (int k = 0; k < kGgufBlkTok; ++k)
             if (k < nk) {
