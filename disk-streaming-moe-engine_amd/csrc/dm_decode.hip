@@ -1254,7 +1254,7 @@ __global__ __launch_bounds__(kThreads) void k_moe_decode_xs(
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt) {
           const uint4 wv =
-              __builtin_bit_cast(uint4, dequant8_shifted(word_of(shc[mt], c), scale_of(shs[mt], c)));
+              __builtin_bit_cast(uint4, dequant8(word_of(shc[mt], c), scale_of(shs[mt], c)));
           const uint32_t wd[4] = {wv.x, wv.y, wv.z, wv.w};
 #pragma unroll
           for (int u = 0; u < 4; ++u) {
@@ -1336,7 +1336,7 @@ __global__ __launch_bounds__(kThreads) void k_moe_decode_xs(
   }
 
 #pragma unroll
-  for (int c = 0; c < 4; ++c) As[c] = dequant8_shifted(word_of(dws, c), scale_of(dss, c));
+  for (int c = 0; c < 4; ++c) As[c] = dequant8(word_of(dws, c), scale_of(dss, c));
   // the softmax sum and slot weights while the loads are in flight; the
   // ranks and outputs in the reference's order in one workgroup
   const int fin_wg = nb - 1;
@@ -1348,7 +1348,7 @@ __global__ __launch_bounds__(kThreads) void k_moe_decode_xs(
 #pragma unroll
   for (int jr = 0; jr < kXsR; ++jr)
 #pragma unroll
-    for (int c = 0; c < 4; ++c) Ar[jr][c] = dequant8_shifted(word_of(dwr[jr], c), scale_of(dsr[jr], c));
+    for (int c = 0; c < 4; ++c) Ar[jr][c] = dequant8(word_of(dwr[jr], c), scale_of(dsr[jr], c));
   // (the empty asm statements keep the dequantization here, ahead of the
   // gate/up tile; the compiler would otherwise sink it to the products)
 #pragma unroll

@@ -120,9 +120,10 @@ __device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t m, uint32_t o) {
 }
 
 // The same weights from four shifted copies of the word (two instructions
-// more per 8 weights).  The one-token fused kernels keep this form: their
-// step, latency- rather than throughput-bound, measured 13.4 us with it
-// against 14.0 us with dequant8 below.
+// more per 8 weights).  The one-token fused kernels keep this form for their
+// gate/up tiles: the XCD-sliced kernel's step measured 13.4 us with it
+// against 14.0 us with dequant8 below there (dequant8 in its down operands:
+// 13.35 against 13.39 us).
 __device__ __forceinline__ bf16x8 dequant8_shifted(uint32_t w, float s) {
   const uint32_t M = 0x000F000Fu, O = 0x64006400u;
   float c0 = -1032.0f * s;
