@@ -671,9 +671,16 @@ hipError_t run_gguf_block(dmh_ctx* c, GgufLayer* G, unsigned long long* status, 
   // router logits and, as column E, the shared-gate logit in the same
   // 16-lane order; the selection kernel applies the gate's sigmoid and its
   // GATE_ERROR checks
-  if ((e = dm::launch_router_generic(dx, L.router, T, L.H, L.E, c->z.p, status, st, L.shgate)) !=
-      hipSuccess)
+  const int rs = (int)(dm::gguf_chain_router_bytes(L) / ((size_t)(L.E + 1) * sizeof(float)));
+  if (L.rchain && dm::router_rows_f32_ok(T, L.H, L.E, rs)) {
+    // many tokens: the chain-ordered copy, four tokens per pass (the same bits)
+    if ((e = dm::launch_router_rows_f32(dx, L.rchain, rs, T, L.H, L.E, c->z.p, status, st)) !=
+        hipSuccess)
+      return e;
+  } else if ((e = dm::launch_router_generic(dx, L.router, T, L.H, L.E, c->z.p, status, st,
+                                            L.shgate)) != hipSuccess) {
     return e;
+  }
   if ((e = dm::launch_router_select(c->z.p, L.E + 1, T, L.E, L.K, 1, dids, dprobs, dshg, status,
                                     st)) != hipSuccess)
     return e;

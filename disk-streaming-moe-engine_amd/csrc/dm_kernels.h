@@ -28,6 +28,14 @@ hipError_t launch_router_generic(const float* x, const float* w, int T, int H, i
                                  unsigned long long* status, hipStream_t st,
                                  const float* w_sh = nullptr);
 
+// The same logits (z[T][E + 1], column E the shared gate) for T >= 8 tokens
+// from the chain-ordered fp32 copy of a GGUF layer's router and shared gate
+// (rows of rs floats, launch_chain_router), four tokens per pass over each
+// lane's chain held in registers; H / 64 in {8, 16, 32}.
+bool router_rows_f32_ok(int T, int H, int E, int rs);
+hipError_t launch_router_rows_f32(const float* x, const float* rchain, int rs, int T, int H, int E,
+                                  float* z, unsigned long long* status, hipStream_t st);
+
 // ---- decode path (one token per launch set) ----
 hipError_t launch_router_dec(const LayerDev& L, const float* x, int T, float* z,
                              unsigned long long* status, hipStream_t st,

@@ -483,6 +483,117 @@ __global__ __launch_bounds__(256) void k_router_rows(
   }
 }
 
+// The fp32 router of the GGUF layers for many tokens: k_router_rows' form
+// (each lane's chain of weights in registers, four tokens per pass, the
+// activations from LDS) on the chain-ordered fp32 copy of the router and the
+// shared gate (launch_chain_router: rows of rs floats, float4 group 16 q + l
+// = steps 4q .. 4q + 3 of chain l), with k_router_lds's checks: a
+// non-finite activation (kPhX), routed router weight (kPhRouterW) or routed
+// logit (kPhLogit).  The chains, their order and the halving tree are
+// k_router_lds's (H % 16 == 0: no tail), so the logits are its bits.
+template <int NQ>
+__global__ __launch_bounds__(256) void k_router_rows_f32(const float* __restrict__ x,
+                                                         const float* __restrict__ rchain, int rs,
+                                                         int E, int T, int tpw,
+                                                         float* __restrict__ z,
+                                                         unsigned long long* status) {
+  extern __shared__ __attribute__((aligned(16))) float xs4[];  // [H][kRdTok]
+  constexpr int H = NQ * 64;
+  const int l = threadIdx.x & 15;
+  const int e = blockIdx.x * 16 + (threadIdx.x >> 4);
+  const bool wave_live = blockIdx.x * 16 + (threadIdx.x >> 6) * 4 <= E;  // uniform per wave
+  f32x4 wf[NQ];
+  {
+    const f32x4* wp = reinterpret_cast<const f32x4*>(rchain + (size_t)min(e, E) * rs) + l;
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) wf[q] = wp[16 * q];
+  }
+  if (blockIdx.y == 0 && e < E) {
+    bool bad = false;
+#pragma unroll
+    for (int q = 0; q < NQ; ++q)
+      bad |= !finite_f(wf[q].x) || !finite_f(wf[q].y) || !finite_f(wf[q].z) || !finite_f(wf[q].w);
+    if (bad) record_err(status, err_key(kPhRouterW, 0, 0, 0, 0));
+  }
+  const int tb = blockIdx.y * tpw, te = min(T, tb + tpw);
+  for (int t0 = tb; t0 < te; t0 += kRdTok) {
+    const int nt = min(kRdTok, te - t0);
+    bool bad = false;
+    for (int k = threadIdx.x; k < H; k += 256) {
+      float v[kRdTok];
+#pragma unroll
+      for (int tt = 0; tt < kRdTok; ++tt) {
+        v[tt] = x[(size_t)(t0 + min(tt, nt - 1)) * H + k];
+        bad |= tt < nt && !finite_f(v[tt]);
+      }
+      *reinterpret_cast<float4*>(xs4 + (size_t)k * kRdTok) = make_float4(v[0], v[1], v[2], v[3]);
+    }
+    if (bad && blockIdx.x == 0) record_err(status, err_key(kPhX, 0, 0, 0, 0));
+    __syncthreads();
+    if (wave_live) {
+      float acc[kRdTok] = {0.0f, 0.0f, 0.0f, 0.0f};
+      const uint32_t xa0 = lds_u32(xs4 + (size_t)l * kRdTok);
+      f32x4 xc[4], xn[4];
+      lds_read_steps4(xa0, xc);
+#pragma unroll
+      for (int c = 0; c < NQ; ++c) {
+        if (c + 1 < NQ) {
+          lds_read_steps4(xa0 + (c + 1) * 4 * 256, xn);
+          lds_wait_steps4<4>(xc);
+        } else {
+          lds_wait_steps4<0>(xc);
+        }
+        // steps 4c .. 4c + 3 of chain l, in order
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const float wv = wf[c][u];
+          acc[0] = acc[0] + xc[u][0] * wv;
+          acc[1] = acc[1] + xc[u][1] * wv;
+          acc[2] = acc[2] + xc[u][2] * wv;
+          acc[3] = acc[3] + xc[u][3] * wv;
+        }
+        asm volatile("" : "+v"(acc[0]), "+v"(acc[1]), "+v"(acc[2]), "+v"(acc[3]));
+        if (c + 1 < NQ) {
+#pragma unroll
+          for (int k = 0; k < 4; ++k) xc[k] = xn[k];
+        }
+      }
+#pragma unroll
+      for (int tt = 0; tt < kRdTok; ++tt) {
+#pragma unroll
+        for (int wdt = 8; wdt >= 1; wdt >>= 1) acc[tt] = acc[tt] + __shfl_down(acc[tt], wdt, 16);
+        if (l == 0 && e <= E && tt < nt) {
+          if (e < E && !finite_f(acc[tt])) record_err(status, err_key(kPhLogit, t0 + tt, 0, e, 0));
+          z[(size_t)(t0 + tt) * (E + 1) + e] = acc[tt];
+        }
+      }
+    }
+    __syncthreads();  // xs4 is restaged for the next tokens
+  }
+}
+
+bool router_rows_f32_ok(int T, int H, int E, int rs) {
+  const int nq = H % 64 == 0 ? H / 64 : 0;
+  return T >= 2 * kRdTok && (nq == 32 || nq == 16 || nq == 8) && rs >= H && rs % 4 == 0 && E >= 1;
+}
+
+hipError_t launch_router_rows_f32(const float* x, const float* rchain, int rs, int T, int H, int E,
+                                  float* z, unsigned long long* status, hipStream_t st) {
+  if (!router_rows_f32_ok(T, H, E, rs)) return hipErrorInvalidValue;
+  const int blocks = (E + 1 + 15) / 16;
+  const int want = (1024 + blocks - 1) / blocks;
+  int tpw = (T + want - 1) / want;
+  tpw = ((tpw + kRdTok - 1) / kRdTok) * kRdTok;
+  const dim3 g(blocks, (T + tpw - 1) / tpw);
+  const size_t lds = (size_t)H * kRdTok * sizeof(float);
+  switch (H / 64) {
+    case 32: hipLaunchKernelGGL(k_router_rows_f32<32>, g, dim3(256), lds, st, x, rchain, rs, E, T, tpw, z, status); break;
+    case 16: hipLaunchKernelGGL(k_router_rows_f32<16>, g, dim3(256), lds, st, x, rchain, rs, E, T, tpw, z, status); break;
+    default: hipLaunchKernelGGL(k_router_rows_f32<8>, g, dim3(256), lds, st, x, rchain, rs, E, T, tpw, z, status); break;
+  }
+  return hipGetLastError();
+}
+
 hipError_t launch_router_dec(const LayerDev& L, const float* x, int T, float* z,
                              unsigned long long* status, hipStream_t st, const int* gate) {
   const int blocks = (L.E + 1 + 15) / 16;

@@ -112,6 +112,18 @@ def test_many_tokens_grouped_qwen_shape(block, oracle, qwen_gguf):
         y1, i1, p1, s1 = block.forward_port_moe_gguf(x[t:t + 1], None, 22, 1)
         assert np.array_equal(y[t].view(np.uint32), y1[0].view(np.uint32)), t
         assert np.array_equal(ids[t], i1[0]) and np.array_equal(probs[t], p1[0]), t
+    # 16 tokens take the lane-chain fp32 router: a non-finite activation is
+    # the router stage's error, as in every other form
+    xb = x[:16].copy()
+    xb[5, 7] = np.nan
+    with pytest.raises(DismoenError) as ei:
+        block.forward_port_moe_gguf(xb, None, 22, 16)
+    assert json.loads(str(ei.value)) == {"error_type": "ACT_LOAD_FAILED",
+                                         "detail": "non-finite value in activation",
+                                         "stage": "router", "layer": 22}
+    y16, i16, p16, _ = block.forward_port_moe_gguf(x[:16], None, 22, 16)
+    assert np.array_equal(i16, ids[:16]) and np.array_equal(p16, probs[:16])
+    assert np.array_equal(y16.view(np.uint32), y[:16].view(np.uint32))
 
 
 @pytest.mark.parametrize("ty", [12, 8, 0])
